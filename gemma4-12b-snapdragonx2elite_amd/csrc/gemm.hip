@@ -1,0 +1,370 @@
+// Prefill GEMMs on gfx950 MFMA, plus the per-row int8 activation quantizer.
+//
+//   W8A8 : C = A8 @ W8^T (int32, exact), Y = f16((f32(C) * sa[m]) * sw[n])
+//          (vk/coopgemm_w8a8.comp)          v_mfma_i32_16x16x64_i8
+//   W4A8 : as W8A8 with W8 = int8(clamp(rint((q-8) * ratio), +-127)) made
+//          on the fly from the int4 codes (vk/coopgemm_w4a8.comp)
+//   W4A16: Y = f16(X @ f16((q-8) * s)^T), fp32 accumulate
+//          (vk/coopgemm_i4h.comp, which accumulates in f16; this one
+//          accumulates in fp32)          v_mfma_f32_16x16x32_f16
+//
+// One kernel template serves all three: every k-step stages 64-byte rows of
+// both operands in LDS (64 int8 or 32 f16 elements), so the LDS layout, the
+// XOR swizzle and the MFMA fragment reads are shared; only the B-operand
+// producer (byte copy, int4 -> f16 dequant, int4 -> int8 requant) and the
+// MFMA/epilogue differ.
+//
+// Tiling: BM x BN macro tile per 256-thread workgroup (4 waves as 2 x 2),
+// each wave a (BM/2) x (BN/2) block of 16x16 MFMA tiles; LDS double
+// buffered with one barrier per k-step; the next k-step's global loads are
+// in flight while the current one's MFMAs run. Workgroups are remapped so
+// each XCD (8 per MI355X, own L2) works on a contiguous 1/8 of the grid
+// ordered by weight panel, which keeps a weight panel's re-reads in one L2.
+#include "q4mi_common.h"
+
+namespace q4 {
+
+enum { OP_W8A8 = 0, OP_W4A16 = 1, OP_W4A8 = 2 };
+
+struct GemmArgs {
+  const void* A;        // int8 [M][K] or f16 [M][K]
+  const void* B;        // int8 [N][K] (W8A8) or panel-64 int4 units
+  const uint16_t* bsc;  // panel-64 fp16 scales (W4A16) or ratio (W4A8)
+  const float* sa;      // [M]
+  const void* sw;       // [N] f32 or f16
+  int sw_f16;
+  uint16_t* Y;          // f16 [M][N] (may be NULL for int paths if C given)
+  int32_t* C;           // int32 [M][N] or NULL
+  int M, N, K;
+};
+
+// LDS byte offset of 16-byte chunk c (0..3) of staged row r. The XOR keeps
+// both the row-per-lane MFMA reads and the chunk-per-lane stores free of
+// bank conflicts.
+__device__ inline int lds_off(int r, int c) { return r * 64 + ((c ^ ((r >> 1) & 3)) << 4); }
+
+__device__ inline uint32_t pk_h2(v2h v) { return __builtin_bit_cast(uint32_t, v); }
+
+// int4 unit -> 32 f16 values f16((q - 8) * s), 4 chunks of 8 (k order).
+// Low nibbles: 0x6400 | q = 1024 + q; high nibbles: 0x6400 | 16q =
+// 1024 + 16q. Both become q - 8 exactly, then one RNE multiply by s, which
+// is the reference's float16_t((float(q) - 8.0) * scl).
+__device__ inline void dequant_unit_f16(const uint4 u, _Float16 s, uint4 out[4]) {
+  const uint32_t w[4] = {u.x, u.y, u.z, u.w};
+  const v2h sv = {s, s};
+  const v2h off_lo = {(_Float16)1032.0f, (_Float16)1032.0f};
+  const v2h sixteenth = {(_Float16)0.0625f, (_Float16)0.0625f};
+  const v2h off_hi = {(_Float16)72.0f, (_Float16)72.0f};
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const uint32_t w8 = w[i] >> 8;
+    v2h p0 = __builtin_bit_cast(v2h, (w[i] & 0x000F000Fu) | 0x64006400u);
+    v2h p1 = __builtin_bit_cast(v2h, (w[i] & 0x00F000F0u) | 0x64006400u);
+    v2h p2 = __builtin_bit_cast(v2h, (w8 & 0x000F000Fu) | 0x64006400u);
+    v2h p3 = __builtin_bit_cast(v2h, (w8 & 0x00F000F0u) | 0x64006400u);
+    p0 = (p0 - off_lo) * sv;
+    p1 = (p1 * sixteenth - off_hi) * sv;
+    p2 = (p2 - off_lo) * sv;
+    p3 = (p3 * sixteenth - off_hi) * sv;
+    out[i] = make_uint4(pk_h2(p0), pk_h2(p1), pk_h2(p2), pk_h2(p3));
+  }
+}
+
+// int4 unit -> 32 int8 values clamp(rint((q - 8) * r), -127, 127), k order.
+__device__ inline void requant_unit_i8(const uint4 u, float r, uint4 out[2]) {
+  const uint32_t w[4] = {u.x, u.y, u.z, u.w};
+  uint32_t o[8];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      uint32_t word = 0;
+#pragma unroll
+      for (int e4 = 0; e4 < 4; ++e4) {
+        const int e = 4 * h + e4;
+        const float q = (float)(int)((w[i] >> (4 * nib_pos(e))) & 15u) - 8.0f;
+        float v = rintf(__fmul_rn(q, r));
+        v = fminf(fmaxf(v, -127.0f), 127.0f);
+        word |= ((uint32_t)(int)v & 0xFFu) << (8 * e4);
+      }
+      o[2 * i + h] = word;
+    }
+  }
+  out[0] = make_uint4(o[0], o[1], o[2], o[3]);
+  out[1] = make_uint4(o[4], o[5], o[6], o[7]);
+}
+
+template <int OP, int BM, int BN>
+__global__ void __launch_bounds__(256) gemm_kernel(const GemmArgs g) {
+  constexpr int STAGE = (BM + BN) * 64;
+  constexpr int WM = BM / 2, WN = BN / 2, FM = WM / 16, FN = WN / 16;
+  constexpr int A_CH = BM / 64;                                      // A chunks per thread per k-step
+  constexpr int B_CH = (OP == OP_W8A8) ? BN / 64 : (OP == OP_W4A16 ? BN / 256 : BN / 128);
+  constexpr bool F16 = (OP == OP_W4A16);
+  static_assert(BN % 256 == 0 || OP == OP_W8A8, "int4 B producers need BN % 256 == 0");
+  typedef typename std::conditional<F16, v4f, v4i>::type acc_t;
+
+  __shared__ __attribute__((aligned(16))) uint8_t lds[2 * STAGE];
+
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int wm = wave >> 1, wn = wave & 1;
+  const int M = g.M, N = g.N, K = g.K;
+  const int ntm = (M + BM - 1) / BM;
+  const int G = gridDim.x, w = blockIdx.x;
+  const int v = (G % 8 == 0) ? (w % 8) * (G / 8) + w / 8 : w;
+  const int tm = v % ntm, tn = v / ntm;
+  const int m0 = tm * BM, n0 = tn * BN;
+  const int nblk = K / BLK;
+  const int nk = F16 ? K / 32 : K / 64;                               // k-steps (64-byte rows)
+  const long a_row_bytes = F16 ? 2L * K : (long)K;
+
+  // ---- per-thread global sources ----
+  const uint8_t* Ab = reinterpret_cast<const uint8_t*>(g.A);
+  const int a_chunk = tid & 3;
+  long a_src[A_CH];
+#pragma unroll
+  for (int i = 0; i < A_CH; ++i) {
+    const int r = (tid >> 2) + 64 * i;
+    a_src[i] = (long)min(m0 + r, M - 1) * a_row_bytes + a_chunk * 16;
+  }
+
+  uint4 ra[A_CH];
+  uint4 rb[(OP == OP_W8A8) ? B_CH : 1];
+  uint4 ru[(OP == OP_W8A8) ? 1 : B_CH];
+  uint16_t rs[(OP == OP_W8A8) ? 1 : B_CH];
+
+  auto load_regs = [&](int kt) {
+#pragma unroll
+    for (int i = 0; i < A_CH; ++i) ra[i] = *reinterpret_cast<const uint4*>(Ab + a_src[i] + (long)kt * 64);
+    if constexpr (OP == OP_W8A8) {
+      const uint8_t* Bb = reinterpret_cast<const uint8_t*>(g.B);
+#pragma unroll
+      for (int i = 0; i < B_CH; ++i) {
+        const int r = (tid >> 2) + 64 * i;
+        const long src = (long)min(n0 + r, N - 1) * K + a_chunk * 16 + (long)kt * 64;
+        rb[i] = *reinterpret_cast<const uint4*>(Bb + src);
+      }
+    } else {
+      const uint4* U = reinterpret_cast<const uint4*>(g.B);
+#pragma unroll
+      for (int i = 0; i < B_CH; ++i) {
+        // W4A16: one block per k-step, row = tid + 256 i.
+        // W4A8: two blocks per k-step, i = 2 * rr + h, row = tid + 256 rr.
+        const int rr = (OP == OP_W4A16) ? i : i / 2;
+        const int blk = (OP == OP_W4A16) ? kt : 2 * kt + (i & 1);
+        const int n = min(n0 + tid + 256 * rr, N - 1);
+        const long idx = panel_index(n, blk, nblk);
+        ru[i] = U[idx];
+        rs[i] = g.bsc[idx];
+      }
+    }
+  };
+
+  auto store_lds = [&](int stage) {
+    uint8_t* base = lds + stage * STAGE;
+#pragma unroll
+    for (int i = 0; i < A_CH; ++i) {
+      const int r = (tid >> 2) + 64 * i;
+      *reinterpret_cast<uint4*>(base + lds_off(r, a_chunk)) = ra[i];
+    }
+    if constexpr (OP == OP_W8A8) {
+#pragma unroll
+      for (int i = 0; i < B_CH; ++i) {
+        const int r = BM + (tid >> 2) + 64 * i;
+        *reinterpret_cast<uint4*>(base + lds_off(r, a_chunk)) = rb[i];
+      }
+    } else if constexpr (OP == OP_W4A16) {
+#pragma unroll
+      for (int i = 0; i < B_CH; ++i) {
+        const int r = BM + tid + 256 * i;
+        uint4 o[4];
+        dequant_unit_f16(ru[i], __builtin_bit_cast(_Float16, rs[i]), o);
+#pragma unroll
+        for (int c = 0; c < 4; ++c) *reinterpret_cast<uint4*>(base + lds_off(r, c)) = o[c];
+      }
+    } else {
+#pragma unroll
+      for (int i = 0; i < B_CH; ++i) {
+        const int r = BM + tid + 256 * (i / 2);
+        uint4 o[2];
+        requant_unit_i8(ru[i], h2f(rs[i]), o);
+        *reinterpret_cast<uint4*>(base + lds_off(r, 2 * (i & 1))) = o[0];
+        *reinterpret_cast<uint4*>(base + lds_off(r, 2 * (i & 1) + 1)) = o[1];
+      }
+    }
+  };
+
+  acc_t acc[FM][FN];
+#pragma unroll
+  for (int i = 0; i < FM; ++i)
+#pragma unroll
+    for (int j = 0; j < FN; ++j) acc[i][j] = acc_t{0, 0, 0, 0};
+
+  load_regs(0);
+  store_lds(0);
+  __syncthreads();
+
+  const int frow = lane & 15, fch = lane >> 4;
+  for (int kt = 0; kt < nk; ++kt) {
+    const int cur = kt & 1;
+    if (kt + 1 < nk) load_regs(kt + 1);
+    const uint8_t* base = lds + cur * STAGE;
+    v4i fa[FM], fb[FN];
+#pragma unroll
+    for (int i = 0; i < FM; ++i) fa[i] = *reinterpret_cast<const v4i*>(base + lds_off(wm * WM + 16 * i + frow, fch));
+#pragma unroll
+    for (int j = 0; j < FN; ++j)
+      fb[j] = *reinterpret_cast<const v4i*>(base + lds_off(BM + wn * WN + 16 * j + frow, fch));
+#pragma unroll
+    for (int i = 0; i < FM; ++i)
+#pragma unroll
+      for (int j = 0; j < FN; ++j) {
+        if constexpr (F16)
+          acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(v8h, fa[i]),
+                                                             __builtin_bit_cast(v8h, fb[j]), acc[i][j], 0, 0, 0);
+        else
+          acc[i][j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(fa[i], fb[j], acc[i][j], 0, 0, 0);
+      }
+    if (kt + 1 < nk) store_lds(cur ^ 1);
+    __syncthreads();
+  }
+
+  // ---- epilogue: lane holds D[4*(lane/16) + r][lane%16] of each tile ----
+  const int col = lane & 15, rq = (lane >> 4) * 4;
+#pragma unroll
+  for (int j = 0; j < FN; ++j) {
+    const int n = n0 + wn * WN + 16 * j + col;
+    if (n >= N) continue;
+    float swn = 1.0f;
+    if constexpr (!F16)
+      swn = g.sw_f16 ? h2f(reinterpret_cast<const uint16_t*>(g.sw)[n]) : reinterpret_cast<const float*>(g.sw)[n];
+#pragma unroll
+    for (int i = 0; i < FM; ++i) {
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int m = m0 + wm * WM + 16 * i + rq + r;
+        if (m >= M) continue;
+        const long o = (long)m * N + n;
+        if constexpr (F16) {
+          g.Y[o] = f2h(acc[i][j][r]);
+        } else {
+          const int c = acc[i][j][r];
+          if (g.C) g.C[o] = c;
+          if (g.Y) g.Y[o] = f2h(__fmul_rn(__fmul_rn((float)c, g.sa[m]), swn));
+        }
+      }
+    }
+  }
+}
+
+// ---- per-row int8 activation quantizer (vk/cast_i8.comp) -----------------
+template <int XT>
+__global__ void __launch_bounds__(256) quant_act_kernel(const void* __restrict__ X, int K, int8_t* __restrict__ A,
+                                                        float* __restrict__ sa) {
+  __shared__ float red[4];
+  const int m = blockIdx.x, tid = threadIdx.x;
+  auto ld4 = [&](int i, float v[4]) {  // elements 4i..4i+3 of row m
+    if constexpr (XT == Q4_DT_F16) {
+      ushort4 h = reinterpret_cast<const ushort4*>(reinterpret_cast<const uint16_t*>(X) + (long)m * K)[i];
+      v[0] = h2f(h.x); v[1] = h2f(h.y); v[2] = h2f(h.z); v[3] = h2f(h.w);
+    } else {
+      float4 f = reinterpret_cast<const float4*>(reinterpret_cast<const float*>(X) + (long)m * K)[i];
+      v[0] = f.x; v[1] = f.y; v[2] = f.z; v[3] = f.w;
+    }
+  };
+  const int K4 = K / 4;
+  float mx = 0.0f;
+  for (int i = tid; i < K4; i += 256) {
+    float v[4];
+    ld4(i, v);
+    mx = fmaxf(mx, fmaxf(fmaxf(fabsf(v[0]), fabsf(v[1])), fmaxf(fabsf(v[2]), fabsf(v[3]))));
+  }
+  for (int off = 32; off > 0; off >>= 1) mx = fmaxf(mx, __shfl_xor(mx, off, 64));
+  if ((tid & 63) == 0) red[tid >> 6] = mx;
+  __syncthreads();
+  mx = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+  const float s = fmaxf(__fdiv_rn(mx, 127.0f), 1e-12f);
+  if (tid == 0) sa[m] = s;
+  uint32_t* dst = reinterpret_cast<uint32_t*>(A + (long)m * K);
+  for (int i = tid; i < K4; i += 256) {
+    float v[4];
+    ld4(i, v);
+    uint32_t word = 0;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      float q = rintf(__fdiv_rn(v[e], s));
+      q = fminf(fmaxf(q, -127.0f), 127.0f);
+      word |= ((uint32_t)(int)q & 0xFFu) << (8 * e);
+    }
+    dst[i] = word;
+  }
+}
+
+template <int OP, int BM, int BN>
+static int launch_gemm(const GemmArgs& g, void* stream, const char* name) {
+  const int ntm = ceil_div(g.M, BM), ntn = ceil_div(g.N, BN);
+  hipLaunchKernelGGL((gemm_kernel<OP, BM, BN>), dim3(ntm * ntn), dim3(256), 0, as_stream(stream), g);
+  Q4_LAUNCHED(name);
+  return Q4_OK;
+}
+
+}  // namespace q4
+
+using namespace q4;
+
+extern "C" {
+
+int q4_quant_act_i8(const void* X, int x_dtype, int8_t* A, float* sa, int M, int K, void* stream) {
+  clear_error();
+  Q4_ARG(M > 0 && K > 0 && K % 4 == 0, "bad shape M=%d K=%d (K must be a multiple of 4)", M, K);
+  Q4_ARG(X && A && sa, "null pointer");
+  Q4_ARG(x_dtype == Q4_DT_F32 || x_dtype == Q4_DT_F16, "bad x dtype %d", x_dtype);
+  Q4_ARG(((uintptr_t)X & 15) == 0 && ((uintptr_t)A & 3) == 0, "misaligned X or A");
+  if (x_dtype == Q4_DT_F16)
+    hipLaunchKernelGGL(quant_act_kernel<Q4_DT_F16>, dim3(M), dim3(256), 0, as_stream(stream), X, K, A, sa);
+  else
+    hipLaunchKernelGGL(quant_act_kernel<Q4_DT_F32>, dim3(M), dim3(256), 0, as_stream(stream), X, K, A, sa);
+  Q4_LAUNCHED("quant_act_i8");
+  return Q4_OK;
+}
+
+int q4_gemm_w8a8(const int8_t* A, const int8_t* W8, const float* sa, const void* sw, int sw_dtype, uint16_t* Y,
+                 int32_t* C, int M, int N, int K, void* stream) {
+  clear_error();
+  Q4_ARG(M > 0 && N > 0 && K > 0 && K % 64 == 0, "bad W8A8 shape M=%d N=%d K=%d (K must be a multiple of 64)", M, N,
+         K);
+  Q4_ARG((long)127 * 127 * K < (1L << 31), "K=%d overflows the int32 accumulator", K);
+  Q4_ARG(A && W8 && (Y || C), "null pointer");
+  Q4_ARG(!Y || (sa && sw), "Y needs sa and sw");
+  Q4_ARG(sw_dtype == Q4_DT_F32 || sw_dtype == Q4_DT_F16, "bad sw dtype %d", sw_dtype);
+  Q4_ARG(((uintptr_t)A & 15) == 0 && ((uintptr_t)W8 & 15) == 0, "A and W8 must be 16-byte aligned");
+  GemmArgs g{A, W8, nullptr, sa, sw, sw_dtype == Q4_DT_F16, Y, C, M, N, K};
+  return launch_gemm<OP_W8A8, 256, 256>(g, stream, "gemm_w8a8");
+}
+
+int q4_gemm_w4a8(const int8_t* A, const uint32_t* wq, const uint16_t* ratio, const float* sa, const void* sw,
+                 int sw_dtype, uint16_t* Y, int32_t* C, int M, int N, int K, void* stream) {
+  clear_error();
+  Q4_ARG(M > 0 && N > 0 && K > 0 && K % 64 == 0, "bad W4A8 shape M=%d N=%d K=%d (K must be a multiple of 64)", M, N,
+         K);
+  Q4_ARG((long)127 * 127 * K < (1L << 31), "K=%d overflows the int32 accumulator", K);
+  Q4_ARG(A && wq && ratio && (Y || C), "null pointer");
+  Q4_ARG(!Y || (sa && sw), "Y needs sa and sw");
+  Q4_ARG(sw_dtype == Q4_DT_F32 || sw_dtype == Q4_DT_F16, "bad sw dtype %d", sw_dtype);
+  Q4_ARG(((uintptr_t)A & 15) == 0 && ((uintptr_t)wq & 15) == 0, "A and wq must be 16-byte aligned");
+  GemmArgs g{A, wq, ratio, sa, sw, sw_dtype == Q4_DT_F16, Y, C, M, N, K};
+  return launch_gemm<OP_W4A8, 256, 256>(g, stream, "gemm_w4a8");
+}
+
+int q4_gemm_w4a16(const uint16_t* X, const uint32_t* wq, const uint16_t* sc16, uint16_t* Y, int M, int N, int K,
+                  void* stream) {
+  clear_error();
+  Q4_ARG(M > 0 && N > 0 && K > 0 && K % 32 == 0, "bad W4A16 shape M=%d N=%d K=%d (K must be a multiple of 32)", M, N,
+         K);
+  Q4_ARG(X && wq && sc16 && Y, "null pointer");
+  Q4_ARG(((uintptr_t)X & 15) == 0 && ((uintptr_t)wq & 15) == 0, "X and wq must be 16-byte aligned");
+  GemmArgs g{X, wq, sc16, nullptr, nullptr, 0, Y, nullptr, M, N, K};
+  return launch_gemm<OP_W4A16, 256, 256>(g, stream, "gemm_w4a16");
+}
+
+}  // extern "C"

@@ -1,0 +1,148 @@
+// Library runtime: error state, version, staging casts, hipGraph
+// record/replay and the bounded stream wait.
+#include "q4mi_common.h"
+
+#include <chrono>
+#include <thread>
+
+namespace q4 {
+
+static thread_local char g_err[512];
+
+void set_error(const char* fmt, ...) {
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(g_err, sizeof(g_err), fmt, ap);
+  va_end(ap);
+}
+void clear_error() { g_err[0] = 0; }
+
+// f32 -> f16 (RNE) and f16 -> f32 staging casts, 4 elements per thread.
+__global__ void cast_f32_f16_kernel(const float* __restrict__ src, uint16_t* __restrict__ dst, size_t n) {
+  size_t i = ((size_t)blockIdx.x * blockDim.x + threadIdx.x) * 4;
+  if (i + 4 <= n) {
+    float4 v = *reinterpret_cast<const float4*>(src + i);
+    ushort4 o;
+    o.x = f2h(v.x); o.y = f2h(v.y); o.z = f2h(v.z); o.w = f2h(v.w);
+    *reinterpret_cast<ushort4*>(dst + i) = o;
+  } else {
+    for (; i < n; ++i) dst[i] = f2h(src[i]);
+  }
+}
+
+__global__ void cast_f16_f32_kernel(const uint16_t* __restrict__ src, float* __restrict__ dst, size_t n) {
+  size_t i = ((size_t)blockIdx.x * blockDim.x + threadIdx.x) * 4;
+  if (i + 4 <= n) {
+    ushort4 v = *reinterpret_cast<const ushort4*>(src + i);
+    float4 o;
+    o.x = h2f(v.x); o.y = h2f(v.y); o.z = h2f(v.z); o.w = h2f(v.w);
+    *reinterpret_cast<float4*>(dst + i) = o;
+  } else {
+    for (; i < n; ++i) dst[i] = h2f(src[i]);
+  }
+}
+
+}  // namespace q4
+
+using namespace q4;
+
+extern "C" {
+
+const char* q4_version(void) { return "q4mi 0.1.0 gfx950"; }
+
+const char* q4_last_error(void) { return g_err; }
+
+int q4_dev_bytes(int N, int K, size_t* wq_bytes, size_t* scale_elems) {
+  clear_error();
+  Q4_ARG(N > 0 && K > 0 && K % BLK == 0, "bad shape N=%d K=%d (K must be a positive multiple of 32)", N, K);
+  size_t units = (size_t)pad_rows(N) * (K / BLK);
+  if (wq_bytes) *wq_bytes = units * 16;
+  if (scale_elems) *scale_elems = units;
+  return Q4_OK;
+}
+
+int q4_cast_f32_f16(const float* src, uint16_t* dst, size_t n, void* stream) {
+  clear_error();
+  Q4_ARG(src && dst, "null pointer");
+  Q4_ARG(((uintptr_t)src & 15) == 0 && ((uintptr_t)dst & 7) == 0, "misaligned cast buffers");
+  if (n == 0) return Q4_OK;
+  size_t threads = (n + 3) / 4;
+  unsigned grid = (unsigned)((threads + 255) / 256);
+  hipLaunchKernelGGL(cast_f32_f16_kernel, dim3(grid), dim3(256), 0, as_stream(stream), src, dst, n);
+  Q4_LAUNCHED("cast_f32_f16");
+  return Q4_OK;
+}
+
+int q4_cast_f16_f32(const uint16_t* src, float* dst, size_t n, void* stream) {
+  clear_error();
+  Q4_ARG(src && dst, "null pointer");
+  Q4_ARG(((uintptr_t)src & 7) == 0 && ((uintptr_t)dst & 15) == 0, "misaligned cast buffers");
+  if (n == 0) return Q4_OK;
+  size_t threads = (n + 3) / 4;
+  unsigned grid = (unsigned)((threads + 255) / 256);
+  hipLaunchKernelGGL(cast_f16_f32_kernel, dim3(grid), dim3(256), 0, as_stream(stream), src, dst, n);
+  Q4_LAUNCHED("cast_f16_f32");
+  return Q4_OK;
+}
+
+int q4_graph_begin(void* stream) {
+  clear_error();
+  Q4_ARG(stream != nullptr, "graph capture needs a non-null stream");
+  Q4_HIP(hipStreamBeginCapture(as_stream(stream), hipStreamCaptureModeThreadLocal));
+  return Q4_OK;
+}
+
+int q4_graph_end(void* stream, void** graph_exec) {
+  clear_error();
+  Q4_ARG(stream != nullptr && graph_exec != nullptr, "null stream or output pointer");
+  hipGraph_t g = nullptr;
+  Q4_HIP(hipStreamEndCapture(as_stream(stream), &g));
+  hipGraphExec_t ge = nullptr;
+  hipError_t e = hipGraphInstantiate(&ge, g, nullptr, nullptr, 0);
+  (void)hipGraphDestroy(g);
+  if (e != hipSuccess) {
+    set_error("hipGraphInstantiate failed: %s", hipGetErrorString(e));
+    return Q4_ERR_HIP;
+  }
+  *graph_exec = (void*)ge;
+  return Q4_OK;
+}
+
+int q4_graph_launch(void* graph_exec, void* stream) {
+  clear_error();
+  Q4_ARG(graph_exec != nullptr, "null graph");
+  Q4_HIP(hipGraphLaunch((hipGraphExec_t)graph_exec, as_stream(stream)));
+  return Q4_OK;
+}
+
+int q4_graph_destroy(void* graph_exec) {
+  clear_error();
+  if (!graph_exec) return Q4_OK;
+  Q4_HIP(hipGraphExecDestroy((hipGraphExec_t)graph_exec));
+  return Q4_OK;
+}
+
+int q4_stream_wait(void* stream, int timeout_ms) {
+  clear_error();
+  if (timeout_ms <= 0) {
+    Q4_HIP(hipStreamSynchronize(as_stream(stream)));
+    return Q4_OK;
+  }
+  auto t0 = std::chrono::steady_clock::now();
+  for (;;) {
+    hipError_t e = hipStreamQuery(as_stream(stream));
+    if (e == hipSuccess) return Q4_OK;
+    if (e != hipErrorNotReady) {
+      set_error("hipStreamQuery failed: %s", hipGetErrorString(e));
+      return Q4_ERR_HIP;
+    }
+    auto ms = std::chrono::duration_cast<std::chrono::milliseconds>(std::chrono::steady_clock::now() - t0).count();
+    if (ms >= timeout_ms) {
+      set_error("stream wait timed out after %d ms", timeout_ms);
+      return Q4_ERR_TIMEOUT;
+    }
+    std::this_thread::sleep_for(std::chrono::microseconds(50));
+  }
+}
+
+}  // extern "C"

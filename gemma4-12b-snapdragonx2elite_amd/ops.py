@@ -1,0 +1,327 @@
+"""Functional API over libq4mi: torch tensors in, torch tensors out.
+
+PyTorch is only plumbing here (device memory, streams); every byte of
+arithmetic runs in the HIP kernels of libq4mi.so. All tensors must be CUDA
+(ROCm) tensors on the current device; work is enqueued on torch's current
+stream. Storage dtypes: panel-64 weight words as int32, fp16 values as
+float16, e4m3 bytes as uint8, int8 as int8.
+"""
+from __future__ import annotations
+
+import ctypes as C
+
+import torch
+
+from . import _lib
+from ._lib import DT_F16, DT_F32, OP_GEMV, SCALE_E4M3, SCALE_F16, call, lib
+
+BLK = 32
+PANEL = 64
+
+
+def _stream(stream=None):
+    s = stream if stream is not None else torch.cuda.current_stream()
+    return C.c_void_p(s.cuda_stream)
+
+
+def _p(t) -> C.c_void_p:
+    if t is None:
+        return C.c_void_p(0)
+    if isinstance(t, int):
+        return C.c_void_p(t)
+    if not t.is_cuda:
+        raise ValueError("libq4mi takes device tensors only")
+    if not t.is_contiguous():
+        raise ValueError("libq4mi takes contiguous tensors only")
+    return C.c_void_p(t.data_ptr())
+
+
+def _dt(t) -> int:
+    if t.dtype == torch.float32:
+        return DT_F32
+    if t.dtype == torch.float16:
+        return DT_F16
+    raise ValueError(f"unsupported dtype {t.dtype} (float32 or float16)")
+
+
+def dev_sizes(N: int, K: int):
+    """(bytes of the panel-64 words, number of per-(row, block) scale entries)."""
+    wb, se = C.c_size_t(), C.c_size_t()
+    call("q4_dev_bytes", N, K, C.byref(wb), C.byref(se))
+    return wb.value, se.value
+
+
+def _nbytes(t) -> int:
+    return t.numel() * t.element_size()
+
+
+def _need(t, nbytes: int, what: str) -> None:
+    """Host-side bound check: the kernels trust these sizes."""
+    if t is None or _nbytes(t) < nbytes:
+        got = None if t is None else _nbytes(t)
+        raise ValueError(f"{what}: need {nbytes} bytes, got {got}")
+
+
+def _check_int4(wq, scales, N, K, scale_bytes=2):
+    wb, se = dev_sizes(N, K)
+    _need(wq, wb, "panel-64 weight words")
+    _need(scales, se * scale_bytes, "panel-64 scales")
+
+
+def _empty_weights(N, K, device):
+    wb, se = dev_sizes(N, K)
+    return torch.empty(wb // 4, dtype=torch.int32, device=device), se
+
+
+# ---------------------------------------------------------------- weights
+def quantize(W: torch.Tensor):
+    """W float32 [N, K] (device) -> (wq int32 words, sc16 float16 panel, sc32 float32 [N, K/32])."""
+    if W.dtype != torch.float32 or W.dim() != 2:
+        raise ValueError("quantize expects a 2-D float32 tensor")
+    W = W.contiguous()
+    N, K = W.shape
+    wq, se = _empty_weights(N, K, W.device)
+    sc16 = torch.empty(se, dtype=torch.float16, device=W.device)
+    sc32 = torch.empty((N, K // BLK), dtype=torch.float32, device=W.device)
+    call("q4_quantize", _p(W), N, K, _p(wq), _p(sc16), _p(sc32), _stream())
+    return wq, sc16, sc32
+
+
+def scales_e4m3(sc32: torch.Tensor, N: int, K: int):
+    """fp32 scales [N, K/32] -> (e4m3 panel bytes uint8, inv float). Synchronizes once to read inv."""
+    _, se = dev_sizes(N, K)
+    sc8 = torch.empty(se, dtype=torch.uint8, device=sc32.device)
+    inv = torch.empty(1, dtype=torch.float32, device=sc32.device)
+    work = torch.empty(1, dtype=torch.int32, device=sc32.device)
+    call("q4_scales_e4m3", _p(sc32.contiguous()), N, K, _p(sc8), _p(inv), _p(work), _stream())
+    return sc8, float(inv.item())
+
+
+def w8_fold(wq: torch.Tensor, sc32: torch.Tensor, N: int, K: int):
+    """-> (W8 int8 [N, K], s_w float32 [N], s_w float16 [N])."""
+    W8 = torch.empty((N, K), dtype=torch.int8, device=wq.device)
+    sw32 = torch.empty(N, dtype=torch.float32, device=wq.device)
+    sw16 = torch.empty(N, dtype=torch.float16, device=wq.device)
+    call("q4_w8_fold", _p(wq), _p(sc32.contiguous()), N, K, _p(W8), _p(sw32), _p(sw16), _stream())
+    return W8, sw32, sw16
+
+
+def w4a8_ratio(sc32: torch.Tensor, sw32: torch.Tensor, N: int, K: int) -> torch.Tensor:
+    _, se = dev_sizes(N, K)
+    ratio = torch.empty(se, dtype=torch.float16, device=sc32.device)
+    call("q4_w4a8_ratio", _p(sc32.contiguous()), _p(sw32), N, K, _p(ratio), _stream())
+    return ratio
+
+
+def repack_ref(wp: torch.Tensor | None, sc_ref: torch.Tensor | None, N: int, K: int):
+    """Reference layouts (wp [K, N/8] words, fp16 scales [K/32, N]) -> (wq, sc16 panel)."""
+    dev = (wp if wp is not None else sc_ref).device
+    wq, se = _empty_weights(N, K, dev) if wp is not None else (None, dev_sizes(N, K)[1])
+    sc = torch.empty(se, dtype=torch.float16, device=dev) if sc_ref is not None else None
+    call("q4_repack_ref", _p(wp), _p(sc_ref), N, K, _p(wq), _p(sc), _stream())
+    return wq, sc
+
+
+def repack_e4m3_ref(sc_ref: torch.Tensor, N: int, K: int) -> torch.Tensor:
+    _, se = dev_sizes(N, K)
+    out = torch.empty(se, dtype=torch.uint8, device=sc_ref.device)
+    call("q4_repack_e4m3_ref", _p(sc_ref), N, K, _p(out), _stream())
+    return out
+
+
+def repack_w8_ref(w8_kn: torch.Tensor, N: int, K: int) -> torch.Tensor:
+    out = torch.empty((N, K), dtype=torch.int8, device=w8_kn.device)
+    call("q4_repack_w8_ref", _p(w8_kn), N, K, _p(out), _stream())
+    return out
+
+
+# ------------------------------------------------------------------ GEMV
+class Workspace:
+    """Caller-owned split-K workspace (fp32 partials + per-panel tickets).
+
+    Zero-filled once at creation; every GEMV leaves it ready for the next
+    one, so it can be shared by all GEMVs issued in order on one stream
+    (including inside a captured hipGraph). Do not share across streams.
+    """
+
+    def __init__(self, nbytes: int, device="cuda"):
+        self.nbytes = int(nbytes)
+        self.t = torch.empty(max(self.nbytes, 256), dtype=torch.uint8, device=device)
+        call("q4_workspace_init", _p(self.t), self.t.numel(), _stream())
+
+    @staticmethod
+    def bytes_for(N: int, K: int, split: int = 0) -> int:
+        return int(lib().q4_workspace_bytes(OP_GEMV, N, K, split))
+
+    @property
+    def ptr(self):
+        return self.t.data_ptr()
+
+
+def auto_split(N: int, K: int) -> int:
+    return int(lib().q4_gemv_auto_split(N, K))
+
+
+_WS = {}
+_CAPTURING = [0]   # > 0 while a Graph capture is open on this thread
+
+
+def default_workspace(N: int, K: int, split: int = 0, device="cuda") -> Workspace | None:
+    """A per-device workspace big enough for this GEMV (grown, never shrunk)."""
+    need = Workspace.bytes_for(N, K, split)
+    if need == 0:
+        return None
+    if _CAPTURING[0]:
+        raise RuntimeError("a split-K GEMV inside a graph capture needs a workspace allocated before "
+                           "the capture (pass ws=...); allocating and zero-filling one cannot be captured")
+    key = torch.device(device).index if torch.device(device).index is not None else torch.cuda.current_device()
+    ws = _WS.get(key)
+    if ws is None or ws.nbytes < need:
+        if ws is not None:  # keep the old one alive: descriptors/graphs may still point at it
+            _WS.setdefault(("old", key), []).append(ws)
+        ws = Workspace(max(need, 1 << 20), device=device)
+        _WS[key] = ws
+    return ws
+
+
+def gemv(x: torch.Tensor, wq: torch.Tensor, scales: torch.Tensor, N: int, K: int, *, scale_fmt: int = SCALE_F16,
+         inv: float = 1.0, y: torch.Tensor | None = None, y_dtype=None, split: int = 0,
+         ws: Workspace | None = None) -> torch.Tensor:
+    """y[N] = sum_k ((q-8) * s) * x[k] (fp32 accumulate; times inv for e4m3 scales)."""
+    if x.numel() != K:
+        raise ValueError(f"x has {x.numel()} elements, expected K={K}")
+    if y is None:
+        y = torch.empty(N, dtype=y_dtype or x.dtype, device=x.device)
+    elif y.numel() < N:
+        raise ValueError("y too small")
+    _check_int4(wq, scales, N, K, 1 if scale_fmt == SCALE_E4M3 else 2)
+    _need(y, N * y.element_size(), "y")
+    if ws is None:
+        ws = default_workspace(N, K, split, x.device)
+    call("q4_gemv", _p(x), _dt(x), _p(wq), _p(scales), scale_fmt, C.c_float(inv), _p(y), _dt(y), N, K, split,
+         _p(ws.t) if ws else C.c_void_p(0), ws.t.numel() if ws else 0, _stream())
+    return y
+
+
+# ------------------------------------------------------------------ GEMMs
+def gemm_w4a16(X: torch.Tensor, wq: torch.Tensor, sc16: torch.Tensor, N: int, Y: torch.Tensor | None = None):
+    if X.dtype != torch.float16 or X.dim() != 2:
+        raise ValueError("X must be a 2-D float16 tensor")
+    M, K = X.shape
+    _check_int4(wq, sc16, N, K)
+    Y = torch.empty((M, N), dtype=torch.float16, device=X.device) if Y is None else Y
+    _need(Y, M * N * 2, "Y")
+    call("q4_gemm_w4a16", _p(X), _p(wq), _p(sc16), _p(Y), M, N, K, _stream())
+    return Y
+
+
+def quant_act_i8(X: torch.Tensor, A: torch.Tensor | None = None, sa: torch.Tensor | None = None):
+    M, K = X.shape
+    A = torch.empty((M, K), dtype=torch.int8, device=X.device) if A is None else A
+    sa = torch.empty(M, dtype=torch.float32, device=X.device) if sa is None else sa
+    _need(A, M * K, "A")
+    _need(sa, M * 4, "sa")
+    call("q4_quant_act_i8", _p(X), _dt(X), _p(A), _p(sa), M, K, _stream())
+    return A, sa
+
+
+def gemm_w8a8(A: torch.Tensor, W8: torch.Tensor, sa: torch.Tensor, sw: torch.Tensor, *, want_c: bool = False,
+              Y: torch.Tensor | None = None):
+    M, K = A.shape
+    N = W8.shape[0]
+    if A.dtype != torch.int8 or W8.dtype != torch.int8 or W8.dim() != 2 or W8.shape[1] != K:
+        raise ValueError("gemm_w8a8 expects int8 A [M, K] and int8 W8 [N, K]")
+    _need(sa, M * 4, "sa")
+    _need(sw, N * sw.element_size(), "sw")
+    Y = torch.empty((M, N), dtype=torch.float16, device=A.device) if Y is None else Y
+    _need(Y, M * N * 2, "Y")
+    Cm = torch.empty((M, N), dtype=torch.int32, device=A.device) if want_c else None
+    call("q4_gemm_w8a8", _p(A), _p(W8), _p(sa), _p(sw), _dt(sw), _p(Y), _p(Cm), M, N, K, _stream())
+    return (Y, Cm) if want_c else Y
+
+
+def gemm_w4a8(A: torch.Tensor, wq: torch.Tensor, ratio: torch.Tensor, sa: torch.Tensor, sw: torch.Tensor, N: int, *,
+              want_c: bool = False, Y: torch.Tensor | None = None):
+    M, K = A.shape
+    if A.dtype != torch.int8:
+        raise ValueError("gemm_w4a8 expects int8 A [M, K]")
+    _check_int4(wq, ratio, N, K)
+    _need(sa, M * 4, "sa")
+    _need(sw, N * sw.element_size(), "sw")
+    Y = torch.empty((M, N), dtype=torch.float16, device=A.device) if Y is None else Y
+    _need(Y, M * N * 2, "Y")
+    Cm = torch.empty((M, N), dtype=torch.int32, device=A.device) if want_c else None
+    call("q4_gemm_w4a8", _p(A), _p(wq), _p(ratio), _p(sa), _p(sw), _dt(sw), _p(Y), _p(Cm), M, N, K, _stream())
+    return (Y, Cm) if want_c else Y
+
+
+def cast_f32_f16(src: torch.Tensor, dst: torch.Tensor | None = None) -> torch.Tensor:
+    dst = torch.empty(src.shape, dtype=torch.float16, device=src.device) if dst is None else dst
+    _need(dst, src.numel() * 2, "dst")
+    call("q4_cast_f32_f16", _p(src), _p(dst), src.numel(), _stream())
+    return dst
+
+
+def cast_f16_f32(src: torch.Tensor, dst: torch.Tensor | None = None) -> torch.Tensor:
+    dst = torch.empty(src.shape, dtype=torch.float32, device=src.device) if dst is None else dst
+    _need(dst, src.numel() * 4, "dst")
+    call("q4_cast_f16_f32", _p(src), _p(dst), src.numel(), _stream())
+    return dst
+
+
+# ----------------------------------------------------------- graphs/waits
+class Graph:
+    """A hipGraph captured from a stream: ``with g.capture(): ...`` then ``g.launch()``."""
+
+    def __init__(self, stream: torch.cuda.Stream | None = None):
+        self.stream = stream or torch.cuda.Stream()
+        self.exec = None
+
+    def capture(self):
+        g = self
+
+        class _Cap:
+            def __enter__(self_):
+                g.stream.wait_stream(torch.cuda.current_stream())
+                self_.ctx = torch.cuda.stream(g.stream)
+                self_.ctx.__enter__()
+                call("q4_graph_begin", _stream(g.stream))
+                _CAPTURING[0] += 1
+                return g
+
+            def __exit__(self_, et, ev, tb):
+                h = C.c_void_p()
+                _CAPTURING[0] -= 1
+                try:
+                    call("q4_graph_end", _stream(g.stream), C.byref(h))
+                finally:
+                    self_.ctx.__exit__(et, ev, tb)
+                g.exec = h
+                return False
+
+        return _Cap()
+
+    def launch(self, stream=None):
+        if self.exec is None:
+            raise RuntimeError("graph not captured")
+        call("q4_graph_launch", self.exec, _stream(stream or self.stream))
+
+    def destroy(self):
+        if self.exec is not None:
+            call("q4_graph_destroy", self.exec)
+            self.exec = None
+
+    def __del__(self):
+        try:
+            self.destroy()
+        except Exception:
+            pass
+
+
+def stream_wait(stream=None, timeout_ms: int = 0, label: str = "") -> None:
+    """Bounded wait; raises RuntimeError('GPU fence TIMEOUT after <ms>ms at [label]') on expiry,
+    the message the reference's fence wait raises (src/vk_engine.py:299-302)."""
+    st = lib().q4_stream_wait(_stream(stream), int(timeout_ms))
+    if st == _lib.Q4_ERR_TIMEOUT:
+        raise RuntimeError(f"GPU fence TIMEOUT after {timeout_ms}ms at [{label}]")
+    _lib.check("q4_stream_wait", st)

@@ -1,0 +1,241 @@
+"""Drop-in host helpers for the quantized matmul path, with the reference
+engine's call signatures (src/vk_engine.py of
+monstercameron/Gemma4-12B-SnapdragonX2Elite).
+
+The reference records Vulkan dispatches of GLSL shaders; here the same calls
+enqueue HIP kernels of libq4mi.so on torch's current stream, and "recording
+once" is a hipGraph capture (:func:`record`), replayed per token with a
+bounded, labelled wait (:func:`submit`).
+
+=====================  ====================================================
+reference              here
+=====================  ====================================================
+``quant(W, pf)``       same tuple ``(bw, bs, split, nblk, inv, bs16, w8,
+  :125-159             sw8)``; buffers are device :class:`Buf` in the
+                       panel-64 layout, quantized on the GPU bit-exactly
+``i4(lin, pf)`` :186   same
+``Buf`` :56-69         device buffer with ``write``/``read``/``size``
+``gemv_ds`` :214-226   same arguments; returns ``(dp, dr, N, split, WGx)``
+                       with ``dr`` always None (the split-K reduce is
+                       fused into the GEMV launch)
+``gemv(g)`` :270-272   launches (or, inside :func:`record`, captures)
+``gemm_ds`` :351-365   same arguments/return shape ``(cin, gem, cout, N, K)``
+``gmm(C, t, L, tag)``  ``C`` is a torch stream or None (current stream)
+  :391-400
+fence wait :293-302    :func:`submit` / :func:`wait` raise
+                       ``RuntimeError('GPU fence TIMEOUT after ..ms at [..]')``
+=====================  ====================================================
+
+Flags are read at import like the reference: ``GEMV_FP8=1`` selects e4m3
+decode scales, ``PREFILL_I8=1`` the W8A8 prefill GEMM,
+``GEMMA4_FENCE_TIMEOUT_MS`` the wait bound.
+"""
+from __future__ import annotations
+
+import os
+from typing import NamedTuple
+
+import numpy as np
+import torch
+
+from . import ops
+from ._lib import SCALE_E4M3, SCALE_F16
+
+FP8 = os.environ.get("GEMV_FP8") == "1"
+PREFILL_I8 = os.environ.get("PREFILL_I8") == "1"
+BLK = 32
+MC = 128                    # prefill chunk (rows per prefill GEMM), src/vk_engine.py:339
+_FENCE_MS = int(os.environ.get("GEMMA4_FENCE_TIMEOUT_MS", "0"))
+KEEP: list = []             # buffers owned for the process lifetime (src/vk_engine.py:71)
+
+
+class Buf:
+    """Device buffer of ``nbytes`` (src/vk_engine.py:56-69)."""
+
+    __slots__ = ("t", "size")
+
+    def __init__(self, nbytes: int = 0, device=None, tensor: torch.Tensor | None = None):
+        if tensor is not None:
+            self.t = tensor.contiguous()
+            self.size = self.t.numel() * self.t.element_size()
+        else:
+            self.t = torch.zeros(max(16, int(nbytes)), dtype=torch.uint8, device=device or "cuda")
+            self.size = int(nbytes)
+
+    @property
+    def ptr(self) -> int:
+        return self.t.data_ptr()
+
+    def write(self, arr) -> None:
+        a = np.ascontiguousarray(arr)
+        src = torch.from_numpy(a.reshape(-1).view(np.uint8))
+        dst = self.t.view(torch.uint8).reshape(-1)[: a.nbytes]
+        dst.copy_(src)
+        torch.cuda.current_stream().synchronize()
+
+    def read(self, nbytes: int) -> bytes:
+        return self.t.view(torch.uint8).reshape(-1)[:nbytes].cpu().numpy().tobytes()
+
+    def view(self, dtype, count: int | None = None, byte_off: int = 0) -> torch.Tensor:
+        u8 = self.t.view(torch.uint8).reshape(-1)
+        esz = torch.empty((), dtype=dtype).element_size()
+        n = count if count is not None else (u8.numel() - byte_off) // esz
+        return u8[byte_off: byte_off + n * esz].view(dtype)
+
+
+class QW(NamedTuple):
+    bw: Buf
+    bs: Buf
+    split: int
+    nblk: int
+    inv: float
+    bs16: Buf
+    w8: Buf | None
+    sw8: Buf | None
+
+
+def quant(W, pf: bool = True, fp8: bool | None = None, prefill_i8: bool | None = None) -> QW:
+    """int4 block quantization of ``W[N, K]`` on the GPU (src/vk_engine.py:125-159)."""
+    fp8 = FP8 if fp8 is None else fp8
+    prefill_i8 = PREFILL_I8 if prefill_i8 is None else prefill_i8
+    Wt = torch.as_tensor(W).to(device="cuda", dtype=torch.float32).contiguous()
+    N, K = Wt.shape
+    nblk = K // BLK
+    wq, sc16, sc32 = ops.quantize(Wt)
+    del Wt
+    inv = 1.0
+    bs16 = Buf(tensor=sc16)
+    bs = bs16
+    if fp8:
+        sc8, inv = ops.scales_e4m3(sc32, N, K)
+        bs = Buf(tensor=sc8)
+    split = ops.auto_split(N, K)
+    w8 = sw8 = None
+    if prefill_i8 and pf:
+        W8, _sw32, sw16 = ops.w8_fold(wq, sc32, N, K)
+        w8, sw8 = Buf(tensor=W8), Buf(tensor=sw16)
+    return QW(Buf(tensor=wq), bs, split, nblk, float(inv), bs16, w8, sw8)
+
+
+def i4(lin, pf: bool = True):
+    """Quantize an ``nn.Linear`` and drop its fp weight (src/vk_engine.py:186)."""
+    W = lin.weight.detach().float()
+    lin.weight = None
+    return quant(W, pf), tuple(W.shape)
+
+
+class GemvDesc(NamedTuple):
+    dp: tuple
+    dr: None
+    N: int
+    split: int
+    WGx: int
+
+
+def gemv_ds(qw, inbuf: Buf, outbuf: Buf, out_off: int = 0) -> GemvDesc:
+    """Bind a quantized matrix to fp32 input/output buffers (src/vk_engine.py:214-226)."""
+    (bw, bs, split, nblk, inv, _bs16, _w8, _sw8), (N, K) = qw
+    fmt = SCALE_E4M3 if bs.t.dtype == torch.uint8 else SCALE_F16
+    ws = ops.default_workspace(N, K, split, bw.t.device)
+    if ws is not None:
+        KEEP.append(ws)
+    x = inbuf.view(torch.float32, K)
+    y = outbuf.view(torch.float32, N, out_off)
+    dp = (x, bw.t, bs.t, fmt, inv, y, N, K, split, ws)
+    return GemvDesc(dp, None, N, split, (N + 63) // 64)
+
+
+def gemv(g: GemvDesc) -> None:
+    """Enqueue (or capture) one GEMV (src/vk_engine.py:270-272)."""
+    x, wq, sc, fmt, inv, y, N, K, split, ws = g.dp
+    ops.gemv(x, wq, sc, N, K, scale_fmt=fmt, inv=inv, y=y, split=split, ws=ws)
+
+
+_STAGE: dict = {}
+
+
+def _stage(name: str, nbytes: int) -> Buf:
+    b = _STAGE.get(name)
+    if b is None or b.size < nbytes:
+        b = Buf(nbytes)
+        KEEP.append(b)
+        _STAGE[name] = b
+    return b
+
+
+def gemm_ds(qw, inbuf: Buf, outbuf: Buf, prefill_i8: bool | None = None):
+    """Prefill GEMM wiring for an ``MC``-row chunk (src/vk_engine.py:351-365).
+
+    f16 route: cast f32->f16, W4A16 GEMM, cast f16->f32. W8A8 route
+    (``PREFILL_I8``): per-row int8 quant, W8A8 GEMM, cast f16->f32.
+    """
+    prefill_i8 = PREFILL_I8 if prefill_i8 is None else prefill_i8
+    (bw, _bs, _s, _n, _inv, bs16, w8, sw8), (N, K) = qw
+    xin = inbuf.view(torch.float32, MC * K).view(MC, K)
+    yout = outbuf.view(torch.float32, MC * N).view(MC, N)
+    y16 = _stage("Yf16", MC * max(N, K) * 2).view(torch.float16, MC * N).view(MC, N)
+    if prefill_i8:
+        if w8 is None:
+            raise ValueError("PREFILL_I8 needs int8 weights: quantize with pf=True and prefill_i8=True")
+        a8 = _stage("Ai8", MC * max(N, K)).view(torch.int8, MC * K).view(MC, K)
+        sa = _stage("SAb", MC * 4).view(torch.float32, MC)
+        W8 = w8.t.view(N, K)
+        sw = sw8.t
+        cin = ("quant_act_i8", xin, a8, sa)
+        gem = ("w8a8", a8, W8, sa, sw, y16)
+    else:
+        x16 = _stage("Xf16", MC * max(N, K) * 2).view(torch.float16, MC * K).view(MC, K)
+        cin = ("cast_dn", xin, x16)
+        gem = ("w4a16", x16, bw.t, bs16.t, N, y16)
+    cout = ("cast_up", y16, yout)
+    return (cin, gem, cout, N, K)
+
+
+def _run(op):
+    kind = op[0]
+    if kind == "cast_dn":
+        ops.cast_f32_f16(op[1], op[2])
+    elif kind == "cast_up":
+        ops.cast_f16_f32(op[1], op[2])
+    elif kind == "quant_act_i8":
+        ops.quant_act_i8(op[1], op[2], op[3])
+    elif kind == "w8a8":
+        ops.gemm_w8a8(op[1], op[2], op[3], op[4], Y=op[5])
+    elif kind == "w4a16":
+        ops.gemm_w4a16(op[1], op[2], op[3], op[4], Y=op[5])
+    else:
+        raise ValueError(kind)
+
+
+def gmm(C, t, L=None, tag: str = "") -> None:
+    """cast -> GEMM -> cast for one prefill matmul (src/vk_engine.py:391-400).
+    ``C``: torch stream to enqueue on (None = current stream)."""
+    cin, gem, cout, _N, _K = t
+    if C is None:
+        for op in (cin, gem, cout):
+            _run(op)
+    else:
+        with torch.cuda.stream(C):
+            for op in (cin, gem, cout):
+                _run(op)
+
+
+# ------------------------------------------------------- record-once submit
+def record(body) -> ops.Graph:
+    """Capture everything ``body()`` enqueues into one hipGraph
+    (the command buffer recorded once, src/vk_engine.py:254-290)."""
+    g = ops.Graph()
+    with g.capture():
+        body()
+    return g
+
+
+def wait(stream=None, label: str = "", timeout_ms: int | None = None) -> None:
+    """Bounded wait (src/vk_engine.py:293-302); infinite when the bound is 0."""
+    ops.stream_wait(stream, _FENCE_MS if timeout_ms is None else timeout_ms, label)
+
+
+def submit(g: ops.Graph, label: str = "", timeout_ms: int | None = None) -> None:
+    """Replay a recorded graph and wait for it (src/vk_engine.py:312-319)."""
+    g.launch()
+    wait(g.stream, label, timeout_ms)

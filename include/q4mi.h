@@ -1,0 +1,182 @@
+/*
+ * q4mi.h - C ABI of the MI355X (gfx950) int4/int8 quantized matrix-product
+ * library (libq4mi.so).
+ *
+ * Every entry point takes plain device pointers, sizes and a HIP stream
+ * (hipStream_t passed as void*; NULL = the null stream), enqueues work on
+ * that stream and returns an int status (Q4_OK on success). On failure
+ * q4_last_error() returns a message for the calling thread. The library
+ * never allocates or frees caller memory; the split-K workspace is
+ * caller-owned and sized by q4_workspace_bytes().
+ *
+ * Citations are relative to the reference repository
+ * (monstercameron/Gemma4-12B-SnapdragonX2Elite) root.
+ *
+ * Weight formats
+ *   reference ("ref"): wp[K][N/8] uint32, nibble j of wp[k][i] = code of row
+ *     8i+j at k (src/vk_engine.py:129-130); fp16 scales [K/32][N]
+ *     (src/vk_engine.py:131); e4m3 scales [K/32][N] bytes
+ *     (src/vk_engine.py:133-137); int8 weights [K][N] (src/vk_engine.py:155).
+ *   device ("panel-64", this library): rows padded to a multiple of 64; one
+ *     16-byte unit per (row n, block b) at unit index
+ *     ((n/64)*(K/32) + b)*64 + n%64; word i of a unit holds k = 32b+8i+e,
+ *     e = 0..7, at nibble position (e&1)*4 + (e>>1). Scales (fp16, e4m3, or
+ *     the fp16 W4A8 ratio) use the same ((n/64)*(K/32) + b)*64 + n%64 index.
+ *     int8 weights for W8A8 are [N][K] (K contiguous).
+ *   Codes are stored offset-8: nibble value = signed code + 8.
+ */
+#ifndef Q4MI_H
+#define Q4MI_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* status codes */
+#define Q4_OK 0
+#define Q4_ERR_ARG 1         /* bad shape, pointer, dtype or size */
+#define Q4_ERR_HIP 2         /* a HIP runtime call failed */
+#define Q4_ERR_TIMEOUT 3     /* bounded wait expired (q4_stream_wait) */
+
+/* element types for activations / outputs / per-row weight scales */
+#define Q4_DT_F32 0
+#define Q4_DT_F16 1
+
+/* block-scale formats of the int4 GEMV */
+#define Q4_SCALE_F16 0
+#define Q4_SCALE_E4M3 1
+
+/* op ids for q4_workspace_bytes */
+#define Q4_OP_GEMV 0
+
+/* ---- library info / errors --------------------------------------------- */
+const char* q4_version(void);
+/* Message of the last failed call on this thread ("" if none). */
+const char* q4_last_error(void);
+/* Bytes of the panel-64 weight words and of one per-(row,block) fp16 array
+ * for an N x K matrix (K multiple of 32). */
+int q4_dev_bytes(int N, int K, size_t* wq_bytes, size_t* scale_elems);
+
+/* ---- weight preparation (load time) -------------------------------------
+ * Replaces the numpy quantizer quant() (src/vk_engine.py:125-159).        */
+
+/* W f32 [N][K] -> codes (panel-64 words), fp16 scales (panel-64) and the
+ * unrounded fp32 scales sc32 [N][K/32] (row-major; may be NULL).
+ * src/vk_engine.py:126-131. */
+int q4_quantize(const float* W, int N, int K, uint32_t* wq, uint16_t* sc16,
+                float* sc32, void* stream);
+
+/* fp32 scales sc32 [N][K/32] -> e4m3 scales (panel-64 bytes) with the
+ * per-tensor power-of-two lift; writes inv = 2^-shift to *inv_dev (device
+ * float) and the max scale bits to *work (device uint32, caller-owned,
+ * zeroed by this call). src/vk_engine.py:133-137. */
+int q4_scales_e4m3(const float* sc32, int N, int K, uint8_t* sc8,
+                   float* inv_dev, uint32_t* work, void* stream);
+
+/* W8A8 weight fold from codes + unrounded fp32 scales:
+ * W8 [N][K] int8, s_w [N] as fp32 (sw32, may be NULL) and fp16 (sw16, may
+ * be NULL). src/vk_engine.py:152-157. */
+int q4_w8_fold(const uint32_t* wq, const float* sc32, int N, int K,
+               int8_t* W8, float* sw32, uint16_t* sw16, void* stream);
+
+/* W4A8 requant ratio f16(sc32 / s_w) in panel-64 order.
+ * benchmarks/coopgemm_w4a8.py:84. */
+int q4_w4a8_ratio(const float* sc32, const float* sw32, int N, int K,
+                  uint16_t* ratio, void* stream);
+
+/* Reference layouts -> device layouts (drop-in for buffers produced by the
+ * reference quantizer). wp [K][N/8] -> panel-64 words; fp16 scales
+ * [K/32][N] -> panel-64 (sc_ref/sc_dev may be NULL to skip).
+ * src/vk_engine.py:129-131. */
+int q4_repack_ref(const uint32_t* wp, const uint16_t* sc_ref, int N, int K,
+                  uint32_t* wq, uint16_t* sc_dev, void* stream);
+/* e4m3 scales [K/32][N] bytes -> panel-64 bytes. src/vk_engine.py:137. */
+int q4_repack_e4m3_ref(const uint8_t* sc_ref, int N, int K, uint8_t* sc_dev,
+                       void* stream);
+/* int8 weights [K][N] -> [N][K]. src/vk_engine.py:155. */
+int q4_repack_w8_ref(const int8_t* w8_kn, int N, int K, int8_t* w8_nk,
+                     void* stream);
+
+/* ---- decode GEMV ---------------------------------------------------------
+ * y[N] = sum_k ((q[n,k]-8) * s[n,k/32]) * x[k]   (fp32 accumulate), times
+ * inv for e4m3 scales. Replaces gemv.comp + reduce.comp
+ * (vk/gemv.comp:11-33, vk/reduce.comp:8-12) / gemv_fp8.comp
+ * (vk/gemv_fp8.comp:20-40) as recorded by gemv_ds()/gemv()
+ * (src/vk_engine.py:214-226, 270-272).
+ * x: x_dtype [K]; y: y_dtype [N]. split = number of workgroups sharing one
+ * 64-row panel along K (0 = choose automatically). When the effective split
+ * is > 1 a workspace of q4_workspace_bytes(Q4_OP_GEMV, N, K, split) bytes is
+ * required; it must be zero-filled once before first use (q4_workspace_init)
+ * and is left ready for the next call. One workspace per stream. */
+size_t q4_workspace_bytes(int op, int N, int K, int split);
+int q4_workspace_init(void* ws, size_t bytes, void* stream);
+/* The split the library uses for an N x K GEMV when asked for split = 0
+ * (the MI355X counterpart of src/vk_engine.py:143-148). */
+int q4_gemv_auto_split(int N, int K);
+
+int q4_gemv(const void* x, int x_dtype, const uint32_t* wq,
+            const void* scales, int scale_fmt, float inv, void* y,
+            int y_dtype, int N, int K, int split, void* ws, size_t ws_bytes,
+            void* stream);
+/* fp16-scale GEMV (vk/gemv.comp). */
+int q4_gemv_f16s(const void* x, int x_dtype, const uint32_t* wq,
+                 const uint16_t* sc16, void* y, int y_dtype, int N, int K,
+                 int split, void* ws, size_t ws_bytes, void* stream);
+/* e4m3-scale GEMV (vk/gemv_fp8.comp); inv as in the shader's uniform e.x. */
+int q4_gemv_e4m3s(const void* x, int x_dtype, const uint32_t* wq,
+                  const uint8_t* sc8, float inv, void* y, int y_dtype, int N,
+                  int K, int split, void* ws, size_t ws_bytes, void* stream);
+
+/* ---- prefill GEMMs -------------------------------------------------------
+ * W4A16: Y f16 [M][N] = X f16 [M][K] @ f16((q-8)*s)^T, fp32 accumulate.
+ * Replaces coopgemm_i4h.comp (vk/coopgemm_i4h.comp:13-35) as wired by
+ * gemm_ds()/gmm() (src/vk_engine.py:351-365, 391-400). */
+int q4_gemm_w4a16(const uint16_t* X, const uint32_t* wq, const uint16_t* sc16,
+                  uint16_t* Y, int M, int N, int K, void* stream);
+
+/* Per-row int8 activation quantizer: sa[m] = max(absmax/127, 1e-12),
+ * A = clamp(rint(x / sa), -127, 127) (IEEE fp32 divide).
+ * vk/cast_i8.comp:11-19, rounding per benchmarks/coopgemm_w4a8.py:87-88. */
+int q4_quant_act_i8(const void* X, int x_dtype, int8_t* A, float* sa, int M,
+                    int K, void* stream);
+
+/* W8A8: C int32 = A int8 [M][K] @ W8 int8 [N][K]^T (exact),
+ * Y f16 [M][N] = f16((f32(C) * sa[m]) * sw[n]); sw is sw_dtype [N].
+ * C (int32 [M][N]) is written only if non-NULL. Y may be NULL when C is not.
+ * vk/coopgemm_w8a8.comp:18-37. */
+int q4_gemm_w8a8(const int8_t* A, const int8_t* W8, const float* sa,
+                 const void* sw, int sw_dtype, uint16_t* Y, int32_t* C, int M,
+                 int N, int K, void* stream);
+
+/* W4A8: as W8A8 with B = int8(clamp(rint((q-8) * ratio[n,b]), -127, 127))
+ * formed on the fly from the int4 codes and the panel-64 fp16 ratio.
+ * vk/coopgemm_w4a8.comp:21-50. */
+int q4_gemm_w4a8(const int8_t* A, const uint32_t* wq, const uint16_t* ratio,
+                 const float* sa, const void* sw, int sw_dtype, uint16_t* Y,
+                 int32_t* C, int M, int N, int K, void* stream);
+
+/* f32 <-> f16 staging casts around a prefill GEMM.
+ * vk/cast_dn.comp:7, vk/cast_up.comp:7 (wired at src/vk_engine.py:398-400). */
+int q4_cast_f32_f16(const float* src, uint16_t* dst, size_t n, void* stream);
+int q4_cast_f16_f32(const uint16_t* src, float* dst, size_t n, void* stream);
+
+/* ---- record-once submit --------------------------------------------------
+ * The per-token command buffer recorded once and resubmitted
+ * (src/vk_engine.py:254-290, forward() :312-319) becomes a hipGraph captured
+ * from a (non-null) stream. */
+int q4_graph_begin(void* stream);
+int q4_graph_end(void* stream, void** graph_exec);
+int q4_graph_launch(void* graph_exec, void* stream);
+int q4_graph_destroy(void* graph_exec);
+/* Bounded wait for all work on the stream: Q4_ERR_TIMEOUT after timeout_ms
+ * (<= 0 waits forever). The counterpart of the fence wait with
+ * GEMMA4_FENCE_TIMEOUT_MS (src/vk_engine.py:293-302). */
+int q4_stream_wait(void* stream, int timeout_ms);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* Q4MI_H */

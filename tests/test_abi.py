@@ -1,0 +1,89 @@
+"""C-ABI checks that need no GPU: the library loads, exports every entry point
+include/q4mi.h declares, the ctypes table matches the header, and argument
+validation fails with a status + message before any device work."""
+import ctypes as C
+import re
+from pathlib import Path
+
+import pytest
+
+ROOT = Path(__file__).resolve().parents[1]
+HEADER = ROOT / "include" / "q4mi.h"
+
+
+def header_functions():
+    text = re.sub(r"/\*.*?\*/", "", HEADER.read_text(), flags=re.S)
+    names = re.findall(r"^\s*(?:const\s+)?[A-Za-z_][\w\s\*]*?\b(q4_\w+)\s*\(", text, flags=re.M)
+    return sorted(set(names))
+
+
+def test_header_parse_sane():
+    names = header_functions()
+    assert "q4_gemv" in names and "q4_gemm_w8a8" in names and "q4_last_error" in names
+    assert len(names) >= 25
+
+
+def test_library_exports_every_header_symbol(g4):
+    lib = g4._lib.lib()
+    missing = [n for n in header_functions() if not hasattr(lib, n)]
+    assert not missing, f"missing exports: {missing}"
+
+
+def test_ctypes_table_matches_header(g4):
+    assert sorted(g4._lib.SIGNATURES) == header_functions()
+
+
+def test_version_and_error_strings(g4):
+    lib = g4._lib.lib()
+    assert lib.q4_version().decode().startswith("q4mi")
+    assert lib.q4_last_error() is not None
+
+
+def _err(g4):
+    return g4._lib.lib().q4_last_error().decode()
+
+
+def test_argument_errors_without_gpu(g4):
+    lib = g4._lib.lib()
+    null = C.c_void_p(0)
+    # K not a multiple of 32
+    st = lib.q4_gemv(null, 0, null, null, 0, C.c_float(1.0), null, 0, 128, 100, 0, null, 0, null)
+    assert st == g4._lib.Q4_ERR_ARG and "multiple of 32" in _err(g4)
+    # null pointers
+    st = lib.q4_gemv(null, 0, null, null, 0, C.c_float(1.0), null, 0, 128, 128, 0, null, 0, null)
+    assert st == g4._lib.Q4_ERR_ARG and "null" in _err(g4)
+    # W8A8: K must be a multiple of 64
+    st = lib.q4_gemm_w8a8(null, null, null, null, 0, null, null, 64, 64, 96, null)
+    assert st == g4._lib.Q4_ERR_ARG and "multiple of 64" in _err(g4)
+    # int32 accumulator bound
+    st = lib.q4_gemm_w8a8(null, null, null, null, 0, null, null, 64, 64, 64 * 2100, null)
+    assert st == g4._lib.Q4_ERR_ARG and "overflow" in _err(g4)
+    # graph capture needs a real stream
+    assert lib.q4_graph_begin(null) == g4._lib.Q4_ERR_ARG
+    # reference layout needs N % 8 == 0
+    st = lib.q4_repack_ref(null, null, 12, 32, null, null, null)
+    assert st == g4._lib.Q4_ERR_ARG and "N % 8" in _err(g4)
+
+
+def test_sizes_and_split_queries(g4):
+    lib = g4._lib.lib()
+    wb, se = C.c_size_t(), C.c_size_t()
+    assert lib.q4_dev_bytes(15360, 3840, C.byref(wb), C.byref(se)) == 0
+    assert wb.value == 15360 * 3840 // 2 and se.value == 15360 * 120
+    assert lib.q4_dev_bytes(70, 64, C.byref(wb), C.byref(se)) == 0
+    assert se.value == 128 * 2  # rows padded to whole 64-row panels
+    # lm_head needs no split-K, small-N matrices do, and the workspace covers it
+    assert lib.q4_gemv_auto_split(262144, 3840) == 1
+    for N, K in [(15360, 3840), (2048, 3840), (3840, 15360), (3840, 4096)]:
+        s = lib.q4_gemv_auto_split(N, K)
+        assert 1 < s <= K // 32
+        ws = lib.q4_workspace_bytes(0, N, K, 0)
+        assert ws >= s * N * 4 + (N // 64) * 4 and ws % 256 == 0
+    assert lib.q4_workspace_bytes(0, 262144, 3840, 0) == 0
+    # an explicit split too small for the LDS staging cap is raised
+    assert lib.q4_workspace_bytes(0, 64, 15360, 1) > 0
+
+
+def test_missing_library_fails_loudly(g4, tmp_path):
+    with pytest.raises(FileNotFoundError, match="no CPU fallback"):
+        g4._lib.lib(tmp_path / "nope.so")

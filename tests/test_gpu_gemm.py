@@ -1,0 +1,127 @@
+"""Prefill GEMMs and the int8 activation quantizer vs the oracle.
+
+Bit-exact: int8 activation codes and scales, W8A8/W4A8 int32 accumulators
+and their fp16 epilogue. W4A16: normwise <= 1e-3 against the oracle's exact
+fp32 dequant + fp32 matmul (the kernel rounds each dequantized weight to
+fp16 as the reference shader does, then accumulates in fp32).
+"""
+import numpy as np
+import pytest
+import torch
+
+from oracle import q4_oracle as O
+from tests.helpers import synth_int4, to_np, upload_int4
+
+pytestmark = pytest.mark.gpu
+
+
+# ------------------------------------------------------ activation quant
+@pytest.mark.parametrize("M,K", [(1, 4), (3, 64), (128, 3840), (2048, 3840), (17, 15360)])
+@pytest.mark.parametrize("dt", [np.float32, np.float16])
+def test_quant_act_i8_bit_exact(gpu, M, K, dt):
+    rng = np.random.default_rng(M + K)
+    X = rng.standard_normal((M, K)).astype(dt)
+    if M >= 3:
+        X[0] = 0                                   # zero row -> 1e-12 scale
+        X[1, :4] = [127, 2.5, -3.5, 0.5] if K >= 4 else X[1, :4]   # absmax 127 -> exact ties
+    A, sa = O.quant_act_i8(X)
+    gA, gsa = gpu.quant_act_i8(torch.from_numpy(X).cuda())
+    assert (to_np(gsa) == sa).all()
+    assert (to_np(gA) == A).all()
+
+
+# ------------------------------------------------------------------ W8A8
+def _w8a8_case(rng, M, N, K):
+    W = (rng.standard_normal((N, K)) * 0.08).astype(np.float32)
+    q, sc = O.quant_codes(W)
+    W8, sw = O.w8_fold(q, sc)
+    X = rng.standard_normal((M, K)).astype(np.float16)
+    A, sa = O.quant_act_i8(X)
+    return A, sa, W8, sw
+
+
+@pytest.mark.parametrize("M,N,K", [(64, 256, 64), (100, 320, 128), (256, 512, 3840), (128, 15360, 3840),
+                                   (300, 3840, 15360)])
+@pytest.mark.parametrize("swdt", [np.float32, np.float16])
+def test_w8a8_bit_exact(gpu, M, N, K, swdt):
+    rng = np.random.default_rng(M * 3 + N + K)
+    A, sa, W8, sw = _w8a8_case(rng, M, N, K)
+    sw_used = sw.astype(swdt)
+    C, Y = O.gemm_w8a8_ref(A, W8, sa, sw_used.astype(np.float32))
+    gY, gC = gpu.gemm_w8a8(torch.from_numpy(A).cuda(), torch.from_numpy(W8).cuda(), torch.from_numpy(sa).cuda(),
+                           torch.from_numpy(sw_used).cuda(), want_c=True)
+    assert (to_np(gC) == C).all()
+    assert (to_np(gY).view(np.uint16) == Y.view(np.uint16)).all()
+
+
+def test_w8a8_config_size_rows(gpu):
+    """M=2048, N=15360, K=3840. The int32 accumulator of 96 rows
+    (spread over all M-tiles) and every fp16 output are checked bit-exactly."""
+    rng = np.random.default_rng(0)
+    M, N, K = 2048, 15360, 3840
+    codes = rng.integers(-8, 8, (N, K))
+    s = np.abs(rng.normal(0, 0.02, (N, K // 32))).astype(np.float16).astype(np.float32)
+    q = (codes + 8).astype(np.uint8)
+    W8, sw = O.w8_fold(q, s)
+    X = rng.standard_normal((M, K)).astype(np.float16)
+    A, sa = O.quant_act_i8(X)
+    gA, gsa = gpu.quant_act_i8(torch.from_numpy(X).cuda())
+    assert (to_np(gA) == A).all() and (to_np(gsa) == sa).all()
+    gY, gC = gpu.gemm_w8a8(gA, torch.from_numpy(W8).cuda(), gsa, torch.from_numpy(sw).cuda(), want_c=True)
+    rows = np.sort(rng.choice(M, 96, replace=False))
+    C = O.int_matmul_exact(A[rows], W8)
+    assert (to_np(gC[torch.from_numpy(rows).cuda()]) == C).all()
+    Y = O.w8a8_epilogue(to_np(gC), sa, sw)   # epilogue on every element, from the (pinned) accumulator
+    assert (to_np(gY).view(np.uint16) == Y.view(np.uint16)).all()
+
+
+# ------------------------------------------------------------------ W4A8
+@pytest.mark.parametrize("M,N,K", [(64, 256, 64), (100, 512, 3840), (128, 15360, 3840)])
+def test_w4a8_bit_exact(gpu, M, N, K):
+    rng = np.random.default_rng(M + N + K + 1)
+    W = (rng.standard_normal((N, K)) * 0.08).astype(np.float32)
+    q, sc = O.quant_codes(W)
+    _, sw = O.w8_fold(q, sc)
+    ratio = O.w4a8_ratio(sc, sw)
+    B = O.w4a8_weights(q, ratio)
+    X = (rng.standard_normal((M, K)) * 0.3).astype(np.float32)
+    A, sa = O.quant_act_i8(X)
+    sw16 = sw.astype(np.float16)
+    C, Y = O.gemm_w8a8_ref(A, B, sa, sw16.astype(np.float32))
+    wq = torch.from_numpy(O.pack_dev(q).view(np.int32)).cuda()
+    r = torch.from_numpy(O.scales_dev(ratio)).cuda()
+    gY, gC = gpu.gemm_w4a8(torch.from_numpy(A).cuda(), wq, r, torch.from_numpy(sa).cuda(),
+                           torch.from_numpy(sw16).cuda(), N, want_c=True)
+    assert (to_np(gC) == C).all()
+    assert (to_np(gY).view(np.uint16) == Y.view(np.uint16)).all()
+
+
+# ----------------------------------------------------------------- W4A16
+@pytest.mark.parametrize("M,N,K", [(64, 256, 32), (100, 320, 96), (128, 3840, 15360), (512, 15360, 3840),
+                                   (512, 3840, 15360)])
+def test_w4a16(gpu, M, N, K):
+    rng = np.random.default_rng(M + 2 * N + K)
+    q, s = synth_int4(rng, N, K)
+    X = rng.standard_normal((M, K)).astype(np.float16)
+    ref = O.gemm_w4a16_ref(X, q, s)
+    wq, sc = upload_int4(q, s)
+    Y = gpu.gemm_w4a16(torch.from_numpy(X).cuda(), wq, sc, N)
+    Yh = to_np(Y).astype(np.float32)
+    err = O.normwise_rel_err(Yh, ref)
+    assert err <= 1e-3, err
+    assert O.cosine(Yh, ref) > 0.99999
+
+
+def test_w4a16_matches_f16_rounded_weights(gpu):
+    """The kernel's dequant is f16((q-8)*s) per weight: against that exact
+    product (computed in float64) the only remaining error is fp32
+    accumulation and the final fp16 rounding."""
+    rng = np.random.default_rng(31)
+    M, N, K = 96, 384, 512
+    q, s = synth_int4(rng, N, K)
+    X = rng.standard_normal((M, K)).astype(np.float16)
+    Wh = O.dequant(q, s).astype(np.float16).astype(np.float64)
+    ref = X.astype(np.float64) @ Wh.T
+    wq, sc = upload_int4(q, s)
+    Y = to_np(gpu.gemm_w4a16(torch.from_numpy(X).cuda(), wq, sc, N)).astype(np.float64)
+    assert np.abs(Y - ref).max() <= np.abs(ref).max() * 2.0 ** -11 * 1.01

@@ -1,0 +1,194 @@
+"""Decode GEMV (fp16 and e4m3 block scales) vs the oracle.
+
+Tolerance: normwise max|y - ref| / max|ref| <= 1e-3 with the oracle's fp32
+dequant+matmul (the reference's own numpy formulation) on the same inputs;
+fp32 outputs are held to 2e-5. Full-size shapes are checked entirely against
+the oracle plus size-independent properties (linearity, split invariance,
+determinism, graph replay == eager).
+"""
+import numpy as np
+import pytest
+import torch
+
+from oracle import q4_oracle as O
+from tests.helpers import synth_int4, to_np, upload_int4
+
+pytestmark = pytest.mark.gpu
+TOL_F16 = 1e-3
+TOL_F32 = 2e-5
+
+
+def _case(rng, N, K):
+    q, s = synth_int4(rng, N, K)
+    x = rng.standard_normal(K).astype(np.float16)
+    return q, s, x
+
+
+@pytest.mark.parametrize("N,K", [(64, 32), (100, 96), (256, 256), (4096, 3840), (3840, 4096), (2048, 3840)])
+@pytest.mark.parametrize("xdt,ydt", [(torch.float16, torch.float16), (torch.float16, torch.float32),
+                                     (torch.float32, torch.float32)])
+def test_gemv_f16_scales(gpu, N, K, xdt, ydt):
+    rng = np.random.default_rng(N * 7 + K)
+    q, s, x = _case(rng, N, K)
+    xin = x.astype(np.float32) if xdt == torch.float32 else x
+    ref = O.gemv_ref(q, s, xin)
+    wq, sc = upload_int4(q, s)
+    y = gpu.gemv(torch.from_numpy(xin).cuda(), wq, sc, N, K, y_dtype=ydt)
+    err = O.normwise_rel_err(to_np(y).astype(np.float32), ref)
+    assert err <= (TOL_F16 if ydt == torch.float16 else TOL_F32), err
+
+
+@pytest.mark.parametrize("split", [1, 2, 3, 5, 8, 120])
+def test_gemv_split_invariance(gpu, split):
+    rng = np.random.default_rng(21)
+    N, K = 512, 3840
+    q, s, x = _case(rng, N, K)
+    ref = O.gemv_ref(q, s, x)
+    wq, sc = upload_int4(q, s)
+    y = gpu.gemv(torch.from_numpy(x).cuda(), wq, sc, N, K, y_dtype=torch.float32, split=split)
+    assert O.normwise_rel_err(to_np(y), ref) <= TOL_F32
+
+
+def test_gemv_c1_full_size(gpu):
+    """configs[0] shape: N=15360, K=3840, fp16 x and y, seeded as the config states."""
+    rng = np.random.default_rng(0)
+    x = rng.standard_normal(3840).astype(np.float16)
+    codes = rng.integers(-8, 8, (15360, 3840))
+    s = np.abs(rng.normal(0, 0.02, (15360, 120))).astype(np.float16).astype(np.float32)
+    q = (codes + 8).astype(np.uint8)
+    ref = O.gemv_ref(q, s, x)
+    wq, sc = upload_int4(q, s)
+    y = gpu.gemv(torch.from_numpy(x).cuda(), wq, sc, 15360, 3840)
+    yh = to_np(y)
+    assert yh.dtype == np.float16
+    assert O.normwise_rel_err(yh.astype(np.float32), ref) <= TOL_F16
+    assert O.cosine(yh, ref) > 0.99999
+    # deterministic: same bits on a second launch (fixed split-K reduction order)
+    y2 = gpu.gemv(torch.from_numpy(x).cuda(), wq, sc, 15360, 3840)
+    assert torch.equal(y, y2)
+
+
+def test_gemv_e4m3_scales(gpu):
+    """e4m3 block scales; the oracle uses identically rounded scales."""
+    rng = np.random.default_rng(2)
+    for N, K in [(256, 256), (15360, 3840), (3840, 15360)]:
+        q, s, x = _case(rng, N, K)
+        e8, inv, _ = O.e4m3_lift(s)
+        s_used = O.e4m3_decode(e8)
+        ref = O.gemv_ref(q, s_used, x, inv=inv)
+        wq, _ = upload_int4(q, s)
+        sc8 = torch.from_numpy(O.scales_dev(e8)).cuda()
+        y = gpu.gemv(torch.from_numpy(x).cuda(), wq, sc8, N, K, scale_fmt=gpu.SCALE_E4M3, inv=inv,
+                     y_dtype=torch.float32)
+        assert O.normwise_rel_err(to_np(y), ref) <= TOL_F32
+
+
+def test_gemv_e4m3_from_gpu_quantizer(gpu):
+    rng = np.random.default_rng(3)
+    N, K = 1024, 3840
+    W = (rng.standard_normal((N, K)) * 0.05).astype(np.float32)
+    x = rng.standard_normal(K).astype(np.float32)
+    q, sc = O.quant_codes(W)
+    e8, inv, _ = O.e4m3_lift(sc)
+    ref = O.gemv_ref(q, O.e4m3_decode(e8), x, inv=inv)
+    wq, _sc16, sc32 = gpu.quantize(torch.from_numpy(W).cuda())
+    sc8, ginv = gpu.scales_e4m3(sc32, N, K)
+    y = gpu.gemv(torch.from_numpy(x).cuda(), wq, sc8, N, K, scale_fmt=gpu.SCALE_E4M3, inv=ginv)
+    assert O.normwise_rel_err(to_np(y), ref) <= TOL_F32
+
+
+def test_gemv_lm_head_rows(gpu):
+    """lm_head shape N=262144, K=3840 (no split-K): every row checked in row slices."""
+    N, K = 262144, 3840
+    g = torch.Generator(device="cuda").manual_seed(5)
+    nblk = K // 32
+    words = torch.randint(-2 ** 31, 2 ** 31 - 1, (N * nblk * 4,), dtype=torch.int64, device="cuda",
+                          generator=g).to(torch.int32)
+    sc = (torch.randn(N * nblk, device="cuda", generator=g) * 0.02).abs().to(torch.float16)
+    x = torch.randn(K, device="cuda", generator=g).to(torch.float16)
+    y = to_np(gpu.gemv(x, words, sc, N, K, y_dtype=torch.float32))
+    wh, sh, xh = to_np(words).view(np.uint32), to_np(sc), to_np(x)
+    npan = 256                                              # 16384-row slices: first, middle, last
+    for p0 in (0, 1024, 2048 + 37, N // 64 - npan):
+        sl = slice(p0 * nblk * 64 * 4, (p0 + npan) * nblk * 64 * 4)
+        rows = npan * 64
+        q = O.unpack_dev(wh[sl], rows, K)
+        s = O.unscales_dev(sh[p0 * nblk * 64:(p0 + npan) * nblk * 64], rows, nblk).astype(np.float32)
+        ref = O.gemv_ref(q, s, xh)
+        assert O.normwise_rel_err(y[p0 * 64:p0 * 64 + rows], ref) <= TOL_F32
+
+
+def test_gemv_linearity_full_size(gpu):
+    """y(a x1 + b x2) == a y(x1) + b y(x2) at the gate_up shape (size-independent property)."""
+    N, K = 30720, 3840
+    g = torch.Generator(device="cuda").manual_seed(9)
+    words = torch.randint(-2 ** 31, 2 ** 31 - 1, (N * (K // 32) * 4,), dtype=torch.int64, device="cuda",
+                          generator=g).to(torch.int32)
+    sc = (torch.randn(N * (K // 32), device="cuda", generator=g) * 0.02).abs().to(torch.float16)
+    x1 = torch.randn(K, device="cuda", generator=g)
+    x2 = torch.randn(K, device="cuda", generator=g)
+    y1 = gpu.gemv(x1, words, sc, N, K)
+    y2 = gpu.gemv(x2, words, sc, N, K)
+    y3 = gpu.gemv(0.5 * x1 + 2.0 * x2, words, sc, N, K)
+    comb = 0.5 * y1 + 2.0 * y2
+    rel = (y3 - comb).abs().max() / comb.abs().max()
+    assert rel.item() < 1e-5
+
+
+def test_gemv_output_offset_and_untouched_neighbours(gpu):
+    rng = np.random.default_rng(6)
+    N, K = 200, 128
+    q, s, x = _case(rng, N, K)
+    wq, sc = upload_int4(q, s)
+    out = torch.full((N + 64,), 7.0, device="cuda")
+    gpu.gemv(torch.from_numpy(x.astype(np.float32)).cuda(), wq, sc, N, K, y=out[32:32 + N])
+    o = to_np(out)
+    assert (o[:32] == 7.0).all() and (o[32 + N:] == 7.0).all()
+    assert O.normwise_rel_err(o[32:32 + N], O.gemv_ref(q, s, x)) <= TOL_F32
+
+
+def test_gemv_graph_replay_matches_eager(gpu):
+    """A captured sequence of split-K GEMVs sharing one workspace replays
+    bit-identically to eager execution, replay after replay."""
+    rng = np.random.default_rng(7)
+    shapes = [(4096, 3840), (2048, 3840), (3840, 4096), (3840, 15360), (15360, 3840)]
+    mats = []
+    for N, K in shapes:
+        q, s = synth_int4(rng, N, K)
+        wq, sc = upload_int4(q, s)
+        x = torch.from_numpy(rng.standard_normal(K).astype(np.float16)).cuda()
+        mats.append((N, K, wq, sc, x, torch.empty(N, device="cuda")))
+    ws = gpu.Workspace(max(gpu.Workspace.bytes_for(N, K) for N, K in shapes))
+
+    def body():
+        for N, K, wq, sc, x, y in mats:
+            gpu.gemv(x, wq, sc, N, K, y=y, ws=ws)
+
+    body()
+    torch.cuda.synchronize()
+    eager = [m[5].clone() for m in mats]
+    for m in mats:
+        m[5].zero_()
+    graph = gpu.Graph()
+    with graph.capture():
+        body()
+    for _ in range(3):
+        for m in mats:
+            m[5].zero_()
+        torch.cuda.synchronize()
+        graph.launch()
+        gpu.stream_wait(graph.stream)
+        for m, e in zip(mats, eager):
+            assert torch.equal(m[5], e)
+        torch.cuda.synchronize()
+    graph.destroy()
+
+
+def test_gemv_rejects_small_workspace(gpu):
+    N, K = 2048, 3840
+    wq = torch.zeros(N * K // 8, dtype=torch.int32, device="cuda")
+    sc = torch.zeros(N * K // 32, dtype=torch.float16, device="cuda")
+    x = torch.zeros(K, dtype=torch.float16, device="cuda")
+    small = gpu.Workspace(256)
+    with pytest.raises(gpu._lib.Q4Error, match="workspace"):
+        gpu.gemv(x, wq, sc, N, K, ws=small, split=8)

@@ -1,0 +1,83 @@
+"""Host-side logic on the CPU: error mapping, the labelled fence-timeout
+message the reference's callers match on (src/vk_engine.py:299-302,
+src/serve.py:49), split/workspace bookkeeping, and loud failure without a
+GPU. The timeout is forced from the host (the wait entry point reports
+expiry), so no GPU work is involved."""
+import ctypes as C
+import importlib
+
+import pytest
+
+
+class _FakeLib:
+    def __init__(self, status, msg=b""):
+        self.status, self.msg = status, msg
+
+    def q4_stream_wait(self, stream, ms):
+        return self.status
+
+    def q4_last_error(self):
+        return self.msg
+
+
+@pytest.fixture
+def ops(g4, monkeypatch):
+    ops = importlib.import_module("g4mi.ops")
+    monkeypatch.setattr(ops, "_stream", lambda s=None: C.c_void_p(0))
+    return ops
+
+
+def test_fence_timeout_message(ops, g4, monkeypatch):
+    fake = _FakeLib(g4._lib.Q4_ERR_TIMEOUT, b"stream wait timed out after 5 ms")
+    monkeypatch.setattr(ops, "lib", lambda: fake)
+    monkeypatch.setattr(g4._lib, "lib", lambda path=None: fake)
+    with pytest.raises(RuntimeError, match=r"GPU fence TIMEOUT after 5ms at \[decode pos=7\]"):
+        ops.stream_wait(None, 5, "decode pos=7")
+
+
+def test_wait_other_error_is_q4error(ops, g4, monkeypatch):
+    fake = _FakeLib(g4._lib.Q4_ERR_HIP, b"hipStreamQuery failed: boom")
+    monkeypatch.setattr(ops, "lib", lambda: fake)
+    monkeypatch.setattr(g4._lib, "lib", lambda path=None: fake)
+    with pytest.raises(g4._lib.Q4Error, match="boom"):
+        ops.stream_wait(None, 5, "x")
+
+
+def test_wait_ok(ops, g4, monkeypatch):
+    fake = _FakeLib(0)
+    monkeypatch.setattr(ops, "lib", lambda: fake)
+    ops.stream_wait(None, 0, "x")
+
+
+def test_engine_wait_uses_env_bound(g4, monkeypatch):
+    E = importlib.import_module("g4mi.vk_engine")
+    seen = {}
+    monkeypatch.setattr(E.ops, "stream_wait", lambda s, ms, label: seen.update(ms=ms, label=label))
+    monkeypatch.setattr(E, "_FENCE_MS", 1234)
+    E.wait(None, "decode pos=3")
+    assert seen == {"ms": 1234, "label": "decode pos=3"}
+
+
+def test_call_raises_with_library_message(g4):
+    with pytest.raises(g4._lib.Q4Error, match="multiple of 32"):
+        g4._lib.call("q4_dev_bytes", 64, 33, None, None)
+
+
+def test_ops_reject_host_tensors(ops):
+    torch = pytest.importorskip("torch")
+    with pytest.raises(ValueError, match="device tensors"):
+        ops._p(torch.zeros(4))
+
+
+def test_graph_capture_refuses_workspace_allocation(ops, g4, monkeypatch):
+    monkeypatch.setattr(ops, "_CAPTURING", [1])
+    with pytest.raises(RuntimeError, match="before the capture"):
+        ops.default_workspace(2048, 3840)
+
+
+def test_split_matches_library(ops, g4):
+    for N, K in [(15360, 3840), (262144, 3840), (3840, 15360), (2048, 3840), (30720, 3840)]:
+        s = ops.auto_split(N, K)
+        assert 1 <= s <= K // 32
+        ws = ops.Workspace.bytes_for(N, K)
+        assert (ws == 0) == (s == 1)
