@@ -1,0 +1,311 @@
+"""Benchmark of the int4/int8 quantized matmul path on one MI355X.
+
+Default workload (the headline, one "step" = one decoded token): the decode
+GEMV set of 48 distinct Gemma-style layers {q 4096x3840, k 2048x3840,
+v 2048x3840, o 3840x4096, fused gate_up 30720x3840, down 3840x15360} plus
+lm_head 262144x3840, int4 block-32 codes with fp16 scales, fp16 activations
+and outputs, captured once as a hipGraph and replayed per token. Every
+weight byte is distinct (6.6 GB per token), so the 256 MB Infinity Cache
+cannot serve repeats. value = algorithmic bytes per token / time per token.
+
+Also measured in the same run: the W8A8 prefill GEMM at M=2048, N=15360,
+K=3840 (int8 MFMA) and the W4A16 GEMM at M=512 (f16 MFMA), each as a
+fraction of MI355X's dense peak, and the CPU baseline (the oracle's numpy
+dequant+matmul, the reference's own formulation) on a bounded sample.
+
+Data are synthetic (random codes/scales/activations of the stated shapes).
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+from pathlib import Path
+
+ROOT = Path(__file__).resolve().parent
+sys.path.insert(0, str(ROOT))
+
+METRIC = "int4 GEMV HBM GB/s (% of 8 TB/s) + W8A8 prefill GEMM TOPS (% int8 MFMA peak)"
+HBM_PEAK_GBS = 8000.0
+INT8_PEAK_TOPS = 5000.0      # dense int8 MFMA, MI355X
+F16_PEAK_TFLOPS = 2500.0     # dense f16 MFMA, MI355X
+H, QN, KVN, I, V = 3840, 4096, 2048, 15360, 262144
+LAYERS = 48
+LAYER_SHAPES = [("q", QN, H), ("k", KVN, H), ("v", KVN, H), ("o", H, QN), ("gate_up", 2 * I, H), ("down", H, I)]
+
+
+def gemv_bytes(N: int, K: int, scale_bytes: int = 2) -> int:
+    """Algorithmic bytes of one int4 GEMV: weights, block scales, fp16 x, fp16 y."""
+    return N * K // 2 + (N * K // 32) * scale_bytes + 2 * K + 2 * N
+
+
+def load_ops():
+    import importlib
+
+    import __graft_entry__ as G
+
+    G.load_package()
+    return importlib.import_module("g4mi.ops")
+
+
+# ------------------------------------------------------------- GPU legs
+def bench_decode(ops, steps: int, warmup: int):
+    import torch
+
+    dev = torch.device("cuda:0")
+    gen = torch.Generator(device=dev).manual_seed(0)
+    mats = []
+
+    def make(N, K):
+        words = torch.randint(-2 ** 31, 2 ** 31 - 1, (N * K // 8,), dtype=torch.int64, device=dev,
+                              generator=gen).to(torch.int32)
+        sc = (torch.randn(N * K // 32, device=dev, generator=gen) * 0.02).abs().to(torch.float16)
+        return words, sc
+
+    xs = {K: torch.randn(K, device=dev, generator=gen).to(torch.float16) for K in (H, QN, I)}
+    ys = {}
+    for _ in range(LAYERS):
+        for name, N, K in LAYER_SHAPES:
+            w, s = make(N, K)
+            ys.setdefault(name, torch.empty(N, dtype=torch.float16, device=dev))
+            mats.append((name, N, K, w, s))
+    w, s = make(V, H)
+    ys["lm_head"] = torch.empty(V, dtype=torch.float16, device=dev)
+    mats.append(("lm_head", V, H, w, s))
+    ws = ops.Workspace(max(ops.Workspace.bytes_for(N, K) for _, N, K, _, _ in mats))
+    torch.cuda.synchronize()
+
+    def token():
+        for name, N, K, w, s in mats:
+            ops.gemv(xs[K], w, s, N, K, y=ys[name], ws=ws)
+
+    graph = ops.Graph()
+    with graph.capture():
+        token()
+    st = graph.stream
+    for _ in range(warmup):
+        graph.launch()
+    torch.cuda.synchronize()
+    t0 = torch.cuda.Event(enable_timing=True)
+    t1 = torch.cuda.Event(enable_timing=True)
+    t0.record(st)
+    for _ in range(steps):
+        graph.launch()
+    t1.record(st)
+    t1.synchronize()
+    torch.cuda.synchronize()
+    ms = t0.elapsed_time(t1) / steps
+    nbytes = sum(gemv_bytes(N, K) for _, N, K, _, _ in mats)
+    launches = len(mats)
+    # per-shape kernel time: one graph of the 48 same-shape launches per shape, same stream
+    per_shape = {}
+    for name in [n for n, _, _ in LAYER_SHAPES] + ["lm_head"]:
+        sel = [m for m in mats if m[0] == name]
+        g2 = ops.Graph(st)
+        with g2.capture():
+            for _, N, K, w, s in sel:
+                ops.gemv(xs[K], w, s, N, K, y=ys[name], ws=ws)
+        reps = max(3, 480 // len(sel))
+        for _ in range(2):
+            g2.launch()
+        a = torch.cuda.Event(enable_timing=True)
+        b = torch.cuda.Event(enable_timing=True)
+        a.record(st)
+        for _ in range(reps):
+            g2.launch()
+        b.record(st)
+        b.synchronize()
+        us = a.elapsed_time(b) * 1e3 / (reps * len(sel))
+        N, K = sel[0][1], sel[0][2]
+        per_shape[name] = {"N": N, "K": K, "us_per_launch": round(us, 3),
+                           "GBps": round(gemv_bytes(N, K) / us / 1e3, 1), "split": ops.auto_split(N, K)}
+        g2.destroy()
+    graph.destroy()
+    del mats, ws
+    torch.cuda.empty_cache()
+    return {"ms_per_step": ms, "bytes_per_step": nbytes, "launches": launches,
+            "GBps": nbytes / (ms * 1e-3) / 1e9, "per_shape": per_shape}
+
+
+def bench_w8a8(ops, iters: int = 50):
+    import torch
+
+    dev = torch.device("cuda:0")
+    gen = torch.Generator(device=dev).manual_seed(1)
+    M, N, K = 2048, 15360, 3840
+    X = torch.randn((M, K), device=dev, generator=gen).to(torch.float16)
+    W8s = [torch.randint(-127, 128, (N, K), device=dev, generator=gen, dtype=torch.int8) for _ in range(4)]
+    sw = (torch.rand(N, device=dev, generator=gen) * 1e-3 + 1e-4).to(torch.float32)
+    A, sa = ops.quant_act_i8(X)
+    Y = torch.empty((M, N), dtype=torch.float16, device=dev)
+    st = torch.cuda.current_stream()
+    for i in range(5):
+        ops.gemm_w8a8(A, W8s[i % 4], sa, sw, Y=Y)
+    a = torch.cuda.Event(enable_timing=True)
+    b = torch.cuda.Event(enable_timing=True)
+    a.record(st)
+    for i in range(iters):
+        ops.gemm_w8a8(A, W8s[i % 4], sa, sw, Y=Y)
+    b.record(st)
+    b.synchronize()
+    us = a.elapsed_time(b) * 1e3 / iters
+    # activation quantizer (bandwidth-bound: 2MK read + MK write)
+    a.record(st)
+    for _ in range(iters):
+        ops.quant_act_i8(X, A, sa)
+    b.record(st)
+    b.synchronize()
+    us_q = a.elapsed_time(b) * 1e3 / iters
+    tops = 2.0 * M * N * K / (us * 1e-6) / 1e12
+    return {"M": M, "N": N, "K": K, "us": round(us, 2), "TOPS": round(tops, 1),
+            "frac_of_int8_peak": round(tops / INT8_PEAK_TOPS, 4),
+            "quant_act_us": round(us_q, 2), "quant_act_GBps": round(3 * M * K / (us_q * 1e-6) / 1e9, 1)}
+
+
+def bench_w4a16(ops, iters: int = 30):
+    import torch
+
+    dev = torch.device("cuda:0")
+    gen = torch.Generator(device=dev).manual_seed(2)
+    out = {}
+    for M, N, K in [(512, 15360, 3840), (512, 3840, 15360)]:
+        X = torch.randn((M, K), device=dev, generator=gen).to(torch.float16)
+        words = torch.randint(-2 ** 31, 2 ** 31 - 1, (N * K // 8,), dtype=torch.int64, device=dev,
+                              generator=gen).to(torch.int32)
+        sc = (torch.randn(N * K // 32, device=dev, generator=gen) * 0.02).abs().to(torch.float16)
+        Y = torch.empty((M, N), dtype=torch.float16, device=dev)
+        st = torch.cuda.current_stream()
+        for _ in range(3):
+            ops.gemm_w4a16(X, words, sc, N, Y=Y)
+        a = torch.cuda.Event(enable_timing=True)
+        b = torch.cuda.Event(enable_timing=True)
+        a.record(st)
+        for _ in range(iters):
+            ops.gemm_w4a16(X, words, sc, N, Y=Y)
+        b.record(st)
+        b.synchronize()
+        us = a.elapsed_time(b) * 1e3 / iters
+        tf = 2.0 * M * N * K / (us * 1e-6) / 1e12
+        out[f"M{M}_N{N}_K{K}"] = {"us": round(us, 2), "TFLOPS": round(tf, 1),
+                                 "frac_of_f16_peak": round(tf / F16_PEAK_TFLOPS, 4)}
+    return out
+
+
+# --------------------------------------------------------- CPU baseline
+def cpu_baseline(budget_s: float = 15.0):
+    """The oracle's numpy GEMV (dequant + matmul, the reference's formulation)
+    over whole layers of the decode set, repeated until ~budget_s of CPU work."""
+    import numpy as np
+
+    from oracle import q4_oracle as O
+
+    rng = np.random.default_rng(0)
+    x = {K: rng.standard_normal(K).astype(np.float16) for K in (H, QN, I)}
+    layer = []
+    for name, N, K in LAYER_SHAPES:
+        q = rng.integers(0, 16, (N, K), dtype=np.uint8)
+        s = np.abs(rng.normal(0, 0.02, (N, K // 32))).astype(np.float16).astype(np.float32)
+        layer.append((N, K, q, s))
+    t_total, nbytes, gemvs, layers = 0.0, 0, 0, 0
+    while t_total < budget_s and layers < 64:
+        for N, K, q, s in layer:
+            t0 = time.perf_counter()
+            O.gemv_ref(q, s, x[K]).astype(np.float16)
+            t_total += time.perf_counter() - t0
+            nbytes += gemv_bytes(N, K)
+            gemvs += 1
+        layers += 1
+    threads = None
+    try:
+        from threadpoolctl import threadpool_info
+
+        threads = max((p.get("num_threads") or 0) for p in threadpool_info()) or None
+    except Exception:
+        pass
+    if threads is None:
+        threads = int(os.environ.get("OMP_NUM_THREADS", "1"))
+    return {"value": round(nbytes / t_total / 1e9, 3), "unit": "GB/s", "cores": threads, "kind": "port",
+            "sample": f"{layers} decode layers ({gemvs} GEMVs, {nbytes / 1e9:.2f} GB algorithmic) of the same "
+                      f"shapes through the oracle's numpy dequant+matmul in {t_total:.1f} s; "
+                      f"os.cpu_count()={os.cpu_count()}, affinity={len(os.sched_getaffinity(0))}"}
+
+
+def main():
+    ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=200)
+    ap.add_argument("--warmup", type=int, default=20)
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
+    ap.add_argument("--no-gemm", action="store_true", help="skip the prefill GEMM legs")
+    ap.add_argument("--cpu-budget", type=float, default=15.0)
+    args = ap.parse_args()
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
+        print("bench.py measures one GPU: this path is a single-GPU kernel set (multi-GPU sharding is "
+              "design-only); run with --gpus 1", file=sys.stderr)
+        sys.exit(2)
+
+    import torch
+
+    torch.cuda.set_device(0)
+    ops = load_ops()
+    print(f"[bench] decode graph: {LAYERS} layers + lm_head, {args.steps} steps after {args.warmup} warmup",
+          flush=True)
+    dec = bench_decode(ops, args.steps, args.warmup)
+    print(f"[bench] decode {dec['ms_per_step']:.3f} ms/token, {dec['GBps']:.0f} GB/s", flush=True)
+    w8 = w4 = None
+    if not args.no_gemm:
+        w8 = bench_w8a8(ops)
+        print(f"[bench] w8a8 {w8}", flush=True)
+        w4 = bench_w4a16(ops)
+        print(f"[bench] w4a16 {w4}", flush=True)
+    cpu = None
+    if not args.no_cpu:
+        cpu = cpu_baseline(args.cpu_budget)
+        print(f"[bench] cpu {cpu}", flush=True)
+
+    ms = dec["ms_per_step"]
+    per_launch_us = ms * 1e3 / dec["launches"]
+    achieved = dec["bytes_per_step"] / dec["launches"] / (per_launch_us * 1e-6) / 1e9
+    line = {
+        "metric": METRIC,
+        "value": round(dec["GBps"], 1),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "i4xf16->f32",
+        "data": "synthetic",
+        "config": {
+            "workload": "decode-step int4 GEMV set: 48 distinct layers {q 4096x3840, k 2048x3840, v 2048x3840, "
+                        "o 3840x4096, gate_up 30720x3840, down 3840x15360} + lm_head 262144x3840, block-32 fp16 "
+                        "scales, fp16 x/y, one hipGraph replay per token",
+            "bytes_per_step": dec["bytes_per_step"],
+            "kernels_per_step": dec["launches"],
+            "frac_of_hbm_peak": round(dec["GBps"] / HBM_PEAK_GBS, 4),
+            "per_shape": dec["per_shape"],
+        },
+        "roofline": {
+            "bound": "hbm",
+            "kernel": "gemv_kernel<f16 x, f16 scales, f16 y>",
+            "achieved": round(achieved, 1),
+            "peak": HBM_PEAK_GBS,
+            "unit": "GB/s",
+            "frac": round(achieved / HBM_PEAK_GBS, 4),
+            "traffic": None,
+            "avg_launch_us": round(per_launch_us, 3),
+        },
+        "cpu_baseline": cpu,
+        "w8a8": w8,
+        "w4a16": w4,
+    }
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

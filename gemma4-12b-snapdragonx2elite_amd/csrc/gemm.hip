@@ -250,7 +250,7 @@ __global__ void __launch_bounds__(256) gemm_kernel(const GemmArgs g) {
         } else {
           const int c = acc[i][j][r];
           if (g.C) g.C[o] = c;
-          if (g.Y) g.Y[o] = f2h(__fmul_rn(__fmul_rn((float)c, g.sa[m]), swn));
+          if (g.Y) g.Y[o] = f2h_after_f32(__fmul_rn(__fmul_rn((float)c, g.sa[m]), swn));
         }
       }
     }

@@ -38,6 +38,11 @@ constexpr int GEMV_WAVES = GEMV_THREADS / 64;
 constexpr int GEMV_MAXB = 128;    // blocks of x a workgroup stages (LDS cap)
 constexpr int GEMV_U = 8;         // units in flight per lane
 constexpr int GEMV_TARGET_WGS = 1024;
+// Split-K workspace layout: tickets for up to GEMV_MAX_TICKETS panels at a
+// fixed offset 0 (so GEMVs of different shapes sharing one workspace never
+// see each other's partials as tickets), then the fp32 partials.
+constexpr int GEMV_MAX_TICKETS = 16384;
+constexpr size_t GEMV_TICKET_BYTES = GEMV_MAX_TICKETS * sizeof(uint32_t);
 
 __device__ inline v2h as_h2(uint32_t v) { return __builtin_bit_cast(v2h, v); }
 
@@ -230,7 +235,7 @@ static int effective_split(int N, int K, int split) {
 static size_t ws_bytes(int N, int K, int split) {
   if (split <= 1) return 0;
   const size_t NP = (size_t)pad_rows(N);
-  size_t b = (size_t)split * NP * sizeof(float) + (NP / PANEL) * sizeof(uint32_t);
+  size_t b = GEMV_TICKET_BYTES + (size_t)split * NP * sizeof(float);
   return (b + 255) & ~(size_t)255;
 }
 
@@ -273,9 +278,9 @@ int q4_gemv(const void* x, int x_dtype, const uint32_t* wq, const void* scales, 
   Q4_ARG(need == 0 || (ws && ws_size >= need), "GEMV N=%d K=%d split=%d needs a %zu-byte workspace (got %zu)", N, K,
          s, need, ws ? ws_size : (size_t)0);
   const int panels = ceil_div(N, PANEL);
-  float* part = need ? reinterpret_cast<float*>(ws) : nullptr;
-  uint32_t* cnt = need ? reinterpret_cast<uint32_t*>(reinterpret_cast<char*>(ws) + (size_t)s * pad_rows(N) * 4)
-                       : nullptr;
+  Q4_ARG(need == 0 || panels <= GEMV_MAX_TICKETS, "split-K GEMV supports at most %d rows", GEMV_MAX_TICKETS * PANEL);
+  uint32_t* cnt = need ? reinterpret_cast<uint32_t*>(ws) : nullptr;
+  float* part = need ? reinterpret_cast<float*>(reinterpret_cast<char*>(ws) + GEMV_TICKET_BYTES) : nullptr;
   const float outscale = scale_fmt == Q4_SCALE_E4M3 ? inv * 256.0f : 1.0f;
   gemv_fn fn = pick(x_dtype, scale_fmt, y_dtype);
   hipLaunchKernelGGL(fn, dim3(panels, s), dim3(GEMV_THREADS), 0, as_stream(stream), x,

@@ -75,6 +75,16 @@ __device__ inline uint16_t f2h(float f) {
   return __half_as_ushort(__float2half_rn(f));
 }
 
+// Round an fp32 value that is the result of an fp32 operation to fp16.
+// The empty asm pins the fp32 rounding of that operation: without it the
+// compiler may fold "fp32 multiply, then fp16 convert" into one
+// mixed-precision instruction that rounds the exact product straight to
+// fp16, which differs from numpy's two roundings at fp16 half-way points.
+__device__ inline uint16_t f2h_after_f32(float f) {
+  asm volatile("" : "+v"(f));
+  return f2h(f);
+}
+
 // e4m3fn byte -> f16 bits holding value * 2^-8 (exact for every code): the
 // 7 magnitude bits land in the f16 exponent/mantissa fields, so the e4m3
 // bias (7) becomes the f16 bias (15) and subnormals stay subnormal.

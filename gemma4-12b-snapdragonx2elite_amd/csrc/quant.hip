@@ -47,7 +47,7 @@ __global__ void quantize_kernel(const float* __restrict__ W, int N, int K, int n
     w[k >> 3] |= ((uint32_t)c & 15u) << (4 * nib_pos(k & 7));
   }
   wq[u] = make_uint4(w[0], w[1], w[2], w[3]);
-  sc16[u] = f2h(sc);
+  sc16[u] = f2h_after_f32(sc);
   if (sc32) sc32[(long)n * nblk + b] = sc;
 }
 
@@ -126,7 +126,7 @@ __global__ void __launch_bounds__(256) w8_fold_kernel(const uint4* __restrict__ 
   const float sw = fmaxf(__fdiv_rn(amax, 127.0f), 1e-12f);
   if (threadIdx.x == 0) {
     if (sw32) sw32[n] = sw;
-    if (sw16) sw16[n] = f2h(sw);
+    if (sw16) sw16[n] = f2h_after_f32(sw);
   }
   for (int b = threadIdx.x; b < nblk; b += blockDim.x) {
     float q[BLK];
@@ -160,7 +160,7 @@ __global__ void w4a8_ratio_kernel(const float* __restrict__ sc32, const float* _
   long pb = u / PANEL;
   int b = (int)(pb % nblk);
   int n = (int)(pb / nblk) * PANEL + r;
-  ratio[u] = (n < N) ? f2h(__fdiv_rn(sc32[(long)n * nblk + b], sw32[n])) : (uint16_t)0;
+  ratio[u] = (n < N) ? f2h_after_f32(__fdiv_rn(sc32[(long)n * nblk + b], sw32[n])) : (uint16_t)0;
 }
 
 // ---- repacks from the reference layouts ----------------------------------

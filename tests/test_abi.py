@@ -78,7 +78,7 @@ def test_sizes_and_split_queries(g4):
         s = lib.q4_gemv_auto_split(N, K)
         assert 1 < s <= K // 32
         ws = lib.q4_workspace_bytes(0, N, K, 0)
-        assert ws >= s * N * 4 + (N // 64) * 4 and ws % 256 == 0
+        assert ws >= 65536 + s * N * 4 and ws % 256 == 0
     assert lib.q4_workspace_bytes(0, 262144, 3840, 0) == 0
     # an explicit split too small for the LDS staging cap is raised
     assert lib.q4_workspace_bytes(0, 64, 15360, 1) > 0
