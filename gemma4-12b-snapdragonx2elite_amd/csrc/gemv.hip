@@ -10,10 +10,14 @@
 //    lane = row, and every 16-byte unit load of a wave covers 1 KB of
 //    contiguous HBM (one 32-element block of 64 rows). Scales of the same
 //    64 rows are 128 contiguous bytes.
-//  * A workgroup (4 waves) owns one panel and a contiguous block range;
-//    the x slice for that range is staged once in LDS (and summed per
-//    block), the 4 waves split the range, and an LDS reduction combines
-//    them. No cross-lane shuffles are needed in the inner loop.
+//  * A workgroup (4 waves) owns R consecutive rows of a panel (R = 8..64,
+//    chosen per shape so the grid has enough workgroups to fill 256 CUs)
+//    and the whole K range: lane = (row r, block slot), 64/R slots per wave,
+//    so each wave load covers R*16 contiguous bytes (>= one 128 B line) per
+//    block. The x vector is staged once per workgroup in LDS together with
+//    per-block sums; slots reduce with xor-shuffles and then across waves
+//    through LDS, in a fixed order (deterministic). No cross-workgroup
+//    communication is needed for any decode shape.
 //  * Register dequant without conversions: masking a word with 0x000F000F
 //    yields two fp16 subnormals q*2^-24; with 0x00F000F0, 16q*2^-24.
 //    v_dot2_f32_f16 multiplies them by an fp16 x pair with fp32
@@ -24,22 +28,23 @@
 //  * fp32 x (the engine's residual-stream activations) takes an exact fp32
 //    path: bytes of (w & 0x0F0F0F0F) and (w >> 4 & 0x0F0F0F0F) convert
 //    with v_cvt_f32_ubyteN and accumulate with FMAs.
-//  * K is split across workgroups when a matrix has too few panels to fill
-//    256 CUs. The last workgroup of a panel (atomic ticket) sums the fp32
-//    partials in split order and writes y, then re-arms the ticket, so one
-//    launch does the whole GEMV deterministically and the workspace stays
-//    ready for the next call (and for hipGraph replay) without a memset.
+//  * Matrices with fewer than 2048 rows also split K across workgroups; the
+//    last workgroup of a row group (atomic ticket, agent-scope
+//    release/acquire by one wave) sums the fp32 partials in split order and
+//    re-arms the ticket, so the launch stays single and deterministic and
+//    the workspace is ready for the next call (and hipGraph replay).
 #include "q4mi_common.h"
 
 namespace q4 {
 
 constexpr int GEMV_THREADS = 256;
 constexpr int GEMV_WAVES = GEMV_THREADS / 64;
-constexpr int GEMV_MAXB = 128;    // blocks of x a workgroup stages (LDS cap)
-constexpr int GEMV_U = 8;         // units in flight per lane
-constexpr int GEMV_TARGET_WGS = 1024;
-// Split-K workspace layout: tickets for up to GEMV_MAX_TICKETS panels at a
-// fixed offset 0 (so GEMVs of different shapes sharing one workspace never
+constexpr int GEMV_U = 8;                  // units in flight per lane
+constexpr int GEMV_LDS_MAX = 64 * 1024;    // x staging cap per workgroup (bytes)
+constexpr int GEMV_TARGET_WGS = 768;       // pick the largest R that still gives this many workgroups
+constexpr int GEMV_MIN_WGS = 256;          // below this, K is split across workgroups
+// Split-K workspace layout: tickets for up to GEMV_MAX_TICKETS row groups at
+// a fixed offset 0 (so GEMVs of different shapes sharing one workspace never
 // see each other's partials as tickets), then the fp32 partials.
 constexpr int GEMV_MAX_TICKETS = 16384;
 constexpr size_t GEMV_TICKET_BYTES = GEMV_MAX_TICKETS * sizeof(uint32_t);
@@ -92,30 +97,33 @@ __device__ inline float load_scale(const void* __restrict__ scv, long idx) {
   }
 }
 
-template <int XT, int ST, int YT>
+template <int R, int XT, int ST, int YT>
 __global__ void __launch_bounds__(GEMV_THREADS)
 gemv_kernel(const void* __restrict__ xv, const uint4* __restrict__ wq, const void* __restrict__ scv, float outscale,
             void* __restrict__ yv, int N, int nblk, int split, float* __restrict__ part, uint32_t* __restrict__ cnt) {
   constexpr bool XH = (XT == Q4_DT_F16);
-  __shared__ __attribute__((aligned(16))) uint32_t xs_h[XH ? GEMV_MAXB * 16 : 1];
-  __shared__ __attribute__((aligned(16))) float xs_f[XH ? 1 : GEMV_MAXB * BLK];
-  __shared__ float xsum[GEMV_MAXB];
-  __shared__ float red[GEMV_WAVES][64];
-  __shared__ int is_last;
+  constexpr int SW = 64 / R;               // block slots per wave
+  constexpr int S = SW * GEMV_WAVES;       // block slots per workgroup
+  extern __shared__ __attribute__((aligned(16))) uint32_t smem[];
+  __shared__ float red[GEMV_WAVES][R];
 
-  const int p = blockIdx.x, s = blockIdx.y;
+  const int g = blockIdx.x, s = blockIdx.y;
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+  const int r = lane % R, slot = wave * SW + lane / R;
   const int b_lo = (int)((long)s * nblk / split);
   const int nb = (int)((long)(s + 1) * nblk / split) - b_lo;
   const long k0 = (long)b_lo * BLK;
+  uint32_t* xs_h = smem;
+  float* xs_f = reinterpret_cast<float*>(smem);
+  float* xsum = reinterpret_cast<float*>(smem + (XH ? nb * 16 : nb * BLK));
 
-  // ---- stage the x slice [k0, k0 + 32 nb) ----
+  // ---- stage the x slice [k0, k0 + 32 nb) and its per-block sums ----
   if constexpr (XH) {
-    const uint32_t* x2 = reinterpret_cast<const uint32_t*>(xv) + k0 / 2;
-    for (int i = tid; i < nb * 16; i += GEMV_THREADS) xs_h[i] = x2[i];
+    const uint4* x4 = reinterpret_cast<const uint4*>(reinterpret_cast<const uint16_t*>(xv) + k0);
+    for (int i = tid; i < nb * 4; i += GEMV_THREADS) reinterpret_cast<uint4*>(xs_h)[i] = x4[i];
   } else {
-    const float* xf = reinterpret_cast<const float*>(xv) + k0;
-    for (int i = tid; i < nb * BLK; i += GEMV_THREADS) xs_f[i] = xf[i];
+    const float4* x4 = reinterpret_cast<const float4*>(reinterpret_cast<const float*>(xv) + k0);
+    for (int i = tid; i < nb * 8; i += GEMV_THREADS) reinterpret_cast<float4*>(xs_f)[i] = x4[i];
   }
   __syncthreads();
   for (int j = tid; j < nb; j += GEMV_THREADS) {
@@ -134,109 +142,130 @@ gemv_kernel(const void* __restrict__ xv, const uint4* __restrict__ wq, const voi
   }
   __syncthreads();
 
-  // ---- this wave's share of the block range ----
-  const int j_lo = wave * nb / GEMV_WAVES, j_hi = (wave + 1) * nb / GEMV_WAVES;
-  const long ubase = ((long)p * nblk + b_lo) * PANEL + lane;  // unit (p, b_lo + j) = ubase + 64 j
+  // ---- this lane's blocks: slot, slot + S, slot + 2S, ... ----
+  const int n0 = g * R;
+  const long ubase = ((long)(n0 / PANEL) * nblk + b_lo) * PANEL + (n0 % PANEL) + r;  // unit of block j: ubase + 64 j
   float acc = 0.0f;
-  for (int j = j_lo; j < j_hi; j += GEMV_U) {
+  for (int j = slot; j < nb; j += S * GEMV_U) {
     uint4 u[GEMV_U];
     float sc[GEMV_U];
 #pragma unroll
     for (int t = 0; t < GEMV_U; ++t) {
-      const int jj = min(j + t, j_hi - 1);
+      const int jj = min(j + t * S, nb - 1);
       u[t] = wq[ubase + (long)jj * PANEL];
       sc[t] = load_scale<ST>(scv, ubase + (long)jj * PANEL);
     }
 #pragma unroll
     for (int t = 0; t < GEMV_U; ++t) {
-      if (j + t < j_hi) {
+      const int jj = j + t * S;
+      if (jj < nb) {
         float d;
-        if constexpr (XH) d = block_dot_h(u[t], xs_h + (j + t) * 16, xsum[j + t]);
-        else d = block_dot_f(u[t], xs_f + (j + t) * BLK, xsum[j + t]);
+        if constexpr (XH) d = block_dot_h(u[t], xs_h + jj * 16, xsum[jj]);
+        else d = block_dot_f(u[t], xs_f + jj * BLK, xsum[jj]);
         acc = fmaf(sc[t], d, acc);
       }
     }
   }
-  red[wave][lane] = acc;
+  // slots of a row: lanes r, r + R, r + 2R, ... of each wave, then the 4 waves
+#pragma unroll
+  for (int off = R; off < 64; off <<= 1) acc += __shfl_xor(acc, off, 64);
+  if (lane < R) red[wave][r] = acc;
   __syncthreads();
+  if (wave != 0) return;
 
-  const int n = p * PANEL + lane;
+  const int n = n0 + r;
+  float v = 0.0f;
+  if (lane < R) v = (((red[0][r] + red[1][r]) + red[2][r]) + red[3][r]) * outscale;
   if (split == 1) {
-    if (wave == 0 && n < N) {
-      float v = ((red[0][lane] + red[1][lane]) + red[2][lane]) + red[3][lane];
-      v *= outscale;
+    if (lane < R && n < N) {
       if constexpr (YT == Q4_DT_F16) reinterpret_cast<uint16_t*>(yv)[n] = f2h(v);
       else reinterpret_cast<float*>(yv)[n] = v;
     }
     return;
   }
 
-  // ---- split-K: publish this workgroup's partial, last one reduces ----
-  const long NP = (long)gridDim.x * PANEL;
-  if (wave == 0) {
-    float v = ((red[0][lane] + red[1][lane]) + red[2][lane]) + red[3][lane];
-    part[(long)s * NP + n] = v * outscale;
-  }
-  __threadfence();
-  __syncthreads();
-  if (tid == 0) {
-    const uint32_t prev = atomicAdd(&cnt[p], 1u);
-    is_last = (prev == (uint32_t)(split - 1));
-  }
-  __syncthreads();
-  if (!is_last) return;
-  __threadfence();
-  if (wave == 0) {
-    float v = 0.0f;
+  // ---- split-K: publish this workgroup's partial; the last one reduces ----
+  const long NP = (long)gridDim.x * R;
+  if (lane < R) part[(long)s * NP + n] = v;
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");
+  uint32_t prev = 0;
+  if (lane == 0) prev = __hip_atomic_fetch_add(&cnt[g], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  prev = __shfl(prev, 0, 64);
+  if (prev != (uint32_t)(split - 1)) return;
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
+  if (lane < R) {
+    float t = 0.0f;
     for (int c = 0; c < split; ++c)
-      v += __hip_atomic_load(part + (long)c * NP + n, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      t += __hip_atomic_load(part + (long)c * NP + n, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     if (n < N) {
-      if constexpr (YT == Q4_DT_F16) reinterpret_cast<uint16_t*>(yv)[n] = f2h(v);
-      else reinterpret_cast<float*>(yv)[n] = v;
+      if constexpr (YT == Q4_DT_F16) reinterpret_cast<uint16_t*>(yv)[n] = f2h(t);
+      else reinterpret_cast<float*>(yv)[n] = t;
     }
   }
-  if (tid == 0) __hip_atomic_store(&cnt[p], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  if (lane == 0) __hip_atomic_store(&cnt[g], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
 typedef void (*gemv_fn)(const void*, const uint4*, const void*, float, void*, int, int, int, float*, uint32_t*);
 
-template <int XT, int ST>
+template <int R, int XT, int ST>
 static gemv_fn pick_y(int yt) {
-  return yt == Q4_DT_F16 ? gemv_kernel<XT, ST, Q4_DT_F16> : gemv_kernel<XT, ST, Q4_DT_F32>;
+  return yt == Q4_DT_F16 ? gemv_kernel<R, XT, ST, Q4_DT_F16> : gemv_kernel<R, XT, ST, Q4_DT_F32>;
 }
-template <int XT>
+template <int R, int XT>
 static gemv_fn pick_s(int st, int yt) {
-  return st == Q4_SCALE_E4M3 ? pick_y<XT, Q4_SCALE_E4M3>(yt) : pick_y<XT, Q4_SCALE_F16>(yt);
+  return st == Q4_SCALE_E4M3 ? pick_y<R, XT, Q4_SCALE_E4M3>(yt) : pick_y<R, XT, Q4_SCALE_F16>(yt);
 }
-static gemv_fn pick(int xt, int st, int yt) {
-  return xt == Q4_DT_F16 ? pick_s<Q4_DT_F16>(st, yt) : pick_s<Q4_DT_F32>(st, yt);
+template <int R>
+static gemv_fn pick_x(int xt, int st, int yt) {
+  return xt == Q4_DT_F16 ? pick_s<R, Q4_DT_F16>(st, yt) : pick_s<R, Q4_DT_F32>(st, yt);
 }
-
-static int auto_split(int N, int K) {
-  const int nblk = K / BLK;
-  const int panels = ceil_div(N, PANEL);
-  int s = ceil_div(GEMV_TARGET_WGS, panels);
-  const int cap = nblk / 8 > 0 ? nblk / 8 : 1;  // keep >= 8 blocks (2 per wave) per workgroup
-  if (s > cap) s = cap;
-  const int need = ceil_div(nblk, GEMV_MAXB);
-  if (s < need) s = need;
-  return s < 1 ? 1 : s;
+static gemv_fn pick(int R, int xt, int st, int yt) {
+  switch (R) {
+    case 64: return pick_x<64>(xt, st, yt);
+    case 32: return pick_x<32>(xt, st, yt);
+    case 16: return pick_x<16>(xt, st, yt);
+    default: return pick_x<8>(xt, st, yt);
+  }
 }
 
-static int effective_split(int N, int K, int split) {
-  const int nblk = K / BLK;
-  int s = split > 0 ? split : auto_split(N, K);
-  const int need = ceil_div(nblk, GEMV_MAXB);
-  if (s < need) s = need;
+struct GemvPlan {
+  int R, split, nb_max;
+  size_t lds, ws;
+};
+
+// Rows per workgroup and K split for an N x K GEMV. Q4MI_GEMV_ROWS
+// (8/16/32/64) overrides R for tuning sweeps.
+static GemvPlan plan(int N, int K, int split_req, int x_dtype) {
+  const int NP = pad_rows(N), nblk = K / BLK;
+  int R = 8;
+  for (int c : {64, 32, 16, 8})
+    if (NP / c >= GEMV_TARGET_WGS) { R = c; break; }
+  if (const char* e = getenv("Q4MI_GEMV_ROWS")) {
+    int v = atoi(e);
+    if (v == 8 || v == 16 || v == 32 || v == 64) R = v;
+  }
+  const int wgs = NP / R;
+  int s = split_req;
+  if (s <= 0) {
+    s = 1;
+    if (wgs < GEMV_MIN_WGS) {
+      s = ceil_div(2 * GEMV_MIN_WGS, wgs);
+      const int cap = nblk / 16 > 0 ? nblk / 16 : 1;   // keep >= 16 blocks per workgroup
+      if (s > cap) s = cap;
+    }
+  }
+  const int per_block = (x_dtype == Q4_DT_F16 ? 64 : 128) + 4;
+  const int max_nb = GEMV_LDS_MAX / per_block;
+  if (s < ceil_div(nblk, max_nb)) s = ceil_div(nblk, max_nb);
   if (s > nblk) s = nblk;
-  return s;
-}
-
-static size_t ws_bytes(int N, int K, int split) {
-  if (split <= 1) return 0;
-  const size_t NP = (size_t)pad_rows(N);
-  size_t b = GEMV_TICKET_BYTES + (size_t)split * NP * sizeof(float);
-  return (b + 255) & ~(size_t)255;
+  GemvPlan p;
+  p.R = R;
+  p.split = s;
+  p.nb_max = ceil_div(nblk, s);
+  p.lds = (size_t)p.nb_max * per_block;
+  p.ws = 0;
+  if (s > 1) p.ws = (GEMV_TICKET_BYTES + (size_t)s * NP * sizeof(float) + 255) & ~(size_t)255;
+  return p;
 }
 
 }  // namespace q4
@@ -247,12 +276,14 @@ extern "C" {
 
 int q4_gemv_auto_split(int N, int K) {
   if (N <= 0 || K <= 0 || K % BLK) return 1;
-  return effective_split(N, K, 0);
+  return plan(N, K, 0, Q4_DT_F16).split;
 }
 
 size_t q4_workspace_bytes(int op, int N, int K, int split) {
   if (op != Q4_OP_GEMV || N <= 0 || K <= 0 || K % BLK) return 0;
-  return ws_bytes(N, K, effective_split(N, K, split));
+  // size for the larger (fp32-x) staging plan so one workspace serves both activation types
+  GemvPlan a = plan(N, K, split, Q4_DT_F16), b = plan(N, K, split, Q4_DT_F32);
+  return a.ws > b.ws ? a.ws : b.ws;
 }
 
 int q4_workspace_init(void* ws, size_t bytes, void* stream) {
@@ -270,21 +301,19 @@ int q4_gemv(const void* x, int x_dtype, const uint32_t* wq, const void* scales, 
   Q4_ARG(x_dtype == Q4_DT_F32 || x_dtype == Q4_DT_F16, "bad x dtype %d", x_dtype);
   Q4_ARG(y_dtype == Q4_DT_F32 || y_dtype == Q4_DT_F16, "bad y dtype %d", y_dtype);
   Q4_ARG(scale_fmt == Q4_SCALE_F16 || scale_fmt == Q4_SCALE_E4M3, "bad scale format %d", scale_fmt);
-  Q4_ARG(((uintptr_t)wq & 15) == 0, "wq must be 16-byte aligned");
-  Q4_ARG(((uintptr_t)x & (x_dtype == Q4_DT_F16 ? 3 : 3)) == 0, "x must be 4-byte aligned");
+  Q4_ARG(((uintptr_t)wq & 15) == 0 && ((uintptr_t)x & 15) == 0, "wq and x must be 16-byte aligned");
   Q4_ARG(N <= (1 << 30) && (long)K <= (1L << 24), "GEMV too large");
-  const int s = effective_split(N, K, split);
-  const size_t need = ws_bytes(N, K, s);
-  Q4_ARG(need == 0 || (ws && ws_size >= need), "GEMV N=%d K=%d split=%d needs a %zu-byte workspace (got %zu)", N, K,
-         s, need, ws ? ws_size : (size_t)0);
-  const int panels = ceil_div(N, PANEL);
-  Q4_ARG(need == 0 || panels <= GEMV_MAX_TICKETS, "split-K GEMV supports at most %d rows", GEMV_MAX_TICKETS * PANEL);
-  uint32_t* cnt = need ? reinterpret_cast<uint32_t*>(ws) : nullptr;
-  float* part = need ? reinterpret_cast<float*>(reinterpret_cast<char*>(ws) + GEMV_TICKET_BYTES) : nullptr;
+  const GemvPlan pl = plan(N, K, split, x_dtype);
+  Q4_ARG(pl.ws == 0 || (ws && ws_size >= pl.ws), "GEMV N=%d K=%d split=%d needs a %zu-byte workspace (got %zu)", N,
+         K, pl.split, pl.ws, ws ? ws_size : (size_t)0);
+  const int groups = pad_rows(N) / pl.R;
+  Q4_ARG(pl.ws == 0 || groups <= GEMV_MAX_TICKETS, "split-K GEMV supports at most %d row groups", GEMV_MAX_TICKETS);
+  uint32_t* cnt = pl.ws ? reinterpret_cast<uint32_t*>(ws) : nullptr;
+  float* part = pl.ws ? reinterpret_cast<float*>(reinterpret_cast<char*>(ws) + GEMV_TICKET_BYTES) : nullptr;
   const float outscale = scale_fmt == Q4_SCALE_E4M3 ? inv * 256.0f : 1.0f;
-  gemv_fn fn = pick(x_dtype, scale_fmt, y_dtype);
-  hipLaunchKernelGGL(fn, dim3(panels, s), dim3(GEMV_THREADS), 0, as_stream(stream), x,
-                     reinterpret_cast<const uint4*>(wq), scales, outscale, y, N, K / BLK, s, part, cnt);
+  gemv_fn fn = pick(pl.R, x_dtype, scale_fmt, y_dtype);
+  hipLaunchKernelGGL(fn, dim3(groups, pl.split), dim3(GEMV_THREADS), pl.lds, as_stream(stream), x,
+                     reinterpret_cast<const uint4*>(wq), scales, outscale, y, N, K / BLK, pl.split, part, cnt);
   Q4_LAUNCHED("gemv");
   return Q4_OK;
 }

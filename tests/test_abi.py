@@ -72,16 +72,18 @@ def test_sizes_and_split_queries(g4):
     assert wb.value == 15360 * 3840 // 2 and se.value == 15360 * 120
     assert lib.q4_dev_bytes(70, 64, C.byref(wb), C.byref(se)) == 0
     assert se.value == 128 * 2  # rows padded to whole 64-row panels
-    # lm_head needs no split-K, small-N matrices do, and the workspace covers it
-    assert lib.q4_gemv_auto_split(262144, 3840) == 1
-    for N, K in [(15360, 3840), (2048, 3840), (3840, 15360), (3840, 4096)]:
+    # every decode shape runs without split-K (no workspace) ...
+    for N, K in [(262144, 3840), (30720, 3840), (15360, 3840), (2048, 3840), (3840, 15360), (3840, 4096)]:
+        assert lib.q4_gemv_auto_split(N, K) == 1
+        assert lib.q4_workspace_bytes(0, N, K, 0) == 0
+    # ... small matrices split K across workgroups and need the workspace
+    for N, K in [(512, 3840), (256, 15360), (64, 4096)]:
         s = lib.q4_gemv_auto_split(N, K)
         assert 1 < s <= K // 32
         ws = lib.q4_workspace_bytes(0, N, K, 0)
         assert ws >= 65536 + s * N * 4 and ws % 256 == 0
-    assert lib.q4_workspace_bytes(0, 262144, 3840, 0) == 0
     # an explicit split too small for the LDS staging cap is raised
-    assert lib.q4_workspace_bytes(0, 64, 15360, 1) > 0
+    assert lib.q4_workspace_bytes(0, 64, 32768, 1) > 0  # fp32 x of K=32768 exceeds one LDS staging
 
 
 def test_missing_library_fails_loudly(g4, tmp_path):

@@ -24,7 +24,8 @@ def _case(rng, N, K):
     return q, s, x
 
 
-@pytest.mark.parametrize("N,K", [(64, 32), (100, 96), (256, 256), (4096, 3840), (3840, 4096), (2048, 3840)])
+@pytest.mark.parametrize("N,K", [(64, 32), (100, 96), (256, 256), (520, 3840), (4096, 3840), (3840, 4096),
+                                 (2048, 3840), (1000, 15360)])
 @pytest.mark.parametrize("xdt,ydt", [(torch.float16, torch.float16), (torch.float16, torch.float32),
                                      (torch.float32, torch.float32)])
 def test_gemv_f16_scales(gpu, N, K, xdt, ydt):
@@ -39,7 +40,10 @@ def test_gemv_f16_scales(gpu, N, K, xdt, ydt):
 
 
 @pytest.mark.parametrize("split", [1, 2, 3, 5, 8, 120])
-def test_gemv_split_invariance(gpu, split):
+@pytest.mark.parametrize("rows", [None, "8", "64"])
+def test_gemv_split_invariance(gpu, split, rows, monkeypatch):
+    if rows:
+        monkeypatch.setenv("Q4MI_GEMV_ROWS", rows)
     rng = np.random.default_rng(21)
     N, K = 512, 3840
     q, s, x = _case(rng, N, K)
@@ -151,7 +155,7 @@ def test_gemv_graph_replay_matches_eager(gpu):
     """A captured sequence of split-K GEMVs sharing one workspace replays
     bit-identically to eager execution, replay after replay."""
     rng = np.random.default_rng(7)
-    shapes = [(4096, 3840), (2048, 3840), (3840, 4096), (3840, 15360), (15360, 3840)]
+    shapes = [(4096, 3840), (512, 3840), (2048, 3840), (256, 15360), (3840, 4096), (3840, 15360), (15360, 3840)]
     mats = []
     for N, K in shapes:
         q, s = synth_int4(rng, N, K)
