@@ -72,7 +72,7 @@ def test_ops_reject_host_tensors(ops):
 def test_graph_capture_refuses_workspace_allocation(ops, g4, monkeypatch):
     monkeypatch.setattr(ops, "_CAPTURING", [1])
     with pytest.raises(RuntimeError, match="before the capture"):
-        ops.default_workspace(2048, 3840)
+        ops.default_workspace(512, 3840)  # a small matrix: split-K, needs a workspace
 
 
 def test_split_matches_library(ops, g4):
