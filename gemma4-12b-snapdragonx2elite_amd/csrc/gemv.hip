@@ -39,10 +39,9 @@ namespace q4 {
 
 constexpr int GEMV_THREADS = 256;
 constexpr int GEMV_WAVES = GEMV_THREADS / 64;
-constexpr int GEMV_U = 8;                  // units in flight per lane
 constexpr int GEMV_LDS_MAX = 64 * 1024;    // x staging cap per workgroup (bytes)
-constexpr int GEMV_TARGET_WGS = 768;       // pick the largest R that still gives this many workgroups
-constexpr int GEMV_MIN_WGS = 256;          // below this, K is split across workgroups
+constexpr int GEMV_TARGET_WGS = 768;       // preferred workgroup count (see plan())
+constexpr int GEMV_MIN_WGS = 256;          // one per CU; below this K is split across workgroups
 // Split-K workspace layout: tickets for up to GEMV_MAX_TICKETS row groups at
 // a fixed offset 0 (so GEMVs of different shapes sharing one workspace never
 // see each other's partials as tickets), then the fp32 partials.
@@ -97,7 +96,7 @@ __device__ inline float load_scale(const void* __restrict__ scv, long idx) {
   }
 }
 
-template <int R, int XT, int ST, int YT>
+template <int R, int U, int XT, int ST, int YT>
 __global__ void __launch_bounds__(GEMV_THREADS)
 gemv_kernel(const void* __restrict__ xv, const uint4* __restrict__ wq, const void* __restrict__ scv, float outscale,
             void* __restrict__ yv, int N, int nblk, int split, float* __restrict__ part, uint32_t* __restrict__ cnt) {
@@ -117,13 +116,41 @@ gemv_kernel(const void* __restrict__ xv, const uint4* __restrict__ wq, const voi
   float* xs_f = reinterpret_cast<float*>(smem);
   float* xsum = reinterpret_cast<float*>(smem + (XH ? nb * 16 : nb * BLK));
 
-  // ---- stage the x slice [k0, k0 + 32 nb) and its per-block sums ----
-  if constexpr (XH) {
-    const uint4* x4 = reinterpret_cast<const uint4*>(reinterpret_cast<const uint16_t*>(xv) + k0);
-    for (int i = tid; i < nb * 4; i += GEMV_THREADS) reinterpret_cast<uint4*>(xs_h)[i] = x4[i];
-  } else {
-    const float4* x4 = reinterpret_cast<const float4*>(reinterpret_cast<const float*>(xv) + k0);
-    for (int i = tid; i < nb * 8; i += GEMV_THREADS) reinterpret_cast<float4*>(xs_f)[i] = x4[i];
+  // ---- stage the x slice [k0, k0 + 32 nb). The first round of x loads is
+  //      issued, then the first batch of weight units, then the x stores to
+  //      LDS: every load is unconditional (indices clamped) so the in-order
+  //      load counter lets the x stores wait for the x loads only, and the
+  //      weight latency overlaps the staging (the barrier waits on LDS). ----
+  constexpr int XU = 4;  // 16-byte x loads per thread per round
+  const int n16 = XH ? nb * 4 : nb * 8;
+  const uint4* x4 = XH ? reinterpret_cast<const uint4*>(reinterpret_cast<const uint16_t*>(xv) + k0)
+                       : reinterpret_cast<const uint4*>(reinterpret_cast<const float*>(xv) + k0);
+  uint4 t4[XU];
+#pragma unroll
+  for (int q = 0; q < XU; ++q) t4[q] = x4[min(tid + q * GEMV_THREADS, n16 - 1)];
+  const int n0 = g * R;
+  const long ubase = ((long)(n0 / PANEL) * nblk + b_lo) * PANEL + (n0 % PANEL) + r;  // unit of block j: ubase + 64 j
+  uint4 u[U];
+  float sc[U];
+#pragma unroll
+  for (int t = 0; t < U; ++t) {  // first batch (same as load_batch(slot) below)
+    const int jj = min(slot + t * S, nb - 1);
+    u[t] = wq[ubase + (long)jj * PANEL];
+    sc[t] = load_scale<ST>(scv, ubase + (long)jj * PANEL);
+  }
+#pragma unroll
+  for (int q = 0; q < XU; ++q) {
+    const int i = tid + q * GEMV_THREADS;
+    if (i < n16) reinterpret_cast<uint4*>(smem)[i] = t4[q];
+  }
+  for (int i0 = tid + XU * GEMV_THREADS; i0 < n16; i0 += GEMV_THREADS * XU) {  // long K only
+#pragma unroll
+    for (int q = 0; q < XU; ++q) t4[q] = x4[min(i0 + q * GEMV_THREADS, n16 - 1)];
+#pragma unroll
+    for (int q = 0; q < XU; ++q) {
+      const int i = i0 + q * GEMV_THREADS;
+      if (i < n16) reinterpret_cast<uint4*>(smem)[i] = t4[q];
+    }
   }
   __syncthreads();
   for (int j = tid; j < nb; j += GEMV_THREADS) {
@@ -142,21 +169,20 @@ gemv_kernel(const void* __restrict__ xv, const uint4* __restrict__ wq, const voi
   }
   __syncthreads();
 
-  // ---- this lane's blocks: slot, slot + S, slot + 2S, ... ----
-  const int n0 = g * R;
-  const long ubase = ((long)(n0 / PANEL) * nblk + b_lo) * PANEL + (n0 % PANEL) + r;  // unit of block j: ubase + 64 j
-  float acc = 0.0f;
-  for (int j = slot; j < nb; j += S * GEMV_U) {
-    uint4 u[GEMV_U];
-    float sc[GEMV_U];
+  // ---- this lane's blocks: slot, slot + S, slot + 2S, ... in batches of U;
+  //      a batch is loaded (unconditionally, clamped) before it is used ----
+  auto load_batch = [&](int j) {
 #pragma unroll
-    for (int t = 0; t < GEMV_U; ++t) {
+    for (int t = 0; t < U; ++t) {
       const int jj = min(j + t * S, nb - 1);
       u[t] = wq[ubase + (long)jj * PANEL];
       sc[t] = load_scale<ST>(scv, ubase + (long)jj * PANEL);
     }
+  };
+  float acc = 0.0f;
+  for (int j = slot;;) {
 #pragma unroll
-    for (int t = 0; t < GEMV_U; ++t) {
+    for (int t = 0; t < U; ++t) {
       const int jj = j + t * S;
       if (jj < nb) {
         float d;
@@ -165,6 +191,9 @@ gemv_kernel(const void* __restrict__ xv, const uint4* __restrict__ wq, const voi
         acc = fmaf(sc[t], d, acc);
       }
     }
+    j += S * U;
+    if (j >= nb) break;
+    load_batch(j);
   }
   // slots of a row: lanes r, r + R, r + 2R, ... of each wave, then the 4 waves
 #pragma unroll
@@ -207,39 +236,50 @@ gemv_kernel(const void* __restrict__ xv, const uint4* __restrict__ wq, const voi
 
 typedef void (*gemv_fn)(const void*, const uint4*, const void*, float, void*, int, int, int, float*, uint32_t*);
 
-template <int R, int XT, int ST>
+template <int R, int U, int XT, int ST>
 static gemv_fn pick_y(int yt) {
-  return yt == Q4_DT_F16 ? gemv_kernel<R, XT, ST, Q4_DT_F16> : gemv_kernel<R, XT, ST, Q4_DT_F32>;
+  return yt == Q4_DT_F16 ? gemv_kernel<R, U, XT, ST, Q4_DT_F16> : gemv_kernel<R, U, XT, ST, Q4_DT_F32>;
 }
-template <int R, int XT>
+template <int R, int U, int XT>
 static gemv_fn pick_s(int st, int yt) {
-  return st == Q4_SCALE_E4M3 ? pick_y<R, XT, Q4_SCALE_E4M3>(yt) : pick_y<R, XT, Q4_SCALE_F16>(yt);
+  return st == Q4_SCALE_E4M3 ? pick_y<R, U, XT, Q4_SCALE_E4M3>(yt) : pick_y<R, U, XT, Q4_SCALE_F16>(yt);
+}
+template <int R, int U>
+static gemv_fn pick_x(int xt, int st, int yt) {
+  return xt == Q4_DT_F16 ? pick_s<R, U, Q4_DT_F16>(st, yt) : pick_s<R, U, Q4_DT_F32>(st, yt);
 }
 template <int R>
-static gemv_fn pick_x(int xt, int st, int yt) {
-  return xt == Q4_DT_F16 ? pick_s<R, Q4_DT_F16>(st, yt) : pick_s<R, Q4_DT_F32>(st, yt);
+static gemv_fn pick_u(int U, int xt, int st, int yt) {
+  return U == 4 ? pick_x<R, 4>(xt, st, yt) : pick_x<R, 8>(xt, st, yt);
 }
-static gemv_fn pick(int R, int xt, int st, int yt) {
+static gemv_fn pick(int R, int U, int xt, int st, int yt) {
   switch (R) {
-    case 64: return pick_x<64>(xt, st, yt);
-    case 32: return pick_x<32>(xt, st, yt);
-    case 16: return pick_x<16>(xt, st, yt);
-    default: return pick_x<8>(xt, st, yt);
+    case 64: return pick_u<64>(U, xt, st, yt);
+    case 32: return pick_u<32>(U, xt, st, yt);
+    case 16: return pick_u<16>(U, xt, st, yt);
+    default: return pick_u<8>(U, xt, st, yt);
   }
 }
 
 struct GemvPlan {
-  int R, split, nb_max;
+  int R, U, split, nb_max;
   size_t lds, ws;
 };
 
-// Rows per workgroup and K split for an N x K GEMV. Q4MI_GEMV_ROWS
-// (8/16/32/64) overrides R for tuning sweeps.
+// Rows per workgroup R, units in flight U and K split for an N x K GEMV
+// (measured on MI355X over the decode shapes: the largest R that still gives
+// GEMV_TARGET_WGS workgroups, else the largest that gives one per CU; U = 4
+// when every lane's blocks fit one batch of 4). Q4MI_GEMV_ROWS (8/16/32/64)
+// overrides R for tuning sweeps.
 static GemvPlan plan(int N, int K, int split_req, int x_dtype) {
   const int NP = pad_rows(N), nblk = K / BLK;
-  int R = 8;
+  int R = 0;
   for (int c : {64, 32, 16, 8})
     if (NP / c >= GEMV_TARGET_WGS) { R = c; break; }
+  if (R == 0)
+    for (int c : {64, 32, 16, 8})
+      if (NP / c >= GEMV_MIN_WGS) { R = c; break; }
+  if (R == 0) R = 8;
   if (const char* e = getenv("Q4MI_GEMV_ROWS")) {
     int v = atoi(e);
     if (v == 8 || v == 16 || v == 32 || v == 64) R = v;
@@ -262,6 +302,7 @@ static GemvPlan plan(int N, int K, int split_req, int x_dtype) {
   p.R = R;
   p.split = s;
   p.nb_max = ceil_div(nblk, s);
+  p.U = ceil_div(p.nb_max, (64 / R) * GEMV_WAVES) <= 4 ? 4 : 8;
   p.lds = (size_t)p.nb_max * per_block;
   p.ws = 0;
   if (s > 1) p.ws = (GEMV_TICKET_BYTES + (size_t)s * NP * sizeof(float) + 255) & ~(size_t)255;
@@ -311,7 +352,7 @@ int q4_gemv(const void* x, int x_dtype, const uint32_t* wq, const void* scales, 
   uint32_t* cnt = pl.ws ? reinterpret_cast<uint32_t*>(ws) : nullptr;
   float* part = pl.ws ? reinterpret_cast<float*>(reinterpret_cast<char*>(ws) + GEMV_TICKET_BYTES) : nullptr;
   const float outscale = scale_fmt == Q4_SCALE_E4M3 ? inv * 256.0f : 1.0f;
-  gemv_fn fn = pick(pl.R, x_dtype, scale_fmt, y_dtype);
+  gemv_fn fn = pick(pl.R, pl.U, x_dtype, scale_fmt, y_dtype);
   hipLaunchKernelGGL(fn, dim3(groups, pl.split), dim3(GEMV_THREADS), pl.lds, as_stream(stream), x,
                      reinterpret_cast<const uint4*>(wq), scales, outscale, y, N, K / BLK, pl.split, part, cnt);
   Q4_LAUNCHED("gemv");
