@@ -1,12 +1,12 @@
 // Prefill GEMMs on gfx950 MFMA, plus the per-row int8 activation quantizer.
 //
 //   W8A8 : C = A8 @ W8^T (int32, exact), Y = f16((f32(C) * sa[m]) * sw[n])
-//          (vk/coopgemm_w8a8.comp)          v_mfma_i32_16x16x64_i8
+//          (vk/coopgemm_w8a8.comp)          v_mfma_i32_32x32x32_i8
 //   W4A8 : as W8A8 with W8 = int8(clamp(rint((q-8) * ratio), +-127)) made
 //          on the fly from the int4 codes (vk/coopgemm_w4a8.comp)
 //   W4A16: Y = f16(X @ f16((q-8) * s)^T), fp32 accumulate
 //          (vk/coopgemm_i4h.comp, which accumulates in f16; this one
-//          accumulates in fp32)          v_mfma_f32_16x16x32_f16
+//          accumulates in fp32)          v_mfma_f32_32x32x16_f16
 //
 // One kernel template serves all three: every k-step stages 64-byte rows of
 // both operands in LDS (64 int8 or 32 f16 elements), so the LDS layout, the
@@ -15,9 +15,12 @@
 // MFMA/epilogue differ.
 //
 // Tiling: BM x BN macro tile per 256-thread workgroup (4 waves as 2 x 2),
-// each wave a (BM/2) x (BN/2) block of 16x16 MFMA tiles; LDS double
-// buffered with one barrier per k-step; the next k-step's global loads are
-// in flight while the current one's MFMAs run. Workgroups are remapped so
+// each wave a (BM/2) x (BN/2) block of 32x32 MFMA tiles
+// (v_mfma_i32_32x32x32_i8 / v_mfma_f32_32x32x16_f16: both take 16 operand
+// bytes per lane, half the operand traffic per MAC of the 16x16 shapes);
+// a 64-byte k-row is two MFMA k-slices. LDS double buffered with one
+// barrier per k-step; the next k-step's global loads are in flight while
+// the current one's MFMAs run. Workgroups are remapped so
 // each XCD (8 per MI355X, own L2) works on a contiguous 1/8 of the grid
 // ordered by weight panel, which keeps a weight panel's re-reads in one L2.
 #include "q4mi_common.h"
@@ -25,6 +28,7 @@
 namespace q4 {
 
 enum { OP_W8A8 = 0, OP_W4A16 = 1, OP_W4A8 = 2 };
+constexpr int GEMM_WAVES_EPI = 4;
 
 struct GemmArgs {
   const void* A;        // int8 [M][K] or f16 [M][K]
@@ -49,7 +53,7 @@ __device__ inline uint32_t pk_h2(v2h v) { return __builtin_bit_cast(uint32_t, v)
 // Low nibbles: 0x6400 | q = 1024 + q; high nibbles: 0x6400 | 16q =
 // 1024 + 16q. Both become q - 8 exactly, then one RNE multiply by s, which
 // is the reference's float16_t((float(q) - 8.0) * scl).
-__device__ inline void dequant_unit_f16(const uint4 u, _Float16 s, uint4 out[4]) {
+__device__ inline void dequant_unit_f16(const v4u u, _Float16 s, v4u out[4]) {
   const uint32_t w[4] = {u.x, u.y, u.z, u.w};
   const v2h sv = {s, s};
   const v2h off_lo = {(_Float16)1032.0f, (_Float16)1032.0f};
@@ -66,12 +70,12 @@ __device__ inline void dequant_unit_f16(const uint4 u, _Float16 s, uint4 out[4])
     p1 = (p1 * sixteenth - off_hi) * sv;
     p2 = (p2 - off_lo) * sv;
     p3 = (p3 * sixteenth - off_hi) * sv;
-    out[i] = make_uint4(pk_h2(p0), pk_h2(p1), pk_h2(p2), pk_h2(p3));
+    out[i] = v4u{pk_h2(p0), pk_h2(p1), pk_h2(p2), pk_h2(p3)};
   }
 }
 
 // int4 unit -> 32 int8 values clamp(rint((q - 8) * r), -127, 127), k order.
-__device__ inline void requant_unit_i8(const uint4 u, float r, uint4 out[2]) {
+__device__ inline void requant_unit_i8(const v4u u, float r, v4u out[2]) {
   const uint32_t w[4] = {u.x, u.y, u.z, u.w};
   uint32_t o[8];
 #pragma unroll
@@ -90,21 +94,40 @@ __device__ inline void requant_unit_i8(const uint4 u, float r, uint4 out[2]) {
       o[2 * i + h] = word;
     }
   }
-  out[0] = make_uint4(o[0], o[1], o[2], o[3]);
-  out[1] = make_uint4(o[4], o[5], o[6], o[7]);
+  out[0] = v4u{o[0], o[1], o[2], o[3]};
+  out[1] = v4u{o[4], o[5], o[6], o[7]};
+}
+
+typedef int v16i __attribute__((ext_vector_type(16)));
+typedef float v16f __attribute__((ext_vector_type(16)));
+
+// Copy one 32x32 accumulator tile (16 registers per lane) into an LDS strip
+// with row stride `st` words: register v goes to row 8 (v / 4) + v % 4 (the
+// lane's 4-row half is folded into p). Each element is moved to a VGPR
+// first (the empty asm with a "v" operand): LDS stores taking the elements
+// straight from the accumulator registers were compiled to 16 stores of the
+// tile's first register.
+template <class V>
+__device__ inline void store_tile_strip(uint32_t* p, int st, const V t) {
+  uint32_t e[16];
+  __builtin_memcpy(e, &t, sizeof(e));
+#pragma unroll
+  for (int v = 0; v < 16; ++v) p[(8 * (v >> 2) + (v & 3)) * st] = e[v];
 }
 
 template <int OP, int BM, int BN>
 __global__ void __launch_bounds__(256) gemm_kernel(const GemmArgs g) {
   constexpr int STAGE = (BM + BN) * 64;
-  constexpr int WM = BM / 2, WN = BN / 2, FM = WM / 16, FN = WN / 16;
+  constexpr int WM = BM / 2, WN = BN / 2, FM = WM / 32, FN = WN / 32;
   constexpr int A_CH = BM / 64;                                      // A chunks per thread per k-step
   constexpr int B_CH = (OP == OP_W8A8) ? BN / 64 : (OP == OP_W4A16 ? BN / 256 : BN / 128);
   constexpr bool F16 = (OP == OP_W4A16);
   static_assert(BN % 256 == 0 || OP == OP_W8A8, "int4 B producers need BN % 256 == 0");
-  typedef typename std::conditional<F16, v4f, v4i>::type acc_t;
+  typedef typename std::conditional<F16, v16f, v16i>::type acc_t;
 
-  __shared__ __attribute__((aligned(16))) uint8_t lds[2 * STAGE];
+  constexpr int EST = 36;  // epilogue strip row stride in 32-bit words (16-byte aligned, staggers banks)
+  constexpr int EPI = GEMM_WAVES_EPI * WM * EST * 4;
+  __shared__ __attribute__((aligned(16))) uint8_t lds[2 * STAGE > EPI ? 2 * STAGE : EPI];
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int wm = wave >> 1, wn = wave & 1;
@@ -118,144 +141,188 @@ __global__ void __launch_bounds__(256) gemm_kernel(const GemmArgs g) {
   const int nk = F16 ? K / 32 : K / 64;                               // k-steps (64-byte rows)
   const long a_row_bytes = F16 ? 2L * K : (long)K;
 
-  // ---- per-thread global sources ----
+  // ---- per-thread global sources: rows (tid / 4) + 64 i, 16-byte chunk tid % 4 ----
   const uint8_t* Ab = reinterpret_cast<const uint8_t*>(g.A);
   const int a_chunk = tid & 3;
-  long a_src[A_CH];
+  const uint8_t* a_src[A_CH];
 #pragma unroll
-  for (int i = 0; i < A_CH; ++i) {
-    const int r = (tid >> 2) + 64 * i;
-    a_src[i] = (long)min(m0 + r, M - 1) * a_row_bytes + a_chunk * 16;
+  for (int i = 0; i < A_CH; ++i)
+    a_src[i] = Ab + (long)min(m0 + (tid >> 2) + 64 * i, M - 1) * a_row_bytes + a_chunk * 16;
+  const uint8_t* b_src[(OP == OP_W8A8) ? B_CH : 1];
+  if constexpr (OP == OP_W8A8) {
+#pragma unroll
+    for (int i = 0; i < B_CH; ++i)
+      b_src[i] = reinterpret_cast<const uint8_t*>(g.B) + (long)min(n0 + (tid >> 2) + 64 * i, N - 1) * K + a_chunk * 16;
   }
 
-  uint4 ra[A_CH];
-  uint4 rb[(OP == OP_W8A8) ? B_CH : 1];
-  uint4 ru[(OP == OP_W8A8) ? 1 : B_CH];
+  // native vector registers (HIP's uint4 is a union struct the compiler keeps in scratch here)
+  v4u ra[A_CH];
+  v4u rb[(OP == OP_W8A8) ? B_CH : 1];
+  v4u ru[(OP == OP_W8A8) ? 1 : B_CH];
   uint16_t rs[(OP == OP_W8A8) ? 1 : B_CH];
 
-  auto load_regs = [&](int kt) {
-#pragma unroll
-    for (int i = 0; i < A_CH; ++i) ra[i] = *reinterpret_cast<const uint4*>(Ab + a_src[i] + (long)kt * 64);
-    if constexpr (OP == OP_W8A8) {
-      const uint8_t* Bb = reinterpret_cast<const uint8_t*>(g.B);
-#pragma unroll
-      for (int i = 0; i < B_CH; ++i) {
-        const int r = (tid >> 2) + 64 * i;
-        const long src = (long)min(n0 + r, N - 1) * K + a_chunk * 16 + (long)kt * 64;
-        rb[i] = *reinterpret_cast<const uint4*>(Bb + src);
-      }
-    } else {
-      const uint4* U = reinterpret_cast<const uint4*>(g.B);
-#pragma unroll
-      for (int i = 0; i < B_CH; ++i) {
-        // W4A16: one block per k-step, row = tid + 256 i.
-        // W4A8: two blocks per k-step, i = 2 * rr + h, row = tid + 256 rr.
-        const int rr = (OP == OP_W4A16) ? i : i / 2;
-        const int blk = (OP == OP_W4A16) ? kt : 2 * kt + (i & 1);
-        const int n = min(n0 + tid + 256 * rr, N - 1);
-        const long idx = panel_index(n, blk, nblk);
-        ru[i] = U[idx];
-        rs[i] = g.bsc[idx];
-      }
-    }
-  };
+#define Q4_LOAD_REGS(kt_)                                                                              \
+  do {                                                                                                 \
+    const int kt_v = (kt_);                                                                            \
+    _Pragma("unroll") for (int i = 0; i < A_CH; ++i) ra[i] =                                          \
+        *reinterpret_cast<const v4u*>(a_src[i] + (long)kt_v * 64);                                   \
+    if constexpr (OP == OP_W8A8) {                                                                     \
+      _Pragma("unroll") for (int i = 0; i < B_CH; ++i) rb[i] =                                        \
+          *reinterpret_cast<const v4u*>(b_src[i] + (long)kt_v * 64);                                 \
+    } else {                                                                                           \
+      const v4u* U = reinterpret_cast<const v4u*>(g.B);                                               \
+      _Pragma("unroll") for (int i = 0; i < B_CH; ++i) {                                              \
+        /* W4A16: one block per k-step, row = tid + 256 i;                                          */ \
+        /* W4A8: two blocks per k-step, i = 2 rr + h, row = tid + 256 rr                              */ \
+        const int rr = (OP == OP_W4A16) ? i : i / 2;                                                   \
+        const int blk = (OP == OP_W4A16) ? kt_v : 2 * kt_v + (i & 1);                                  \
+        const int n = min(n0 + tid + 256 * rr, N - 1);                                                 \
+        const long idx = panel_index(n, blk, nblk);                                                    \
+        ru[i] = U[idx];                                                                                \
+        rs[i] = g.bsc[idx];                                                                            \
+      }                                                                                                \
+    }                                                                                                  \
+  } while (0)
 
-  auto store_lds = [&](int stage) {
-    uint8_t* base = lds + stage * STAGE;
-#pragma unroll
-    for (int i = 0; i < A_CH; ++i) {
-      const int r = (tid >> 2) + 64 * i;
-      *reinterpret_cast<uint4*>(base + lds_off(r, a_chunk)) = ra[i];
-    }
-    if constexpr (OP == OP_W8A8) {
-#pragma unroll
-      for (int i = 0; i < B_CH; ++i) {
-        const int r = BM + (tid >> 2) + 64 * i;
-        *reinterpret_cast<uint4*>(base + lds_off(r, a_chunk)) = rb[i];
-      }
-    } else if constexpr (OP == OP_W4A16) {
-#pragma unroll
-      for (int i = 0; i < B_CH; ++i) {
-        const int r = BM + tid + 256 * i;
-        uint4 o[4];
-        dequant_unit_f16(ru[i], __builtin_bit_cast(_Float16, rs[i]), o);
-#pragma unroll
-        for (int c = 0; c < 4; ++c) *reinterpret_cast<uint4*>(base + lds_off(r, c)) = o[c];
-      }
-    } else {
-#pragma unroll
-      for (int i = 0; i < B_CH; ++i) {
-        const int r = BM + tid + 256 * (i / 2);
-        uint4 o[2];
-        requant_unit_i8(ru[i], h2f(rs[i]), o);
-        *reinterpret_cast<uint4*>(base + lds_off(r, 2 * (i & 1))) = o[0];
-        *reinterpret_cast<uint4*>(base + lds_off(r, 2 * (i & 1) + 1)) = o[1];
-      }
-    }
-  };
+#define Q4_STORE_LDS(stage_)                                                                           \
+  do {                                                                                                 \
+    uint8_t* base_ = lds + (stage_) * STAGE;                                                           \
+    _Pragma("unroll") for (int i = 0; i < A_CH; ++i) {                                                \
+      const int r = (tid >> 2) + 64 * i;                                                               \
+      *reinterpret_cast<v4u*>(base_ + lds_off(r, a_chunk)) = ra[i];                                    \
+    }                                                                                                  \
+    if constexpr (OP == OP_W8A8) {                                                                     \
+      _Pragma("unroll") for (int i = 0; i < B_CH; ++i) {                                              \
+        const int r = BM + (tid >> 2) + 64 * i;                                                        \
+        *reinterpret_cast<v4u*>(base_ + lds_off(r, a_chunk)) = rb[i];                                  \
+      }                                                                                                \
+    } else if constexpr (OP == OP_W4A16) {                                                             \
+      _Pragma("unroll") for (int i = 0; i < B_CH; ++i) {                                              \
+        const int r = BM + tid + 256 * i;                                                              \
+        v4u o[4];                                                                                      \
+        dequant_unit_f16(ru[i], __builtin_bit_cast(_Float16, rs[i]), o);                               \
+        _Pragma("unroll") for (int c = 0; c < 4; ++c)                                                  \
+            *reinterpret_cast<v4u*>(base_ + lds_off(r, c)) = o[c];                                     \
+      }                                                                                                \
+    } else {                                                                                           \
+      _Pragma("unroll") for (int i = 0; i < B_CH; ++i) {                                              \
+        const int r = BM + tid + 256 * (i / 2);                                                        \
+        v4u o[2];                                                                                      \
+        requant_unit_i8(ru[i], h2f(rs[i]), o);                                                         \
+        *reinterpret_cast<v4u*>(base_ + lds_off(r, 2 * (i & 1))) = o[0];                               \
+        *reinterpret_cast<v4u*>(base_ + lds_off(r, 2 * (i & 1) + 1)) = o[1];                           \
+      }                                                                                                \
+    }                                                                                                  \
+  } while (0)
 
   acc_t acc[FM][FN];
 #pragma unroll
   for (int i = 0; i < FM; ++i)
 #pragma unroll
-    for (int j = 0; j < FN; ++j) acc[i][j] = acc_t{0, 0, 0, 0};
+    for (int j = 0; j < FN; ++j) acc[i][j] = acc_t{};
 
-  load_regs(0);
-  store_lds(0);
+  Q4_LOAD_REGS(0);
+  Q4_STORE_LDS(0);
   __syncthreads();
 
-  const int frow = lane & 15, fch = lane >> 4;
+  // MFMA operand: row lane % 32 of a 32-row tile, 16 bytes at byte 16 * (lane / 32) of the 32-byte k-slice
+  const int frow = lane & 31, fhalf = lane >> 5;
   for (int kt = 0; kt < nk; ++kt) {
     const int cur = kt & 1;
-    if (kt + 1 < nk) load_regs(kt + 1);
+    if (kt + 1 < nk) Q4_LOAD_REGS(kt + 1);
     const uint8_t* base = lds + cur * STAGE;
-    v4i fa[FM], fb[FN];
 #pragma unroll
-    for (int i = 0; i < FM; ++i) fa[i] = *reinterpret_cast<const v4i*>(base + lds_off(wm * WM + 16 * i + frow, fch));
+    for (int ks = 0; ks < 2; ++ks) {
+      const int ch = 2 * ks + fhalf;
+      v4i fa[FM], fb[FN];
 #pragma unroll
-    for (int j = 0; j < FN; ++j)
-      fb[j] = *reinterpret_cast<const v4i*>(base + lds_off(BM + wn * WN + 16 * j + frow, fch));
+      for (int i = 0; i < FM; ++i) fa[i] = *reinterpret_cast<const v4i*>(base + lds_off(wm * WM + 32 * i + frow, ch));
 #pragma unroll
-    for (int i = 0; i < FM; ++i)
+      for (int j = 0; j < FN; ++j)
+        fb[j] = *reinterpret_cast<const v4i*>(base + lds_off(BM + wn * WN + 32 * j + frow, ch));
 #pragma unroll
-      for (int j = 0; j < FN; ++j) {
-        if constexpr (F16)
-          acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(v8h, fa[i]),
-                                                             __builtin_bit_cast(v8h, fb[j]), acc[i][j], 0, 0, 0);
-        else
-          acc[i][j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(fa[i], fb[j], acc[i][j], 0, 0, 0);
-      }
-    if (kt + 1 < nk) store_lds(cur ^ 1);
+      for (int i = 0; i < FM; ++i)
+#pragma unroll
+        for (int j = 0; j < FN; ++j) {
+          if constexpr (F16)
+            acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(v8h, fa[i]),
+                                                               __builtin_bit_cast(v8h, fb[j]), acc[i][j], 0, 0, 0);
+          else
+            acc[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(fa[i], fb[j], acc[i][j], 0, 0, 0);
+        }
+    }
+    if (kt + 1 < nk) Q4_STORE_LDS(cur ^ 1);
     __syncthreads();
   }
 
-  // ---- epilogue: lane holds D[4*(lane/16) + r][lane%16] of each tile ----
-  const int col = lane & 15, rq = (lane >> 4) * 4;
+  // ---- epilogue through LDS (free after the loop's last barrier). Register
+  //      v of lane holds D[8 (v / 4) + 4 (lane / 32) + v % 4][lane % 32].
+  //      Each wave copies one 32-column strip of its tile into its own LDS
+  //      region with straight-line code (no branches next to the
+  //      accumulator reads), then reads it back 4 columns per lane for
+  //      bounds-checked, row-contiguous stores. ----
+  uint32_t* strip = reinterpret_cast<uint32_t*>(lds) + wave * (WM * EST);
+  const int col = lane & 31, rh = (lane >> 5) * 4;
+  const int mw = m0 + wm * WM, nw = n0 + wn * WN;
+  const int rrow = lane >> 3, rcol = (lane & 7) * 4;
 #pragma unroll
   for (int j = 0; j < FN; ++j) {
-    const int n = n0 + wn * WN + 16 * j + col;
-    if (n >= N) continue;
-    float swn = 1.0f;
-    if constexpr (!F16)
-      swn = g.sw_f16 ? h2f(reinterpret_cast<const uint16_t*>(g.sw)[n]) : reinterpret_cast<const float*>(g.sw)[n];
 #pragma unroll
-    for (int i = 0; i < FM; ++i) {
+    for (int i = 0; i < FM; ++i) store_tile_strip(strip + (32 * i + rh) * EST + col, EST, acc[i][j]);
+    __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0): this wave's strip is in LDS
+    __builtin_amdgcn_wave_barrier();
+    const int n = nw + 32 * j + rcol;
+    float swv[4] = {1.0f, 1.0f, 1.0f, 1.0f};
+    if constexpr (!F16) {
 #pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const int m = m0 + wm * WM + 16 * i + rq + r;
-        if (m >= M) continue;
-        const long o = (long)m * N + n;
-        if constexpr (F16) {
-          g.Y[o] = f2h(acc[i][j][r]);
+      for (int e = 0; e < 4; ++e) {
+        const int ne = min(n + e, N - 1);
+        swv[e] = g.sw_f16 ? h2f(reinterpret_cast<const uint16_t*>(g.sw)[ne]) : reinterpret_cast<const float*>(g.sw)[ne];
+      }
+    }
+    for (int it = 0; it < WM / 8; ++it) {
+      const int row = 8 * it + rrow;
+      const int m = mw + row;
+      const uint4 q = *reinterpret_cast<const uint4*>(strip + row * EST + rcol);
+      const uint32_t qv[4] = {q.x, q.y, q.z, q.w};
+      if (m >= M) continue;
+      const long o = (long)m * N + n;
+      if constexpr (F16) {
+        uint16_t h[4];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) h[e] = f2h(__builtin_bit_cast(float, qv[e]));
+        if (n + 3 < N && (o & 3) == 0) {
+          *reinterpret_cast<ushort4*>(g.Y + o) = make_ushort4(h[0], h[1], h[2], h[3]);
         } else {
-          const int c = acc[i][j][r];
-          if (g.C) g.C[o] = c;
-          if (g.Y) g.Y[o] = f2h_after_f32(__fmul_rn(__fmul_rn((float)c, g.sa[m]), swn));
+          for (int e = 0; e < 4; ++e)
+            if (n + e < N) g.Y[o + e] = h[e];
+        }
+      } else {
+        const float sam = g.sa ? g.sa[m] : 0.0f;
+        uint16_t h[4];
+#pragma unroll
+        for (int e = 0; e < 4; ++e)
+          h[e] = f2h_after_f32(__fmul_rn(__fmul_rn((float)(int)qv[e], sam), swv[e]));
+        const bool vec = n + 3 < N && (o & 3) == 0;
+        if (g.C) {
+          if (vec) *reinterpret_cast<uint4*>(g.C + o) = q;
+          else
+            for (int e = 0; e < 4; ++e)
+              if (n + e < N) g.C[o + e] = (int32_t)qv[e];
+        }
+        if (g.Y) {
+          if (vec) *reinterpret_cast<ushort4*>(g.Y + o) = make_ushort4(h[0], h[1], h[2], h[3]);
+          else
+            for (int e = 0; e < 4; ++e)
+              if (n + e < N) g.Y[o + e] = h[e];
         }
       }
     }
+    __builtin_amdgcn_wave_barrier();  // strip reads done before the next strip overwrites it
   }
 }
+#undef Q4_LOAD_REGS
+#undef Q4_STORE_LDS
 
 // ---- per-row int8 activation quantizer (vk/cast_i8.comp) -----------------
 template <int XT>
@@ -301,11 +368,18 @@ __global__ void __launch_bounds__(256) quant_act_kernel(const void* __restrict__
 }
 
 template <int OP, int BM, int BN>
-static int launch_gemm(const GemmArgs& g, void* stream, const char* name) {
+static int launch_tiles(const GemmArgs& g, void* stream, const char* name) {
   const int ntm = ceil_div(g.M, BM), ntn = ceil_div(g.N, BN);
   hipLaunchKernelGGL((gemm_kernel<OP, BM, BN>), dim3(ntm * ntn), dim3(256), 0, as_stream(stream), g);
   Q4_LAUNCHED(name);
   return Q4_OK;
+}
+
+// 256 x 256 tiles when they give at least one workgroup per CU, else 128 x 256.
+template <int OP>
+static int launch_gemm(const GemmArgs& g, void* stream, const char* name) {
+  if ((long)ceil_div(g.M, 256) * ceil_div(g.N, 256) >= 256) return launch_tiles<OP, 256, 256>(g, stream, name);
+  return launch_tiles<OP, 128, 256>(g, stream, name);
 }
 
 }  // namespace q4
@@ -339,7 +413,7 @@ int q4_gemm_w8a8(const int8_t* A, const int8_t* W8, const float* sa, const void*
   Q4_ARG(sw_dtype == Q4_DT_F32 || sw_dtype == Q4_DT_F16, "bad sw dtype %d", sw_dtype);
   Q4_ARG(((uintptr_t)A & 15) == 0 && ((uintptr_t)W8 & 15) == 0, "A and W8 must be 16-byte aligned");
   GemmArgs g{A, W8, nullptr, sa, sw, sw_dtype == Q4_DT_F16, Y, C, M, N, K};
-  return launch_gemm<OP_W8A8, 256, 256>(g, stream, "gemm_w8a8");
+  return launch_gemm<OP_W8A8>(g, stream, "gemm_w8a8");
 }
 
 int q4_gemm_w4a8(const int8_t* A, const uint32_t* wq, const uint16_t* ratio, const float* sa, const void* sw,
@@ -353,7 +427,7 @@ int q4_gemm_w4a8(const int8_t* A, const uint32_t* wq, const uint16_t* ratio, con
   Q4_ARG(sw_dtype == Q4_DT_F32 || sw_dtype == Q4_DT_F16, "bad sw dtype %d", sw_dtype);
   Q4_ARG(((uintptr_t)A & 15) == 0 && ((uintptr_t)wq & 15) == 0, "A and wq must be 16-byte aligned");
   GemmArgs g{A, wq, ratio, sa, sw, sw_dtype == Q4_DT_F16, Y, C, M, N, K};
-  return launch_gemm<OP_W4A8, 256, 256>(g, stream, "gemm_w4a8");
+  return launch_gemm<OP_W4A8>(g, stream, "gemm_w4a8");
 }
 
 int q4_gemm_w4a16(const uint16_t* X, const uint32_t* wq, const uint16_t* sc16, uint16_t* Y, int M, int N, int K,
@@ -364,7 +438,7 @@ int q4_gemm_w4a16(const uint16_t* X, const uint32_t* wq, const uint16_t* sc16, u
   Q4_ARG(X && wq && sc16 && Y, "null pointer");
   Q4_ARG(((uintptr_t)X & 15) == 0 && ((uintptr_t)wq & 15) == 0, "X and wq must be 16-byte aligned");
   GemmArgs g{X, wq, sc16, nullptr, nullptr, 0, Y, nullptr, M, N, K};
-  return launch_gemm<OP_W4A16, 256, 256>(g, stream, "gemm_w4a16");
+  return launch_gemm<OP_W4A16>(g, stream, "gemm_w4a16");
 }
 
 }  // extern "C"

@@ -18,6 +18,7 @@ constexpr int BLK = 32;     // K elements per scale block
 constexpr int PANEL = 64;   // rows per device panel (one wave64, lane = row)
 
 typedef int v4i __attribute__((ext_vector_type(4)));
+typedef unsigned int v4u __attribute__((ext_vector_type(4)));
 typedef float v4f __attribute__((ext_vector_type(4)));
 typedef _Float16 v8h __attribute__((ext_vector_type(8)));
 typedef _Float16 v2h __attribute__((ext_vector_type(2)));
