@@ -45,7 +45,19 @@ struct GemmArgs {
 // LDS byte offset of 16-byte chunk c (0..3) of staged row r. The XOR keeps
 // both the row-per-lane MFMA reads and the chunk-per-lane stores free of
 // bank conflicts.
-__device__ inline int lds_off(int r, int c) { return r * 64 + ((c ^ ((r >> 1) & 3)) << 4); }
+#ifndef Q4MI_GEMM_SWZ
+#define Q4MI_GEMM_SWZ 1
+#endif
+__device__ inline int lds_off(int r, int c) {
+#if Q4MI_GEMM_SWZ
+  // distinct 16-byte bank groups for any 8 consecutive rows (same chunk) and
+  // for rows {0, 4, 8, 12} (+1, +2, +3) of any 16: conflict-free whether the
+  // LDS serves 8 or 16 lanes of a ds_read_b128 per cycle
+  return r * 64 + ((c ^ (((r >> 1) & 3) ^ ((r >> 3) & 1))) << 4);
+#else
+  return r * 64 + ((c ^ ((r >> 1) & 3)) << 4);
+#endif
+}
 
 __device__ inline uint32_t pk_h2(v2h v) { return __builtin_bit_cast(uint32_t, v); }
 
@@ -115,7 +127,15 @@ __device__ inline void store_tile_strip(uint32_t* p, int st, const V t) {
   for (int v = 0; v < 16; ++v) p[(8 * (v >> 2) + (v & 3)) * st] = e[v];
 }
 
-template <int OP, int BM, int BN>
+template <bool F16, class A>
+__device__ inline A q4_mfma(v4i a, v4i b, A c) {
+  if constexpr (F16)
+    return __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(v8h, a), __builtin_bit_cast(v8h, b), c, 0, 0, 0);
+  else
+    return __builtin_amdgcn_mfma_i32_32x32x32_i8(a, b, c, 0, 0, 0);
+}
+
+template <int OP, int BM, int BN, int D>
 __global__ void __launch_bounds__(256) gemm_kernel(const GemmArgs g) {
   constexpr int STAGE = (BM + BN) * 64;
   constexpr int WM = BM / 2, WN = BN / 2, FM = WM / 32, FN = WN / 32;
@@ -155,19 +175,22 @@ __global__ void __launch_bounds__(256) gemm_kernel(const GemmArgs g) {
       b_src[i] = reinterpret_cast<const uint8_t*>(g.B) + (long)min(n0 + (tid >> 2) + 64 * i, N - 1) * K + a_chunk * 16;
   }
 
-  // native vector registers (HIP's uint4 is a union struct the compiler keeps in scratch here)
-  v4u ra[A_CH];
-  v4u rb[(OP == OP_W8A8) ? B_CH : 1];
-  v4u ru[(OP == OP_W8A8) ? 1 : B_CH];
-  uint16_t rs[(OP == OP_W8A8) ? 1 : B_CH];
+  // D rotating register buffers of one k-step each (native vector registers:
+  // HIP's uint4 is a union struct the compiler keeps in scratch here). A
+  // k-step is loaded D iterations before it is staged into LDS, so D - 1
+  // k-steps of MFMA work hide the global load latency.
+  v4u ra[D][A_CH];
+  v4u rb[D][(OP == OP_W8A8) ? B_CH : 1];
+  v4u ru[D][(OP == OP_W8A8) ? 1 : B_CH];
+  uint16_t rs[D][(OP == OP_W8A8) ? 1 : B_CH];
 
-#define Q4_LOAD_REGS(kt_)                                                                              \
+#define Q4_LOAD_REGS(buf_, kt_)                                                                        \
   do {                                                                                                 \
-    const int kt_v = (kt_);                                                                            \
-    _Pragma("unroll") for (int i = 0; i < A_CH; ++i) ra[i] =                                          \
+    const int kt_v = min((kt_), nk - 1); /* clamped: every load unconditional */                       \
+    _Pragma("unroll") for (int i = 0; i < A_CH; ++i) ra[buf_][i] =                                    \
         *reinterpret_cast<const v4u*>(a_src[i] + (long)kt_v * 64);                                   \
     if constexpr (OP == OP_W8A8) {                                                                     \
-      _Pragma("unroll") for (int i = 0; i < B_CH; ++i) rb[i] =                                        \
+      _Pragma("unroll") for (int i = 0; i < B_CH; ++i) rb[buf_][i] =                                  \
           *reinterpret_cast<const v4u*>(b_src[i] + (long)kt_v * 64);                                 \
     } else {                                                                                           \
       const v4u* U = reinterpret_cast<const v4u*>(g.B);                                               \
@@ -178,29 +201,29 @@ __global__ void __launch_bounds__(256) gemm_kernel(const GemmArgs g) {
         const int blk = (OP == OP_W4A16) ? kt_v : 2 * kt_v + (i & 1);                                  \
         const int n = min(n0 + tid + 256 * rr, N - 1);                                                 \
         const long idx = panel_index(n, blk, nblk);                                                    \
-        ru[i] = U[idx];                                                                                \
-        rs[i] = g.bsc[idx];                                                                            \
+        ru[buf_][i] = U[idx];                                                                          \
+        rs[buf_][i] = g.bsc[idx];                                                                      \
       }                                                                                                \
     }                                                                                                  \
   } while (0)
 
-#define Q4_STORE_LDS(stage_)                                                                           \
+#define Q4_STORE_LDS(buf_, stage_)                                                                     \
   do {                                                                                                 \
     uint8_t* base_ = lds + (stage_) * STAGE;                                                           \
     _Pragma("unroll") for (int i = 0; i < A_CH; ++i) {                                                \
       const int r = (tid >> 2) + 64 * i;                                                               \
-      *reinterpret_cast<v4u*>(base_ + lds_off(r, a_chunk)) = ra[i];                                    \
+      *reinterpret_cast<v4u*>(base_ + lds_off(r, a_chunk)) = ra[buf_][i];                              \
     }                                                                                                  \
     if constexpr (OP == OP_W8A8) {                                                                     \
       _Pragma("unroll") for (int i = 0; i < B_CH; ++i) {                                              \
         const int r = BM + (tid >> 2) + 64 * i;                                                        \
-        *reinterpret_cast<v4u*>(base_ + lds_off(r, a_chunk)) = rb[i];                                  \
+        *reinterpret_cast<v4u*>(base_ + lds_off(r, a_chunk)) = rb[buf_][i];                            \
       }                                                                                                \
     } else if constexpr (OP == OP_W4A16) {                                                             \
       _Pragma("unroll") for (int i = 0; i < B_CH; ++i) {                                              \
         const int r = BM + tid + 256 * i;                                                              \
         v4u o[4];                                                                                      \
-        dequant_unit_f16(ru[i], __builtin_bit_cast(_Float16, rs[i]), o);                               \
+        dequant_unit_f16(ru[buf_][i], __builtin_bit_cast(_Float16, rs[buf_][i]), o);                   \
         _Pragma("unroll") for (int c = 0; c < 4; ++c)                                                  \
             *reinterpret_cast<v4u*>(base_ + lds_off(r, c)) = o[c];                                     \
       }                                                                                                \
@@ -208,7 +231,7 @@ __global__ void __launch_bounds__(256) gemm_kernel(const GemmArgs g) {
       _Pragma("unroll") for (int i = 0; i < B_CH; ++i) {                                              \
         const int r = BM + tid + 256 * (i / 2);                                                        \
         v4u o[2];                                                                                      \
-        requant_unit_i8(ru[i], h2f(rs[i]), o);                                                         \
+        requant_unit_i8(ru[buf_][i], h2f(rs[buf_][i]), o);                                             \
         *reinterpret_cast<v4u*>(base_ + lds_off(r, 2 * (i & 1))) = o[0];                               \
         *reinterpret_cast<v4u*>(base_ + lds_off(r, 2 * (i & 1) + 1)) = o[1];                           \
       }                                                                                                \
@@ -221,38 +244,72 @@ __global__ void __launch_bounds__(256) gemm_kernel(const GemmArgs g) {
 #pragma unroll
     for (int j = 0; j < FN; ++j) acc[i][j] = acc_t{};
 
-  Q4_LOAD_REGS(0);
-  Q4_STORE_LDS(0);
+#pragma unroll
+  for (int d = 0; d < D; ++d) Q4_LOAD_REGS(d, d);
+  Q4_STORE_LDS(0, 0);
   __syncthreads();
 
   // MFMA operand: row lane % 32 of a 32-row tile, 16 bytes at byte 16 * (lane / 32) of the 32-byte k-slice
   const int frow = lane & 31, fhalf = lane >> 5;
-  for (int kt = 0; kt < nk; ++kt) {
-    const int cur = kt & 1;
-    if (kt + 1 < nk) Q4_LOAD_REGS(kt + 1);
-    const uint8_t* base = lds + cur * STAGE;
-#pragma unroll
-    for (int ks = 0; ks < 2; ++ks) {
-      const int ch = 2 * ks + fhalf;
-      v4i fa[FM], fb[FN];
-#pragma unroll
-      for (int i = 0; i < FM; ++i) fa[i] = *reinterpret_cast<const v4i*>(base + lds_off(wm * WM + 32 * i + frow, ch));
-#pragma unroll
-      for (int j = 0; j < FN; ++j)
-        fb[j] = *reinterpret_cast<const v4i*>(base + lds_off(BM + wn * WN + 32 * j + frow, ch));
-#pragma unroll
-      for (int i = 0; i < FM; ++i)
-#pragma unroll
-        for (int j = 0; j < FN; ++j) {
-          if constexpr (F16)
-            acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(v8h, fa[i]),
-                                                               __builtin_bit_cast(v8h, fb[j]), acc[i][j], 0, 0, 0);
-          else
-            acc[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(fa[i], fb[j], acc[i][j], 0, 0, 0);
-        }
+  {
+    // Explicit software pipeline per k-step, D rotating register buffers:
+    // global loads of k-step kt + D first, both k-slices' fragments read from
+    // LDS, then MFMAs of slice 0 interleaved with the slice-1 fragment reads
+    // and MFMAs of slice 1 interleaved with the LDS stores of k-step kt + 1
+    // (loaded D - 1 k-steps ago, into the other stage), one barrier. The
+    // sched_group_barrier sequence pins that order so the MFMA pipe is fed
+    // while LDS and memory requests are in flight.
+#define Q4_KSTEP(dl_, ds_)                                                                               \
+    do {                                                                                                \
+      Q4_LOAD_REGS(dl_, kt + D);                                                                        \
+      const uint8_t* base = lds + (kt & 1) * STAGE;                                                     \
+      v4i fa0[FM], fb0[FN], fa1[FM], fb1[FN];                                                           \
+      _Pragma("unroll") for (int i = 0; i < FM; ++i)                                                    \
+          fa0[i] = *reinterpret_cast<const v4i*>(base + lds_off(wm * WM + 32 * i + frow, fhalf));       \
+      _Pragma("unroll") for (int j = 0; j < FN; ++j)                                                    \
+          fb0[j] = *reinterpret_cast<const v4i*>(base + lds_off(BM + wn * WN + 32 * j + frow, fhalf));  \
+      _Pragma("unroll") for (int i = 0; i < FM; ++i)                                                    \
+          fa1[i] = *reinterpret_cast<const v4i*>(base + lds_off(wm * WM + 32 * i + frow, 2 + fhalf));   \
+      _Pragma("unroll") for (int j = 0; j < FN; ++j)                                                    \
+          fb1[j] = *reinterpret_cast<const v4i*>(base + lds_off(BM + wn * WN + 32 * j + frow, 2 + fhalf)); \
+      _Pragma("unroll") for (int i = 0; i < FM; ++i)                                                    \
+        _Pragma("unroll") for (int j = 0; j < FN; ++j) acc[i][j] = q4_mfma<F16>(fa0[i], fb0[j], acc[i][j]); \
+      _Pragma("unroll") for (int i = 0; i < FM; ++i)                                                    \
+        _Pragma("unroll") for (int j = 0; j < FN; ++j) acc[i][j] = q4_mfma<F16>(fa1[i], fb1[j], acc[i][j]); \
+      Q4_STORE_LDS(ds_, (kt + 1) & 1); /* past the last k-step: clamped data nobody reads */            \
+      Q4_SCHED();                                                                                       \
+      __syncthreads();                                                                                  \
+    } while (0)
+#if !defined(Q4MI_GEMM_SGB) || Q4MI_GEMM_SGB
+    constexpr int NMF = FM * FN;                                          // MFMAs per k-slice
+    constexpr int NRD = FM + FN;                                          // fragment reads per k-slice
+    constexpr int NVM = (OP == OP_W8A8) ? A_CH + B_CH : A_CH + 2 * B_CH;  // global loads per k-step
+    constexpr int NWR = (OP == OP_W8A8) ? A_CH + B_CH : (OP == OP_W4A16 ? A_CH + 4 * B_CH : A_CH + 2 * B_CH);
+#define Q4_SCHED()                                                                                      \
+    do {                                                                                                \
+      __builtin_amdgcn_sched_group_barrier(0x020, NVM, 0);                                              \
+      __builtin_amdgcn_sched_group_barrier(0x100, NRD, 0);                                              \
+      _Pragma("unroll") for (int q = 0; q < NRD; ++q) {                                                 \
+        __builtin_amdgcn_sched_group_barrier(0x008, NMF / NRD > 0 ? NMF / NRD : 1, 0);                  \
+        __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);                                              \
+      }                                                                                                 \
+      __builtin_amdgcn_sched_group_barrier(0x008, NMF - (NMF / NRD) * NRD, 0);                          \
+      _Pragma("unroll") for (int q = 0; q < NWR; ++q) {                                                 \
+        __builtin_amdgcn_sched_group_barrier(0x008, NMF / NWR > 0 ? NMF / NWR : 1, 0);                  \
+        __builtin_amdgcn_sched_group_barrier(0x200, 1, 0);                                              \
+      }                                                                                                 \
+    } while (0)
+#else
+#define Q4_SCHED() do {} while (0)
+#endif
+    for (int kt0 = 0; kt0 < nk; kt0 += D) {
+      { const int kt = kt0;     Q4_KSTEP(0, 1 % D); }
+      if constexpr (D > 1) { const int kt = kt0 + 1; Q4_KSTEP(1 % D, 2 % D); }
+      if constexpr (D > 2) { const int kt = kt0 + 2; Q4_KSTEP(2 % D, 3 % D); }
+      if constexpr (D > 3) { const int kt = kt0 + 3; Q4_KSTEP(3 % D, 4 % D); }
     }
-    if (kt + 1 < nk) Q4_STORE_LDS(cur ^ 1);
-    __syncthreads();
+#undef Q4_KSTEP
+#undef Q4_SCHED
   }
 
   // ---- epilogue through LDS (free after the loop's last barrier). Register
@@ -265,6 +322,24 @@ __global__ void __launch_bounds__(256) gemm_kernel(const GemmArgs g) {
   const int col = lane & 31, rh = (lane >> 5) * 4;
   const int mw = m0 + wm * WM, nw = n0 + wn * WN;
   const int rrow = lane >> 3, rcol = (lane & 7) * 4;
+  constexpr int NIT = WM / 8;  // strip rows handled per lane: 8 it + lane / 8
+  // every per-row / per-column scale this lane needs, loaded up front (the
+  // loads are independent; issuing them inside the store loop would put one
+  // L2 round trip per row on the critical path)
+  float sav[F16 ? 1 : NIT];
+  float swv[F16 ? 1 : FN][4];
+  if constexpr (!F16) {
+#pragma unroll
+    for (int it = 0; it < NIT; ++it) sav[it] = g.sa ? g.sa[min(mw + 8 * it + rrow, M - 1)] : 0.0f;
+#pragma unroll
+    for (int j = 0; j < FN; ++j)
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const int ne = min(nw + 32 * j + rcol + e, N - 1);
+        swv[j][e] = g.sw_f16 ? h2f(reinterpret_cast<const uint16_t*>(g.sw)[ne])
+                             : (g.sw ? reinterpret_cast<const float*>(g.sw)[ne] : 0.0f);
+      }
+  }
 #pragma unroll
   for (int j = 0; j < FN; ++j) {
 #pragma unroll
@@ -272,49 +347,42 @@ __global__ void __launch_bounds__(256) gemm_kernel(const GemmArgs g) {
     __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0): this wave's strip is in LDS
     __builtin_amdgcn_wave_barrier();
     const int n = nw + 32 * j + rcol;
-    float swv[4] = {1.0f, 1.0f, 1.0f, 1.0f};
-    if constexpr (!F16) {
 #pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        const int ne = min(n + e, N - 1);
-        swv[e] = g.sw_f16 ? h2f(reinterpret_cast<const uint16_t*>(g.sw)[ne]) : reinterpret_cast<const float*>(g.sw)[ne];
-      }
-    }
-    for (int it = 0; it < WM / 8; ++it) {
+    for (int it = 0; it < NIT; ++it) {
       const int row = 8 * it + rrow;
       const int m = mw + row;
       const uint4 q = *reinterpret_cast<const uint4*>(strip + row * EST + rcol);
       const uint32_t qv[4] = {q.x, q.y, q.z, q.w};
-      if (m >= M) continue;
-      const long o = (long)m * N + n;
-      if constexpr (F16) {
-        uint16_t h[4];
-#pragma unroll
-        for (int e = 0; e < 4; ++e) h[e] = f2h(__builtin_bit_cast(float, qv[e]));
-        if (n + 3 < N && (o & 3) == 0) {
-          *reinterpret_cast<ushort4*>(g.Y + o) = make_ushort4(h[0], h[1], h[2], h[3]);
-        } else {
-          for (int e = 0; e < 4; ++e)
-            if (n + e < N) g.Y[o + e] = h[e];
-        }
-      } else {
-        const float sam = g.sa ? g.sa[m] : 0.0f;
-        uint16_t h[4];
-#pragma unroll
-        for (int e = 0; e < 4; ++e)
-          h[e] = f2h_after_f32(__fmul_rn(__fmul_rn((float)(int)qv[e], sam), swv[e]));
+      if (m < M) {
+        const long o = (long)m * N + n;
         const bool vec = n + 3 < N && (o & 3) == 0;
-        if (g.C) {
-          if (vec) *reinterpret_cast<uint4*>(g.C + o) = q;
-          else
-            for (int e = 0; e < 4; ++e)
-              if (n + e < N) g.C[o + e] = (int32_t)qv[e];
-        }
-        if (g.Y) {
-          if (vec) *reinterpret_cast<ushort4*>(g.Y + o) = make_ushort4(h[0], h[1], h[2], h[3]);
-          else
+        if constexpr (F16) {
+          uint16_t h[4];
+#pragma unroll
+          for (int e = 0; e < 4; ++e) h[e] = f2h(__builtin_bit_cast(float, qv[e]));
+          if (vec) {
+            *reinterpret_cast<ushort4*>(g.Y + o) = make_ushort4(h[0], h[1], h[2], h[3]);
+          } else {
             for (int e = 0; e < 4; ++e)
               if (n + e < N) g.Y[o + e] = h[e];
+          }
+        } else {
+          if (g.C) {
+            if (vec) *reinterpret_cast<uint4*>(g.C + o) = q;
+            else
+              for (int e = 0; e < 4; ++e)
+                if (n + e < N) g.C[o + e] = (int32_t)qv[e];
+          }
+          if (g.Y) {
+            uint16_t h[4];
+#pragma unroll
+            for (int e = 0; e < 4; ++e)
+              h[e] = f2h_after_f32(__fmul_rn(__fmul_rn((float)(int)qv[e], sav[it]), swv[j][e]));
+            if (vec) *reinterpret_cast<ushort4*>(g.Y + o) = make_ushort4(h[0], h[1], h[2], h[3]);
+            else
+              for (int e = 0; e < 4; ++e)
+                if (n + e < N) g.Y[o + e] = h[e];
+          }
         }
       }
     }
@@ -370,15 +438,29 @@ __global__ void __launch_bounds__(256) quant_act_kernel(const void* __restrict__
 template <int OP, int BM, int BN>
 static int launch_tiles(const GemmArgs& g, void* stream, const char* name) {
   const int ntm = ceil_div(g.M, BM), ntn = ceil_div(g.N, BN);
-  hipLaunchKernelGGL((gemm_kernel<OP, BM, BN>), dim3(ntm * ntn), dim3(256), 0, as_stream(stream), g);
+  const int nk = OP == OP_W4A16 ? g.K / 32 : g.K / 64;
+#ifndef Q4MI_GEMM_DEEP
+#define Q4MI_GEMM_DEEP 2
+#endif
+#ifndef Q4MI_GEMM_DEEP_SMALL
+#define Q4MI_GEMM_DEEP_SMALL 4
+#endif
+  constexpr int DEEP = BM >= 256 ? Q4MI_GEMM_DEEP : Q4MI_GEMM_DEEP_SMALL;
+  if (nk % DEEP == 0)
+    hipLaunchKernelGGL((gemm_kernel<OP, BM, BN, DEEP>), dim3(ntm * ntn), dim3(256), 0, as_stream(stream), g);
+  else
+    hipLaunchKernelGGL((gemm_kernel<OP, BM, BN, 1>), dim3(ntm * ntn), dim3(256), 0, as_stream(stream), g);
   Q4_LAUNCHED(name);
   return Q4_OK;
 }
 
-// 256 x 256 tiles when they give at least one workgroup per CU, else 128 x 256.
+// 128 x 256 tiles: with a 4-deep register prefetch they fit the register
+// file without spills (256 x 256 tiles spill at any prefetch depth > 1).
 template <int OP>
 static int launch_gemm(const GemmArgs& g, void* stream, const char* name) {
+#if !defined(Q4MI_GEMM_BIG) || Q4MI_GEMM_BIG
   if ((long)ceil_div(g.M, 256) * ceil_div(g.N, 256) >= 256) return launch_tiles<OP, 256, 256>(g, stream, name);
+#endif
   return launch_tiles<OP, 128, 256>(g, stream, name);
 }
 
