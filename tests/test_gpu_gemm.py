@@ -55,7 +55,7 @@ def test_w8a8_bit_exact(gpu, M, N, K, swdt):
 
 
 def test_w8a8_config_size_rows(gpu):
-    """M=2048, N=15360, K=3840. The int32 accumulator of 96 rows
+    """Prefill shape M=2048, N=15360, K=3840. The int32 accumulator of 96 rows
     (spread over all M-tiles) and every fp16 output are checked bit-exactly."""
     rng = np.random.default_rng(0)
     M, N, K = 2048, 15360, 3840

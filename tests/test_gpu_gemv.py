@@ -54,7 +54,7 @@ def test_gemv_split_invariance(gpu, split, rows, monkeypatch):
 
 
 def test_gemv_c1_full_size(gpu):
-    """configs[0] shape: N=15360, K=3840, fp16 x and y, seeded as the config states."""
+    """Down-projection-sized GEMV N=15360, K=3840, fp16 x and y, seed 0."""
     rng = np.random.default_rng(0)
     x = rng.standard_normal(3840).astype(np.float16)
     codes = rng.integers(-8, 8, (15360, 3840))
@@ -73,7 +73,7 @@ def test_gemv_c1_full_size(gpu):
 
 
 def test_gemv_e4m3_scales(gpu):
-    """configs[2]: e4m3 block scales; the oracle uses identically rounded scales."""
+    """e4m3 block scales; the oracle uses identically rounded scales."""
     rng = np.random.default_rng(2)
     for N, K in [(256, 256), (15360, 3840), (3840, 15360)]:
         q, s, x = _case(rng, N, K)
