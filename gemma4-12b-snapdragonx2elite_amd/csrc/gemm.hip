@@ -8,27 +8,48 @@
 //          (vk/coopgemm_i4h.comp, which accumulates in f16; this one
 //          accumulates in fp32)          v_mfma_f32_32x32x16_f16
 //
-// One kernel template serves all three: every k-step stages 64-byte rows of
-// both operands in LDS (64 int8 or 32 f16 elements), so the LDS layout, the
-// XOR swizzle and the MFMA fragment reads are shared; only the B-operand
-// producer (byte copy, int4 -> f16 dequant, int4 -> int8 requant) and the
-// MFMA/epilogue differ.
+// Both kernels stage the activation tile A through an LDS ring filled by
+// direct-to-LDS loads (global_load_lds_dwordx4: no VGPR round trip, no
+// staging registers) and feed 4 waves (2 x 2, each a (BM/2) x 128 block of
+// 32x32 MFMA tiles) from it. They differ in how the weight operand B
+// arrives:
+//  * W8A8 (w8a8_kernel): int8 rows are loaded into registers one and a half
+//    k-steps ahead and written into a second LDS ring; fragments are read
+//    from LDS like A's. Direct-to-LDS loads sustain only ~24 B/clk per CU on
+//    MI355X, half of what the 256x256 tile needs, so the two operands take
+//    the two load paths.
+//  * W4A16 / W4A8 (w4_kernel): each lane loads the 8-byte half of a
+//    32-element int4 unit that its MFMA fragment needs (the panel-64 layout
+//    makes the 32 rows of a fragment 512 contiguous bytes) several k-steps
+//    ahead, and dequantizes (f16) or requantizes (int8) it straight into
+//    fragment registers. B never touches LDS, which leaves LDS bandwidth to
+//    A: with the 128-row tiles that M = 512 needs, staging both operands in
+//    LDS would need more than the ~128 B/clk LDS read bandwidth per CU.
+//    The k order inside a fragment is permuted consistently for A and B
+//    (a dot product does not care) so each lane's 16 k-values come from one
+//    contiguous half-unit.
 //
-// Tiling: BM x BN macro tile per 256-thread workgroup (4 waves as 2 x 2),
-// each wave a (BM/2) x (BN/2) block of 32x32 MFMA tiles
-// (v_mfma_i32_32x32x32_i8 / v_mfma_f32_32x32x16_f16: both take 16 operand
-// bytes per lane, half the operand traffic per MAC of the 16x16 shapes);
-// a 64-byte k-row is two MFMA k-slices. LDS double buffered with one
-// barrier per k-step; the next k-step's global loads are in flight while
-// the current one's MFMAs run. Workgroups are remapped so
-// each XCD (8 per MI355X, own L2) works on a contiguous 1/8 of the grid
-// ordered by weight panel, which keeps a weight panel's re-reads in one L2.
+// All global loads are issued through inline asm and all waits are explicit
+// s_waitcnt vmcnt(n) with the count fixed by the issue order: the compiler's
+// own tracking of direct-to-LDS writes is conservative (it waits for every
+// outstanding load before each LDS access), which would serialize the ring.
+// Each wait also pins the registers it covers (an empty asm that reads and
+// writes them), so no use of a loaded value can be scheduled above its wait.
+//
+// Workgroups are remapped so each XCD (8 per MI355X, own L2) works on a
+// contiguous 1/8 of the tile grid ordered by weight panel. W4A16 splits K
+// across workgroups when the tile grid alone cannot fill the 256 CUs
+// (tall-K shapes such as the down projection), writing fp32 partials that a
+// second kernel sums in split order (deterministic).
 #include "q4mi_common.h"
 
 namespace q4 {
 
 enum { OP_W8A8 = 0, OP_W4A16 = 1, OP_W4A8 = 2 };
-constexpr int GEMM_WAVES_EPI = 4;
+
+typedef unsigned v2u __attribute__((ext_vector_type(2)));
+typedef int v16i __attribute__((ext_vector_type(16)));
+typedef float v16f __attribute__((ext_vector_type(16)));
 
 struct GemmArgs {
   const void* A;        // int8 [M][K] or f16 [M][K]
@@ -39,59 +60,81 @@ struct GemmArgs {
   int sw_f16;
   uint16_t* Y;          // f16 [M][N] (may be NULL for int paths if C given)
   int32_t* C;           // int32 [M][N] or NULL
+  float* P;             // W4A16 split-K: fp32 partials [split][M][N]
   int M, N, K;
 };
 
-// LDS byte offset of 16-byte chunk c (0..3) of staged row r. The XOR keeps
-// both the row-per-lane MFMA reads and the chunk-per-lane stores free of
-// bank conflicts.
-#ifndef Q4MI_GEMM_SWZ
-#define Q4MI_GEMM_SWZ 1
-#endif
-__device__ inline int lds_off(int r, int c) {
-#if Q4MI_GEMM_SWZ
-  // distinct 16-byte bank groups for any 8 consecutive rows (same chunk) and
-  // for rows {0, 4, 8, 12} (+1, +2, +3) of any 16: conflict-free whether the
-  // LDS serves 8 or 16 lanes of a ds_read_b128 per cycle
-  return r * 64 + ((c ^ (((r >> 1) & 3) ^ ((r >> 3) & 1))) << 4);
-#else
-  return r * 64 + ((c ^ ((r >> 1) & 3)) << 4);
-#endif
+// ---- inline-asm memory operations ------------------------------------------
+// 16 bytes per lane from global memory into LDS at lds_dst + 16 * lane
+// (lds_dst wave-uniform).
+__device__ inline void dma16(const void* gptr, const void* lds_dst) {
+  const unsigned l = __builtin_amdgcn_readfirstlane((unsigned)(uintptr_t)lds_dst);
+  asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(gptr), "s"(l) : "memory");
 }
+__device__ inline v4u ld16(const void* p) {
+  v4u r;
+  asm volatile("global_load_dwordx4 %0, %1, off" : "=v"(r) : "v"(p));
+  return r;
+}
+__device__ inline v2u ld8(const void* p) {
+  v2u r;
+  asm volatile("global_load_dwordx2 %0, %1, off" : "=v"(r) : "v"(p));
+  return r;
+}
+__device__ inline uint32_t ld2(const void* p) {
+  uint32_t r;
+  asm volatile("global_load_ushort %0, %1, off" : "=v"(r) : "v"(p));
+  return r;
+}
+template <int N>
+__device__ inline void vmwait() {
+  static_assert(N >= 0 && N < 64, "vmcnt range");
+  asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
+}
+__device__ inline void lgkm0() { asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory"); }
+template <class T>
+__device__ inline void pin(T& v) {
+  asm volatile("" : "+v"(v));
+}
+
+// LDS byte offset of 16-byte chunk c (0..3) of staged 64-byte row r. The XOR
+// keeps both the row-per-lane MFMA reads and the chunk-per-lane writes free
+// of bank conflicts: distinct 16-byte bank groups for any 8 consecutive rows
+// (same chunk) and for rows {0, 4, 8, 12} (+1, +2, +3) of any 16, whether
+// the LDS serves 8 or 16 lanes of a ds_read_b128 per cycle.
+__device__ inline int swz(int r) { return ((r >> 1) & 3) ^ ((r >> 3) & 1); }
+__device__ inline int lds_off(int r, int c) { return r * 64 + ((c ^ swz(r)) << 4); }
 
 __device__ inline uint32_t pk_h2(v2h v) { return __builtin_bit_cast(uint32_t, v); }
 
-// int4 unit -> 32 f16 values f16((q - 8) * s), 4 chunks of 8 (k order).
-// Low nibbles: 0x6400 | q = 1024 + q; high nibbles: 0x6400 | 16q =
-// 1024 + 16q. Both become q - 8 exactly, then one RNE multiply by s, which
-// is the reference's float16_t((float(q) - 8.0) * scl).
-__device__ inline void dequant_unit_f16(const v4u u, _Float16 s, v4u out[4]) {
-  const uint32_t w[4] = {u.x, u.y, u.z, u.w};
-  const v2h sv = {s, s};
+// One device word (8 int4 codes, k order e = 0..7 at nibble (e&1)*4 + (e>>1))
+// -> 8 f16 values f16((q - 8) * s) in k order. Low nibbles: 0x6400 | q =
+// 1024 + q; high nibbles: 0x6400 | 16q = 1024 + 16q. Both become q - 8
+// exactly, then one RNE multiply by s: the reference's
+// float16_t((float(q) - 8.0) * scl) (vk/coopgemm_i4h.comp:24).
+__device__ inline v4u dequant_word_f16(uint32_t w, v2h sv) {
   const v2h off_lo = {(_Float16)1032.0f, (_Float16)1032.0f};
   const v2h sixteenth = {(_Float16)0.0625f, (_Float16)0.0625f};
   const v2h off_hi = {(_Float16)72.0f, (_Float16)72.0f};
-#pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    const uint32_t w8 = w[i] >> 8;
-    v2h p0 = __builtin_bit_cast(v2h, (w[i] & 0x000F000Fu) | 0x64006400u);
-    v2h p1 = __builtin_bit_cast(v2h, (w[i] & 0x00F000F0u) | 0x64006400u);
-    v2h p2 = __builtin_bit_cast(v2h, (w8 & 0x000F000Fu) | 0x64006400u);
-    v2h p3 = __builtin_bit_cast(v2h, (w8 & 0x00F000F0u) | 0x64006400u);
-    p0 = (p0 - off_lo) * sv;
-    p1 = (p1 * sixteenth - off_hi) * sv;
-    p2 = (p2 - off_lo) * sv;
-    p3 = (p3 * sixteenth - off_hi) * sv;
-    out[i] = v4u{pk_h2(p0), pk_h2(p1), pk_h2(p2), pk_h2(p3)};
-  }
+  const uint32_t w8 = w >> 8;
+  v2h p0 = __builtin_bit_cast(v2h, (w & 0x000F000Fu) | 0x64006400u);
+  v2h p1 = __builtin_bit_cast(v2h, (w & 0x00F000F0u) | 0x64006400u);
+  v2h p2 = __builtin_bit_cast(v2h, (w8 & 0x000F000Fu) | 0x64006400u);
+  v2h p3 = __builtin_bit_cast(v2h, (w8 & 0x00F000F0u) | 0x64006400u);
+  p0 = (p0 - off_lo) * sv;
+  p1 = (p1 * sixteenth - off_hi) * sv;
+  p2 = (p2 - off_lo) * sv;
+  p3 = (p3 * sixteenth - off_hi) * sv;
+  return v4u{pk_h2(p0), pk_h2(p1), pk_h2(p2), pk_h2(p3)};
 }
 
-// int4 unit -> 32 int8 values clamp(rint((q - 8) * r), -127, 127), k order.
-__device__ inline void requant_unit_i8(const v4u u, float r, v4u out[2]) {
-  const uint32_t w[4] = {u.x, u.y, u.z, u.w};
-  uint32_t o[8];
+// Two device words (16 codes, k order) -> 16 int8 values
+// clamp(rint((q - 8) * r), -127, 127) in k order (vk/coopgemm_w4a8.comp:28-34).
+__device__ inline v4u requant_words_i8(uint32_t wa, uint32_t wb, float r) {
+  const uint32_t w[2] = {wa, wb};
+  uint32_t o[4];
 #pragma unroll
-  for (int i = 0; i < 4; ++i) {
+  for (int i = 0; i < 2; ++i) {
 #pragma unroll
     for (int h = 0; h < 2; ++h) {
       uint32_t word = 0;
@@ -106,19 +149,15 @@ __device__ inline void requant_unit_i8(const v4u u, float r, v4u out[2]) {
       o[2 * i + h] = word;
     }
   }
-  out[0] = v4u{o[0], o[1], o[2], o[3]};
-  out[1] = v4u{o[4], o[5], o[6], o[7]};
+  return v4u{o[0], o[1], o[2], o[3]};
 }
-
-typedef int v16i __attribute__((ext_vector_type(16)));
-typedef float v16f __attribute__((ext_vector_type(16)));
 
 // Copy one 32x32 accumulator tile (16 registers per lane) into an LDS strip
 // with row stride `st` words: register v goes to row 8 (v / 4) + v % 4 (the
-// lane's 4-row half is folded into p). Each element is moved to a VGPR
-// first (the empty asm with a "v" operand): LDS stores taking the elements
-// straight from the accumulator registers were compiled to 16 stores of the
-// tile's first register.
+// lane's 4-row half is folded into p). The elements go through a memcpy to a
+// plain array first: LDS stores taking the elements straight from the
+// accumulator registers were compiled to 16 stores of the tile's first
+// register.
 template <class V>
 __device__ inline void store_tile_strip(uint32_t* p, int st, const V t) {
   uint32_t e[16];
@@ -127,115 +166,343 @@ __device__ inline void store_tile_strip(uint32_t* p, int st, const V t) {
   for (int v = 0; v < 16; ++v) p[(8 * (v >> 2) + (v & 3)) * st] = e[v];
 }
 
-template <bool F16, class A>
-__device__ inline A q4_mfma(v4i a, v4i b, A c) {
-  if constexpr (F16)
-    return __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(v8h, a), __builtin_bit_cast(v8h, b), c, 0, 0, 0);
-  else
-    return __builtin_amdgcn_mfma_i32_32x32x32_i8(a, b, c, 0, 0, 0);
+// Tile (tm, tn) of workgroup w: each XCD (workgroups w % 8, round-robin
+// dispatch) gets a contiguous 1/8 of the grid, M fastest, so the tiles an XCD
+// runs together share weight panels in its L2.
+__device__ inline void tile_of(int w, int G, int ntm, int& tm, int& tn) {
+  const int v = (G % 8 == 0) ? (w % 8) * (G / 8) + w / 8 : w;
+  tm = v % ntm;
+  tn = v / ntm;
 }
 
-template <int OP, int BM, int BN, int D>
-__global__ void __launch_bounds__(256) gemm_kernel(const GemmArgs g) {
-  constexpr int STAGE = (BM + BN) * 64;
-  constexpr int WM = BM / 2, WN = BN / 2, FM = WM / 32, FN = WN / 32;
-  constexpr int A_CH = BM / 64;                                      // A chunks per thread per k-step
-  constexpr int B_CH = (OP == OP_W8A8) ? BN / 64 : (OP == OP_W4A16 ? BN / 256 : BN / 128);
-  constexpr bool F16 = (OP == OP_W4A16);
-  static_assert(BN % 256 == 0 || OP == OP_W8A8, "int4 B producers need BN % 256 == 0");
-  typedef typename std::conditional<F16, v16f, v16i>::type acc_t;
+constexpr int EST = 68;  // epilogue strip row stride (words): 64 columns + 4 to stagger banks
 
-  constexpr int EST = 36;  // epilogue strip row stride in 32-bit words (16-byte aligned, staggers banks)
-  constexpr int EPI = GEMM_WAVES_EPI * WM * EST * 4;
-  __shared__ __attribute__((aligned(16))) uint8_t lds[2 * STAGE > EPI ? 2 * STAGE : EPI];
+// Epilogue: the wave's WM x 128 accumulator block goes through a 64-column
+// LDS strip per half (so each stored row segment is a full 128-byte line of
+// f16 Y) and is stored row-contiguously, 4 columns per lane. MODE 0: int32
+// accumulators -> Y = f16((f32(C) * sa) * sw) and/or C; MODE 1: fp32 -> f16
+// Y; MODE 2: fp32 -> fp32 partials P.
+template <int MODE, int WM, class acc_t>
+__device__ inline void epilogue(const GemmArgs& g, uint32_t* strip, const acc_t (&acc)[WM / 32][4], int mw, int nw,
+                                float* P) {
+  constexpr int FM = WM / 32, NIT = WM / 4;
+  const int lane = threadIdx.x & 63;
+  const int col = lane & 31, rh = (lane >> 5) * 4;
+  const int rrow = lane >> 4, rcol = (lane & 15) * 4;
+  const int M = g.M, N = g.N;
+  // every per-row scale this lane needs, loaded up front (independent loads;
+  // inside the store loop each would put an L2 round trip on the critical path)
+  float sav[MODE == 0 ? NIT : 1];
+  if constexpr (MODE == 0) {
+#pragma unroll
+    for (int it = 0; it < NIT; ++it) sav[it] = g.Y ? g.sa[min(mw + 4 * it + rrow, M - 1)] : 0.0f;
+  }
+#pragma unroll
+  for (int jp = 0; jp < 2; ++jp) {
+    const int n = nw + 64 * jp + rcol;
+    float swv[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+    if constexpr (MODE == 0) {
+      if (g.Y) {
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const int ne = min(n + e, N - 1);
+          swv[e] = g.sw_f16 ? h2f(reinterpret_cast<const uint16_t*>(g.sw)[ne]) : reinterpret_cast<const float*>(g.sw)[ne];
+        }
+      }
+    }
+#pragma unroll
+    for (int h = 0; h < 2; ++h)
+#pragma unroll
+      for (int i = 0; i < FM; ++i) store_tile_strip(strip + (32 * i + rh) * EST + 32 * h + col, EST, acc[i][2 * jp + h]);
+    lgkm0();
+    __builtin_amdgcn_wave_barrier();
+#pragma unroll
+    for (int it = 0; it < NIT; ++it) {
+      const int row = 4 * it + rrow;
+      const int m = mw + row;
+      const v4u q = *reinterpret_cast<const v4u*>(strip + row * EST + rcol);
+      // elements through a plain array: bit-casting q[e] of the vector inside
+      // the unrolled loop was compiled to four stores of element 0
+      uint32_t qv[4];
+      __builtin_memcpy(qv, &q, sizeof(qv));
+      if (m < M) {
+        const long o = (long)m * N + n;
+        const bool vec = n + 3 < N && (o & 3) == 0;
+        if constexpr (MODE == 2) {
+          if (vec) {
+            *reinterpret_cast<v4u*>(P + o) = q;
+          } else {
+            for (int e = 0; e < 4; ++e)
+              if (n + e < N) P[o + e] = __builtin_bit_cast(float, qv[e]);
+          }
+        } else {
+          uint16_t hv[4];
+          if constexpr (MODE == 1) {
+#pragma unroll
+            for (int e = 0; e < 4; ++e) hv[e] = f2h(__builtin_bit_cast(float, qv[e]));
+          } else {
+            if (g.C) {
+              if (vec) {
+                *reinterpret_cast<v4u*>(g.C + o) = q;
+              } else {
+                for (int e = 0; e < 4; ++e)
+                  if (n + e < N) g.C[o + e] = (int32_t)qv[e];
+              }
+            }
+#pragma unroll
+            for (int e = 0; e < 4; ++e)
+              hv[e] = f2h_after_f32(__fmul_rn(__fmul_rn((float)(int)qv[e], sav[it]), swv[e]));
+          }
+          if (MODE == 1 || g.Y) {
+            if (vec) {
+              *reinterpret_cast<ushort4*>(g.Y + o) = make_ushort4(hv[0], hv[1], hv[2], hv[3]);
+            } else {
+              for (int e = 0; e < 4; ++e)
+                if (n + e < N) g.Y[o + e] = hv[e];
+            }
+          }
+        }
+      }
+    }
+    __builtin_amdgcn_wave_barrier();  // strip reads done before the next half overwrites it
+  }
+}
+
+// ---- W8A8 ---------------------------------------------------------------------
+// BM x 256 tile, K step 64 bytes. LDS: A ring (4 stages, direct loads) and B
+// ring (4 stages, register loads + ds_write) in two arrays.
+// Issue order per k-step j: B(j + 3) register loads, then A(j + 4) direct
+// loads (into the stage k-step j used, whose fragments every wave read in
+// the previous k-step); in the middle of k-step j, B(j + 2) is written to
+// LDS; one barrier at the end makes k-step j + 2 visible. MFMAs of k-step j
+// run from registers while k-step j + 1's fragments are read.
+template <int BM>
+__global__ void __launch_bounds__(256) w8a8_kernel(const GemmArgs g) {
+  constexpr int BN = 256, S = 4, WM = BM / 2, WN = 128, FM = WM / 32, FN = 4;
+  constexpr int NA = BM / 64;  // A direct loads per thread per k-step
+  constexpr int NB = 4;        // B register loads per thread per k-step
+  constexpr int AST = BM * 64, BST = BN * 64;
+  constexpr int EPI = 2 * WM * EST * 4;  // two waves' epilogue strips per array
+  constexpr int LA = S * AST > EPI ? S * AST : EPI;
+  constexpr int LB = S * BST > EPI ? S * BST : EPI;
+  // separate arrays: ldsA is written only by direct loads, ldsB only by ds_write
+  __shared__ __attribute__((aligned(16))) uint8_t ldsA[LA];
+  __shared__ __attribute__((aligned(16))) uint8_t ldsB[LB];
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int wm = wave >> 1, wn = wave & 1;
   const int M = g.M, N = g.N, K = g.K;
-  const int ntm = (M + BM - 1) / BM;
-  const int G = gridDim.x, w = blockIdx.x;
-  const int v = (G % 8 == 0) ? (w % 8) * (G / 8) + w / 8 : w;
-  const int tm = v % ntm, tn = v / ntm;
+  int tm, tn;
+  tile_of(blockIdx.x, gridDim.x, (M + BM - 1) / BM, tm, tn);
   const int m0 = tm * BM, n0 = tn * BN;
-  const int nblk = K / BLK;
-  const int nk = F16 ? K / 32 : K / 64;                               // k-steps (64-byte rows)
-  const long a_row_bytes = F16 ? 2L * K : (long)K;
+  const int nk = K / 64;
 
-  // ---- per-thread global sources: rows (tid / 4) + 64 i, 16-byte chunk tid % 4 ----
-  const uint8_t* Ab = reinterpret_cast<const uint8_t*>(g.A);
-  const int a_chunk = tid & 3;
-  const uint8_t* a_src[A_CH];
+  // A: wave instruction i stages rows (wave * NA + i) * 16 .. + 16, 4 lanes per row
+  const int8_t* asrc[NA];
 #pragma unroll
-  for (int i = 0; i < A_CH; ++i)
-    a_src[i] = Ab + (long)min(m0 + (tid >> 2) + 64 * i, M - 1) * a_row_bytes + a_chunk * 16;
-  const uint8_t* b_src[(OP == OP_W8A8) ? B_CH : 1];
-  if constexpr (OP == OP_W8A8) {
-#pragma unroll
-    for (int i = 0; i < B_CH; ++i)
-      b_src[i] = reinterpret_cast<const uint8_t*>(g.B) + (long)min(n0 + (tid >> 2) + 64 * i, N - 1) * K + a_chunk * 16;
+  for (int i = 0; i < NA; ++i) {
+    const int r = (wave * NA + i) * 16 + (lane >> 2);
+    asrc[i] = reinterpret_cast<const int8_t*>(g.A) + (long)min(m0 + r, M - 1) * K + (((lane & 3) ^ swz(r)) << 4);
   }
+  // B: thread rows (tid / 4) + 64 i, chunk tid % 4
+  const int8_t* bsrc[NB];
+#pragma unroll
+  for (int i = 0; i < NB; ++i)
+    bsrc[i] = reinterpret_cast<const int8_t*>(g.B) + (long)min(n0 + (tid >> 2) + 64 * i, N - 1) * K + (tid & 3) * 16;
+  const int bdst = lds_off(tid >> 2, tid & 3);  // + 4096 i (64 rows further, same swizzle)
 
-  // D rotating register buffers of one k-step each (native vector registers:
-  // HIP's uint4 is a union struct the compiler keeps in scratch here). A
-  // k-step is loaded D iterations before it is staged into LDS, so D - 1
-  // k-steps of MFMA work hide the global load latency.
-  v4u ra[D][A_CH];
-  v4u rb[D][(OP == OP_W8A8) ? B_CH : 1];
-  v4u ru[D][(OP == OP_W8A8) ? 1 : B_CH];
-  uint16_t rs[D][(OP == OP_W8A8) ? 1 : B_CH];
-
-#define Q4_LOAD_REGS(buf_, kt_)                                                                        \
-  do {                                                                                                 \
-    const int kt_v = min((kt_), nk - 1); /* clamped: every load unconditional */                       \
-    _Pragma("unroll") for (int i = 0; i < A_CH; ++i) ra[buf_][i] =                                    \
-        *reinterpret_cast<const v4u*>(a_src[i] + (long)kt_v * 64);                                   \
-    if constexpr (OP == OP_W8A8) {                                                                     \
-      _Pragma("unroll") for (int i = 0; i < B_CH; ++i) rb[buf_][i] =                                  \
-          *reinterpret_cast<const v4u*>(b_src[i] + (long)kt_v * 64);                                 \
-    } else {                                                                                           \
-      const v4u* U = reinterpret_cast<const v4u*>(g.B);                                               \
-      _Pragma("unroll") for (int i = 0; i < B_CH; ++i) {                                              \
-        /* W4A16: one block per k-step, row = tid + 256 i;                                          */ \
-        /* W4A8: two blocks per k-step, i = 2 rr + h, row = tid + 256 rr                              */ \
-        const int rr = (OP == OP_W4A16) ? i : i / 2;                                                   \
-        const int blk = (OP == OP_W4A16) ? kt_v : 2 * kt_v + (i & 1);                                  \
-        const int n = min(n0 + tid + 256 * rr, N - 1);                                                 \
-        const long idx = panel_index(n, blk, nblk);                                                    \
-        ru[buf_][i] = U[idx];                                                                          \
-        rs[buf_][i] = g.bsc[idx];                                                                      \
-      }                                                                                                \
-    }                                                                                                  \
+  v4u rb[2][NB];
+#define W8_LOAD_B(set_, kt_)                                                                    \
+  do {                                                                                          \
+    const long ko_ = (long)min((kt_), nk - 1) * 64;                                             \
+    _Pragma("unroll") for (int i = 0; i < NB; ++i) rb[set_][i] = ld16(bsrc[i] + ko_);          \
+  } while (0)
+#define W8_LOAD_A(kt_)                                                                          \
+  do {                                                                                          \
+    const long ko_ = (long)min((kt_), nk - 1) * 64;                                             \
+    uint8_t* st_ = ldsA + ((kt_) % S) * AST;                                                    \
+    _Pragma("unroll") for (int i = 0; i < NA; ++i) dma16(asrc[i] + ko_, st_ + (wave * NA + i) * 1024); \
+  } while (0)
+#define W8_STORE_B(set_, kt_)                                                                   \
+  do {                                                                                          \
+    uint8_t* st_ = ldsB + ((kt_) % S) * BST + bdst;                                             \
+    _Pragma("unroll") for (int i = 0; i < NB; ++i) {                                            \
+      pin(rb[set_][i]);                                                                         \
+      *reinterpret_cast<v4u*>(st_ + 4096 * i) = rb[set_][i];                                    \
+    }                                                                                           \
   } while (0)
 
-#define Q4_STORE_LDS(buf_, stage_)                                                                     \
-  do {                                                                                                 \
-    uint8_t* base_ = lds + (stage_) * STAGE;                                                           \
-    _Pragma("unroll") for (int i = 0; i < A_CH; ++i) {                                                \
-      const int r = (tid >> 2) + 64 * i;                                                               \
-      *reinterpret_cast<v4u*>(base_ + lds_off(r, a_chunk)) = ra[buf_][i];                              \
-    }                                                                                                  \
-    if constexpr (OP == OP_W8A8) {                                                                     \
-      _Pragma("unroll") for (int i = 0; i < B_CH; ++i) {                                              \
-        const int r = BM + (tid >> 2) + 64 * i;                                                        \
-        *reinterpret_cast<v4u*>(base_ + lds_off(r, a_chunk)) = rb[buf_][i];                            \
-      }                                                                                                \
-    } else if constexpr (OP == OP_W4A16) {                                                             \
-      _Pragma("unroll") for (int i = 0; i < B_CH; ++i) {                                              \
-        const int r = BM + tid + 256 * i;                                                              \
-        v4u o[4];                                                                                      \
-        dequant_unit_f16(ru[buf_][i], __builtin_bit_cast(_Float16, rs[buf_][i]), o);                   \
-        _Pragma("unroll") for (int c = 0; c < 4; ++c)                                                  \
-            *reinterpret_cast<v4u*>(base_ + lds_off(r, c)) = o[c];                                     \
-      }                                                                                                \
-    } else {                                                                                           \
-      _Pragma("unroll") for (int i = 0; i < B_CH; ++i) {                                              \
-        const int r = BM + tid + 256 * (i / 2);                                                        \
-        v4u o[2];                                                                                      \
-        requant_unit_i8(ru[buf_][i], h2f(rs[buf_][i]), o);                                             \
-        *reinterpret_cast<v4u*>(base_ + lds_off(r, 2 * (i & 1))) = o[0];                               \
-        *reinterpret_cast<v4u*>(base_ + lds_off(r, 2 * (i & 1) + 1)) = o[1];                           \
-      }                                                                                                \
-    }                                                                                                  \
+  v16i acc[FM][FN];
+#pragma unroll
+  for (int i = 0; i < FM; ++i)
+#pragma unroll
+    for (int j = 0; j < FN; ++j) acc[i][j] = v16i{};
+
+  const int frow = lane & 31, fh = lane >> 5;
+  auto rdA = [&](int stage, int i, int c) {
+    return *reinterpret_cast<const v4i*>(ldsA + stage * AST + lds_off(wm * WM + 32 * i + frow, c));
+  };
+  auto rdB = [&](int stage, int j, int c) {
+    return *reinterpret_cast<const v4i*>(ldsB + stage * BST + lds_off(wn * WN + 32 * j + frow, c));
+  };
+
+  // prologue, in the steady-state issue order: A0, [B0 A1], [B1 A2], [B2 A3]
+  W8_LOAD_A(0);
+  W8_LOAD_B(0, 0);
+  W8_LOAD_A(1);
+  W8_LOAD_B(1, 1);
+  W8_LOAD_A(2);
+  vmwait<2 * NA + NB>();  // B0 (and A0) landed
+  W8_STORE_B(0, 0);
+  W8_LOAD_B(0, 2);
+  W8_LOAD_A(3);
+  vmwait<2 * NA + NB>();  // B1 (and A1) landed
+  W8_STORE_B(1, 1);
+  lgkm0();
+  __builtin_amdgcn_s_barrier();  // stages 0 and 1 visible
+  v4i fa[2][2][FM], fb[2][2][FN];  // [buffer][k-slice][tile]
+#pragma unroll
+  for (int sl = 0; sl < 2; ++sl) {
+#pragma unroll
+    for (int i = 0; i < FM; ++i) fa[0][sl][i] = rdA(0, i, 2 * sl + fh);
+#pragma unroll
+    for (int j = 0; j < FN; ++j) fb[0][sl][j] = rdB(0, j, 2 * sl + fh);
+  }
+  lgkm0();
+  __builtin_amdgcn_s_barrier();  // stage 0 read by every wave: the first k-step may refill it
+
+  constexpr int NRD = FM + FN;  // fragment reads per k-slice
+  constexpr int NMF = FM * FN;  // MFMAs per k-slice
+#define W8_KSTEP(cur, nxt)                                                                                  \
+  do {                                                                                                      \
+    W8_LOAD_B(nxt, kt + 3);                                                                                 \
+    W8_LOAD_A(kt + 4);                                                                                      \
+    const int st1 = (kt + 1) % S;                                                                           \
+    _Pragma("unroll") for (int i = 0; i < FM; ++i) fa[nxt][0][i] = rdA(st1, i, fh);                         \
+    _Pragma("unroll") for (int j = 0; j < FN; ++j) fb[nxt][0][j] = rdB(st1, j, fh);                         \
+    _Pragma("unroll") for (int i = 0; i < FM; ++i)                                                          \
+      _Pragma("unroll") for (int j = 0; j < FN; ++j)                                                        \
+        acc[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(fa[cur][0][i], fb[cur][0][j], acc[i][j], 0, 0, 0);   \
+    _Pragma("unroll") for (int q = 0; q < NRD; ++q) {                                                       \
+      __builtin_amdgcn_sched_group_barrier(0x008, NMF / NRD > 0 ? NMF / NRD : 1, 0);                        \
+      __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);                                                    \
+    }                                                                                                       \
+    __builtin_amdgcn_sched_group_barrier(0x008, NMF - (NMF / NRD) * NRD, 0);                                \
+    vmwait<2 * NA + NB>(); /* B(kt + 2) landed */                                                           \
+    W8_STORE_B(cur, kt + 2);                                                                                \
+    _Pragma("unroll") for (int i = 0; i < FM; ++i) fa[nxt][1][i] = rdA(st1, i, 2 + fh);                     \
+    _Pragma("unroll") for (int j = 0; j < FN; ++j) fb[nxt][1][j] = rdB(st1, j, 2 + fh);                     \
+    _Pragma("unroll") for (int i = 0; i < FM; ++i)                                                          \
+      _Pragma("unroll") for (int j = 0; j < FN; ++j)                                                        \
+        acc[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(fa[cur][1][i], fb[cur][1][j], acc[i][j], 0, 0, 0);   \
+    _Pragma("unroll") for (int q = 0; q < NB; ++q) {                                                        \
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);                                                    \
+      __builtin_amdgcn_sched_group_barrier(0x200, 1, 0);                                                    \
+    }                                                                                                       \
+    _Pragma("unroll") for (int q = 0; q < NRD; ++q) {                                                       \
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);                                                    \
+      __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);                                                    \
+    }                                                                                                       \
+    __builtin_amdgcn_sched_group_barrier(0x008, NMF - NB - NRD > 0 ? NMF - NB - NRD : 0, 0);                \
+    lgkm0();                                                                                                \
+    __builtin_amdgcn_s_barrier(); /* k-step kt + 2 visible */                                               \
+  } while (0)
+  // register sets alternate: B(kt + 2) sits in set kt & 1, B(kt + 3) goes to the other
+  int kt = 0;
+  for (; kt + 1 < nk; kt += 2) {
+    W8_KSTEP(0, 1);
+    ++kt;
+    W8_KSTEP(1, 0);
+    --kt;
+  }
+  if (kt < nk) W8_KSTEP(0, 1);
+#undef W8_KSTEP
+#undef W8_LOAD_A
+#undef W8_LOAD_B
+#undef W8_STORE_B
+  vmwait<0>();
+  // The last k-steps' B loads (clamped, never stored) are dead to the
+  // compiler right after their asm: without this pin it may hand their
+  // registers to epilogue address arithmetic that the in-flight data would
+  // then overwrite.
+#pragma unroll
+  for (int s = 0; s < 2; ++s)
+#pragma unroll
+    for (int i = 0; i < NB; ++i) pin(rb[s][i]);
+  __builtin_amdgcn_s_barrier();  // every direct load landed before the strips reuse LDS
+
+  uint32_t* strip = reinterpret_cast<uint32_t*>(wave < 2 ? ldsA : ldsB) + (wave & 1) * (WM * EST);
+  epilogue<0, WM>(g, strip, acc, m0 + wm * WM, n0 + wn * WN, nullptr);
+}
+
+// ---- W4A16 / W4A8 ---------------------------------------------------------------
+// BM x 256 tile, K step one 64-byte A row (32 f16 for W4A16, 64 int8 for
+// W4A8). A: S-stage LDS ring of direct loads (k-step j + S goes into the
+// stage k-step j used). B: each lane's half-units for its FN tiles, loaded
+// three k-steps ahead into a 4-deep register ring, converted to fragments
+// one k-step ahead.
+//   W4A16, slice s (16 k), lane half h: B = dequant(word 2h + s of the unit
+//     of block kt) = k 16h + 8s .. + 8; A = chunk 2h + s of the row.
+//   W4A8, slice s (32 k = block 2kt + s), half h: B = requant(words 2h,
+//     2h + 1 of that block's unit) = k 32s + 16h .. + 16; A = chunk 2s + h.
+template <int OP, int BM>
+__global__ void __launch_bounds__(256) w4_kernel(const GemmArgs g, int split) {
+  constexpr bool F16 = (OP == OP_W4A16);
+  constexpr int BN = 256, WM = BM / 2, WN = 128, FM = WM / 32, FN = 4;
+  constexpr int S = BM == 128 ? 8 : 6;        // A ring stages
+  constexpr int NA = BM / 64;                 // A direct loads per thread per k-step
+  constexpr int NBLK = F16 ? 1 : 2;           // int4 blocks per k-step
+  constexpr int NBR = 2 * NBLK * FN;          // B loads per thread per k-step (half-unit + scale per block per tile)
+  constexpr int AST = BM * 64;
+  constexpr int EPI = 4 * WM * EST * 4;
+  constexpr int LA = S * AST > EPI ? S * AST : EPI;
+  static_assert(S >= 5, "the wait counts assume A(j + 2) is issued before B(j + 1)");
+  __shared__ __attribute__((aligned(16))) uint8_t ldsA[LA];
+  typedef typename std::conditional<F16, v16f, v16i>::type acc_t;
+
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int wm = wave >> 1, wn = wave & 1;
+  const int M = g.M, N = g.N, K = g.K;
+  int tm, tn;
+  tile_of(blockIdx.x, gridDim.x, (M + BM - 1) / BM, tm, tn);
+  const int m0 = tm * BM, n0 = tn * BN;
+  const int nblk = K / BLK;
+  const int nk_all = F16 ? nblk : nblk / 2;
+  const int kz = blockIdx.y;
+  const int k_lo = (int)((long)kz * nk_all / split), nk = (int)((long)(kz + 1) * nk_all / split) - k_lo;
+  const long a_row_bytes = F16 ? 2L * K : (long)K;
+
+  const uint8_t* asrc[NA];
+#pragma unroll
+  for (int i = 0; i < NA; ++i) {
+    const int r = (wave * NA + i) * 16 + (lane >> 2);
+    asrc[i] = reinterpret_cast<const uint8_t*>(g.A) + (long)min(m0 + r, M - 1) * a_row_bytes + (long)k_lo * 64 +
+              (((lane & 3) ^ swz(r)) << 4);
+  }
+  // B: tile j covers rows n0 + wn * 128 + 32 j + lane % 32; lane half h = lane / 32
+  const int h = lane >> 5;
+  const uint8_t* Bu = reinterpret_cast<const uint8_t*>(g.B);
+  long bidx[FN];  // panel index of (row, block k_lo * NBLK)
+#pragma unroll
+  for (int j = 0; j < FN; ++j) bidx[j] = panel_index(min(n0 + wn * WN + 32 * j + (lane & 31), N - 1), k_lo * NBLK, nblk);
+
+  v2u ru[4][FN][NBLK];
+  uint32_t rs[4][FN][NBLK];
+#define W4_LOAD_B(set_, kt_)                                                                         \
+  do {                                                                                               \
+    const long bo_ = (long)min((kt_), nk - 1) * NBLK * PANEL;                                        \
+    _Pragma("unroll") for (int j = 0; j < FN; ++j)                                                   \
+      _Pragma("unroll") for (int b = 0; b < NBLK; ++b) {                                             \
+        const long ix_ = bidx[j] + bo_ + b * PANEL;                                                  \
+        ru[set_][j][b] = ld8(Bu + ix_ * 16 + 8 * h);                                                 \
+        rs[set_][j][b] = ld2(g.bsc + ix_);                                                           \
+      }                                                                                              \
+  } while (0)
+#define W4_LOAD_A(kt_)                                                                               \
+  do {                                                                                               \
+    const long ko_ = (long)min((kt_), nk - 1) * 64;                                                  \
+    uint8_t* st_ = ldsA + ((kt_) % S) * AST;                                                         \
+    _Pragma("unroll") for (int i = 0; i < NA; ++i) dma16(asrc[i] + ko_, st_ + (wave * NA + i) * 1024); \
   } while (0)
 
   acc_t acc[FM][FN];
@@ -244,153 +511,146 @@ __global__ void __launch_bounds__(256) gemm_kernel(const GemmArgs g) {
 #pragma unroll
     for (int j = 0; j < FN; ++j) acc[i][j] = acc_t{};
 
-#pragma unroll
-  for (int d = 0; d < D; ++d) Q4_LOAD_REGS(d, d);
-  Q4_STORE_LDS(0, 0);
-  __syncthreads();
+  const int frow = lane & 31;
+  auto rdA = [&](int stage, int i, int s) {
+    const int c = F16 ? 2 * h + s : 2 * s + h;
+    return *reinterpret_cast<const v4i*>(ldsA + stage * AST + lds_off(wm * WM + 32 * i + frow, c));
+  };
+  v4i fa[2][2][FM], fb[2][2][FN];  // [buffer][k-slice][tile]
+#define W4_MAKE_B(buf_, set_)                                                                        \
+  do {                                                                                               \
+    _Pragma("unroll") for (int j = 0; j < FN; ++j) {                                                 \
+      pin(ru[set_][j][0]);                                                                           \
+      pin(rs[set_][j][0]);                                                                           \
+      if constexpr (F16) {                                                                           \
+        const _Float16 s_ = __builtin_bit_cast(_Float16, (uint16_t)rs[set_][j][0]);                   \
+        const v2h sv_ = {s_, s_};                                                                    \
+        fb[buf_][0][j] = __builtin_bit_cast(v4i, dequant_word_f16(ru[set_][j][0].x, sv_));           \
+        fb[buf_][1][j] = __builtin_bit_cast(v4i, dequant_word_f16(ru[set_][j][0].y, sv_));           \
+      } else {                                                                                       \
+        pin(ru[set_][j][NBLK - 1]);                                                                  \
+        pin(rs[set_][j][NBLK - 1]);                                                                  \
+        _Pragma("unroll") for (int b = 0; b < NBLK; ++b) fb[buf_][b][j] = __builtin_bit_cast(v4i,   \
+            requant_words_i8(ru[set_][j][b].x, ru[set_][j][b].y, h2f((uint16_t)rs[set_][j][b])));      \
+      }                                                                                              \
+    }                                                                                                \
+  } while (0)
 
-  // MFMA operand: row lane % 32 of a 32-row tile, 16 bytes at byte 16 * (lane / 32) of the 32-byte k-slice
-  const int frow = lane & 31, fhalf = lane >> 5;
-  {
-    // Explicit software pipeline per k-step, D rotating register buffers:
-    // global loads of k-step kt + D first, both k-slices' fragments read from
-    // LDS, then MFMAs of slice 0 interleaved with the slice-1 fragment reads
-    // and MFMAs of slice 1 interleaved with the LDS stores of k-step kt + 1
-    // (loaded D - 1 k-steps ago, into the other stage), one barrier. The
-    // sched_group_barrier sequence pins that order so the MFMA pipe is fed
-    // while LDS and memory requests are in flight.
-#define Q4_KSTEP(dl_, ds_)                                                                               \
-    do {                                                                                                \
-      Q4_LOAD_REGS(dl_, kt + D);                                                                        \
-      const uint8_t* base = lds + (kt & 1) * STAGE;                                                     \
-      v4i fa0[FM], fb0[FN], fa1[FM], fb1[FN];                                                           \
-      _Pragma("unroll") for (int i = 0; i < FM; ++i)                                                    \
-          fa0[i] = *reinterpret_cast<const v4i*>(base + lds_off(wm * WM + 32 * i + frow, fhalf));       \
-      _Pragma("unroll") for (int j = 0; j < FN; ++j)                                                    \
-          fb0[j] = *reinterpret_cast<const v4i*>(base + lds_off(BM + wn * WN + 32 * j + frow, fhalf));  \
-      _Pragma("unroll") for (int i = 0; i < FM; ++i)                                                    \
-          fa1[i] = *reinterpret_cast<const v4i*>(base + lds_off(wm * WM + 32 * i + frow, 2 + fhalf));   \
-      _Pragma("unroll") for (int j = 0; j < FN; ++j)                                                    \
-          fb1[j] = *reinterpret_cast<const v4i*>(base + lds_off(BM + wn * WN + 32 * j + frow, 2 + fhalf)); \
-      _Pragma("unroll") for (int i = 0; i < FM; ++i)                                                    \
-        _Pragma("unroll") for (int j = 0; j < FN; ++j) acc[i][j] = q4_mfma<F16>(fa0[i], fb0[j], acc[i][j]); \
-      _Pragma("unroll") for (int i = 0; i < FM; ++i)                                                    \
-        _Pragma("unroll") for (int j = 0; j < FN; ++j) acc[i][j] = q4_mfma<F16>(fa1[i], fb1[j], acc[i][j]); \
-      Q4_STORE_LDS(ds_, (kt + 1) & 1); /* past the last k-step: clamped data nobody reads */            \
-      Q4_SCHED();                                                                                       \
-      __syncthreads();                                                                                  \
-    } while (0)
-#if !defined(Q4MI_GEMM_SGB) || Q4MI_GEMM_SGB
-    constexpr int NMF = FM * FN;                                          // MFMAs per k-slice
-    constexpr int NRD = FM + FN;                                          // fragment reads per k-slice
-    constexpr int NVM = (OP == OP_W8A8) ? A_CH + B_CH : A_CH + 2 * B_CH;  // global loads per k-step
-    constexpr int NWR = (OP == OP_W8A8) ? A_CH + B_CH : (OP == OP_W4A16 ? A_CH + 4 * B_CH : A_CH + 2 * B_CH);
-#define Q4_SCHED()                                                                                      \
-    do {                                                                                                \
-      __builtin_amdgcn_sched_group_barrier(0x020, NVM, 0);                                              \
-      __builtin_amdgcn_sched_group_barrier(0x100, NRD, 0);                                              \
-      _Pragma("unroll") for (int q = 0; q < NRD; ++q) {                                                 \
-        __builtin_amdgcn_sched_group_barrier(0x008, NMF / NRD > 0 ? NMF / NRD : 1, 0);                  \
-        __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);                                              \
-      }                                                                                                 \
-      __builtin_amdgcn_sched_group_barrier(0x008, NMF - (NMF / NRD) * NRD, 0);                          \
-      _Pragma("unroll") for (int q = 0; q < NWR; ++q) {                                                 \
-        __builtin_amdgcn_sched_group_barrier(0x008, NMF / NWR > 0 ? NMF / NWR : 1, 0);                  \
-        __builtin_amdgcn_sched_group_barrier(0x200, 1, 0);                                              \
-      }                                                                                                 \
-    } while (0)
-#else
-#define Q4_SCHED() do {} while (0)
-#endif
-    for (int kt0 = 0; kt0 < nk; kt0 += D) {
-      { const int kt = kt0;     Q4_KSTEP(0, 1 % D); }
-      if constexpr (D > 1) { const int kt = kt0 + 1; Q4_KSTEP(1 % D, 2 % D); }
-      if constexpr (D > 2) { const int kt = kt0 + 2; Q4_KSTEP(2 % D, 3 % D); }
-      if constexpr (D > 3) { const int kt = kt0 + 3; Q4_KSTEP(3 % D, 4 % D); }
-    }
-#undef Q4_KSTEP
-#undef Q4_SCHED
+  // prologue in the steady-state issue order: A0 .. A(S-4), [B0 A(S-3)], [B1 A(S-2)], [B2 A(S-1)]
+#pragma unroll
+  for (int s = 0; s < S - 3; ++s) W4_LOAD_A(s);
+  W4_LOAD_B(0, 0);
+  W4_LOAD_A(S - 3);
+  W4_LOAD_B(1, 1);
+  W4_LOAD_A(S - 2);
+  W4_LOAD_B(2, 2);
+  W4_LOAD_A(S - 1);
+  vmwait<3 * NA + 2 * NBR>();  // B0 and A0 .. A(S-4) landed
+  W4_MAKE_B(0, 0);
+  __builtin_amdgcn_s_barrier();  // stages 0 and 1 visible
+#pragma unroll
+  for (int sl = 0; sl < 2; ++sl)
+#pragma unroll
+    for (int i = 0; i < FM; ++i) fa[0][sl][i] = rdA(0, i, sl);
+  lgkm0();
+  __builtin_amdgcn_s_barrier();  // stage 0 read by every wave: the first k-step may refill it
+
+  constexpr int NMF = 2 * FM * FN;
+#define W4_KSTEP(cur, nxt, bset_load, bset_make)                                                     \
+  do {                                                                                               \
+    W4_LOAD_B(bset_load, kt + 3);                                                                    \
+    W4_LOAD_A(kt + S);                                                                               \
+    vmwait<3 * NA + 2 * NBR>(); /* B(kt + 1) landed, and A(kt + 2) before it */                      \
+    const int st1 = (kt + 1) % S;                                                                    \
+    _Pragma("unroll") for (int sl = 0; sl < 2; ++sl)                                                 \
+      _Pragma("unroll") for (int i = 0; i < FM; ++i) fa[nxt][sl][i] = rdA(st1, i, sl);               \
+    W4_MAKE_B(nxt, bset_make);                                                                       \
+    _Pragma("unroll") for (int sl = 0; sl < 2; ++sl)                                                 \
+      _Pragma("unroll") for (int i = 0; i < FM; ++i)                                                 \
+        _Pragma("unroll") for (int j = 0; j < FN; ++j) {                                             \
+          if constexpr (F16)                                                                         \
+            acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(v8h, fa[cur][sl][i]), \
+                          __builtin_bit_cast(v8h, fb[cur][sl][j]), acc[i][j], 0, 0, 0);              \
+          else                                                                                       \
+            acc[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(fa[cur][sl][i], fb[cur][sl][j], acc[i][j], 0, 0, 0); \
+        }                                                                                            \
+    if constexpr (F16) { /* W4A8 (not a throughput path) is left to the default scheduler */       \
+      __builtin_amdgcn_sched_group_barrier(0x100, 2 * FM, 0);                                        \
+      _Pragma("unroll") for (int q = 0; q < NMF; ++q) {                                              \
+        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);                                           \
+        __builtin_amdgcn_sched_group_barrier(0x002, 7, 0);                                           \
+      }                                                                                              \
+    }                                                                                                \
+    lgkm0();                                                                                         \
+    __builtin_amdgcn_s_barrier(); /* k-step kt + 2 visible; stage kt free */                         \
+  } while (0)
+  // register ring: B(kt) in set kt % 4; fragment buffers alternate with kt % 2
+  int kt = 0;
+  for (; kt + 3 < nk; kt += 4) {
+    W4_KSTEP(0, 1, 3, 1);
+    ++kt;
+    W4_KSTEP(1, 0, 0, 2);
+    ++kt;
+    W4_KSTEP(0, 1, 1, 3);
+    ++kt;
+    W4_KSTEP(1, 0, 2, 0);
+    kt -= 3;
   }
-
-  // ---- epilogue through LDS (free after the loop's last barrier). Register
-  //      v of lane holds D[8 (v / 4) + 4 (lane / 32) + v % 4][lane % 32].
-  //      Each wave copies one 32-column strip of its tile into its own LDS
-  //      region with straight-line code (no branches next to the
-  //      accumulator reads), then reads it back 4 columns per lane for
-  //      bounds-checked, row-contiguous stores. ----
-  uint32_t* strip = reinterpret_cast<uint32_t*>(lds) + wave * (WM * EST);
-  const int col = lane & 31, rh = (lane >> 5) * 4;
-  const int mw = m0 + wm * WM, nw = n0 + wn * WN;
-  const int rrow = lane >> 3, rcol = (lane & 7) * 4;
-  constexpr int NIT = WM / 8;  // strip rows handled per lane: 8 it + lane / 8
-  // every per-row / per-column scale this lane needs, loaded up front (the
-  // loads are independent; issuing them inside the store loop would put one
-  // L2 round trip per row on the critical path)
-  float sav[F16 ? 1 : NIT];
-  float swv[F16 ? 1 : FN][4];
-  if constexpr (!F16) {
+  if (kt < nk) {
+    W4_KSTEP(0, 1, 3, 1);
+    ++kt;
+    if (kt < nk) {
+      W4_KSTEP(1, 0, 0, 2);
+      ++kt;
+      if (kt < nk) W4_KSTEP(0, 1, 1, 3);
+    }
+  }
+#undef W4_KSTEP
+#undef W4_LOAD_A
+#undef W4_LOAD_B
+#undef W4_MAKE_B
+  vmwait<0>();
+  // keep the last k-steps' (unused) B registers live until their loads landed:
+  // otherwise the compiler may reuse them for epilogue addresses
 #pragma unroll
-    for (int it = 0; it < NIT; ++it) sav[it] = g.sa ? g.sa[min(mw + 8 * it + rrow, M - 1)] : 0.0f;
+  for (int s = 0; s < 4; ++s)
 #pragma unroll
     for (int j = 0; j < FN; ++j)
 #pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        const int ne = min(nw + 32 * j + rcol + e, N - 1);
-        swv[j][e] = g.sw_f16 ? h2f(reinterpret_cast<const uint16_t*>(g.sw)[ne])
-                             : (g.sw ? reinterpret_cast<const float*>(g.sw)[ne] : 0.0f);
+      for (int b = 0; b < NBLK; ++b) {
+        pin(ru[s][j][b]);
+        pin(rs[s][j][b]);
       }
-  }
-#pragma unroll
-  for (int j = 0; j < FN; ++j) {
-#pragma unroll
-    for (int i = 0; i < FM; ++i) store_tile_strip(strip + (32 * i + rh) * EST + col, EST, acc[i][j]);
-    __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0): this wave's strip is in LDS
-    __builtin_amdgcn_wave_barrier();
-    const int n = nw + 32 * j + rcol;
-#pragma unroll
-    for (int it = 0; it < NIT; ++it) {
-      const int row = 8 * it + rrow;
-      const int m = mw + row;
-      const uint4 q = *reinterpret_cast<const uint4*>(strip + row * EST + rcol);
-      const uint32_t qv[4] = {q.x, q.y, q.z, q.w};
-      if (m < M) {
-        const long o = (long)m * N + n;
-        const bool vec = n + 3 < N && (o & 3) == 0;
-        if constexpr (F16) {
-          uint16_t h[4];
-#pragma unroll
-          for (int e = 0; e < 4; ++e) h[e] = f2h(__builtin_bit_cast(float, qv[e]));
-          if (vec) {
-            *reinterpret_cast<ushort4*>(g.Y + o) = make_ushort4(h[0], h[1], h[2], h[3]);
-          } else {
-            for (int e = 0; e < 4; ++e)
-              if (n + e < N) g.Y[o + e] = h[e];
-          }
-        } else {
-          if (g.C) {
-            if (vec) *reinterpret_cast<uint4*>(g.C + o) = q;
-            else
-              for (int e = 0; e < 4; ++e)
-                if (n + e < N) g.C[o + e] = (int32_t)qv[e];
-          }
-          if (g.Y) {
-            uint16_t h[4];
-#pragma unroll
-            for (int e = 0; e < 4; ++e)
-              h[e] = f2h_after_f32(__fmul_rn(__fmul_rn((float)(int)qv[e], sav[it]), swv[j][e]));
-            if (vec) *reinterpret_cast<ushort4*>(g.Y + o) = make_ushort4(h[0], h[1], h[2], h[3]);
-            else
-              for (int e = 0; e < 4; ++e)
-                if (n + e < N) g.Y[o + e] = h[e];
-          }
-        }
-      }
-    }
-    __builtin_amdgcn_wave_barrier();  // strip reads done before the next strip overwrites it
+  __builtin_amdgcn_s_barrier();  // every direct load landed before the strips reuse LDS
+
+  uint32_t* strip = reinterpret_cast<uint32_t*>(ldsA) + wave * (WM * EST);
+  if constexpr (F16) {
+    if (split > 1)
+      epilogue<2, WM>(g, strip, acc, m0 + wm * WM, n0 + wn * WN, g.P + (long)kz * M * N);
+    else
+      epilogue<1, WM>(g, strip, acc, m0 + wm * WM, n0 + wn * WN, nullptr);
+  } else {
+    epilogue<0, WM>(g, strip, acc, m0 + wm * WM, n0 + wn * WN, nullptr);
   }
 }
-#undef Q4_LOAD_REGS
-#undef Q4_STORE_LDS
+
+// Y[i] = f16(sum over splits of P[s][i]) in split order (4 elements per thread).
+__global__ void __launch_bounds__(256) splitk_reduce_kernel(const float* __restrict__ P, uint16_t* __restrict__ Y,
+                                                            long n, int split) {
+  const long i = ((long)blockIdx.x * 256 + threadIdx.x) * 4;
+  if (i >= n) return;
+  if (i + 3 < n) {
+    v4f t = *reinterpret_cast<const v4f*>(P + i);
+    for (int s = 1; s < split; ++s) t += *reinterpret_cast<const v4f*>(P + (long)s * n + i);
+    *reinterpret_cast<ushort4*>(Y + i) = make_ushort4(f2h(t.x), f2h(t.y), f2h(t.z), f2h(t.w));
+  } else {
+    for (long e = i; e < n; ++e) {
+      float t = P[e];
+      for (int s = 1; s < split; ++s) t += P[(long)s * n + e];
+      Y[e] = f2h(t);
+    }
+  }
+}
 
 // ---- per-row int8 activation quantizer (vk/cast_i8.comp) -----------------
 template <int XT>
@@ -400,8 +660,8 @@ __global__ void __launch_bounds__(256) quant_act_kernel(const void* __restrict__
   const int m = blockIdx.x, tid = threadIdx.x;
   auto ld4 = [&](int i, float v[4]) {  // elements 4i..4i+3 of row m
     if constexpr (XT == Q4_DT_F16) {
-      ushort4 h = reinterpret_cast<const ushort4*>(reinterpret_cast<const uint16_t*>(X) + (long)m * K)[i];
-      v[0] = h2f(h.x); v[1] = h2f(h.y); v[2] = h2f(h.z); v[3] = h2f(h.w);
+      ushort4 hh = reinterpret_cast<const ushort4*>(reinterpret_cast<const uint16_t*>(X) + (long)m * K)[i];
+      v[0] = h2f(hh.x); v[1] = h2f(hh.y); v[2] = h2f(hh.z); v[3] = h2f(hh.w);
     } else {
       float4 f = reinterpret_cast<const float4*>(reinterpret_cast<const float*>(X) + (long)m * K)[i];
       v[0] = f.x; v[1] = f.y; v[2] = f.z; v[3] = f.w;
@@ -435,33 +695,24 @@ __global__ void __launch_bounds__(256) quant_act_kernel(const void* __restrict__
   }
 }
 
-template <int OP, int BM, int BN>
-static int launch_tiles(const GemmArgs& g, void* stream, const char* name) {
-  const int ntm = ceil_div(g.M, BM), ntn = ceil_div(g.N, BN);
-  const int nk = OP == OP_W4A16 ? g.K / 32 : g.K / 64;
-#ifndef Q4MI_GEMM_DEEP
-#define Q4MI_GEMM_DEEP 2
-#endif
-#ifndef Q4MI_GEMM_DEEP_SMALL
-#define Q4MI_GEMM_DEEP_SMALL 4
-#endif
-  constexpr int DEEP = BM >= 256 ? Q4MI_GEMM_DEEP : Q4MI_GEMM_DEEP_SMALL;
-  if (nk % DEEP == 0)
-    hipLaunchKernelGGL((gemm_kernel<OP, BM, BN, DEEP>), dim3(ntm * ntn), dim3(256), 0, as_stream(stream), g);
-  else
-    hipLaunchKernelGGL((gemm_kernel<OP, BM, BN, 1>), dim3(ntm * ntn), dim3(256), 0, as_stream(stream), g);
-  Q4_LAUNCHED(name);
-  return Q4_OK;
+// ---- host-side launch policy ----------------------------------------------------
+// 256 x 256 tiles when they give >= 256 workgroups (one per CU), else
+// 128 x 256. W4A16 splits K (>= 32 k-steps per split) until the grid has
+// >= 240 workgroups, when a workspace for the partials is available.
+static int tiles(int M, int N, int BM) { return ceil_div(M, BM) * ceil_div(N, 256); }
+static int pick_bm(int M, int N) { return tiles(M, N, 256) >= 256 ? 256 : 128; }
+
+static int w4a16_split(int M, int N, int K) {
+  const int t = tiles(M, N, pick_bm(M, N));
+  const int nk = K / 32;
+  int s = 1;
+  while (t * s < 240 && nk / (s + 1) >= 32) ++s;
+  return s;
 }
 
-// 128 x 256 tiles: with a 4-deep register prefetch they fit the register
-// file without spills (256 x 256 tiles spill at any prefetch depth > 1).
-template <int OP>
-static int launch_gemm(const GemmArgs& g, void* stream, const char* name) {
-#if !defined(Q4MI_GEMM_BIG) || Q4MI_GEMM_BIG
-  if ((long)ceil_div(g.M, 256) * ceil_div(g.N, 256) >= 256) return launch_tiles<OP, 256, 256>(g, stream, name);
-#endif
-  return launch_tiles<OP, 128, 256>(g, stream, name);
+template <int OP, int BM>
+static void launch_w4(const GemmArgs& g, int split, hipStream_t st) {
+  hipLaunchKernelGGL((w4_kernel<OP, BM>), dim3(tiles(g.M, g.N, BM), split), dim3(256), 0, st, g, split);
 }
 
 }  // namespace q4
@@ -494,8 +745,13 @@ int q4_gemm_w8a8(const int8_t* A, const int8_t* W8, const float* sa, const void*
   Q4_ARG(!Y || (sa && sw), "Y needs sa and sw");
   Q4_ARG(sw_dtype == Q4_DT_F32 || sw_dtype == Q4_DT_F16, "bad sw dtype %d", sw_dtype);
   Q4_ARG(((uintptr_t)A & 15) == 0 && ((uintptr_t)W8 & 15) == 0, "A and W8 must be 16-byte aligned");
-  GemmArgs g{A, W8, nullptr, sa, sw, sw_dtype == Q4_DT_F16, Y, C, M, N, K};
-  return launch_gemm<OP_W8A8>(g, stream, "gemm_w8a8");
+  GemmArgs g{A, W8, nullptr, sa, sw, sw_dtype == Q4_DT_F16, Y, C, nullptr, M, N, K};
+  if (pick_bm(M, N) == 256)
+    hipLaunchKernelGGL(w8a8_kernel<256>, dim3(tiles(M, N, 256)), dim3(256), 0, as_stream(stream), g);
+  else
+    hipLaunchKernelGGL(w8a8_kernel<128>, dim3(tiles(M, N, 128)), dim3(256), 0, as_stream(stream), g);
+  Q4_LAUNCHED("gemm_w8a8");
+  return Q4_OK;
 }
 
 int q4_gemm_w4a8(const int8_t* A, const uint32_t* wq, const uint16_t* ratio, const float* sa, const void* sw,
@@ -508,19 +764,50 @@ int q4_gemm_w4a8(const int8_t* A, const uint32_t* wq, const uint16_t* ratio, con
   Q4_ARG(!Y || (sa && sw), "Y needs sa and sw");
   Q4_ARG(sw_dtype == Q4_DT_F32 || sw_dtype == Q4_DT_F16, "bad sw dtype %d", sw_dtype);
   Q4_ARG(((uintptr_t)A & 15) == 0 && ((uintptr_t)wq & 15) == 0, "A and wq must be 16-byte aligned");
-  GemmArgs g{A, wq, ratio, sa, sw, sw_dtype == Q4_DT_F16, Y, C, M, N, K};
-  return launch_gemm<OP_W4A8>(g, stream, "gemm_w4a8");
+  GemmArgs g{A, wq, ratio, sa, sw, sw_dtype == Q4_DT_F16, Y, C, nullptr, M, N, K};
+  // 128-row tiles only: with 256 rows the requant register ring does not fit
+  // without spills, and a spill of a register whose load is still in flight
+  // would store it before the data arrives
+  launch_w4<OP_W4A8, 128>(g, 1, as_stream(stream));
+  Q4_LAUNCHED("gemm_w4a8");
+  return Q4_OK;
 }
 
-int q4_gemm_w4a16(const uint16_t* X, const uint32_t* wq, const uint16_t* sc16, uint16_t* Y, int M, int N, int K,
-                  void* stream) {
+size_t q4_gemm_workspace_bytes(int op, int M, int N, int K) {
+  if (op != Q4_OP_W4A16 || M <= 0 || N <= 0 || K <= 0 || K % 32) return 0;
+  const int s = w4a16_split(M, N, K);
+  return s > 1 ? (size_t)s * M * N * sizeof(float) : 0;
+}
+
+int q4_gemm_w4a16_ws(const uint16_t* X, const uint32_t* wq, const uint16_t* sc16, uint16_t* Y, int M, int N, int K,
+                     void* ws, size_t ws_bytes, void* stream) {
   clear_error();
   Q4_ARG(M > 0 && N > 0 && K > 0 && K % 32 == 0, "bad W4A16 shape M=%d N=%d K=%d (K must be a multiple of 32)", M, N,
          K);
   Q4_ARG(X && wq && sc16 && Y, "null pointer");
   Q4_ARG(((uintptr_t)X & 15) == 0 && ((uintptr_t)wq & 15) == 0, "X and wq must be 16-byte aligned");
-  GemmArgs g{X, wq, sc16, nullptr, nullptr, 0, Y, nullptr, M, N, K};
-  return launch_gemm<OP_W4A16>(g, stream, "gemm_w4a16");
+  Q4_ARG(!ws || ((uintptr_t)ws & 15) == 0, "workspace must be 16-byte aligned");
+  int split = w4a16_split(M, N, K);
+  if (split > 1 && (!ws || ws_bytes < (size_t)split * M * N * sizeof(float))) split = 1;  // no room: one pass
+  GemmArgs g{X, wq, sc16, nullptr, nullptr, 0, Y, nullptr, split > 1 ? reinterpret_cast<float*>(ws) : nullptr,
+             M, N, K};
+  if (pick_bm(M, N) == 256)
+    launch_w4<OP_W4A16, 256>(g, split, as_stream(stream));
+  else
+    launch_w4<OP_W4A16, 128>(g, split, as_stream(stream));
+  Q4_LAUNCHED("gemm_w4a16");
+  if (split > 1) {
+    const long n = (long)M * N;
+    hipLaunchKernelGGL(splitk_reduce_kernel, dim3(ceil_div(n, 1024)), dim3(256), 0, as_stream(stream), g.P, Y, n,
+                       split);
+    Q4_LAUNCHED("gemm_w4a16 split-K reduce");
+  }
+  return Q4_OK;
+}
+
+int q4_gemm_w4a16(const uint16_t* X, const uint32_t* wq, const uint16_t* sc16, uint16_t* Y, int M, int N, int K,
+                  void* stream) {
+  return q4_gemm_w4a16_ws(X, wq, sc16, Y, M, N, K, nullptr, 0, stream);
 }
 
 }  // extern "C"

@@ -204,15 +204,35 @@ def gemv(x: torch.Tensor, wq: torch.Tensor, scales: torch.Tensor, N: int, K: int
 
 
 # ------------------------------------------------------------------ GEMMs
-def gemm_w4a16(X: torch.Tensor, wq: torch.Tensor, sc16: torch.Tensor, N: int, Y: torch.Tensor | None = None):
+def gemm_w4a16(X: torch.Tensor, wq: torch.Tensor, sc16: torch.Tensor, N: int, Y: torch.Tensor | None = None,
+               ws: torch.Tensor | None = None):
+    """Y f16 [M, N] = X f16 [M, K] @ f16((q-8) * s)^T (fp32 accumulate).
+
+    Tall-K shapes split K across workgroups into fp32 partials: pass ``ws``
+    (a device tensor of at least ``gemm_workspace_bytes(M, N, K)`` bytes) or
+    one is allocated here; capture code must pass its own."""
     if X.dtype != torch.float16 or X.dim() != 2:
         raise ValueError("X must be a 2-D float16 tensor")
     M, K = X.shape
     _check_int4(wq, sc16, N, K)
     Y = torch.empty((M, N), dtype=torch.float16, device=X.device) if Y is None else Y
     _need(Y, M * N * 2, "Y")
-    call("q4_gemm_w4a16", _p(X), _p(wq), _p(sc16), _p(Y), M, N, K, _stream())
+    need = gemm_workspace_bytes(M, N, K)
+    if need and ws is None:
+        if _CAPTURING[0]:
+            raise RuntimeError("a split-K W4A16 GEMM inside a graph capture needs a workspace allocated before "
+                               "the capture (pass ws=...)")
+        ws = torch.empty(need, dtype=torch.uint8, device=X.device)
+    if ws is not None:
+        _need(ws, need, "W4A16 split-K workspace")
+    call("q4_gemm_w4a16_ws", _p(X), _p(wq), _p(sc16), _p(Y), M, N, K, _p(ws), _nbytes(ws) if ws is not None else 0,
+         _stream())
     return Y
+
+
+def gemm_workspace_bytes(M: int, N: int, K: int) -> int:
+    """Workspace bytes of a W4A16 GEMM (0 when it runs without splitting K)."""
+    return int(lib().q4_gemm_workspace_bytes(_lib.OP_W4A16, M, N, K))
 
 
 def quant_act_i8(X: torch.Tensor, A: torch.Tensor | None = None, sa: torch.Tensor | None = None):

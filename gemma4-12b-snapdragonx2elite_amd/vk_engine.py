@@ -186,7 +186,9 @@ def gemm_ds(qw, inbuf: Buf, outbuf: Buf, prefill_i8: bool | None = None):
     else:
         x16 = _stage("Xf16", MC * max(N, K) * 2).view(torch.float16, MC * K).view(MC, K)
         cin = ("cast_dn", xin, x16)
-        gem = ("w4a16", x16, bw.t, bs16.t, N, y16)
+        need = ops.gemm_workspace_bytes(MC, N, K)   # split-K partials, allocated here so recording can capture
+        ws = _stage("W4ws", need).view(torch.uint8, need) if need else None
+        gem = ("w4a16", x16, bw.t, bs16.t, N, y16, ws)
     cout = ("cast_up", y16, yout)
     return (cin, gem, cout, N, K)
 
@@ -202,7 +204,7 @@ def _run(op):
     elif kind == "w8a8":
         ops.gemm_w8a8(op[1], op[2], op[3], op[4], Y=op[5])
     elif kind == "w4a16":
-        ops.gemm_w4a16(op[1], op[2], op[3], op[4], Y=op[5])
+        ops.gemm_w4a16(op[1], op[2], op[3], op[4], Y=op[5], ws=op[6])
     else:
         raise ValueError(kind)
 

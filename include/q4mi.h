@@ -49,8 +49,9 @@ extern "C" {
 #define Q4_SCALE_F16 0
 #define Q4_SCALE_E4M3 1
 
-/* op ids for q4_workspace_bytes */
+/* op ids for q4_workspace_bytes / q4_gemm_workspace_bytes */
 #define Q4_OP_GEMV 0
+#define Q4_OP_W4A16 1
 
 /* ---- library info / errors --------------------------------------------- */
 const char* q4_version(void);
@@ -136,6 +137,17 @@ int q4_gemv_e4m3s(const void* x, int x_dtype, const uint32_t* wq,
  * gemm_ds()/gmm() (src/vk_engine.py:351-365, 391-400). */
 int q4_gemm_w4a16(const uint16_t* X, const uint32_t* wq, const uint16_t* sc16,
                   uint16_t* Y, int M, int N, int K, void* stream);
+/* The same product with a caller-owned workspace: when the M x N tile grid
+ * is too small to fill the GPU (tall-K shapes such as the down projection,
+ * src/vk_engine.py:423), K is split across workgroups and fp32 partials
+ * [split][M][N] are summed in split order by a second kernel
+ * (deterministic). ws may be NULL or smaller than
+ * q4_gemm_workspace_bytes(Q4_OP_W4A16, M, N, K); the call then runs
+ * without splitting, exactly like q4_gemm_w4a16. */
+size_t q4_gemm_workspace_bytes(int op, int M, int N, int K);
+int q4_gemm_w4a16_ws(const uint16_t* X, const uint32_t* wq,
+                     const uint16_t* sc16, uint16_t* Y, int M, int N, int K,
+                     void* ws, size_t ws_bytes, void* stream);
 
 /* Per-row int8 activation quantizer: sa[m] = max(absmax/127, 1e-12),
  * A = clamp(rint(x / sa), -127, 127) (IEEE fp32 divide).

@@ -40,8 +40,8 @@ def _w8a8_case(rng, M, N, K):
     return A, sa, W8, sw
 
 
-@pytest.mark.parametrize("M,N,K", [(64, 256, 64), (100, 320, 128), (256, 512, 3840), (128, 15360, 3840),
-                                   (300, 3840, 15360)])
+@pytest.mark.parametrize("M,N,K", [(64, 256, 64), (100, 320, 128), (70, 300, 192), (256, 512, 3840),
+                                   (128, 15360, 3840), (300, 3840, 15360), (1024, 2048, 320)])
 @pytest.mark.parametrize("swdt", [np.float32, np.float16])
 def test_w8a8_bit_exact(gpu, M, N, K, swdt):
     rng = np.random.default_rng(M * 3 + N + K)
@@ -76,7 +76,7 @@ def test_w8a8_config_size_rows(gpu):
 
 
 # ------------------------------------------------------------------ W4A8
-@pytest.mark.parametrize("M,N,K", [(64, 256, 64), (100, 512, 3840), (128, 15360, 3840)])
+@pytest.mark.parametrize("M,N,K", [(64, 256, 64), (100, 512, 3840), (33, 300, 320), (128, 15360, 3840)])
 def test_w4a8_bit_exact(gpu, M, N, K):
     rng = np.random.default_rng(M + N + K + 1)
     W = (rng.standard_normal((N, K)) * 0.08).astype(np.float32)
@@ -97,8 +97,8 @@ def test_w4a8_bit_exact(gpu, M, N, K):
 
 
 # ----------------------------------------------------------------- W4A16
-@pytest.mark.parametrize("M,N,K", [(64, 256, 32), (100, 320, 96), (128, 3840, 15360), (512, 15360, 3840),
-                                   (512, 3840, 15360)])
+@pytest.mark.parametrize("M,N,K", [(64, 256, 32), (100, 320, 96), (40, 300, 224), (128, 3840, 15360),
+                                   (512, 15360, 3840), (512, 3840, 15360), (1024, 8192, 256), (2048, 8192, 96)])
 def test_w4a16(gpu, M, N, K):
     rng = np.random.default_rng(M + 2 * N + K)
     q, s = synth_int4(rng, N, K)
