@@ -76,10 +76,29 @@ def bench_decode(ops, steps: int, warmup: int):
     mats.append(("lm_head", V, H, w, s))
     ws = ops.Workspace(max(ops.Workspace.bytes_for(N, K) for _, N, K, _, _ in mats))
     torch.cuda.synchronize()
+    # q, k and v read the same normed activation: one batched launch per layer
+    # (the reference dispatches them back to back on one input buffer)
+    launches = []
+    i = 0
+    while i < len(mats):
+        if mats[i][0] == "q":
+            launches.append(("qkv", mats[i:i + 3]))
+            i += 3
+        else:
+            launches.append((mats[i][0], [mats[i]]))
+            i += 1
+
+    def launch(sel):
+        if len(sel) == 1:
+            _, N, K, w, s = sel[0]
+            ops.gemv(xs[K], w, s, N, K, y=ys[sel[0][0]], ws=ws)
+        else:
+            K = sel[0][2]
+            ops.gemv_batch(xs[K], [(w, s, N, ys[nm], None) for nm, N, _, w, s in sel], K)
 
     def token():
-        for name, N, K, w, s in mats:
-            ops.gemv(xs[K], w, s, N, K, y=ys[name], ws=ws)
+        for _, sel in launches:
+            launch(sel)
 
     graph = ops.Graph()
     with graph.capture():
@@ -98,15 +117,14 @@ def bench_decode(ops, steps: int, warmup: int):
     torch.cuda.synchronize()
     ms = t0.elapsed_time(t1) / steps
     nbytes = sum(gemv_bytes(N, K) for _, N, K, _, _ in mats)
-    launches = len(mats)
     # per-shape kernel time: one graph of the 48 same-shape launches per shape, same stream
     per_shape = {}
-    for name in [n for n, _, _ in LAYER_SHAPES] + ["lm_head"]:
-        sel = [m for m in mats if m[0] == name]
+    for name in ["qkv", "o", "gate_up", "down", "lm_head"]:
+        sel = [lz for nm, lz in launches if nm == name]
         g2 = ops.Graph(st)
         with g2.capture():
-            for _, N, K, w, s in sel:
-                ops.gemv(xs[K], w, s, N, K, y=ys[name], ws=ws)
+            for lz in sel:
+                launch(lz)
         reps = max(3, 480 // len(sel))
         for _ in range(2):
             g2.launch()
@@ -118,43 +136,56 @@ def bench_decode(ops, steps: int, warmup: int):
         b.record(st)
         b.synchronize()
         us = a.elapsed_time(b) * 1e3 / (reps * len(sel))
-        N, K = sel[0][1], sel[0][2]
-        per_shape[name] = {"N": N, "K": K, "us_per_launch": round(us, 3),
-                           "GBps": round(gemv_bytes(N, K) / us / 1e3, 1), "split": ops.auto_split(N, K)}
+        lb = sum(gemv_bytes(N, K) for _, N, K, _, _ in sel[0])
+        per_shape[name] = {"N": "+".join(str(m[1]) for m in sel[0]), "K": sel[0][0][2],
+                           "us_per_launch": round(us, 3), "GBps": round(lb / us / 1e3, 1),
+                           "bytes_per_launch": lb, "launches_per_token": len(sel)}
         g2.destroy()
     graph.destroy()
     del mats, ws
     torch.cuda.empty_cache()
-    return {"ms_per_step": ms, "bytes_per_step": nbytes, "launches": launches,
+    return {"ms_per_step": ms, "bytes_per_step": nbytes, "launches": len(launches),
             "GBps": nbytes / (ms * 1e-3) / 1e9, "per_shape": per_shape}
 
 
 def counter_workload(ops):
-    """The roofline kernel alone, for hardware-counter runs: 48 gate_up GEMVs
-    (30720x3840, distinct weights, as in one decode token) followed by one
-    512 MiB device copy whose FETCH_SIZE / WRITE_SIZE readings calibrate the
-    counters' units."""
+    """The decode-token GEMV launches, for hardware-counter runs: 16 launches
+    of each layer shape (qkv batched, o, gate_up, down; distinct weights) and
+    2 lm_head launches, then one 512 MiB device copy whose FETCH_SIZE /
+    WRITE_SIZE readings calibrate the counters' units."""
     import torch
 
     dev = torch.device("cuda:0")
     gen = torch.Generator(device=dev).manual_seed(0)
-    N, K = 2 * I, H
-    mats = []
-    for _ in range(LAYERS):
+
+    def make(N, K):
         w = torch.randint(-2 ** 31, 2 ** 31 - 1, (N * K // 8,), dtype=torch.int64, device=dev,
                           generator=gen).to(torch.int32)
         s = (torch.randn(N * K // 32, device=dev, generator=gen) * 0.02).abs().to(torch.float16)
-        mats.append((w, s))
-    x = torch.randn(K, device=dev, generator=gen).to(torch.float16)
-    y = torch.empty(N, dtype=torch.float16, device=dev)
+        return w, s
+
+    xs = {K: torch.randn(K, device=dev, generator=gen).to(torch.float16) for K in (H, QN, I)}
+    reps = 16
     src = torch.ones(512 * 2 ** 20 // 4, dtype=torch.float32, device=dev)
     dst = torch.empty_like(src)
-    torch.cuda.synchronize()
-    for w, s in mats:
-        ops.gemv(x, w, s, N, K, y=y)
+    for name, shapes in [("qkv", [(QN, H), (KVN, H), (KVN, H)]), ("o", [(H, QN)]), ("gate_up", [(2 * I, H)]),
+                         ("down", [(H, I)]), ("lm_head", [(V, H)])]:
+        n = 2 if name == "lm_head" else reps
+        mats = [[make(N, K) for N, K in shapes] for _ in range(n)]
+        K = shapes[0][1]
+        ys = [torch.empty(N, dtype=torch.float16, device=dev) for N, _ in shapes]
+        torch.cuda.synchronize()
+        for m in mats:
+            if len(shapes) == 1:
+                ops.gemv(xs[K], m[0][0], m[0][1], shapes[0][0], K, y=ys[0])
+            else:
+                ops.gemv_batch(xs[K], [(w, s, N, y, None) for (w, s), (N, _), y in zip(m, shapes, ys)], K)
+        torch.cuda.synchronize()
+        del mats
+        print(f"[bench] counter workload: {n} x {name}", flush=True)
     dst.copy_(src)
     torch.cuda.synchronize()
-    print(f"[bench] counter workload done: {LAYERS} x gemv {N}x{K}, copy {src.numel() * 4} B", flush=True)
+    print(f"[bench] counter workload done: copy {src.numel() * 4} B", flush=True)
 
 
 def bench_w8a8(ops, iters: int = 50):
@@ -221,6 +252,19 @@ def bench_w4a16(ops, iters: int = 30):
     return out
 
 
+def committed_traffic(shape: str):
+    """HBM bytes per launch of a decode GEMV shape from the committed
+    rocprofv3 FETCH_SIZE/WRITE_SIZE summary (calibrated by a copy of known
+    size), or None when the summary does not cover the current kernel."""
+    import re
+
+    f = ROOT / "profiles" / "gemv_decode_hbm_traffic.md"
+    if not f.exists():
+        return None
+    m = re.search(rf"^traffic {shape}: (\d+) B per launch$", f.read_text(), flags=re.M)
+    return int(m.group(1)) if m else None
+
+
 # --------------------------------------------------------- CPU baseline
 def cpu_baseline(budget_s: float = 15.0):
     """The oracle's numpy GEMV (dequant + matmul, the reference's formulation)
@@ -269,8 +313,8 @@ def main():
     ap.add_argument("--no-gemm", action="store_true", help="skip the prefill GEMM legs")
     ap.add_argument("--cpu-budget", type=float, default=15.0)
     ap.add_argument("--counters", action="store_true",
-                    help="run only the roofline kernel (48 gate_up GEMVs) and a 512 MiB calibration copy, "
-                         "for rocprofv3 --pmc passes; prints no JSON line")
+                    help="run only the decode GEMV launches (16 per layer shape, 2 lm_head) and a 512 MiB "
+                         "calibration copy, for rocprofv3 --pmc passes; prints no JSON line")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU: this path is a single-GPU kernel set (multi-GPU sharding is "
@@ -304,7 +348,7 @@ def main():
     # of the token; its average launch duration is measured above with HIP events over a graph of its 48
     # launches on the decode stream
     gu = dec["per_shape"]["gate_up"]
-    gu_bytes = gemv_bytes(gu["N"], gu["K"])
+    gu_bytes = gu["bytes_per_launch"]
     achieved = gu_bytes / (gu["us_per_launch"] * 1e-6) / 1e9
     line = {
         "metric": METRIC,
@@ -322,7 +366,8 @@ def main():
         "config": {
             "workload": "decode-step int4 GEMV set: 48 distinct layers {q 4096x3840, k 2048x3840, v 2048x3840, "
                         "o 3840x4096, gate_up 30720x3840, down 3840x15360} + lm_head 262144x3840, block-32 fp16 "
-                        "scales, fp16 x/y, one hipGraph replay per token",
+                        "scales, fp16 x/y, one hipGraph replay per token (q/k/v of a layer read one x: one "
+                        "batched launch)",
             "bytes_per_step": dec["bytes_per_step"],
             "kernels_per_step": dec["launches"],
             "frac_of_hbm_peak": round(dec["GBps"] / HBM_PEAK_GBS, 4),
@@ -335,7 +380,7 @@ def main():
             "peak": HBM_PEAK_GBS,
             "unit": "GB/s",
             "frac": round(achieved / HBM_PEAK_GBS, 4),
-            "traffic": None,
+            "traffic": committed_traffic("gate_up"),
             "bytes_per_launch": gu_bytes,
             "avg_launch_us": gu["us_per_launch"],
         },

@@ -17,6 +17,7 @@ DT_F32, DT_F16 = 0, 1
 SCALE_F16, SCALE_E4M3 = 0, 1
 OP_GEMV = 0
 OP_W4A16 = 1
+GEMV_MAX_BATCH = 8
 
 _vp, _i, _f, _sz = C.c_void_p, C.c_int, C.c_float, C.c_size_t
 
@@ -38,6 +39,7 @@ SIGNATURES = {
     "q4_gemv": (_i, [_vp, _i, _vp, _vp, _i, _f, _vp, _i, _i, _i, _i, _vp, _sz, _vp]),
     "q4_gemv_f16s": (_i, [_vp, _i, _vp, _vp, _vp, _i, _i, _i, _i, _vp, _sz, _vp]),
     "q4_gemv_e4m3s": (_i, [_vp, _i, _vp, _vp, _f, _vp, _i, _i, _i, _i, _vp, _sz, _vp]),
+    "q4_gemv_batch": (_i, [_vp, _i, _i, _i, _i, _i, _vp, _vp, _vp, _vp, _vp, _vp]),
     "q4_gemm_w4a16": (_i, [_vp, _vp, _vp, _vp, _i, _i, _i, _vp]),
     "q4_gemm_workspace_bytes": (_sz, [_i, _i, _i, _i]),
     "q4_gemm_w4a16_ws": (_i, [_vp, _vp, _vp, _vp, _i, _i, _i, _vp, _sz, _vp]),

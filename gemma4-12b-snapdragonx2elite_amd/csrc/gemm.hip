@@ -47,7 +47,6 @@ namespace q4 {
 
 enum { OP_W8A8 = 0, OP_W4A16 = 1, OP_W4A8 = 2 };
 
-typedef unsigned v2u __attribute__((ext_vector_type(2)));
 typedef int v16i __attribute__((ext_vector_type(16)));
 typedef float v16f __attribute__((ext_vector_type(16)));
 
@@ -63,39 +62,6 @@ struct GemmArgs {
   float* P;             // W4A16 split-K: fp32 partials [split][M][N]
   int M, N, K;
 };
-
-// ---- inline-asm memory operations ------------------------------------------
-// 16 bytes per lane from global memory into LDS at lds_dst + 16 * lane
-// (lds_dst wave-uniform).
-__device__ inline void dma16(const void* gptr, const void* lds_dst) {
-  const unsigned l = __builtin_amdgcn_readfirstlane((unsigned)(uintptr_t)lds_dst);
-  asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(gptr), "s"(l) : "memory");
-}
-__device__ inline v4u ld16(const void* p) {
-  v4u r;
-  asm volatile("global_load_dwordx4 %0, %1, off" : "=v"(r) : "v"(p));
-  return r;
-}
-__device__ inline v2u ld8(const void* p) {
-  v2u r;
-  asm volatile("global_load_dwordx2 %0, %1, off" : "=v"(r) : "v"(p));
-  return r;
-}
-__device__ inline uint32_t ld2(const void* p) {
-  uint32_t r;
-  asm volatile("global_load_ushort %0, %1, off" : "=v"(r) : "v"(p));
-  return r;
-}
-template <int N>
-__device__ inline void vmwait() {
-  static_assert(N >= 0 && N < 64, "vmcnt range");
-  asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
-}
-__device__ inline void lgkm0() { asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory"); }
-template <class T>
-__device__ inline void pin(T& v) {
-  asm volatile("" : "+v"(v));
-}
 
 // LDS byte offset of 16-byte chunk c (0..3) of staged 64-byte row r. The XOR
 // keeps both the row-per-lane MFMA reads and the chunk-per-lane writes free

@@ -11,23 +11,24 @@
 //    contiguous HBM (one 32-element block of 64 rows). Scales of the same
 //    64 rows are 128 contiguous bytes.
 //  * A workgroup (4 waves) owns R consecutive rows of a panel (R = 8..64,
-//    chosen per shape so the grid has enough workgroups to fill 256 CUs)
-//    and the whole K range: lane = (row r, block slot), 64/R slots per wave,
-//    so each wave load covers R*16 contiguous bytes (>= one 128 B line) per
-//    block. The x vector is staged once per workgroup in LDS together with
-//    per-block sums; slots reduce with xor-shuffles and then across waves
-//    through LDS, in a fixed order (deterministic). No cross-workgroup
-//    communication is needed for any decode shape.
-//  * Register dequant without conversions: masking a word with 0x000F000F
-//    yields two fp16 subnormals q*2^-24; with 0x00F000F0, 16q*2^-24.
-//    v_dot2_f32_f16 multiplies them by an fp16 x pair with fp32
-//    accumulation (products exact), and the offset-8 is removed once per
-//    block with the staged block sum: sum (q-8) x = sum q x - 8 sum x.
-//    The device nibble order puts elements (2m, 2m+1) of a word into the
-//    two halves, so x pairs are used as stored. 9 VALU ops per 8 weights.
-//  * fp32 x (the engine's residual-stream activations) takes an exact fp32
-//    path: bytes of (w & 0x0F0F0F0F) and (w >> 4 & 0x0F0F0F0F) convert
-//    with v_cvt_f32_ubyteN and accumulate with FMAs.
+//    chosen per shape so the grid fills 256 CUs and every lane's blocks fit
+//    one batch of loads) and the whole K range: lane = (row r, block slot),
+//    64/R slots per wave, so each wave load covers R*16 contiguous bytes
+//    (>= one 128 B line) per block. Workgroups are ordered XCD-major so the
+//    workgroups of one panel share its scale lines in one L2.
+//  * The x slice is copied to LDS with direct-to-LDS loads; every weight
+//    unit and scale of the lane is then requested at once with streaming
+//    loads, and each unit is consumed after its own wait count, so HBM sees
+//    the whole matrix requested up front and the x copy overlaps it.
+//  * Register dequant: a masked nibble pair OR 0x6400 is the fp16 pair
+//    1024 + q (or 1024 + 16q); one packed add (or fma) makes it q - 8
+//    exactly, and v_dot2_f32_f16 accumulates the exact products with the
+//    fp16 x pair in fp32. The block scale multiplies the block's sum.
+//  * Slots reduce with xor-shuffles and then across waves through LDS, in a
+//    fixed order (deterministic).
+//  * fp32 x (the engine's residual-stream activations) takes an fp32 path:
+//    bytes of (w & 0x0F0F0F0F) and (w >> 4 & 0x0F0F0F0F) convert with
+//    v_cvt_f32_ubyteN and accumulate with FMAs.
 //  * Matrices with fewer than 2048 rows also split K across workgroups; the
 //    last workgroup of a row group (atomic ticket, agent-scope
 //    release/acquire by one wave) sums the fp32 partials in split order and
@@ -50,150 +51,157 @@ constexpr size_t GEMV_TICKET_BYTES = GEMV_MAX_TICKETS * sizeof(uint32_t);
 
 __device__ inline v2h as_h2(uint32_t v) { return __builtin_bit_cast(v2h, v); }
 
-// sum_{k in block} (q_k - 8) x_k for fp16 x. xp: 16 fp16 pairs of the block.
-__device__ inline float block_dot_h(const uint4 u, const uint32_t* __restrict__ xp, float xsum) {
-  const uint32_t w[4] = {u.x, u.y, u.z, u.w};
+// sum_{k in block} (q_k - 8) x_k for fp16 x; xp: the block's 16 fp16 pairs.
+// Each word yields four fp16 pairs of (q - 8) without conversions: OR-ing a
+// masked nibble pair into 0x6400 gives 1024 + q (low nibbles) or 1024 + 16q
+// (high nibbles) exactly, and one packed add / fma takes that to q - 8
+// exactly. The device nibble order puts elements (2m, 2m+1) in the two
+// halves, so the x pairs are used as stored. v_dot2_f32_f16 forms the exact
+// products (q - 8) * x and accumulates in fp32. 13 VALU ops per 8 weights.
+__device__ inline float block_dot_h(const v4u u, const uint32_t* __restrict__ xp) {
+  const v2h off_lo = {(_Float16)-1032.0f, (_Float16)-1032.0f};
+  const v2h sixteenth = {(_Float16)0.0625f, (_Float16)0.0625f};
+  const v2h off_hi = {(_Float16)-72.0f, (_Float16)-72.0f};
   float lo = 0.0f, hi = 0.0f;
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
-    const uint32_t w8 = w[i] >> 8;
-    lo = __builtin_amdgcn_fdot2(as_h2(w[i] & 0x000F000Fu), as_h2(xp[4 * i + 0]), lo, false);
-    hi = __builtin_amdgcn_fdot2(as_h2(w[i] & 0x00F000F0u), as_h2(xp[4 * i + 1]), hi, false);
-    lo = __builtin_amdgcn_fdot2(as_h2(w8 & 0x000F000Fu), as_h2(xp[4 * i + 2]), lo, false);
-    hi = __builtin_amdgcn_fdot2(as_h2(w8 & 0x00F000F0u), as_h2(xp[4 * i + 3]), hi, false);
+    const uint32_t w = u[i], w8 = w >> 8;
+    const v2h p0 = as_h2((w & 0x000F000Fu) | 0x64006400u) + off_lo;
+    const v2h p1 = as_h2((w & 0x00F000F0u) | 0x64006400u) * sixteenth + off_hi;
+    const v2h p2 = as_h2((w8 & 0x000F000Fu) | 0x64006400u) + off_lo;
+    const v2h p3 = as_h2((w8 & 0x00F000F0u) | 0x64006400u) * sixteenth + off_hi;
+    lo = __builtin_amdgcn_fdot2(p0, as_h2(xp[4 * i + 0]), lo, false);
+    hi = __builtin_amdgcn_fdot2(p1, as_h2(xp[4 * i + 1]), hi, false);
+    lo = __builtin_amdgcn_fdot2(p2, as_h2(xp[4 * i + 2]), lo, false);
+    hi = __builtin_amdgcn_fdot2(p3, as_h2(xp[4 * i + 3]), hi, false);
   }
-  // lo = 2^-24 * sum q x over low nibbles, hi = 2^-20 * sum q x over high nibbles
-  return fmaf(hi, 1048576.0f, lo * 16777216.0f) - 8.0f * xsum;
+  return lo + hi;
 }
 
-// Same for fp32 x. xf: 32 floats of the block in natural order.
-__device__ inline float block_dot_f(const uint4 u, const float* __restrict__ xf, float xsum) {
-  const uint32_t w[4] = {u.x, u.y, u.z, u.w};
+// Same for fp32 x; xf: the block's 32 floats in natural order. Bytes of
+// (w & 0x0F0F0F0F) are elements e0 e4 e1 e5, of (w >> 4 & 0x0F0F0F0F)
+// e2 e6 e3 e7; q - 8 is exact in fp32.
+__device__ inline float block_dot_f(const v4u u, const float* __restrict__ xf) {
   float acc = 0.0f;
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
-    const uint32_t a = w[i] & 0x0F0F0F0Fu;          // bytes: e0 e4 e1 e5
-    const uint32_t b = (w[i] >> 4) & 0x0F0F0F0Fu;   // bytes: e2 e6 e3 e7
+    const uint32_t a = u[i] & 0x0F0F0F0Fu;
+    const uint32_t b = (u[i] >> 4) & 0x0F0F0F0Fu;
     const float* x = xf + 8 * i;
-    acc = fmaf((float)(a & 0xFFu), x[0], acc);
-    acc = fmaf((float)((a >> 8) & 0xFFu), x[4], acc);
-    acc = fmaf((float)((a >> 16) & 0xFFu), x[1], acc);
-    acc = fmaf((float)(a >> 24), x[5], acc);
-    acc = fmaf((float)(b & 0xFFu), x[2], acc);
-    acc = fmaf((float)((b >> 8) & 0xFFu), x[6], acc);
-    acc = fmaf((float)((b >> 16) & 0xFFu), x[3], acc);
-    acc = fmaf((float)(b >> 24), x[7], acc);
+    acc = fmaf((float)(a & 0xFFu) - 8.0f, x[0], acc);
+    acc = fmaf((float)((a >> 8) & 0xFFu) - 8.0f, x[4], acc);
+    acc = fmaf((float)((a >> 16) & 0xFFu) - 8.0f, x[1], acc);
+    acc = fmaf((float)(a >> 24) - 8.0f, x[5], acc);
+    acc = fmaf((float)(b & 0xFFu) - 8.0f, x[2], acc);
+    acc = fmaf((float)((b >> 8) & 0xFFu) - 8.0f, x[6], acc);
+    acc = fmaf((float)((b >> 16) & 0xFFu) - 8.0f, x[3], acc);
+    acc = fmaf((float)(b >> 24) - 8.0f, x[7], acc);
   }
-  return acc - 8.0f * xsum;
+  return acc;
 }
 
+// Load of the block scale at index idx, as raw bits. Not a streaming load:
+// a panel's 128-byte scale line is shared by the 64/R workgroups of that
+// panel, which should find it in L2.
 template <int ST>
-__device__ inline float load_scale(const void* __restrict__ scv, long idx) {
-  if constexpr (ST == Q4_SCALE_F16) {
-    return h2f(reinterpret_cast<const uint16_t*>(scv)[idx]);
-  } else {
-    return h2f(e4m3_to_h_scaled(reinterpret_cast<const uint8_t*>(scv)[idx]));  // value * 2^-8
-  }
+__device__ inline uint32_t load_scale(const void* __restrict__ scv, long idx) {
+  if constexpr (ST == Q4_SCALE_F16) return ld2(reinterpret_cast<const uint16_t*>(scv) + idx);
+  else return ld1(reinterpret_cast<const uint8_t*>(scv) + idx);
+}
+template <int ST>
+__device__ inline float scale_value(uint32_t bits) {
+  if constexpr (ST == Q4_SCALE_F16) return h2f((uint16_t)bits);
+  else return h2f(e4m3_to_h_scaled(bits));  // value * 2^-8
 }
 
+// Row group of workgroup b in a launch of G workgroups. Workgroups are
+// dispatched round-robin over the 8 XCDs (b % 8), each with its own L2.
+// XCD-major order gives every XCD one contiguous range of row groups, so
+// the 64/R workgroups of a 64-row panel, which share the panel's 128-byte
+// scale lines, run on one XCD (at most one panel per XCD boundary is split)
+// and each line is fetched from HBM once instead of once per XCD.
+__device__ inline int xcd_major(int b, int G) {
+  const int x = b & 7, per = G >> 3, rem = G & 7;
+  return x * per + min(x, rem) + (b >> 3);
+}
+
+// Rows [g*R, g*R + R) of one GEMV over the K slice s of split (the whole K
+// when split == 1). NP = row groups of the launch * R (split-K partial stride).
+//
+// Order of work per wave: (1) direct-to-LDS loads of the wave's share of the
+// x slice (no registers), (2) the lane's first U weight units (streaming
+// loads) and scales (clamped indices so the count is static), (3) wait for
+// the x loads only (s_waitcnt vmcnt(2U): loads return in order) and one
+// barrier, (4) unit t is used after vmcnt(2(U-1-t)), so the dot products
+// start while later units are still in flight. Lanes with more than U blocks
+// (long K) load and use further batches the same way.
 template <int R, int U, int XT, int ST, int YT>
-__global__ void __launch_bounds__(GEMV_THREADS)
-gemv_kernel(const void* __restrict__ xv, const uint4* __restrict__ wq, const void* __restrict__ scv, float outscale,
-            void* __restrict__ yv, int N, int nblk, int split, float* __restrict__ part, uint32_t* __restrict__ cnt) {
+__device__ __forceinline__ void gemv_rows(const void* __restrict__ xv, const uint4* __restrict__ wq,
+                                          const void* __restrict__ scv, float outscale, void* __restrict__ yv,
+                                          int N, int nblk, int g, int s, int split, long NP,
+                                          float* __restrict__ part, uint32_t* __restrict__ cnt,
+                                          uint32_t* __restrict__ smem, float (*red)[R]) {
   constexpr bool XH = (XT == Q4_DT_F16);
   constexpr int SW = 64 / R;               // block slots per wave
   constexpr int S = SW * GEMV_WAVES;       // block slots per workgroup
-  extern __shared__ __attribute__((aligned(16))) uint32_t smem[];
-  __shared__ float red[GEMV_WAVES][R];
-
-  const int g = blockIdx.x, s = blockIdx.y;
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
   const int r = lane % R, slot = wave * SW + lane / R;
-  const int b_lo = (int)((long)s * nblk / split);
-  const int nb = (int)((long)(s + 1) * nblk / split) - b_lo;
+  int b_lo = 0, nb = nblk;
+  if (split > 1) {  // (a 64-bit division: kept off the common path)
+    b_lo = (int)((long)s * nblk / split);
+    nb = (int)((long)(s + 1) * nblk / split) - b_lo;
+  }
   const long k0 = (long)b_lo * BLK;
-  uint32_t* xs_h = smem;
-  float* xs_f = reinterpret_cast<float*>(smem);
-  float* xsum = reinterpret_cast<float*>(smem + (XH ? nb * 16 : nb * BLK));
 
-  // ---- stage the x slice [k0, k0 + 32 nb). The first round of x loads is
-  //      issued, then the first batch of weight units, then the x stores to
-  //      LDS: every load is unconditional (indices clamped) so the in-order
-  //      load counter lets the x stores wait for the x loads only, and the
-  //      weight latency overlaps the staging (the barrier waits on LDS). ----
-  constexpr int XU = 4;  // 16-byte x loads per thread per round
+  // (1) x slice [k0, k0 + 32 nb) -> LDS, 1 KB per wave instruction; chunks
+  //     past the slice re-read its last chunk into the padding of the area
   const int n16 = XH ? nb * 4 : nb * 8;
-  const uint4* x4 = XH ? reinterpret_cast<const uint4*>(reinterpret_cast<const uint16_t*>(xv) + k0)
-                       : reinterpret_cast<const uint4*>(reinterpret_cast<const float*>(xv) + k0);
-  uint4 t4[XU];
-#pragma unroll
-  for (int q = 0; q < XU; ++q) t4[q] = x4[min(tid + q * GEMV_THREADS, n16 - 1)];
+  const int nv = (n16 + 63) >> 6;
+  const uint8_t* xsrc = reinterpret_cast<const uint8_t*>(xv) + k0 * (XH ? 2 : 4);
+  for (int v = wave; v < nv; v += GEMV_WAVES) dma16(xsrc + (long)min(v * 64 + lane, n16 - 1) * 16, smem + v * 256);
+
+  // (2) first batch of weight units and scales: blocks slot, slot + S, ...
   const int n0 = g * R;
   const long ubase = ((long)(n0 / PANEL) * nblk + b_lo) * PANEL + (n0 % PANEL) + r;  // unit of block j: ubase + 64 j
-  uint4 u[U];
-  float sc[U];
+  const uint8_t* wb = reinterpret_cast<const uint8_t*>(wq);
+  v4u u[U];
+  uint32_t sb[U];
 #pragma unroll
-  for (int t = 0; t < U; ++t) {  // first batch (same as load_batch(slot) below)
-    const int jj = min(slot + t * S, nb - 1);
-    u[t] = wq[ubase + (long)jj * PANEL];
-    sc[t] = load_scale<ST>(scv, ubase + (long)jj * PANEL);
+  for (int t = 0; t < U; ++t) {
+    const long ix = ubase + (long)min(slot + t * S, nb - 1) * PANEL;
+    u[t] = ld16_nt(wb + ix * 16);
+    sb[t] = load_scale<ST>(scv, ix);
   }
-#pragma unroll
-  for (int q = 0; q < XU; ++q) {
-    const int i = tid + q * GEMV_THREADS;
-    if (i < n16) reinterpret_cast<uint4*>(smem)[i] = t4[q];
-  }
-  for (int i0 = tid + XU * GEMV_THREADS; i0 < n16; i0 += GEMV_THREADS * XU) {  // long K only
-#pragma unroll
-    for (int q = 0; q < XU; ++q) t4[q] = x4[min(i0 + q * GEMV_THREADS, n16 - 1)];
-#pragma unroll
-    for (int q = 0; q < XU; ++q) {
-      const int i = i0 + q * GEMV_THREADS;
-      if (i < n16) reinterpret_cast<uint4*>(smem)[i] = t4[q];
-    }
-  }
-  __syncthreads();
-  for (int j = tid; j < nb; j += GEMV_THREADS) {
-    float t = 0.0f;
-    if constexpr (XH) {
-#pragma unroll
-      for (int i = 0; i < 16; ++i) {
-        v2h pr = as_h2(xs_h[j * 16 + i]);
-        t += (float)pr.x + (float)pr.y;
-      }
-    } else {
-#pragma unroll
-      for (int i = 0; i < BLK; ++i) t += xs_f[j * BLK + i];
-    }
-    xsum[j] = t;
-  }
+  // (3) this wave's x chunks have landed; the barrier publishes every wave's
+  vmwait<2 * U>();
   __syncthreads();
 
-  // ---- this lane's blocks: slot, slot + S, slot + 2S, ... in batches of U;
-  //      a batch is loaded (unconditionally, clamped) before it is used ----
-  auto load_batch = [&](int j) {
-#pragma unroll
-    for (int t = 0; t < U; ++t) {
-      const int jj = min(j + t * S, nb - 1);
-      u[t] = wq[ubase + (long)jj * PANEL];
-      sc[t] = load_scale<ST>(scv, ubase + (long)jj * PANEL);
-    }
-  };
+  // (4) dot products, unit by unit as they arrive
+  const uint32_t* xs_h = smem;
+  const float* xs_f = reinterpret_cast<const float*>(smem);
   float acc = 0.0f;
   for (int j = slot;;) {
-#pragma unroll
-    for (int t = 0; t < U; ++t) {
+    static_for<0, U>([&](auto tc) {
+      constexpr int t = decltype(tc)::value;
+      vmwait<2 * (U - 1 - t)>();
+      pin(u[t]);
+      pin(sb[t]);
       const int jj = j + t * S;
       if (jj < nb) {
         float d;
-        if constexpr (XH) d = block_dot_h(u[t], xs_h + jj * 16, xsum[jj]);
-        else d = block_dot_f(u[t], xs_f + jj * BLK, xsum[jj]);
-        acc = fmaf(sc[t], d, acc);
+        if constexpr (XH) d = block_dot_h(u[t], xs_h + jj * 16);
+        else d = block_dot_f(u[t], xs_f + jj * BLK);
+        acc = fmaf(scale_value<ST>(sb[t]), d, acc);
       }
-    }
+    });
     j += S * U;
-    if (j >= nb) break;
-    load_batch(j);
+    if (__builtin_amdgcn_readfirstlane(j - slot) >= nb) break;  // wave-uniform: j - slot is the same in every lane
+#pragma unroll
+    for (int t = 0; t < U; ++t) {
+      const long ix = ubase + (long)min(j + t * S, nb - 1) * PANEL;
+      u[t] = ld16_nt(wb + ix * 16);
+      sb[t] = load_scale<ST>(scv, ix);
+    }
   }
   // slots of a row: lanes r, r + R, r + 2R, ... of each wave, then the 4 waves
 #pragma unroll
@@ -214,7 +222,6 @@ gemv_kernel(const void* __restrict__ xv, const uint4* __restrict__ wq, const voi
   }
 
   // ---- split-K: publish this workgroup's partial; the last one reduces ----
-  const long NP = (long)gridDim.x * R;
   if (lane < R) part[(long)s * NP + n] = v;
   __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");
   uint32_t prev = 0;
@@ -234,25 +241,87 @@ gemv_kernel(const void* __restrict__ xv, const uint4* __restrict__ wq, const voi
   if (lane == 0) __hip_atomic_store(&cnt[g], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
+template <int R, int U, int XT, int ST, int YT>
+__global__ void __launch_bounds__(GEMV_THREADS)
+gemv_kernel(const void* __restrict__ xv, const uint4* __restrict__ wq, const void* __restrict__ scv, float outscale,
+            void* __restrict__ yv, int N, int nblk, int split, float* __restrict__ part, uint32_t* __restrict__ cnt) {
+  extern __shared__ __attribute__((aligned(16))) uint32_t smem[];
+  __shared__ float red[GEMV_WAVES][R];
+  // split-K grids (small matrices only) keep the plain order: their row
+  // groups are reduced through the workspace, not through L2 reuse
+  const int g = gridDim.y == 1 ? xcd_major(blockIdx.x, gridDim.x) : blockIdx.x;
+  gemv_rows<R, U, XT, ST, YT>(xv, wq, scv, outscale, yv, N, nblk, g, blockIdx.y, split, (long)gridDim.x * R, part,
+                              cnt, smem, red);
+}
+
+// Several GEMVs over one x (same K and types) in one launch: segment i owns
+// row groups [g_end[i-1], g_end[i]) of the grid; every segment covers whole
+// panels.
+struct GemvSeg {
+  const uint4* wq;
+  const void* sc;
+  void* y;
+  float outscale;
+  int N;
+  int g_end;
+};
+struct GemvSegs {
+  GemvSeg s[Q4_GEMV_MAX_BATCH];
+  int count;
+};
+
+template <int R, int U, int XT, int ST, int YT>
+__global__ void __launch_bounds__(GEMV_THREADS)
+gemv_batch_kernel(const void* __restrict__ xv, int nblk, const GemvSegs segs) {
+  extern __shared__ __attribute__((aligned(16))) uint32_t smem[];
+  __shared__ float red[GEMV_WAVES][R];
+  const int g = xcd_major(blockIdx.x, gridDim.x);
+  // segment selection with compile-time indices only (the argument block
+  // stays in the kernarg segment; a dynamic index would copy it to scratch)
+  const uint4* wq = segs.s[0].wq;
+  const void* sc = segs.s[0].sc;
+  void* y = segs.s[0].y;
+  float os = segs.s[0].outscale;
+  int N = segs.s[0].N, g0 = 0;
+#pragma unroll
+  for (int t = 1; t < Q4_GEMV_MAX_BATCH; ++t) {
+    if (t < segs.count && g >= segs.s[t - 1].g_end) {
+      wq = segs.s[t].wq;
+      sc = segs.s[t].sc;
+      y = segs.s[t].y;
+      os = segs.s[t].outscale;
+      N = segs.s[t].N;
+      g0 = segs.s[t - 1].g_end;
+    }
+  }
+  gemv_rows<R, U, XT, ST, YT>(xv, wq, sc, os, y, N, nblk, g - g0, 0, 1, 0, nullptr, nullptr, smem, red);
+}
+
 typedef void (*gemv_fn)(const void*, const uint4*, const void*, float, void*, int, int, int, float*, uint32_t*);
+typedef void (*gemv_batch_fn)(const void*, int, const GemvSegs);
+struct GemvFns {
+  gemv_fn one;
+  gemv_batch_fn many;
+};
 
 template <int R, int U, int XT, int ST>
-static gemv_fn pick_y(int yt) {
-  return yt == Q4_DT_F16 ? gemv_kernel<R, U, XT, ST, Q4_DT_F16> : gemv_kernel<R, U, XT, ST, Q4_DT_F32>;
+static GemvFns pick_y(int yt) {
+  if (yt == Q4_DT_F16) return {gemv_kernel<R, U, XT, ST, Q4_DT_F16>, gemv_batch_kernel<R, U, XT, ST, Q4_DT_F16>};
+  return {gemv_kernel<R, U, XT, ST, Q4_DT_F32>, gemv_batch_kernel<R, U, XT, ST, Q4_DT_F32>};
 }
 template <int R, int U, int XT>
-static gemv_fn pick_s(int st, int yt) {
+static GemvFns pick_s(int st, int yt) {
   return st == Q4_SCALE_E4M3 ? pick_y<R, U, XT, Q4_SCALE_E4M3>(yt) : pick_y<R, U, XT, Q4_SCALE_F16>(yt);
 }
 template <int R, int U>
-static gemv_fn pick_x(int xt, int st, int yt) {
+static GemvFns pick_x(int xt, int st, int yt) {
   return xt == Q4_DT_F16 ? pick_s<R, U, Q4_DT_F16>(st, yt) : pick_s<R, U, Q4_DT_F32>(st, yt);
 }
 template <int R>
-static gemv_fn pick_u(int U, int xt, int st, int yt) {
-  return U == 4 ? pick_x<R, 4>(xt, st, yt) : pick_x<R, 8>(xt, st, yt);
+static GemvFns pick_u(int U, int xt, int st, int yt) {
+  return U == 4 ? pick_x<R, 4>(xt, st, yt) : U == 8 ? pick_x<R, 8>(xt, st, yt) : pick_x<R, 16>(xt, st, yt);
 }
-static gemv_fn pick(int R, int U, int xt, int st, int yt) {
+static GemvFns pick(int R, int U, int xt, int st, int yt) {
   switch (R) {
     case 64: return pick_u<64>(U, xt, st, yt);
     case 32: return pick_u<32>(U, xt, st, yt);
@@ -261,18 +330,11 @@ static gemv_fn pick(int R, int U, int xt, int st, int yt) {
   }
 }
 
-struct GemvPlan {
-  int R, U, split, nb_max;
-  size_t lds, ws;
-};
-
-// Rows per workgroup R, units in flight U and K split for an N x K GEMV
-// (measured on MI355X over the decode shapes: the largest R that still gives
-// GEMV_TARGET_WGS workgroups, else the largest that gives one per CU; U = 4
-// when every lane's blocks fit one batch of 4). Q4MI_GEMV_ROWS (8/16/32/64)
-// overrides R for tuning sweeps.
-static GemvPlan plan(int N, int K, int split_req, int x_dtype) {
-  const int NP = pad_rows(N), nblk = K / BLK;
+// Rows per workgroup R for NP padded rows: the largest R that gives
+// GEMV_TARGET_WGS workgroups, else the largest that gives one workgroup per
+// CU, else 8. Q4MI_GEMV_ROWS (8/16/32/64) overrides R for tuning sweeps.
+static int rows_per_group(int NP, int nblk) {
+  (void)nblk;
   int R = 0;
   for (int c : {64, 32, 16, 8})
     if (NP / c >= GEMV_TARGET_WGS) { R = c; break; }
@@ -284,6 +346,36 @@ static GemvPlan plan(int N, int K, int split_req, int x_dtype) {
     int v = atoi(e);
     if (v == 8 || v == 16 || v == 32 || v == 64) R = v;
   }
+  return R;
+}
+
+// Units in flight per lane (one batch) for nb blocks per workgroup and
+// wgs workgroups: 4 when every lane's blocks fit 4 or the grid is at most
+// two workgroups per CU, else 8. Measured on MI355X over the decode shapes:
+// more loads in flight per lane than this is slower (16 loses 5-25%).
+// Q4MI_GEMV_UNITS (4/8/16) overrides it for tuning sweeps.
+static int units_in_flight(int nb, int R, long wgs) {
+  if (const char* e = getenv("Q4MI_GEMV_UNITS")) {
+    int v = atoi(e);
+    if (v == 4 || v == 8 || v == 16) return v;
+  }
+  const int per_lane = ceil_div(nb, (64 / R) * GEMV_WAVES);
+  return per_lane <= 4 || wgs <= 2 * GEMV_MIN_WGS ? 4 : 8;
+}
+
+// LDS bytes of x per block, and of the staging area for nb blocks (whole
+// 1 KB direct-load rows).
+static int x_block_bytes(int x_dtype) { return x_dtype == Q4_DT_F16 ? 64 : 128; }
+static size_t x_stage_lds(int nb, int x_dtype) { return (size_t)ceil_div((long)nb * x_block_bytes(x_dtype), 1024) * 1024; }
+
+struct GemvPlan {
+  int R, U, split, nb_max;
+  size_t lds, ws;
+};
+
+static GemvPlan plan(int N, int K, int split_req, int x_dtype) {
+  const int NP = pad_rows(N), nblk = K / BLK;
+  const int R = rows_per_group(NP, nblk);
   const int wgs = NP / R;
   int s = split_req;
   if (s <= 0) {
@@ -294,16 +386,15 @@ static GemvPlan plan(int N, int K, int split_req, int x_dtype) {
       if (s > cap) s = cap;
     }
   }
-  const int per_block = (x_dtype == Q4_DT_F16 ? 64 : 128) + 4;
-  const int max_nb = GEMV_LDS_MAX / per_block;
+  const int max_nb = GEMV_LDS_MAX / x_block_bytes(x_dtype);
   if (s < ceil_div(nblk, max_nb)) s = ceil_div(nblk, max_nb);
   if (s > nblk) s = nblk;
   GemvPlan p;
   p.R = R;
   p.split = s;
   p.nb_max = ceil_div(nblk, s);
-  p.U = ceil_div(p.nb_max, (64 / R) * GEMV_WAVES) <= 4 ? 4 : 8;
-  p.lds = (size_t)p.nb_max * per_block;
+  p.U = units_in_flight(p.nb_max, R, (long)wgs * s);
+  p.lds = x_stage_lds(p.nb_max, x_dtype);
   p.ws = 0;
   if (s > 1) p.ws = (GEMV_TICKET_BYTES + (size_t)s * NP * sizeof(float) + 255) & ~(size_t)255;
   return p;
@@ -352,7 +443,7 @@ int q4_gemv(const void* x, int x_dtype, const uint32_t* wq, const void* scales, 
   uint32_t* cnt = pl.ws ? reinterpret_cast<uint32_t*>(ws) : nullptr;
   float* part = pl.ws ? reinterpret_cast<float*>(reinterpret_cast<char*>(ws) + GEMV_TICKET_BYTES) : nullptr;
   const float outscale = scale_fmt == Q4_SCALE_E4M3 ? inv * 256.0f : 1.0f;
-  gemv_fn fn = pick(pl.R, pl.U, x_dtype, scale_fmt, y_dtype);
+  gemv_fn fn = pick(pl.R, pl.U, x_dtype, scale_fmt, y_dtype).one;
   hipLaunchKernelGGL(fn, dim3(groups, pl.split), dim3(GEMV_THREADS), pl.lds, as_stream(stream), x,
                      reinterpret_cast<const uint4*>(wq), scales, outscale, y, N, K / BLK, pl.split, part, cnt);
   Q4_LAUNCHED("gemv");
@@ -367,6 +458,50 @@ int q4_gemv_f16s(const void* x, int x_dtype, const uint32_t* wq, const uint16_t*
 int q4_gemv_e4m3s(const void* x, int x_dtype, const uint32_t* wq, const uint8_t* sc8, float inv, void* y, int y_dtype,
                   int N, int K, int split, void* ws, size_t ws_size, void* stream) {
   return q4_gemv(x, x_dtype, wq, sc8, Q4_SCALE_E4M3, inv, y, y_dtype, N, K, split, ws, ws_size, stream);
+}
+
+int q4_gemv_batch(const void* x, int x_dtype, int K, int scale_fmt, int y_dtype, int count,
+                  const uint32_t* const* wq, const void* const* scales, const float* inv, void* const* y,
+                  const int* N, void* stream) {
+  clear_error();
+  Q4_ARG(count >= 1 && count <= Q4_GEMV_MAX_BATCH, "batch of %d GEMVs (1..%d)", count, Q4_GEMV_MAX_BATCH);
+  Q4_ARG(wq && scales && y && N && x, "null pointer");
+  Q4_ARG(K > 0 && K % BLK == 0 && (long)K <= (1L << 24), "bad GEMV K=%d (a positive multiple of 32)", K);
+  Q4_ARG(x_dtype == Q4_DT_F32 || x_dtype == Q4_DT_F16, "bad x dtype %d", x_dtype);
+  Q4_ARG(y_dtype == Q4_DT_F32 || y_dtype == Q4_DT_F16, "bad y dtype %d", y_dtype);
+  Q4_ARG(scale_fmt == Q4_SCALE_F16 || scale_fmt == Q4_SCALE_E4M3, "bad scale format %d", scale_fmt);
+  Q4_ARG(((uintptr_t)x & 15) == 0, "x must be 16-byte aligned");
+  const int nblk = K / BLK;
+  Q4_ARG((long)nblk * x_block_bytes(x_dtype) <= GEMV_LDS_MAX, "batched GEMV needs K <= %d for this x dtype (got %d)",
+         GEMV_LDS_MAX / x_block_bytes(x_dtype) * BLK, K);
+  long NP = 0;
+  for (int i = 0; i < count; ++i) {
+    Q4_ARG(wq[i] && scales[i] && y[i], "null pointer in batch entry %d", i);
+    Q4_ARG(N[i] > 0 && N[i] <= (1 << 30), "bad N=%d in batch entry %d", N[i], i);
+    Q4_ARG(((uintptr_t)wq[i] & 15) == 0, "wq of batch entry %d must be 16-byte aligned", i);
+    NP += pad_rows(N[i]);
+  }
+  Q4_ARG(NP <= (1L << 30), "batched GEMV too large");
+  const int R = rows_per_group((int)NP, nblk);
+  GemvSegs segs;
+  memset(&segs, 0, sizeof(segs));
+  segs.count = count;
+  int groups = 0;
+  for (int i = 0; i < count; ++i) {
+    groups += pad_rows(N[i]) / R;
+    segs.s[i].wq = reinterpret_cast<const uint4*>(wq[i]);
+    segs.s[i].sc = scales[i];
+    segs.s[i].y = y[i];
+    segs.s[i].outscale = scale_fmt == Q4_SCALE_E4M3 ? (inv ? inv[i] : 1.0f) * 256.0f : 1.0f;
+    segs.s[i].N = N[i];
+    segs.s[i].g_end = groups;
+  }
+  const int U = units_in_flight(nblk, R, groups);
+  gemv_batch_fn fn = pick(R, U, x_dtype, scale_fmt, y_dtype).many;
+  hipLaunchKernelGGL(fn, dim3(groups), dim3(GEMV_THREADS), x_stage_lds(nblk, x_dtype), as_stream(stream), x, nblk,
+                     segs);
+  Q4_LAUNCHED("gemv_batch");
+  return Q4_OK;
 }
 
 }  // extern "C"

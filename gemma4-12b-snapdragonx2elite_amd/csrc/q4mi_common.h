@@ -22,6 +22,7 @@ typedef unsigned int v4u __attribute__((ext_vector_type(4)));
 typedef float v4f __attribute__((ext_vector_type(4)));
 typedef _Float16 v8h __attribute__((ext_vector_type(8)));
 typedef _Float16 v2h __attribute__((ext_vector_type(2)));
+typedef unsigned v2u __attribute__((ext_vector_type(2)));
 
 void set_error(const char* fmt, ...);
 void clear_error();
@@ -91,6 +92,68 @@ __device__ inline uint16_t f2h_after_f32(float f) {
 // bias (7) becomes the f16 bias (15) and subnormals stay subnormal.
 __device__ inline uint16_t e4m3_to_h_scaled(uint32_t b) {
   return (uint16_t)(((b & 0x80u) << 8) | ((b & 0x7Fu) << 7));
+}
+
+// ---- inline-asm memory operations ------------------------------------------
+// Loads issued through asm are invisible to the compiler's wait-count
+// tracking: the kernel waits for them with explicit s_waitcnt vmcnt(n), the
+// count fixed by the issue order (vector memory loads return in order), and
+// pins the registers a wait covers (an empty asm that reads and writes them)
+// so no use of a loaded value is scheduled above its wait. Volatile asm
+// statements keep their relative order; the direct-to-LDS load also
+// clobbers memory, so LDS accesses stay on their side of it.
+
+// 16 bytes per lane from global memory into LDS at lds_dst + 16 * lane
+// (lds_dst wave-uniform).
+__device__ inline void dma16(const void* gptr, const void* lds_dst) {
+  const unsigned l = __builtin_amdgcn_readfirstlane((unsigned)(uintptr_t)lds_dst);
+  asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(gptr), "s"(l) : "memory");
+}
+__device__ inline v4u ld16(const void* p) {
+  v4u r;
+  asm volatile("global_load_dwordx4 %0, %1, off" : "=v"(r) : "v"(p));
+  return r;
+}
+__device__ inline v2u ld8(const void* p) {
+  v2u r;
+  asm volatile("global_load_dwordx2 %0, %1, off" : "=v"(r) : "v"(p));
+  return r;
+}
+__device__ inline uint32_t ld2(const void* p) {
+  uint32_t r;
+  asm volatile("global_load_ushort %0, %1, off" : "=v"(r) : "v"(p));
+  return r;
+}
+__device__ inline uint32_t ld1(const void* p) {
+  uint32_t r;
+  asm volatile("global_load_ubyte %0, %1, off" : "=v"(r) : "v"(p));
+  return r;
+}
+// Streaming (non-temporal) variants for data read exactly once.
+__device__ inline v4u ld16_nt(const void* p) {
+  v4u r;
+  asm volatile("global_load_dwordx4 %0, %1, off nt" : "=v"(r) : "v"(p));
+  return r;
+}
+template <int N>
+__device__ inline void vmwait() {
+  static_assert(N >= 0 && N < 64, "vmcnt range");
+  asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
+}
+__device__ inline void lgkm0() { asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory"); }
+template <class T>
+__device__ inline void pin(T& v) {
+  asm volatile("" : "+v"(v));
+}
+
+// f(std::integral_constant<int, I>) for I = B .. E-1, unrolled at compile
+// time (wait counts and register indices must be constants).
+template <int B, int E, class F>
+__device__ __forceinline__ void static_for(F&& f) {
+  if constexpr (B < E) {
+    f(std::integral_constant<int, B>{});
+    static_for<B + 1, E>(f);
+  }
 }
 
 }  // namespace q4

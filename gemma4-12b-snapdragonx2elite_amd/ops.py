@@ -13,7 +13,7 @@ import ctypes as C
 import torch
 
 from . import _lib
-from ._lib import DT_F16, DT_F32, OP_GEMV, SCALE_E4M3, SCALE_F16, call, lib
+from ._lib import DT_F16, DT_F32, GEMV_MAX_BATCH, OP_GEMV, SCALE_E4M3, SCALE_F16, call, lib
 
 BLK = 32
 PANEL = 64
@@ -201,6 +201,43 @@ def gemv(x: torch.Tensor, wq: torch.Tensor, scales: torch.Tensor, N: int, K: int
     call("q4_gemv", _p(x), _dt(x), _p(wq), _p(scales), scale_fmt, C.c_float(inv), _p(y), _dt(y), N, K, split,
          _p(ws.t) if ws else C.c_void_p(0), ws.t.numel() if ws else 0, _stream())
     return y
+
+
+def gemv_batch_max_k(x_dtype) -> int:
+    """Largest K a batched GEMV stages for this activation dtype."""
+    return 32768 if x_dtype == torch.float16 else 16384
+
+
+def gemv_batch(x: torch.Tensor, mats, K: int, *, scale_fmt: int = SCALE_F16, y_dtype=None):
+    """Several GEMVs over one activation ``x`` in one launch.
+
+    ``mats``: sequence of ``(wq, scales, N, y, inv)`` (``y`` may be None: a new
+    tensor; ``inv`` only matters for e4m3 scales). Returns the list of outputs.
+    Every output gets the arithmetic of :func:`gemv` with split 1."""
+    n = len(mats)
+    if not 1 <= n <= GEMV_MAX_BATCH:
+        raise ValueError(f"gemv_batch takes 1..{GEMV_MAX_BATCH} matrices, got {n}")
+    if x.numel() != K:
+        raise ValueError(f"x has {x.numel()} elements, expected K={K}")
+    ys, keep = [], []
+    wqs, scs, yps = (C.c_void_p * n)(), (C.c_void_p * n)(), (C.c_void_p * n)()
+    Ns, invs = (C.c_int * n)(), (C.c_float * n)()
+    ydt = None
+    for i, (wq, sc, N, y, inv) in enumerate(mats):
+        if y is None:
+            y = torch.empty(N, dtype=y_dtype or x.dtype, device=x.device)
+        _check_int4(wq, sc, N, K, 1 if scale_fmt == SCALE_E4M3 else 2)
+        _need(y, N * y.element_size(), f"y of batch entry {i}")
+        if ydt is None:
+            ydt = _dt(y)
+        elif _dt(y) != ydt:
+            raise ValueError("all outputs of a GEMV batch must share one dtype")
+        wqs[i], scs[i], yps[i] = _p(wq), _p(sc), _p(y)
+        Ns[i], invs[i] = int(N), float(inv if inv is not None else 1.0)
+        ys.append(y)
+        keep.append((wq, sc))
+    call("q4_gemv_batch", _p(x), _dt(x), K, scale_fmt, ydt, n, wqs, scs, invs, yps, Ns, _stream())
+    return ys
 
 
 # ------------------------------------------------------------------ GEMMs

@@ -19,6 +19,8 @@ reference              here
                        with ``dr`` always None (the split-K reduce is
                        fused into the GEMV launch)
 ``gemv(g)`` :270-272   launches (or, inside :func:`record`, captures)
+``gemv_many(gs)``      (new) descriptors on one input buffer as one
+                       batched launch, e.g. q/k/v :232-234, gate/up :242-243
 ``gemm_ds`` :351-365   same arguments/return shape ``(cin, gem, cout, N, K)``
 ``gmm(C, t, L, tag)``  ``C`` is a torch stream or None (current stream)
   :391-400
@@ -149,6 +151,31 @@ def gemv(g: GemvDesc) -> None:
     """Enqueue (or capture) one GEMV (src/vk_engine.py:270-272)."""
     x, wq, sc, fmt, inv, y, N, K, split, ws = g.dp
     ops.gemv(x, wq, sc, N, K, scale_fmt=fmt, inv=inv, y=y, split=split, ws=ws)
+
+
+def gemv_many(gs) -> None:
+    """Enqueue several :func:`gemv_ds` descriptors that read the same input
+    buffer (q/k/v into the qkv buffer, gate/up: src/vk_engine.py:232-234,
+    242-243) as one batched launch. Descriptors that cannot share a launch
+    (different inputs, K, scale format, more than the batch limit) are
+    launched one by one; the results are the same either way."""
+    gs = list(gs)
+    groups: list = []
+    for g in gs:
+        x, _wq, sc, fmt, _inv, _y, _N, K, _split, _ws = g.dp
+        last = groups[-1] if groups else None
+        if (last is not None and len(last) < ops.GEMV_MAX_BATCH and last[0].dp[0].data_ptr() == x.data_ptr()
+                and last[0].dp[7] == K and last[0].dp[3] == fmt and last[0].dp[5].dtype == g.dp[5].dtype
+                and K <= ops.gemv_batch_max_k(x.dtype)):
+            last.append(g)
+        else:
+            groups.append([g])
+    for grp in groups:
+        if len(grp) == 1:
+            gemv(grp[0])
+            continue
+        x, _, _, fmt, _, _, _, K, _, _ = grp[0].dp
+        ops.gemv_batch(x, [(d.dp[1], d.dp[2], d.dp[6], d.dp[5], d.dp[4]) for d in grp], K, scale_fmt=fmt)
 
 
 _STAGE: dict = {}

@@ -131,6 +131,23 @@ int q4_gemv_e4m3s(const void* x, int x_dtype, const uint32_t* wq,
                   const uint8_t* sc8, float inv, void* y, int y_dtype, int N,
                   int K, int split, void* ws, size_t ws_bytes, void* stream);
 
+/* Several decode GEMVs that read the same activation x, in one launch:
+ * y_i[N_i] = (GEMV of matrix i) x for i < count, with the arithmetic of
+ * q4_gemv (split 1, no workspace). All matrices share K, the x dtype, the
+ * scale format and the y dtype; each has its own words wq[i], scales[i],
+ * output y[i] (may be offsets into one buffer) and, for e4m3 scales,
+ * inv[i] (inv may be NULL for fp16 scales). The reference records these
+ * as consecutive gemv_ds() dispatches on one input buffer, each followed by
+ * a global barrier: q/k/v into the qkv buffer (src/vk_engine.py:232-234,
+ * recorded at :278-279) and gate/up (:242-243, recorded at :284). The x
+ * slice must fit the workgroup staging area: K <= 32768 for fp16 x,
+ * K <= 16384 for fp32 x. */
+#define Q4_GEMV_MAX_BATCH 8
+int q4_gemv_batch(const void* x, int x_dtype, int K, int scale_fmt,
+                  int y_dtype, int count, const uint32_t* const* wq,
+                  const void* const* scales, const float* inv,
+                  void* const* y, const int* N, void* stream);
+
 /* ---- prefill GEMMs -------------------------------------------------------
  * W4A16: Y f16 [M][N] = X f16 [M][K] @ f16((q-8)*s)^T, fp32 accumulate.
  * Replaces coopgemm_i4h.comp (vk/coopgemm_i4h.comp:13-35) as wired by

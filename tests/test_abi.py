@@ -63,6 +63,18 @@ def test_argument_errors_without_gpu(g4):
     # reference layout needs N % 8 == 0
     st = lib.q4_repack_ref(null, null, 12, 32, null, null, null)
     assert st == g4._lib.Q4_ERR_ARG and "N % 8" in _err(g4)
+    # batched GEMV: count outside 1..8, K beyond the x staging area, bad entry
+    P = C.c_void_p * 9
+    ptrs, Ns = P(*([1 << 20] * 9)), (C.c_int * 9)(*([64] * 9))
+    st = lib.q4_gemv_batch(C.c_void_p(1 << 20), 1, 256, 0, 1, 0, ptrs, ptrs, None, ptrs, Ns, null)
+    assert st == g4._lib.Q4_ERR_ARG and "batch of 0" in _err(g4)
+    st = lib.q4_gemv_batch(C.c_void_p(1 << 20), 1, 256, 0, 1, 9, ptrs, ptrs, None, ptrs, Ns, null)
+    assert st == g4._lib.Q4_ERR_ARG and "batch of 9" in _err(g4)
+    st = lib.q4_gemv_batch(C.c_void_p(1 << 20), 0, 16416, 0, 1, 2, ptrs, ptrs, None, ptrs, Ns, null)
+    assert st == g4._lib.Q4_ERR_ARG and "K <= 16384" in _err(g4)
+    Ns[1] = 0
+    st = lib.q4_gemv_batch(C.c_void_p(1 << 20), 1, 256, 0, 1, 2, ptrs, ptrs, None, ptrs, Ns, null)
+    assert st == g4._lib.Q4_ERR_ARG and "entry 1" in _err(g4)
 
 
 def test_sizes_and_split_queries(g4):

@@ -50,6 +50,38 @@ def test_quant_gemv_ds_gemv(E, fp8):
     assert O.cosine(y, W @ x) > 0.98
 
 
+@pytest.mark.parametrize("fp8", [False, True])
+def test_gemv_many_qkv_into_one_buffer(E, fp8):
+    """q/k/v descriptors on one input buffer, written at their offsets of one
+    qkv buffer (src/vk_engine.py:232-234), launched as one batch: the same
+    values as three gemv() calls (both compared with the oracle)."""
+    rng = np.random.default_rng(43)
+    K = 3840
+    shapes = [4096, 2048, 2048]
+    x = rng.standard_normal(K).astype(np.float32)
+    inbuf, qkv = E.Buf(K * 4), E.Buf(sum(shapes) * 4)
+    inbuf.write(x)
+    descs, refs, off = [], [], 0
+    for N in shapes:
+        W = _w(rng, N, K)
+        qw = E.quant(W, fp8=fp8, prefill_i8=False)
+        descs.append(E.gemv_ds((qw, (N, K)), inbuf, qkv, out_off=off * 4))
+        q, sc = O.quant_codes(W)
+        if fp8:
+            e8, inv, _ = O.e4m3_lift(sc)
+            refs.append(O.gemv_ref(q, O.e4m3_decode(e8), x, inv=inv))
+        else:
+            refs.append(O.gemv_ref(q, sc.astype(np.float16).astype(np.float32), x))
+        off += N
+    E.gemv_many(descs)
+    torch.cuda.synchronize()
+    y = np.frombuffer(qkv.read(sum(shapes) * 4), np.float32)
+    off = 0
+    for N, ref in zip(shapes, refs):
+        assert O.normwise_rel_err(y[off:off + N], ref) <= 2e-5
+        off += N
+
+
 @pytest.mark.parametrize("i8", [False, True])
 def test_gemm_ds_gmm_prefill_chunk(E, i8):
     rng = np.random.default_rng(42)

@@ -196,3 +196,69 @@ def test_gemv_rejects_small_workspace(gpu):
     small = gpu.Workspace(256)
     with pytest.raises(gpu._lib.Q4Error, match="workspace"):
         gpu.gemv(x, wq, sc, N, K, ws=small, split=8)
+
+
+# ---------------------------------------------------------------- batched launch
+@pytest.mark.parametrize("shapes,K", [([4096, 2048, 2048], 3840),      # q, k, v of one layer
+                                      ([15360, 15360], 3840),         # gate, up
+                                      ([64, 100, 520, 8, 64], 256),   # ragged, padded panels
+                                      ([3840], 15360)])               # one entry, long K
+@pytest.mark.parametrize("xdt,ydt", [(torch.float16, torch.float16), (torch.float32, torch.float32)])
+def test_gemv_batch_vs_oracle(gpu, shapes, K, xdt, ydt):
+    rng = np.random.default_rng(sum(shapes) + K)
+    x = rng.standard_normal(K).astype(np.float16)
+    xin = x.astype(np.float32) if xdt == torch.float32 else x
+    mats, refs = [], []
+    for N in shapes:
+        q, s = synth_int4(rng, N, K)
+        wq, sc = upload_int4(q, s)
+        mats.append((wq, sc, N, None, None))
+        refs.append(O.gemv_ref(q, s, xin))
+    ys = gpu.gemv_batch(torch.from_numpy(xin).cuda(), mats, K, y_dtype=ydt)
+    tol = TOL_F16 if ydt == torch.float16 else TOL_F32
+    for y, ref in zip(ys, refs):
+        assert O.normwise_rel_err(to_np(y).astype(np.float32), ref) <= tol
+
+
+@pytest.mark.parametrize("rows", ["8", "16", "32", "64"])
+def test_gemv_batch_bit_identical_to_single_launches(gpu, rows, monkeypatch):
+    """Same rows-per-workgroup => the batched launch sums in the same order as
+    one q4_gemv per matrix (split 1): bit-identical outputs, written into one
+    buffer at the q/k/v offsets without touching the gaps."""
+    monkeypatch.setenv("Q4MI_GEMV_ROWS", rows)
+    rng = np.random.default_rng(int(rows))
+    K = 3840
+    shapes = [512, 256, 256]
+    x = torch.from_numpy(rng.standard_normal(K).astype(np.float16)).cuda()
+    out = torch.full((sum(shapes) + 64,), 7.0, dtype=torch.float16, device="cuda")
+    mats, singles, off = [], [], 0
+    for N in shapes:
+        q, s = synth_int4(rng, N, K)
+        wq, sc = upload_int4(q, s)
+        mats.append((wq, sc, N, out[off + 16: off + 16 + N], None))
+        singles.append(gpu.gemv(x, wq, sc, N, K, split=1))
+        off += N
+    gpu.gemv_batch(x, mats, K)
+    o = to_np(out).view(np.uint16)
+    off = 0
+    for N, y1 in zip(shapes, singles):
+        assert (o[off + 16: off + 16 + N] == to_np(y1).view(np.uint16)).all()
+        off += N
+    assert (to_np(out)[:16] == 7.0).all() and (to_np(out)[16 + sum(shapes):] == 7.0).all()
+
+
+def test_gemv_batch_e4m3(gpu):
+    rng = np.random.default_rng(5)
+    K = 3840
+    x = rng.standard_normal(K).astype(np.float16)
+    mats, refs = [], []
+    for N in (1024, 512):
+        q, s32 = synth_int4(rng, N, K)
+        e8, inv, _ = O.e4m3_lift(s32)
+        sc8 = torch.from_numpy(O.scales_dev(e8)).cuda()
+        wq = torch.from_numpy(O.pack_dev(q).view(np.int32)).cuda()
+        mats.append((wq, sc8, N, None, inv))
+        refs.append(O.gemv_ref(q, O.e4m3_decode(e8), x, inv=inv))
+    ys = gpu.gemv_batch(torch.from_numpy(x).cuda(), mats, K, scale_fmt=gpu.SCALE_E4M3, y_dtype=torch.float32)
+    for y, ref in zip(ys, refs):
+        assert O.normwise_rel_err(to_np(y), ref) <= TOL_F32
