@@ -375,7 +375,7 @@ def main():
         },
         "roofline": {
             "bound": "hbm",
-            "kernel": "gemv_kernel<R=32,U=8,f16 x,f16 scales,f16 y> (gate_up 30720x3840)",
+            "kernel": "gemv_kernel<f16 x, f16 scales, f16 y> (gate_up 30720x3840, 64 rows per workgroup)",
             "achieved": round(achieved, 1),
             "peak": HBM_PEAK_GBS,
             "unit": "GB/s",

@@ -20,10 +20,12 @@
 //    unit and scale of the lane is then requested at once with streaming
 //    loads, and each unit is consumed after its own wait count, so HBM sees
 //    the whole matrix requested up front and the x copy overlaps it.
-//  * Register dequant: a masked nibble pair OR 0x6400 is the fp16 pair
-//    1024 + q (or 1024 + 16q); one packed add (or fma) makes it q - 8
-//    exactly, and v_dot2_f32_f16 accumulates the exact products with the
-//    fp16 x pair in fp32. The block scale multiplies the block's sum.
+//  * Register dequant without conversions: masking a word with 0x000F000F
+//    yields two fp16 subnormals q*2^-24; with 0x00F000F0, 16q*2^-24.
+//    v_dot2_f32_f16 multiplies them by an fp16 x pair with fp32
+//    accumulation (products exact), and the offset 8 is removed once per
+//    block with the block sum staged next to x: sum (q-8) x = sum q x -
+//    8 sum x. The block scale multiplies the block's sum.
 //  * Slots reduce with xor-shuffles and then across waves through LDS, in a
 //    fixed order (deterministic).
 //  * fp32 x (the engine's residual-stream activations) takes an fp32 path:
@@ -41,7 +43,7 @@ namespace q4 {
 constexpr int GEMV_THREADS = 256;
 constexpr int GEMV_WAVES = GEMV_THREADS / 64;
 constexpr int GEMV_LDS_MAX = 64 * 1024;    // x staging cap per workgroup (bytes)
-constexpr int GEMV_TARGET_WGS = 768;       // preferred workgroup count (see plan())
+constexpr int GEMV_TARGET_WGS = 480;       // preferred workgroup count (see rows_per_group())
 constexpr int GEMV_MIN_WGS = 256;          // one per CU; below this K is split across workgroups
 // Split-K workspace layout: tickets for up to GEMV_MAX_TICKETS row groups at
 // a fixed offset 0 (so GEMVs of different shapes sharing one workspace never
@@ -51,31 +53,26 @@ constexpr size_t GEMV_TICKET_BYTES = GEMV_MAX_TICKETS * sizeof(uint32_t);
 
 __device__ inline v2h as_h2(uint32_t v) { return __builtin_bit_cast(v2h, v); }
 
-// sum_{k in block} (q_k - 8) x_k for fp16 x; xp: the block's 16 fp16 pairs.
-// Each word yields four fp16 pairs of (q - 8) without conversions: OR-ing a
-// masked nibble pair into 0x6400 gives 1024 + q (low nibbles) or 1024 + 16q
-// (high nibbles) exactly, and one packed add / fma takes that to q - 8
-// exactly. The device nibble order puts elements (2m, 2m+1) in the two
-// halves, so the x pairs are used as stored. v_dot2_f32_f16 forms the exact
-// products (q - 8) * x and accumulates in fp32. 13 VALU ops per 8 weights.
-__device__ inline float block_dot_h(const v4u u, const uint32_t* __restrict__ xp) {
-  const v2h off_lo = {(_Float16)-1032.0f, (_Float16)-1032.0f};
-  const v2h sixteenth = {(_Float16)0.0625f, (_Float16)0.0625f};
-  const v2h off_hi = {(_Float16)-72.0f, (_Float16)-72.0f};
+// sum_{k in block} (q_k - 8) x_k for fp16 x; xp: the block's 16 fp16 pairs,
+// xsum: the block's sum of x. Conversion-free dequant: masking a word with
+// 0x000F000F yields the fp16 pair q * 2^-24 (two subnormals), with
+// 0x00F000F0 the pair 16q * 2^-24; v_dot2_f32_f16 multiplies them by the x
+// pair exactly and accumulates in fp32, and the offset 8 is taken off once
+// per block with the block sum: sum (q - 8) x = sum q x - 8 sum x. The
+// device nibble order puts elements (2m, 2m+1) in the two halves, so the x
+// pairs are used as stored. 9 VALU ops per 8 weights.
+__device__ inline float block_dot_h(const v4u u, const uint32_t* __restrict__ xp, float xsum) {
   float lo = 0.0f, hi = 0.0f;
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
     const uint32_t w = u[i], w8 = w >> 8;
-    const v2h p0 = as_h2((w & 0x000F000Fu) | 0x64006400u) + off_lo;
-    const v2h p1 = as_h2((w & 0x00F000F0u) | 0x64006400u) * sixteenth + off_hi;
-    const v2h p2 = as_h2((w8 & 0x000F000Fu) | 0x64006400u) + off_lo;
-    const v2h p3 = as_h2((w8 & 0x00F000F0u) | 0x64006400u) * sixteenth + off_hi;
-    lo = __builtin_amdgcn_fdot2(p0, as_h2(xp[4 * i + 0]), lo, false);
-    hi = __builtin_amdgcn_fdot2(p1, as_h2(xp[4 * i + 1]), hi, false);
-    lo = __builtin_amdgcn_fdot2(p2, as_h2(xp[4 * i + 2]), lo, false);
-    hi = __builtin_amdgcn_fdot2(p3, as_h2(xp[4 * i + 3]), hi, false);
+    lo = __builtin_amdgcn_fdot2(as_h2(w & 0x000F000Fu), as_h2(xp[4 * i + 0]), lo, false);
+    hi = __builtin_amdgcn_fdot2(as_h2(w & 0x00F000F0u), as_h2(xp[4 * i + 1]), hi, false);
+    lo = __builtin_amdgcn_fdot2(as_h2(w8 & 0x000F000Fu), as_h2(xp[4 * i + 2]), lo, false);
+    hi = __builtin_amdgcn_fdot2(as_h2(w8 & 0x00F000F0u), as_h2(xp[4 * i + 3]), hi, false);
   }
-  return lo + hi;
+  // lo = 2^-24 sum q x over the low nibbles, hi = 2^-20 sum q x over the high ones
+  return fmaf(hi, 1048576.0f, lo * 16777216.0f) - 8.0f * xsum;
 }
 
 // Same for fp32 x; xf: the block's 32 floats in natural order. Bytes of
@@ -172,13 +169,25 @@ __device__ __forceinline__ void gemv_rows(const void* __restrict__ xv, const uin
     u[t] = ld16_nt(wb + ix * 16);
     sb[t] = load_scale<ST>(scv, ix);
   }
-  // (3) this wave's x chunks have landed; the barrier publishes every wave's
+  // (3) this wave's x chunks have landed; the barrier publishes every wave's.
+  //     For fp16 x the block sums follow the x slice in LDS.
   vmwait<2 * U>();
   __syncthreads();
-
-  // (4) dot products, unit by unit as they arrive
   const uint32_t* xs_h = smem;
   const float* xs_f = reinterpret_cast<const float*>(smem);
+  float* xsum = reinterpret_cast<float*>(smem + nv * 256);
+  if constexpr (XH) {
+    const v2h one2 = {(_Float16)1.0f, (_Float16)1.0f};
+    for (int j = tid; j < nb; j += GEMV_THREADS) {
+      float t = 0.0f;
+#pragma unroll
+      for (int i = 0; i < 16; ++i) t = __builtin_amdgcn_fdot2(as_h2(xs_h[j * 16 + i]), one2, t, false);
+      xsum[j] = t;
+    }
+    __syncthreads();
+  }
+
+  // (4) dot products, unit by unit as they arrive
   float acc = 0.0f;
   for (int j = slot;;) {
     static_for<0, U>([&](auto tc) {
@@ -189,7 +198,7 @@ __device__ __forceinline__ void gemv_rows(const void* __restrict__ xv, const uin
       const int jj = j + t * S;
       if (jj < nb) {
         float d;
-        if constexpr (XH) d = block_dot_h(u[t], xs_h + jj * 16);
+        if constexpr (XH) d = block_dot_h(u[t], xs_h + jj * 16, xsum[jj]);
         else d = block_dot_f(u[t], xs_f + jj * BLK);
         acc = fmaf(scale_value<ST>(sb[t]), d, acc);
       }
@@ -331,8 +340,11 @@ static GemvFns pick(int R, int U, int xt, int st, int yt) {
 }
 
 // Rows per workgroup R for NP padded rows: the largest R that gives
-// GEMV_TARGET_WGS workgroups, else the largest that gives one workgroup per
-// CU, else 8. Q4MI_GEMV_ROWS (8/16/32/64) overrides R for tuning sweeps.
+// GEMV_TARGET_WGS workgroups (about two per CU), else the largest that gives
+// one workgroup per CU, else 8 (measured on MI355X over the decode shapes:
+// 64 rows for gate_up and lm_head, 32 for 15360 rows, 16 for the batched
+// q/k/v, 8 for the 3840-row o and down). Q4MI_GEMV_ROWS (8/16/32/64)
+// overrides R for tuning sweeps.
 static int rows_per_group(int NP, int nblk) {
   (void)nblk;
   int R = 0;
@@ -349,24 +361,27 @@ static int rows_per_group(int NP, int nblk) {
   return R;
 }
 
-// Units in flight per lane (one batch) for nb blocks per workgroup and
-// wgs workgroups: 4 when every lane's blocks fit 4 or the grid is at most
-// two workgroups per CU, else 8. Measured on MI355X over the decode shapes:
-// more loads in flight per lane than this is slower (16 loses 5-25%).
-// Q4MI_GEMV_UNITS (4/8/16) overrides it for tuning sweeps.
-static int units_in_flight(int nb, int R, long wgs) {
+// Units in flight per lane (one batch) for nb blocks per workgroup: 8 for
+// 32- and 64-row workgroups with more than 4 blocks per lane, else 4.
+// Measured on MI355X over the decode shapes: more loads in flight per lane
+// than this is slower (16 loses 5-25%). Q4MI_GEMV_UNITS (4/8/16) overrides
+// it for tuning sweeps.
+static int units_in_flight(int nb, int R) {
   if (const char* e = getenv("Q4MI_GEMV_UNITS")) {
     int v = atoi(e);
     if (v == 4 || v == 8 || v == 16) return v;
   }
   const int per_lane = ceil_div(nb, (64 / R) * GEMV_WAVES);
-  return per_lane <= 4 || wgs <= 2 * GEMV_MIN_WGS ? 4 : 8;
+  return R >= 32 && per_lane > 4 ? 8 : 4;
 }
 
 // LDS bytes of x per block, and of the staging area for nb blocks (whole
-// 1 KB direct-load rows).
+// 1 KB direct-load rows, then the fp32 block sums for fp16 x).
 static int x_block_bytes(int x_dtype) { return x_dtype == Q4_DT_F16 ? 64 : 128; }
-static size_t x_stage_lds(int nb, int x_dtype) { return (size_t)ceil_div((long)nb * x_block_bytes(x_dtype), 1024) * 1024; }
+static size_t x_stage_lds(int nb, int x_dtype) {
+  const size_t x = (size_t)ceil_div((long)nb * x_block_bytes(x_dtype), 1024) * 1024;
+  return x_dtype == Q4_DT_F16 ? x + (size_t)ceil_div(nb, 4) * 16 : x;  // + fp32 block sums
+}
 
 struct GemvPlan {
   int R, U, split, nb_max;
@@ -393,7 +408,7 @@ static GemvPlan plan(int N, int K, int split_req, int x_dtype) {
   p.R = R;
   p.split = s;
   p.nb_max = ceil_div(nblk, s);
-  p.U = units_in_flight(p.nb_max, R, (long)wgs * s);
+  p.U = units_in_flight(p.nb_max, R);
   p.lds = x_stage_lds(p.nb_max, x_dtype);
   p.ws = 0;
   if (s > 1) p.ws = (GEMV_TICKET_BYTES + (size_t)s * NP * sizeof(float) + 255) & ~(size_t)255;
@@ -496,7 +511,7 @@ int q4_gemv_batch(const void* x, int x_dtype, int K, int scale_fmt, int y_dtype,
     segs.s[i].N = N[i];
     segs.s[i].g_end = groups;
   }
-  const int U = units_in_flight(nblk, R, groups);
+  const int U = units_in_flight(nblk, R);
   gemv_batch_fn fn = pick(R, U, x_dtype, scale_fmt, y_dtype).many;
   hipLaunchKernelGGL(fn, dim3(groups), dim3(GEMV_THREADS), x_stage_lds(nblk, x_dtype), as_stream(stream), x, nblk,
                      segs);
