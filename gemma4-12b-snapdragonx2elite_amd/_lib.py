@@ -46,6 +46,9 @@ SIGNATURES = {
     "q4_quant_act_i8": (_i, [_vp, _i, _vp, _vp, _i, _i, _vp]),
     "q4_gemm_w8a8": (_i, [_vp, _vp, _vp, _vp, _i, _vp, _vp, _i, _i, _i, _vp]),
     "q4_gemm_w4a8": (_i, [_vp, _vp, _vp, _vp, _vp, _i, _vp, _vp, _i, _i, _i, _vp]),
+    "q4_w8_packed_bytes": (_sz, [_i, _i]),
+    "q4_w8_pack": (_i, [_vp, _i, _i, _vp, _vp]),
+    "q4_gemm_w8a8_packed": (_i, [_vp, _vp, _vp, _vp, _i, _vp, _vp, _i, _i, _i, _vp]),
     "q4_cast_f32_f16": (_i, [_vp, _vp, _sz, _vp]),
     "q4_cast_f16_f32": (_i, [_vp, _vp, _sz, _vp]),
     "q4_graph_begin": (_i, [_vp]),

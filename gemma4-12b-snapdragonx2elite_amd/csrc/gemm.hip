@@ -143,14 +143,15 @@ __device__ inline void tile_of(int w, int G, int ntm, int& tm, int& tn) {
 
 constexpr int EST = 68;  // epilogue strip row stride (words): 64 columns + 4 to stagger banks
 
-// Epilogue: the wave's WM x 128 accumulator block goes through a 64-column
-// LDS strip per half (so each stored row segment is a full 128-byte line of
+// Epilogue: the wave's WM x (32 FN) accumulator block goes through a
+// 64-column LDS strip per 64 columns (so each stored row segment is a full 128-byte line of
 // f16 Y) and is stored row-contiguously, 4 columns per lane. MODE 0: int32
 // accumulators -> Y = f16((f32(C) * sa) * sw) and/or C; MODE 1: fp32 -> f16
 // Y; MODE 2: fp32 -> fp32 partials P.
-template <int MODE, int WM, class acc_t>
-__device__ inline void epilogue(const GemmArgs& g, uint32_t* strip, const acc_t (&acc)[WM / 32][4], int mw, int nw,
+template <int MODE, int WM, int FN = 4, class acc_t>
+__device__ inline void epilogue(const GemmArgs& g, uint32_t* strip, const acc_t (&acc)[WM / 32][FN], int mw, int nw,
                                 float* P) {
+  static_assert(FN == 2 || FN == 4, "64 or 128 columns per wave block");
   constexpr int FM = WM / 32, NIT = WM / 4;
   const int lane = threadIdx.x & 63;
   const int col = lane & 31, rh = (lane >> 5) * 4;
@@ -164,7 +165,7 @@ __device__ inline void epilogue(const GemmArgs& g, uint32_t* strip, const acc_t 
     for (int it = 0; it < NIT; ++it) sav[it] = g.Y ? g.sa[min(mw + 4 * it + rrow, M - 1)] : 0.0f;
   }
 #pragma unroll
-  for (int jp = 0; jp < 2; ++jp) {
+  for (int jp = 0; jp < FN / 2; ++jp) {
     const int n = nw + 64 * jp + rcol;
     float swv[4] = {0.0f, 0.0f, 0.0f, 0.0f};
     if constexpr (MODE == 0) {
@@ -231,6 +232,49 @@ __device__ inline void epilogue(const GemmArgs& g, uint32_t* strip, const acc_t 
       }
     }
     __builtin_amdgcn_wave_barrier();  // strip reads done before the next half overwrites it
+  }
+}
+
+// Epilogue of a wave's 256 x 64 int32 block that lies wholly inside Y, with
+// no int32 output: Y = f16((f32(C) * sa) * sw), the same arithmetic as
+// epilogue<0> without its bounds and output-kind branches. Four 64-row
+// chunks go through the wave's LDS strip; a chunk's scales are loaded
+// before its strip is filled.
+template <class acc_t>
+__device__ inline void epilogue_w8_full(const GemmArgs& g, uint32_t* strip, const acc_t (&acc)[8][2], int m0, int nw) {
+  const int lane = threadIdx.x & 63;
+  const int col = lane & 31, rh = (lane >> 5) * 4;
+  const int rrow = lane >> 4, rcol = (lane & 15) * 4;
+  const int N = g.N;
+  float swv[4];
+#pragma unroll
+  for (int e = 0; e < 4; ++e)
+    swv[e] = g.sw_f16 ? h2f(reinterpret_cast<const uint16_t*>(g.sw)[nw + rcol + e])
+                      : reinterpret_cast<const float*>(g.sw)[nw + rcol + e];
+#pragma unroll
+  for (int c = 0; c < 4; ++c) {
+    float sav[16];  // this chunk's row scales, loaded before the strip is filled
+#pragma unroll
+    for (int it = 0; it < 16; ++it) sav[it] = g.sa[m0 + 64 * c + 4 * it + rrow];
+#pragma unroll
+    for (int h = 0; h < 2; ++h)
+#pragma unroll
+      for (int i = 0; i < 2; ++i) store_tile_strip(strip + (32 * i + rh) * EST + 32 * h + col, EST, acc[2 * c + i][h]);
+    lgkm0();
+    __builtin_amdgcn_wave_barrier();
+#pragma unroll
+    for (int it = 0; it < 16; ++it) {
+      const int row = 4 * it + rrow;
+      const v4u q = *reinterpret_cast<const v4u*>(strip + row * EST + rcol);
+      uint32_t qv[4];
+      __builtin_memcpy(qv, &q, sizeof(qv));
+      uint16_t hv[4];
+#pragma unroll
+      for (int e = 0; e < 4; ++e) hv[e] = f2h_after_f32(__fmul_rn(__fmul_rn((float)(int)qv[e], sav[it]), swv[e]));
+      *reinterpret_cast<ushort4*>(g.Y + (long)(m0 + 64 * c + row) * N + nw + rcol) =
+          make_ushort4(hv[0], hv[1], hv[2], hv[3]);
+    }
+    __builtin_amdgcn_wave_barrier();  // strip reads done before the next chunk overwrites it
   }
 }
 
@@ -399,6 +443,232 @@ __global__ void __launch_bounds__(256) w8a8_kernel(const GemmArgs g) {
 
   uint32_t* strip = reinterpret_cast<uint32_t*>(wave < 2 ? ldsA : ldsB) + (wave & 1) * (WM * EST);
   epilogue<0, WM>(g, strip, acc, m0 + wm * WM, n0 + wn * WN, nullptr);
+}
+
+// ---- W8A8 on packed weights ----------------------------------------------------
+// Packed ("tile-32") int8 weights: rows padded to a multiple of 32 and K to
+// a multiple of 128 (Kp), padding zero; the 32 x 32-byte block of n-tile t
+// (rows 32t .. 32t+31) and k-slice s (bytes 32s .. 32s+31) is 1 KB at byte
+// (t * (Kp/32) + s) * 1024, and lane l of a wave finds its
+// v_mfma_i32_32x32x32_i8 B operand (row 32t + l % 32, bytes
+// 32s + 16 (l / 32) .. +16) at byte 16 l of the block. A wave fetches one B
+// fragment as 1 KB of contiguous HBM/L2 straight into registers.
+__host__ __device__ inline int w8p_kpad(int K) { return (K + 127) / 128 * 128; }
+// Position XOR of the 16-byte chunks of staged A row r (128-byte rows): rows
+// r .. r+7 (r % 8 == 0) get distinct values, and so do the even and the odd
+// rows of any 16 (r % 16 == 0), so a ds_read_b128 of one chunk index over
+// 32 consecutive rows is bank-conflict-free whether the LDS serves 8 lanes
+// (32 banks) or 16 lanes (64 banks) per cycle: with 128-byte rows, 64 banks
+// see rows r and r + 2 at the same bank offset.
+__device__ inline int w8p_swz(int r) { return (r & 7) ^ ((r >> 3) & 1); }
+__host__ __device__ inline long w8p_block(int t, int s, int kslices) { return ((long)t * kslices + s) * 1024; }
+
+// W8 [N][K] -> packed. One thread per 16-byte chunk; padding is zero.
+__global__ void __launch_bounds__(256) w8_pack_kernel(const int8_t* __restrict__ W8, int N, int K,
+                                                      int8_t* __restrict__ out, long chunks) {
+  const long c = (long)blockIdx.x * 256 + threadIdx.x;
+  if (c >= chunks) return;
+  const int ks = w8p_kpad(K) / 32;
+  const long b = c >> 6;
+  const int l = (int)(c & 63);
+  const int t = (int)(b / ks), sl = (int)(b % ks);
+  const int row = 32 * t + (l & 31);
+  const long k0 = 32L * sl + 16 * (l >> 5);
+  v4u v = {0u, 0u, 0u, 0u};
+  if (row < N && k0 < K) v = *reinterpret_cast<const v4u*>(W8 + (long)row * K + k0);
+  *reinterpret_cast<v4u*>(out + c * 16) = v;
+}
+
+// BM x 256 tile, K step 128 bytes (4 k-slices of 32). Wave w owns columns
+// n0 + 64w .. +64 and all BM rows: (BM/32) x 2 MFMA tiles, BM/32 * 2 * 16
+// accumulators. A: S = 4 stage LDS ring of direct loads (BM rows x 128 B,
+// 16-byte chunks XOR-swizzled by w8p_swz(row)); B: each lane's fragments of the wave's
+// two n-tiles for one k-step (8 x 16 B) are loaded two k-steps ahead into a
+// 3-set register ring. Per k-step kt:
+//   top:      B(kt+2) loads, A(kt+2) direct loads (into the stage k-step kt-2 used)
+//   slice 0:  read A slice 1 | MFMAs of slice 0
+//   slice 1:  read A slice 2 | MFMAs of slice 1
+//   wait for B(kt+1), A(kt+1) (vmcnt: 16 loads of k-step kt+2 may be in flight); barrier
+//   slice 2:  read A slice 3 | MFMAs of slice 2
+//   slice 3:  read A slice 0 of k-step kt+1 | MFMAs of slice 3
+// The stage written at the top of k-step kt was last read in k-step kt-2,
+// before the barrier of k-step kt-1. When K % 128 == 64 the packed weights
+// of the last k-step's two missing slices are zero, so the (clamped, stale)
+// activation chunks there add nothing: every k-step runs all four slices.
+template <int BM, bool TAIL>
+__global__ void __launch_bounds__(256) w8p_kernel(const GemmArgs g) {
+  constexpr int S = 4, FM = BM / 32, FN = 2;
+  constexpr int AST = BM * 128;        // bytes per A stage
+  constexpr int NA = BM / 32;          // A direct loads per wave per k-step (8 rows of 128 B each)
+  constexpr int NB = FN * 4;           // B loads per lane per k-step
+  constexpr int EPI = 4 * 64 * EST * 4;  // four waves' epilogue strips (64 rows each)
+  __shared__ __attribute__((aligned(16))) uint8_t ldsA[S * AST > EPI ? S * AST : EPI];
+
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int M = g.M, N = g.N, K = g.K;
+  int tm, tn;
+  tile_of(blockIdx.x, gridDim.x, (M + BM - 1) / BM, tm, tn);
+  const int m0 = tm * BM, n0 = tn * 256;
+  const int ks = w8p_kpad(K) / 32;     // k-slices of the packed weights
+  const int nk = ks / 4;               // k-steps
+
+  // A: wave instruction i stages rows (wave * NA + i) * 8 .. +8; lane -> row r = row0 + lane / 8,
+  // LDS position lane % 8 of row r holds chunk (lane % 8) ^ w8p_swz(r). Byte offsets from A
+  // are 32-bit (the entry point checks M * K < 2^31).
+  int chunk[2];  // chunk byte offset for even / odd i (bit 3 of the row)
+#pragma unroll
+  for (int e = 0; e < 2; ++e) chunk[e] = ((lane & 7) ^ ((lane >> 3) & 7) ^ e) << 4;
+  uint32_t aoff[NA];
+#pragma unroll
+  for (int i = 0; i < NA; ++i)
+    aoff[i] = (uint32_t)(min(m0 + (wave * NA + i) * 8 + (lane >> 3), M - 1) * K + chunk[(wave * NA + i) & 1]);
+  // B: n-tiles (n0 + 64 wave) / 32 + j of the packed weights (32-bit offsets: the
+  // entry point checks the packed size < 2^31)
+  const int ntiles = (N + 31) / 32;
+  uint32_t boff[FN];
+#pragma unroll
+  for (int j = 0; j < FN; ++j) boff[j] = (uint32_t)(w8p_block(min((n0 + 64 * wave) / 32 + j, ntiles - 1), 0, ks) + 16 * lane);
+  const uint8_t* Ab = reinterpret_cast<const uint8_t*>(g.A);
+  const uint8_t* Bb = reinterpret_cast<const uint8_t*>(g.B);
+
+  v4i rb[3][FN][4];
+  // VMEM operation o (0 .. NB + NA - 1) of a k-step: o < NB loads B fragment
+  // (slice o / FN, n-tile o % FN) of k-step kl into register set SETL; the
+  // next NA are the direct loads of k-step kl's A rows into stage kst % 4.
+  auto vmem_op = [&](auto oc, auto setlc, int kl, int kst) {
+    constexpr int o = decltype(oc)::value, setl = decltype(setlc)::value;
+    if constexpr (o < NB) {
+      constexpr int q = o / FN, j = o % FN;
+      rb[setl][j][q] = __builtin_bit_cast(v4i, ld16_so(Bb + (long)min(kl * 4 + q, ks - 1) * 1024, boff[j]));
+    } else if constexpr (o < NB + NA) {
+      constexpr int i = o - NB;
+      uint8_t* st = ldsA + (kst & 3) * AST + (wave * NA + i) * 1024;
+      if constexpr (TAIL) {  // chunk offsets clamped inside the row (a two-slice last k-step)
+        const int c = chunk[(wave * NA + i) & 1];
+        dma16_so(Ab, aoff[i] + (min(kl * 128 + c, K - 16) - c), st);
+      } else {
+        dma16_so(Ab + (long)kl * 128, aoff[i], st);
+      }
+    }
+  };
+
+  v16i acc[FM][FN];
+#pragma unroll
+  for (int i = 0; i < FM; ++i)
+#pragma unroll
+    for (int j = 0; j < FN; ++j) acc[i][j] = v16i{};
+
+  const int frow = lane & 31, fh = lane >> 5;
+  // A fragment of m-tile i, k-slice q (0..3) from stage st: row 32 i + lane % 32,
+  // chunk 2 q + lane / 32, found at position chunk ^ w8p_swz(row)
+  auto rdA = [&](int st, int i, int q) {
+    const int r = 32 * i + frow;
+    return *reinterpret_cast<const v4i*>(ldsA + st * AST + r * 128 + (((2 * q + fh) ^ w8p_swz(r)) << 4));
+  };
+  v4i fa[2][FM];
+
+  // prologue: A0, B0, A1, B1; wait for A0, B0; read slice 0 of stage 0
+  using I0 = std::integral_constant<int, 0>;
+  using I1 = std::integral_constant<int, 1>;
+  using I2 = std::integral_constant<int, 2>;
+  auto load_kstep = [&](auto setc, int kl, int kst) {  // A rows first, then the B fragments
+    static_for<NB, NB + NA>([&](auto oc) { vmem_op(oc, setc, kl, kst); });
+    static_for<0, NB>([&](auto oc) { vmem_op(oc, setc, kl, kst); });
+  };
+  load_kstep(I0{}, 0, 0);
+  load_kstep(I1{}, min(1, nk - 1), 1);
+  vmwait<NA + NB>();
+#pragma unroll
+  for (int j = 0; j < FN; ++j)
+#pragma unroll
+    for (int q = 0; q < 4; ++q) pin(rb[0][j][q]);
+  __syncthreads();
+#pragma unroll
+  for (int i = 0; i < FM; ++i) fa[0][i] = rdA(0, i, 0);
+
+  // One k-step: 4 slices of 4 groups; group g of slice q reads two fragments
+  // of the next slice, runs the MFMAs of m-tiles 2g, 2g+1 and issues VMEM
+  // operation 4q + g of k-step kt+2 (so the 16 loads of a k-step are spread
+  // over its MFMAs instead of queueing at the texture unit together). B(kt+2)
+  // goes out in slices 0-1 and A(kt+2) in slices 2-3, so at the start of
+  // slice 2 exactly the NB loads of B(kt+2) may still be in flight after
+  // A(kt+1): vmcnt(NB), then the barrier publishes A(kt+1) before slice 3
+  // reads its first fragments.
+  static_assert(NB == 8 && NB + NA <= 16 && FM % 4 == 0, "one VMEM operation per group");
+  int kt = 0;
+  auto kstep = [&](auto setc, auto setnc, auto setlc) {
+    constexpr int set = decltype(setc)::value, setn = decltype(setnc)::value;
+    const int st = kt & 3, stn = (kt + 1) & 3;
+    const int kl = min(kt + 2, nk - 1);
+    static_for<0, 4>([&](auto qc) {
+      constexpr int q = decltype(qc)::value, cb = q & 1, nbuf = cb ^ 1;
+      if constexpr (q == 2) {
+        vmwait<NB>();  // B(kt+1), A(kt+1) landed in this wave
+#pragma unroll
+        for (int j = 0; j < FN; ++j)
+#pragma unroll
+          for (int qq = 0; qq < 4; ++qq) pin(rb[setn][j][qq]);
+        __syncthreads();  // ... and in every wave
+      }
+      static_for<0, 4>([&](auto gc) {
+        constexpr int g = decltype(gc)::value;
+        constexpr int i0 = g * (FM / 4);
+#pragma unroll
+        for (int ii = i0; ii < i0 + FM / 4; ++ii) fa[nbuf][ii] = q < 3 ? rdA(st, ii, q + 1) : rdA(stn, ii, 0);
+#pragma unroll
+        for (int ii = i0; ii < i0 + FM / 4; ++ii)
+#pragma unroll
+          for (int j = 0; j < FN; ++j)
+            acc[ii][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(fa[cb][ii], rb[set][j][q], acc[ii][j], 0, 0, 0);
+#pragma unroll
+        for (int r = 0; r < FM / 4; ++r) {
+          __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+          __builtin_amdgcn_sched_group_barrier(0x008, FN, 0);
+        }
+        vmem_op(std::integral_constant<int, 4 * q + g>{}, setlc, kl, kt + 2);
+        __builtin_amdgcn_sched_barrier(0);
+      });
+    });
+  };
+  // B register sets rotate with period 3: B(kt) lives in set kt % 3
+  for (; kt + 2 < nk; kt += 3) {
+    kstep(I0{}, I1{}, I2{});
+    ++kt;
+    kstep(I1{}, I2{}, I0{});
+    ++kt;
+    kstep(I2{}, I0{}, I1{});
+    kt -= 2;
+  }
+  if (kt < nk) {
+    kstep(I0{}, I1{}, I2{});
+    ++kt;
+    if (kt < nk) kstep(I1{}, I2{}, I0{});
+  }
+  vmwait<0>();
+  // the last k-steps' B loads (clamped, never used) must land before their
+  // registers can be reused by the epilogue
+#pragma unroll
+  for (int s = 0; s < 3; ++s)
+#pragma unroll
+    for (int j = 0; j < FN; ++j)
+#pragma unroll
+      for (int q = 0; q < 4; ++q) pin(rb[s][j][q]);
+  __syncthreads();  // every direct load landed and every fragment read before the strips reuse LDS
+
+  uint32_t* strip = reinterpret_cast<uint32_t*>(ldsA) + wave * (64 * EST);
+  if constexpr (BM == 256) {
+    // a tile wholly inside Y (N % 4 == 0 keeps the 8-byte stores aligned), Y only
+    if (m0 + BM <= M && n0 + 256 <= N && !g.C && g.Y && (N & 3) == 0) {
+      epilogue_w8_full(g, strip, acc, m0, n0 + 64 * wave);
+      return;
+    }
+  }
+#pragma unroll
+  for (int c = 0; c < FM / 2; ++c) {
+    // by value: a reference into acc would take its address and put it in scratch
+    const v16i sub[2][FN] = {{acc[2 * c][0], acc[2 * c][1]}, {acc[2 * c + 1][0], acc[2 * c + 1][1]}};
+    epilogue<0, 64, FN>(g, strip, sub, m0 + 64 * c, n0 + 64 * wave, nullptr);
+  }
 }
 
 // ---- W4A16 / W4A8 ---------------------------------------------------------------
@@ -717,6 +987,49 @@ int q4_gemm_w8a8(const int8_t* A, const int8_t* W8, const float* sa, const void*
   else
     hipLaunchKernelGGL(w8a8_kernel<128>, dim3(tiles(M, N, 128)), dim3(256), 0, as_stream(stream), g);
   Q4_LAUNCHED("gemm_w8a8");
+  return Q4_OK;
+}
+
+size_t q4_w8_packed_bytes(int N, int K) {
+  if (N <= 0 || K <= 0 || K % 32) return 0;
+  return (size_t)ceil_div(N, 32) * 32 * w8p_kpad(K);
+}
+
+int q4_w8_pack(const int8_t* W8, int N, int K, int8_t* W8p, void* stream) {
+  clear_error();
+  Q4_ARG(N > 0 && K > 0 && K % 32 == 0, "bad W8 shape N=%d K=%d (K must be a multiple of 32)", N, K);
+  Q4_ARG(W8 && W8p, "null pointer");
+  Q4_ARG(((uintptr_t)W8 & 15) == 0 && ((uintptr_t)W8p & 15) == 0, "W8 and W8p must be 16-byte aligned");
+  const long chunks = (long)q4_w8_packed_bytes(N, K) / 16;
+  hipLaunchKernelGGL(w8_pack_kernel, dim3(ceil_div(chunks, 256)), dim3(256), 0, as_stream(stream), W8, N, K, W8p,
+                     chunks);
+  Q4_LAUNCHED("w8_pack");
+  return Q4_OK;
+}
+
+int q4_gemm_w8a8_packed(const int8_t* A, const int8_t* W8p, const float* sa, const void* sw, int sw_dtype,
+                        uint16_t* Y, int32_t* C, int M, int N, int K, void* stream) {
+  clear_error();
+  Q4_ARG(M > 0 && N > 0 && K > 0 && K % 64 == 0, "bad W8A8 shape M=%d N=%d K=%d (K must be a multiple of 64)", M, N,
+         K);
+  Q4_ARG((long)127 * 127 * K < (1L << 31), "K=%d overflows the int32 accumulator", K);
+  Q4_ARG(A && W8p && (Y || C), "null pointer");
+  Q4_ARG(!Y || (sa && sw), "Y needs sa and sw");
+  Q4_ARG(sw_dtype == Q4_DT_F32 || sw_dtype == Q4_DT_F16, "bad sw dtype %d", sw_dtype);
+  Q4_ARG(((uintptr_t)A & 15) == 0 && ((uintptr_t)W8p & 15) == 0, "A and W8p must be 16-byte aligned");
+  Q4_ARG((long)M * K < (1L << 31) && (long)q4_w8_packed_bytes(N, K) < (1L << 31),
+         "packed W8A8 needs M*K and the packed weights under 2 GiB (32-bit offsets)");
+  GemmArgs g{A, W8p, nullptr, sa, sw, sw_dtype == Q4_DT_F16, Y, C, nullptr, M, N, K};
+  const bool tail = K % 128 != 0;
+  const hipStream_t st = as_stream(stream);
+  if (pick_bm(M, N) == 256) {
+    if (tail) hipLaunchKernelGGL((w8p_kernel<256, true>), dim3(tiles(M, N, 256)), dim3(256), 0, st, g);
+    else hipLaunchKernelGGL((w8p_kernel<256, false>), dim3(tiles(M, N, 256)), dim3(256), 0, st, g);
+  } else {
+    if (tail) hipLaunchKernelGGL((w8p_kernel<128, true>), dim3(tiles(M, N, 128)), dim3(256), 0, st, g);
+    else hipLaunchKernelGGL((w8p_kernel<128, false>), dim3(tiles(M, N, 128)), dim3(256), 0, st, g);
+  }
+  Q4_LAUNCHED("gemm_w8a8_packed");
   return Q4_OK;
 }
 

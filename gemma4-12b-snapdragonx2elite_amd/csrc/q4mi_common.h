@@ -129,6 +129,19 @@ __device__ inline uint32_t ld1(const void* p) {
   asm volatile("global_load_ubyte %0, %1, off" : "=v"(r) : "v"(p));
   return r;
 }
+// Uniform base (SGPR pair) + per-lane 32-bit byte offset: one VGPR per
+// address instead of two.
+__device__ inline v4u ld16_so(const void* sbase, uint32_t voff) {
+  v4u r;
+  asm volatile("global_load_dwordx4 %0, %1, %2" : "=v"(r) : "v"(voff), "s"(sbase));
+  return r;
+}
+// Direct-to-LDS load at uniform base + per-lane offset (lds_dst as dma16).
+__device__ inline void dma16_so(const void* sbase, uint32_t voff, const void* lds_dst) {
+  const unsigned l = __builtin_amdgcn_readfirstlane((unsigned)(uintptr_t)lds_dst);
+  asm volatile("s_mov_b32 m0, %2\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, %1" ::"v"(voff), "s"(sbase), "s"(l)
+               : "memory");
+}
 // Streaming (non-temporal) variants for data read exactly once.
 __device__ inline v4u ld16_nt(const void* p) {
   v4u r;

@@ -297,6 +297,32 @@ def gemm_w8a8(A: torch.Tensor, W8: torch.Tensor, sa: torch.Tensor, sw: torch.Ten
     return (Y, Cm) if want_c else Y
 
 
+def w8_pack(W8: torch.Tensor) -> torch.Tensor:
+    """int8 W8 [N, K] -> the packed layout of :func:`gemm_w8a8_packed` (flat int8)."""
+    if W8.dtype != torch.int8 or W8.dim() != 2:
+        raise ValueError("w8_pack expects int8 W8 [N, K]")
+    N, K = W8.shape
+    out = torch.empty(int(lib().q4_w8_packed_bytes(N, K)), dtype=torch.int8, device=W8.device)
+    call("q4_w8_pack", _p(W8.contiguous()), N, K, _p(out), _stream())
+    return out
+
+
+def gemm_w8a8_packed(A: torch.Tensor, W8p: torch.Tensor, sa: torch.Tensor, sw: torch.Tensor, N: int, *,
+                     want_c: bool = False, Y: torch.Tensor | None = None):
+    """W8A8 on packed weights (:func:`w8_pack`); same results as :func:`gemm_w8a8`."""
+    M, K = A.shape
+    if A.dtype != torch.int8 or W8p.dtype != torch.int8:
+        raise ValueError("gemm_w8a8_packed expects int8 A [M, K] and packed int8 weights")
+    _need(W8p, int(lib().q4_w8_packed_bytes(N, K)), "packed W8")
+    _need(sa, M * 4, "sa")
+    _need(sw, N * sw.element_size(), "sw")
+    Y = torch.empty((M, N), dtype=torch.float16, device=A.device) if Y is None else Y
+    _need(Y, M * N * 2, "Y")
+    Cm = torch.empty((M, N), dtype=torch.int32, device=A.device) if want_c else None
+    call("q4_gemm_w8a8_packed", _p(A), _p(W8p), _p(sa), _p(sw), _dt(sw), _p(Y), _p(Cm), M, N, K, _stream())
+    return (Y, Cm) if want_c else Y
+
+
 def gemm_w4a8(A: torch.Tensor, wq: torch.Tensor, ratio: torch.Tensor, sa: torch.Tensor, sw: torch.Tensor, N: int, *,
               want_c: bool = False, Y: torch.Tensor | None = None):
     M, K = A.shape

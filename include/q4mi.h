@@ -180,6 +180,20 @@ int q4_gemm_w8a8(const int8_t* A, const int8_t* W8, const float* sa,
                  const void* sw, int sw_dtype, uint16_t* Y, int32_t* C, int M,
                  int N, int K, void* stream);
 
+/* The same W8A8 product on packed weights: the layout the int8 MFMA reads
+ * one 1 KB fragment at a time (rows padded to a multiple of 32 and K to a
+ * multiple of 128, Kp; the block of rows 32t..32t+31 and K bytes
+ * 32s..32s+31 is 1 KB at (t*(Kp/32) + s)*1024, lane l's 16 bytes at 16*l:
+ * row 32t + l%32, bytes 32s + 16*(l/32)). q4_w8_pack converts W8 [N][K]
+ * once at load time (q4_w8_packed_bytes bytes, padding zero).
+ * Bit-identical results to q4_gemm_w8a8.
+ * vk/coopgemm_w8a8.comp:18-37 (weights as folded at src/vk_engine.py:152-157). */
+size_t q4_w8_packed_bytes(int N, int K);
+int q4_w8_pack(const int8_t* W8, int N, int K, int8_t* W8p, void* stream);
+int q4_gemm_w8a8_packed(const int8_t* A, const int8_t* W8p, const float* sa,
+                        const void* sw, int sw_dtype, uint16_t* Y,
+                        int32_t* C, int M, int N, int K, void* stream);
+
 /* W4A8: as W8A8 with B = int8(clamp(rint((q-8) * ratio[n,b]), -127, 127))
  * formed on the fly from the int4 codes and the panel-64 fp16 ratio.
  * vk/coopgemm_w4a8.comp:21-50. */

@@ -225,6 +225,33 @@ def unscales_dev(flat: np.ndarray, N: int, nblk: int) -> np.ndarray:
     return np.ascontiguousarray(np.asarray(flat).reshape(NP // PANEL, nblk, PANEL).transpose(0, 2, 1)).reshape(NP, nblk)[:N]
 
 
+def pack_w8_dev(W8: np.ndarray) -> np.ndarray:
+    """int8 ``W8[N, K]`` -> the packed W8A8 layout of this build (flat int8).
+
+    Rows padded to a multiple of 32 and K to a multiple of 128 (``Kp``), the
+    padding zero. The 32 x 32-byte block of n-tile ``t`` (rows ``32t ..
+    32t+31``) and k-slice ``s`` (bytes ``32s .. 32s+31``) is 1 KB at byte
+    ``(t * Kp/32 + s) * 1024``; its 16-byte chunk ``l`` (0..63) holds row
+    ``32t + l % 32``, bytes ``32s + 16 (l // 32) .. +16``.
+    """
+    W8 = np.asarray(W8, dtype=np.int8)
+    N, K = W8.shape
+    if K % 32:
+        raise ValueError(f"K={K} is not a multiple of 32")
+    NP, Kp = -(-N // 32) * 32, -(-K // 128) * 128
+    Wp = np.zeros((NP, Kp), np.int8)
+    Wp[:N, :K] = W8
+    t = Wp.reshape(NP // 32, 32, Kp // 32, 2, 16)          # t, r, s, h, byte
+    return np.ascontiguousarray(t.transpose(0, 2, 3, 1, 4)).reshape(-1)   # t, s, h, r, byte
+
+
+def unpack_w8_dev(flat: np.ndarray, N: int, K: int) -> np.ndarray:
+    """Inverse of :func:`pack_w8_dev` (drops the padding)."""
+    NP, Kp = -(-N // 32) * 32, -(-K // 128) * 128
+    t = np.asarray(flat, dtype=np.int8).reshape(NP // 32, Kp // 32, 2, 32, 16)   # t, s, h, r, byte
+    return np.ascontiguousarray(t.transpose(0, 3, 1, 2, 4)).reshape(NP, Kp)[:N, :K]
+
+
 # --------------------------------------------------------------------------
 # dequant + matmul references (the reference's own numpy checks)
 # --------------------------------------------------------------------------

@@ -75,6 +75,54 @@ def test_w8a8_config_size_rows(gpu):
     assert (to_np(gY).view(np.uint16) == Y.view(np.uint16)).all()
 
 
+# ------------------------------------------------------ W8A8, packed weights
+@pytest.mark.parametrize("N,K", [(256, 64), (300, 192), (15360, 3840), (40, 320)])
+def test_w8_pack_layout(gpu, N, K):
+    rng = np.random.default_rng(N + K)
+    W8 = rng.integers(-127, 128, (N, K), dtype=np.int8)
+    got = to_np(gpu.w8_pack(torch.from_numpy(W8).cuda()))
+    assert (got == O.pack_w8_dev(W8)).all()
+
+
+@pytest.mark.parametrize("M,N,K", [(64, 256, 64), (100, 320, 128), (70, 300, 192), (256, 512, 3840),
+                                   (128, 15360, 3840), (300, 3840, 15360), (1024, 2048, 320), (520, 600, 4096)])
+@pytest.mark.parametrize("swdt", [np.float32, np.float16])
+def test_w8a8_packed_bit_exact(gpu, M, N, K, swdt):
+    """Same cases as the [N][K] kernel (K % 128 == 64 included: the last k-step
+    then runs on zero-padded weights), plus bit-identity with that kernel."""
+    rng = np.random.default_rng(M * 3 + N + K)
+    A, sa, W8, sw = _w8a8_case(rng, M, N, K)
+    sw_used = sw.astype(swdt)
+    C, Y = O.gemm_w8a8_ref(A, W8, sa, sw_used.astype(np.float32))
+    gA, gsa, gsw = torch.from_numpy(A).cuda(), torch.from_numpy(sa).cuda(), torch.from_numpy(sw_used).cuda()
+    W8p = torch.from_numpy(O.pack_w8_dev(W8)).cuda()
+    gY, gC = gpu.gemm_w8a8_packed(gA, W8p, gsa, gsw, N, want_c=True)
+    assert (to_np(gC) == C).all()
+    assert (to_np(gY).view(np.uint16) == Y.view(np.uint16)).all()
+    gY2 = gpu.gemm_w8a8(gA, torch.from_numpy(W8).cuda(), gsa, gsw)
+    assert (to_np(gY2).view(np.uint16) == to_np(gY).view(np.uint16)).all()
+
+
+def test_w8a8_packed_config_size_rows(gpu):
+    """M=2048, N=15360, K=3840 on packed weights packed on the GPU: 96 rows of
+    the int32 accumulator vs the oracle, every fp16 output vs the oracle's
+    epilogue of the accumulator."""
+    rng = np.random.default_rng(0)
+    M, N, K = 2048, 15360, 3840
+    codes = rng.integers(-8, 8, (N, K))
+    s = np.abs(rng.normal(0, 0.02, (N, K // 32))).astype(np.float16).astype(np.float32)
+    W8, sw = O.w8_fold((codes + 8).astype(np.uint8), s)
+    X = rng.standard_normal((M, K)).astype(np.float16)
+    A, sa = O.quant_act_i8(X)
+    gA, gsa = gpu.quant_act_i8(torch.from_numpy(X).cuda())
+    W8p = gpu.w8_pack(torch.from_numpy(W8).cuda())
+    gY, gC = gpu.gemm_w8a8_packed(gA, W8p, gsa, torch.from_numpy(sw).cuda(), N, want_c=True)
+    rows = np.sort(rng.choice(M, 96, replace=False))
+    assert (to_np(gC[torch.from_numpy(rows).cuda()]) == O.int_matmul_exact(A[rows], W8)).all()
+    Y = O.w8a8_epilogue(to_np(gC), sa, sw)
+    assert (to_np(gY).view(np.uint16) == Y.view(np.uint16)).all()
+
+
 # ------------------------------------------------------------------ W4A8
 @pytest.mark.parametrize("M,N,K", [(64, 256, 64), (100, 512, 3840), (33, 300, 320), (128, 15360, 3840)])
 def test_w4a8_bit_exact(gpu, M, N, K):

@@ -101,6 +101,27 @@ def test_pack_dev_roundtrip_random():
     assert (O.unscales_dev(O.scales_dev(s), 100, 3) == s).all()
 
 
+def test_pack_w8_dev_known_positions():
+    """Chunk l of block (t, s) = row 32t + l % 32, bytes 32s + 16 (l // 32) .. +16."""
+    N, K = 70, 192                                  # 3 n-tiles (last padded), K padded to 256
+    W8 = np.zeros((N, K), np.int8)
+    W8[33, 2 * 32 + 16 + 5] = 7                     # t=1, r=1, s=2, h=1, byte 5
+    W8[69, 191] = -3                                # t=2, r=5, s=5, h=1, byte 15
+    flat = O.pack_w8_dev(W8)
+    kp = 256 // 32
+    assert flat.size == 96 * 256
+    assert flat[(1 * kp + 2) * 1024 + (32 + 1) * 16 + 5] == 7
+    assert flat[(2 * kp + 5) * 1024 + (32 + 5) * 16 + 15] == -3
+    assert np.count_nonzero(flat) == 2              # padding (rows 70..95, bytes 192..255) is zero
+
+
+def test_pack_w8_dev_roundtrip_random():
+    rng = np.random.default_rng(5)
+    for N, K in [(64, 128), (100, 320), (32, 3840)]:
+        W8 = rng.integers(-127, 128, (N, K), dtype=np.int8)
+        assert (O.unpack_w8_dev(O.pack_w8_dev(W8), N, K) == W8).all()
+
+
 def test_scales_f16_ref_layout():
     sc = np.array([[1.0, 2.0], [3.0, 4.0], [5.0, 6.0]], np.float32)  # [N=3, nblk=2]
     assert O.scales_f16_ref(sc).tolist() == [[1.0, 3.0, 5.0], [2.0, 4.0, 6.0]]
