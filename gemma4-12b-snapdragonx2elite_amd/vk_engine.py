@@ -115,7 +115,10 @@ def quant(W, pf: bool = True, fp8: bool | None = None, prefill_i8: bool | None =
     w8 = sw8 = None
     if prefill_i8 and pf:
         W8, _sw32, sw16 = ops.w8_fold(wq, sc32, N, K)
-        w8, sw8 = Buf(tensor=W8), Buf(tensor=sw16)
+        # int8 weights kept in the packed layout the W8A8 kernel reads (the
+        # reference keeps Wi8T [K, N], src/vk_engine.py:155)
+        w8, sw8 = Buf(tensor=ops.w8_pack(W8)), Buf(tensor=sw16)
+        del W8
     return QW(Buf(tensor=wq), bs, split, nblk, float(inv), bs16, w8, sw8)
 
 
@@ -206,10 +209,10 @@ def gemm_ds(qw, inbuf: Buf, outbuf: Buf, prefill_i8: bool | None = None):
             raise ValueError("PREFILL_I8 needs int8 weights: quantize with pf=True and prefill_i8=True")
         a8 = _stage("Ai8", MC * max(N, K)).view(torch.int8, MC * K).view(MC, K)
         sa = _stage("SAb", MC * 4).view(torch.float32, MC)
-        W8 = w8.t.view(N, K)
+        W8p = w8.t
         sw = sw8.t
         cin = ("quant_act_i8", xin, a8, sa)
-        gem = ("w8a8", a8, W8, sa, sw, y16)
+        gem = ("w8a8", a8, W8p, sa, sw, y16, N)
     else:
         x16 = _stage("Xf16", MC * max(N, K) * 2).view(torch.float16, MC * K).view(MC, K)
         cin = ("cast_dn", xin, x16)
@@ -229,7 +232,7 @@ def _run(op):
     elif kind == "quant_act_i8":
         ops.quant_act_i8(op[1], op[2], op[3])
     elif kind == "w8a8":
-        ops.gemm_w8a8(op[1], op[2], op[3], op[4], Y=op[5])
+        ops.gemm_w8a8_packed(op[1], op[2], op[3], op[4], op[6], Y=op[5])
     elif kind == "w4a16":
         ops.gemm_w4a16(op[1], op[2], op[3], op[4], Y=op[5], ws=op[6])
     else:
