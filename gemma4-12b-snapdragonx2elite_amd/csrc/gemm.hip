@@ -671,6 +671,231 @@ __global__ void __launch_bounds__(256) w8p_kernel(const GemmArgs g) {
   }
 }
 
+// ---- W4A16, waves split along N -------------------------------------------------
+// BM x 256 tile, K step 64 (128 bytes of f16 A = two int4 blocks). Wave w owns
+// columns n0 + 64w .. +64 and all BM rows: (BM/32) x 2 tiles of
+// v_mfma_f32_32x32x16_f16, fp32 accumulate. A: 4-stage LDS ring of direct
+// loads (128-byte rows, chunks swizzled by w8p_swz). B: each lane's
+// half-units (8 bytes: words 2h, 2h+1 of the unit of its row and block,
+// h = lane / 32) and block scales for the wave's 2 n-tiles x 2 blocks are
+// loaded two k-steps ahead into a 3-set register ring and dequantized to f16
+// fragments slice by slice (f16((q - 8) * s), one RNE multiply, as
+// vk/coopgemm_i4h.comp:24). In k-slice q = 2bb + s (block bb of the k-step)
+// lane half h multiplies A chunk 4bb + 2h + s (k = 32bb + 16h + 8s .. +8 of
+// the step) by word 2h + s of its unit, the same k: the k order inside an
+// MFMA is permuted identically for A and B. The schedule is w8p_kernel's:
+// one VMEM operation per group of MFMAs (B(kt+2) in slices 0-1, A(kt+2) in
+// slices 2-3), vmcnt(NB) + barrier at the start of slice 2. An odd block
+// count leaves a last k-step with one block: the other block's scales read
+// as zero, and its (clamped, stale) A chunks add nothing. With split > 1,
+// blockIdx.y selects a contiguous range of k-steps and fp32 partials go to P.
+template <int BM, bool TAIL>
+__global__ void __launch_bounds__(256) w4p_kernel(const GemmArgs g, int split) {
+  constexpr int S = 4, FM = BM / 32, FN = 2;
+  constexpr int AST = BM * 128;      // bytes per A stage
+  constexpr int NA = BM / 32;        // A direct loads per wave per k-step
+  constexpr int NB = FN * 2 * 2;     // B loads per lane per k-step: n-tile x block x (half-unit, scale)
+  constexpr int EPI = 4 * 64 * EST * 4;
+  __shared__ __attribute__((aligned(16))) uint8_t ldsA[S * AST > EPI ? S * AST : EPI];
+
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int M = g.M, N = g.N, K = g.K;
+  int tm, tn;
+  tile_of(blockIdx.x, gridDim.x, (M + BM - 1) / BM, tm, tn);
+  const int m0 = tm * BM, n0 = tn * 256;
+  const int nblk = K / BLK;
+  const int nk_all = (nblk + 1) / 2;
+  const int kz = blockIdx.y;
+  const int k_lo = (int)((long)kz * nk_all / split), nk = (int)((long)(kz + 1) * nk_all / split) - k_lo;
+  const int h = lane >> 5;
+
+  // A: as w8p_kernel, rows of 2K bytes (32-bit offsets: the entry point checks 2MK < 2^31)
+  int chunk[2];
+#pragma unroll
+  for (int e = 0; e < 2; ++e) chunk[e] = ((lane & 7) ^ ((lane >> 3) & 7) ^ e) << 4;
+  uint32_t aoff[NA];
+#pragma unroll
+  for (int i = 0; i < NA; ++i)
+    aoff[i] = (uint32_t)((long)min(m0 + (wave * NA + i) * 8 + (lane >> 3), M - 1) * 2 * K + (long)k_lo * 128 +
+                         chunk[(wave * NA + i) & 1]);
+  // B: unit index of (row, block 0) for the lane's row of each n-tile
+  uint32_t ubase[FN];
+#pragma unroll
+  for (int j = 0; j < FN; ++j) {
+    const int row = min(n0 + 64 * wave + 32 * j + (lane & 31), N - 1);
+    ubase[j] = (uint32_t)panel_index(row, 0, nblk);
+  }
+  const uint8_t* Ab = reinterpret_cast<const uint8_t*>(g.A);
+  const uint8_t* Bb = reinterpret_cast<const uint8_t*>(g.B);
+  const uint8_t* Sb = reinterpret_cast<const uint8_t*>(g.bsc);
+
+  v2u ru[3][FN][2];        // [set][n-tile][block] half-units
+  uint32_t rs[3][FN][2];   // [set][n-tile][block] scale bits
+  // VMEM operation o of a k-step: o < NB loads (n-tile, block, half-unit or
+  // scale) of k-step kl (relative to k_lo) into set SETL; then NA direct loads
+  // of A into stage kst % 4.
+  auto vmem_op = [&](auto oc, auto setlc, int kl, int kst) {
+    constexpr int o = decltype(oc)::value, setl = decltype(setlc)::value;
+    if constexpr (o < NB) {
+      constexpr int j = o / 4, bb = (o / 2) % 2, kind = o % 2;
+      const int blk = min(2 * (k_lo + kl) + bb, nblk - 1);
+      if constexpr (kind == 0) ru[setl][j][bb] = ld8_so(Bb + (long)blk * PANEL * 16, ubase[j] * 16 + 8 * h);
+      else rs[setl][j][bb] = ld2_so(Sb + (long)blk * PANEL * 2, ubase[j] * 2);
+    } else if constexpr (o < NB + NA) {
+      constexpr int i = o - NB;
+      uint8_t* st = ldsA + (kst & 3) * AST + (wave * NA + i) * 1024;
+      if constexpr (TAIL) {  // chunks past the row's end (a one-block last k-step) clamped inside the row
+        const int c = chunk[(wave * NA + i) & 1];
+        const int lim = 2 * K - 16 - k_lo * 128;  // last 16-byte chunk of the row, relative to k_lo
+        dma16_so(Ab, aoff[i] + (min(kl * 128 + c, lim) - c), st);
+      } else {
+        dma16_so(Ab + (long)kl * 128, aoff[i], st);
+      }
+    }
+  };
+
+  v16f acc[FM][FN];
+#pragma unroll
+  for (int i = 0; i < FM; ++i)
+#pragma unroll
+    for (int j = 0; j < FN; ++j) acc[i][j] = v16f{};
+
+  const int frow = lane & 31;
+  // A fragment of m-tile i, k-slice q = 2bb + s from stage st: chunk 4bb + 2h + s of row 32i + lane % 32
+  auto rdA = [&](int st, int i, int q) {
+    const int r = 32 * i + frow;
+    const int c = 4 * (q >> 1) + 2 * h + (q & 1);
+    return *reinterpret_cast<const v4i*>(ldsA + st * AST + r * 128 + ((c ^ w8p_swz(r)) << 4));
+  };
+  v4i fa[2][FM];
+
+  using I0 = std::integral_constant<int, 0>;
+  using I1 = std::integral_constant<int, 1>;
+  using I2 = std::integral_constant<int, 2>;
+  auto load_kstep = [&](auto setc, int kl, int kst) {  // A rows first, then B
+    static_for<NB, NB + NA>([&](auto oc) { vmem_op(oc, setc, kl, kst); });
+    static_for<0, NB>([&](auto oc) { vmem_op(oc, setc, kl, kst); });
+  };
+  load_kstep(I0{}, 0, 0);
+  load_kstep(I1{}, min(1, nk - 1), 1);
+  vmwait<NA + NB>();
+#pragma unroll
+  for (int j = 0; j < FN; ++j)
+#pragma unroll
+    for (int bb = 0; bb < 2; ++bb) {
+      pin(ru[0][j][bb]);
+      pin(rs[0][j][bb]);
+    }
+  __syncthreads();
+#pragma unroll
+  for (int i = 0; i < FM; ++i) fa[0][i] = rdA(0, i, 0);
+
+  // B fragment of n-tile j for k-slice q = 2bb + s of the k-step whose
+  // half-units sit in register set SET; zero scale for the absent second
+  // block of an odd block count
+  auto bfrag = [&](auto setc, int j, int q, bool half) {
+    constexpr int set = decltype(setc)::value;
+    const int bb = q >> 1;
+    const uint16_t sbits = (bb == 1 && half) ? (uint16_t)0 : (uint16_t)rs[set][j][bb];
+    const _Float16 sc = __builtin_bit_cast(_Float16, sbits);
+    const v2h sv = {sc, sc};
+    return __builtin_bit_cast(v4i, dequant_word_f16((q & 1) ? ru[set][j][bb].y : ru[set][j][bb].x, sv));
+  };
+  v4i fb[2][FN];  // [slice parity][n-tile]: slice q's fragments, built during slice q - 1
+#pragma unroll
+  for (int j = 0; j < FN; ++j) fb[0][j] = bfrag(I0{}, j, 0, 2 * k_lo + 1 >= nblk);
+
+  static_assert(NB == 8 && NB + NA <= 16 && FM % 4 == 0, "one VMEM operation per group");
+  int kt = 0;
+  auto kstep = [&](auto setc, auto setnc, auto setlc) {
+    constexpr int set = decltype(setc)::value, setn = decltype(setnc)::value;
+    const int st = kt & 3, stn = (kt + 1) & 3;
+    const int kl = min(kt + 2, nk - 1);
+    const bool half = 2 * (k_lo + kt) + 1 >= nblk, half_n = 2 * (k_lo + kt + 1) + 1 >= nblk;
+    static_for<0, 4>([&](auto qc) {
+      constexpr int q = decltype(qc)::value, cb = q & 1, nbuf = cb ^ 1;
+      if constexpr (q == 2) {
+        vmwait<NB>();  // B(kt+1), A(kt+1) landed in this wave
+#pragma unroll
+        for (int j = 0; j < FN; ++j)
+#pragma unroll
+          for (int b2 = 0; b2 < 2; ++b2) {
+            pin(ru[setn][j][b2]);
+            pin(rs[setn][j][b2]);
+          }
+        __syncthreads();  // ... and in every wave
+      }
+      static_for<0, 4>([&](auto gc) {
+        constexpr int g = decltype(gc)::value;
+        constexpr int i0 = g * (FM / 4);
+#pragma unroll
+        for (int ii = i0; ii < i0 + FM / 4; ++ii) fa[nbuf][ii] = q < 3 ? rdA(st, ii, q + 1) : rdA(stn, ii, 0);
+        // the next slice's B fragment of n-tile g, while this slice's MFMAs run
+        if constexpr (g < FN) {
+          if constexpr (q < 3) fb[nbuf][g] = bfrag(setc, g, q + 1, half);
+          else fb[nbuf][g] = bfrag(setnc, g, 0, half_n);
+        }
+#pragma unroll
+        for (int ii = i0; ii < i0 + FM / 4; ++ii)
+#pragma unroll
+          for (int j = 0; j < FN; ++j)
+            acc[ii][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(v8h, fa[cb][ii]),
+                                                                __builtin_bit_cast(v8h, fb[cb][j]), acc[ii][j], 0, 0, 0);
+        if constexpr (g < FN) {
+          __builtin_amdgcn_sched_group_barrier(0x100, FM / 4, 0);
+#pragma unroll
+          for (int r = 0; r < FM / 4 * FN; ++r) {
+            __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+            __builtin_amdgcn_sched_group_barrier(0x002, 6, 0);
+          }
+        } else {
+#pragma unroll
+          for (int r = 0; r < FM / 4; ++r) {
+            __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+            __builtin_amdgcn_sched_group_barrier(0x008, FN, 0);
+          }
+        }
+        vmem_op(std::integral_constant<int, 4 * q + g>{}, setlc, kl, kt + 2);
+        __builtin_amdgcn_sched_barrier(0);
+      });
+    });
+  };
+  for (; kt + 2 < nk; kt += 3) {
+    kstep(I0{}, I1{}, I2{});
+    ++kt;
+    kstep(I1{}, I2{}, I0{});
+    ++kt;
+    kstep(I2{}, I0{}, I1{});
+    kt -= 2;
+  }
+  if (kt < nk) {
+    kstep(I0{}, I1{}, I2{});
+    ++kt;
+    if (kt < nk) kstep(I1{}, I2{}, I0{});
+  }
+  vmwait<0>();
+#pragma unroll
+  for (int s3 = 0; s3 < 3; ++s3)
+#pragma unroll
+    for (int j = 0; j < FN; ++j)
+#pragma unroll
+      for (int bb = 0; bb < 2; ++bb) {
+        pin(ru[s3][j][bb]);
+        pin(rs[s3][j][bb]);
+      }
+  __syncthreads();  // every direct load landed and every fragment read before the strips reuse LDS
+
+  uint32_t* strip = reinterpret_cast<uint32_t*>(ldsA) + wave * (64 * EST);
+#pragma unroll
+  for (int c = 0; c < FM / 2; ++c) {
+    const v16f sub[2][FN] = {{acc[2 * c][0], acc[2 * c][1]}, {acc[2 * c + 1][0], acc[2 * c + 1][1]}};
+    if (split > 1)
+      epilogue<2, 64, FN>(g, strip, sub, m0 + 64 * c, n0 + 64 * wave, g.P + (long)kz * M * N);
+    else
+      epilogue<1, 64, FN>(g, strip, sub, m0 + 64 * c, n0 + 64 * wave, nullptr);
+  }
+}
+
 // ---- W4A16 / W4A8 ---------------------------------------------------------------
 // BM x 256 tile, K step one 64-byte A row (32 f16 for W4A16, 64 int8 for
 // W4A8). A: S-stage LDS ring of direct loads (k-step j + S goes into the
@@ -940,10 +1165,17 @@ static int pick_bm(int M, int N) { return tiles(M, N, 256) >= 256 ? 256 : 128; }
 
 static int w4a16_split(int M, int N, int K) {
   const int t = tiles(M, N, pick_bm(M, N));
-  const int nk = K / 32;
+  const int nk = (K / 32 + 1) / 2;  // k-steps of 64
   int s = 1;
-  while (t * s < 240 && nk / (s + 1) >= 32) ++s;
+  while (t * s < 240 && nk / (s + 1) >= 16) ++s;
   return s;
+}
+
+template <int BM>
+static void launch_w4p(const GemmArgs& g, int split, hipStream_t st) {
+  const dim3 grid(tiles(g.M, g.N, BM), split);
+  if (g.K % 64) hipLaunchKernelGGL((w4p_kernel<BM, true>), grid, dim3(256), 0, st, g, split);
+  else hipLaunchKernelGGL((w4p_kernel<BM, false>), grid, dim3(256), 0, st, g, split);
 }
 
 template <int OP, int BM>
@@ -1070,10 +1302,12 @@ int q4_gemm_w4a16_ws(const uint16_t* X, const uint32_t* wq, const uint16_t* sc16
   if (split > 1 && (!ws || ws_bytes < (size_t)split * M * N * sizeof(float))) split = 1;  // no room: one pass
   GemmArgs g{X, wq, sc16, nullptr, nullptr, 0, Y, nullptr, split > 1 ? reinterpret_cast<float*>(ws) : nullptr,
              M, N, K};
+  Q4_ARG(2L * M * K < (1L << 31) && (long)pad_rows(N) * (K / BLK) * 16 < (1L << 31),
+         "W4A16 needs X and the int4 weights under 2 GiB (32-bit offsets)");
   if (pick_bm(M, N) == 256)
-    launch_w4<OP_W4A16, 256>(g, split, as_stream(stream));
+    launch_w4p<256>(g, split, as_stream(stream));
   else
-    launch_w4<OP_W4A16, 128>(g, split, as_stream(stream));
+    launch_w4p<128>(g, split, as_stream(stream));
   Q4_LAUNCHED("gemm_w4a16");
   if (split > 1) {
     const long n = (long)M * N;

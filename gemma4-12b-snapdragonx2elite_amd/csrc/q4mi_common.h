@@ -136,6 +136,16 @@ __device__ inline v4u ld16_so(const void* sbase, uint32_t voff) {
   asm volatile("global_load_dwordx4 %0, %1, %2" : "=v"(r) : "v"(voff), "s"(sbase));
   return r;
 }
+__device__ inline v2u ld8_so(const void* sbase, uint32_t voff) {
+  v2u r;
+  asm volatile("global_load_dwordx2 %0, %1, %2" : "=v"(r) : "v"(voff), "s"(sbase));
+  return r;
+}
+__device__ inline uint32_t ld2_so(const void* sbase, uint32_t voff) {
+  uint32_t r;
+  asm volatile("global_load_ushort %0, %1, %2" : "=v"(r) : "v"(voff), "s"(sbase));
+  return r;
+}
 // Direct-to-LDS load at uniform base + per-lane offset (lds_dst as dma16).
 __device__ inline void dma16_so(const void* sbase, uint32_t voff, const void* lds_dst) {
   const unsigned l = __builtin_amdgcn_readfirstlane((unsigned)(uintptr_t)lds_dst);
