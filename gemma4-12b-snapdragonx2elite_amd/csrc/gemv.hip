@@ -11,15 +11,16 @@
 //    contiguous HBM (one 32-element block of 64 rows). Scales of the same
 //    64 rows are 128 contiguous bytes.
 //  * A workgroup (4 waves) owns R consecutive rows of a panel (R = 8..64,
-//    chosen per shape so the grid fills 256 CUs and every lane's blocks fit
-//    one batch of loads) and the whole K range: lane = (row r, block slot),
-//    64/R slots per wave, so each wave load covers R*16 contiguous bytes
-//    (>= one 128 B line) per block. Workgroups are ordered XCD-major so the
-//    workgroups of one panel share its scale lines in one L2.
-//  * The x slice is copied to LDS with direct-to-LDS loads; every weight
-//    unit and scale of the lane is then requested at once with streaming
-//    loads, and each unit is consumed after its own wait count, so HBM sees
-//    the whole matrix requested up front and the x copy overlaps it.
+//    chosen per shape so the grid fills 256 CUs) and the whole K range:
+//    lane = (row r, block slot), 64/R slots per wave, so each wave load
+//    covers R*16 contiguous bytes (>= one 128 B line) per block. Workgroups
+//    are ordered XCD-major so the workgroups of one panel share its scale
+//    lines in one L2.
+//  * The x slice is copied to LDS with direct-to-LDS loads; every lane then
+//    keeps U weight units and their scales in flight in a register ring
+//    (streaming loads, explicit wait counts): a unit is used as soon as it
+//    has landed and its registers are refilled with a unit U places on. U
+//    is sized so the whole grid keeps about 8 MB in flight.
 //  * Register dequant without conversions: masking a word with 0x000F000F
 //    yields two fp16 subnormals q*2^-24; with 0x00F000F0, 16q*2^-24.
 //    v_dot2_f32_f16 multiplies them by an fp16 x pair with fp32
@@ -44,7 +45,8 @@ constexpr int GEMV_THREADS = 256;
 constexpr int GEMV_WAVES = GEMV_THREADS / 64;
 constexpr int GEMV_LDS_MAX = 64 * 1024;    // x staging cap per workgroup (bytes)
 constexpr int GEMV_TARGET_WGS = 480;       // preferred workgroup count (see rows_per_group())
-constexpr int GEMV_MIN_WGS = 256;          // one per CU; below this K is split across workgroups
+constexpr int GEMV_MIN_WGS = 240;          // about one per CU; below this K is split across workgroups
+constexpr long GEMV_INFLIGHT_UNITS = 8L << 16;  // 16-byte weight units in flight over a grid (8 MB)
 // Split-K workspace layout: tickets for up to GEMV_MAX_TICKETS row groups at
 // a fixed offset 0 (so GEMVs of different shapes sharing one workspace never
 // see each other's partials as tickets), then the fp32 partials.
@@ -129,9 +131,9 @@ __device__ inline int xcd_major(int b, int G) {
 // x slice (no registers), (2) the lane's first U weight units (streaming
 // loads) and scales (clamped indices so the count is static), (3) wait for
 // the x loads only (s_waitcnt vmcnt(2U): loads return in order) and one
-// barrier, (4) unit t is used after vmcnt(2(U-1-t)), so the dot products
-// start while later units are still in flight. Lanes with more than U blocks
-// (long K) load and use further batches the same way.
+// barrier, (4) each unit is used as soon as it has landed and its registers
+// are refilled with the lane's unit U places further on, so every lane keeps
+// U units in flight until its last round.
 template <int R, int U, int XT, int ST, int YT>
 __device__ __forceinline__ void gemv_rows(const void* __restrict__ xv, const uint4* __restrict__ wq,
                                           const void* __restrict__ scv, float outscale, void* __restrict__ yv,
@@ -150,14 +152,27 @@ __device__ __forceinline__ void gemv_rows(const void* __restrict__ xv, const uin
   }
   const long k0 = (long)b_lo * BLK;
 
-  // (1) x slice [k0, k0 + 32 nb) -> LDS, 1 KB per wave instruction; chunks
-  //     past the slice re-read its last chunk into the padding of the area
-  const int n16 = XH ? nb * 4 : nb * 8;
-  const int nv = (n16 + 63) >> 6;
-  const uint8_t* xsrc = reinterpret_cast<const uint8_t*>(xv) + k0 * (XH ? 2 : 4);
-  for (int v = wave; v < nv; v += GEMV_WAVES) dma16(xsrc + (long)min(v * 64 + lane, n16 - 1) * 16, smem + v * 256);
+  // (1) the x blocks this wave uses -> LDS, 1 KB per direct-load
+  //     instruction. Wave w uses blocks j with (j mod S) / SW == w, i.e. SW
+  //     consecutive blocks every S; its local block lb = (j / S) SW + j mod SW
+  //     is stored at lb * XB in the wave's own area (positions past the
+  //     slice re-read its last block), so no other wave's data is needed.
+  constexpr int XB = XH ? 64 : 128;         // x bytes per block
+  constexpr int CPB = XB / 16;              // 16-byte chunks per block
+  constexpr int BPD = 64 / CPB;             // blocks per direct load
+  const int nbw = (nb + S - 1) / S * SW;    // local blocks per wave (wave-uniform)
+  const int nvw = (nbw + BPD - 1) / BPD;    // direct loads per wave
+  uint32_t* xw = smem + wave * nvw * 256;
+  {
+    const uint8_t* xsrc = reinterpret_cast<const uint8_t*>(xv) + k0 * (XH ? 2 : 4);
+    for (int v = 0; v < nvw; ++v) {
+      const int lb = v * BPD + lane / CPB;
+      const int j = min(lb / SW * S + wave * SW + lb % SW, nb - 1);
+      dma16(xsrc + (long)j * XB + (lane % CPB) * 16, xw + v * 256);
+    }
+  }
 
-  // (2) first batch of weight units and scales: blocks slot, slot + S, ...
+  // (2) first U weight units and scales of the lane: blocks slot, slot + S, ...
   const int n0 = g * R;
   const long ubase = ((long)(n0 / PANEL) * nblk + b_lo) * PANEL + (n0 % PANEL) + r;  // unit of block j: ubase + 64 j
   const uint8_t* wb = reinterpret_cast<const uint8_t*>(wq);
@@ -169,49 +184,60 @@ __device__ __forceinline__ void gemv_rows(const void* __restrict__ xv, const uin
     u[t] = ld16_nt(wb + ix * 16);
     sb[t] = load_scale<ST>(scv, ix);
   }
-  // (3) this wave's x chunks have landed; the barrier publishes every wave's.
-  //     For fp16 x the block sums follow the x slice in LDS.
+  // (3) this wave's x blocks have landed (loads complete in order); for fp16
+  //     x the wave sums each of its blocks into its own LDS area. A wave's
+  //     LDS operations execute in order: no barrier is needed.
   vmwait<2 * U>();
-  __syncthreads();
-  const uint32_t* xs_h = smem;
-  const float* xs_f = reinterpret_cast<const float*>(smem);
-  float* xsum = reinterpret_cast<float*>(smem + nv * 256);
+  const uint32_t* xs_h = xw;
+  const float* xs_f = reinterpret_cast<const float*>(xw);
+  float* xsum = reinterpret_cast<float*>(smem + GEMV_WAVES * nvw * 256) + wave * nbw;
   if constexpr (XH) {
     const v2h one2 = {(_Float16)1.0f, (_Float16)1.0f};
-    for (int j = tid; j < nb; j += GEMV_THREADS) {
+    for (int lb = lane; lb < nbw; lb += 64) {
       float t = 0.0f;
 #pragma unroll
-      for (int i = 0; i < 16; ++i) t = __builtin_amdgcn_fdot2(as_h2(xs_h[j * 16 + i]), one2, t, false);
-      xsum[j] = t;
+      for (int i = 0; i < 16; ++i) t = __builtin_amdgcn_fdot2(as_h2(xs_h[lb * 16 + i]), one2, t, false);
+      xsum[lb] = t;
     }
-    __syncthreads();
   }
 
-  // (4) dot products, unit by unit as they arrive
+  // (4) dot products, unit by unit as they arrive. Unit c of the lane is
+  //     block slot + c S, local block c SW + slot % SW. In every round but
+  //     the last, unit t's registers are refilled with unit t + U right
+  //     after use, so U units (2U loads) stay in flight and unit t is always
+  //     2(U-1) loads behind the newest; the last round drains them.
   float acc = 0.0f;
-  for (int j = slot;;) {
+  auto use = [&](int jj, int lb, const v4u& w, uint32_t sv) {
+    if (jj < nb) {
+      float d;
+      if constexpr (XH) d = block_dot_h(w, xs_h + lb * 16, xsum[lb]);
+      else d = block_dot_f(w, xs_f + lb * BLK);
+      acc = fmaf(scale_value<ST>(sv), d, acc);
+    }
+  };
+  const int rounds = ((nb + S - 1) / S + U - 1) / U;  // wave-uniform (slot 0 has the most units)
+  int j = slot, lb = lane / R;
+  for (int rd = 1; rd < rounds; ++rd) {
     static_for<0, U>([&](auto tc) {
       constexpr int t = decltype(tc)::value;
-      vmwait<2 * (U - 1 - t)>();
+      vmwait<2 * (U - 1)>();
       pin(u[t]);
       pin(sb[t]);
-      const int jj = j + t * S;
-      if (jj < nb) {
-        float d;
-        if constexpr (XH) d = block_dot_h(u[t], xs_h + jj * 16, xsum[jj]);
-        else d = block_dot_f(u[t], xs_f + jj * BLK);
-        acc = fmaf(scale_value<ST>(sb[t]), d, acc);
-      }
-    });
-    j += S * U;
-    if (__builtin_amdgcn_readfirstlane(j - slot) >= nb) break;  // wave-uniform: j - slot is the same in every lane
-#pragma unroll
-    for (int t = 0; t < U; ++t) {
-      const long ix = ubase + (long)min(j + t * S, nb - 1) * PANEL;
+      use(j + t * S, lb + t * SW, u[t], sb[t]);
+      const long ix = ubase + (long)min(j + (t + U) * S, nb - 1) * PANEL;
       u[t] = ld16_nt(wb + ix * 16);
       sb[t] = load_scale<ST>(scv, ix);
-    }
+    });
+    j += S * U;
+    lb += SW * U;
   }
+  static_for<0, U>([&](auto tc) {
+    constexpr int t = decltype(tc)::value;
+    vmwait<2 * (U - 1 - t)>();
+    pin(u[t]);
+    pin(sb[t]);
+    use(j + t * S, lb + t * SW, u[t], sb[t]);
+  });
   // slots of a row: lanes r, r + R, r + 2R, ... of each wave, then the 4 waves
 #pragma unroll
   for (int off = R; off < 64; off <<= 1) acc += __shfl_xor(acc, off, 64);
@@ -328,7 +354,7 @@ static GemvFns pick_x(int xt, int st, int yt) {
 }
 template <int R>
 static GemvFns pick_u(int U, int xt, int st, int yt) {
-  return U == 4 ? pick_x<R, 4>(xt, st, yt) : U == 8 ? pick_x<R, 8>(xt, st, yt) : pick_x<R, 16>(xt, st, yt);
+  return U == 4 ? pick_x<R, 4>(xt, st, yt) : pick_x<R, 8>(xt, st, yt);
 }
 static GemvFns pick(int R, int U, int xt, int st, int yt) {
   switch (R) {
@@ -339,16 +365,16 @@ static GemvFns pick(int R, int U, int xt, int st, int yt) {
   }
 }
 
-// Rows per workgroup R for NP padded rows: the largest R that gives
-// GEMV_TARGET_WGS workgroups (about two per CU), else the largest that gives
-// one workgroup per CU, else 8 (measured on MI355X over the decode shapes:
-// 64 rows for gate_up and lm_head, 32 for 15360 rows, 16 for the batched
-// q/k/v, 8 for the 3840-row o and down). Q4MI_GEMV_ROWS (8/16/32/64)
-// overrides R for tuning sweeps.
-static int rows_per_group(int NP, int nblk) {
-  (void)nblk;
+// Rows per workgroup R for NP padded rows: the largest R of 64, 32, 16 that
+// gives GEMV_TARGET_WGS workgroups (about two per CU), else the largest R
+// that gives GEMV_MIN_WGS (about one per CU), else 8. Measured on MI355X over
+// the decode shapes: 64 rows for gate_up and lm_head, 32 for 15360 rows, 16
+// for the batched q/k/v and for the 3840-row o and down (240 workgroups with
+// 8 units in flight beat 480 with 4: each workgroup stages the whole x, 30 KB
+// for down). Q4MI_GEMV_ROWS (8/16/32/64) overrides R for tuning sweeps.
+static int rows_per_group(int NP) {
   int R = 0;
-  for (int c : {64, 32, 16, 8})
+  for (int c : {64, 32, 16})
     if (NP / c >= GEMV_TARGET_WGS) { R = c; break; }
   if (R == 0)
     for (int c : {64, 32, 16, 8})
@@ -361,26 +387,30 @@ static int rows_per_group(int NP, int nblk) {
   return R;
 }
 
-// Units in flight per lane (one batch) for nb blocks per workgroup: 8 for
-// 32- and 64-row workgroups with more than 4 blocks per lane, else 4.
-// Measured on MI355X over the decode shapes: more loads in flight per lane
-// than this is slower (16 loses 5-25%). Q4MI_GEMV_UNITS (4/8/16) overrides
-// it for tuning sweeps.
-static int units_in_flight(int nb, int R) {
+// Units in flight per lane for a grid of wgs workgroups with nb blocks each:
+// 8 while the whole grid keeps at most GEMV_INFLIGHT_UNITS in flight (8 MB
+// of weights, what HBM needs at ~1.1 us of loaded latency), else 4; 4 when
+// a lane has at most 4 blocks. Measured on MI355X: the best of 4/8/16 for
+// every decode shape follows this rule (more in flight only queues).
+// Q4MI_GEMV_UNITS (4/8) overrides it for tuning sweeps.
+static int units_in_flight(int nb, int R, long wgs) {
   if (const char* e = getenv("Q4MI_GEMV_UNITS")) {
     int v = atoi(e);
-    if (v == 4 || v == 8 || v == 16) return v;
+    if (v == 4 || v == 8) return v;
   }
   const int per_lane = ceil_div(nb, (64 / R) * GEMV_WAVES);
-  return R >= 32 && per_lane > 4 ? 8 : 4;
+  return per_lane > 4 && wgs * GEMV_THREADS * 8 <= GEMV_INFLIGHT_UNITS ? 8 : 4;
 }
 
-// LDS bytes of x per block, and of the staging area for nb blocks (whole
-// 1 KB direct-load rows, then the fp32 block sums for fp16 x).
+// LDS bytes of x per block, and of the staging area for nb blocks and R
+// rows per workgroup: each wave's local blocks in whole 1 KB direct-load
+// rows, then (fp16 x) each wave's fp32 block sums.
 static int x_block_bytes(int x_dtype) { return x_dtype == Q4_DT_F16 ? 64 : 128; }
-static size_t x_stage_lds(int nb, int x_dtype) {
-  const size_t x = (size_t)ceil_div((long)nb * x_block_bytes(x_dtype), 1024) * 1024;
-  return x_dtype == Q4_DT_F16 ? x + (size_t)ceil_div(nb, 4) * 16 : x;  // + fp32 block sums
+static size_t x_stage_lds(int nb, int x_dtype, int R) {
+  const int SW = 64 / R, S = SW * GEMV_WAVES;
+  const long nbw = (long)ceil_div(nb, S) * SW;
+  const size_t per_wave = (size_t)ceil_div(nbw * x_block_bytes(x_dtype), 1024) * 1024;
+  return GEMV_WAVES * per_wave + (x_dtype == Q4_DT_F16 ? (size_t)GEMV_WAVES * nbw * sizeof(float) : 0);
 }
 
 struct GemvPlan {
@@ -390,7 +420,7 @@ struct GemvPlan {
 
 static GemvPlan plan(int N, int K, int split_req, int x_dtype) {
   const int NP = pad_rows(N), nblk = K / BLK;
-  const int R = rows_per_group(NP, nblk);
+  const int R = rows_per_group(NP);
   const int wgs = NP / R;
   int s = split_req;
   if (s <= 0) {
@@ -408,8 +438,8 @@ static GemvPlan plan(int N, int K, int split_req, int x_dtype) {
   p.R = R;
   p.split = s;
   p.nb_max = ceil_div(nblk, s);
-  p.U = units_in_flight(p.nb_max, R);
-  p.lds = x_stage_lds(p.nb_max, x_dtype);
+  p.U = units_in_flight(p.nb_max, R, (long)wgs * s);
+  p.lds = x_stage_lds(p.nb_max, x_dtype, R);
   p.ws = 0;
   if (s > 1) p.ws = (GEMV_TICKET_BYTES + (size_t)s * NP * sizeof(float) + 255) & ~(size_t)255;
   return p;
@@ -420,6 +450,7 @@ static GemvPlan plan(int N, int K, int split_req, int x_dtype) {
 using namespace q4;
 
 extern "C" {
+
 
 int q4_gemv_auto_split(int N, int K) {
   if (N <= 0 || K <= 0 || K % BLK) return 1;
@@ -497,7 +528,7 @@ int q4_gemv_batch(const void* x, int x_dtype, int K, int scale_fmt, int y_dtype,
     NP += pad_rows(N[i]);
   }
   Q4_ARG(NP <= (1L << 30), "batched GEMV too large");
-  const int R = rows_per_group((int)NP, nblk);
+  const int R = rows_per_group((int)NP);
   GemvSegs segs;
   memset(&segs, 0, sizeof(segs));
   segs.count = count;
@@ -511,9 +542,9 @@ int q4_gemv_batch(const void* x, int x_dtype, int K, int scale_fmt, int y_dtype,
     segs.s[i].N = N[i];
     segs.s[i].g_end = groups;
   }
-  const int U = units_in_flight(nblk, R);
+  const int U = units_in_flight(nblk, R, groups);
   gemv_batch_fn fn = pick(R, U, x_dtype, scale_fmt, y_dtype).many;
-  hipLaunchKernelGGL(fn, dim3(groups), dim3(GEMV_THREADS), x_stage_lds(nblk, x_dtype), as_stream(stream), x, nblk,
+  hipLaunchKernelGGL(fn, dim3(groups), dim3(GEMV_THREADS), x_stage_lds(nblk, x_dtype, R), as_stream(stream), x, nblk,
                      segs);
   Q4_LAUNCHED("gemv_batch");
   return Q4_OK;

@@ -53,6 +53,50 @@ def test_gemv_split_invariance(gpu, split, rows, monkeypatch):
     assert O.normwise_rel_err(to_np(y), ref) <= TOL_F32
 
 
+@pytest.mark.parametrize("rows", ["8", "16", "32", "64"])
+@pytest.mark.parametrize("N,nblk", [(64, 3), (256, 37), (192, 200), (320, 481)])
+def test_gemv_units_in_flight(gpu, rows, N, nblk, monkeypatch):
+    """Every rows-per-workgroup x units-in-flight variant against the oracle,
+    with block counts that leave the lanes' last round of the load ring
+    partly empty (3, 37, 200, 481 blocks), fp16 and fp32 x. The units are
+    consumed in the same order whatever the ring size, so U = 4 and U = 8
+    give bit-identical outputs."""
+    monkeypatch.setenv("Q4MI_GEMV_ROWS", rows)
+    K = 32 * nblk
+    rng = np.random.default_rng(N + nblk)
+    q, s, x = _case(rng, N, K)
+    wq, sc = upload_int4(q, s)
+    for xin, ydt, tol in [(x, torch.float16, TOL_F16), (x.astype(np.float32), torch.float32, TOL_F32)]:
+        ref = O.gemv_ref(q, s, xin)
+        outs = []
+        for units in ["4", "8"]:
+            monkeypatch.setenv("Q4MI_GEMV_UNITS", units)
+            y = gpu.gemv(torch.from_numpy(xin).cuda(), wq, sc, N, K, y_dtype=ydt, split=1)
+            assert O.normwise_rel_err(to_np(y).astype(np.float32), ref) <= tol, (units, ydt)
+            outs.append(y)
+        assert torch.equal(outs[0], outs[1])
+
+
+@pytest.mark.parametrize("K,xdt,rows", [(32768, torch.float16, "64"), (32768, torch.float16, "8"),
+                                        (16384, torch.float32, "16")])
+def test_gemv_largest_x_staging(gpu, K, xdt, rows, monkeypatch):
+    """The longest x one workgroup stages without a K split (64 KB of x, plus
+    the block sums for fp16 x), through q4_gemv and q4_gemv_batch: the same
+    rows per workgroup give bit-identical outputs."""
+    monkeypatch.setenv("Q4MI_GEMV_ROWS", rows)
+    N = 128
+    rng = np.random.default_rng(K + int(rows))
+    q, s, x = _case(rng, N, K)
+    xin = x if xdt == torch.float16 else x.astype(np.float32)
+    ref = O.gemv_ref(q, s, xin)
+    wq, sc = upload_int4(q, s)
+    xt = torch.from_numpy(xin).cuda()
+    y = gpu.gemv(xt, wq, sc, N, K, y_dtype=torch.float32, split=1)
+    assert O.normwise_rel_err(to_np(y), ref) <= TOL_F32
+    (yb,) = gpu.gemv_batch(xt, [(wq, sc, N, None, None)], K, y_dtype=torch.float32)
+    assert torch.equal(y, yb)
+
+
 def test_gemv_c1_full_size(gpu):
     """Down-projection-sized GEMV N=15360, K=3840, fp16 x and y, seed 0."""
     rng = np.random.default_rng(0)
