@@ -8,7 +8,9 @@ and outputs, captured once as a hipGraph and replayed per token. Every
 weight byte is distinct (6.6 GB per token), so the 256 MB Infinity Cache
 cannot serve repeats. value = algorithmic bytes per token / time per token.
 
-Also measured in the same run: the W8A8 prefill GEMM at M=2048, N=15360,
+Also measured in the same run: single GEMV shapes on their own (15360x3840
+with fp16 and with e4m3 scales, lm_head 262144x3840), the per-token time
+distribution, the W8A8 prefill GEMM at M=2048, N=15360,
 K=3840 (int8 MFMA) and the W4A16 GEMM at M=512 (f16 MFMA), each as a
 fraction of MI355X's dense peak, and the CPU baseline (the oracle's numpy
 dequant+matmul, the reference's own formulation) on a bounded sample.
@@ -116,6 +118,15 @@ def bench_decode(ops, steps: int, warmup: int):
     t1.synchronize()
     torch.cuda.synchronize()
     ms = t0.elapsed_time(t1) / steps
+    # distribution: every replay between its own pair of events (a separate pass)
+    evs = [torch.cuda.Event(enable_timing=True) for _ in range(steps + 1)]
+    evs[0].record(st)
+    for i in range(steps):
+        graph.launch()
+        evs[i + 1].record(st)
+    evs[-1].synchronize()
+    per = sorted(evs[i].elapsed_time(evs[i + 1]) for i in range(steps))
+    pct = {f"p{q}": round(per[min(steps - 1, int(q / 100 * steps))], 4) for q in (10, 50, 90)}
     nbytes = sum(gemv_bytes(N, K) for _, N, K, _, _ in mats)
     # per-shape kernel time: one graph of the 48 same-shape launches per shape, same stream
     per_shape = {}
@@ -145,7 +156,52 @@ def bench_decode(ops, steps: int, warmup: int):
     del mats, ws
     torch.cuda.empty_cache()
     return {"ms_per_step": ms, "bytes_per_step": nbytes, "launches": len(launches),
-            "GBps": nbytes / (ms * 1e-3) / 1e9, "per_shape": per_shape}
+            "GBps": nbytes / (ms * 1e-3) / 1e9, "per_shape": per_shape, "ms_per_step_percentiles": pct}
+
+
+def bench_gemv_single(ops, N: int, K: int, e4m3: bool, reps: int = 10):
+    """One GEMV shape on its own: a graph of launches over distinct weights
+    (>= 1.5 GB, so the 256 MB Infinity Cache cannot serve repeats), HIP events
+    around the replays; time per launch, GB/s of algorithmic bytes."""
+    import torch
+
+    dev = torch.device("cuda:0")
+    gen = torch.Generator(device=dev).manual_seed(3)
+    sb = 1 if e4m3 else 2
+    per = gemv_bytes(N, K, sb)
+    n = max(4, (1536 << 20) // per)
+    x = torch.randn(K, device=dev, generator=gen).to(torch.float16)
+    y = torch.empty(N, dtype=torch.float16, device=dev)
+    mats = []
+    for _ in range(n):
+        w = torch.randint(-2 ** 31, 2 ** 31 - 1, (N * K // 8,), dtype=torch.int64, device=dev,
+                          generator=gen).to(torch.int32)
+        if e4m3:  # e4m3 codes of scale values 2^-2 .. 2^2 (timing does not depend on the values)
+            s = torch.randint(0x28, 0x48, (N * K // 32,), dtype=torch.int32, device=dev, generator=gen).to(torch.uint8)
+        else:
+            s = (torch.randn(N * K // 32, device=dev, generator=gen) * 0.02).abs().to(torch.float16)
+        mats.append((w, s))
+    fmt = ops.SCALE_E4M3 if e4m3 else ops.SCALE_F16
+    g = ops.Graph()
+    with g.capture():
+        for w, s in mats:
+            ops.gemv(x, w, s, N, K, scale_fmt=fmt, inv=0.5, y=y)
+    g.launch()
+    g.launch()
+    a = torch.cuda.Event(enable_timing=True)
+    b = torch.cuda.Event(enable_timing=True)
+    a.record(g.stream)
+    for _ in range(reps):
+        g.launch()
+    b.record(g.stream)
+    b.synchronize()
+    us = a.elapsed_time(b) * 1e3 / (reps * n)
+    g.destroy()
+    del mats
+    torch.cuda.empty_cache()
+    return {"N": N, "K": K, "scales": "e4m3" if e4m3 else "f16", "us_per_launch": round(us, 3),
+            "bytes_per_launch": per, "GBps": round(per / us / 1e3, 1),
+            "frac_of_hbm_peak": round(per / us / 1e3 / HBM_PEAK_GBS, 4), "distinct_weight_sets": n}
 
 
 def counter_workload(ops):
@@ -336,7 +392,12 @@ def main():
     print(f"[bench] decode graph: {LAYERS} layers + lm_head, {args.steps} steps after {args.warmup} warmup",
           flush=True)
     dec = bench_decode(ops, args.steps, args.warmup)
-    print(f"[bench] decode {dec['ms_per_step']:.3f} ms/token, {dec['GBps']:.0f} GB/s", flush=True)
+    print(f"[bench] decode {dec['ms_per_step']:.3f} ms/token, {dec['GBps']:.0f} GB/s "
+          f"(per-token {dec['ms_per_step_percentiles']})", flush=True)
+    single = {"c1_15360x3840_f16_scales": bench_gemv_single(ops, I, H, False),
+              "c3_15360x3840_e4m3_scales": bench_gemv_single(ops, I, H, True),
+              "lm_head_262144x3840_f16_scales": bench_gemv_single(ops, V, H, False, reps=4)}
+    print(f"[bench] single-shape gemv {single}", flush=True)
     w8 = w4 = None
     if not args.no_gemm:
         w8 = bench_w8a8(ops)
@@ -377,6 +438,8 @@ def main():
             "kernels_per_step": dec["launches"],
             "frac_of_hbm_peak": round(dec["GBps"] / HBM_PEAK_GBS, 4),
             "per_shape": dec["per_shape"],
+            "ms_per_step_percentiles": dec["ms_per_step_percentiles"],
+            "single_shape_gemv": single,
         },
         "roofline": {
             "bound": "hbm",
