@@ -51,6 +51,12 @@ SIGNATURES = {
     "q4_gemm_w8a8_packed": (_i, [_vp, _vp, _vp, _vp, _i, _vp, _vp, _i, _i, _i, _vp]),
     "q4_cast_f32_f16": (_i, [_vp, _vp, _sz, _vp]),
     "q4_cast_f16_f32": (_i, [_vp, _vp, _sz, _vp]),
+    "q4_rmsnorm": (_i, [_vp, _vp, _vp, _i, _i, _vp]),
+    "q4_normadd": (_i, [_vp, _vp, _vp, _i, _f, _vp]),
+    "q4_gelumul": (_i, [_vp, _vp, _vp, _i, _i, _vp]),
+    "q4_prepkv": (_i, [_vp, _vp, _vp, _vp, _vp, _vp, _i, _i, _i, _i, _i, _i, _i, _vp, _vp]),
+    "q4_attn_workspace_bytes": (_sz, [_i, _i, _i]),
+    "q4_attn": (_i, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _i, _i, _i, _i, _i, _i, _i, _vp, _vp, _sz, _vp]),
     "q4_graph_begin": (_i, [_vp]),
     "q4_graph_end": (_i, [_vp, C.POINTER(_vp)]),
     "q4_graph_launch": (_i, [_vp, _vp]),

@@ -352,6 +352,92 @@ def cast_f16_f32(src: torch.Tensor, dst: torch.Tensor | None = None) -> torch.Te
     return dst
 
 
+# ------------------------------------------------------ decode-token ops
+def _f32(t, n: int, what: str) -> None:
+    if t.dtype != torch.float32:
+        raise ValueError(f"{what} must be float32")
+    _need(t, 4 * n, what)
+
+
+def rmsnorm(x: torch.Tensor, w: torch.Tensor, y: torch.Tensor | None = None, y_dtype=torch.float32) -> torch.Tensor:
+    """y = x / sqrt(mean(x^2) + 1e-6) * w over the whole of ``x`` (fp32)."""
+    D = x.numel()
+    _f32(x, D, "x")
+    _f32(w, D, "w")
+    y = torch.empty(D, dtype=y_dtype, device=x.device) if y is None else y
+    _need(y, D * y.element_size(), "y")
+    call("q4_rmsnorm", _p(x), _p(w), _p(y), _dt(y), D, _stream())
+    return y
+
+
+def normadd(x: torch.Tensor, w: torch.Tensor, h: torch.Tensor, scale: float = 0.0) -> torch.Tensor:
+    """h = (h + rmsnorm(x) * w) * scale in place (scale 0: unscaled)."""
+    D = x.numel()
+    for t, nm in ((x, "x"), (w, "w"), (h, "h")):
+        _f32(t, D, nm)
+    call("q4_normadd", _p(x), _p(w), _p(h), D, C.c_float(scale), _stream())
+    return h
+
+
+def gelumul(gate: torch.Tensor, up: torch.Tensor, out: torch.Tensor | None = None, out_dtype=torch.float32):
+    """out = gelu_tanh(gate) * up (fp32 in)."""
+    n = gate.numel()
+    _f32(gate, n, "gate")
+    _f32(up, n, "up")
+    out = torch.empty(n, dtype=out_dtype, device=gate.device) if out is None else out
+    _need(out, n * out.element_size(), "out")
+    call("q4_gelumul", _p(gate), _p(up), _p(out), _dt(out), n, _stream())
+    return out
+
+
+def _kv_checks(kc, vc, nkv, stride, hd, dyn):
+    for t, nm in ((kc, "kc"), (vc, "vc")):
+        if t.dtype != torch.float16:
+            raise ValueError(f"{nm} must be float16")
+        _need(t, 2 * nkv * stride * hd, nm)
+    if dyn.dtype != torch.int32 or dyn.numel() < 1 or not dyn.is_cuda:
+        raise ValueError("dyn must be a device int32 tensor holding the position")
+
+
+def prepkv(qkv, knw, cosb, sinb, kc, vc, *, nkv: int, hd: int, koff: int, voff: int, keqv: bool, stride: int,
+           window: int, dyn: torch.Tensor) -> None:
+    """Write this token's normed+roped K and normed V of every KV head into
+    the fp16 caches at slot dyn[0] (mod window for a ring)."""
+    _f32(qkv, max(koff, koff if keqv else voff) + nkv * hd, "qkv")
+    _f32(knw, hd, "knw")
+    _f32(cosb, hd, "cosb")
+    _f32(sinb, hd, "sinb")
+    _kv_checks(kc, vc, nkv, stride, hd, dyn)
+    call("q4_prepkv", _p(qkv), _p(knw), _p(cosb), _p(sinb), _p(kc), _p(vc), nkv, hd, koff, voff, int(bool(keqv)),
+         stride, window, _p(dyn), _stream())
+
+
+def attn_workspace(nH: int, hd: int, stride: int, device="cuda") -> torch.Tensor:
+    """Scratch of q4_attn for this shape (no initialisation needed)."""
+    n = int(lib().q4_attn_workspace_bytes(nH, hd, stride))
+    return torch.empty(max(n, 4) // 4, dtype=torch.float32, device=device)
+
+
+def attn(qkv, qnw, cosb, sinb, kc, vc, out=None, *, nH: int, nkv: int, hd: int, stride: int, window: int,
+         qoff: int, grp: int, dyn: torch.Tensor, ws: torch.Tensor | None = None) -> torch.Tensor:
+    """Decode attention of nH query heads over the cached keys (softmax of
+    q.k, no score scaling); out[nH * hd] fp32."""
+    _f32(qkv, qoff + nH * hd, "qkv")
+    _f32(qnw, hd, "qnw")
+    _f32(cosb, hd, "cosb")
+    _f32(sinb, hd, "sinb")
+    _kv_checks(kc, vc, nkv, stride, hd, dyn)
+    out = torch.empty(nH * hd, dtype=torch.float32, device=qkv.device) if out is None else out
+    _f32(out, nH * hd, "out")
+    if ws is None:
+        if _CAPTURING[0]:
+            raise RuntimeError("attention inside a graph capture needs a workspace allocated before the capture")
+        ws = attn_workspace(nH, hd, stride, qkv.device)
+    call("q4_attn", _p(qkv), _p(qnw), _p(cosb), _p(sinb), _p(kc), _p(vc), _p(out), nH, nkv, hd, stride, window,
+         qoff, grp, _p(dyn), _p(ws), _nbytes(ws), _stream())
+    return out
+
+
 # ----------------------------------------------------------- graphs/waits
 class Graph:
     """A hipGraph captured from a stream: ``with g.capture(): ...`` then ``g.launch()``."""

@@ -206,6 +206,44 @@ int q4_gemm_w4a8(const int8_t* A, const uint32_t* wq, const uint16_t* ratio,
 int q4_cast_f32_f16(const float* src, uint16_t* dst, size_t n, void* stream);
 int q4_cast_f16_f32(const uint16_t* src, float* dst, size_t n, void* stream);
 
+/* ---- decode-token ops between the GEMVs ------------------------------------
+ * fp32 activations as in the reference; the KV cache is fp16
+ * [nkv][stride][hd] per layer (src/vk_engine.py:204). The token position is
+ * read from device memory (dyn[0], the reference's DYN buffer,
+ * src/vk_engine.py:306-310) so a captured graph replays every token. */
+
+/* y = x * inv * w, inv = 1/sqrt(mean(x^2) + 1e-6); y fp32 or fp16
+ * (y_dtype). vk/rmsnorm.comp:8-12 (normbg, src/vk_engine.py:227-228). */
+int q4_rmsnorm(const float* x, const float* w, void* y, int y_dtype, int D, void* stream);
+
+/* h = (h + x * inv * w) * scale (scale 0 = unscaled).
+ * vk/normadd.comp:8-12 (d_na / d_nas, src/vk_engine.py:242,248-249). */
+int q4_normadd(const float* x, const float* w, float* h, int D, float scale, void* stream);
+
+/* out = 0.5 g (1 + tanh(0.79788456 (g + 0.044715 g^3))) * up; out fp32 or
+ * fp16. vk/gelumul.comp:7-8 (d_gm, src/vk_engine.py:246). */
+int q4_gelumul(const float* gate, const float* up, void* out, int out_dtype, int n, void* stream);
+
+/* This token's K (k-norm with weight knw, RoPE with cosb/sinb) and V
+ * (v-norm; read at koff when keqv) of every KV head into cache slot
+ * dyn[0] % window (window > 0) or dyn[0]; nothing is written when the slot
+ * is past stride. vk/prepkv.comp:16-30 (d_prep, src/vk_engine.py:236-237). */
+int q4_prepkv(const float* qkv, const float* knw, const float* cosb, const float* sinb,
+              uint16_t* kc, uint16_t* vc, int nkv, int hd, int koff, int voff, int keqv,
+              int stride, int window, const uint32_t* dyn, void* stream);
+
+/* Decode attention of nH query heads (q at qoff in qkv; q-norm with qnw,
+ * RoPE) over the first T = dyn[0]+1 (or min(dyn[0]+1, window)) cached keys
+ * of KV head h/grp: softmax(q.k) weighted sum of V into out[nH*hd]. Split
+ * along the keys (two launches); ws: q4_attn_workspace_bytes(nH, hd, stride)
+ * bytes, no initialisation needed. vk/attn.comp:18-53 (d_attn,
+ * src/vk_engine.py:238-239). */
+size_t q4_attn_workspace_bytes(int nH, int hd, int stride);
+int q4_attn(const float* qkv, const float* qnw, const float* cosb, const float* sinb,
+            const uint16_t* kc, const uint16_t* vc, float* out, int nH, int nkv, int hd,
+            int stride, int window, int qoff, int grp, const uint32_t* dyn, void* ws,
+            size_t ws_bytes, void* stream);
+
 /* ---- record-once submit --------------------------------------------------
  * The per-token command buffer recorded once and resubmitted
  * (src/vk_engine.py:254-290, forward() :312-319) becomes a hipGraph captured

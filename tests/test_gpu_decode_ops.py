@@ -1,0 +1,178 @@
+"""GPU parity of the decode-token ops (rmsnorm, normadd, gelumul, prepkv,
+attention) against the oracle (oracle/decode_ops_oracle.py, float64).
+
+Tolerances (fp32 arithmetic against the float64 value of the shaders'
+formulas): normwise max|y - ref| / max|ref| <= 2e-6 for the fp32 norms and
+gelumul, <= 1e-3 for fp16 outputs, KV-cache entries within one fp16 ulp of
+the oracle's rounding (the fp32 value can sit on the other side of an fp16
+rounding boundary), attention normwise <= 1e-4 (scores of ~|q||k| without
+scaling amplify fp32 rounding in the softmax).
+"""
+import numpy as np
+import pytest
+import torch
+
+from oracle import decode_ops_oracle as D
+from oracle import q4_oracle as O
+
+pytestmark = pytest.mark.gpu
+
+
+def _t(a, dtype=torch.float32):
+    return torch.from_numpy(np.ascontiguousarray(a)).to(dtype).cuda()
+
+
+def _np(t):
+    torch.cuda.synchronize()
+    return t.detach().cpu().numpy()
+
+
+@pytest.mark.parametrize("D_", [3840, 15360, 100, 1])
+def test_rmsnorm(gpu, D_):
+    rng = np.random.default_rng(D_)
+    x = (rng.standard_normal(D_) * 3).astype(np.float32)
+    w = (rng.random(D_) + 0.5).astype(np.float32)
+    ref = D.rmsnorm_ref(x, w)
+    y = gpu.rmsnorm(_t(x), _t(w))
+    assert O.normwise_rel_err(_np(y), ref) <= 2e-6
+    yh = gpu.rmsnorm(_t(x), _t(w), y_dtype=torch.float16)
+    assert yh.dtype == torch.float16 and O.normwise_rel_err(_np(yh).astype(np.float64), ref) <= 1e-3
+
+
+@pytest.mark.parametrize("scale", [0.0, 0.37])
+def test_normadd(gpu, scale):
+    rng = np.random.default_rng(7)
+    x, h = rng.standard_normal((2, 3840)).astype(np.float32)
+    w = rng.random(3840).astype(np.float32)
+    ref = D.normadd_ref(x, w, h, scale)
+    ht = _t(h)
+    gpu.normadd(_t(x), _t(w), ht, scale)
+    assert O.normwise_rel_err(_np(ht), ref) <= 2e-6
+
+
+@pytest.mark.parametrize("n", [15360, 37])
+def test_gelumul(gpu, n):
+    rng = np.random.default_rng(n)
+    g = (rng.standard_normal(n) * 3).astype(np.float32)
+    u = rng.standard_normal(n).astype(np.float32)
+    ref = D.gelumul_ref(g, u)
+    assert O.normwise_rel_err(_np(gpu.gelumul(_t(g), _t(u))), ref) <= 2e-6
+    assert O.normwise_rel_err(_np(gpu.gelumul(_t(g), _t(u), out_dtype=torch.float16)).astype(np.float64), ref) <= 1e-3
+
+
+def _rope_tables(rng, hd):
+    ang = rng.random(hd // 2) * 6.0
+    return (np.concatenate([np.cos(ang), np.cos(ang)]).astype(np.float32),
+            np.concatenate([np.sin(ang), np.sin(ang)]).astype(np.float32))
+
+
+def _within_one_f16_ulp(got, ref):
+    g = got.astype(np.float64)
+    r = ref.astype(np.float16).astype(np.float64)
+    ulp = np.spacing(np.abs(ref).astype(np.float16)).astype(np.float64)
+    return np.all(np.abs(g - r) <= ulp)
+
+
+@pytest.mark.parametrize("hd,nkv,stride,window,pos,keqv", [(256, 8, 64, 64, 100, False), (512, 2, 300, 0, 257, True),
+                                                           (256, 8, 64, 64, 0, False)])
+def test_prepkv(gpu, hd, nkv, stride, window, pos, keqv):
+    rng = np.random.default_rng(hd + pos)
+    nq = 16 * hd
+    qkv = (rng.standard_normal(nq + 2 * nkv * hd) * 2).astype(np.float32)
+    knw = (rng.random(hd) + 0.5).astype(np.float32)
+    cs, sn = _rope_tables(rng, hd)
+    kc0 = rng.standard_normal(nkv * stride * hd).astype(np.float16)
+    vc0 = rng.standard_normal(nkv * stride * hd).astype(np.float16)
+    koff, voff = nq, nq + nkv * hd
+    rk, rv = D.prepkv_ref(qkv, knw, cs, sn, kc0, vc0, nkv=nkv, hd=hd, koff=koff, voff=voff, keqv=keqv,
+                          stride=stride, window=window, pos=pos)
+    kc, vc = _t(kc0, torch.float16), _t(vc0, torch.float16)
+    dyn = torch.tensor([pos, pos + 1, 0, 0], dtype=torch.int32, device="cuda")
+    gpu.prepkv(_t(qkv), _t(knw), _t(cs), _t(sn), kc, vc, nkv=nkv, hd=hd, koff=koff, voff=voff, keqv=keqv,
+               stride=stride, window=window, dyn=dyn)
+    gk, gv = _np(kc), _np(vc)
+    slot = D.kv_slot(pos, window)
+    rows = [h * stride + slot for h in range(nkv)]
+    mask = np.ones(nkv * stride, bool)
+    mask[rows] = False
+    assert np.array_equal(gk.reshape(-1, hd)[mask], kc0.reshape(-1, hd)[mask])  # other slots untouched
+    assert np.array_equal(gv.reshape(-1, hd)[mask], vc0.reshape(-1, hd)[mask])
+    # the written rows against the oracle's float64 values, within one fp16 ulp
+    vo = koff if keqv else voff
+    for h in range(nkv):
+        k = qkv[koff + h * hd: koff + (h + 1) * hd].astype(np.float64)
+        kref = D.rope_ref(k * D.rms_inv(k) * knw, cs, sn)
+        v = qkv[vo + h * hd: vo + (h + 1) * hd].astype(np.float64)
+        vref = v * D.rms_inv(v)
+        r = rows[h]
+        assert _within_one_f16_ulp(gk.reshape(-1, hd)[r], kref)
+        assert _within_one_f16_ulp(gv.reshape(-1, hd)[r], vref)
+        assert np.mean(gk.reshape(-1, hd)[r] == rk.reshape(-1, hd)[r]) > 0.99
+
+
+def _attn_case(rng, nH, nkv, hd, stride):
+    qkv = (rng.standard_normal(nH * hd + 2 * nkv * hd) * 2).astype(np.float32)
+    qnw = (rng.random(hd) * 0.2 + 0.05).astype(np.float32)   # scores of a few units, as after q/k norms
+    cs, sn = _rope_tables(rng, hd)
+    kc = rng.standard_normal(nkv * stride * hd).astype(np.float16)
+    vc = rng.standard_normal(nkv * stride * hd).astype(np.float16)
+    return qkv, qnw, cs, sn, kc, vc
+
+
+@pytest.mark.parametrize("nH,nkv,hd,stride,window,pos", [
+    (16, 8, 256, 1024, 1024, 0),      # one key
+    (16, 8, 256, 1024, 1024, 300),    # two splits, ragged
+    (16, 8, 256, 1024, 1024, 5000),   # ring full: T = window
+    (16, 2, 512, 2048, 0, 1500),      # global layer, hd 512, grp 8
+    (4, 4, 64, 40, 0, 39),            # tiny, last slot
+])
+def test_attn(gpu, nH, nkv, hd, stride, window, pos):
+    rng = np.random.default_rng(nH * hd + pos)
+    qkv, qnw, cs, sn, kc, vc = _attn_case(rng, nH, nkv, hd, stride)
+    kw = dict(nH=nH, hd=hd, stride=stride, window=window, qoff=0, grp=nH // nkv, pos=pos)
+    ref = D.attn_ref(qkv, qnw, cs, sn, kc, vc, **kw)
+    dyn = torch.tensor([pos, pos + 1, 0, 0], dtype=torch.int32, device="cuda")
+    out = gpu.attn(_t(qkv), _t(qnw), _t(cs), _t(sn), _t(kc, torch.float16), _t(vc, torch.float16), nH=nH, nkv=nkv,
+                   hd=hd, stride=stride, window=window, qoff=0, grp=nH // nkv, dyn=dyn)
+    got = _np(out)
+    assert O.normwise_rel_err(got, ref) <= 1e-4
+    assert O.cosine(got, ref) > 0.999999
+
+
+def test_prepkv_attn_graph_replay_follows_position(gpu):
+    """prepkv + attention captured once; the position lives in device memory
+    and advances between replays (as the engine's DYN buffer does). Every
+    replay matches the eager result of the same position bit for bit, and
+    the oracle."""
+    rng = np.random.default_rng(11)
+    nH, nkv, hd, stride, window = 8, 4, 256, 512, 512
+    qkv, qnw, cs, sn, kc0, vc0 = _attn_case(rng, nH, nkv, hd, stride)
+    knw = (rng.random(hd) + 0.5).astype(np.float32)
+    koff, voff = nH * hd, nH * hd + nkv * hd
+    args = dict(nkv=nkv, hd=hd, koff=koff, voff=voff, keqv=False, stride=stride, window=window)
+    akw = dict(nH=nH, nkv=nkv, hd=hd, stride=stride, window=window, qoff=0, grp=nH // nkv)
+    t_qkv, t_knw, t_qnw, t_cs, t_sn = _t(qkv), _t(knw), _t(qnw), _t(cs), _t(sn)
+    kc, vc = _t(kc0, torch.float16), _t(vc0, torch.float16)
+    kc_e, vc_e = kc.clone(), vc.clone()
+    dyn = torch.zeros(4, dtype=torch.int32, device="cuda")
+    dyn_e = torch.zeros(4, dtype=torch.int32, device="cuda")
+    ws = gpu.attn_workspace(nH, hd, stride)
+    out = torch.empty(nH * hd, device="cuda")
+    g = gpu.Graph()
+    with g.capture():
+        gpu.prepkv(t_qkv, t_knw, t_cs, t_sn, kc, vc, dyn=dyn, **args)
+        gpu.attn(t_qkv, t_qnw, t_cs, t_sn, kc, vc, out, dyn=dyn, ws=ws, **akw)
+    for pos in [0, 1, 255, 256, 600]:
+        dyn.copy_(torch.tensor([pos, pos + 1, 0, 0], dtype=torch.int32))
+        dyn_e.copy_(dyn)
+        torch.cuda.synchronize()
+        g.launch()
+        torch.cuda.synchronize()
+        gpu.prepkv(t_qkv, t_knw, t_cs, t_sn, kc_e, vc_e, dyn=dyn_e, **args)
+        oe = gpu.attn(t_qkv, t_qnw, t_cs, t_sn, kc_e, vc_e, dyn=dyn_e, **akw)
+        torch.cuda.synchronize()
+        assert torch.equal(out, oe) and torch.equal(kc, kc_e) and torch.equal(vc, vc_e), pos
+        ref = D.attn_ref(qkv, qnw, cs, sn, _np(kc), _np(vc), nH=nH, hd=hd, stride=stride, window=window, qoff=0,
+                         grp=nH // nkv, pos=pos)
+        assert O.normwise_rel_err(_np(out), ref) <= 1e-4, pos
+    g.destroy()
