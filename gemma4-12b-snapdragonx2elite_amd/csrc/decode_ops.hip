@@ -15,20 +15,21 @@
 //    kernels, so a captured graph replays every token without updates (the
 //    reference's DYN uniform buffer, src/vk_engine.py:306-310).
 //  * Attention is split along the cached keys (flash-decoding): workgroup
-//    (head, split) scores up to ATT_CH keys, one key per thread (the q row
-//    broadcast from LDS, 16-byte fp16 key loads), forms its chunk's softmax
-//    numerator and running max, and accumulates p V with coalesced V-row
-//    reads; a second kernel merges the splits' (max, sum, accumulator)
-//    triples. The grid covers the cache capacity and splits past the
-//    current length exit at once, so the launch shape does not depend on
-//    the position.
+//    (head, split) takes ATT_CH = 64 keys, 16 per wave, reads each key and
+//    value row with one coalesced wave access (all 16 rows of a wave in
+//    flight at once), forms its chunk's softmax numerator and maximum and
+//    the unnormalised p V; a second kernel merges the splits' (max, sum,
+//    accumulator) triples. The grid covers the cache capacity and splits
+//    past the current length exit at once, so the launch shape does not
+//    depend on the position; 64-key splits put a 1024-key window of 16
+//    heads on 256 workgroups.
 #include "q4mi_common.h"
 
 namespace q4 {
 
 constexpr int NORM_THREADS = 1024;
 constexpr int ATT_THREADS = 256;
-constexpr int ATT_CH = 256;       // keys per attention split (one per thread)
+constexpr int ATT_CH = 64;        // keys per attention split (16 per wave)
 constexpr int ATT_MAX_HD = 512;   // head dims up to 512 (global layers)
 constexpr float NORM_EPS = 1e-6f;
 
@@ -147,89 +148,155 @@ __device__ inline int att_len(uint32_t pos, int window, int stride) {
   return (int)min(T, (long)stride);
 }
 
+// Loads of E halves (E = 1, 2, 4, 8) as one 2/4/8/16-byte access.
+template <int E>
+struct HalfVec {
+  uint16_t h[E];
+};
+template <int E>
+__device__ inline HalfVec<E> ld_halves(const uint16_t* p) {
+  HalfVec<E> r;
+  if constexpr (E == 8) {
+    const v4u u = *reinterpret_cast<const v4u*>(p);
+    __builtin_memcpy(r.h, &u, 16);
+  } else if constexpr (E == 4) {
+    const v2u u = *reinterpret_cast<const v2u*>(p);
+    __builtin_memcpy(r.h, &u, 8);
+  } else if constexpr (E == 2) {
+    const uint32_t u = *reinterpret_cast<const uint32_t*>(p);
+    __builtin_memcpy(r.h, &u, 4);
+  } else {
+    r.h[0] = *p;
+  }
+  return r;
+}
+
 // Split blockIdx.y of head blockIdx.x: keys [ATT_CH y, ATT_CH (y+1)) of the
-// current length. Writes (max, sum, unnormalised accumulator[hd]) to ws.
+// current length, hd = 64 EPL. Wave w takes keys 16 w .. 16 w + 15 of the
+// split. Scores: a key row (128 EPL bytes) is read by LPK = 8 EPL lanes, 16
+// bytes each, so one wave load covers 64 / LPK whole rows (coalesced) and
+// the wave's 16 rows are all in flight at once; each lane keeps its 8
+// elements of q in registers and the row's lanes reduce with xor-shuffles.
+// p V: lane l owns elements EPL l .. EPL l + EPL - 1, one coalesced load
+// per key, the wave's 16 keys in flight at once. Keys past the length read
+// the last live row (in bounds) with weight 0. Writes (max, sum,
+// unnormalised accumulator[hd]) to ws.
+template <int EPL>
 __global__ void __launch_bounds__(ATT_THREADS) attn_split_kernel(const float* __restrict__ qkv, const float* __restrict__ qnw,
                                                                  const float* __restrict__ cs, const float* __restrict__ sn,
                                                                  const uint16_t* __restrict__ kc,
-                                                                 const uint16_t* __restrict__ vc, int hd, int stride,
+                                                                 const uint16_t* __restrict__ vc, int stride,
                                                                  int window, int qoff, int grp,
                                                                  const uint32_t* __restrict__ dyn,
                                                                  float* __restrict__ ws) {
-  __shared__ float qv[ATT_MAX_HD], qr[ATT_MAX_HD], p[ATT_CH], red[ATT_THREADS / 64];
-  __shared__ float accp[ATT_THREADS / 64][ATT_MAX_HD];
+  constexpr int HD = 64 * EPL, LPK = 8 * EPL, KPI = 64 / LPK, KPW = ATT_CH / (ATT_THREADS / 64);
+  constexpr int NI = KPW / KPI;  // score loads per wave
+  __shared__ float qv[HD], qr[HD], p[ATT_CH], red[ATT_THREADS / 64];
+  __shared__ float accp[ATT_THREADS / 64][HD];
   const int h = blockIdx.x, sp = blockIdx.y, t = threadIdx.x;
   const int T = att_len(dyn[0], window, stride);
   const int j0 = sp * ATT_CH;
   if (j0 >= T) return;  // past the current length: the merge reads only the live splits
   const int n = min(ATT_CH, T - j0);
   const int kvh = h / grp;
+  const int wave = t >> 6, lane = t & 63;
 
   // q: norm with weight, RoPE (vk/attn.comp:23-30)
-  for (int i = t; i < hd; i += ATT_THREADS) qv[i] = qkv[qoff + h * hd + i];
+  for (int i = t; i < HD; i += ATT_THREADS) qv[i] = qkv[qoff + h * HD + i];
   __syncthreads();
-  norm_rope_head(qv, qr, qnw, cs, sn, hd, red);
+  norm_rope_head(qv, qr, qnw, cs, sn, HD, red);
 
-  // scores, one key per thread: q . k_j, 8 fp16 per 16-byte load
-  float s = -INFINITY;
-  if (t < n) {
-    const v4u* kr = reinterpret_cast<const v4u*>(kc + ((long)kvh * stride + j0 + t) * hd);
-    float d = 0.0f;
-    for (int c = 0; c < hd / 8; ++c) {
-      const v4u u = kr[c];
+  const long kv0 = (long)kvh * stride * HD;
+  {
+    const int kk = lane / LPK, ch = lane % LPK;
+    float q8[8];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) q8[e] = qr[8 * ch + e];
+    v4u u[NI];
+#pragma unroll
+    for (int b = 0; b < NI; ++b) {
+      const int j = min(j0 + KPW * wave + KPI * b + kk, T - 1);
+      u[b] = *reinterpret_cast<const v4u*>(kc + kv0 + (long)j * HD + 8 * ch);
+    }
+#pragma unroll
+    for (int b = 0; b < NI; ++b) {
+      float d = 0.0f;
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
-        d = fmaf(qr[8 * c + 2 * e], h2f((uint16_t)(u[e] & 0xFFFFu)), d);
-        d = fmaf(qr[8 * c + 2 * e + 1], h2f((uint16_t)(u[e] >> 16)), d);
+        d = fmaf(q8[2 * e], h2f((uint16_t)(u[b][e] & 0xFFFFu)), d);
+        d = fmaf(q8[2 * e + 1], h2f((uint16_t)(u[b][e] >> 16)), d);
       }
+#pragma unroll
+      for (int o = LPK / 2; o > 0; o >>= 1) d += __shfl_xor(d, o, 64);
+      const int key = KPW * wave + KPI * b + kk;
+      if (ch == 0) p[key] = key < n ? d : -INFINITY;
     }
-    s = d;
   }
-  const float m = block_max(s, red);
-  const float pj = t < n ? expf(s - m) : 0.0f;
-  p[t] = pj;
+  __syncthreads();
+  const float s = p[t < ATT_CH ? t : 0];
+  const float m = block_max(t < ATT_CH ? s : -INFINITY, red);
+  const float pj = (t < ATT_CH && s != -INFINITY) ? expf(s - m) : 0.0f;
+  __syncthreads();
+  if (t < ATT_CH) p[t] = pj;
   const float l = block_sum(pj, red);  // (its barriers also publish p)
 
-  // p V: wave w takes keys w, w+4, ...; lanes cover hd (coalesced V rows)
-  const int wave = t >> 6, lane = t & 63;
-  float a[ATT_MAX_HD / 64];
+  float a[EPL];
 #pragma unroll
-  for (int r = 0; r < ATT_MAX_HD / 64; ++r) a[r] = 0.0f;
-  for (int j = wave; j < n; j += ATT_THREADS / 64) {
-    const uint16_t* vr = vc + ((long)kvh * stride + j0 + j) * hd;
-    const float pw = p[j];
+  for (int e = 0; e < EPL; ++e) a[e] = 0.0f;
+  {
+    HalfVec<EPL> v[KPW];
 #pragma unroll
-    for (int r = 0; r < ATT_MAX_HD / 64; ++r)
-      if (64 * r + lane < hd) a[r] = fmaf(pw, h2f(vr[64 * r + lane]), a[r]);
+    for (int k = 0; k < KPW; ++k) {
+      const int j = min(j0 + KPW * wave + k, T - 1);
+      v[k] = ld_halves<EPL>(vc + kv0 + (long)j * HD + EPL * lane);
+    }
+#pragma unroll
+    for (int k = 0; k < KPW; ++k) {
+      const float pw = p[KPW * wave + k];
+#pragma unroll
+      for (int e = 0; e < EPL; ++e) a[e] = fmaf(pw, h2f(v[k].h[e]), a[e]);
+    }
   }
 #pragma unroll
-  for (int r = 0; r < ATT_MAX_HD / 64; ++r)
-    if (64 * r + lane < hd) accp[wave][64 * r + lane] = a[r];
+  for (int e = 0; e < EPL; ++e) accp[wave][EPL * lane + e] = a[e];
   __syncthreads();
-  float* out = ws + ((long)h * gridDim.y + sp) * (hd + 2);
+  float* out = ws + ((long)h * gridDim.y + sp) * (HD + 2);
   if (t == 0) {
     out[0] = m;
     out[1] = l;
   }
-  for (int i = t; i < hd; i += ATT_THREADS) out[2 + i] = ((accp[0][i] + accp[1][i]) + accp[2][i]) + accp[3][i];
+  for (int i = t; i < HD; i += ATT_THREADS) out[2 + i] = ((accp[0][i] + accp[1][i]) + accp[2][i]) + accp[3][i];
 }
 
-// out[h] = sum_c acc_c exp(m_c - M) / sum_c l_c exp(m_c - M) over the live splits
-__global__ void __launch_bounds__(ATT_THREADS) attn_merge_kernel(const float* __restrict__ ws, float* __restrict__ out,
+// out[h] = sum_c acc_c w_c / sum_c l_c w_c, w_c = exp(m_c - M), over the
+// live splits (weights staged in LDS: ns floats of dynamic shared memory);
+// out fp32 or fp16
+template <int YT>
+__global__ void __launch_bounds__(ATT_THREADS) attn_merge_kernel(const float* __restrict__ ws, void* __restrict__ out,
                                                                  int hd, int nsplit, int stride, int window,
                                                                  const uint32_t* __restrict__ dyn) {
+  extern __shared__ float wsh[];
+  __shared__ float red[ATT_THREADS / 64];
   const int h = blockIdx.x, t = threadIdx.x;
   const int T = att_len(dyn[0], window, stride);
   const int ns = (T + ATT_CH - 1) / ATT_CH;
   const float* w = ws + (long)h * nsplit * (hd + 2);
   float M = -INFINITY;
-  for (int c = 0; c < ns; ++c) M = fmaxf(M, w[(long)c * (hd + 2)]);
+  for (int c = t; c < ns; c += ATT_THREADS) M = fmaxf(M, w[(long)c * (hd + 2)]);
+  M = block_max(M, red);
   float L = 0.0f;
-  for (int c = 0; c < ns; ++c) L = fmaf(w[(long)c * (hd + 2) + 1], expf(w[(long)c * (hd + 2)] - M), L);
+  for (int c = t; c < ns; c += ATT_THREADS) {
+    const float wc = expf(w[(long)c * (hd + 2)] - M);
+    wsh[c] = wc;
+    L = fmaf(w[(long)c * (hd + 2) + 1], wc, L);
+  }
+  L = block_sum(L, red);  // (its barriers also publish wsh)
   for (int i = t; i < hd; i += ATT_THREADS) {
     float a = 0.0f;
-    for (int c = 0; c < ns; ++c) a = fmaf(w[(long)c * (hd + 2) + 2 + i], expf(w[(long)c * (hd + 2)] - M), a);
-    out[h * hd + i] = a / L;
+    for (int c = 0; c < ns; ++c) a = fmaf(w[(long)c * (hd + 2) + 2 + i], wsh[c], a);
+    const float v = a / L;
+    if constexpr (YT == Q4_DT_F16) reinterpret_cast<uint16_t*>(out)[h * hd + i] = f2h(v);
+    else reinterpret_cast<float*>(out)[h * hd + i] = v;
   }
 }
 
@@ -297,23 +364,39 @@ size_t q4_attn_workspace_bytes(int nH, int hd, int stride) {
 }
 
 int q4_attn(const float* qkv, const float* qnw, const float* cosb, const float* sinb, const uint16_t* kc,
-            const uint16_t* vc, float* out, int nH, int nkv, int hd, int stride, int window, int qoff, int grp,
-            const uint32_t* dyn, void* ws, size_t ws_bytes, void* stream) {
+            const uint16_t* vc, void* out, int out_dtype, int nH, int nkv, int hd, int stride, int window, int qoff,
+            int grp, const uint32_t* dyn, void* ws, size_t ws_bytes, void* stream) {
   clear_error();
   Q4_ARG(qkv && qnw && cosb && sinb && kc && vc && out && dyn && ws, "null pointer");
+  Q4_ARG(out_dtype == Q4_DT_F32 || out_dtype == Q4_DT_F16, "bad out_dtype");
   Q4_ARG(nH > 0 && nkv > 0 && grp > 0 && nH == nkv * grp, "need nH == nkv * grp (got %d, %d, %d)", nH, nkv, grp);
-  Q4_ARG(hd > 0 && hd % 8 == 0 && hd <= ATT_MAX_HD, "head dim must be a multiple of 8 and <= %d (got %d)",
-         ATT_MAX_HD, hd);
+  Q4_ARG(hd == 64 || hd == 128 || hd == 256 || hd == 512, "head dim must be 64, 128, 256 or 512 (got %d)", hd);
   Q4_ARG(stride > 0 && window >= 0 && window <= stride && qoff >= 0, "bad sizes");
   Q4_ARG(((uintptr_t)kc & 15) == 0, "kc must be 16-byte aligned");
   const size_t need = q4_attn_workspace_bytes(nH, hd, stride);
   Q4_ARG(ws_bytes >= need, "attention workspace too small: %zu < %zu bytes", ws_bytes, need);
   const int ns = attn_splits(stride);
-  hipLaunchKernelGGL(attn_split_kernel, dim3(nH, ns), dim3(ATT_THREADS), 0, as_stream(stream), qkv, qnw, cosb, sinb,
-                     kc, vc, hd, stride, window, qoff, grp, dyn, reinterpret_cast<float*>(ws));
+  const size_t msh = (size_t)ns * sizeof(float);
+  Q4_ARG(msh <= 64 * 1024, "cache depth %d needs %d attention splits (more than the merge stages)", stride, ns);
+  hipStream_t st = as_stream(stream);
+  float* wsf = reinterpret_cast<float*>(ws);
+  switch (hd) {
+    case 64: hipLaunchKernelGGL(attn_split_kernel<1>, dim3(nH, ns), dim3(ATT_THREADS), 0, st, qkv, qnw, cosb, sinb, kc, vc,
+                                stride, window, qoff, grp, dyn, wsf); break;
+    case 128: hipLaunchKernelGGL(attn_split_kernel<2>, dim3(nH, ns), dim3(ATT_THREADS), 0, st, qkv, qnw, cosb, sinb, kc, vc,
+                                 stride, window, qoff, grp, dyn, wsf); break;
+    case 256: hipLaunchKernelGGL(attn_split_kernel<4>, dim3(nH, ns), dim3(ATT_THREADS), 0, st, qkv, qnw, cosb, sinb, kc, vc,
+                                 stride, window, qoff, grp, dyn, wsf); break;
+    default: hipLaunchKernelGGL(attn_split_kernel<8>, dim3(nH, ns), dim3(ATT_THREADS), 0, st, qkv, qnw, cosb, sinb, kc, vc,
+                                stride, window, qoff, grp, dyn, wsf); break;
+  }
   Q4_LAUNCHED("attn_split");
-  hipLaunchKernelGGL(attn_merge_kernel, dim3(nH), dim3(ATT_THREADS), 0, as_stream(stream),
-                     reinterpret_cast<const float*>(ws), out, hd, ns, stride, window, dyn);
+  if (out_dtype == Q4_DT_F16)
+    hipLaunchKernelGGL(attn_merge_kernel<Q4_DT_F16>, dim3(nH), dim3(ATT_THREADS), msh, st, wsf, out, hd, ns, stride,
+                       window, dyn);
+  else
+    hipLaunchKernelGGL(attn_merge_kernel<Q4_DT_F32>, dim3(nH), dim3(ATT_THREADS), msh, st, wsf, out, hd, ns, stride,
+                       window, dyn);
   Q4_LAUNCHED("attn_merge");
   return Q4_OK;
 }

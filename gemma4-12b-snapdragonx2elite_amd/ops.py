@@ -419,22 +419,22 @@ def attn_workspace(nH: int, hd: int, stride: int, device="cuda") -> torch.Tensor
 
 
 def attn(qkv, qnw, cosb, sinb, kc, vc, out=None, *, nH: int, nkv: int, hd: int, stride: int, window: int,
-         qoff: int, grp: int, dyn: torch.Tensor, ws: torch.Tensor | None = None) -> torch.Tensor:
+         qoff: int, grp: int, dyn: torch.Tensor, ws: torch.Tensor | None = None, out_dtype=torch.float32):
     """Decode attention of nH query heads over the cached keys (softmax of
-    q.k, no score scaling); out[nH * hd] fp32."""
+    q.k, no score scaling); out[nH * hd] fp32 or fp16."""
     _f32(qkv, qoff + nH * hd, "qkv")
     _f32(qnw, hd, "qnw")
     _f32(cosb, hd, "cosb")
     _f32(sinb, hd, "sinb")
     _kv_checks(kc, vc, nkv, stride, hd, dyn)
-    out = torch.empty(nH * hd, dtype=torch.float32, device=qkv.device) if out is None else out
-    _f32(out, nH * hd, "out")
+    out = torch.empty(nH * hd, dtype=out_dtype, device=qkv.device) if out is None else out
+    _need(out, nH * hd * out.element_size(), "out")
     if ws is None:
         if _CAPTURING[0]:
             raise RuntimeError("attention inside a graph capture needs a workspace allocated before the capture")
         ws = attn_workspace(nH, hd, stride, qkv.device)
-    call("q4_attn", _p(qkv), _p(qnw), _p(cosb), _p(sinb), _p(kc), _p(vc), _p(out), nH, nkv, hd, stride, window,
-         qoff, grp, _p(dyn), _p(ws), _nbytes(ws), _stream())
+    call("q4_attn", _p(qkv), _p(qnw), _p(cosb), _p(sinb), _p(kc), _p(vc), _p(out), _dt(out), nH, nkv, hd, stride,
+         window, qoff, grp, _p(dyn), _p(ws), _nbytes(ws), _stream())
     return out
 
 

@@ -24,6 +24,11 @@ reference              here
 ``gemm_ds`` :351-365   same arguments/return shape ``(cin, gem, cout, N, K)``
 ``gmm(C, t, L, tag)``  ``C`` is a torch stream or None (current stream)
   :391-400
+``normbg`` :227-228,   :func:`normbg`, :func:`normadd_ds`, :func:`gelumul_ds`,
+``ds(LN/LP/LA, ..)``   :func:`prepkv_ds`, :func:`attn_ds` build the non-GEMV
+  :235-249             descriptors of a layer with the reference's buffers
+                       and uniforms; :func:`disp` enqueues one
+``buf_u32`` :71-73     same (the DYN position buffer is one)
 fence wait :293-302    :func:`submit` / :func:`wait` raise
                        ``RuntimeError('GPU fence TIMEOUT after ..ms at [..]')``
 =====================  ====================================================
@@ -252,6 +257,84 @@ def gmm(C, t, L=None, tag: str = "") -> None:
                 _run(op)
 
 
+# ------------------------------------------------- decode-token ops (non-GEMV)
+def buf_u32(vals) -> Buf:
+    """Small uint32 buffer (uniforms, the DYN position buffer), kept alive
+    for the process (src/vk_engine.py:71-73)."""
+    b = Buf(max(16, len(vals) * 4))
+    b.write(np.array(vals, np.uint32))
+    KEEP.append(b)
+    return b
+
+
+def _u32(du) -> np.ndarray:
+    """Words of a small uniform given as a Buf (read once, at descriptor time) or a sequence."""
+    if isinstance(du, Buf):
+        return np.frombuffer(du.read(16), np.uint32)
+    return np.asarray(list(du) + [0] * (4 - len(du)), np.uint32)
+
+
+class OpDesc(NamedTuple):
+    """A recorded non-GEMV dispatch: ``disp(d)`` enqueues it."""
+    fn: object
+    args: tuple
+    kw: dict
+
+
+def disp(d: OpDesc) -> None:
+    """Enqueue (or, inside :func:`record`, capture) one op descriptor
+    (the reference's ``disp``, src/vk_engine.py:265-269)."""
+    d.fn(*d.args, **d.kw)
+
+
+def _f32v(b: Buf, n: int, byte_off: int = 0) -> torch.Tensor:
+    return b.view(torch.float32, n, byte_off)
+
+
+def normbg(inbuf: Buf, wb: Buf, outbuf: Buf, du) -> OpDesc:
+    """RMS norm of ``du[0]`` floats of ``inbuf`` times ``wb`` into ``outbuf``
+    (src/vk_engine.py:227-228, vk/rmsnorm.comp)."""
+    D = int(_u32(du)[0])
+    return OpDesc(ops.rmsnorm, (_f32v(inbuf, D), _f32v(wb, D), _f32v(outbuf, D)), {})
+
+
+def normadd_ds(xbuf: Buf, wb: Buf, hbuf: Buf, du) -> OpDesc:
+    """``h = (h + norm(x) * w) * sc``, ``sc`` the float whose bits are
+    ``du[1]`` (0: unscaled) (d_na / d_nas, src/vk_engine.py:242,248-249)."""
+    u = _u32(du)
+    D, sc = int(u[0]), float(u[1:2].view(np.float32)[0])
+    return OpDesc(ops.normadd, (_f32v(xbuf, D), _f32v(wb, D), _f32v(hbuf, D), sc), {})
+
+
+def gelumul_ds(gate: Buf, up: Buf, out: Buf, du) -> OpDesc:
+    """``out = gelu_tanh(gate) * up`` over ``du[0]`` floats (d_gm, src/vk_engine.py:246)."""
+    n = int(_u32(du)[0])
+    return OpDesc(ops.gelumul, (_f32v(gate, n), _f32v(up, n), _f32v(out, n)), {})
+
+
+def prepkv_ds(qkv: Buf, knw: Buf, cosb: Buf, sinb: Buf, kc: Buf, vc: Buf, P, dyn: Buf) -> OpDesc:
+    """This token's K/V into the fp16 caches (d_prep, src/vk_engine.py:235-237);
+    ``P`` = (nkv, hd, koff, voff, keqv, stride, window, 0) in floats/slots."""
+    nkv, hd, koff, voff, keqv, stride, window = (int(v) for v in np.asarray(P, np.uint32)[:7])
+    kw = dict(nkv=nkv, hd=hd, koff=koff, voff=voff, keqv=bool(keqv), stride=stride, window=window,
+              dyn=dyn.view(torch.int32, 4))
+    return OpDesc(ops.prepkv, (qkv.view(torch.float32), _f32v(knw, hd), _f32v(cosb, hd), _f32v(sinb, hd),
+                               kc.view(torch.float16), vc.view(torch.float16)), kw)
+
+
+def attn_ds(qkv: Buf, qnw: Buf, cosb: Buf, sinb: Buf, kc: Buf, vc: Buf, out: Buf, A, dyn: Buf) -> OpDesc:
+    """Decode attention (d_attn, src/vk_engine.py:238-239); ``A`` = (nH, nkv,
+    hd, stride, window, qoff, grp, 0). The split-key scratch is allocated
+    here, before any recording."""
+    nH, nkv, hd, stride, window, qoff, grp = (int(v) for v in np.asarray(A, np.uint32)[:7])
+    ws = ops.attn_workspace(nH, hd, stride, qkv.t.device)
+    KEEP.append(ws)
+    kw = dict(nH=nH, nkv=nkv, hd=hd, stride=stride, window=window, qoff=qoff, grp=grp,
+              dyn=dyn.view(torch.int32, 4), ws=ws)
+    return OpDesc(ops.attn, (qkv.view(torch.float32), _f32v(qnw, hd), _f32v(cosb, hd), _f32v(sinb, hd),
+                             kc.view(torch.float16), vc.view(torch.float16), _f32v(out, nH * hd)), kw)
+
+
 # ------------------------------------------------------- record-once submit
 def record(body) -> ops.Graph:
     """Capture everything ``body()`` enqueues into one hipGraph
@@ -260,6 +343,32 @@ def record(body) -> ops.Graph:
     with g.capture():
         body()
     return g
+
+
+def record_decode(layers, d_fin: OpDesc, d_lm: GemvDesc) -> ops.Graph:
+    """Record one decode token in the reference's dispatch order
+    (src/vk_engine.py:274-287): per layer norm, q/k/v (one batched launch),
+    prepkv, attention, o, normadd, norm, gate/up (one launch), gelumul,
+    down, normadd (layer scale); then the final norm and lm_head. ``layers``
+    holds the reference's per-layer descriptor keys (``d_in``, ``d_q``,
+    ``d_k``, ``d_v`` (may be None), ``d_prep``, ``d_attn``, ``d_o``, ``d_na``,
+    ``d_pfn``, ``d_g``, ``d_u``, ``d_gm``, ``d_d``, ``d_nas``)."""
+    def body():
+        for L in layers:
+            disp(L["d_in"])
+            gemv_many([L["d_q"], L["d_k"]] + ([L["d_v"]] if L.get("d_v") is not None else []))
+            disp(L["d_prep"])
+            disp(L["d_attn"])
+            gemv(L["d_o"])
+            disp(L["d_na"])
+            disp(L["d_pfn"])
+            gemv_many([L["d_g"], L["d_u"]])
+            disp(L["d_gm"])
+            gemv(L["d_d"])
+            disp(L["d_nas"])
+        disp(d_fin)
+        gemv(d_lm)
+    return record(body)
 
 
 def wait(stream=None, label: str = "", timeout_ms: int | None = None) -> None:

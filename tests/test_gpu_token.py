@@ -1,0 +1,124 @@
+"""A whole decode token through the engine mirror (vk_engine.py): a small
+Gemma-style model (one sliding-window layer, one global k==v layer) built
+with the reference's descriptor helpers, recorded once in the reference's
+dispatch order (src/vk_engine.py:274-287) and replayed per token with the
+position and RoPE tables written to device buffers, against the oracle's
+token step (oracle GEMV on the same int4 codes and fp16 scales, oracle
+decode ops, fp16 KV caches carried along).
+
+Tolerance: logits normwise max|y - ref| / max|ref| <= 1e-3 over 20 tokens
+(the ring of the sliding layer wraps at 16), fp32 device arithmetic against
+float64.
+"""
+import importlib
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import decode_ops_oracle as D
+from oracle import q4_oracle as O
+
+pytestmark = pytest.mark.gpu
+
+H, NH, I, V = 256, 4, 512, 1024
+LAYERS = [dict(hd=64, nkv=2, keqv=False, window=16, stride=16, scl=0.5),
+          dict(hd=128, nkv=1, keqv=True, window=0, stride=64, scl=1.0)]
+
+
+def _rope(pos, hd):
+    inv = 1.0 / (10000.0 ** (np.arange(0, hd, 2) / hd))
+    ang = pos * inv
+    return (np.concatenate([np.cos(ang)] * 2).astype(np.float32), np.concatenate([np.sin(ang)] * 2).astype(np.float32))
+
+
+def test_decode_token_through_the_engine_mirror(g4, gpu):
+    E = importlib.import_module("g4mi.vk_engine")
+    rng = np.random.default_rng(0)
+    f32 = lambda a: np.asarray(a, np.float32)
+
+    def lin(N, K):
+        W = f32(rng.standard_normal((N, K)) * (1.0 / np.sqrt(K)))
+        q, sc = O.quant_codes(W)
+        return E.quant(W, pf=False, fp8=False, prefill_i8=False), (N, K), (q, sc.astype(np.float16).astype(np.float32))
+
+    def wbuf(a):
+        b = E.Buf(f32(a).nbytes)
+        b.write(f32(a))
+        return b
+
+    fb = lambda n: E.Buf(n * 4)
+    maxq = max(NH * L["hd"] for L in LAYERS)
+    B = {k: fb(n) for k, n in dict(h=H, normed=H, normed2=H, o=H, down=H, normed_f=H, attn=maxq, gate=I, up=I,
+                                   act=I, logits=V, qkv=maxq + 2 * 2 * 128).items()}
+    cosb = {hd: fb(hd) for hd in (64, 128)}
+    sinb = {hd: fb(hd) for hd in (64, 128)}
+    DYN = E.buf_u32([0, 0, 0, 0])
+    DUH, DUI = E.buf_u32([H, 0, 0, 0]), E.buf_u32([I, 0, 0, 0])
+    layers, ref_layers = [], []
+    for cfg in LAYERS:
+        hd, nkv, keqv = cfg["hd"], cfg["nkv"], cfg["keqv"]
+        nq, nk = NH * hd, nkv * hd
+        qp, kp = lin(nq, H), lin(nk, H)
+        vp = None if keqv else lin(nk, H)
+        op, gp, up, dp = lin(H, nq), lin(I, H), lin(I, H), lin(H, I)
+        norms = {k: f32(rng.random(n) + 0.5) for k, n in dict(qnw=hd, knw=hd, inw=H, paw=H, pfw=H, ofw=H).items()}
+        kc, vc = E.Buf(nkv * cfg["stride"] * hd * 2), E.Buf(nkv * cfg["stride"] * hd * 2)
+        nb = {k: wbuf(v) for k, v in norms.items()}
+        P = [nkv, hd, nq, nq + nk, int(keqv), cfg["stride"], cfg["window"], 0]
+        A = [NH, nkv, hd, cfg["stride"], cfg["window"], 0, NH // nkv, 0]
+        nas = E.buf_u32([H, int(np.array([cfg["scl"]], np.float32).view(np.uint32)[0]), 0, 0])
+        L = dict(d_in=E.normbg(B["h"], nb["inw"], B["normed"], DUH),
+                 d_q=E.gemv_ds(qp[:2], B["normed"], B["qkv"], 0),
+                 d_k=E.gemv_ds(kp[:2], B["normed"], B["qkv"], nq * 4),
+                 d_v=None if keqv else E.gemv_ds(vp[:2], B["normed"], B["qkv"], (nq + nk) * 4),
+                 d_prep=E.prepkv_ds(B["qkv"], nb["knw"], cosb[hd], sinb[hd], kc, vc, P, DYN),
+                 d_attn=E.attn_ds(B["qkv"], nb["qnw"], cosb[hd], sinb[hd], kc, vc, B["attn"], A, DYN),
+                 d_o=E.gemv_ds(op[:2], B["attn"], B["o"], 0),
+                 d_na=E.normadd_ds(B["o"], nb["paw"], B["h"], DUH),
+                 d_pfn=E.normbg(B["h"], nb["pfw"], B["normed2"], DUH),
+                 d_g=E.gemv_ds(gp[:2], B["normed2"], B["gate"], 0),
+                 d_u=E.gemv_ds(up[:2], B["normed2"], B["up"], 0),
+                 d_gm=E.gelumul_ds(B["gate"], B["up"], B["act"], DUI),
+                 d_d=E.gemv_ds(dp[:2], B["act"], B["down"], 0),
+                 d_nas=E.normadd_ds(B["down"], nb["ofw"], B["h"], nas))
+        layers.append(L)
+        ref_layers.append(dict(cfg, nq=nq, nk=nk, q=qp[2], k=kp[2], v=None if keqv else vp[2], o=op[2], g=gp[2],
+                               u=up[2], d=dp[2], kc=np.zeros(nkv * cfg["stride"] * hd, np.float16),
+                               vc=np.zeros(nkv * cfg["stride"] * hd, np.float16), **norms))
+    lm = lin(V, H)
+    finw = f32(rng.random(H) + 0.5)
+    d_fin = E.normbg(B["h"], wbuf(finw), B["normed_f"], DUH)
+    d_lm = E.gemv_ds(lm[:2], B["normed_f"], B["logits"], 0)
+    graph = E.record_decode(layers, d_fin, d_lm)
+
+    gv = lambda qs, x: O.gemv_ref(qs[0], qs[1], x).astype(np.float64)
+    for pos in range(20):
+        emb = f32(rng.standard_normal(H))
+        B["h"].write(emb)
+        DYN.write(np.array([pos, pos + 1, 0, 0], np.uint32))
+        tabs = {hd: _rope(pos, hd) for hd in (64, 128)}
+        for hd, (c, s) in tabs.items():
+            cosb[hd].write(c)
+            sinb[hd].write(s)
+        E.submit(graph, label=f"decode pos={pos}", timeout_ms=20000)
+        logits = np.frombuffer(B["logits"].read(V * 4), np.float32)
+
+        h = emb.astype(np.float64)
+        for R in ref_layers:
+            hd, nq, nk = R["hd"], R["nq"], R["nk"]
+            c, s = tabs[hd]
+            x = D.rmsnorm_ref(h, R["inw"])
+            qkv = np.concatenate([gv(R["q"], x), gv(R["k"], x)] + ([] if R["keqv"] else [gv(R["v"], x)]))
+            R["kc"], R["vc"] = D.prepkv_ref(qkv, R["knw"], c, s, R["kc"], R["vc"], nkv=R["nkv"], hd=hd, koff=nq,
+                                            voff=nq + nk, keqv=R["keqv"], stride=R["stride"], window=R["window"],
+                                            pos=pos)
+            att = D.attn_ref(qkv, R["qnw"], c, s, R["kc"], R["vc"], nH=NH, hd=hd, stride=R["stride"],
+                             window=R["window"], qoff=0, grp=NH // R["nkv"], pos=pos)
+            h = D.normadd_ref(gv(R["o"], att), R["paw"], h)
+            x2 = D.rmsnorm_ref(h, R["pfw"])
+            act = D.gelumul_ref(gv(R["g"], x2), gv(R["u"], x2))
+            h = D.normadd_ref(gv(R["d"], act), R["ofw"], h, R["scl"])
+        ref = gv(lm[2], D.rmsnorm_ref(h, finw))
+        assert O.normwise_rel_err(logits, ref) <= 1e-3, pos
+    graph.destroy()
