@@ -204,14 +204,17 @@ def bench_gemv_single(ops, N: int, K: int, e4m3: bool, reps: int = 10):
             "frac_of_hbm_peak": round(per / us / 1e3 / HBM_PEAK_GBS, 4), "distinct_weight_sets": n}
 
 
-def bench_token_step(ops, steps: int, warmup: int, pos: int = 1023):
+def bench_token_step(ops, steps: int, warmup: int, pos: int = 1023, fast: bool = False):
     """A whole decode token through the engine mirror (vk_engine.py): the
     reference's per-layer dispatch order (norm, q/k/v, prepkv, attention, o,
     normadd, norm, gate/up, gelumul, down, normadd) for 48 layers of the
     decode-set shapes (16 query heads and 8 KV heads of 256, a 1024-slot
     sliding-window fp16 KV cache per layer) plus the final norm and
-    lm_head, fp32 activations as in the reference, recorded once and
-    replayed with the position in device memory. Synthetic int4 weights."""
+    lm_head, recorded once and replayed with the position in device
+    memory. Synthetic int4 weights. ``fast=False``: fp32 activations
+    everywhere and one launch per reference dispatch (the reference's
+    buffers); ``fast=True``: every normadd fused with the rmsnorm that
+    follows it and fp16 GEMV inputs (the residual stream stays fp32)."""
     import importlib
 
     import numpy as np
@@ -234,6 +237,7 @@ def bench_token_step(ops, steps: int, warmup: int, pos: int = 1023):
         return E.Buf(tensor=(torch.rand(n, device=dev, generator=gen) + lo).to(torch.float32))
 
     fb = lambda n: E.Buf(n * 4)
+    xdt = torch.float16 if fast else torch.float32
     B = {k: fb(n) for k, n in dict(h=H, normed=H, normed2=H, o=H, down=H, normed_f=H, attn=nq, gate=I, up=I, act=I,
                                    logits=V, qkv=nq + 2 * nk).items()}
     cosb, sinb = vec(hd, -0.5), vec(hd, -0.5)
@@ -247,24 +251,24 @@ def bench_token_step(ops, steps: int, warmup: int, pos: int = 1023):
         P = [nkv, hd, nq, nq + nk, 0, win, win, 0]
         A = [nH, nkv, hd, win, win, 0, nH // nkv, 0]
         layers.append(dict(
-            d_in=E.normbg(B["h"], vec(H), B["normed"], DUH),
-            d_q=E.gemv_ds(qw(nq, H), B["normed"], B["qkv"], 0),
-            d_k=E.gemv_ds(qw(nk, H), B["normed"], B["qkv"], nq * 4),
-            d_v=E.gemv_ds(qw(nk, H), B["normed"], B["qkv"], (nq + nk) * 4),
+            d_in=E.normbg(B["h"], vec(H), B["normed"], DUH, out_dtype=xdt),
+            d_q=E.gemv_ds(qw(nq, H), B["normed"], B["qkv"], 0, x_dtype=xdt),
+            d_k=E.gemv_ds(qw(nk, H), B["normed"], B["qkv"], nq * 4, x_dtype=xdt),
+            d_v=E.gemv_ds(qw(nk, H), B["normed"], B["qkv"], (nq + nk) * 4, x_dtype=xdt),
             d_prep=E.prepkv_ds(B["qkv"], vec(hd), cosb, sinb, kc, vc, P, DYN),
-            d_attn=E.attn_ds(B["qkv"], vec(hd, 0.05), cosb, sinb, kc, vc, B["attn"], A, DYN),
-            d_o=E.gemv_ds(qw(H, nq), B["attn"], B["o"], 0),
+            d_attn=E.attn_ds(B["qkv"], vec(hd, 0.05), cosb, sinb, kc, vc, B["attn"], A, DYN, out_dtype=xdt),
+            d_o=E.gemv_ds(qw(H, nq), B["attn"], B["o"], 0, x_dtype=xdt),
             d_na=E.normadd_ds(B["o"], vec(H), B["h"], DUH),
-            d_pfn=E.normbg(B["h"], vec(H), B["normed2"], DUH),
-            d_g=E.gemv_ds(qw(I, H), B["normed2"], B["gate"], 0),
-            d_u=E.gemv_ds(qw(I, H), B["normed2"], B["up"], 0),
-            d_gm=E.gelumul_ds(B["gate"], B["up"], B["act"], DUI),
-            d_d=E.gemv_ds(qw(H, I), B["act"], B["down"], 0),
+            d_pfn=E.normbg(B["h"], vec(H), B["normed2"], DUH, out_dtype=xdt),
+            d_g=E.gemv_ds(qw(I, H), B["normed2"], B["gate"], 0, x_dtype=xdt),
+            d_u=E.gemv_ds(qw(I, H), B["normed2"], B["up"], 0, x_dtype=xdt),
+            d_gm=E.gelumul_ds(B["gate"], B["up"], B["act"], DUI, out_dtype=xdt),
+            d_d=E.gemv_ds(qw(H, I), B["act"], B["down"], 0, x_dtype=xdt),
             d_nas=E.normadd_ds(B["down"], vec(H), B["h"], nas)))
-    d_fin = E.normbg(B["h"], vec(H), B["normed_f"], DUH)
-    d_lm = E.gemv_ds(qw(V, H), B["normed_f"], B["logits"], 0)
+    d_fin = E.normbg(B["h"], vec(H), B["normed_f"], DUH, out_dtype=xdt)
+    d_lm = E.gemv_ds(qw(V, H), B["normed_f"], B["logits"], 0, x_dtype=xdt)
     B["h"].write(np.ones(H, np.float32))
-    graph = E.record_decode(layers, d_fin, d_lm)
+    graph = E.record_decode(layers, d_fin, d_lm, fuse=fast)
     for _ in range(warmup):
         graph.launch()
     torch.cuda.synchronize()
@@ -277,17 +281,19 @@ def bench_token_step(ops, steps: int, warmup: int, pos: int = 1023):
     b.synchronize()
     ms = a.elapsed_time(b) / steps
     T = min(pos + 1, win)
-    wbytes = LAYERS * sum(gemv_bytes(N, K) + 2 * K for N, K in  # fp32 x: 2K more bytes than the fp16 count
-                          [(nq, H), (nk, H), (nk, H), (H, nq), (I, H), (I, H), (H, I)]) + gemv_bytes(V, H) + 2 * H
+    xb = 0 if fast else 1  # fp32 x: 2K more bytes than the fp16 count
+    wbytes = LAYERS * sum(gemv_bytes(N, K) + 2 * K * xb for N, K in
+                          [(nq, H), (nk, H), (nk, H), (H, nq), (I, H), (I, H), (H, I)]) + gemv_bytes(V, H) + 2 * H * xb
     kvbytes = LAYERS * 2 * nkv * T * hd * 2
     graph.destroy()
     del layers, B
     E.KEEP.clear()
     torch.cuda.empty_cache()
     return {"ms_per_token": round(ms, 4), "position": pos, "keys_attended": T,
+            "activations": "fp32 residual stream, fp16 GEMV inputs, fused norms" if fast else "fp32 (reference)",
             "weight_bytes": wbytes, "kv_cache_bytes_read": kvbytes,
             "GBps": round((wbytes + kvbytes) / (ms * 1e-3) / 1e9, 1),
-            "kernels_per_token": LAYERS * 12 + 2}
+            "kernels_per_token": LAYERS * (10 if fast else 12) + 2}
 
 
 def counter_workload(ops):
@@ -480,7 +486,8 @@ def main():
     dec = bench_decode(ops, args.steps, args.warmup)
     print(f"[bench] decode {dec['ms_per_step']:.3f} ms/token, {dec['GBps']:.0f} GB/s "
           f"(per-token {dec['ms_per_step_percentiles']})", flush=True)
-    tok = bench_token_step(ops, max(20, args.steps // 4), 5)
+    tok = {"reference_dispatches": bench_token_step(ops, max(20, args.steps // 4), 5),
+           "fused": bench_token_step(ops, max(20, args.steps // 4), 5, fast=True)}
     print(f"[bench] token step {tok}", flush=True)
     single = {"c1_15360x3840_f16_scales": bench_gemv_single(ops, I, H, False),
               "c3_15360x3840_e4m3_scales": bench_gemv_single(ops, I, H, True),

@@ -53,6 +53,7 @@ SIGNATURES = {
     "q4_cast_f16_f32": (_i, [_vp, _vp, _sz, _vp]),
     "q4_rmsnorm": (_i, [_vp, _vp, _vp, _i, _i, _vp]),
     "q4_normadd": (_i, [_vp, _vp, _vp, _i, _f, _vp]),
+    "q4_normadd_rmsnorm": (_i, [_vp, _vp, _vp, _i, _f, _vp, _vp, _i, _vp]),
     "q4_gelumul": (_i, [_vp, _vp, _vp, _i, _i, _vp]),
     "q4_prepkv": (_i, [_vp, _vp, _vp, _vp, _vp, _vp, _i, _i, _i, _i, _i, _i, _i, _vp, _vp]),
     "q4_attn_workspace_bytes": (_sz, [_i, _i, _i]),

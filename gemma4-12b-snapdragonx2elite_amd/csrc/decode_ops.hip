@@ -59,30 +59,93 @@ __device__ inline float block_max(float v, float* red) {
 
 __device__ inline float inv_rms(float sumsq, int D) { return 1.0f / sqrtf(sumsq / (float)D + NORM_EPS); }
 
+// Elements of a norm kernel: thread t holds elements t + NORM_THREADS r,
+// r < NORM_PER, in registers (every operand is loaded before the first
+// reduction, so the kernel makes one memory round trip, not one per
+// dependent step); longer vectors take a second, plain loop.
+constexpr int NORM_PER = 4;
+
+template <int YT>
+__device__ inline void store_y(void* y, int i, float v) {
+  if constexpr (YT == Q4_DT_F16) reinterpret_cast<uint16_t*>(y)[i] = f2h(v);
+  else reinterpret_cast<float*>(y)[i] = v;
+}
+
 // y = (x * inv) * w   (vk/rmsnorm.comp:8-12); y fp32 or fp16
 template <int YT>
 __global__ void __launch_bounds__(NORM_THREADS) rmsnorm_kernel(const float* __restrict__ x, const float* __restrict__ w,
                                                                void* __restrict__ y, int D) {
   __shared__ float red[NORM_THREADS / 64];
-  float s = 0.0f;
-  for (int i = threadIdx.x; i < D; i += NORM_THREADS) s = fmaf(x[i], x[i], s);
-  const float inv = inv_rms(block_sum(s, red), D);
-  for (int i = threadIdx.x; i < D; i += NORM_THREADS) {
-    const float v = __fmul_rn(__fmul_rn(x[i], inv), w[i]);
-    if constexpr (YT == Q4_DT_F16) reinterpret_cast<uint16_t*>(y)[i] = f2h(v);
-    else reinterpret_cast<float*>(y)[i] = v;
+  const int t = threadIdx.x;
+  float xv[NORM_PER], wv[NORM_PER];
+#pragma unroll
+  for (int r = 0; r < NORM_PER; ++r) {
+    const int i = t + NORM_THREADS * r;
+    xv[r] = i < D ? x[i] : 0.0f;
+    wv[r] = i < D ? w[i] : 0.0f;
   }
+  float s = 0.0f;
+#pragma unroll
+  for (int r = 0; r < NORM_PER; ++r) s = fmaf(xv[r], xv[r], s);
+  for (int i = t + NORM_THREADS * NORM_PER; i < D; i += NORM_THREADS) s = fmaf(x[i], x[i], s);
+  const float inv = inv_rms(block_sum(s, red), D);
+#pragma unroll
+  for (int r = 0; r < NORM_PER; ++r) {
+    const int i = t + NORM_THREADS * r;
+    if (i < D) store_y<YT>(y, i, __fmul_rn(__fmul_rn(xv[r], inv), wv[r]));
+  }
+  for (int i = t + NORM_THREADS * NORM_PER; i < D; i += NORM_THREADS)
+    store_y<YT>(y, i, __fmul_rn(__fmul_rn(x[i], inv), w[i]));
 }
 
-// h = (h + (x * inv) * w) * sc   (vk/normadd.comp:8-12)
+// h = (h + (x * inv) * w) * sc   (vk/normadd.comp:8-12); with FUSE, then
+// y = (h * inv2) * w2, the rmsnorm the reference records next on the new h
+// (src/vk_engine.py:242-243 and :248-249 followed by the next layer's :231
+// or the final norm :250), in the same workgroup: h never leaves registers.
+template <bool FUSE, int YT>
 __global__ void __launch_bounds__(NORM_THREADS) normadd_kernel(const float* __restrict__ x, const float* __restrict__ w,
-                                                               float* __restrict__ h, int D, float sc) {
+                                                               float* __restrict__ h, int D, float sc,
+                                                               const float* __restrict__ w2, void* __restrict__ y) {
   __shared__ float red[NORM_THREADS / 64];
+  const int t = threadIdx.x;
+  float xv[NORM_PER], wv[NORM_PER], hv[NORM_PER], w2v[NORM_PER];
+#pragma unroll
+  for (int r = 0; r < NORM_PER; ++r) {
+    const int i = t + NORM_THREADS * r;
+    xv[r] = i < D ? x[i] : 0.0f;
+    wv[r] = i < D ? w[i] : 0.0f;
+    hv[r] = i < D ? h[i] : 0.0f;
+    if constexpr (FUSE) w2v[r] = i < D ? w2[i] : 0.0f;
+  }
   float s = 0.0f;
-  for (int i = threadIdx.x; i < D; i += NORM_THREADS) s = fmaf(x[i], x[i], s);
+#pragma unroll
+  for (int r = 0; r < NORM_PER; ++r) s = fmaf(xv[r], xv[r], s);
+  for (int i = t + NORM_THREADS * NORM_PER; i < D; i += NORM_THREADS) s = fmaf(x[i], x[i], s);
   const float inv = inv_rms(block_sum(s, red), D);
-  for (int i = threadIdx.x; i < D; i += NORM_THREADS)
-    h[i] = __fmul_rn(__fadd_rn(h[i], __fmul_rn(__fmul_rn(x[i], inv), w[i])), sc);
+  float s2 = 0.0f;
+#pragma unroll
+  for (int r = 0; r < NORM_PER; ++r) {
+    const int i = t + NORM_THREADS * r;
+    hv[r] = __fmul_rn(__fadd_rn(hv[r], __fmul_rn(__fmul_rn(xv[r], inv), wv[r])), sc);
+    if (i < D) h[i] = hv[r];
+    s2 = fmaf(hv[r], hv[r], s2);  // padding elements are 0
+  }
+  for (int i = t + NORM_THREADS * NORM_PER; i < D; i += NORM_THREADS) {
+    const float v = __fmul_rn(__fadd_rn(h[i], __fmul_rn(__fmul_rn(x[i], inv), w[i])), sc);
+    h[i] = v;
+    s2 = fmaf(v, v, s2);
+  }
+  if constexpr (FUSE) {
+    const float inv2 = inv_rms(block_sum(s2, red), D);
+#pragma unroll
+    for (int r = 0; r < NORM_PER; ++r) {
+      const int i = t + NORM_THREADS * r;
+      if (i < D) store_y<YT>(y, i, __fmul_rn(__fmul_rn(hv[r], inv2), w2v[r]));
+    }
+    // (the tail was written to h by this thread above; it rereads its own writes)
+    for (int i = t + NORM_THREADS * NORM_PER; i < D; i += NORM_THREADS)
+      store_y<YT>(y, i, __fmul_rn(__fmul_rn(h[i], inv2), w2[i]));
+  }
 }
 
 // out = gelu_tanh(gate) * up   (vk/gelumul.comp:7-8); out fp32 or fp16
@@ -325,9 +388,26 @@ int q4_normadd(const float* x, const float* w, float* h, int D, float scale, voi
   clear_error();
   Q4_ARG(x && w && h, "null pointer");
   Q4_ARG(D > 0, "bad D=%d", D);
-  hipLaunchKernelGGL(normadd_kernel, dim3(1), dim3(NORM_THREADS), 0, as_stream(stream), x, w, h, D,
-                     scale == 0.0f ? 1.0f : scale);
+  hipLaunchKernelGGL((normadd_kernel<false, Q4_DT_F32>), dim3(1), dim3(NORM_THREADS), 0, as_stream(stream), x, w, h, D,
+                     scale == 0.0f ? 1.0f : scale, nullptr, nullptr);
   Q4_LAUNCHED("normadd");
+  return Q4_OK;
+}
+
+int q4_normadd_rmsnorm(const float* x, const float* w, float* h, int D, float scale, const float* w2, void* y,
+                       int y_dtype, void* stream) {
+  clear_error();
+  Q4_ARG(x && w && h && w2 && y, "null pointer");
+  Q4_ARG(D > 0, "bad D=%d", D);
+  Q4_ARG(y_dtype == Q4_DT_F32 || y_dtype == Q4_DT_F16, "bad y_dtype");
+  const float sc = scale == 0.0f ? 1.0f : scale;
+  if (y_dtype == Q4_DT_F16)
+    hipLaunchKernelGGL((normadd_kernel<true, Q4_DT_F16>), dim3(1), dim3(NORM_THREADS), 0, as_stream(stream), x, w, h, D,
+                       sc, w2, y);
+  else
+    hipLaunchKernelGGL((normadd_kernel<true, Q4_DT_F32>), dim3(1), dim3(NORM_THREADS), 0, as_stream(stream), x, w, h, D,
+                       sc, w2, y);
+  Q4_LAUNCHED("normadd_rmsnorm");
   return Q4_OK;
 }
 

@@ -379,6 +379,18 @@ def normadd(x: torch.Tensor, w: torch.Tensor, h: torch.Tensor, scale: float = 0.
     return h
 
 
+def normadd_rmsnorm(x: torch.Tensor, w: torch.Tensor, h: torch.Tensor, w2: torch.Tensor, scale: float = 0.0,
+                    y: torch.Tensor | None = None, y_dtype=torch.float32) -> torch.Tensor:
+    """:func:`normadd` then :func:`rmsnorm` of the new ``h`` with ``w2``, one launch; returns ``y``."""
+    D = x.numel()
+    for t, nm in ((x, "x"), (w, "w"), (h, "h"), (w2, "w2")):
+        _f32(t, D, nm)
+    y = torch.empty(D, dtype=y_dtype, device=x.device) if y is None else y
+    _need(y, D * y.element_size(), "y")
+    call("q4_normadd_rmsnorm", _p(x), _p(w), _p(h), D, C.c_float(scale), _p(w2), _p(y), _dt(y), _stream())
+    return y
+
+
 def gelumul(gate: torch.Tensor, up: torch.Tensor, out: torch.Tensor | None = None, out_dtype=torch.float32):
     """out = gelu_tanh(gate) * up (fp32 in)."""
     n = gate.numel()

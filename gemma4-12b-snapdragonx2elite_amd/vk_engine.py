@@ -142,14 +142,17 @@ class GemvDesc(NamedTuple):
     WGx: int
 
 
-def gemv_ds(qw, inbuf: Buf, outbuf: Buf, out_off: int = 0) -> GemvDesc:
-    """Bind a quantized matrix to fp32 input/output buffers (src/vk_engine.py:214-226)."""
+def gemv_ds(qw, inbuf: Buf, outbuf: Buf, out_off: int = 0, x_dtype=torch.float32) -> GemvDesc:
+    """Bind a quantized matrix to fp32 input/output buffers (src/vk_engine.py:214-226).
+    ``x_dtype=torch.float16`` reads an fp16 input buffer instead (written by a
+    producer with an fp16 output: :func:`normbg`, :func:`gelumul_ds`,
+    :func:`attn_ds`)."""
     (bw, bs, split, nblk, inv, _bs16, _w8, _sw8), (N, K) = qw
     fmt = SCALE_E4M3 if bs.t.dtype == torch.uint8 else SCALE_F16
     ws = ops.default_workspace(N, K, split, bw.t.device)
     if ws is not None:
         KEEP.append(ws)
-    x = inbuf.view(torch.float32, K)
+    x = inbuf.view(x_dtype, K)
     y = outbuf.view(torch.float32, N, out_off)
     dp = (x, bw.t, bs.t, fmt, inv, y, N, K, split, ws)
     return GemvDesc(dp, None, N, split, (N + 63) // 64)
@@ -173,7 +176,7 @@ def gemv_many(gs) -> None:
         x, _wq, sc, fmt, _inv, _y, _N, K, _split, _ws = g.dp
         last = groups[-1] if groups else None
         if (last is not None and len(last) < ops.GEMV_MAX_BATCH and last[0].dp[0].data_ptr() == x.data_ptr()
-                and last[0].dp[7] == K and last[0].dp[3] == fmt and last[0].dp[5].dtype == g.dp[5].dtype
+                and last[0].dp[0].dtype == x.dtype and last[0].dp[7] == K and last[0].dp[3] == fmt and last[0].dp[5].dtype == g.dp[5].dtype
                 and K <= ops.gemv_batch_max_k(x.dtype)):
             last.append(g)
         else:
@@ -291,11 +294,12 @@ def _f32v(b: Buf, n: int, byte_off: int = 0) -> torch.Tensor:
     return b.view(torch.float32, n, byte_off)
 
 
-def normbg(inbuf: Buf, wb: Buf, outbuf: Buf, du) -> OpDesc:
+def normbg(inbuf: Buf, wb: Buf, outbuf: Buf, du, out_dtype=torch.float32) -> OpDesc:
     """RMS norm of ``du[0]`` floats of ``inbuf`` times ``wb`` into ``outbuf``
-    (src/vk_engine.py:227-228, vk/rmsnorm.comp)."""
+    (src/vk_engine.py:227-228, vk/rmsnorm.comp); ``out_dtype`` fp32 (the
+    reference) or fp16."""
     D = int(_u32(du)[0])
-    return OpDesc(ops.rmsnorm, (_f32v(inbuf, D), _f32v(wb, D), _f32v(outbuf, D)), {})
+    return OpDesc(ops.rmsnorm, (_f32v(inbuf, D), _f32v(wb, D), outbuf.view(out_dtype, D)), {})
 
 
 def normadd_ds(xbuf: Buf, wb: Buf, hbuf: Buf, du) -> OpDesc:
@@ -306,10 +310,10 @@ def normadd_ds(xbuf: Buf, wb: Buf, hbuf: Buf, du) -> OpDesc:
     return OpDesc(ops.normadd, (_f32v(xbuf, D), _f32v(wb, D), _f32v(hbuf, D), sc), {})
 
 
-def gelumul_ds(gate: Buf, up: Buf, out: Buf, du) -> OpDesc:
+def gelumul_ds(gate: Buf, up: Buf, out: Buf, du, out_dtype=torch.float32) -> OpDesc:
     """``out = gelu_tanh(gate) * up`` over ``du[0]`` floats (d_gm, src/vk_engine.py:246)."""
     n = int(_u32(du)[0])
-    return OpDesc(ops.gelumul, (_f32v(gate, n), _f32v(up, n), _f32v(out, n)), {})
+    return OpDesc(ops.gelumul, (_f32v(gate, n), _f32v(up, n), out.view(out_dtype, n)), {})
 
 
 def prepkv_ds(qkv: Buf, knw: Buf, cosb: Buf, sinb: Buf, kc: Buf, vc: Buf, P, dyn: Buf) -> OpDesc:
@@ -322,7 +326,8 @@ def prepkv_ds(qkv: Buf, knw: Buf, cosb: Buf, sinb: Buf, kc: Buf, vc: Buf, P, dyn
                                kc.view(torch.float16), vc.view(torch.float16)), kw)
 
 
-def attn_ds(qkv: Buf, qnw: Buf, cosb: Buf, sinb: Buf, kc: Buf, vc: Buf, out: Buf, A, dyn: Buf) -> OpDesc:
+def attn_ds(qkv: Buf, qnw: Buf, cosb: Buf, sinb: Buf, kc: Buf, vc: Buf, out: Buf, A, dyn: Buf,
+            out_dtype=torch.float32) -> OpDesc:
     """Decode attention (d_attn, src/vk_engine.py:238-239); ``A`` = (nH, nkv,
     hd, stride, window, qoff, grp, 0). The split-key scratch is allocated
     here, before any recording."""
@@ -332,7 +337,7 @@ def attn_ds(qkv: Buf, qnw: Buf, cosb: Buf, sinb: Buf, kc: Buf, vc: Buf, out: Buf
     kw = dict(nH=nH, nkv=nkv, hd=hd, stride=stride, window=window, qoff=qoff, grp=grp,
               dyn=dyn.view(torch.int32, 4), ws=ws)
     return OpDesc(ops.attn, (qkv.view(torch.float32), _f32v(qnw, hd), _f32v(cosb, hd), _f32v(sinb, hd),
-                             kc.view(torch.float16), vc.view(torch.float16), _f32v(out, nH * hd)), kw)
+                             kc.view(torch.float16), vc.view(torch.float16), out.view(out_dtype, nH * hd)), kw)
 
 
 # ------------------------------------------------------- record-once submit
@@ -345,30 +350,53 @@ def record(body) -> ops.Graph:
     return g
 
 
-def record_decode(layers, d_fin: OpDesc, d_lm: GemvDesc) -> ops.Graph:
+def record_decode(layers, d_fin: OpDesc, d_lm: GemvDesc, fuse: bool = True) -> ops.Graph:
     """Record one decode token in the reference's dispatch order
     (src/vk_engine.py:274-287): per layer norm, q/k/v (one batched launch),
     prepkv, attention, o, normadd, norm, gate/up (one launch), gelumul,
     down, normadd (layer scale); then the final norm and lm_head. ``layers``
     holds the reference's per-layer descriptor keys (``d_in``, ``d_q``,
     ``d_k``, ``d_v`` (may be None), ``d_prep``, ``d_attn``, ``d_o``, ``d_na``,
-    ``d_pfn``, ``d_g``, ``d_u``, ``d_gm``, ``d_d``, ``d_nas``)."""
+    ``d_pfn``, ``d_g``, ``d_u``, ``d_gm``, ``d_d``, ``d_nas``).
+
+    With ``fuse`` (default), every normadd that is followed by an rmsnorm of
+    the same residual vector (the post-attention normadd and the MLP norm;
+    a layer's last normadd and the next layer's input norm or the final
+    norm) runs as one :func:`ops.normadd_rmsnorm` launch: two launches fewer
+    per layer, same arithmetic."""
+    seq = []
+    for L in layers:
+        seq += [L["d_in"], ("gemvs", [L["d_q"], L["d_k"]] + ([L["d_v"]] if L.get("d_v") is not None else [])),
+                L["d_prep"], L["d_attn"], ("gemvs", [L["d_o"]]), L["d_na"], L["d_pfn"],
+                ("gemvs", [L["d_g"], L["d_u"]]), L["d_gm"], ("gemvs", [L["d_d"]]), L["d_nas"]]
+    seq += [d_fin, ("gemvs", [d_lm])]
+    if fuse:
+        seq = _fuse_norms(seq)
+
     def body():
-        for L in layers:
-            disp(L["d_in"])
-            gemv_many([L["d_q"], L["d_k"]] + ([L["d_v"]] if L.get("d_v") is not None else []))
-            disp(L["d_prep"])
-            disp(L["d_attn"])
-            gemv(L["d_o"])
-            disp(L["d_na"])
-            disp(L["d_pfn"])
-            gemv_many([L["d_g"], L["d_u"]])
-            disp(L["d_gm"])
-            gemv(L["d_d"])
-            disp(L["d_nas"])
-        disp(d_fin)
-        gemv(d_lm)
+        for op in seq:
+            if isinstance(op, tuple) and op and op[0] == "gemvs":
+                gemv_many(op[1])
+            else:
+                disp(op)
     return record(body)
+
+
+def _fuse_norms(seq):
+    out, i = [], 0
+    while i < len(seq):
+        a = seq[i]
+        b = seq[i + 1] if i + 1 < len(seq) else None
+        if (isinstance(a, OpDesc) and isinstance(b, OpDesc) and a.fn is ops.normadd and b.fn is ops.rmsnorm
+                and a.args[2].data_ptr() == b.args[0].data_ptr() and a.args[2].numel() == b.args[0].numel()):
+            x, w, h, sc = a.args
+            _, w2, y = b.args
+            out.append(OpDesc(ops.normadd_rmsnorm, (x, w, h, w2, sc, y), {}))
+            i += 2
+        else:
+            out.append(a)
+            i += 1
+    return out
 
 
 def wait(stream=None, label: str = "", timeout_ms: int | None = None) -> None:

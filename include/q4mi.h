@@ -220,6 +220,14 @@ int q4_rmsnorm(const float* x, const float* w, void* y, int y_dtype, int D, void
  * vk/normadd.comp:8-12 (d_na / d_nas, src/vk_engine.py:242,248-249). */
 int q4_normadd(const float* x, const float* w, float* h, int D, float scale, void* stream);
 
+/* q4_normadd followed by q4_rmsnorm of the new h with weight w2 into y (fp32
+ * or fp16), in one launch: the normadd the reference records at the end of
+ * an attention or MLP block and the rmsnorm it records next on h
+ * (src/vk_engine.py:242-243, and :248-249 followed by the next layer's :231
+ * or the final norm :250). */
+int q4_normadd_rmsnorm(const float* x, const float* w, float* h, int D, float scale,
+                       const float* w2, void* y, int y_dtype, void* stream);
+
 /* out = 0.5 g (1 + tanh(0.79788456 (g + 0.044715 g^3))) * up; out fp32 or
  * fp16. vk/gelumul.comp:7-8 (d_gm, src/vk_engine.py:246). */
 int q4_gelumul(const float* gate, const float* up, void* out, int out_dtype, int n, void* stream);

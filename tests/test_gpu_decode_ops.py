@@ -39,15 +39,33 @@ def test_rmsnorm(gpu, D_):
     assert yh.dtype == torch.float16 and O.normwise_rel_err(_np(yh).astype(np.float64), ref) <= 1e-3
 
 
-@pytest.mark.parametrize("scale", [0.0, 0.37])
-def test_normadd(gpu, scale):
+@pytest.mark.parametrize("scale,n", [(0.0, 3840), (0.37, 3840), (0.5, 5000), (0.0, 100)])
+def test_normadd(gpu, scale, n):
     rng = np.random.default_rng(7)
-    x, h = rng.standard_normal((2, 3840)).astype(np.float32)
-    w = rng.random(3840).astype(np.float32)
+    x, h = rng.standard_normal((2, n)).astype(np.float32)
+    w = rng.random(n).astype(np.float32)
     ref = D.normadd_ref(x, w, h, scale)
     ht = _t(h)
     gpu.normadd(_t(x), _t(w), ht, scale)
     assert O.normwise_rel_err(_np(ht), ref) <= 2e-6
+
+
+@pytest.mark.parametrize("scale,n,ydt", [(0.0, 3840, torch.float32), (0.5, 3840, torch.float16),
+                                         (0.25, 5000, torch.float32), (0.0, 1, torch.float32)])
+def test_normadd_rmsnorm_fused(gpu, scale, n, ydt):
+    """One launch = normadd then rmsnorm of the new h: h as q4_normadd leaves
+    it (bit for bit), y against the oracle's rmsnorm of the oracle's h."""
+    rng = np.random.default_rng(n)
+    x, h = rng.standard_normal((2, n)).astype(np.float32)
+    w, w2 = (rng.random((2, n)) + 0.5).astype(np.float32)
+    href = D.normadd_ref(x, w, h, scale)
+    yref = D.rmsnorm_ref(href, w2)
+    ht, ht2 = _t(h), _t(h)
+    y = gpu.normadd_rmsnorm(_t(x), _t(w), ht, _t(w2), scale, y_dtype=ydt)
+    gpu.normadd(_t(x), _t(w), ht2, scale)
+    assert torch.equal(ht, ht2)
+    assert O.normwise_rel_err(_np(ht), href) <= 2e-6
+    assert O.normwise_rel_err(_np(y).astype(np.float64), yref) <= (2e-6 if ydt == torch.float32 else 1e-3)
 
 
 @pytest.mark.parametrize("n", [15360, 37])
