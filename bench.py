@@ -214,7 +214,8 @@ def bench_token_step(ops, steps: int, warmup: int, pos: int = 1023, fast: bool =
     memory. Synthetic int4 weights. ``fast=False``: fp32 activations
     everywhere and one launch per reference dispatch (the reference's
     buffers); ``fast=True``: every normadd fused with the rmsnorm that
-    follows it and fp16 GEMV inputs (the residual stream stays fp32)."""
+    follows it, gate/up interleaved with the gelumul in their GEMV's
+    epilogue, and fp16 GEMV inputs (the residual stream stays fp32)."""
     import importlib
 
     import numpy as np
@@ -250,6 +251,7 @@ def bench_token_step(ops, steps: int, warmup: int, pos: int = 1023, fast: bool =
             E.Buf(tensor=torch.randn(nkv * win * hd, device=dev, generator=gen).to(torch.float16))
         P = [nkv, hd, nq, nq + nk, 0, win, win, 0]
         A = [nH, nkv, hd, win, win, 0, nH // nkv, 0]
+        qg, qu = qw(I, H), qw(I, H)
         layers.append(dict(
             d_in=E.normbg(B["h"], vec(H), B["normed"], DUH, out_dtype=xdt),
             d_q=E.gemv_ds(qw(nq, H), B["normed"], B["qkv"], 0, x_dtype=xdt),
@@ -260,11 +262,15 @@ def bench_token_step(ops, steps: int, warmup: int, pos: int = 1023, fast: bool =
             d_o=E.gemv_ds(qw(H, nq), B["attn"], B["o"], 0, x_dtype=xdt),
             d_na=E.normadd_ds(B["o"], vec(H), B["h"], DUH),
             d_pfn=E.normbg(B["h"], vec(H), B["normed2"], DUH, out_dtype=xdt),
-            d_g=E.gemv_ds(qw(I, H), B["normed2"], B["gate"], 0, x_dtype=xdt),
-            d_u=E.gemv_ds(qw(I, H), B["normed2"], B["up"], 0, x_dtype=xdt),
+            d_g=E.gemv_ds(qg, B["normed2"], B["gate"], 0, x_dtype=xdt),
+            d_u=E.gemv_ds(qu, B["normed2"], B["up"], 0, x_dtype=xdt),
             d_gm=E.gelumul_ds(B["gate"], B["up"], B["act"], DUI, out_dtype=xdt),
             d_d=E.gemv_ds(qw(H, I), B["act"], B["down"], 0, x_dtype=xdt),
             d_nas=E.normadd_ds(B["down"], vec(H), B["h"], nas)))
+        if fast:  # gate/up interleaved once, gelumul in the GEMV epilogue; the separate copies are dropped
+            layers[-1]["d_gu"] = E.gate_up_ds(qg, qu, B["normed2"], B["act"], x_dtype=xdt, act_dtype=xdt)
+            layers[-1]["d_g"] = layers[-1]["d_u"] = None
+        del qg, qu
     d_fin = E.normbg(B["h"], vec(H), B["normed_f"], DUH, out_dtype=xdt)
     d_lm = E.gemv_ds(qw(V, H), B["normed_f"], B["logits"], 0, x_dtype=xdt)
     B["h"].write(np.ones(H, np.float32))
@@ -290,10 +296,11 @@ def bench_token_step(ops, steps: int, warmup: int, pos: int = 1023, fast: bool =
     E.KEEP.clear()
     torch.cuda.empty_cache()
     return {"ms_per_token": round(ms, 4), "position": pos, "keys_attended": T,
-            "activations": "fp32 residual stream, fp16 GEMV inputs, fused norms" if fast else "fp32 (reference)",
+            "activations": ("fp32 residual stream, fp16 GEMV inputs, fused norms, gelumul in the gate/up GEMV"
+                            if fast else "fp32 (reference)"),
             "weight_bytes": wbytes, "kv_cache_bytes_read": kvbytes,
             "GBps": round((wbytes + kvbytes) / (ms * 1e-3) / 1e9, 1),
-            "kernels_per_token": LAYERS * (10 if fast else 12) + 2}
+            "kernels_per_token": LAYERS * (9 if fast else 12) + 2}
 
 
 def counter_workload(ops):

@@ -154,10 +154,7 @@ __global__ void __launch_bounds__(256) gelumul_kernel(const float* __restrict__ 
                                                       void* __restrict__ out, int n) {
   const int i = blockIdx.x * 256 + threadIdx.x;
   if (i >= n) return;
-  const float x = gate[i];
-  const float inner = __fmul_rn(0.7978845608028654f, __fadd_rn(x, __fmul_rn(__fmul_rn(__fmul_rn(0.044715f, x), x), x)));
-  const float g = __fmul_rn(__fmul_rn(0.5f, x), __fadd_rn(1.0f, tanhf(inner)));
-  const float v = __fmul_rn(g, up[i]);
+  const float v = __fmul_rn(gelu_tanh(gate[i]), up[i]);
   if constexpr (YT == Q4_DT_F16) reinterpret_cast<uint16_t*>(out)[i] = f2h(v);
   else reinterpret_cast<float*>(out)[i] = v;
 }

@@ -124,6 +124,26 @@ __device__ inline int xcd_major(int b, int G) {
   return x * per + min(x, rem) + (b >> 3);
 }
 
+// Output of wave 0 (all 64 lanes call this; lanes with live hold row n):
+// y[n], or, for a gate/up matrix with interleaved rows (row 2i = gate row
+// i, row 2i + 1 = up row i), act[i] = gelu_tanh(y[2i]) * y[2i + 1]: the
+// pair sits in lanes r, r ^ 1 of the wave (R and the row group's first row
+// are even). This is vk/gelumul.comp applied in the GEMV's epilogue.
+template <int YT>
+__device__ inline void store_rows(void* __restrict__ yv, int n, float v, int N, bool live, int gated) {
+  int o = n;
+  if (gated) {
+    const float up = __shfl_xor(v, 1, 64);
+    if (n & 1) return;
+    v = __fmul_rn(gelu_tanh(v), up);
+    o = n >> 1;
+  }
+  if (live && n < N) {
+    if constexpr (YT == Q4_DT_F16) reinterpret_cast<uint16_t*>(yv)[o] = f2h(v);
+    else reinterpret_cast<float*>(yv)[o] = v;
+  }
+}
+
 // Rows [g*R, g*R + R) of one GEMV over the K slice s of split (the whole K
 // when split == 1). NP = row groups of the launch * R (split-K partial stride).
 //
@@ -139,7 +159,7 @@ __device__ __forceinline__ void gemv_rows(const void* __restrict__ xv, const uin
                                           const void* __restrict__ scv, float outscale, void* __restrict__ yv,
                                           int N, int nblk, int g, int s, int split, long NP,
                                           float* __restrict__ part, uint32_t* __restrict__ cnt,
-                                          uint32_t* __restrict__ smem, float (*red)[R]) {
+                                          uint32_t* __restrict__ smem, float (*red)[R], int gated) {
   constexpr bool XH = (XT == Q4_DT_F16);
   constexpr int SW = 64 / R;               // block slots per wave
   constexpr int S = SW * GEMV_WAVES;       // block slots per workgroup
@@ -249,10 +269,7 @@ __device__ __forceinline__ void gemv_rows(const void* __restrict__ xv, const uin
   float v = 0.0f;
   if (lane < R) v = (((red[0][r] + red[1][r]) + red[2][r]) + red[3][r]) * outscale;
   if (split == 1) {
-    if (lane < R && n < N) {
-      if constexpr (YT == Q4_DT_F16) reinterpret_cast<uint16_t*>(yv)[n] = f2h(v);
-      else reinterpret_cast<float*>(yv)[n] = v;
-    }
+    store_rows<YT>(yv, n, v, N, lane < R, gated);
     return;
   }
 
@@ -264,29 +281,26 @@ __device__ __forceinline__ void gemv_rows(const void* __restrict__ xv, const uin
   prev = __shfl(prev, 0, 64);
   if (prev != (uint32_t)(split - 1)) return;
   __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
-  if (lane < R) {
-    float t = 0.0f;
+  float t = 0.0f;
+  if (lane < R)
     for (int c = 0; c < split; ++c)
       t += __hip_atomic_load(part + (long)c * NP + n, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    if (n < N) {
-      if constexpr (YT == Q4_DT_F16) reinterpret_cast<uint16_t*>(yv)[n] = f2h(t);
-      else reinterpret_cast<float*>(yv)[n] = t;
-    }
-  }
+  store_rows<YT>(yv, n, t, N, lane < R, gated);
   if (lane == 0) __hip_atomic_store(&cnt[g], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
 template <int R, int U, int XT, int ST, int YT>
 __global__ void __launch_bounds__(GEMV_THREADS)
 gemv_kernel(const void* __restrict__ xv, const uint4* __restrict__ wq, const void* __restrict__ scv, float outscale,
-            void* __restrict__ yv, int N, int nblk, int split, float* __restrict__ part, uint32_t* __restrict__ cnt) {
+            void* __restrict__ yv, int N, int nblk, int split, float* __restrict__ part, uint32_t* __restrict__ cnt,
+            int gated) {
   extern __shared__ __attribute__((aligned(16))) uint32_t smem[];
   __shared__ float red[GEMV_WAVES][R];
   // split-K grids (small matrices only) keep the plain order: their row
   // groups are reduced through the workspace, not through L2 reuse
   const int g = gridDim.y == 1 ? xcd_major(blockIdx.x, gridDim.x) : blockIdx.x;
   gemv_rows<R, U, XT, ST, YT>(xv, wq, scv, outscale, yv, N, nblk, g, blockIdx.y, split, (long)gridDim.x * R, part,
-                              cnt, smem, red);
+                              cnt, smem, red, gated);
 }
 
 // Several GEMVs over one x (same K and types) in one launch: segment i owns
@@ -329,10 +343,10 @@ gemv_batch_kernel(const void* __restrict__ xv, int nblk, const GemvSegs segs) {
       g0 = segs.s[t - 1].g_end;
     }
   }
-  gemv_rows<R, U, XT, ST, YT>(xv, wq, sc, os, y, N, nblk, g - g0, 0, 1, 0, nullptr, nullptr, smem, red);
+  gemv_rows<R, U, XT, ST, YT>(xv, wq, sc, os, y, N, nblk, g - g0, 0, 1, 0, nullptr, nullptr, smem, red, 0);
 }
 
-typedef void (*gemv_fn)(const void*, const uint4*, const void*, float, void*, int, int, int, float*, uint32_t*);
+typedef void (*gemv_fn)(const void*, const uint4*, const void*, float, void*, int, int, int, float*, uint32_t*, int);
 typedef void (*gemv_batch_fn)(const void*, int, const GemvSegs);
 struct GemvFns {
   gemv_fn one;
@@ -471,9 +485,9 @@ int q4_workspace_init(void* ws, size_t bytes, void* stream) {
   return Q4_OK;
 }
 
-int q4_gemv(const void* x, int x_dtype, const uint32_t* wq, const void* scales, int scale_fmt, float inv, void* y,
-            int y_dtype, int N, int K, int split, void* ws, size_t ws_size, void* stream) {
-  clear_error();
+static int gemv_launch(const void* x, int x_dtype, const uint32_t* wq, const void* scales, int scale_fmt, float inv,
+                       void* y, int y_dtype, int N, int K, int split, void* ws, size_t ws_size, void* stream,
+                       int gated) {
   Q4_ARG(N > 0 && K > 0 && K % BLK == 0, "bad GEMV shape N=%d K=%d (K must be a positive multiple of 32)", N, K);
   Q4_ARG(x && wq && scales && y, "null pointer");
   Q4_ARG(x_dtype == Q4_DT_F32 || x_dtype == Q4_DT_F16, "bad x dtype %d", x_dtype);
@@ -491,9 +505,22 @@ int q4_gemv(const void* x, int x_dtype, const uint32_t* wq, const void* scales, 
   const float outscale = scale_fmt == Q4_SCALE_E4M3 ? inv * 256.0f : 1.0f;
   gemv_fn fn = pick(pl.R, pl.U, x_dtype, scale_fmt, y_dtype).one;
   hipLaunchKernelGGL(fn, dim3(groups, pl.split), dim3(GEMV_THREADS), pl.lds, as_stream(stream), x,
-                     reinterpret_cast<const uint4*>(wq), scales, outscale, y, N, K / BLK, pl.split, part, cnt);
+                     reinterpret_cast<const uint4*>(wq), scales, outscale, y, N, K / BLK, pl.split, part, cnt, gated);
   Q4_LAUNCHED("gemv");
   return Q4_OK;
+}
+
+int q4_gemv(const void* x, int x_dtype, const uint32_t* wq, const void* scales, int scale_fmt, float inv, void* y,
+            int y_dtype, int N, int K, int split, void* ws, size_t ws_size, void* stream) {
+  clear_error();
+  return gemv_launch(x, x_dtype, wq, scales, scale_fmt, inv, y, y_dtype, N, K, split, ws, ws_size, stream, 0);
+}
+
+int q4_gemv_gated(const void* x, int x_dtype, const uint32_t* wq, const void* scales, int scale_fmt, float inv,
+                  void* act, int act_dtype, int N, int K, int split, void* ws, size_t ws_size, void* stream) {
+  clear_error();
+  Q4_ARG(N > 0 && N % 2 == 0, "gated GEMV needs an even row count (interleaved gate/up rows), got N=%d", N);
+  return gemv_launch(x, x_dtype, wq, scales, scale_fmt, inv, act, act_dtype, N, K, split, ws, ws_size, stream, 1);
 }
 
 int q4_gemv_f16s(const void* x, int x_dtype, const uint32_t* wq, const uint16_t* sc16, void* y, int y_dtype, int N,

@@ -171,6 +171,14 @@ __device__ inline void pin(T& v) {
 
 // f(std::integral_constant<int, I>) for I = B .. E-1, unrolled at compile
 // time (wait counts and register indices must be constants).
+// tanh-form GELU with the reference's operation order (vk/gelumul.comp:8):
+// 0.5 x (1 + tanh(0.7978845608028654 (x + 0.044715 x^3))), each product and
+// sum rounded once.
+__device__ inline float gelu_tanh(float x) {
+  const float inner = __fmul_rn(0.7978845608028654f, __fadd_rn(x, __fmul_rn(__fmul_rn(__fmul_rn(0.044715f, x), x), x)));
+  return __fmul_rn(__fmul_rn(0.5f, x), __fadd_rn(1.0f, tanhf(inner)));
+}
+
 template <int B, int E, class F>
 __device__ __forceinline__ void static_for(F&& f) {
   if constexpr (B < E) {

@@ -217,6 +217,26 @@ __global__ void transpose_i8_kernel(const int8_t* __restrict__ src, int rows, in
   }
 }
 
+// Two panel-64 matrices A, B (N rows each, N % 32 == 0) -> one of 2N rows
+// with row 2i = A row i and row 2i + 1 = B row i, units and scales (sb
+// bytes each) moved as they are. One thread per output (row, block) unit.
+__global__ void interleave_rows_kernel(const uint4* __restrict__ wa, const uint8_t* __restrict__ sa,
+                                       const uint4* __restrict__ wb, const uint8_t* __restrict__ sbp, int nblk,
+                                       int sbytes, uint4* __restrict__ wo, uint8_t* __restrict__ so, long units) {
+  const long u = (long)blockIdx.x * 256 + threadIdx.x;
+  if (u >= units) return;
+  const int r64 = (int)(u % PANEL);
+  const long pb = u / PANEL;  // panel * nblk + block
+  const int b = (int)(pb % nblk);
+  const int n2 = (int)(pb / nblk) * PANEL + r64;  // output row
+  const int n = n2 >> 1;
+  const long src = ((long)(n / PANEL) * nblk + b) * PANEL + n % PANEL;
+  const bool odd = n2 & 1;
+  wo[u] = odd ? wb[src] : wa[src];
+  const uint8_t* sp = (odd ? sbp : sa) + src * sbytes;
+  for (int i = 0; i < sbytes; ++i) so[u * sbytes + i] = sp[i];
+}
+
 static int check_wk(int N, int K) {
   Q4_ARG(N > 0 && K > 0 && K % BLK == 0, "bad shape N=%d K=%d (K must be a positive multiple of 32)", N, K);
   Q4_ARG((long)N * K < (1L << 40), "matrix too large");
@@ -297,6 +317,25 @@ int q4_repack_ref(const uint32_t* wp, const uint16_t* sc_ref, int N, int K, uint
   hipLaunchKernelGGL(repack_ref_kernel, dim3(ceil_div(units, 256)), dim3(256), 0, as_stream(stream), wp, sc_ref, N, K,
                      nblk, reinterpret_cast<uint4*>(wq), sc_dev);
   Q4_LAUNCHED("repack_ref");
+  return Q4_OK;
+}
+
+int q4_interleave_rows(const uint32_t* wa, const void* sa, const uint32_t* wb, const void* sb, int N, int K,
+                       int scale_bytes, uint32_t* wout, void* sout, void* stream) {
+  clear_error();
+  if (int st = check_wk(N, K)) return st;
+  Q4_ARG(wa && sa && wb && sb && wout && sout, "null pointer");
+  Q4_ARG(N % 32 == 0, "interleaving needs N %% 32 == 0 (got N=%d)", N);
+  Q4_ARG(scale_bytes == 1 || scale_bytes == 2, "scale_bytes must be 1 or 2");
+  Q4_ARG(((uintptr_t)wa & 15) == 0 && ((uintptr_t)wb & 15) == 0 && ((uintptr_t)wout & 15) == 0,
+         "weight words must be 16-byte aligned");
+  const int nblk = K / BLK;
+  const long units = (long)2 * N * nblk;
+  hipLaunchKernelGGL(interleave_rows_kernel, dim3(ceil_div(units, 256)), dim3(256), 0, as_stream(stream),
+                     reinterpret_cast<const uint4*>(wa), reinterpret_cast<const uint8_t*>(sa),
+                     reinterpret_cast<const uint4*>(wb), reinterpret_cast<const uint8_t*>(sb), nblk, scale_bytes,
+                     reinterpret_cast<uint4*>(wout), reinterpret_cast<uint8_t*>(sout), units);
+  Q4_LAUNCHED("interleave_rows");
   return Q4_OK;
 }
 

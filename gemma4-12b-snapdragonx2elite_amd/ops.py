@@ -203,6 +203,40 @@ def gemv(x: torch.Tensor, wq: torch.Tensor, scales: torch.Tensor, N: int, K: int
     return y
 
 
+def interleave_rows(wa: torch.Tensor, sa: torch.Tensor, wb: torch.Tensor, sb: torch.Tensor, N: int, K: int):
+    """Gate/up matrices (panel-64, N rows each) -> one of 2N rows, row 2i from
+    ``wa``/``sa`` and row 2i + 1 from ``wb``/``sb`` (the layout of :func:`gemv_gated`)."""
+    sbytes = sa.element_size()
+    if sb.element_size() != sbytes:
+        raise ValueError("both scale arrays must have the same element size")
+    _check_int4(wa, sa, N, K, sbytes)
+    _check_int4(wb, sb, N, K, sbytes)
+    wo, se = _empty_weights(2 * N, K, wa.device)
+    so = torch.empty(se, dtype=sa.dtype, device=wa.device)
+    call("q4_interleave_rows", _p(wa), _p(sa), _p(wb), _p(sb), N, K, sbytes, _p(wo), _p(so), _stream())
+    return wo, so
+
+
+def gemv_gated(x: torch.Tensor, wq: torch.Tensor, scales: torch.Tensor, N: int, K: int, *,
+               scale_fmt: int = SCALE_F16, inv: float = 1.0, act: torch.Tensor | None = None, act_dtype=None,
+               split: int = 0, ws: Workspace | None = None) -> torch.Tensor:
+    """act[i] = gelu_tanh(y[2i]) * y[2i+1] of the GEMV y over an interleaved
+    gate/up matrix of N rows (:func:`interleave_rows`); act has N/2 elements."""
+    if x.numel() != K:
+        raise ValueError(f"x has {x.numel()} elements, expected K={K}")
+    if N % 2:
+        raise ValueError("gated GEMV needs an even row count")
+    if act is None:
+        act = torch.empty(N // 2, dtype=act_dtype or x.dtype, device=x.device)
+    _check_int4(wq, scales, N, K, 1 if scale_fmt == SCALE_E4M3 else 2)
+    _need(act, (N // 2) * act.element_size(), "act")
+    if ws is None:
+        ws = default_workspace(N, K, split, x.device)
+    call("q4_gemv_gated", _p(x), _dt(x), _p(wq), _p(scales), scale_fmt, C.c_float(inv), _p(act), _dt(act), N, K,
+         split, _p(ws.t) if ws else C.c_void_p(0), ws.t.numel() if ws else 0, _stream())
+    return act
+
+
 def gemv_batch_max_k(x_dtype) -> int:
     """Largest K a batched GEMV stages for this activation dtype."""
     return 32768 if x_dtype == torch.float16 else 16384

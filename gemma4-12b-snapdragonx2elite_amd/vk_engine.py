@@ -29,6 +29,8 @@ reference              here
   :235-249             descriptors of a layer with the reference's buffers
                        and uniforms; :func:`disp` enqueues one
 ``buf_u32`` :71-73     same (the DYN position buffer is one)
+``d_g/d_u/d_gm``       :func:`gate_up_ds`: gate/up rows interleaved once, the
+  :242-246             gelumul in the GEMV epilogue (one launch)
 fence wait :293-302    :func:`submit` / :func:`wait` raise
                        ``RuntimeError('GPU fence TIMEOUT after ..ms at [..]')``
 =====================  ====================================================
@@ -316,6 +318,28 @@ def gelumul_ds(gate: Buf, up: Buf, out: Buf, du, out_dtype=torch.float32) -> OpD
     return OpDesc(ops.gelumul, (_f32v(gate, n), _f32v(up, n), out.view(out_dtype, n)), {})
 
 
+def gate_up_ds(qg, qu, inbuf: Buf, actbuf: Buf, x_dtype=torch.float32, act_dtype=torch.float32) -> OpDesc | None:
+    """The gate and up GEMVs and the gelumul after them (src/vk_engine.py:242-243,
+    246) as one launch: the two matrices are interleaved row by row here (a
+    copy of their weights, made once) and the GEMV's epilogue writes
+    ``act = gelu_tanh(gate) * up``. Returns None when the two cannot share
+    one matrix (different shapes, scale formats or e4m3 lifts); then record
+    the separate descriptors."""
+    (bwg, bsg, _sg, _nb, invg, _a, _b, _c), (N, K) = qg
+    (bwu, bsu, _su, _nb2, invu, _d, _e, _f), (N2, K2) = qu
+    if (N, K) != (N2, K2) or bsg.t.dtype != bsu.t.dtype or invg != invu or N % 32:
+        return None
+    fmt = SCALE_E4M3 if bsg.t.dtype == torch.uint8 else SCALE_F16
+    wo, so = ops.interleave_rows(bwg.t, bsg.t, bwu.t, bsu.t, N, K)
+    KEEP.extend([wo, so])
+    split = ops.auto_split(2 * N, K)
+    ws = ops.default_workspace(2 * N, K, split, wo.device)
+    if ws is not None:
+        KEEP.append(ws)
+    return OpDesc(ops.gemv_gated, (inbuf.view(x_dtype, K), wo, so, 2 * N, K),
+                  dict(scale_fmt=fmt, inv=invg, act=actbuf.view(act_dtype, N), split=split, ws=ws))
+
+
 def prepkv_ds(qkv: Buf, knw: Buf, cosb: Buf, sinb: Buf, kc: Buf, vc: Buf, P, dyn: Buf) -> OpDesc:
     """This token's K/V into the fp16 caches (d_prep, src/vk_engine.py:235-237);
     ``P`` = (nkv, hd, koff, voff, keqv, stride, window, 0) in floats/slots."""
@@ -357,7 +381,9 @@ def record_decode(layers, d_fin: OpDesc, d_lm: GemvDesc, fuse: bool = True) -> o
     down, normadd (layer scale); then the final norm and lm_head. ``layers``
     holds the reference's per-layer descriptor keys (``d_in``, ``d_q``,
     ``d_k``, ``d_v`` (may be None), ``d_prep``, ``d_attn``, ``d_o``, ``d_na``,
-    ``d_pfn``, ``d_g``, ``d_u``, ``d_gm``, ``d_d``, ``d_nas``).
+    ``d_pfn``, ``d_g``, ``d_u``, ``d_gm``, ``d_d``, ``d_nas``); a layer with a
+    ``d_gu`` descriptor (:func:`gate_up_ds`) runs it in place of ``d_g``,
+    ``d_u`` and ``d_gm``.
 
     With ``fuse`` (default), every normadd that is followed by an rmsnorm of
     the same residual vector (the post-attention normadd and the MLP norm;
@@ -368,7 +394,8 @@ def record_decode(layers, d_fin: OpDesc, d_lm: GemvDesc, fuse: bool = True) -> o
     for L in layers:
         seq += [L["d_in"], ("gemvs", [L["d_q"], L["d_k"]] + ([L["d_v"]] if L.get("d_v") is not None else [])),
                 L["d_prep"], L["d_attn"], ("gemvs", [L["d_o"]]), L["d_na"], L["d_pfn"],
-                ("gemvs", [L["d_g"], L["d_u"]]), L["d_gm"], ("gemvs", [L["d_d"]]), L["d_nas"]]
+                *([L["d_gu"]] if L.get("d_gu") is not None else [("gemvs", [L["d_g"], L["d_u"]]), L["d_gm"]]),
+                ("gemvs", [L["d_d"]]), L["d_nas"]]
     seq += [d_fin, ("gemvs", [d_lm])]
     if fuse:
         seq = _fuse_norms(seq)

@@ -94,6 +94,14 @@ int q4_w4a8_ratio(const float* sc32, const float* sw32, int N, int K,
  * src/vk_engine.py:129-131. */
 int q4_repack_ref(const uint32_t* wp, const uint16_t* sc_ref, int N, int K,
                   uint32_t* wq, uint16_t* sc_dev, void* stream);
+/* Gate and up matrices (panel-64, N rows each, N % 32 == 0) -> one panel-64
+ * matrix of 2N rows with row 2i = gate row i and row 2i+1 = up row i, words
+ * and scales (scale_bytes 2 for fp16, 1 for e4m3) as they are: the layout
+ * q4_gemv_gated reads. Load time; the reference keeps gate_proj and
+ * up_proj as two matrices (src/vk_engine.py:198) and runs gelumul on their
+ * outputs (:246). */
+int q4_interleave_rows(const uint32_t* wa, const void* sa, const uint32_t* wb, const void* sb,
+                       int N, int K, int scale_bytes, uint32_t* wout, void* sout, void* stream);
 /* e4m3 scales [K/32][N] bytes -> panel-64 bytes. src/vk_engine.py:137. */
 int q4_repack_e4m3_ref(const uint8_t* sc_ref, int N, int K, uint8_t* sc_dev,
                        void* stream);
@@ -130,6 +138,15 @@ int q4_gemv_f16s(const void* x, int x_dtype, const uint32_t* wq,
 int q4_gemv_e4m3s(const void* x, int x_dtype, const uint32_t* wq,
                   const uint8_t* sc8, float inv, void* y, int y_dtype, int N,
                   int K, int split, void* ws, size_t ws_bytes, void* stream);
+
+/* GEMV over an interleaved gate/up matrix (q4_interleave_rows; N = 2 I
+ * rows) with the gelumul of the reference (vk/gelumul.comp:7-8, d_gm at
+ * src/vk_engine.py:246) in its epilogue: act[i] = gelu_tanh(y[2i]) * y[2i+1]
+ * for i < N/2, act in act_dtype. Same arguments and plan as q4_gemv; the
+ * gate/up GEMVs (:242-243) and the gelumul dispatch become one launch. */
+int q4_gemv_gated(const void* x, int x_dtype, const uint32_t* wq, const void* scales,
+                  int scale_fmt, float inv, void* act, int act_dtype, int N, int K, int split,
+                  void* ws, size_t ws_bytes, void* stream);
 
 /* Several decode GEMVs that read the same activation x, in one launch:
  * y_i[N_i] = (GEMV of matrix i) x for i < count, with the arithmetic of

@@ -306,3 +306,32 @@ def test_gemv_batch_e4m3(gpu):
     ys = gpu.gemv_batch(torch.from_numpy(x).cuda(), mats, K, scale_fmt=gpu.SCALE_E4M3, y_dtype=torch.float32)
     for y, ref in zip(ys, refs):
         assert O.normwise_rel_err(to_np(y), ref) <= TOL_F32
+
+
+# ------------------------------------------------------------ gated gate/up
+@pytest.mark.parametrize("I,K", [(15360, 3840), (64, 256), (96, 3840)])
+@pytest.mark.parametrize("xdt,adt", [(torch.float16, torch.float16), (torch.float32, torch.float32)])
+def test_gemv_gated_vs_oracle(gpu, I, K, xdt, adt):
+    """Interleaved gate/up rows and the gelumul epilogue: act = gelu_tanh(W_g x)
+    * (W_u x) against the oracle's GEMVs and gelumul (normwise <= 5e-5 fp32,
+    the product doubles the GEMVs' relative error; <= 1e-3 fp16). I = 64 and
+    96 take the split-K path."""
+    from oracle import decode_ops_oracle as D
+    rng = np.random.default_rng(I + K)
+    qg, sg = synth_int4(rng, I, K)
+    qu, su = synth_int4(rng, I, K)
+    x = rng.standard_normal(K).astype(np.float16)
+    xin = x if xdt == torch.float16 else x.astype(np.float32)
+    ref = D.gelumul_ref(O.gemv_ref(qg, sg, xin), O.gemv_ref(qu, su, xin))
+    wg, scg = upload_int4(qg, sg)
+    wu, scu = upload_int4(qu, su)
+    wo, so = gpu.interleave_rows(wg, scg, wu, scu, I, K)
+    # layout: row 2i of the interleaved matrix is gate row i, row 2i+1 up row i, bit for bit
+    codes = O.unpack_dev(to_np(wo).view(np.uint32), 2 * I, K)
+    assert np.array_equal(codes[0::2], qg) and np.array_equal(codes[1::2], qu)
+    sc = O.unscales_dev(to_np(so), 2 * I, K // 32)
+    assert np.array_equal(sc[0::2], sg.astype(np.float16)) and np.array_equal(sc[1::2], su.astype(np.float16))
+    act = gpu.gemv_gated(torch.from_numpy(xin).cuda(), wo, so, 2 * I, K, act_dtype=adt)
+    assert act.numel() == I and act.dtype == adt
+    tol = 1e-3 if adt == torch.float16 else 5e-5
+    assert O.normwise_rel_err(to_np(act).astype(np.float64), ref) <= tol

@@ -32,11 +32,13 @@ def _rope(pos, hd):
     return (np.concatenate([np.cos(ang)] * 2).astype(np.float32), np.concatenate([np.sin(ang)] * 2).astype(np.float32))
 
 
-@pytest.mark.parametrize("fuse,half", [(False, False), (True, False), (True, True)])
-def test_decode_token_through_the_engine_mirror(g4, gpu, fuse, half):
+@pytest.mark.parametrize("fuse,half,gated", [(False, False, False), (True, False, False), (True, True, False),
+                                             (True, True, True), (False, False, True)])
+def test_decode_token_through_the_engine_mirror(g4, gpu, fuse, half, gated):
     """fuse: normadd + next rmsnorm as one launch; half: fp16 GEMV inputs
     (norm, gelumul and attention write fp16, the residual stream stays
-    fp32): the oracle rounds the same GEMV inputs to fp16."""
+    fp32): the oracle rounds the same GEMV inputs to fp16; gated: gate/up
+    interleaved with the gelumul in the GEMV epilogue."""
     E = importlib.import_module("g4mi.vk_engine")
     xdt = torch.float16 if half else torch.float32
     rx = (lambda v: np.asarray(v).astype(np.float16).astype(np.float64)) if half else (lambda v: v)
@@ -91,6 +93,9 @@ def test_decode_token_through_the_engine_mirror(g4, gpu, fuse, half):
                  d_gm=E.gelumul_ds(B["gate"], B["up"], B["act"], DUI, out_dtype=xdt),
                  d_d=E.gemv_ds(dp[:2], B["act"], B["down"], 0, x_dtype=xdt),
                  d_nas=E.normadd_ds(B["down"], nb["ofw"], B["h"], nas))
+        if gated:
+            L["d_gu"] = E.gate_up_ds(gp[:2], up[:2], B["normed2"], B["act"], x_dtype=xdt, act_dtype=xdt)
+            assert L["d_gu"] is not None
         layers.append(L)
         ref_layers.append(dict(cfg, nq=nq, nk=nk, q=qp[2], k=kp[2], v=None if keqv else vp[2], o=op[2], g=gp[2],
                                u=up[2], d=dp[2], kc=np.zeros(nkv * cfg["stride"] * hd, np.float16),
