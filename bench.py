@@ -475,6 +475,10 @@ def main():
     ap.add_argument("--counters", action="store_true",
                     help="run only the decode GEMV launches (16 per layer shape, 2 lm_head) and a 512 MiB "
                          "calibration copy, for rocprofv3 --pmc passes; prints no JSON line")
+    ap.add_argument("--no-token", action="store_true", help="skip the whole-token legs")
+    ap.add_argument("--token-only", action="store_true",
+                    help="run only the whole-token legs (reference dispatches, then fused) for --steps replays; "
+                         "prints their results, no JSON line")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU: this path is a single-GPU kernel set (multi-GPU sharding is "
@@ -488,14 +492,20 @@ def main():
     if args.counters:
         counter_workload(ops)
         return
+    if args.token_only:
+        for fast in (False, True):
+            print(f"[bench] token step {bench_token_step(ops, args.steps, args.warmup, fast=fast)}", flush=True)
+        return
     print(f"[bench] decode graph: {LAYERS} layers + lm_head, {args.steps} steps after {args.warmup} warmup",
           flush=True)
     dec = bench_decode(ops, args.steps, args.warmup)
     print(f"[bench] decode {dec['ms_per_step']:.3f} ms/token, {dec['GBps']:.0f} GB/s "
           f"(per-token {dec['ms_per_step_percentiles']})", flush=True)
-    tok = {"reference_dispatches": bench_token_step(ops, max(20, args.steps // 4), 5),
-           "fused": bench_token_step(ops, max(20, args.steps // 4), 5, fast=True)}
-    print(f"[bench] token step {tok}", flush=True)
+    tok = None
+    if not args.no_token:
+        tok = {"reference_dispatches": bench_token_step(ops, max(20, args.steps // 4), 5),
+               "fused": bench_token_step(ops, max(20, args.steps // 4), 5, fast=True)}
+        print(f"[bench] token step {tok}", flush=True)
     single = {"c1_15360x3840_f16_scales": bench_gemv_single(ops, I, H, False),
               "c3_15360x3840_e4m3_scales": bench_gemv_single(ops, I, H, True),
               "lm_head_262144x3840_f16_scales": bench_gemv_single(ops, V, H, False, reps=4)}
