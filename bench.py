@@ -300,7 +300,7 @@ def bench_token_step(ops, steps: int, warmup: int, pos: int = 1023, fast: bool =
                             if fast else "fp32 (reference)"),
             "weight_bytes": wbytes, "kv_cache_bytes_read": kvbytes,
             "GBps": round((wbytes + kvbytes) / (ms * 1e-3) / 1e9, 1),
-            "kernels_per_token": LAYERS * (9 if fast else 12) + 2}
+            "kernels_per_token": LAYERS * (8 if fast else 12) + 2}
 
 
 def counter_workload(ops):

@@ -60,6 +60,8 @@ SIGNATURES = {
     "q4_prepkv": (_i, [_vp, _vp, _vp, _vp, _vp, _vp, _i, _i, _i, _i, _i, _i, _i, _vp, _vp]),
     "q4_attn_workspace_bytes": (_sz, [_i, _i, _i]),
     "q4_attn": (_i, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _i, _i, _i, _i, _i, _i, _i, _i, _vp, _vp, _sz, _vp]),
+    "q4_prepkv_attn": (_i, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _i, _i, _i, _i, _i, _i, _i, _i, _i, _i, _i, _vp,
+                            _vp, _sz, _vp]),
     "q4_graph_begin": (_i, [_vp]),
     "q4_graph_end": (_i, [_vp, C.POINTER(_vp)]),
     "q4_graph_launch": (_i, [_vp, _vp]),

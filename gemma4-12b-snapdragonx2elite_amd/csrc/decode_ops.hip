@@ -241,25 +241,58 @@ __device__ inline HalfVec<E> ld_halves(const uint16_t* p) {
 // per key, the wave's 16 keys in flight at once. Keys past the length read
 // the last live row (in bounds) with weight 0. Writes (max, sum,
 // unnormalised accumulator[hd]) to ws.
-template <int EPL>
+//
+// With PREP (prepkv folded in, vk/prepkv.comp:16-30): the workgroups of the
+// split that holds this token's cache slot form the token's K (k-norm with
+// weight, RoPE) and V (v-norm) themselves, rounded to fp16 as the cache
+// holds them, and use them for that key in place of the cache row (which
+// they never read); the workgroup of the first query head of each KV head
+// writes them to the cache for the next tokens. No other workgroup touches
+// that row, so one launch replaces prepkv + this kernel.
+template <int EPL, bool PREP>
 __global__ void __launch_bounds__(ATT_THREADS) attn_split_kernel(const float* __restrict__ qkv, const float* __restrict__ qnw,
                                                                  const float* __restrict__ cs, const float* __restrict__ sn,
-                                                                 const uint16_t* __restrict__ kc,
-                                                                 const uint16_t* __restrict__ vc, int stride,
-                                                                 int window, int qoff, int grp,
+                                                                 uint16_t* __restrict__ kc, uint16_t* __restrict__ vc,
+                                                                 int stride, int window, int qoff, int grp,
                                                                  const uint32_t* __restrict__ dyn,
-                                                                 float* __restrict__ ws) {
+                                                                 float* __restrict__ ws, const float* __restrict__ knw,
+                                                                 int koff, int voff) {
   constexpr int HD = 64 * EPL, LPK = 8 * EPL, KPI = 64 / LPK, KPW = ATT_CH / (ATT_THREADS / 64);
   constexpr int NI = KPW / KPI;  // score loads per wave
   __shared__ float qv[HD], qr[HD], p[ATT_CH], red[ATT_THREADS / 64];
   __shared__ float accp[ATT_THREADS / 64][HD];
+  __shared__ float knew[PREP ? HD : 1], vnew[PREP ? HD : 1];
   const int h = blockIdx.x, sp = blockIdx.y, t = threadIdx.x;
-  const int T = att_len(dyn[0], window, stride);
+  const uint32_t pos = dyn[0];
+  const int T = att_len(pos, window, stride);
   const int j0 = sp * ATT_CH;
   if (j0 >= T) return;  // past the current length: the merge reads only the live splits
   const int n = min(ATT_CH, T - j0);
   const int kvh = h / grp;
   const int wave = t >> 6, lane = t & 63;
+  const int slot = kv_slot(pos, window);
+  const int kslot = PREP && slot < stride && slot >= j0 && slot < j0 + n ? slot - j0 : -1;  // workgroup-uniform
+
+  if constexpr (PREP) {
+    if (kslot >= 0) {
+      for (int i = t; i < HD; i += ATT_THREADS) qv[i] = qkv[koff + kvh * HD + i];
+      __syncthreads();
+      norm_rope_head(qv, knew, knw, cs, sn, HD, red);
+      for (int i = t; i < HD; i += ATT_THREADS) knew[i] = h2f(f2h(knew[i]));
+      for (int i = t; i < HD; i += ATT_THREADS) vnew[i] = qkv[voff + kvh * HD + i];
+      __syncthreads();
+      norm_rope_head(vnew, nullptr, nullptr, nullptr, nullptr, HD, red);
+      for (int i = t; i < HD; i += ATT_THREADS) vnew[i] = h2f(f2h(vnew[i]));
+      if (h % grp == 0) {
+        const long o = ((long)kvh * stride + slot) * HD;
+        for (int i = t; i < HD; i += ATT_THREADS) {
+          kc[o + i] = f2h(knew[i]);
+          vc[o + i] = f2h(vnew[i]);
+        }
+      }
+      __syncthreads();  // qv is reused for q below
+    }
+  }
 
   // q: norm with weight, RoPE (vk/attn.comp:23-30)
   for (int i = t; i < HD; i += ATT_THREADS) qv[i] = qkv[qoff + h * HD + i];
@@ -280,15 +313,20 @@ __global__ void __launch_bounds__(ATT_THREADS) attn_split_kernel(const float* __
     }
 #pragma unroll
     for (int b = 0; b < NI; ++b) {
+      const int key = KPW * wave + KPI * b + kk;
+      // this token's key (PREP): its fp16-rounded k_new in place of the cache row
+      // it replaces, in the same summation order as every other key
+      const bool fresh = PREP && key == kslot;
       float d = 0.0f;
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
-        d = fmaf(q8[2 * e], h2f((uint16_t)(u[b][e] & 0xFFFFu)), d);
-        d = fmaf(q8[2 * e + 1], h2f((uint16_t)(u[b][e] >> 16)), d);
+        const float k0 = fresh ? knew[8 * ch + 2 * e] : h2f((uint16_t)(u[b][e] & 0xFFFFu));
+        const float k1 = fresh ? knew[8 * ch + 2 * e + 1] : h2f((uint16_t)(u[b][e] >> 16));
+        d = fmaf(q8[2 * e], k0, d);
+        d = fmaf(q8[2 * e + 1], k1, d);
       }
 #pragma unroll
       for (int o = LPK / 2; o > 0; o >>= 1) d += __shfl_xor(d, o, 64);
-      const int key = KPW * wave + KPI * b + kk;
       if (ch == 0) p[key] = key < n ? d : -INFINITY;
     }
   }
@@ -313,8 +351,13 @@ __global__ void __launch_bounds__(ATT_THREADS) attn_split_kernel(const float* __
 #pragma unroll
     for (int k = 0; k < KPW; ++k) {
       const float pw = p[KPW * wave + k];
+      if (PREP && KPW * wave + k == kslot) {  // this token's value row
 #pragma unroll
-      for (int e = 0; e < EPL; ++e) a[e] = fmaf(pw, h2f(v[k].h[e]), a[e]);
+        for (int e = 0; e < EPL; ++e) a[e] = fmaf(pw, vnew[EPL * lane + e], a[e]);
+      } else {
+#pragma unroll
+        for (int e = 0; e < EPL; ++e) a[e] = fmaf(pw, h2f(v[k].h[e]), a[e]);
+      }
     }
   }
 #pragma unroll
@@ -440,15 +483,15 @@ size_t q4_attn_workspace_bytes(int nH, int hd, int stride) {
   return (size_t)nH * attn_splits(stride) * (hd + 2) * sizeof(float);
 }
 
-int q4_attn(const float* qkv, const float* qnw, const float* cosb, const float* sinb, const uint16_t* kc,
-            const uint16_t* vc, void* out, int out_dtype, int nH, int nkv, int hd, int stride, int window, int qoff,
-            int grp, const uint32_t* dyn, void* ws, size_t ws_bytes, void* stream) {
-  clear_error();
+static int attn_launch(const float* qkv, const float* qnw, const float* cosb, const float* sinb, uint16_t* kc,
+                       uint16_t* vc, void* out, int out_dtype, int nH, int nkv, int hd, int stride, int window,
+                       int qoff, int grp, const uint32_t* dyn, void* ws, size_t ws_bytes, void* stream,
+                       const float* knw, int koff, int voff) {
   Q4_ARG(qkv && qnw && cosb && sinb && kc && vc && out && dyn && ws, "null pointer");
   Q4_ARG(out_dtype == Q4_DT_F32 || out_dtype == Q4_DT_F16, "bad out_dtype");
   Q4_ARG(nH > 0 && nkv > 0 && grp > 0 && nH == nkv * grp, "need nH == nkv * grp (got %d, %d, %d)", nH, nkv, grp);
   Q4_ARG(hd == 64 || hd == 128 || hd == 256 || hd == 512, "head dim must be 64, 128, 256 or 512 (got %d)", hd);
-  Q4_ARG(stride > 0 && window >= 0 && window <= stride && qoff >= 0, "bad sizes");
+  Q4_ARG(stride > 0 && window >= 0 && window <= stride && qoff >= 0 && koff >= 0 && voff >= 0, "bad sizes");
   Q4_ARG(((uintptr_t)kc & 15) == 0, "kc must be 16-byte aligned");
   const size_t need = q4_attn_workspace_bytes(nH, hd, stride);
   Q4_ARG(ws_bytes >= need, "attention workspace too small: %zu < %zu bytes", ws_bytes, need);
@@ -457,16 +500,18 @@ int q4_attn(const float* qkv, const float* qnw, const float* cosb, const float* 
   Q4_ARG(msh <= 64 * 1024, "cache depth %d needs %d attention splits (more than the merge stages)", stride, ns);
   hipStream_t st = as_stream(stream);
   float* wsf = reinterpret_cast<float*>(ws);
+  const dim3 grid(nH, ns), blk(ATT_THREADS);
+#define Q4_ATT(E, P)                                                                                            \
+  hipLaunchKernelGGL((attn_split_kernel<E, P>), grid, blk, 0, st, qkv, qnw, cosb, sinb, kc, vc, stride, window, \
+                     qoff, grp, dyn, wsf, knw, koff, voff)
+  const bool prep = knw != nullptr;
   switch (hd) {
-    case 64: hipLaunchKernelGGL(attn_split_kernel<1>, dim3(nH, ns), dim3(ATT_THREADS), 0, st, qkv, qnw, cosb, sinb, kc, vc,
-                                stride, window, qoff, grp, dyn, wsf); break;
-    case 128: hipLaunchKernelGGL(attn_split_kernel<2>, dim3(nH, ns), dim3(ATT_THREADS), 0, st, qkv, qnw, cosb, sinb, kc, vc,
-                                 stride, window, qoff, grp, dyn, wsf); break;
-    case 256: hipLaunchKernelGGL(attn_split_kernel<4>, dim3(nH, ns), dim3(ATT_THREADS), 0, st, qkv, qnw, cosb, sinb, kc, vc,
-                                 stride, window, qoff, grp, dyn, wsf); break;
-    default: hipLaunchKernelGGL(attn_split_kernel<8>, dim3(nH, ns), dim3(ATT_THREADS), 0, st, qkv, qnw, cosb, sinb, kc, vc,
-                                stride, window, qoff, grp, dyn, wsf); break;
+    case 64: if (prep) Q4_ATT(1, true); else Q4_ATT(1, false); break;
+    case 128: if (prep) Q4_ATT(2, true); else Q4_ATT(2, false); break;
+    case 256: if (prep) Q4_ATT(4, true); else Q4_ATT(4, false); break;
+    default: if (prep) Q4_ATT(8, true); else Q4_ATT(8, false); break;
   }
+#undef Q4_ATT
   Q4_LAUNCHED("attn_split");
   if (out_dtype == Q4_DT_F16)
     hipLaunchKernelGGL(attn_merge_kernel<Q4_DT_F16>, dim3(nH), dim3(ATT_THREADS), msh, st, wsf, out, hd, ns, stride,
@@ -476,6 +521,25 @@ int q4_attn(const float* qkv, const float* qnw, const float* cosb, const float* 
                        window, dyn);
   Q4_LAUNCHED("attn_merge");
   return Q4_OK;
+}
+
+int q4_attn(const float* qkv, const float* qnw, const float* cosb, const float* sinb, const uint16_t* kc,
+            const uint16_t* vc, void* out, int out_dtype, int nH, int nkv, int hd, int stride, int window, int qoff,
+            int grp, const uint32_t* dyn, void* ws, size_t ws_bytes, void* stream) {
+  clear_error();
+  // the cache is only read without the folded prepkv
+  return attn_launch(qkv, qnw, cosb, sinb, const_cast<uint16_t*>(kc), const_cast<uint16_t*>(vc), out, out_dtype, nH,
+                     nkv, hd, stride, window, qoff, grp, dyn, ws, ws_bytes, stream, nullptr, 0, 0);
+}
+
+int q4_prepkv_attn(const float* qkv, const float* knw, const float* qnw, const float* cosb, const float* sinb,
+                   uint16_t* kc, uint16_t* vc, void* out, int out_dtype, int nH, int nkv, int hd, int stride,
+                   int window, int qoff, int koff, int voff, int keqv, int grp, const uint32_t* dyn, void* ws,
+                   size_t ws_bytes, void* stream) {
+  clear_error();
+  Q4_ARG(knw, "null pointer");
+  return attn_launch(qkv, qnw, cosb, sinb, kc, vc, out, out_dtype, nH, nkv, hd, stride, window, qoff, grp, dyn, ws,
+                     ws_bytes, stream, knw, koff, keqv ? koff : voff);
 }
 
 }  // extern "C"

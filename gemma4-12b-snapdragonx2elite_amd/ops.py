@@ -484,6 +484,25 @@ def attn(qkv, qnw, cosb, sinb, kc, vc, out=None, *, nH: int, nkv: int, hd: int, 
     return out
 
 
+def prepkv_attn(qkv, knw, qnw, cosb, sinb, kc, vc, out=None, *, nH: int, nkv: int, hd: int, stride: int,
+                window: int, qoff: int, koff: int, voff: int, keqv: bool, grp: int, dyn: torch.Tensor,
+                ws: torch.Tensor | None = None, out_dtype=torch.float32) -> torch.Tensor:
+    """:func:`prepkv` then :func:`attn` of one layer in one pass (same results)."""
+    _f32(qkv, max(qoff + nH * hd, max(koff, koff if keqv else voff) + nkv * hd), "qkv")
+    for t, nm in ((knw, "knw"), (qnw, "qnw"), (cosb, "cosb"), (sinb, "sinb")):
+        _f32(t, hd, nm)
+    _kv_checks(kc, vc, nkv, stride, hd, dyn)
+    out = torch.empty(nH * hd, dtype=out_dtype, device=qkv.device) if out is None else out
+    _need(out, nH * hd * out.element_size(), "out")
+    if ws is None:
+        if _CAPTURING[0]:
+            raise RuntimeError("attention inside a graph capture needs a workspace allocated before the capture")
+        ws = attn_workspace(nH, hd, stride, qkv.device)
+    call("q4_prepkv_attn", _p(qkv), _p(knw), _p(qnw), _p(cosb), _p(sinb), _p(kc), _p(vc), _p(out), _dt(out), nH, nkv,
+         hd, stride, window, qoff, koff, voff, int(bool(keqv)), grp, _p(dyn), _p(ws), _nbytes(ws), _stream())
+    return out
+
+
 # ----------------------------------------------------------- graphs/waits
 class Graph:
     """A hipGraph captured from a stream: ``with g.capture(): ...`` then ``g.launch()``."""

@@ -388,7 +388,8 @@ def record_decode(layers, d_fin: OpDesc, d_lm: GemvDesc, fuse: bool = True) -> o
     With ``fuse`` (default), every normadd that is followed by an rmsnorm of
     the same residual vector (the post-attention normadd and the MLP norm;
     a layer's last normadd and the next layer's input norm or the final
-    norm) runs as one :func:`ops.normadd_rmsnorm` launch: two launches fewer
+    norm) runs as one :func:`ops.normadd_rmsnorm` launch, and prepkv with
+    the attention after it as :func:`ops.prepkv_attn`: three launches fewer
     per layer, same arithmetic."""
     seq = []
     for L in layers:
@@ -410,6 +411,9 @@ def record_decode(layers, d_fin: OpDesc, d_lm: GemvDesc, fuse: bool = True) -> o
 
 
 def _fuse_norms(seq):
+    """Pairs of adjacent descriptors that run as one launch: a normadd and
+    the rmsnorm of the same residual vector after it; a prepkv and the
+    attention that reads the same caches and position after it."""
     out, i = [], 0
     while i < len(seq):
         a = seq[i]
@@ -419,6 +423,17 @@ def _fuse_norms(seq):
             x, w, h, sc = a.args
             _, w2, y = b.args
             out.append(OpDesc(ops.normadd_rmsnorm, (x, w, h, w2, sc, y), {}))
+            i += 2
+        elif (isinstance(a, OpDesc) and isinstance(b, OpDesc) and a.fn is ops.prepkv and b.fn is ops.attn
+              and a.args[0].data_ptr() == b.args[0].data_ptr() and a.args[4].data_ptr() == b.args[4].data_ptr()
+              and a.args[5].data_ptr() == b.args[5].data_ptr() and a.kw["dyn"].data_ptr() == b.kw["dyn"].data_ptr()
+              and a.kw["hd"] == b.kw["hd"] and a.kw["nkv"] == b.kw["nkv"] and a.kw["stride"] == b.kw["stride"]
+              and a.kw["window"] == b.kw["window"] and a.args[2].data_ptr() == b.args[2].data_ptr()
+              and a.args[3].data_ptr() == b.args[3].data_ptr()):
+            qkv, knw, cosb, sinb, kc, vc = a.args
+            _, qnw, _, _, _, _, outt = b.args
+            kw = dict(b.kw, koff=a.kw["koff"], voff=a.kw["voff"], keqv=a.kw["keqv"], out_dtype=outt.dtype)
+            out.append(OpDesc(ops.prepkv_attn, (qkv, knw, qnw, cosb, sinb, kc, vc, outt), kw))
             i += 2
         else:
             out.append(a)

@@ -270,6 +270,17 @@ int q4_attn(const float* qkv, const float* qnw, const float* cosb, const float* 
             int hd, int stride, int window, int qoff, int grp, const uint32_t* dyn, void* ws,
             size_t ws_bytes, void* stream);
 
+/* q4_prepkv and q4_attn of one layer as one pass (two launches instead of
+ * three): the workgroups of the key split that holds this token's slot form
+ * its K (k-norm with knw, RoPE) and V (v-norm; read at koff when keqv),
+ * rounded to fp16 as the cache holds them, use them for that key, and write
+ * them to the cache; outputs and cache contents are those of q4_prepkv
+ * followed by q4_attn. d_prep + d_attn (src/vk_engine.py:235-239,281). */
+int q4_prepkv_attn(const float* qkv, const float* knw, const float* qnw, const float* cosb,
+                   const float* sinb, uint16_t* kc, uint16_t* vc, void* out, int out_dtype, int nH,
+                   int nkv, int hd, int stride, int window, int qoff, int koff, int voff, int keqv,
+                   int grp, const uint32_t* dyn, void* ws, size_t ws_bytes, void* stream);
+
 /* ---- record-once submit --------------------------------------------------
  * The per-token command buffer recorded once and resubmitted
  * (src/vk_engine.py:254-290, forward() :312-319) becomes a hipGraph captured

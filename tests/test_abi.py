@@ -128,3 +128,13 @@ def test_decode_op_argument_errors_without_gpu(g4):
     assert st == g4._lib.Q4_ERR_ARG and "null" in _err(g4)
     st = lib.q4_normadd(fake, fake, fake, 0, C.c_float(1.0), null)
     assert st == g4._lib.Q4_ERR_ARG and "bad D" in _err(g4)
+
+
+def test_prepkv_attn_argument_errors_without_gpu(g4):
+    lib = g4._lib.lib()
+    fake, null = C.c_void_p(256), C.c_void_p(0)
+    st = lib.q4_prepkv_attn(fake, null, *[fake] * 6, 0, 16, 8, 256, 64, 0, 0, 4096, 6144, 0, 2, fake, fake, 1 << 20,
+                            null)
+    assert st == g4._lib.Q4_ERR_ARG and "null" in _err(g4)
+    st = lib.q4_prepkv_attn(*[fake] * 8, 0, 16, 8, 96, 64, 0, 0, 4096, 6144, 0, 2, fake, fake, 1 << 20, null)
+    assert st == g4._lib.Q4_ERR_ARG and "64, 128, 256 or 512" in _err(g4)

@@ -194,3 +194,33 @@ def test_prepkv_attn_graph_replay_follows_position(gpu):
                          grp=nH // nkv, pos=pos)
         assert O.normwise_rel_err(_np(out), ref) <= 1e-4, pos
     g.destroy()
+
+
+@pytest.mark.parametrize("nH,nkv,hd,stride,window,pos,keqv", [
+    (16, 8, 256, 1024, 1024, 0, False),      # first token
+    (16, 8, 256, 1024, 1024, 700, False),    # slot in the middle split
+    (16, 8, 256, 1024, 1024, 2500, False),   # ring wrapped: slot 452, all 1024 keys live
+    (16, 2, 512, 2048, 0, 1500, True),       # global layer, k == v, grp 8
+    (4, 4, 64, 40, 0, 45, False),            # global layer past its cache depth: nothing written
+])
+def test_prepkv_attn_fused_equals_separate(gpu, nH, nkv, hd, stride, window, pos, keqv):
+    """q4_prepkv_attn (prepkv folded into the attention split kernel) leaves
+    the same caches and the same output, bit for bit, as q4_prepkv followed
+    by q4_attn."""
+    rng = np.random.default_rng(nH + hd + pos)
+    qkv, qnw, cs, sn, kc, vc = _attn_case(rng, nH, nkv, hd, stride)
+    knw = (rng.random(hd) + 0.5).astype(np.float32)
+    koff, voff = nH * hd, nH * hd + nkv * hd
+    dyn = torch.tensor([pos, pos + 1, 0, 0], dtype=torch.int32, device="cuda")
+    t = dict(qkv=_t(qkv), knw=_t(knw), qnw=_t(qnw), cs=_t(cs), sn=_t(sn))
+    kc1, vc1 = _t(kc, torch.float16), _t(vc, torch.float16)
+    kc2, vc2 = kc1.clone(), vc1.clone()
+    kw = dict(nH=nH, nkv=nkv, hd=hd, stride=stride, window=window, qoff=0, grp=nH // nkv, dyn=dyn)
+    for odt in (torch.float32, torch.float16):
+        gpu.prepkv(t["qkv"], t["knw"], t["cs"], t["sn"], kc1, vc1, nkv=nkv, hd=hd, koff=koff, voff=voff, keqv=keqv,
+                   stride=stride, window=window, dyn=dyn)
+        o1 = gpu.attn(t["qkv"], t["qnw"], t["cs"], t["sn"], kc1, vc1, out_dtype=odt, **kw)
+        o2 = gpu.prepkv_attn(t["qkv"], t["knw"], t["qnw"], t["cs"], t["sn"], kc2, vc2, koff=koff, voff=voff, keqv=keqv,
+                             out_dtype=odt, **kw)
+        torch.cuda.synchronize()
+        assert torch.equal(o1, o2) and torch.equal(kc1, kc2) and torch.equal(vc1, vc2), odt
