@@ -144,6 +144,16 @@ __device__ inline void store_rows(void* __restrict__ yv, int n, float v, int N, 
   }
 }
 
+// 32-bit words of LDS one row group stages for nb blocks (the x blocks of
+// its 4 waves in whole 1 KB direct-load rows, then their fp32 block sums for
+// fp16 x); the host's x_stage_lds() is the same size in bytes.
+template <int R, int XT>
+__device__ inline int stage_words(int nb) {
+  constexpr int SW = 64 / R, S = SW * GEMV_WAVES, XB = XT == Q4_DT_F16 ? 64 : 128, BPD = 1024 / XB;
+  const int nbw = (nb + S - 1) / S * SW, nvw = (nbw + BPD - 1) / BPD;
+  return GEMV_WAVES * nvw * 256 + (XT == Q4_DT_F16 ? GEMV_WAVES * nbw : 0);
+}
+
 // Rows [g*R, g*R + R) of one GEMV over the K slice s of split (the whole K
 // when split == 1). NP = row groups of the launch * R (split-K partial stride).
 //
@@ -163,7 +173,7 @@ __device__ __forceinline__ void gemv_rows(const void* __restrict__ xv, const uin
   constexpr bool XH = (XT == Q4_DT_F16);
   constexpr int SW = 64 / R;               // block slots per wave
   constexpr int S = SW * GEMV_WAVES;       // block slots per workgroup
-  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+  const int tid = threadIdx.x, wave = (tid >> 6) & (GEMV_WAVES - 1), lane = tid & 63;  // wave within its half
   const int r = lane % R, slot = wave * SW + lane / R;
   int b_lo = 0, nb = nblk;
   if (split > 1) {  // (a 64-bit division: kept off the common path)
@@ -289,18 +299,26 @@ __device__ __forceinline__ void gemv_rows(const void* __restrict__ xv, const uin
   if (lane == 0) __hip_atomic_store(&cnt[g], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
+// A workgroup of 256 threads runs one row group; one of 512 threads runs two
+// adjacent row groups (halves of 4 waves, each with its own LDS area and
+// reduction slots; split 1 only): both start together and share the CU from
+// the first cycle, where two 256-thread workgroups on one CU would start one
+// after the other and the second one's x copy would wait behind the first
+// one's weight loads.
 template <int R, int U, int XT, int ST, int YT>
-__global__ void __launch_bounds__(GEMV_THREADS)
+__global__ void __launch_bounds__(2 * GEMV_THREADS)
 gemv_kernel(const void* __restrict__ xv, const uint4* __restrict__ wq, const void* __restrict__ scv, float outscale,
             void* __restrict__ yv, int N, int nblk, int split, float* __restrict__ part, uint32_t* __restrict__ cnt,
             int gated) {
   extern __shared__ __attribute__((aligned(16))) uint32_t smem[];
-  __shared__ float red[GEMV_WAVES][R];
+  __shared__ float red[2][GEMV_WAVES][R];
+  const int halves = blockDim.x / GEMV_THREADS, half = threadIdx.x / GEMV_THREADS;
   // split-K grids (small matrices only) keep the plain order: their row
   // groups are reduced through the workspace, not through L2 reuse
-  const int g = gridDim.y == 1 ? xcd_major(blockIdx.x, gridDim.x) : blockIdx.x;
-  gemv_rows<R, U, XT, ST, YT>(xv, wq, scv, outscale, yv, N, nblk, g, blockIdx.y, split, (long)gridDim.x * R, part,
-                              cnt, smem, red, gated);
+  const int g = (gridDim.y == 1 ? xcd_major(blockIdx.x, gridDim.x) : blockIdx.x) * halves + half;
+  gemv_rows<R, U, XT, ST, YT>(xv, wq, scv, outscale, yv, N, nblk, g, blockIdx.y, split,
+                              (long)gridDim.x * halves * R, part, cnt, smem + half * stage_words<R, XT>(nblk),
+                              red[half], gated);
 }
 
 // Several GEMVs over one x (same K and types) in one launch: segment i owns
@@ -320,11 +338,12 @@ struct GemvSegs {
 };
 
 template <int R, int U, int XT, int ST, int YT>
-__global__ void __launch_bounds__(GEMV_THREADS)
+__global__ void __launch_bounds__(2 * GEMV_THREADS)
 gemv_batch_kernel(const void* __restrict__ xv, int nblk, const GemvSegs segs) {
   extern __shared__ __attribute__((aligned(16))) uint32_t smem[];
-  __shared__ float red[GEMV_WAVES][R];
-  const int g = xcd_major(blockIdx.x, gridDim.x);
+  __shared__ float red[2][GEMV_WAVES][R];
+  const int halves = blockDim.x / GEMV_THREADS, half = threadIdx.x / GEMV_THREADS;
+  const int g = xcd_major(blockIdx.x, gridDim.x) * halves + half;
   // segment selection with compile-time indices only (the argument block
   // stays in the kernarg segment; a dynamic index would copy it to scratch)
   const uint4* wq = segs.s[0].wq;
@@ -343,7 +362,8 @@ gemv_batch_kernel(const void* __restrict__ xv, int nblk, const GemvSegs segs) {
       g0 = segs.s[t - 1].g_end;
     }
   }
-  gemv_rows<R, U, XT, ST, YT>(xv, wq, sc, os, y, N, nblk, g - g0, 0, 1, 0, nullptr, nullptr, smem, red, 0);
+  gemv_rows<R, U, XT, ST, YT>(xv, wq, sc, os, y, N, nblk, g - g0, 0, 1, 0, nullptr, nullptr,
+                              smem + half * stage_words<R, XT>(nblk), red[half], 0);
 }
 
 typedef void (*gemv_fn)(const void*, const uint4*, const void*, float, void*, int, int, int, float*, uint32_t*, int);
@@ -414,6 +434,17 @@ static int units_in_flight(int nb, int R, long wgs) {
   }
   const int per_lane = ceil_div(nb, (64 / R) * GEMV_WAVES);
   return per_lane > 4 && wgs * GEMV_THREADS * 8 <= GEMV_INFLIGHT_UNITS ? 8 : 4;
+}
+
+// Row groups per workgroup: 2 (a 512-thread workgroup, see gemv_kernel) for
+// unsplit grids of an even number of groups that still give one workgroup
+// per CU after pairing (>= 2 GEMV_MIN_WGS groups) and whose two staging
+// areas fit 64 KB of LDS, else 1. Q4MI_GEMV_PAIR=0
+// forces 1, =1 pairs every unsplit even grid (tests and tuning sweeps).
+static int pair_groups(int groups, int split, size_t lds) {
+  const bool can = split == 1 && groups % 2 == 0 && 2 * lds <= 64 * 1024;
+  if (const char* e = getenv("Q4MI_GEMV_PAIR")) return atoi(e) != 0 && can ? 2 : 1;
+  return can && groups >= 2 * GEMV_MIN_WGS ? 2 : 1;
 }
 
 // LDS bytes of x per block, and of the staging area for nb blocks and R
@@ -504,7 +535,8 @@ static int gemv_launch(const void* x, int x_dtype, const uint32_t* wq, const voi
   float* part = pl.ws ? reinterpret_cast<float*>(reinterpret_cast<char*>(ws) + GEMV_TICKET_BYTES) : nullptr;
   const float outscale = scale_fmt == Q4_SCALE_E4M3 ? inv * 256.0f : 1.0f;
   gemv_fn fn = pick(pl.R, pl.U, x_dtype, scale_fmt, y_dtype).one;
-  hipLaunchKernelGGL(fn, dim3(groups, pl.split), dim3(GEMV_THREADS), pl.lds, as_stream(stream), x,
+  const int hv = pair_groups(groups, pl.split, pl.lds);
+  hipLaunchKernelGGL(fn, dim3(groups / hv, pl.split), dim3(GEMV_THREADS * hv), pl.lds * hv, as_stream(stream), x,
                      reinterpret_cast<const uint4*>(wq), scales, outscale, y, N, K / BLK, pl.split, part, cnt, gated);
   Q4_LAUNCHED("gemv");
   return Q4_OK;
@@ -571,7 +603,10 @@ int q4_gemv_batch(const void* x, int x_dtype, int K, int scale_fmt, int y_dtype,
   }
   const int U = units_in_flight(nblk, R, groups);
   gemv_batch_fn fn = pick(R, U, x_dtype, scale_fmt, y_dtype).many;
-  hipLaunchKernelGGL(fn, dim3(groups), dim3(GEMV_THREADS), x_stage_lds(nblk, x_dtype, R), as_stream(stream), x, nblk,
+  const size_t lds = x_stage_lds(nblk, x_dtype, R);
+  const int hv = pair_groups(groups, 1, lds);
+  hipLaunchKernelGGL(fn, dim3(groups / hv), dim3(GEMV_THREADS * hv), lds * hv,
+                     as_stream(stream), x, nblk,
                      segs);
   Q4_LAUNCHED("gemv_batch");
   return Q4_OK;

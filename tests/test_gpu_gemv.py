@@ -335,3 +335,36 @@ def test_gemv_gated_vs_oracle(gpu, I, K, xdt, adt):
     assert act.numel() == I and act.dtype == adt
     tol = 1e-3 if adt == torch.float16 else 5e-5
     assert O.normwise_rel_err(to_np(act).astype(np.float64), ref) <= tol
+
+
+@pytest.mark.parametrize("N,K,rows", [(15360, 3840, None), (30720, 3840, None), (1024, 4096, "16"), (4096, 15360, "32"),
+                                      (128, 256, None)])
+def test_gemv_paired_row_groups_bit_identical(gpu, N, K, rows, monkeypatch):
+    """Two row groups per 512-thread workgroup compute exactly what two
+    256-thread workgroups do: q4_gemv, q4_gemv_batch and q4_gemv_gated give
+    the same bits with pairing forced on and off (128 rows: split-K, never
+    paired), and match the oracle."""
+    from oracle import decode_ops_oracle as D
+    if rows:
+        monkeypatch.setenv("Q4MI_GEMV_ROWS", rows)
+    rng = np.random.default_rng(N + K)
+    q, s, x = _case(rng, N, K)
+    q2, s2 = synth_int4(rng, N, K)
+    wq, sc = upload_int4(q, s)
+    wq2, sc2 = upload_int4(q2, s2)
+    xt = torch.from_numpy(x).cuda()
+    wo, so = gpu.interleave_rows(wq, sc, wq2, sc2, N, K) if N % 32 == 0 else (None, None)
+    outs = {}
+    for pair in ("0", "1"):
+        monkeypatch.setenv("Q4MI_GEMV_PAIR", pair)
+        y = gpu.gemv(xt, wq, sc, N, K, y_dtype=torch.float32)
+        yb = gpu.gemv_batch(xt, [(wq, sc, N, None, None), (wq2, sc2, N, None, None)], K, y_dtype=torch.float32)
+        act = gpu.gemv_gated(xt, wo, so, 2 * N, K, act_dtype=torch.float32)
+        torch.cuda.synchronize()
+        outs[pair] = (y, yb[0], yb[1], act)
+    for a, b in zip(outs["0"], outs["1"]):
+        assert torch.equal(a, b)
+    assert O.normwise_rel_err(to_np(outs["1"][0]), O.gemv_ref(q, s, x)) <= TOL_F32
+    assert O.normwise_rel_err(to_np(outs["1"][2]), O.gemv_ref(q2, s2, x)) <= TOL_F32
+    ref_act = D.gelumul_ref(O.gemv_ref(q, s, x), O.gemv_ref(q2, s2, x))
+    assert O.normwise_rel_err(to_np(outs["1"][3]).astype(np.float64), ref_act) <= 5e-5
