@@ -136,6 +136,76 @@ def i4(lin, pf: bool = True):
     return quant(W, pf), tuple(W.shape)
 
 
+# ------------------------------------------------- on-disk quantized weights
+QUANT_FORMAT = "q4mi-panel64-v1"
+
+
+def save_quant(path, mats: dict) -> None:
+    """Write quantized matrices ``{name: (QW, (N, K))}`` (as :func:`quant`/:func:`i4`
+    return them) to one safetensors file, in the device layouts the kernels
+    read, so a restart loads them instead of re-quantizing (the reference
+    re-quantizes every model load, ~4 minutes; JOURNEY.md:634-635 names a
+    saved format as the follow-up). Per matrix ``name``: ``name.wq`` (panel-64
+    int4 words, int32), ``name.sc16`` (panel-64 fp16 scales), ``name.sc8``
+    (panel-64 e4m3 scale bytes, when the matrix uses them), ``name.w8`` and
+    ``name.sw8`` (packed int8 weights and fp16 row scales, when present);
+    shape, split, e4m3 ``inv`` and the format tag go in the header metadata.
+    Only tensors and JSON-like metadata are stored: loading executes nothing
+    from the file."""
+    import json
+
+    from safetensors.torch import save_file
+
+    tensors, meta = {}, {"format": QUANT_FORMAT}
+    for name, ((bw, bs, split, nblk, inv, bs16, w8, sw8), (N, K)) in mats.items():
+        if "." in name:
+            raise ValueError(f"matrix name {name!r} may not contain '.'")
+        tensors[f"{name}.wq"] = bw.t.contiguous().cpu()
+        tensors[f"{name}.sc16"] = bs16.t.contiguous().cpu()
+        e4m3 = bs.t.dtype == torch.uint8
+        if e4m3:
+            tensors[f"{name}.sc8"] = bs.t.contiguous().cpu()
+        if w8 is not None:
+            tensors[f"{name}.w8"] = w8.t.contiguous().cpu()
+            tensors[f"{name}.sw8"] = sw8.t.contiguous().cpu()
+        meta[name] = json.dumps({"N": int(N), "K": int(K), "split": int(split), "nblk": int(nblk), "inv": float(inv),
+                                 "e4m3": e4m3})
+    save_file(tensors, str(path), metadata=meta)
+
+
+def load_quant(path, device="cuda") -> dict:
+    """Read a file written by :func:`save_quant`: ``{name: (QW, (N, K))}`` with
+    the buffers on ``device``, ready for :func:`gemv_ds` / :func:`gemm_ds`."""
+    import json
+
+    from safetensors import safe_open
+
+    out = {}
+    with safe_open(str(path), framework="pt", device="cpu") as f:
+        meta = f.metadata() or {}
+        if meta.get("format") != QUANT_FORMAT:
+            raise ValueError(f"{path}: not a {QUANT_FORMAT} file (format {meta.get('format')!r})")
+        keys = set(f.keys())
+        for name, js in meta.items():
+            if name == "format":
+                continue
+            m = json.loads(js)
+            N, K = m["N"], m["K"]
+            get = lambda k: Buf(tensor=f.get_tensor(f"{name}.{k}").to(device)) if f"{name}.{k}" in keys else None
+            bw, bs16 = get("wq"), get("sc16")
+            if bw is None or bs16 is None:
+                raise ValueError(f"{path}: matrix {name!r} lacks its words or scales")
+            wb, se = ops.dev_sizes(N, K)
+            if bw.size != wb or bs16.size != 2 * se:
+                raise ValueError(f"{path}: matrix {name!r} has the wrong size for {N}x{K}")
+            bs = get("sc8") if m["e4m3"] else bs16
+            if bs is None:
+                raise ValueError(f"{path}: matrix {name!r} lacks its e4m3 scales")
+            out[name] = (QW(bw, bs, int(m["split"]), int(m["nblk"]), float(m["inv"]), bs16, get("w8"), get("sw8")),
+                         (N, K))
+    return out
+
+
 class GemvDesc(NamedTuple):
     dp: tuple
     dr: None
