@@ -204,6 +204,65 @@ def bench_gemv_single(ops, N: int, K: int, e4m3: bool, reps: int = 10):
             "frac_of_hbm_peak": round(per / us / 1e3 / HBM_PEAK_GBS, 4), "distinct_weight_sets": n}
 
 
+def bench_small_m(ops, reps: int = 6):
+    """Small-M GEMV (speculative-decode verification: M tokens against one
+    matrix) on the decode shapes, each path timed as a graph of launches over
+    distinct weights (>= 1.5 GB): the MFMA path, the bit-exact VALU path, the
+    W4A16 prefill GEMM at the same M, and M single-vector GEMVs. GB/s counts
+    the weight and scale bytes once per launch (what one GEMV reads)."""
+    import torch
+
+    dev = torch.device("cuda:0")
+    gen = torch.Generator(device=dev).manual_seed(4)
+
+    def timed(fn, n):
+        g = ops.Graph()
+        with g.capture():
+            for i in range(n):
+                fn(i)
+        g.launch()
+        g.launch()
+        a = torch.cuda.Event(enable_timing=True)
+        b = torch.cuda.Event(enable_timing=True)
+        a.record(g.stream)
+        for _ in range(reps):
+            g.launch()
+        b.record(g.stream)
+        b.synchronize()
+        g.destroy()
+        return a.elapsed_time(b) * 1e3 / (reps * n)
+
+    out = {}
+    for name, N, K in [("c1", I, H), ("gate_up", 2 * I, H), ("down", H, I)]:
+        per = gemv_bytes(N, K)
+        n = max(4, (1536 << 20) // per)
+        mats = []
+        for _ in range(n):
+            w = torch.randint(-2 ** 31, 2 ** 31 - 1, (N * K // 8,), dtype=torch.int64, device=dev,
+                              generator=gen).to(torch.int32)
+            s = (torch.randn(N * K // 32, device=dev, generator=gen) * 0.02).abs().to(torch.float16)
+            mats.append((w, s))
+        x1 = torch.randn(K, device=dev, generator=gen).to(torch.float16)
+        y1 = torch.empty(N, dtype=torch.float16, device=dev)
+        t1 = timed(lambda i: ops.gemv(x1, mats[i][0], mats[i][1], N, K, y=y1), n)
+        for M in (4, 8, 16):
+            X = torch.randn((M, K), device=dev, generator=gen).to(torch.float16)
+            Y = torch.empty((M, N), dtype=torch.float16, device=dev)
+            t_mm = timed(lambda i: ops.gemv_multi(X, mats[i][0], mats[i][1], N, K, y=Y), n)
+            t_ex = timed(lambda i: ops.gemv_multi(X, mats[i][0], mats[i][1], N, K, y=Y, exact=True), n)
+            need = ops.gemm_workspace_bytes(M, N, K)
+            ws = torch.empty(need, dtype=torch.uint8, device=dev) if need else None
+            t_w4 = timed(lambda i: ops.gemm_w4a16(X, mats[i][0], mats[i][1], N, Y=Y, ws=ws), n)
+            out[f"{name}_{N}x{K}_M{M}"] = {
+                "mfma_us": round(t_mm, 2), "mfma_GBps": round(per / t_mm / 1e3, 1),
+                "exact_us": round(t_ex, 2), "w4a16_gemm_us": round(t_w4, 2),
+                "m_single_gemvs_us": round(M * t1, 2), "speedup_vs_w4a16": round(t_w4 / t_mm, 2),
+                "speedup_vs_m_gemvs": round(M * t1 / t_mm, 2)}
+        del mats
+        torch.cuda.empty_cache()
+    return out
+
+
 def bench_token_step(ops, steps: int, warmup: int, pos: int = 1023, fast: bool = False):
     """A whole decode token through the engine mirror (vk_engine.py): the
     reference's per-layer dispatch order (norm, q/k/v, prepkv, attention, o,
@@ -510,6 +569,8 @@ def main():
               "c3_15360x3840_e4m3_scales": bench_gemv_single(ops, I, H, True),
               "lm_head_262144x3840_f16_scales": bench_gemv_single(ops, V, H, False, reps=4)}
     print(f"[bench] single-shape gemv {single}", flush=True)
+    small = bench_small_m(ops)
+    print(f"[bench] small-M gemv {small}", flush=True)
     w8 = w4 = None
     if not args.no_gemm:
         w8 = bench_w8a8(ops)
@@ -553,6 +614,7 @@ def main():
             "ms_per_step_percentiles": dec["ms_per_step_percentiles"],
             "single_shape_gemv": single,
             "full_token_step": tok,
+            "small_m_gemv": small,
         },
         "roofline": {
             "bound": "hbm",

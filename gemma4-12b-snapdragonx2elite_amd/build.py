@@ -33,6 +33,11 @@ HIPCC_FLAGS = [
 ]
 
 
+# per-source extra flags: the small-M GEMV's MFMA results are read by VALU
+# at once; in VGPRs (not AGPRs) that saves one v_accvgpr_read per value
+FILE_FLAGS = {"gemv.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"]}
+
+
 def _hipcc() -> str:
     for cand in (shutil.which("hipcc"), "/opt/rocm/bin/hipcc"):
         if cand and Path(cand).exists():
@@ -59,7 +64,7 @@ def build(verbose: bool = False, jobs: int | None = None) -> Path:
 
     def compile_one(pair):
         s, o = pair
-        return s, _run([hipcc, *HIPCC_FLAGS, "-c", str(s), "-o", str(o)])
+        return s, _run([hipcc, *HIPCC_FLAGS, *FILE_FLAGS.get(s.name, []), "-c", str(s), "-o", str(o)])
 
     with cf.ThreadPoolExecutor(jobs) as ex:
         for s, (rc, out) in ex.map(compile_one, zip(srcs, objs)):

@@ -44,6 +44,8 @@ namespace q4 {
 constexpr int GEMV_THREADS = 256;
 constexpr int GEMV_WAVES = GEMV_THREADS / 64;
 constexpr int GEMV_LDS_MAX = 64 * 1024;    // x staging cap per workgroup (bytes)
+constexpr size_t GEMV_MV_LDS_MAX = 144 * 1024;  // x staging cap of the multi-vector GEMV (of 160 KB LDS)
+constexpr int GEMV_MV_MAX = 8;              // vectors per multi-vector GEMV launch
 constexpr int GEMV_TARGET_WGS = 480;       // preferred workgroup count (see rows_per_group())
 constexpr int GEMV_MIN_WGS = 240;          // about one per CU; below this K is split across workgroups
 constexpr long GEMV_INFLIGHT_UNITS = 8L << 16;  // 16-byte weight units in flight over a grid (8 MB)
@@ -321,6 +323,288 @@ gemv_kernel(const void* __restrict__ xv, const uint4* __restrict__ wq, const voi
                               red[half], gated);
 }
 
+// Several activation vectors through one weight stream (speculative-decode
+// verification: M <= MV tokens against the same matrix): rows [g*R, g*R+R)
+// of Y[v][n] = GEMV(x_v) for v < M, fp16 x rows of X[M][K]. The structure
+// is gemv_rows' (per-wave x staging, now MV vectors per wave, the load ring,
+// split 1) and each vector's arithmetic is q4_gemv's exactly (same block
+// dot product, same block order, same reduction order), so every output
+// row is bit-identical to a single GEMV with the same plan; the weight
+// words and scales are loaded once for all vectors.
+template <int R, int U, int ST, int YT, int MV>
+__device__ __forceinline__ void gemv_rows_mv(const uint16_t* __restrict__ X, int M, const uint4* __restrict__ wq,
+                                             const void* __restrict__ scv, float outscale, void* __restrict__ Y,
+                                             int ldy, int N, int nblk, int g, uint32_t* __restrict__ smem,
+                                             float (*red)[MV][R]) {
+  constexpr int SW = 64 / R, S = SW * GEMV_WAVES;
+  constexpr int XB = 64, CPB = XB / 16, BPD = 64 / CPB;
+  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+  const int r = lane % R, slot = wave * SW + lane / R;
+  const int nb = nblk;
+  const int nbw = (nb + S - 1) / S * SW, nvw = (nbw + BPD - 1) / BPD;
+  // LDS: wave w's x areas (one per vector, nvw KB each), then every wave's
+  // block sums (nbw floats per vector)
+  uint32_t* xw = smem + wave * MV * nvw * 256;
+#pragma unroll
+  for (int v = 0; v < MV; ++v) {
+    const uint8_t* xsrc = reinterpret_cast<const uint8_t*>(X + (long)min(v, M - 1) * nblk * BLK);
+    for (int d = 0; d < nvw; ++d) {
+      const int lb = d * BPD + lane / CPB;
+      const int j = min(lb / SW * S + wave * SW + lb % SW, nb - 1);
+      dma16(xsrc + (long)j * XB + (lane % CPB) * 16, xw + (v * nvw + d) * 256);
+    }
+  }
+  const int n0 = g * R;
+  const long ubase = ((long)(n0 / PANEL) * nblk) * PANEL + (n0 % PANEL) + r;
+  const uint8_t* wb = reinterpret_cast<const uint8_t*>(wq);
+  v4u u[U];
+  uint32_t sb[U];
+#pragma unroll
+  for (int t = 0; t < U; ++t) {
+    const long ix = ubase + (long)min(slot + t * S, nb - 1) * PANEL;
+    u[t] = ld16_nt(wb + ix * 16);
+    sb[t] = load_scale<ST>(scv, ix);
+  }
+  vmwait<2 * U>();
+  float* xsum = reinterpret_cast<float*>(smem + GEMV_WAVES * MV * nvw * 256) + wave * MV * nbw;
+  {
+    const v2h one2 = {(_Float16)1.0f, (_Float16)1.0f};
+    for (int lb = lane; lb < nbw; lb += 64) {
+#pragma unroll
+      for (int v = 0; v < MV; ++v) {
+        float t = 0.0f;
+#pragma unroll
+        for (int i = 0; i < 16; ++i) t = __builtin_amdgcn_fdot2(as_h2(xw[(v * nvw) * 256 + lb * 16 + i]), one2, t, false);
+        xsum[v * nbw + lb] = t;
+      }
+    }
+  }
+  float acc[MV];
+#pragma unroll
+  for (int v = 0; v < MV; ++v) acc[v] = 0.0f;
+  auto use = [&](int jj, int lb, const v4u& w, uint32_t sv) {
+    if (jj < nb) {
+      const float sc = scale_value<ST>(sv);
+#pragma unroll
+      for (int v = 0; v < MV; ++v)
+        acc[v] = fmaf(sc, block_dot_h(w, xw + (v * nvw) * 256 + lb * 16, xsum[v * nbw + lb]), acc[v]);
+    }
+  };
+  const int rounds = ((nb + S - 1) / S + U - 1) / U;
+  int j = slot, lb = lane / R;
+  for (int rd = 1; rd < rounds; ++rd) {
+    static_for<0, U>([&](auto tc) {
+      constexpr int t = decltype(tc)::value;
+      vmwait<2 * (U - 1)>();
+      pin(u[t]);
+      pin(sb[t]);
+      use(j + t * S, lb + t * SW, u[t], sb[t]);
+      const long ix = ubase + (long)min(j + (t + U) * S, nb - 1) * PANEL;
+      u[t] = ld16_nt(wb + ix * 16);
+      sb[t] = load_scale<ST>(scv, ix);
+    });
+    j += S * U;
+    lb += SW * U;
+  }
+  static_for<0, U>([&](auto tc) {
+    constexpr int t = decltype(tc)::value;
+    vmwait<2 * (U - 1 - t)>();
+    pin(u[t]);
+    pin(sb[t]);
+    use(j + t * S, lb + t * SW, u[t], sb[t]);
+  });
+#pragma unroll
+  for (int v = 0; v < MV; ++v) {
+#pragma unroll
+    for (int off = R; off < 64; off <<= 1) acc[v] += __shfl_xor(acc[v], off, 64);
+    if (lane < R) red[wave][v][r] = acc[v];
+  }
+  __syncthreads();
+  if (wave != 0) return;
+  const int n = n0 + r;
+  for (int v = 0; v < M && v < MV; ++v) {
+    if (lane < R && n < N) {
+      const float y = (((red[0][v][r] + red[1][v][r]) + red[2][v][r]) + red[3][v][r]) * outscale;
+      if constexpr (YT == Q4_DT_F16) reinterpret_cast<uint16_t*>(Y)[(long)v * ldy + n] = f2h(y);
+      else reinterpret_cast<float*>(Y)[(long)v * ldy + n] = y;
+    }
+  }
+}
+
+template <int R, int U, int ST, int YT, int MV>
+__global__ void __launch_bounds__(GEMV_THREADS)
+gemv_multi_kernel(const uint16_t* __restrict__ X, int M, const uint4* __restrict__ wq, const void* __restrict__ scv,
+                  float outscale, void* __restrict__ Y, int ldy, int N, int nblk) {
+  extern __shared__ __attribute__((aligned(16))) uint32_t smem[];
+  __shared__ float red[GEMV_WAVES][MV][R];
+  gemv_rows_mv<R, U, ST, YT, MV>(X, M, wq, scv, outscale, Y, ldy, N, nblk, xcd_major(blockIdx.x, gridDim.x), smem,
+                                 red);
+}
+
+// ---- small-M GEMV on MFMA ------------------------------------------------------
+// Y[m][n] = outscale * sum_b s[n,b] * sum_{k in b} (q[n,k] - 8) x_m[k] for up
+// to 16 fp16 vectors x_m, the decode GEMV's arithmetic per block (exact
+// (q - 8) times fp16 x summed in fp32, times the fp32 block scale, blocks
+// accumulated in fp32) with the block sums of all vectors from one
+// v_mfma_f32_16x16x32_f16 per 16 rows and block:
+//   A (16 x 32) = the block's x slice of the 16 vector slots (slot m >= M
+//                 repeats vector M - 1; its outputs are not stored),
+//   B (32 x 16) = (q - 8) of 16 weight rows, exact in fp16,
+//   D (16 x 16) = per-block sums; lane (c, g) = (lane % 16, lane / 16) holds
+//                 vectors 4g .. 4g+3 of weight row c and adds them, times the
+//                 block scale of row c, to its fp32 accumulators.
+// Lane (c, g) supplies k = 8g .. 8g+7 of the block to both operands: x
+// elements 8g .. 8g+7 (16 bytes) and word g of the row's 16-byte unit
+// (elements 8g .. 8g+7 at nibbles (e & 1) * 4 + (e >> 1)). Dequant: the
+// masked nibble pairs OR 0x6400 (low nibbles: 1024 + q) or 0x5400 (high
+// nibbles, mantissa bits 4-7: 64 + q), minus 1032 or 72, give q - 8
+// exactly; 9 VALU operations per 8 codes, whatever the number of vectors.
+//
+// A workgroup (4 waves) owns T tiles of 16 rows (16T rows of one 64-row
+// panel). One step of a wave covers 4 (tile, block) pairs, 4/T blocks of
+// all T tiles: each lane loads one whole 16-byte unit (lane (c, g): tile
+// g % T, row c, block g / T of the step; 1 KB of contiguous weights per
+// wave for T = 4), and a 4 x 4 transpose of the words across the four
+// 16-lane rows (two v_permlane32_swap, two v_permlane16_swap) hands lane
+// (c, g) word g of the 4 units of its column, one per MFMA. Steps go to
+// the waves round-robin (the 4 waves read adjacent blocks together); U
+// steps of loads stay in flight (x slices, the unit, 4 scales per step;
+// explicit wait counts as in the GEMV), and the 4 waves' partial sums meet
+// in LDS in wave order (deterministic).
+__device__ inline v8h codes_to_h8(uint32_t w) {
+  const uint32_t w8 = w >> 8;
+  const v2h lo = {(_Float16)-1032.0f, (_Float16)-1032.0f}, hi = {(_Float16)-72.0f, (_Float16)-72.0f};
+  const v2h p0 = as_h2(and_or(w, 0x000F000Fu, 0x64006400u)) + lo;   // e0 e1
+  const v2h p1 = as_h2(and_or(w, 0x00F000F0u, 0x54005400u)) + hi;   // e2 e3
+  const v2h p2 = as_h2(and_or(w8, 0x000F000Fu, 0x64006400u)) + lo;  // e4 e5
+  const v2h p3 = as_h2(and_or(w8, 0x00F000F0u, 0x54005400u)) + hi;  // e6 e7
+  return v8h{p0[0], p0[1], p1[0], p1[1], p2[0], p2[1], p3[0], p3[1]};
+}
+
+// 4 x 4 transpose across the 16-lane rows: on entry word j of lane (c, g)
+// is element (g, j); on return word t of lane (c, g) is element (t, g), the
+// word g of the unit that lane (c, t) loaded.
+__device__ inline v4u transpose_rows(v4u a) {
+  const auto p02 = __builtin_amdgcn_permlane32_swap(a[0], a[2], false, false);
+  const auto p13 = __builtin_amdgcn_permlane32_swap(a[1], a[3], false, false);
+  const auto q01 = __builtin_amdgcn_permlane16_swap(p02[0], p13[0], false, false);
+  const auto q23 = __builtin_amdgcn_permlane16_swap(p02[1], p13[1], false, false);
+  return v4u{q01[0], q01[1], q23[0], q23[1]};
+}
+
+// Scale bits at a uniform base + the lane's offset + OFF bytes.
+template <int ST, int OFF>
+__device__ inline uint32_t mm_scale(const uint8_t* sbase, uint32_t voff) {
+  if constexpr (ST == Q4_SCALE_F16) return ld2_so_off<OFF>(sbase, voff);
+  else return ld1_so_off<OFF>(sbase, voff);
+}
+
+template <int T, int U, int ST, int YT>
+__global__ void __launch_bounds__(GEMV_THREADS)
+gemv_mm_kernel(const uint16_t* __restrict__ X, int M, const uint8_t* __restrict__ wq, const void* __restrict__ scv,
+               float outscale, void* __restrict__ Y, int N, int nblk) {
+  constexpr int BPS = 4 / T;                      // blocks per step
+  constexpr int L = BPS + 1 + 4;                  // loads per step: x slices, the unit, 4 scales
+  constexpr int SB = ST == Q4_SCALE_F16 ? 2 : 1;  // scale bytes
+  static_assert(U * L < 64, "vmcnt range");
+  __shared__ v4f red[GEMV_WAVES][T][64];
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // uniform: block indices and bases live in SGPRs
+  const int c = lane & 15, g = lane >> 4;
+  const int n0 = xcd_major(blockIdx.x, gridDim.x) * 16 * T;
+  // unit index of (row n0 + r, block b) = pu + r + 64 b (the 16T rows lie in one panel)
+  const long pu = (long)(n0 / PANEL) * nblk * PANEL + (n0 % PANEL);
+  const uint8_t* xbase = reinterpret_cast<const uint8_t*>(X);
+  const uint8_t* wbase = wq + pu * 16;
+  const uint8_t* sbase = reinterpret_cast<const uint8_t*>(scv) + pu * SB;
+  const uint32_t xo = (uint32_t)min(c, M - 1) * (uint32_t)(nblk * BLK * 2) + g * 16;
+  const int lrow = 16 * (g % T) + c, lblk = g / T;  // the unit lane (c, g) loads: row, block within the step
+  const uint32_t so = c * SB;
+  const int nsteps = (nblk + BPS - 1) / BPS;
+  const int rounds = ((nsteps + GEMV_WAVES - 1) / GEMV_WAVES + U - 1) / U;
+  v4u xr[U][BPS], wr[U];
+  uint32_t sr[U][4];
+  auto issue = [&](int u, int s) {
+    const int b0 = (wave + GEMV_WAVES * s) * BPS;  // first block of the step
+    static_for<0, BPS>([&](auto ic) {
+      constexpr int i = decltype(ic)::value;
+      xr[u][i] = ld16_so(xbase + (long)min(b0 + i, nblk - 1) * (BLK * 2), xo);
+    });
+    wr[u] = ld16_so(wbase, (uint32_t)(lrow * 16) + ((uint32_t)min(b0 + lblk, nblk - 1) << 10));
+    static_for<0, 4>([&](auto jc) {
+      constexpr int j = decltype(jc)::value;
+      sr[u][j] = mm_scale<ST, 16 * (j % T) * SB>(sbase + (long)min(b0 + j / T, nblk - 1) * (PANEL * SB), so);
+    });
+  };
+  v4f acc[T];
+#pragma unroll
+  for (int t = 0; t < T; ++t) acc[t] = v4f{0.0f, 0.0f, 0.0f, 0.0f};
+  auto use = [&](int u, int s) {
+    const int b0 = (wave + GEMV_WAVES * s) * BPS;
+    if (b0 < nblk) {
+      const v4u w = transpose_rows(wr[u]);
+      v4f d[4];
+      static_for<0, 4>([&](auto jc) {
+        constexpr int j = decltype(jc)::value;
+        if (j / T == 0 || b0 + j / T < nblk)
+          d[j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(v8h, xr[u][j / T]), codes_to_h8(w[j]),
+                                                        v4f{0.0f, 0.0f, 0.0f, 0.0f}, 0, 0, 0);
+      });
+      static_for<0, 4>([&](auto jc) {
+        constexpr int j = decltype(jc)::value;
+        if (j / T == 0 || b0 + j / T < nblk) {
+          const float sc = scale_value<ST>(sr[u][j]);
+#pragma unroll
+          for (int r = 0; r < 4; ++r) acc[j % T][r] = fmaf(sc, d[j][r], acc[j % T][r]);
+        }
+      });
+    }
+  };
+#pragma unroll
+  for (int u = 0; u < U; ++u) issue(u, u);
+  int s = 0;
+  for (int rd = 1; rd < rounds; ++rd) {
+    static_for<0, U>([&](auto uc) {
+      constexpr int u = decltype(uc)::value;
+      vmwait<(U - 1) * L>();
+      pin(wr[u]);
+#pragma unroll
+      for (int i = 0; i < BPS; ++i) pin(xr[u][i]);
+#pragma unroll
+      for (int j = 0; j < 4; ++j) pin(sr[u][j]);
+      use(u, s + u);
+      issue(u, s + u + U);
+    });
+    s += U;
+  }
+  static_for<0, U>([&](auto uc) {
+    constexpr int u = decltype(uc)::value;
+    vmwait<(U - 1 - u) * L>();
+    pin(wr[u]);
+#pragma unroll
+    for (int i = 0; i < BPS; ++i) pin(xr[u][i]);
+#pragma unroll
+    for (int j = 0; j < 4; ++j) pin(sr[u][j]);
+    use(u, s + u);
+  });
+#pragma unroll
+  for (int t = 0; t < T; ++t) red[wave][t][lane] = acc[t];
+  __syncthreads();
+  for (int t = wave; t < T; t += GEMV_WAVES) {
+    const v4f y = ((red[0][t][lane] + red[1][t][lane]) + red[2][t][lane]) + red[3][t][lane];
+    const int n = n0 + 16 * t + c;
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int m = 4 * g + r;
+      if (m < M && n < N) {
+        const float v = y[r] * outscale;
+        if constexpr (YT == Q4_DT_F16) reinterpret_cast<uint16_t*>(Y)[(long)m * N + n] = f2h(v);
+        else reinterpret_cast<float*>(Y)[(long)m * N + n] = v;
+      }
+    }
+  }
+}
+
 // Several GEMVs over one x (same K and types) in one launch: segment i owns
 // row groups [g_end[i-1], g_end[i]) of the grid; every segment covers whole
 // panels.
@@ -397,6 +681,67 @@ static GemvFns pick(int R, int U, int xt, int st, int yt) {
     case 16: return pick_u<16>(U, xt, st, yt);
     default: return pick_u<8>(U, xt, st, yt);
   }
+}
+
+typedef void (*gemv_multi_fn)(const uint16_t*, int, const uint4*, const void*, float, void*, int, int, int);
+template <int R, int U, int ST, int YT>
+static gemv_multi_fn pick_mv_v(int mv) {
+  return mv == 2 ? gemv_multi_kernel<R, U, ST, YT, 2>
+                 : mv == 4 ? gemv_multi_kernel<R, U, ST, YT, 4> : gemv_multi_kernel<R, U, ST, YT, 8>;
+}
+template <int R, int U>
+static gemv_multi_fn pick_mv_sy(int mv, int st, int yt) {
+  if (st == Q4_SCALE_E4M3)
+    return yt == Q4_DT_F16 ? pick_mv_v<R, U, Q4_SCALE_E4M3, Q4_DT_F16>(mv) : pick_mv_v<R, U, Q4_SCALE_E4M3, Q4_DT_F32>(mv);
+  return yt == Q4_DT_F16 ? pick_mv_v<R, U, Q4_SCALE_F16, Q4_DT_F16>(mv) : pick_mv_v<R, U, Q4_SCALE_F16, Q4_DT_F32>(mv);
+}
+template <int R>
+static gemv_multi_fn pick_mv_u(int U, int mv, int st, int yt) {
+  return U == 4 ? pick_mv_sy<R, 4>(mv, st, yt) : pick_mv_sy<R, 8>(mv, st, yt);
+}
+static gemv_multi_fn pick_mv(int R, int U, int mv, int st, int yt) {
+  switch (R) {
+    case 64: return pick_mv_u<64>(U, mv, st, yt);
+    case 32: return pick_mv_u<32>(U, mv, st, yt);
+    case 16: return pick_mv_u<16>(U, mv, st, yt);
+    default: return pick_mv_u<8>(U, mv, st, yt);
+  }
+}
+
+typedef void (*gemv_mm_fn)(const uint16_t*, int, const uint8_t*, const void*, float, void*, int, int);
+template <int T, int U>
+static gemv_mm_fn pick_mm_sy(int st, int yt) {
+  if (st == Q4_SCALE_E4M3)
+    return yt == Q4_DT_F16 ? gemv_mm_kernel<T, U, Q4_SCALE_E4M3, Q4_DT_F16> : gemv_mm_kernel<T, U, Q4_SCALE_E4M3, Q4_DT_F32>;
+  return yt == Q4_DT_F16 ? gemv_mm_kernel<T, U, Q4_SCALE_F16, Q4_DT_F16> : gemv_mm_kernel<T, U, Q4_SCALE_F16, Q4_DT_F32>;
+}
+// (T, U) pairs built: U = 4 or the deepest ring whose U (4/T + 5) loads
+// per step stay under the 63 the wait count can express (T = 1: 6,
+// T = 2: 8, T = 4: 10); the deeper one is the default.
+static gemv_mm_fn pick_mm(int T, bool deep, int st, int yt) {
+  switch (T) {
+    case 4: return deep ? pick_mm_sy<4, 10>(st, yt) : pick_mm_sy<4, 4>(st, yt);
+    case 2: return deep ? pick_mm_sy<2, 8>(st, yt) : pick_mm_sy<2, 4>(st, yt);
+    default: return deep ? pick_mm_sy<1, 6>(st, yt) : pick_mm_sy<1, 4>(st, yt);
+  }
+}
+// Row tiles of 16 per workgroup for NP padded rows: the largest T of 4, 2, 1
+// that still gives GEMV_MIN_WGS workgroups (about one per CU): the x slices
+// each wave reads are shared by T tiles. Q4MI_GEMV_MM_TILES (1/2/4) and
+// Q4MI_GEMV_MM_DEEP (0/1) override the plan for tuning sweeps.
+static int mm_tiles(int NP) {
+  int T = 1;
+  for (int c : {4, 2})
+    if (NP / (16 * c) >= GEMV_MIN_WGS) { T = c; break; }
+  if (const char* e = getenv("Q4MI_GEMV_MM_TILES")) {
+    const int v = atoi(e);
+    if (v == 1 || v == 2 || v == 4) T = v;
+  }
+  return T;
+}
+static bool mm_deep() {
+  const char* e = getenv("Q4MI_GEMV_MM_DEEP");
+  return e ? atoi(e) != 0 : false;
 }
 
 // Rows per workgroup R for NP padded rows: the largest R of 64, 32, 16 that
@@ -563,6 +908,48 @@ int q4_gemv_f16s(const void* x, int x_dtype, const uint32_t* wq, const uint16_t*
 int q4_gemv_e4m3s(const void* x, int x_dtype, const uint32_t* wq, const uint8_t* sc8, float inv, void* y, int y_dtype,
                   int N, int K, int split, void* ws, size_t ws_size, void* stream) {
   return q4_gemv(x, x_dtype, wq, sc8, Q4_SCALE_E4M3, inv, y, y_dtype, N, K, split, ws, ws_size, stream);
+}
+
+int q4_gemv_multi(const void* x, int M, const uint32_t* wq, const void* scales, int scale_fmt, float inv, void* y,
+                  int y_dtype, int N, int K, int exact, void* stream) {
+  clear_error();
+  Q4_ARG(M >= 1 && M <= Q4_GEMV_MAX_VECTORS, "multi-vector GEMV takes 1..%d vectors (got M=%d)", Q4_GEMV_MAX_VECTORS,
+         M);
+  Q4_ARG(N > 0 && K > 0 && K % BLK == 0, "bad GEMV shape N=%d K=%d (K must be a positive multiple of 32)", N, K);
+  Q4_ARG(x && wq && scales && y, "null pointer");
+  Q4_ARG(y_dtype == Q4_DT_F32 || y_dtype == Q4_DT_F16, "bad y dtype %d", y_dtype);
+  Q4_ARG(scale_fmt == Q4_SCALE_F16 || scale_fmt == Q4_SCALE_E4M3, "bad scale format %d", scale_fmt);
+  Q4_ARG(((uintptr_t)wq & 15) == 0 && ((uintptr_t)x & 15) == 0, "wq and x must be 16-byte aligned");
+  Q4_ARG(N <= (1 << 30) && (long)K <= (1L << 24), "GEMV too large");
+  const int NP = pad_rows(N), nblk = K / BLK;
+  const float outscale = scale_fmt == Q4_SCALE_E4M3 ? inv * 256.0f : 1.0f;
+  if (!exact) {
+    const int T = mm_tiles(NP);
+    hipLaunchKernelGGL(pick_mm(T, mm_deep(), scale_fmt, y_dtype), dim3(NP / (16 * T)), dim3(GEMV_THREADS), 0,
+                       as_stream(stream), reinterpret_cast<const uint16_t*>(x), M,
+                       reinterpret_cast<const uint8_t*>(wq), scales, outscale, y, N, nblk);
+    Q4_LAUNCHED("gemv_mm");
+    return Q4_OK;
+  }
+  const int R = rows_per_group(NP), groups = NP / R;
+  const int U = units_in_flight(nblk, R, groups);
+  const size_t ysz = y_dtype == Q4_DT_F16 ? 2 : 4;
+  // launches of up to 8 vectors, fewer where their x slices do not fit the LDS
+  const size_t per_vec = x_stage_lds(nblk, Q4_DT_F16, R);
+  int chunk = GEMV_MV_MAX;
+  while (chunk > 2 && (size_t)chunk * per_vec > GEMV_MV_LDS_MAX) chunk >>= 1;
+  Q4_ARG((size_t)2 * per_vec <= GEMV_MV_LDS_MAX, "multi-vector GEMV with K=%d needs %zu bytes of LDS (max %zu)", K,
+         2 * per_vec, GEMV_MV_LDS_MAX);
+  for (int m0 = 0; m0 < M; m0 += chunk) {
+    const int m = M - m0 < chunk ? M - m0 : chunk;
+    const int mv = m <= 2 ? 2 : m <= 4 ? 4 : 8;
+    hipLaunchKernelGGL(pick_mv(R, U, mv, scale_fmt, y_dtype), dim3(groups), dim3(GEMV_THREADS), mv * per_vec,
+                       as_stream(stream), reinterpret_cast<const uint16_t*>(x) + (long)m0 * K, m,
+                       reinterpret_cast<const uint4*>(wq), scales, outscale,
+                       reinterpret_cast<char*>(y) + (long)m0 * N * ysz, N, N, nblk);
+    Q4_LAUNCHED("gemv_multi");
+  }
+  return Q4_OK;
 }
 
 int q4_gemv_batch(const void* x, int x_dtype, int K, int scale_fmt, int y_dtype, int count,

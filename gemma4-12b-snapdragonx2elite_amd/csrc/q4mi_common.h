@@ -119,6 +119,34 @@ __device__ inline v2u ld8(const void* p) {
   asm volatile("global_load_dwordx2 %0, %1, off" : "=v"(r) : "v"(p));
   return r;
 }
+// Uniform base (SGPR pair) + per-lane 32-bit byte offset + immediate byte
+// offset OFF (-4096 .. 4095), streaming (read-once data).
+template <int OFF>
+__device__ inline uint32_t ld4_so_nt(const void* sbase, uint32_t voff) {
+  uint32_t r;
+  asm volatile("global_load_dword %0, %1, %2 offset:%3 nt" : "=v"(r) : "v"(voff), "s"(sbase), "n"(OFF));
+  return r;
+}
+template <int OFF>
+__device__ inline uint32_t ld2_so_off(const void* sbase, uint32_t voff) {
+  uint32_t r;
+  asm volatile("global_load_ushort %0, %1, %2 offset:%3" : "=v"(r) : "v"(voff), "s"(sbase), "n"(OFF));
+  return r;
+}
+template <int OFF>
+__device__ inline uint32_t ld1_so_off(const void* sbase, uint32_t voff) {
+  uint32_t r;
+  asm volatile("global_load_ubyte %0, %1, %2 offset:%3" : "=v"(r) : "v"(voff), "s"(sbase), "n"(OFF));
+  return r;
+}
+// (a & m) | c in one VALU operation. v_and_or_b32 takes no literal
+// constants and reads at most one SGPR: m comes in an SGPR, c in a VGPR
+// (both loop-invariant, so they are set up once).
+__device__ inline uint32_t and_or(uint32_t a, uint32_t m, uint32_t c) {
+  uint32_t r;
+  asm("v_and_or_b32 %0, %1, %2, %3" : "=v"(r) : "v"(a), "s"(m), "v"(c));
+  return r;
+}
 __device__ inline uint32_t ld2(const void* p) {
   uint32_t r;
   asm volatile("global_load_ushort %0, %1, off" : "=v"(r) : "v"(p));

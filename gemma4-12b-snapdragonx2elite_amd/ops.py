@@ -203,6 +203,34 @@ def gemv(x: torch.Tensor, wq: torch.Tensor, scales: torch.Tensor, N: int, K: int
     return y
 
 
+GEMV_MAX_VECTORS = 16
+
+
+def gemv_multi(x: torch.Tensor, wq: torch.Tensor, scales: torch.Tensor, N: int, K: int, *,
+               scale_fmt: int = SCALE_F16, inv: float = 1.0, y: torch.Tensor | None = None,
+               y_dtype=None, exact: bool = False) -> torch.Tensor:
+    """Y[m] = GEMV of x[m] for the M fp16 rows of ``x`` [M][K] (M <= 16),
+    reading the weights once. ``exact``: every row bit-identical to
+    :func:`gemv` of that row when :func:`gemv` runs unsplit (VALU path, one
+    weight stream per 2-8 vectors); otherwise one MFMA launch for all rows,
+    equal to :func:`gemv` to fp32 rounding. Returns Y [M][N]."""
+    if x.dtype != torch.float16:
+        raise ValueError("multi-vector GEMV takes fp16 activations")
+    if x.dim() != 2 or x.shape[1] != K or not x.is_contiguous():
+        raise ValueError(f"x must be a contiguous [M][K={K}] tensor")
+    M = x.shape[0]
+    if not 1 <= M <= GEMV_MAX_VECTORS:
+        raise ValueError(f"multi-vector GEMV takes 1..{GEMV_MAX_VECTORS} vectors (got {M})")
+    if y is None:
+        y = torch.empty(M, N, dtype=y_dtype or torch.float16, device=x.device)
+    elif y.dim() != 2 or tuple(y.shape) != (M, N) or not y.is_contiguous():
+        raise ValueError(f"y must be a contiguous [{M}][{N}] tensor")
+    _check_int4(wq, scales, N, K, 1 if scale_fmt == SCALE_E4M3 else 2)
+    call("q4_gemv_multi", _p(x), M, _p(wq), _p(scales), scale_fmt, C.c_float(inv), _p(y), _dt(y), N, K,
+         int(bool(exact)), _stream())
+    return y
+
+
 def interleave_rows(wa: torch.Tensor, sa: torch.Tensor, wb: torch.Tensor, sb: torch.Tensor, N: int, K: int):
     """Gate/up matrices (panel-64, N rows each) -> one of 2N rows, row 2i from
     ``wa``/``sa`` and row 2i + 1 from ``wb``/``sb`` (the layout of :func:`gemv_gated`)."""

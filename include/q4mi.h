@@ -165,6 +165,27 @@ int q4_gemv_batch(const void* x, int x_dtype, int K, int scale_fmt,
                   const void* const* scales, const float* inv,
                   void* const* y, const int* N, void* stream);
 
+/* Several activation vectors through one matrix: Y[m][n] = (GEMV of x_m)
+ * for m < M, x fp16 [M][K] (row-major), Y y_dtype [M][N], with the decode
+ * GEMV's arithmetic (exact (q - 8) x products summed per block in fp32,
+ * times the block scale, blocks accumulated in fp32, times inv for e4m3
+ * scales). This is the small-M (M ~ 8) batched GEMV that speculative
+ * decode verification needs and the reference lacks: its coopmat GEMM pads
+ * M to 64 and its GEMV reads the weights once per token (JOURNEY.md:666).
+ *   exact = 0: one launch for all M <= 16 vectors, the block sums from int4
+ *              x fp16 MFMAs; rows agree with q4_gemv to fp32 rounding.
+ *   exact = 1: each row bit-identical to q4_gemv of that x row when
+ *              q4_gemv runs unsplit (N >= 1920), so verification scores
+ *              exactly what token-by-token decode would. The x rows of one
+ *              launch are staged in LDS (144 KB): a launch takes 8 vectors
+ *              for K <= 8192, 4 for K <= 16384, 2 for K <= 32768 (larger K
+ *              is an error), and M is covered by as many launches as
+ *              needed, each reading the weights once. */
+#define Q4_GEMV_MAX_VECTORS 16
+int q4_gemv_multi(const void* x, int M, const uint32_t* wq,
+                  const void* scales, int scale_fmt, float inv, void* y,
+                  int y_dtype, int N, int K, int exact, void* stream);
+
 /* ---- prefill GEMMs -------------------------------------------------------
  * W4A16: Y f16 [M][N] = X f16 [M][K] @ f16((q-8)*s)^T, fp32 accumulate.
  * Replaces coopgemm_i4h.comp (vk/coopgemm_i4h.comp:13-35) as wired by

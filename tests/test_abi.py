@@ -75,6 +75,15 @@ def test_argument_errors_without_gpu(g4):
     Ns[1] = 0
     st = lib.q4_gemv_batch(C.c_void_p(1 << 20), 1, 256, 0, 1, 2, ptrs, ptrs, None, ptrs, Ns, null)
     assert st == g4._lib.Q4_ERR_ARG and "entry 1" in _err(g4)
+    # multi-vector GEMV: M outside 1..16, K beyond two vectors' staging, null pointers
+    p = C.c_void_p(1 << 20)
+    for M in (0, 17):
+        st = lib.q4_gemv_multi(p, M, p, p, 0, C.c_float(1.0), p, 1, 256, 256, 1, null)
+        assert st == g4._lib.Q4_ERR_ARG and f"M={M}" in _err(g4)
+    st = lib.q4_gemv_multi(p, 2, p, p, 0, C.c_float(1.0), p, 1, 256, 65536, 1, null)
+    assert st == g4._lib.Q4_ERR_ARG and "LDS" in _err(g4)
+    st = lib.q4_gemv_multi(p, 2, null, p, 0, C.c_float(1.0), p, 1, 256, 256, 0, null)
+    assert st == g4._lib.Q4_ERR_ARG and "null" in _err(g4)
 
 
 def test_sizes_and_split_queries(g4):
