@@ -41,6 +41,14 @@ SIGNATURES = {
     "q4_gemv_e4m3s": (_i, [_vp, _i, _vp, _vp, _f, _vp, _i, _i, _i, _i, _vp, _sz, _vp]),
     "q4_gemv_batch": (_i, [_vp, _i, _i, _i, _i, _i, _vp, _vp, _vp, _vp, _vp, _vp]),
     "q4_gemv_gated": (_i, [_vp, _i, _vp, _vp, _i, _f, _vp, _i, _i, _i, _i, _vp, _sz, _vp]),
+    "q4_pre_rmsnorm": (_i, [_vp, _vp, _vp, _i, _i, _i, _vp]),
+    "q4_pre_normadd": (_i, [_vp, _i, _vp, _vp, _i, _i, _f, _vp]),
+    "q4_pre_normadd_rmsnorm": (_i, [_vp, _i, _vp, _vp, _i, _i, _f, _vp, _vp, _i, _vp]),
+    "q4_pre_gelumul": (_i, [_vp, _vp, _i, _vp, _i, C.c_long, _vp]),
+    "q4_pre_prepkv": (_i, [_vp, _vp, _i, _i, _vp, _vp, _vp, _vp, _vp, _i, _i, _i, _i, _i, _vp, _vp]),
+    "q4_pre_attn_workspace_bytes": (_sz, [_i, _i, _i, _i]),
+    "q4_pre_attn": (_i, [_vp, _i, _i, _vp, _vp, _vp, _vp, _vp, _vp, _i, _i, _i, _i, _i, _i, _i, _i, _i, _vp, _vp,
+                         _sz, _vp]),
     "q4_gemv_multi": (_i, [_vp, _i, _vp, _vp, _i, _f, _vp, _i, _i, _i, _i, _vp]),
     "q4_interleave_rows": (_i, [_vp, _vp, _vp, _vp, _i, _i, _i, _vp, _vp, _vp]),
     "q4_gemm_w4a16": (_i, [_vp, _vp, _vp, _vp, _i, _i, _i, _vp]),

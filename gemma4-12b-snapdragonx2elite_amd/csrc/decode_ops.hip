@@ -33,6 +33,8 @@ constexpr int ATT_CH = 64;        // keys per attention split (16 per wave)
 constexpr int ATT_MAX_HD = 512;   // head dims up to 512 (global layers)
 constexpr float NORM_EPS = 1e-6f;
 
+__device__ inline float inv_rms(float sumsq, int D) { return 1.0f / sqrtf(sumsq / (float)D + NORM_EPS); }
+
 // Sum over the workgroup, identical in every thread. red: blockDim/64 floats.
 __device__ inline float block_sum(float v, float* red) {
 #pragma unroll
@@ -57,8 +59,6 @@ __device__ inline float block_max(float v, float* red) {
   return m;
 }
 
-__device__ inline float inv_rms(float sumsq, int D) { return 1.0f / sqrtf(sumsq / (float)D + NORM_EPS); }
-
 // Elements of a norm kernel: thread t holds elements t + NORM_THREADS r,
 // r < NORM_PER, in registers (every operand is loaded before the first
 // reduction, so the kernel makes one memory round trip, not one per
@@ -72,11 +72,14 @@ __device__ inline void store_y(void* y, int i, float v) {
 }
 
 // y = (x * inv) * w   (vk/rmsnorm.comp:8-12); y fp32 or fp16
+// Row blockIdx.x of [rows][D] x and y (one row for the decode token).
 template <int YT>
 __global__ void __launch_bounds__(NORM_THREADS) rmsnorm_kernel(const float* __restrict__ x, const float* __restrict__ w,
                                                                void* __restrict__ y, int D) {
   __shared__ float red[NORM_THREADS / 64];
   const int t = threadIdx.x;
+  x += (long)blockIdx.x * D;
+  y = reinterpret_cast<char*>(y) + (long)blockIdx.x * D * (YT == Q4_DT_F16 ? 2 : 4);
   float xv[NORM_PER], wv[NORM_PER];
 #pragma unroll
   for (int r = 0; r < NORM_PER; ++r) {
@@ -102,17 +105,27 @@ __global__ void __launch_bounds__(NORM_THREADS) rmsnorm_kernel(const float* __re
 // y = (h * inv2) * w2, the rmsnorm the reference records next on the new h
 // (src/vk_engine.py:242-243 and :248-249 followed by the next layer's :231
 // or the final norm :250), in the same workgroup: h never leaves registers.
-template <bool FUSE, int YT>
-__global__ void __launch_bounds__(NORM_THREADS) normadd_kernel(const float* __restrict__ x, const float* __restrict__ w,
+// Row blockIdx.x of [rows][D] x, h and y; x fp32 or fp16 (a prefill GEMM's
+// output, whose fp32 value the reference's up-cast gives exactly).
+template <int XT>
+__device__ inline float ld_act(const void* x, long i) {
+  if constexpr (XT == Q4_DT_F16) return h2f(reinterpret_cast<const uint16_t*>(x)[i]);
+  else return reinterpret_cast<const float*>(x)[i];
+}
+template <bool FUSE, int YT, int XT = Q4_DT_F32>
+__global__ void __launch_bounds__(NORM_THREADS) normadd_kernel(const void* __restrict__ xin, const float* __restrict__ w,
                                                                float* __restrict__ h, int D, float sc,
                                                                const float* __restrict__ w2, void* __restrict__ y) {
   __shared__ float red[NORM_THREADS / 64];
   const int t = threadIdx.x;
+  const void* x = reinterpret_cast<const char*>(xin) + (long)blockIdx.x * D * (XT == Q4_DT_F16 ? 2 : 4);
+  h += (long)blockIdx.x * D;
+  if constexpr (FUSE) y = reinterpret_cast<char*>(y) + (long)blockIdx.x * D * (YT == Q4_DT_F16 ? 2 : 4);
   float xv[NORM_PER], wv[NORM_PER], hv[NORM_PER], w2v[NORM_PER];
 #pragma unroll
   for (int r = 0; r < NORM_PER; ++r) {
     const int i = t + NORM_THREADS * r;
-    xv[r] = i < D ? x[i] : 0.0f;
+    xv[r] = i < D ? ld_act<XT>(x, i) : 0.0f;
     wv[r] = i < D ? w[i] : 0.0f;
     hv[r] = i < D ? h[i] : 0.0f;
     if constexpr (FUSE) w2v[r] = i < D ? w2[i] : 0.0f;
@@ -120,7 +133,10 @@ __global__ void __launch_bounds__(NORM_THREADS) normadd_kernel(const float* __re
   float s = 0.0f;
 #pragma unroll
   for (int r = 0; r < NORM_PER; ++r) s = fmaf(xv[r], xv[r], s);
-  for (int i = t + NORM_THREADS * NORM_PER; i < D; i += NORM_THREADS) s = fmaf(x[i], x[i], s);
+  for (int i = t + NORM_THREADS * NORM_PER; i < D; i += NORM_THREADS) {
+    const float v = ld_act<XT>(x, i);
+    s = fmaf(v, v, s);
+  }
   const float inv = inv_rms(block_sum(s, red), D);
   float s2 = 0.0f;
 #pragma unroll
@@ -131,7 +147,7 @@ __global__ void __launch_bounds__(NORM_THREADS) normadd_kernel(const float* __re
     s2 = fmaf(hv[r], hv[r], s2);  // padding elements are 0
   }
   for (int i = t + NORM_THREADS * NORM_PER; i < D; i += NORM_THREADS) {
-    const float v = __fmul_rn(__fadd_rn(h[i], __fmul_rn(__fmul_rn(x[i], inv), w[i])), sc);
+    const float v = __fmul_rn(__fadd_rn(h[i], __fmul_rn(__fmul_rn(ld_act<XT>(x, i), inv), w[i])), sc);
     h[i] = v;
     s2 = fmaf(v, v, s2);
   }
@@ -148,13 +164,14 @@ __global__ void __launch_bounds__(NORM_THREADS) normadd_kernel(const float* __re
   }
 }
 
-// out = gelu_tanh(gate) * up   (vk/gelumul.comp:7-8); out fp32 or fp16
-template <int YT>
-__global__ void __launch_bounds__(256) gelumul_kernel(const float* __restrict__ gate, const float* __restrict__ up,
-                                                      void* __restrict__ out, int n) {
-  const int i = blockIdx.x * 256 + threadIdx.x;
+// out = gelu_tanh(gate) * up   (vk/gelumul.comp:7-8); out fp32 or fp16,
+// gate/up fp32 or fp16 (prefill GEMM outputs)
+template <int YT, int GT = Q4_DT_F32>
+__global__ void __launch_bounds__(256) gelumul_kernel(const void* __restrict__ gate, const void* __restrict__ up,
+                                                      void* __restrict__ out, long n) {
+  const long i = (long)blockIdx.x * 256 + threadIdx.x;
   if (i >= n) return;
-  const float v = __fmul_rn(gelu_tanh(gate[i]), up[i]);
+  const float v = __fmul_rn(gelu_tanh(ld_act<GT>(gate, i)), ld_act<GT>(up, i));
   if constexpr (YT == Q4_DT_F16) reinterpret_cast<uint16_t*>(out)[i] = f2h(v);
   else reinterpret_cast<float*>(out)[i] = v;
 }
@@ -180,7 +197,6 @@ __device__ inline void norm_rope_head(float* v, float* o, const float* __restric
   }
 }
 
-__device__ inline int kv_slot(uint32_t pos, int window) { return window > 0 ? (int)(pos % (uint32_t)window) : (int)pos; }
 
 // K and V of KV head blockIdx.x into slot(pos)   (vk/prepkv.comp:16-30)
 __global__ void __launch_bounds__(ATT_THREADS) prepkv_kernel(const float* __restrict__ qkv, const float* __restrict__ knw,
@@ -203,10 +219,38 @@ __global__ void __launch_bounds__(ATT_THREADS) prepkv_kernel(const float* __rest
   for (int i = t; i < hd; i += ATT_THREADS) vc[o + i] = f2h(hv[i]);
 }
 
-__device__ inline int att_len(uint32_t pos, int window, int stride) {
-  const long T = window > 0 ? min((long)pos + 1, (long)window) : (long)pos + 1;
-  return (int)min(T, (long)stride);
+// Prefill: K and V of KV head blockIdx.x of token blockIdx.y (position
+// dyn[0] + token) into the token's slot, with the token's cos/sin row
+// (vk/pre_prepkv.comp:18-32). k, v: [M][ld] rows of fp32 or fp16 (the
+// prefill GEMM outputs; v == k for k == v layers). Tokens write in parallel:
+// when a chunk wraps a ring, two tokens share a slot and the later one must
+// win, so only the last token of each slot writes (the reference runs its
+// tokens in parallel too and leaves that race to the hardware).
+template <int KT>
+__global__ void __launch_bounds__(ATT_THREADS) pre_prepkv_kernel(const void* __restrict__ k, const void* __restrict__ v,
+                                                                 int ld, const float* __restrict__ knw,
+                                                                 const float* __restrict__ cosM,
+                                                                 const float* __restrict__ sinM, uint16_t* __restrict__ kc,
+                                                                 uint16_t* __restrict__ vc, int hd, int stride,
+                                                                 int window, int M, const uint32_t* __restrict__ dyn) {
+  __shared__ float hv[ATT_MAX_HD], ro[ATT_MAX_HD], red[ATT_THREADS / 64];
+  const int kvh = blockIdx.x, m = blockIdx.y, t = threadIdx.x;
+  if (window > 0 && m + window < M) return;  // a later token of the chunk takes this slot
+  const uint32_t pos = dyn[0] + (uint32_t)m;
+  const int slot = kv_slot(pos, window);
+  if (slot >= stride) return;  // position past a global layer's cache: nothing to write
+  const long o = ((long)kvh * stride + slot) * hd;
+  const long r = (long)m * ld + (long)kvh * hd;
+  for (int i = t; i < hd; i += ATT_THREADS) hv[i] = ld_act<KT>(k, r + i);
+  __syncthreads();
+  norm_rope_head(hv, ro, knw, cosM + (long)m * hd, sinM + (long)m * hd, hd, red);
+  for (int i = t; i < hd; i += ATT_THREADS) kc[o + i] = f2h(ro[i]);
+  for (int i = t; i < hd; i += ATT_THREADS) hv[i] = ld_act<KT>(v, r + i);
+  __syncthreads();
+  norm_rope_head(hv, ro, nullptr, nullptr, nullptr, hd, red);
+  for (int i = t; i < hd; i += ATT_THREADS) vc[o + i] = f2h(hv[i]);
 }
+
 
 // Loads of E halves (E = 1, 2, 4, 8) as one 2/4/8/16-byte access.
 template <int E>
@@ -405,6 +449,15 @@ __global__ void __launch_bounds__(ATT_THREADS) attn_merge_kernel(const float* __
 
 static int attn_splits(int stride) { return ceil_div(stride, ATT_CH); }
 
+template <bool FUSE, int YT>
+static void pre_normadd_launch(const void* x, int x_dtype, const float* w, float* h, int D, int M, float sc,
+                               const float* w2, void* y, hipStream_t st) {
+  if (x_dtype == Q4_DT_F16)
+    hipLaunchKernelGGL((normadd_kernel<FUSE, YT, Q4_DT_F16>), dim3(M), dim3(NORM_THREADS), 0, st, x, w, h, D, sc, w2, y);
+  else
+    hipLaunchKernelGGL((normadd_kernel<FUSE, YT, Q4_DT_F32>), dim3(M), dim3(NORM_THREADS), 0, st, x, w, h, D, sc, w2, y);
+}
+
 }  // namespace q4
 
 using namespace q4;
@@ -540,6 +593,87 @@ int q4_prepkv_attn(const float* qkv, const float* knw, const float* qnw, const f
   Q4_ARG(knw, "null pointer");
   return attn_launch(qkv, qnw, cosb, sinb, kc, vc, out, out_dtype, nH, nkv, hd, stride, window, qoff, grp, dyn, ws,
                      ws_bytes, stream, knw, koff, keqv ? koff : voff);
+}
+
+// ---- batched prefill (one chunk of M tokens) --------------------------------
+
+int q4_pre_rmsnorm(const float* x, const float* w, void* y, int y_dtype, int D, int M, void* stream) {
+  clear_error();
+  Q4_ARG(x && w && y, "null pointer");
+  Q4_ARG(D > 0 && M > 0, "bad sizes D=%d M=%d", D, M);
+  Q4_ARG(y_dtype == Q4_DT_F32 || y_dtype == Q4_DT_F16, "bad y_dtype");
+  if (y_dtype == Q4_DT_F16)
+    hipLaunchKernelGGL(rmsnorm_kernel<Q4_DT_F16>, dim3(M), dim3(NORM_THREADS), 0, as_stream(stream), x, w, y, D);
+  else
+    hipLaunchKernelGGL(rmsnorm_kernel<Q4_DT_F32>, dim3(M), dim3(NORM_THREADS), 0, as_stream(stream), x, w, y, D);
+  Q4_LAUNCHED("pre_rmsnorm");
+  return Q4_OK;
+}
+
+int q4_pre_normadd(const void* x, int x_dtype, const float* w, float* h, int D, int M, float scale, void* stream) {
+  clear_error();
+  Q4_ARG(x && w && h, "null pointer");
+  Q4_ARG(D > 0 && M > 0, "bad sizes D=%d M=%d", D, M);
+  Q4_ARG(x_dtype == Q4_DT_F32 || x_dtype == Q4_DT_F16, "bad x_dtype");
+  pre_normadd_launch<false, Q4_DT_F32>(x, x_dtype, w, h, D, M, scale == 0.0f ? 1.0f : scale, nullptr, nullptr,
+                                       as_stream(stream));
+  Q4_LAUNCHED("pre_normadd");
+  return Q4_OK;
+}
+
+int q4_pre_normadd_rmsnorm(const void* x, int x_dtype, const float* w, float* h, int D, int M, float scale,
+                           const float* w2, void* y, int y_dtype, void* stream) {
+  clear_error();
+  Q4_ARG(x && w && h && w2 && y, "null pointer");
+  Q4_ARG(D > 0 && M > 0, "bad sizes D=%d M=%d", D, M);
+  Q4_ARG(x_dtype == Q4_DT_F32 || x_dtype == Q4_DT_F16, "bad x_dtype");
+  Q4_ARG(y_dtype == Q4_DT_F32 || y_dtype == Q4_DT_F16, "bad y_dtype");
+  const float sc = scale == 0.0f ? 1.0f : scale;
+  if (y_dtype == Q4_DT_F16)
+    pre_normadd_launch<true, Q4_DT_F16>(x, x_dtype, w, h, D, M, sc, w2, y, as_stream(stream));
+  else
+    pre_normadd_launch<true, Q4_DT_F32>(x, x_dtype, w, h, D, M, sc, w2, y, as_stream(stream));
+  Q4_LAUNCHED("pre_normadd_rmsnorm");
+  return Q4_OK;
+}
+
+int q4_pre_gelumul(const void* gate, const void* up, int in_dtype, void* out, int out_dtype, long n, void* stream) {
+  clear_error();
+  Q4_ARG(gate && up && out, "null pointer");
+  Q4_ARG(n > 0 && n <= (1L << 40), "bad n=%ld", n);
+  Q4_ARG(in_dtype == Q4_DT_F32 || in_dtype == Q4_DT_F16, "bad in_dtype");
+  Q4_ARG(out_dtype == Q4_DT_F32 || out_dtype == Q4_DT_F16, "bad out_dtype");
+  const dim3 grid((unsigned)((n + 255) / 256));
+  hipStream_t st = as_stream(stream);
+  if (in_dtype == Q4_DT_F16) {
+    if (out_dtype == Q4_DT_F16) hipLaunchKernelGGL((gelumul_kernel<Q4_DT_F16, Q4_DT_F16>), grid, dim3(256), 0, st, gate, up, out, n);
+    else hipLaunchKernelGGL((gelumul_kernel<Q4_DT_F32, Q4_DT_F16>), grid, dim3(256), 0, st, gate, up, out, n);
+  } else {
+    if (out_dtype == Q4_DT_F16) hipLaunchKernelGGL((gelumul_kernel<Q4_DT_F16, Q4_DT_F32>), grid, dim3(256), 0, st, gate, up, out, n);
+    else hipLaunchKernelGGL((gelumul_kernel<Q4_DT_F32, Q4_DT_F32>), grid, dim3(256), 0, st, gate, up, out, n);
+  }
+  Q4_LAUNCHED("pre_gelumul");
+  return Q4_OK;
+}
+
+int q4_pre_prepkv(const void* k, const void* v, int kv_dtype, int ld, const float* knw, const float* cosM,
+                  const float* sinM, uint16_t* kc, uint16_t* vc, int nkv, int hd, int stride, int window, int M,
+                  const uint32_t* dyn, void* stream) {
+  clear_error();
+  Q4_ARG(k && v && knw && cosM && sinM && kc && vc && dyn, "null pointer");
+  Q4_ARG(kv_dtype == Q4_DT_F32 || kv_dtype == Q4_DT_F16, "bad kv_dtype");
+  Q4_ARG(nkv > 0 && M > 0 && stride > 0 && window >= 0, "bad sizes");
+  Q4_ARG(hd > 0 && hd % 2 == 0 && hd <= ATT_MAX_HD, "head dim must be even and <= %d (got %d)", ATT_MAX_HD, hd);
+  Q4_ARG(ld >= nkv * hd, "row stride %d is shorter than nkv * hd = %d", ld, nkv * hd);
+  Q4_ARG(window <= stride, "window %d exceeds the cache depth %d", window, stride);
+  if (kv_dtype == Q4_DT_F16)
+    hipLaunchKernelGGL(pre_prepkv_kernel<Q4_DT_F16>, dim3(nkv, M), dim3(ATT_THREADS), 0, as_stream(stream), k, v, ld,
+                       knw, cosM, sinM, kc, vc, hd, stride, window, M, dyn);
+  else
+    hipLaunchKernelGGL(pre_prepkv_kernel<Q4_DT_F32>, dim3(nkv, M), dim3(ATT_THREADS), 0, as_stream(stream), k, v, ld,
+                       knw, cosM, sinM, kc, vc, hd, stride, window, M, dyn);
+  Q4_LAUNCHED("pre_prepkv");
+  return Q4_OK;
 }
 
 }  // extern "C"

@@ -1,0 +1,345 @@
+// Batched-prefill attention for gfx950: every token of a chunk of M tokens
+// (positions p0 .. p0+M-1, p0 read from device memory) attends the fp16 KV
+// cache causally, after the chunk's own K/V were written.
+//
+// Replaces vk/pre_attn.comp (recorded per layer at src/vk_engine.py:417),
+// which runs one workgroup per (head, token) and walks the keys one scalar
+// dot product at a time; here the query rows of a KV head are tiled onto
+// MFMAs:
+//  * A workgroup (4 waves) owns 64 query rows of one KV head (row = token *
+//    grp + query head within the group, so the rows share their K and V)
+//    and one split of 128 cache slots; the grid covers the cache capacity
+//    the caller asks for and splits past a workgroup's last token exit at
+//    once, so the launch shape does not depend on p0 (graph replay).
+//  * q prologue, in registers: lane (c, g) of wave w holds row 16w + c,
+//    elements 32j + 8g .. 32j + 8g + 7 of every 32-element chunk j; the
+//    RoPE partner of element e (e +- hd/2) is in the same lane, and the
+//    row's sum of squares needs two xor-shuffles. q is split into fp16
+//    hi + lo parts (q = hi + lo to ~22 bits), so q . k is exact to fp32
+//    rounding with fp16 MFMAs (two per k-step; k is fp16 in the cache).
+//  * Per 32-key tile the workgroup stages K row-major ([key][hd], rows
+//    padded by 16 bytes) and V transposed ([hd][key], pairs of keys per
+//    32-bit word) in LDS from registers. Scores S^T = K q^T: one
+//    v_mfma_f32_16x16x32_f16 pair per 16 keys x 16 rows x 32 elements; lane
+//    (c, g) gets keys 4g .. 4g+3 of row c. Masked keys (past the row's
+//    length, or in a ring slot a later token of the chunk now holds) are
+//    -inf. Online softmax per row over the tile (xor-shuffles across the 4
+//    lanes of a row), then O^T += V^T P^T with v_mfma_f32_16x16x16_f16: the
+//    B operand is exactly the score layout (P rounded to fp16), the A
+//    operand one 8-byte LDS read of the transposed V.
+//  * Each workgroup writes its rows' (max, sum, unnormalised accumulator)
+//    for its split; q4_pre_attn's second kernel merges the splits.
+#include "q4mi_common.h"
+
+namespace q4 {
+
+constexpr int PA_WAVES = 4;
+constexpr int PA_THREADS = 64 * PA_WAVES;
+constexpr int PA_ROWS = 16 * PA_WAVES;  // query rows per workgroup
+constexpr int PA_KT = 32;               // keys per LDS tile
+constexpr int PA_KS = 128;              // keys per split
+constexpr float PA_EPS = 1e-6f;
+
+typedef _Float16 v4h __attribute__((ext_vector_type(4)));
+
+template <int QT>
+__device__ inline float ld_q(const void* q, long i) {
+  if constexpr (QT == Q4_DT_F16) return h2f(reinterpret_cast<const uint16_t*>(q)[i]);
+  else return reinterpret_cast<const float*>(q)[i];
+}
+
+// Position of the key ring slot s holds once positions up to `last` are
+// written (vk/pre_attn.comp:40); for slots never written it is negative.
+__device__ inline long ring_position(int s, uint32_t last, int window) {
+  return (long)last - (long)(((long)last + window - s) % window);
+}
+
+// Workspace row of (token m, head h), split ks: [max, sum, -, -, acc[HD]].
+__device__ inline long pa_ws_index(int m, int h, int nH, int ks, int nsplit, int hd) {
+  return (((long)m * nH + h) * nsplit + ks) * (hd + 4);
+}
+
+template <int HD, int QT>
+__global__ void __launch_bounds__(PA_THREADS)
+pre_attn_kernel(const void* __restrict__ qin, int ldq, const float* __restrict__ qnw, const float* __restrict__ cosM,
+                const float* __restrict__ sinM, const uint16_t* __restrict__ kc, const uint16_t* __restrict__ vc,
+                int stride, int window, int grp, int nH, int M, const uint32_t* __restrict__ dyn,
+                float* __restrict__ ws, int nsplit) {
+  constexpr int NCH = HD / 32;        // 32-element chunks (QK k-steps)
+  constexpr int NDT = HD / 16;        // 16-element output tiles
+  constexpr int CPR = HD / 8;         // 16-byte chunks per K/V row
+  constexpr int KP = HD * 2 + 16;     // K tile row pitch (bytes)
+  constexpr int VP = PA_KT * 2 + 8;   // V^T tile row pitch (bytes)
+  constexpr int KITEMS = PA_KT * CPR, VITEMS = (PA_KT / 2) * CPR;  // 16-byte K chunks, V key-pair chunks per tile
+  constexpr int KLD = (KITEMS + PA_THREADS - 1) / PA_THREADS, VLD = (VITEMS + PA_THREADS - 1) / PA_THREADS;
+  static_assert(NCH % 2 == 0, "head dim");
+  __shared__ __attribute__((aligned(16))) uint8_t ksh[PA_KT * KP];
+  __shared__ __attribute__((aligned(16))) uint8_t vsh[HD * VP];
+
+  const int kvh = blockIdx.x, ks = blockIdx.z;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, c = lane & 15, g = lane >> 4;
+  const uint32_t p0 = dyn[0];
+  const int nrows = M * grp, r0 = blockIdx.y * PA_ROWS;
+  const int mlast = (min(r0 + PA_ROWS, nrows) - 1) / grp;
+  const int Tlast = att_len(p0 + (uint32_t)mlast, window, stride);
+  const int k0 = ks * PA_KS;
+  if (k0 >= Tlast) return;  // no row of this workgroup has keys in this split (uniform)
+  const int kend = min(k0 + PA_KS, Tlast);
+  const uint32_t last = p0 + (uint32_t)M - 1;  // the chunk's last position (all of its K/V are written)
+
+  // ---- this lane's query row: q-norm, RoPE, hi/lo split ----
+  const int R = r0 + 16 * wave + c;
+  const bool live = R < nrows;
+  const int m = live ? R / grp : 0;
+  const int h = kvh * grp + (live ? R % grp : 0);
+  const uint32_t pos = p0 + (uint32_t)m;
+  const int T = att_len(pos, window, stride);
+  v8h qh[NCH], ql[NCH];
+  {
+    float qf[NCH][8];
+    const long qb = (long)m * ldq + (long)h * HD;
+    float ss = 0.0f;
+#pragma unroll
+    for (int j = 0; j < NCH; ++j)
+#pragma unroll
+      for (int u = 0; u < 8; ++u) {
+        qf[j][u] = ld_q<QT>(qin, qb + 32 * j + 8 * g + u);
+        ss = fmaf(qf[j][u], qf[j][u], ss);
+      }
+    ss += __shfl_xor(ss, 16, 64);
+    ss += __shfl_xor(ss, 32, 64);
+    const float inv = 1.0f / sqrtf(ss / (float)HD + PA_EPS);
+#pragma unroll
+    for (int j = 0; j < NCH; ++j)
+#pragma unroll
+      for (int u = 0; u < 8; ++u) qf[j][u] = __fmul_rn(__fmul_rn(qf[j][u], inv), qnw[32 * j + 8 * g + u]);
+    const float* cs = cosM + (long)m * HD;
+    const float* sn = sinM + (long)m * HD;
+#pragma unroll
+    for (int j = 0; j < NCH / 2; ++j)
+#pragma unroll
+      for (int u = 0; u < 8; ++u) {
+        const int e = 32 * j + 8 * g + u, e2 = e + HD / 2;
+        const float a = qf[j][u], b = qf[j + NCH / 2][u];
+        const float ra = __fadd_rn(__fmul_rn(a, cs[e]), __fmul_rn(-b, sn[e]));
+        const float rb = __fadd_rn(__fmul_rn(b, cs[e2]), __fmul_rn(a, sn[e2]));
+        qf[j][u] = ra;
+        qf[j + NCH / 2][u] = rb;
+      }
+#pragma unroll
+    for (int j = 0; j < NCH; ++j)
+#pragma unroll
+      for (int u = 0; u < 8; ++u) {
+        const _Float16 hi = (_Float16)qf[j][u];
+        qh[j][u] = hi;
+        ql[j][u] = (_Float16)(qf[j][u] - (float)hi);
+      }
+  }
+
+  v4f oacc[NDT];
+#pragma unroll
+  for (int d = 0; d < NDT; ++d) oacc[d] = v4f{0.0f, 0.0f, 0.0f, 0.0f};
+  float mrun = -INFINITY, lrun = 0.0f;
+
+  for (int t0 = k0; t0 < kend; t0 += PA_KT) {
+    // ---- stage the tile's K (row-major) and V (transposed, key pairs) ----
+    v4u kr[KLD], va[VLD], vb[VLD];
+#pragma unroll
+    for (int i = 0; i < KLD; ++i) {
+      const int q = min(tid + PA_THREADS * i, KITEMS - 1), key = q / CPR, ch = q % CPR;
+      const int slot = min(t0 + key, stride - 1);
+      kr[i] = *reinterpret_cast<const v4u*>(kc + ((long)kvh * stride + slot) * HD + ch * 8);
+    }
+#pragma unroll
+    for (int i = 0; i < VLD; ++i) {
+      const int q = min(tid + PA_THREADS * i, VITEMS - 1), pr = q / CPR, ch = q % CPR;
+      const int s0 = min(t0 + 2 * pr, stride - 1), s1 = min(t0 + 2 * pr + 1, stride - 1);
+      va[i] = *reinterpret_cast<const v4u*>(vc + ((long)kvh * stride + s0) * HD + ch * 8);
+      vb[i] = *reinterpret_cast<const v4u*>(vc + ((long)kvh * stride + s1) * HD + ch * 8);
+    }
+    __syncthreads();  // every wave is done with the previous tile
+#pragma unroll
+    for (int i = 0; i < KLD; ++i) {
+      const int q = tid + PA_THREADS * i, key = q / CPR, ch = q % CPR;
+      if (q < KITEMS) *reinterpret_cast<v4u*>(ksh + key * KP + ch * 16) = kr[i];
+    }
+#pragma unroll
+    for (int i = 0; i < VLD; ++i) {
+      const int q = tid + PA_THREADS * i, pr = q / CPR, ch = q % CPR;
+      if (q >= VITEMS) continue;
+#pragma unroll
+      for (int w = 0; w < 4; ++w) {
+        // elements 8 ch + 2w, 8 ch + 2w + 1 of keys 2 pr (low half) and 2 pr + 1 (high half)
+        const uint32_t a = va[i][w], b = vb[i][w];
+        *reinterpret_cast<uint32_t*>(vsh + (8 * ch + 2 * w) * VP + 4 * pr) = (a & 0xFFFFu) | (b << 16);
+        *reinterpret_cast<uint32_t*>(vsh + (8 * ch + 2 * w + 1) * VP + 4 * pr) = (a >> 16) | (b & 0xFFFF0000u);
+      }
+    }
+    __syncthreads();
+
+    // ---- scores of the tile's 32 keys for this lane's row ----
+    float sc[2][4];
+#pragma unroll
+    for (int st = 0; st < 2; ++st) {
+      v4f s = v4f{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+      for (int j = 0; j < NCH; ++j) {
+        const v8h a = *reinterpret_cast<const v8h*>(ksh + (16 * st + c) * KP + (4 * j + g) * 16);
+        s = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, qh[j], s, 0, 0, 0);
+        s = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, ql[j], s, 0, 0, 0);
+      }
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const int slot = t0 + 16 * st + 4 * g + e;
+        const bool ok = slot < kend && slot < T && (window == 0 || ring_position(slot, last, window) <= (long)pos);
+        sc[st][e] = ok ? s[e] : -INFINITY;
+      }
+    }
+    // ---- online softmax over the tile ----
+    float tmax = -INFINITY;
+#pragma unroll
+    for (int st = 0; st < 2; ++st)
+#pragma unroll
+      for (int e = 0; e < 4; ++e) tmax = fmaxf(tmax, sc[st][e]);
+    tmax = fmaxf(tmax, __shfl_xor(tmax, 16, 64));
+    tmax = fmaxf(tmax, __shfl_xor(tmax, 32, 64));
+    const float mnew = fmaxf(mrun, tmax);
+    const bool any = mnew != -INFINITY;
+    const float corr = any ? expf(mrun - mnew) : 1.0f;
+    float psum = 0.0f;
+    v4h pb[2];
+#pragma unroll
+    for (int st = 0; st < 2; ++st)
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        // the weights the V product uses are the fp16-rounded ones: the sum
+        // is taken over the same values, so the output stays a weighted mean
+        // of V rows (the row maximum's weight, 1, is exact)
+        const _Float16 p = (_Float16)(any ? expf(sc[st][e] - mnew) : 0.0f);
+        psum += (float)p;
+        pb[st][e] = p;
+      }
+    psum += __shfl_xor(psum, 16, 64);
+    psum += __shfl_xor(psum, 32, 64);
+    lrun = fmaf(lrun, corr, psum);
+    mrun = mnew;
+#pragma unroll
+    for (int d = 0; d < NDT; ++d)
+#pragma unroll
+      for (int e = 0; e < 4; ++e) oacc[d][e] *= corr;
+    // ---- O^T += V^T P^T ----
+#pragma unroll
+    for (int st = 0; st < 2; ++st)
+#pragma unroll
+      for (int d = 0; d < NDT; ++d) {
+        const v4h a = *reinterpret_cast<const v4h*>(vsh + (16 * d + c) * VP + (16 * st + 4 * g) * 2);
+        oacc[d] = __builtin_amdgcn_mfma_f32_16x16x16f16(a, pb[st], oacc[d], 0, 0, 0);
+      }
+  }
+
+  // ---- this split's partial for the row ----
+  if (!live) return;
+  float* o = ws + pa_ws_index(m, h, nH, ks, nsplit, HD);
+  if (g == 0) {
+    o[0] = mrun;
+    o[1] = lrun;
+  }
+#pragma unroll
+  for (int d = 0; d < NDT; ++d) *reinterpret_cast<v4f*>(o + 4 + 16 * d + 4 * g) = oacc[d];
+}
+
+// out[m][h hd + i] = sum_c acc_c w_c / sum_c l_c w_c over the splits that
+// hold keys of token m, w_c = exp(max_c - max); fp32 or fp16 out.
+template <int OT>
+__global__ void __launch_bounds__(256)
+pre_attn_merge_kernel(const float* __restrict__ ws, void* __restrict__ out, int ldo, int hd, int nH, int nsplit,
+                      int stride, int window, const uint32_t* __restrict__ dyn) {
+  const int row = blockIdx.x, m = row / nH, h = row % nH, t = threadIdx.x;
+  const int T = att_len(dyn[0] + (uint32_t)m, window, stride);
+  const int ns = min((T + PA_KS - 1) / PA_KS, nsplit);
+  const float* w = ws + (long)row * nsplit * (hd + 4);
+  float mx = -INFINITY;
+  for (int cc = 0; cc < ns; ++cc) mx = fmaxf(mx, w[(long)cc * (hd + 4)]);
+  float L = 0.0f;
+  for (int cc = 0; cc < ns; ++cc) {
+    const float mc = w[(long)cc * (hd + 4)];
+    if (mc != -INFINITY) L = fmaf(w[(long)cc * (hd + 4) + 1], expf(mc - mx), L);
+  }
+  for (int i = t; i < hd; i += 256) {
+    float a = 0.0f;
+    for (int cc = 0; cc < ns; ++cc) {
+      const float mc = w[(long)cc * (hd + 4)];
+      if (mc != -INFINITY) a = fmaf(w[(long)cc * (hd + 4) + 4 + i], expf(mc - mx), a);
+    }
+    const float v = a / L;
+    const long oi = (long)m * ldo + (long)h * hd + i;
+    if constexpr (OT == Q4_DT_F16) reinterpret_cast<uint16_t*>(out)[oi] = f2h(v);
+    else reinterpret_cast<float*>(out)[oi] = v;
+  }
+}
+
+static int pa_splits(int max_keys) { return (max_keys + PA_KS - 1) / PA_KS; }
+
+}  // namespace q4
+
+using namespace q4;
+
+extern "C" {
+
+size_t q4_pre_attn_workspace_bytes(int M, int nH, int hd, int max_keys) {
+  if (M <= 0 || nH <= 0 || hd <= 0 || max_keys <= 0) return 0;
+  return (size_t)M * nH * pa_splits(max_keys) * (hd + 4) * sizeof(float);
+}
+
+int q4_pre_attn(const void* q, int q_dtype, int ldq, const float* qnw, const float* cosM, const float* sinM,
+                const uint16_t* kc, const uint16_t* vc, void* out, int out_dtype, int ldo, int nH, int nkv, int hd,
+                int stride, int window, int M, int max_keys, const uint32_t* dyn, void* ws, size_t ws_bytes,
+                void* stream) {
+  clear_error();
+  Q4_ARG(q && qnw && cosM && sinM && kc && vc && out && dyn && ws, "null pointer");
+  Q4_ARG(((uintptr_t)kc & 15) == 0 && ((uintptr_t)vc & 15) == 0 && ((uintptr_t)ws & 15) == 0,
+         "kc, vc and ws must be 16-byte aligned");
+  Q4_ARG(q_dtype == Q4_DT_F32 || q_dtype == Q4_DT_F16, "bad q_dtype");
+  Q4_ARG(out_dtype == Q4_DT_F32 || out_dtype == Q4_DT_F16, "bad out_dtype");
+  Q4_ARG(hd == 64 || hd == 128 || hd == 256 || hd == 512, "prefill attention takes head dims 64/128/256/512 (got %d)",
+         hd);
+  Q4_ARG(nH > 0 && nkv > 0 && nH % nkv == 0, "nH=%d must be a multiple of nkv=%d", nH, nkv);
+  Q4_ARG(M > 0 && stride > 0 && window >= 0 && window <= stride, "bad sizes M=%d stride=%d window=%d", M, stride,
+         window);
+  Q4_ARG(window == 0 || M <= window, "a chunk of %d tokens is longer than the %d-slot ring", M, window);
+  Q4_ARG(ldq >= nH * hd && ldo >= nH * hd, "row strides ldq=%d ldo=%d are shorter than nH * hd = %d", ldq, ldo,
+         nH * hd);
+  Q4_ARG(max_keys > 0 && max_keys <= stride, "max_keys=%d must be in 1..stride=%d", max_keys, stride);
+  Q4_ARG(window == 0 || max_keys >= window, "a ring layer needs max_keys >= window (%d)", window);
+  const size_t need = q4_pre_attn_workspace_bytes(M, nH, hd, max_keys);
+  Q4_ARG(ws_bytes >= need, "prefill attention needs a %zu-byte workspace (got %zu)", need, ws_bytes);
+  const int grp = nH / nkv, ns = pa_splits(max_keys);
+  const dim3 grid(nkv, ceil_div(M * grp, PA_ROWS), ns);
+  hipStream_t st = as_stream(stream);
+  float* w = reinterpret_cast<float*>(ws);
+#define PA_LAUNCH(HD_)                                                                                            \
+  if (q_dtype == Q4_DT_F16)                                                                                       \
+    hipLaunchKernelGGL((pre_attn_kernel<HD_, Q4_DT_F16>), grid, dim3(PA_THREADS), 0, st, q, ldq, qnw, cosM, sinM, \
+                       kc, vc, stride, window, grp, nH, M, dyn, w, ns);                                          \
+  else                                                                                                            \
+    hipLaunchKernelGGL((pre_attn_kernel<HD_, Q4_DT_F32>), grid, dim3(PA_THREADS), 0, st, q, ldq, qnw, cosM, sinM, \
+                       kc, vc, stride, window, grp, nH, M, dyn, w, ns);
+  switch (hd) {
+    case 64: PA_LAUNCH(64) break;
+    case 128: PA_LAUNCH(128) break;
+    case 256: PA_LAUNCH(256) break;
+    default: PA_LAUNCH(512) break;
+  }
+#undef PA_LAUNCH
+  Q4_LAUNCHED("pre_attn");
+  if (out_dtype == Q4_DT_F16)
+    hipLaunchKernelGGL(pre_attn_merge_kernel<Q4_DT_F16>, dim3(M * nH), dim3(256), 0, st, w, out, ldo, hd, nH, ns,
+                       stride, window, dyn);
+  else
+    hipLaunchKernelGGL(pre_attn_merge_kernel<Q4_DT_F32>, dim3(M * nH), dim3(256), 0, st, w, out, ldo, hd, nH, ns,
+                       stride, window, dyn);
+  Q4_LAUNCHED("pre_attn_merge");
+  return Q4_OK;
+}
+
+}  // extern "C"

@@ -207,6 +207,15 @@ __device__ inline float gelu_tanh(float x) {
   return __fmul_rn(__fmul_rn(0.5f, x), __fadd_rn(1.0f, tanhf(inner)));
 }
 
+// KV-cache slot of position pos: a ring of `window` slots for sliding
+// layers, the position itself for global ones (window 0).
+__device__ inline int kv_slot(uint32_t pos, int window) { return window > 0 ? (int)(pos % (uint32_t)window) : (int)pos; }
+// Keys the token at pos attends: pos + 1, at most the ring, at most the cache.
+__device__ inline int att_len(uint32_t pos, int window, int stride) {
+  const long T = window > 0 ? min((long)pos + 1, (long)window) : (long)pos + 1;
+  return (int)min(T, (long)stride);
+}
+
 template <int B, int E, class F>
 __device__ __forceinline__ void static_for(F&& f) {
   if constexpr (B < E) {

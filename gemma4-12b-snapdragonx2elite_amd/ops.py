@@ -580,6 +580,97 @@ class Graph:
             pass
 
 
+# ---- batched prefill (one chunk of M tokens, positions dyn[0] .. dyn[0]+M-1) ----
+
+def _rows(t, M: int, D: int, what: str, dtypes=(torch.float32,)):
+    if t.dtype not in dtypes:
+        raise ValueError(f"{what} must be {' or '.join(str(d) for d in dtypes)}")
+    _need(t, M * D * t.element_size(), what)
+
+
+def pre_rmsnorm(x, w, y=None, *, M: int, D: int, y_dtype=torch.float32):
+    """rmsnorm of each of the M rows of x [M][D] (fp32)."""
+    _rows(x, M, D, "x")
+    _f32(w, D, "w")
+    y = torch.empty(M, D, dtype=y_dtype, device=x.device) if y is None else y
+    _rows(y, M, D, "y", (torch.float32, torch.float16))
+    call("q4_pre_rmsnorm", _p(x), _p(w), _p(y), _dt(y), D, M, _stream())
+    return y
+
+
+def pre_normadd(x, w, h, *, M: int, D: int, scale: float = 0.0, w2=None, y=None, y_dtype=torch.float32):
+    """h[m] = (h[m] + rmsnorm(x[m]) * w) * scale per row (x fp32 or fp16);
+    with ``w2``, also y = rmsnorm(h) * w2 in the same launch (returns y)."""
+    _rows(x, M, D, "x", (torch.float32, torch.float16))
+    _f32(w, D, "w")
+    _rows(h, M, D, "h")
+    if w2 is None:
+        call("q4_pre_normadd", _p(x), _dt(x), _p(w), _p(h), D, M, C.c_float(scale), _stream())
+        return h
+    _f32(w2, D, "w2")
+    y = torch.empty(M, D, dtype=y_dtype, device=x.device) if y is None else y
+    _rows(y, M, D, "y", (torch.float32, torch.float16))
+    call("q4_pre_normadd_rmsnorm", _p(x), _dt(x), _p(w), _p(h), D, M, C.c_float(scale), _p(w2), _p(y), _dt(y),
+         _stream())
+    return y
+
+
+def pre_gelumul(gate, up, out=None, out_dtype=torch.float32):
+    """out = gelu_tanh(gate) * up elementwise (gate/up fp32 or fp16, same dtype)."""
+    n = gate.numel()
+    if up.dtype != gate.dtype or up.numel() < n:
+        raise ValueError("gate and up must share dtype and size")
+    _rows(gate, 1, n, "gate", (torch.float32, torch.float16))
+    out = torch.empty(n, dtype=out_dtype, device=gate.device) if out is None else out
+    _need(out, n * out.element_size(), "out")
+    call("q4_pre_gelumul", _p(gate), _p(up), _dt(gate), _p(out), _dt(out), C.c_long(n), _stream())
+    return out
+
+
+def pre_prepkv(k, v, knw, cosM, sinM, kc, vc, *, M: int, ld: int, nkv: int, hd: int, stride: int, window: int,
+               dyn: torch.Tensor) -> None:
+    """K (normed, roped with each token's cos/sin row) and V (normed) of the
+    M tokens into the fp16 caches; k, v [M][ld] fp32 or fp16 (v may be k)."""
+    v = k if v is None else v
+    if v.dtype != k.dtype:
+        raise ValueError("k and v must share a dtype")
+    _rows(k, M, ld, "k", (torch.float32, torch.float16))
+    _rows(v, M, ld, "v", (torch.float32, torch.float16))
+    _f32(knw, hd, "knw")
+    _f32(cosM, M * hd, "cosM")
+    _f32(sinM, M * hd, "sinM")
+    _kv_checks(kc, vc, nkv, stride, hd, dyn)
+    call("q4_pre_prepkv", _p(k), _p(v), _dt(k), ld, _p(knw), _p(cosM), _p(sinM), _p(kc), _p(vc), nkv, hd, stride,
+         window, M, _p(dyn), _stream())
+
+
+def pre_attn_workspace(M: int, nH: int, hd: int, max_keys: int, device="cuda") -> torch.Tensor:
+    """Scratch of :func:`pre_attn` for this shape (no initialisation needed)."""
+    n = int(lib().q4_pre_attn_workspace_bytes(M, nH, hd, max_keys))
+    return torch.empty(max(n, 16) // 4, dtype=torch.float32, device=device)
+
+
+def pre_attn(q, qnw, cosM, sinM, kc, vc, out=None, *, M: int, ldq: int, nH: int, nkv: int, hd: int, stride: int,
+             window: int, max_keys: int, dyn: torch.Tensor, ws: torch.Tensor | None = None,
+             out_dtype=torch.float32) -> torch.Tensor:
+    """Causal attention of the chunk's M tokens over the cache (after the
+    chunk's K/V were written); q [M][ldq] fp32 or fp16; out [M][nH * hd]."""
+    _rows(q, M, ldq, "q", (torch.float32, torch.float16))
+    _f32(qnw, hd, "qnw")
+    _f32(cosM, M * hd, "cosM")
+    _f32(sinM, M * hd, "sinM")
+    _kv_checks(kc, vc, nkv, stride, hd, dyn)
+    out = torch.empty(M, nH * hd, dtype=out_dtype, device=q.device) if out is None else out
+    _rows(out, M, nH * hd, "out", (torch.float32, torch.float16))
+    if ws is None:
+        if _CAPTURING[0]:
+            raise RuntimeError("prefill attention inside a graph capture needs a workspace allocated before it")
+        ws = pre_attn_workspace(M, nH, hd, max_keys, q.device)
+    call("q4_pre_attn", _p(q), _dt(q), ldq, _p(qnw), _p(cosM), _p(sinM), _p(kc), _p(vc), _p(out), _dt(out), nH * hd,
+         nH, nkv, hd, stride, window, M, max_keys, _p(dyn), _p(ws), _nbytes(ws), _stream())
+    return out
+
+
 def stream_wait(stream=None, timeout_ms: int = 0, label: str = "") -> None:
     """Bounded wait; raises RuntimeError('GPU fence TIMEOUT after <ms>ms at [label]') on expiry,
     the message the reference's fence wait raises (src/vk_engine.py:299-302)."""

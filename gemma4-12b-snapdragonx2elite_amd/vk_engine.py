@@ -273,17 +273,23 @@ def _stage(name: str, nbytes: int) -> Buf:
     return b
 
 
-def gemm_ds(qw, inbuf: Buf, outbuf: Buf, prefill_i8: bool | None = None):
+def gemm_ds(qw, inbuf: Buf, outbuf: Buf, prefill_i8: bool | None = None, x_dtype=torch.float32,
+            y_dtype=torch.float32):
     """Prefill GEMM wiring for an ``MC``-row chunk (src/vk_engine.py:351-365).
 
     f16 route: cast f32->f16, W4A16 GEMM, cast f16->f32. W8A8 route
     (``PREFILL_I8``): per-row int8 quant, W8A8 GEMM, cast f16->f32.
+    ``x_dtype=float16``: ``inbuf`` already holds the fp16 rows (its producer
+    wrote them; the cast the reference runs would give the same values) and
+    the f16 route skips its down-cast; ``y_dtype=float16``: the GEMM writes
+    ``outbuf`` directly (its consumer reads fp16) and the up-cast is skipped.
     """
     prefill_i8 = PREFILL_I8 if prefill_i8 is None else prefill_i8
     (bw, _bs, _s, _n, _inv, bs16, w8, sw8), (N, K) = qw
-    xin = inbuf.view(torch.float32, MC * K).view(MC, K)
-    yout = outbuf.view(torch.float32, MC * N).view(MC, N)
-    y16 = _stage("Yf16", MC * max(N, K) * 2).view(torch.float16, MC * N).view(MC, N)
+    xin = inbuf.view(x_dtype, MC * K).view(MC, K)
+    yout = outbuf.view(y_dtype, MC * N).view(MC, N)
+    y16 = yout if y_dtype == torch.float16 else \
+        _stage("Yf16", MC * max(N, K) * 2).view(torch.float16, MC * N).view(MC, N)
     if prefill_i8:
         if w8 is None:
             raise ValueError("PREFILL_I8 needs int8 weights: quantize with pf=True and prefill_i8=True")
@@ -294,12 +300,15 @@ def gemm_ds(qw, inbuf: Buf, outbuf: Buf, prefill_i8: bool | None = None):
         cin = ("quant_act_i8", xin, a8, sa)
         gem = ("w8a8", a8, W8p, sa, sw, y16, N)
     else:
-        x16 = _stage("Xf16", MC * max(N, K) * 2).view(torch.float16, MC * K).view(MC, K)
-        cin = ("cast_dn", xin, x16)
+        if x_dtype == torch.float16:
+            x16, cin = xin, None
+        else:
+            x16 = _stage("Xf16", MC * max(N, K) * 2).view(torch.float16, MC * K).view(MC, K)
+            cin = ("cast_dn", xin, x16)
         need = ops.gemm_workspace_bytes(MC, N, K)   # split-K partials, allocated here so recording can capture
         ws = _stage("W4ws", need).view(torch.uint8, need) if need else None
         gem = ("w4a16", x16, bw.t, bs16.t, N, y16, ws)
-    cout = ("cast_up", y16, yout)
+    cout = None if y_dtype == torch.float16 else ("cast_up", y16, yout)
     return (cin, gem, cout, N, K)
 
 
@@ -323,12 +332,13 @@ def gmm(C, t, L=None, tag: str = "") -> None:
     """cast -> GEMM -> cast for one prefill matmul (src/vk_engine.py:391-400).
     ``C``: torch stream to enqueue on (None = current stream)."""
     cin, gem, cout, _N, _K = t
+    seq = [op for op in (cin, gem, cout) if op is not None]
     if C is None:
-        for op in (cin, gem, cout):
+        for op in seq:
             _run(op)
     else:
         with torch.cuda.stream(C):
-            for op in (cin, gem, cout):
+            for op in seq:
                 _run(op)
 
 
@@ -432,6 +442,107 @@ def attn_ds(qkv: Buf, qnw: Buf, cosb: Buf, sinb: Buf, kc: Buf, vc: Buf, out: Buf
               dyn=dyn.view(torch.int32, 4), ws=ws)
     return OpDesc(ops.attn, (qkv.view(torch.float32), _f32v(qnw, hd), _f32v(cosb, hd), _f32v(sinb, hd),
                              kc.view(torch.float16), vc.view(torch.float16), out.view(out_dtype, nH * hd)), kw)
+
+
+# ----------------------------------------------- batched-prefill layer ops
+def pre_norm_ds(inbuf: Buf, wb: Buf, outbuf: Buf, du, out_dtype=torch.float32) -> OpDesc:
+    """RMS norm of the ``MC`` rows of ``du[0]`` floats (p_in, p_pfn:
+    src/vk_engine.py:369,377, vk/pre_norm.comp)."""
+    D = int(_u32(du)[0])
+    return OpDesc(ops.pre_rmsnorm, (_f32v(inbuf, MC * D), _f32v(wb, D), outbuf.view(out_dtype, MC * D)),
+                  dict(M=MC, D=D))
+
+
+def pre_na_ds(xbuf: Buf, wb: Buf, hbuf: Buf, du, x_dtype=torch.float32) -> OpDesc:
+    """``h = (h + norm(x) * w) * sc`` per row (p_na, p_nas: :376,382-383,
+    vk/pre_na.comp); ``x_dtype=float16`` reads a GEMM's fp16 output."""
+    u = _u32(du)
+    D, sc = int(u[0]), float(u[1:2].view(np.float32)[0])
+    return OpDesc(ops.pre_normadd, (xbuf.view(x_dtype, MC * D), _f32v(wb, D), _f32v(hbuf, MC * D)),
+                  dict(M=MC, D=D, scale=sc))
+
+
+def pre_gelumul_ds(gate: Buf, up: Buf, out: Buf, du, in_dtype=torch.float32, out_dtype=torch.float32) -> OpDesc:
+    """``out = gelu_tanh(gate) * up`` over ``du[0]`` (= MC * I) elements (p_gm, :380)."""
+    n = int(_u32(du)[0])
+    return OpDesc(ops.pre_gelumul, (gate.view(in_dtype, n), up.view(in_dtype, n), out.view(out_dtype, n)), {})
+
+
+def pre_prepkv_ds(kbuf: Buf, vbuf: Buf, knw: Buf, cosM: Buf, sinM: Buf, kc: Buf, vc: Buf, Pp, dyn: Buf,
+                  kv_dtype=torch.float32) -> OpDesc:
+    """The chunk's K/V into the caches (p_prep, :372-374); ``Pp`` = (nkv, hd,
+    nk, 0, stride, window, 0, 0), ``vbuf`` the K buffer for k == v layers,
+    ``dyn`` = (p0, MC, 0, 0)."""
+    nkv, hd, nk, _z, stride, window = (int(v) for v in np.asarray(Pp, np.uint32)[:6])
+    kw = dict(M=MC, ld=nk, nkv=nkv, hd=hd, stride=stride, window=window, dyn=dyn.view(torch.int32, 4))
+    return OpDesc(ops.pre_prepkv, (kbuf.view(kv_dtype, MC * nk), vbuf.view(kv_dtype, MC * nk), _f32v(knw, hd),
+                                   _f32v(cosM, MC * hd), _f32v(sinM, MC * hd), kc.view(torch.float16),
+                                   vc.view(torch.float16)), kw)
+
+
+def pre_attn_ds(qbuf: Buf, qnw: Buf, cosM: Buf, sinM: Buf, kc: Buf, vc: Buf, out: Buf, Aa, dyn: Buf, nkv: int,
+                max_keys: int | None = None, q_dtype=torch.float32, out_dtype=torch.float32) -> OpDesc:
+    """Causal attention of the chunk (p_attn, :375-377); ``Aa`` = (nH, nq, hd,
+    stride, window, grp, 0, 0). ``max_keys`` bounds the keys a token will
+    see (default: the ring for sliding layers, the cache for global ones);
+    the split-key scratch is allocated here, before any recording."""
+    nH, nq, hd, stride, window, grp = (int(v) for v in np.asarray(Aa, np.uint32)[:6])
+    if nH // grp != nkv:
+        raise ValueError(f"grp={grp} does not match nH={nH} / nkv={nkv}")
+    mk = max_keys or (window if window > 0 else stride)
+    ws = ops.pre_attn_workspace(MC, nH, hd, mk, qbuf.t.device)
+    KEEP.append(ws)
+    kw = dict(M=MC, ldq=nq, nH=nH, nkv=nkv, hd=hd, stride=stride, window=window, max_keys=mk,
+              dyn=dyn.view(torch.int32, 4), ws=ws)
+    return OpDesc(ops.pre_attn, (qbuf.view(q_dtype, MC * nq), _f32v(qnw, hd), _f32v(cosM, MC * hd),
+                                 _f32v(sinM, MC * hd), kc.view(torch.float16), vc.view(torch.float16),
+                                 out.view(out_dtype, MC * nH * hd)), kw)
+
+
+def record_prefill(layers, fuse: bool = True) -> ops.Graph:
+    """Record the prefill of one ``MC``-token chunk through ``layers`` in the
+    reference's order (rec_layer, src/vk_engine.py:410-424): per layer
+    p_in, the q/k/v GEMMs, p_prep, p_attn, the o GEMM, p_na, p_pfn, the
+    gate/up GEMMs, p_gm, the down GEMM, p_nas. ``layers`` holds the
+    reference's per-layer keys (``p_in`` ... ``p_nas``; ``p_v`` may be None;
+    GEMM entries are :func:`gemm_ds` tuples). The reference submits one
+    command buffer per layer; one graph holds them all here (the chunk's
+    buffers persist between layers either way). With ``fuse``, each
+    pre_na and the pre_norm of the same rows after it run as one launch."""
+    seq = []
+    for L in layers:
+        seq += [L["p_in"], ("gmm", L["p_q"]), ("gmm", L["p_k"])] + \
+               ([("gmm", L["p_v"])] if L.get("p_v") is not None else []) + \
+               [L["p_prep"], L["p_attn"], ("gmm", L["p_o"]), L["p_na"], L["p_pfn"], ("gmm", L["p_g"]),
+                ("gmm", L["p_u"]), L["p_gm"], ("gmm", L["p_d"]), L["p_nas"]]
+    if fuse:
+        seq = _fuse_pre_norms(seq)
+
+    def body():
+        for op in seq:
+            if isinstance(op, tuple) and op and op[0] == "gmm":
+                gmm(None, op[1])
+            else:
+                disp(op)
+    return record(body)
+
+
+def _fuse_pre_norms(seq):
+    """A pre_na followed by a pre_norm of the same rows: one launch."""
+    out, i = [], 0
+    while i < len(seq):
+        a = seq[i]
+        b = seq[i + 1] if i + 1 < len(seq) else None
+        if (isinstance(a, OpDesc) and isinstance(b, OpDesc) and a.fn is ops.pre_normadd and b.fn is ops.pre_rmsnorm
+                and a.args[2].data_ptr() == b.args[0].data_ptr() and a.kw["D"] == b.kw["D"]):
+            x, w, h = a.args
+            _, w2, y = b.args
+            out.append(OpDesc(ops.pre_normadd, (x, w, h), dict(a.kw, w2=w2, y=y)))
+            i += 2
+        else:
+            out.append(a)
+            i += 1
+    return out
 
 
 # ------------------------------------------------------- record-once submit

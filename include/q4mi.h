@@ -302,6 +302,56 @@ int q4_prepkv_attn(const float* qkv, const float* knw, const float* qnw, const f
                    int nkv, int hd, int stride, int window, int qoff, int koff, int voff, int keqv,
                    int grp, const uint32_t* dyn, void* ws, size_t ws_bytes, void* stream);
 
+/* ---- batched prefill layer ops --------------------------------------------
+ * One chunk of M tokens at positions p0 .. p0+M-1 (p0 = dyn[0], read on the
+ * device so a recorded graph replays every chunk), the reference's prefill
+ * layer graph (src/vk_engine.py:410-424, buffers :339-383). Rows are
+ * [M][D] row-major; x inputs may be fp16 where the reference up-casts an
+ * fp16 GEMM output to fp32 first (that value is exact), outputs that feed a
+ * GEMM may be fp16 where the reference down-casts them (the same rounding).
+ * Row-wise rmsnorm: vk/pre_norm.comp:9-13. */
+int q4_pre_rmsnorm(const float* x, const float* w, void* y, int y_dtype, int D,
+                   int M, void* stream);
+/* Row-wise h = (h + rmsnorm(x) * w) * sc (sc = scale, or 1 for 0):
+ * vk/pre_na.comp:9-14; x fp32 or fp16. */
+int q4_pre_normadd(const void* x, int x_dtype, const float* w, float* h, int D,
+                   int M, float scale, void* stream);
+/* The same followed by the rmsnorm the reference records next on the new h
+ * (p_na then p_pfn, p_nas then the next layer's p_in: :419-420, :424, :413),
+ * one launch per row set. */
+int q4_pre_normadd_rmsnorm(const void* x, int x_dtype, const float* w, float* h,
+                           int D, int M, float scale, const float* w2, void* y,
+                           int y_dtype, void* stream);
+/* gelumul over n = M * I elements with fp32 or fp16 gate/up (the prefill
+ * dispatch of vk/gelumul.comp at :422). */
+int q4_pre_gelumul(const void* gate, const void* up, int in_dtype, void* out,
+                   int out_dtype, long n, void* stream);
+/* Every token's K (k-norm with weight, RoPE with the token's cos/sin row)
+ * and V (v-norm) of every KV head into the fp16 caches at the token's slot:
+ * vk/pre_prepkv.comp:18-32. k, v [M][ld] (v may equal k for k == v layers),
+ * cosM/sinM [M][hd]. When the chunk wraps a ring, the later token of a
+ * shared slot is the one written. */
+int q4_pre_prepkv(const void* k, const void* v, int kv_dtype, int ld,
+                  const float* knw, const float* cosM, const float* sinM,
+                  uint16_t* kc, uint16_t* vc, int nkv, int hd, int stride,
+                  int window, int M, const uint32_t* dyn, void* stream);
+/* Causal attention of every token of the chunk (vk/pre_attn.comp:18-53):
+ * q [M][ldq] (head h at h*hd; fp32 or fp16) with q-norm and RoPE per token,
+ * scores over the first min(pos+1, window or stride) slots of KV head
+ * h / (nH / nkv) (no score scaling), ring slots holding a later token of
+ * the chunk skipped, softmax, fp16 V; out [M][ldo]. Head dims 64, 128,
+ * 256, 512; M <= window for ring layers. max_keys bounds the keys any token
+ * of any chunk the call (or a graph of it) will see (window for ring
+ * layers, the prompt length for global ones); ws: workspace of
+ * q4_pre_attn_workspace_bytes(M, nH, hd, max_keys) bytes. Two launches
+ * (split-key MFMA attention, then the split merge). */
+size_t q4_pre_attn_workspace_bytes(int M, int nH, int hd, int max_keys);
+int q4_pre_attn(const void* q, int q_dtype, int ldq, const float* qnw,
+                const float* cosM, const float* sinM, const uint16_t* kc,
+                const uint16_t* vc, void* out, int out_dtype, int ldo, int nH,
+                int nkv, int hd, int stride, int window, int M, int max_keys,
+                const uint32_t* dyn, void* ws, size_t ws_bytes, void* stream);
+
 /* ---- record-once submit --------------------------------------------------
  * The per-token command buffer recorded once and resubmitted
  * (src/vk_engine.py:254-290, forward() :312-319) becomes a hipGraph captured

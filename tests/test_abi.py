@@ -86,6 +86,28 @@ def test_argument_errors_without_gpu(g4):
     assert st == g4._lib.Q4_ERR_ARG and "null" in _err(g4)
 
 
+def test_prefill_op_argument_errors_without_gpu(g4):
+    lib = g4._lib.lib()
+    p = C.c_void_p(1 << 20)
+    null = C.c_void_p(0)
+    # head dims outside 64/128/256/512
+    st = lib.q4_pre_attn(p, 0, 96 * 4, p, p, p, p, p, p, 0, 96 * 4, 4, 2, 96, 64, 0, 8, 64, p, p, 1 << 30, null)
+    assert st == g4._lib.Q4_ERR_ARG and "head dims" in _err(g4)
+    # a chunk longer than the ring
+    st = lib.q4_pre_attn(p, 0, 1024, p, p, p, p, p, p, 0, 1024, 4, 2, 256, 64, 32, 33, 64, p, p, 1 << 30, null)
+    assert st == g4._lib.Q4_ERR_ARG and "longer than" in _err(g4)
+    # workspace too small
+    need = lib.q4_pre_attn_workspace_bytes(8, 4, 256, 64)
+    assert need == 8 * 4 * 1 * (256 + 4) * 4
+    st = lib.q4_pre_attn(p, 0, 1024, p, p, p, p, p, p, 0, 1024, 4, 2, 256, 64, 0, 8, 64, p, p, need - 1, null)
+    assert st == g4._lib.Q4_ERR_ARG and "workspace" in _err(g4)
+    # prepkv row stride shorter than nkv * hd
+    st = lib.q4_pre_prepkv(p, p, 0, 100, p, p, p, p, p, 2, 64, 16, 16, 4, p, null)
+    assert st == g4._lib.Q4_ERR_ARG and "row stride" in _err(g4)
+    st = lib.q4_pre_normadd(p, 2, p, p, 64, 4, C.c_float(0.0), null)
+    assert st == g4._lib.Q4_ERR_ARG and "x_dtype" in _err(g4)
+
+
 def test_sizes_and_split_queries(g4):
     lib = g4._lib.lib()
     wb, se = C.c_size_t(), C.c_size_t()
