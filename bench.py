@@ -263,6 +263,108 @@ def bench_small_m(ops, reps: int = 6):
     return out
 
 
+def bench_prefill(ops, reps: int = 5, p0: int = 3968):
+    """One 128-token prefill chunk through the 48-layer stack with the
+    batched-prefill layer graph (vk_engine.record_prefill: per layer
+    pre_norm, q/k/v W4A16 GEMMs, pre_prepkv, pre_attn, o GEMM, pre_na +
+    pre_norm, gate/up GEMMs, gelumul, down GEMM, pre_na), fp16 buffers
+    between producers and GEMMs, fused norms. Layers: 40 sliding (16 query
+    and 8 KV heads of 256, 1024-slot ring) and 8 global (16 query heads and
+    one k == v head of 512, every sixth layer), H 3840, I 15360; the chunk
+    is the last of a 4096-token prompt (p0 = 3968: sliding layers attend
+    1024 keys, global layers 4096). Synthetic int4 weights (distinct per
+    layer), HIP events over graph replays. Also times the attention
+    launches alone (their own graph)."""
+    import importlib
+
+    import numpy as np
+    import torch
+
+    E = importlib.import_module("g4mi.vk_engine")
+    MC = E.MC
+    dev = torch.device("cuda:0")
+    gen = torch.Generator(device=dev).manual_seed(5)
+
+    def qw(N, K):
+        w = torch.randint(-2 ** 31, 2 ** 31 - 1, (N * K // 8,), dtype=torch.int64, device=dev,
+                          generator=gen).to(torch.int32)
+        sc = (torch.randn(N * K // 32, device=dev, generator=gen) * 0.02).abs().to(torch.float16)
+        b = E.Buf(tensor=sc)
+        return E.QW(E.Buf(tensor=w), b, 1, K // 32, 1.0, b, None, None), (N, K)
+
+    def fbuf(n, scale=1.0, dtype=torch.float32):
+        return E.Buf(tensor=(torch.rand(n, device=dev, generator=gen) * scale + 0.5 * scale).to(dtype))
+
+    h16 = torch.float16
+    NHq, prompt = 16, p0 + MC
+    Xp = E.Buf(tensor=torch.randn(MC * H, device=dev, generator=gen))
+    Np, Tp = E.Buf(MC * H * 4), E.Buf(MC * H * 4)
+    Qp, Ap = E.Buf(MC * NHq * 512 * 4), E.Buf(MC * NHq * 512 * 4)
+    Kp, Vp = E.Buf(MC * 8 * 256 * 4), E.Buf(MC * 8 * 256 * 4)
+    Gp, Upp, ACp = E.Buf(MC * I * 4), E.Buf(MC * I * 4), E.Buf(MC * I * 4)
+    cosM = {hd: fbuf(MC * hd) for hd in (256, 512)}
+    sinM = {hd: fbuf(MC * hd) for hd in (256, 512)}
+    DYNP = E.buf_u32([p0, MC, 0, 0])
+    DUH = E.buf_u32([H, 0, 0, 0])
+    DUIp = E.buf_u32([MC * I, 0, 0, 0])
+    gk = dict(x_dtype=h16, y_dtype=h16)
+    layers, weight_bytes = [], 0
+    for li in range(LAYERS):
+        glob = li % 6 == 5
+        hd, nkv, window, stride = (512, 1, 0, prompt) if glob else (256, 8, 1024, 1024)
+        nq, nk = NHq * hd, nkv * hd
+        kc = E.Buf(tensor=torch.randn(nkv * stride * hd, device=dev, generator=gen).to(h16))
+        vc = E.Buf(tensor=torch.randn(nkv * stride * hd, device=dev, generator=gen).to(h16))
+        q, k = qw(nq, H), qw(nk, H)
+        v = None if glob else qw(nk, H)
+        o, g, u, d = qw(H, nq), qw(I, H), qw(I, H), qw(H, I)
+        weight_bytes += sum(N * K // 2 + N * K // 16 for _, (N, K) in [q, k, o, g, u, d] + ([v] if v else []))
+        nb = {kk: fbuf(n, 0.1) for kk, n in dict(qnw=hd, knw=hd, inw=H, paw=H, pfw=H, ofw=H).items()}
+        Pp = [nkv, hd, nk, 0, stride, window, 0, 0]
+        Aa = [NHq, nq, hd, stride, window, NHq // nkv, 0, 0]
+        nas = E.buf_u32([H, int(np.array([0.5], np.float32).view(np.uint32)[0]), 0, 0])
+        layers.append(dict(
+            p_in=E.pre_norm_ds(Xp, nb["inw"], Np, DUH, out_dtype=h16),
+            p_q=E.gemm_ds(q, Np, Qp, **gk), p_k=E.gemm_ds(k, Np, Kp, **gk),
+            p_v=None if glob else E.gemm_ds(v, Np, Vp, **gk),
+            p_prep=E.pre_prepkv_ds(Kp, Kp if glob else Vp, nb["knw"], cosM[hd], sinM[hd], kc, vc, Pp, DYNP,
+                                   kv_dtype=h16),
+            p_attn=E.pre_attn_ds(Qp, nb["qnw"], cosM[hd], sinM[hd], kc, vc, Ap, Aa, DYNP, nkv,
+                                 max_keys=prompt if glob else window, q_dtype=h16, out_dtype=h16),
+            p_o=E.gemm_ds(o, Ap, Tp, **gk),
+            p_na=E.pre_na_ds(Tp, nb["paw"], Xp, DUH, x_dtype=h16),
+            p_pfn=E.pre_norm_ds(Xp, nb["pfw"], Np, DUH, out_dtype=h16),
+            p_g=E.gemm_ds(g, Np, Gp, **gk), p_u=E.gemm_ds(u, Np, Upp, **gk),
+            p_gm=E.pre_gelumul_ds(Gp, Upp, ACp, DUIp, in_dtype=h16, out_dtype=h16),
+            p_d=E.gemm_ds(d, ACp, Tp, **gk),
+            p_nas=E.pre_na_ds(Tp, nb["ofw"], Xp, nas, x_dtype=h16)))
+    graph = E.record_prefill(layers, fuse=True)
+    att = E.record(lambda: [E.disp(L["p_attn"]) for L in layers])
+
+    def timed(gr, n):
+        gr.launch()
+        gr.launch()
+        a = torch.cuda.Event(enable_timing=True)
+        b = torch.cuda.Event(enable_timing=True)
+        a.record(gr.stream)
+        for _ in range(n):
+            gr.launch()
+        b.record(gr.stream)
+        b.synchronize()
+        return a.elapsed_time(b) / n
+
+    ms = timed(graph, reps)
+    ms_att = timed(att, reps)
+    graph.destroy()
+    att.destroy()
+    del layers
+    torch.cuda.empty_cache()
+    return {"chunk_tokens": MC, "p0": p0, "layers": LAYERS, "global_layers": LAYERS // 6,
+            "ms_per_chunk": round(ms, 3), "prompt_tok_per_s": round(MC / (ms * 1e-3), 1),
+            "attention_ms_per_chunk": round(ms_att, 3), "attention_share": round(ms_att / ms, 3),
+            "weight_bytes": weight_bytes, "weight_GBps": round(weight_bytes / (ms * 1e-3) / 1e9, 1)}
+
+
 def bench_token_step(ops, steps: int, warmup: int, pos: int = 1023, fast: bool = False):
     """A whole decode token through the engine mirror (vk_engine.py): the
     reference's per-layer dispatch order (norm, q/k/v, prepkv, attention, o,
@@ -535,6 +637,8 @@ def main():
                     help="run only the decode GEMV launches (16 per layer shape, 2 lm_head) and a 512 MiB "
                          "calibration copy, for rocprofv3 --pmc passes; prints no JSON line")
     ap.add_argument("--no-token", action="store_true", help="skip the whole-token legs")
+    ap.add_argument("--prefill-only", action="store_true",
+                    help="run only the prefill-chunk leg; prints its result, no JSON line")
     ap.add_argument("--token-only", action="store_true",
                     help="run only the whole-token legs (reference dispatches, then fused) for --steps replays; "
                          "prints their results, no JSON line")
@@ -550,6 +654,9 @@ def main():
     ops = load_ops()
     if args.counters:
         counter_workload(ops)
+        return
+    if args.prefill_only:
+        print(f"[bench] prefill chunk {bench_prefill(ops, reps=max(1, args.steps // 40))}", flush=True)
         return
     if args.token_only:
         for fast in (False, True):
@@ -571,6 +678,8 @@ def main():
     print(f"[bench] single-shape gemv {single}", flush=True)
     small = bench_small_m(ops)
     print(f"[bench] small-M gemv {small}", flush=True)
+    pre = bench_prefill(ops)
+    print(f"[bench] prefill chunk {pre}", flush=True)
     w8 = w4 = None
     if not args.no_gemm:
         w8 = bench_w8a8(ops)
@@ -615,6 +724,7 @@ def main():
             "single_shape_gemv": single,
             "full_token_step": tok,
             "small_m_gemv": small,
+            "prefill_chunk": pre,
         },
         "roofline": {
             "bound": "hbm",

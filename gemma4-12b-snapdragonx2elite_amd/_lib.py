@@ -46,7 +46,7 @@ SIGNATURES = {
     "q4_pre_normadd_rmsnorm": (_i, [_vp, _i, _vp, _vp, _i, _i, _f, _vp, _vp, _i, _vp]),
     "q4_pre_gelumul": (_i, [_vp, _vp, _i, _vp, _i, C.c_long, _vp]),
     "q4_pre_prepkv": (_i, [_vp, _vp, _i, _i, _vp, _vp, _vp, _vp, _vp, _i, _i, _i, _i, _i, _vp, _vp]),
-    "q4_pre_attn_workspace_bytes": (_sz, [_i, _i, _i, _i]),
+    "q4_pre_attn_workspace_bytes": (_sz, [_i, _i, _i, _i, _i]),
     "q4_pre_attn": (_i, [_vp, _i, _i, _vp, _vp, _vp, _vp, _vp, _vp, _i, _i, _i, _i, _i, _i, _i, _i, _i, _vp, _vp,
                          _sz, _vp]),
     "q4_gemv_multi": (_i, [_vp, _i, _vp, _vp, _i, _f, _vp, _i, _i, _i, _i, _vp]),

@@ -8,9 +8,11 @@
 // MFMAs:
 //  * A workgroup (4 waves) owns 64 query rows of one KV head (row = token *
 //    grp + query head within the group, so the rows share their K and V)
-//    and one split of 128 cache slots; the grid covers the cache capacity
-//    the caller asks for and splits past a workgroup's last token exit at
-//    once, so the launch shape does not depend on p0 (graph replay).
+//    and one split of the cache slots (a multiple of 32 keys, long enough
+//    that the grid has about 256 workgroups: 128 keys for a 1024-slot ring
+//    of 8 KV heads, 512 for 4096 keys of one KV head); the grid covers the
+//    keys the caller bounds and splits past a workgroup's last token exit
+//    at once, so the launch shape does not depend on p0 (graph replay).
 //  * q prologue, in registers: lane (c, g) of wave w holds row 16w + c,
 //    elements 32j + 8g .. 32j + 8g + 7 of every 32-element chunk j; the
 //    RoPE partner of element e (e +- hd/2) is in the same lane, and the
@@ -37,7 +39,7 @@ constexpr int PA_WAVES = 4;
 constexpr int PA_THREADS = 64 * PA_WAVES;
 constexpr int PA_ROWS = 16 * PA_WAVES;  // query rows per workgroup
 constexpr int PA_KT = 32;               // keys per LDS tile
-constexpr int PA_KS = 128;              // keys per split
+constexpr int PA_TARGET_WGS = 256;      // workgroups the split length aims for (one per CU)
 constexpr float PA_EPS = 1e-6f;
 
 typedef _Float16 v4h __attribute__((ext_vector_type(4)));
@@ -64,7 +66,7 @@ __global__ void __launch_bounds__(PA_THREADS)
 pre_attn_kernel(const void* __restrict__ qin, int ldq, const float* __restrict__ qnw, const float* __restrict__ cosM,
                 const float* __restrict__ sinM, const uint16_t* __restrict__ kc, const uint16_t* __restrict__ vc,
                 int stride, int window, int grp, int nH, int M, const uint32_t* __restrict__ dyn,
-                float* __restrict__ ws, int nsplit) {
+                float* __restrict__ ws, int nsplit, int ksl) {
   constexpr int NCH = HD / 32;        // 32-element chunks (QK k-steps)
   constexpr int NDT = HD / 16;        // 16-element output tiles
   constexpr int CPR = HD / 8;         // 16-byte chunks per K/V row
@@ -82,9 +84,9 @@ pre_attn_kernel(const void* __restrict__ qin, int ldq, const float* __restrict__
   const int nrows = M * grp, r0 = blockIdx.y * PA_ROWS;
   const int mlast = (min(r0 + PA_ROWS, nrows) - 1) / grp;
   const int Tlast = att_len(p0 + (uint32_t)mlast, window, stride);
-  const int k0 = ks * PA_KS;
+  const int k0 = ks * ksl;
   if (k0 >= Tlast) return;  // no row of this workgroup has keys in this split (uniform)
-  const int kend = min(k0 + PA_KS, Tlast);
+  const int kend = min(k0 + ksl, Tlast);
   const uint32_t last = p0 + (uint32_t)M - 1;  // the chunk's last position (all of its K/V are written)
 
   // ---- this lane's query row: q-norm, RoPE, hi/lo split ----
@@ -142,37 +144,43 @@ pre_attn_kernel(const void* __restrict__ qin, int ldq, const float* __restrict__
   float mrun = -INFINITY, lrun = 0.0f;
 
   for (int t0 = k0; t0 < kend; t0 += PA_KT) {
-    // ---- stage the tile's K (row-major) and V (transposed, key pairs) ----
-    v4u kr[KLD], va[VLD], vb[VLD];
+    // ---- stage the tile's K (row-major) and V (transposed, key pairs); one
+    //      operand at a time, so the staging registers are those of one ----
+    {
+      v4u kr[KLD];
 #pragma unroll
-    for (int i = 0; i < KLD; ++i) {
-      const int q = min(tid + PA_THREADS * i, KITEMS - 1), key = q / CPR, ch = q % CPR;
-      const int slot = min(t0 + key, stride - 1);
-      kr[i] = *reinterpret_cast<const v4u*>(kc + ((long)kvh * stride + slot) * HD + ch * 8);
+      for (int i = 0; i < KLD; ++i) {
+        const int q = min(tid + PA_THREADS * i, KITEMS - 1), key = q / CPR, ch = q % CPR;
+        const int slot = min(t0 + key, stride - 1);
+        kr[i] = *reinterpret_cast<const v4u*>(kc + ((long)kvh * stride + slot) * HD + ch * 8);
+      }
+      __syncthreads();  // every wave is done with the previous tile
+#pragma unroll
+      for (int i = 0; i < KLD; ++i) {
+        const int q = tid + PA_THREADS * i, key = q / CPR, ch = q % CPR;
+        if (q < KITEMS) *reinterpret_cast<v4u*>(ksh + key * KP + ch * 16) = kr[i];
+      }
     }
+    {
+      v4u va[VLD], vb[VLD];
 #pragma unroll
-    for (int i = 0; i < VLD; ++i) {
-      const int q = min(tid + PA_THREADS * i, VITEMS - 1), pr = q / CPR, ch = q % CPR;
-      const int s0 = min(t0 + 2 * pr, stride - 1), s1 = min(t0 + 2 * pr + 1, stride - 1);
-      va[i] = *reinterpret_cast<const v4u*>(vc + ((long)kvh * stride + s0) * HD + ch * 8);
-      vb[i] = *reinterpret_cast<const v4u*>(vc + ((long)kvh * stride + s1) * HD + ch * 8);
-    }
-    __syncthreads();  // every wave is done with the previous tile
+      for (int i = 0; i < VLD; ++i) {
+        const int q = min(tid + PA_THREADS * i, VITEMS - 1), pr = q / CPR, ch = q % CPR;
+        const int s0 = min(t0 + 2 * pr, stride - 1), s1 = min(t0 + 2 * pr + 1, stride - 1);
+        va[i] = *reinterpret_cast<const v4u*>(vc + ((long)kvh * stride + s0) * HD + ch * 8);
+        vb[i] = *reinterpret_cast<const v4u*>(vc + ((long)kvh * stride + s1) * HD + ch * 8);
+      }
 #pragma unroll
-    for (int i = 0; i < KLD; ++i) {
-      const int q = tid + PA_THREADS * i, key = q / CPR, ch = q % CPR;
-      if (q < KITEMS) *reinterpret_cast<v4u*>(ksh + key * KP + ch * 16) = kr[i];
-    }
+      for (int i = 0; i < VLD; ++i) {
+        const int q = tid + PA_THREADS * i, pr = q / CPR, ch = q % CPR;
+        if (q >= VITEMS) continue;
 #pragma unroll
-    for (int i = 0; i < VLD; ++i) {
-      const int q = tid + PA_THREADS * i, pr = q / CPR, ch = q % CPR;
-      if (q >= VITEMS) continue;
-#pragma unroll
-      for (int w = 0; w < 4; ++w) {
-        // elements 8 ch + 2w, 8 ch + 2w + 1 of keys 2 pr (low half) and 2 pr + 1 (high half)
-        const uint32_t a = va[i][w], b = vb[i][w];
-        *reinterpret_cast<uint32_t*>(vsh + (8 * ch + 2 * w) * VP + 4 * pr) = (a & 0xFFFFu) | (b << 16);
-        *reinterpret_cast<uint32_t*>(vsh + (8 * ch + 2 * w + 1) * VP + 4 * pr) = (a >> 16) | (b & 0xFFFF0000u);
+        for (int w = 0; w < 4; ++w) {
+          // elements 8 ch + 2w, 8 ch + 2w + 1 of keys 2 pr (low half) and 2 pr + 1 (high half)
+          const uint32_t a = va[i][w], b = vb[i][w];
+          *reinterpret_cast<uint32_t*>(vsh + (8 * ch + 2 * w) * VP + 4 * pr) = (a & 0xFFFFu) | (b << 16);
+          *reinterpret_cast<uint32_t*>(vsh + (8 * ch + 2 * w + 1) * VP + 4 * pr) = (a >> 16) | (b & 0xFFFF0000u);
+        }
       }
     }
     __syncthreads();
@@ -253,10 +261,10 @@ pre_attn_kernel(const void* __restrict__ qin, int ldq, const float* __restrict__
 template <int OT>
 __global__ void __launch_bounds__(256)
 pre_attn_merge_kernel(const float* __restrict__ ws, void* __restrict__ out, int ldo, int hd, int nH, int nsplit,
-                      int stride, int window, const uint32_t* __restrict__ dyn) {
+                      int ksl, int stride, int window, const uint32_t* __restrict__ dyn) {
   const int row = blockIdx.x, m = row / nH, h = row % nH, t = threadIdx.x;
   const int T = att_len(dyn[0] + (uint32_t)m, window, stride);
-  const int ns = min((T + PA_KS - 1) / PA_KS, nsplit);
+  const int ns = min((T + ksl - 1) / ksl, nsplit);
   const float* w = ws + (long)row * nsplit * (hd + 4);
   float mx = -INFINITY;
   for (int cc = 0; cc < ns; ++cc) mx = fmaxf(mx, w[(long)cc * (hd + 4)]);
@@ -278,7 +286,13 @@ pre_attn_merge_kernel(const float* __restrict__ ws, void* __restrict__ out, int 
   }
 }
 
-static int pa_splits(int max_keys) { return (max_keys + PA_KS - 1) / PA_KS; }
+// Keys per split for a launch: a multiple of PA_KT, long enough that the
+// (KV head, row block, split) grid has about PA_TARGET_WGS workgroups.
+static int pa_split_len(int M, int nH, int nkv, int max_keys) {
+  const int blocks = nkv * ceil_div(M * (nH / nkv), PA_ROWS);
+  const int want = max(1, ceil_div(PA_TARGET_WGS, blocks));
+  return PA_KT * ceil_div(max_keys, PA_KT * want);
+}
 
 }  // namespace q4
 
@@ -286,9 +300,10 @@ using namespace q4;
 
 extern "C" {
 
-size_t q4_pre_attn_workspace_bytes(int M, int nH, int hd, int max_keys) {
-  if (M <= 0 || nH <= 0 || hd <= 0 || max_keys <= 0) return 0;
-  return (size_t)M * nH * pa_splits(max_keys) * (hd + 4) * sizeof(float);
+size_t q4_pre_attn_workspace_bytes(int M, int nH, int nkv, int hd, int max_keys) {
+  if (M <= 0 || nH <= 0 || nkv <= 0 || nH % nkv || hd <= 0 || max_keys <= 0) return 0;
+  const int ns = ceil_div(max_keys, pa_split_len(M, nH, nkv, max_keys));
+  return (size_t)M * nH * ns * (hd + 4) * sizeof(float);
 }
 
 int q4_pre_attn(const void* q, int q_dtype, int ldq, const float* qnw, const float* cosM, const float* sinM,
@@ -311,19 +326,19 @@ int q4_pre_attn(const void* q, int q_dtype, int ldq, const float* qnw, const flo
          nH * hd);
   Q4_ARG(max_keys > 0 && max_keys <= stride, "max_keys=%d must be in 1..stride=%d", max_keys, stride);
   Q4_ARG(window == 0 || max_keys >= window, "a ring layer needs max_keys >= window (%d)", window);
-  const size_t need = q4_pre_attn_workspace_bytes(M, nH, hd, max_keys);
+  const size_t need = q4_pre_attn_workspace_bytes(M, nH, nkv, hd, max_keys);
   Q4_ARG(ws_bytes >= need, "prefill attention needs a %zu-byte workspace (got %zu)", need, ws_bytes);
-  const int grp = nH / nkv, ns = pa_splits(max_keys);
+  const int grp = nH / nkv, ksl = pa_split_len(M, nH, nkv, max_keys), ns = ceil_div(max_keys, ksl);
   const dim3 grid(nkv, ceil_div(M * grp, PA_ROWS), ns);
   hipStream_t st = as_stream(stream);
   float* w = reinterpret_cast<float*>(ws);
 #define PA_LAUNCH(HD_)                                                                                            \
   if (q_dtype == Q4_DT_F16)                                                                                       \
     hipLaunchKernelGGL((pre_attn_kernel<HD_, Q4_DT_F16>), grid, dim3(PA_THREADS), 0, st, q, ldq, qnw, cosM, sinM, \
-                       kc, vc, stride, window, grp, nH, M, dyn, w, ns);                                          \
+                       kc, vc, stride, window, grp, nH, M, dyn, w, ns, ksl);                                          \
   else                                                                                                            \
     hipLaunchKernelGGL((pre_attn_kernel<HD_, Q4_DT_F32>), grid, dim3(PA_THREADS), 0, st, q, ldq, qnw, cosM, sinM, \
-                       kc, vc, stride, window, grp, nH, M, dyn, w, ns);
+                       kc, vc, stride, window, grp, nH, M, dyn, w, ns, ksl);
   switch (hd) {
     case 64: PA_LAUNCH(64) break;
     case 128: PA_LAUNCH(128) break;
@@ -334,10 +349,10 @@ int q4_pre_attn(const void* q, int q_dtype, int ldq, const float* qnw, const flo
   Q4_LAUNCHED("pre_attn");
   if (out_dtype == Q4_DT_F16)
     hipLaunchKernelGGL(pre_attn_merge_kernel<Q4_DT_F16>, dim3(M * nH), dim3(256), 0, st, w, out, ldo, hd, nH, ns,
-                       stride, window, dyn);
+                       ksl, stride, window, dyn);
   else
     hipLaunchKernelGGL(pre_attn_merge_kernel<Q4_DT_F32>, dim3(M * nH), dim3(256), 0, st, w, out, ldo, hd, nH, ns,
-                       stride, window, dyn);
+                       ksl, stride, window, dyn);
   Q4_LAUNCHED("pre_attn_merge");
   return Q4_OK;
 }

@@ -644,9 +644,9 @@ def pre_prepkv(k, v, knw, cosM, sinM, kc, vc, *, M: int, ld: int, nkv: int, hd: 
          window, M, _p(dyn), _stream())
 
 
-def pre_attn_workspace(M: int, nH: int, hd: int, max_keys: int, device="cuda") -> torch.Tensor:
+def pre_attn_workspace(M: int, nH: int, nkv: int, hd: int, max_keys: int, device="cuda") -> torch.Tensor:
     """Scratch of :func:`pre_attn` for this shape (no initialisation needed)."""
-    n = int(lib().q4_pre_attn_workspace_bytes(M, nH, hd, max_keys))
+    n = int(lib().q4_pre_attn_workspace_bytes(M, nH, nkv, hd, max_keys))
     return torch.empty(max(n, 16) // 4, dtype=torch.float32, device=device)
 
 
@@ -665,7 +665,7 @@ def pre_attn(q, qnw, cosM, sinM, kc, vc, out=None, *, M: int, ldq: int, nH: int,
     if ws is None:
         if _CAPTURING[0]:
             raise RuntimeError("prefill attention inside a graph capture needs a workspace allocated before it")
-        ws = pre_attn_workspace(M, nH, hd, max_keys, q.device)
+        ws = pre_attn_workspace(M, nH, nkv, hd, max_keys, q.device)
     call("q4_pre_attn", _p(q), _dt(q), ldq, _p(qnw), _p(cosM), _p(sinM), _p(kc), _p(vc), _p(out), _dt(out), nH * hd,
          nH, nkv, hd, stride, window, M, max_keys, _p(dyn), _p(ws), _nbytes(ws), _stream())
     return out

@@ -490,7 +490,7 @@ def pre_attn_ds(qbuf: Buf, qnw: Buf, cosM: Buf, sinM: Buf, kc: Buf, vc: Buf, out
     if nH // grp != nkv:
         raise ValueError(f"grp={grp} does not match nH={nH} / nkv={nkv}")
     mk = max_keys or (window if window > 0 else stride)
-    ws = ops.pre_attn_workspace(MC, nH, hd, mk, qbuf.t.device)
+    ws = ops.pre_attn_workspace(MC, nH, nkv, hd, mk, qbuf.t.device)
     KEEP.append(ws)
     kw = dict(M=MC, ldq=nq, nH=nH, nkv=nkv, hd=hd, stride=stride, window=window, max_keys=mk,
               dyn=dyn.view(torch.int32, 4), ws=ws)

@@ -343,9 +343,9 @@ int q4_pre_prepkv(const void* k, const void* v, int kv_dtype, int ld,
  * 256, 512; M <= window for ring layers. max_keys bounds the keys any token
  * of any chunk the call (or a graph of it) will see (window for ring
  * layers, the prompt length for global ones); ws: workspace of
- * q4_pre_attn_workspace_bytes(M, nH, hd, max_keys) bytes. Two launches
+ * q4_pre_attn_workspace_bytes(M, nH, nkv, hd, max_keys) bytes. Two launches
  * (split-key MFMA attention, then the split merge). */
-size_t q4_pre_attn_workspace_bytes(int M, int nH, int hd, int max_keys);
+size_t q4_pre_attn_workspace_bytes(int M, int nH, int nkv, int hd, int max_keys);
 int q4_pre_attn(const void* q, int q_dtype, int ldq, const float* qnw,
                 const float* cosM, const float* sinM, const uint16_t* kc,
                 const uint16_t* vc, void* out, int out_dtype, int ldo, int nH,

@@ -97,8 +97,8 @@ def test_prefill_op_argument_errors_without_gpu(g4):
     st = lib.q4_pre_attn(p, 0, 1024, p, p, p, p, p, p, 0, 1024, 4, 2, 256, 64, 32, 33, 64, p, p, 1 << 30, null)
     assert st == g4._lib.Q4_ERR_ARG and "longer than" in _err(g4)
     # workspace too small
-    need = lib.q4_pre_attn_workspace_bytes(8, 4, 256, 64)
-    assert need == 8 * 4 * 1 * (256 + 4) * 4
+    need = lib.q4_pre_attn_workspace_bytes(8, 4, 2, 256, 64)
+    assert need == 8 * 4 * 2 * (256 + 4) * 4  # 2 KV-head blocks -> 128 splits wanted -> 2 splits of 32 keys
     st = lib.q4_pre_attn(p, 0, 1024, p, p, p, p, p, p, 0, 1024, 4, 2, 256, 64, 0, 8, 64, p, p, need - 1, null)
     assert st == g4._lib.Q4_ERR_ARG and "workspace" in _err(g4)
     # prepkv row stride shorter than nkv * hd

@@ -189,7 +189,7 @@ def test_pre_attn_graph_replay_follows_p0(gpu):
     cs, sn = _t(np.zeros((M, hd))), _t(np.zeros((M, hd)))
     t_knw, t_qnw = _t(knw), _t(qnw)
     dyn = _dyn(0, M)
-    ws = gpu.pre_attn_workspace(M, nH, hd, window)
+    ws = gpu.pre_attn_workspace(M, nH, nkv, hd, window)
     out = torch.empty(M, nH * hd, device="cuda")
     kw = dict(M=M, nkv=nkv, hd=hd, stride=stride, window=window, dyn=dyn)
     akw = dict(M=M, ldq=nH * hd, nH=nH, nkv=nkv, hd=hd, stride=stride, window=window, max_keys=window)
