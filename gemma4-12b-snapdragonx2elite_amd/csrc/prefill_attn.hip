@@ -37,7 +37,6 @@ namespace q4 {
 
 constexpr int PA_WAVES = 4;
 constexpr int PA_THREADS = 64 * PA_WAVES;
-constexpr int PA_ROWS = 16 * PA_WAVES;  // query rows per workgroup
 constexpr int PA_KT = 32;               // keys per LDS tile
 constexpr int PA_TARGET_WGS = 256;      // workgroups the split length aims for (one per CU)
 constexpr float PA_EPS = 1e-6f;
@@ -61,36 +60,93 @@ __device__ inline long pa_ws_index(int m, int h, int nH, int ks, int nsplit, int
   return (((long)m * nH + h) * nsplit + ks) * (hd + 4);
 }
 
+// Tile geometry per head dim: KT keys per LDS tile and DS waves per row
+// group (each wave of a group computes the group's scores and accumulates
+// 1/DS of the output dims). hd 512 takes 16-key tiles and two waves per
+// row group so q (hi + lo), the output accumulators and the next tile's
+// prefetch registers fit without spills.
+template <int HD>
+struct PaGeom {
+  static constexpr int KT = HD >= 512 ? 16 : 32;
+  static constexpr int DS = HD >= 512 ? 2 : 1;
+  static constexpr int ROWS = 16 * PA_WAVES / DS;  // query rows per workgroup
+};
+
 template <int HD, int QT>
 __global__ void __launch_bounds__(PA_THREADS)
 pre_attn_kernel(const void* __restrict__ qin, int ldq, const float* __restrict__ qnw, const float* __restrict__ cosM,
                 const float* __restrict__ sinM, const uint16_t* __restrict__ kc, const uint16_t* __restrict__ vc,
                 int stride, int window, int grp, int nH, int M, const uint32_t* __restrict__ dyn,
                 float* __restrict__ ws, int nsplit, int ksl) {
+  constexpr int KT = PaGeom<HD>::KT, DS = PaGeom<HD>::DS, ROWS = PaGeom<HD>::ROWS;
+  constexpr int NST = KT / 16;        // 16-key subtiles per tile
   constexpr int NCH = HD / 32;        // 32-element chunks (QK k-steps)
-  constexpr int NDT = HD / 16;        // 16-element output tiles
+  constexpr int NDT = HD / 16 / DS;   // 16-element output tiles of this wave
   constexpr int CPR = HD / 8;         // 16-byte chunks per K/V row
   constexpr int KP = HD * 2 + 16;     // K tile row pitch (bytes)
-  constexpr int VP = PA_KT * 2 + 8;   // V^T tile row pitch (bytes)
-  constexpr int KITEMS = PA_KT * CPR, VITEMS = (PA_KT / 2) * CPR;  // 16-byte K chunks, V key-pair chunks per tile
+  constexpr int VP = KT * 2 + 8;      // V^T tile row pitch (bytes)
+  constexpr int KITEMS = KT * CPR, VITEMS = (KT / 2) * CPR;  // 16-byte K chunks, V key-pair chunks per tile
   constexpr int KLD = (KITEMS + PA_THREADS - 1) / PA_THREADS, VLD = (VITEMS + PA_THREADS - 1) / PA_THREADS;
   static_assert(NCH % 2 == 0, "head dim");
-  __shared__ __attribute__((aligned(16))) uint8_t ksh[PA_KT * KP];
+  __shared__ __attribute__((aligned(16))) uint8_t ksh[KT * KP];
   __shared__ __attribute__((aligned(16))) uint8_t vsh[HD * VP];
 
   const int kvh = blockIdx.x, ks = blockIdx.z;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, c = lane & 15, g = lane >> 4;
+  const int rg = wave / DS, dp = wave % DS;  // row group, output part
   const uint32_t p0 = dyn[0];
-  const int nrows = M * grp, r0 = blockIdx.y * PA_ROWS;
-  const int mlast = (min(r0 + PA_ROWS, nrows) - 1) / grp;
+  const int nrows = M * grp, r0 = blockIdx.y * ROWS;
+  const int mlast = (min(r0 + ROWS, nrows) - 1) / grp;
   const int Tlast = att_len(p0 + (uint32_t)mlast, window, stride);
   const int k0 = ks * ksl;
   if (k0 >= Tlast) return;  // no row of this workgroup has keys in this split (uniform)
   const int kend = min(k0 + ksl, Tlast);
   const uint32_t last = p0 + (uint32_t)M - 1;  // the chunk's last position (all of its K/V are written)
 
+  // ---- the next tile's K and V rows, loaded into registers one tile ahead.
+  //      K chunks go to LDS row-major (lanes take consecutive chunks of a
+  //      row); V chunks of key pairs (2 pr, 2 pr + 1) are interleaved into
+  //      32-bit words of the transposed tile, lanes taking consecutive pairs
+  //      so their LDS words are consecutive (no bank conflicts) ----
+  v4u kr[KLD], va[VLD], vb[VLD];
+  auto load_tile = [&](int t0) {
+#pragma unroll
+    for (int i = 0; i < KLD; ++i) {
+      const int q = min(tid + PA_THREADS * i, KITEMS - 1), key = q / CPR, ch = q % CPR;
+      const int slot = min(t0 + key, stride - 1);
+      kr[i] = *reinterpret_cast<const v4u*>(kc + ((long)kvh * stride + slot) * HD + ch * 8);
+    }
+#pragma unroll
+    for (int i = 0; i < VLD; ++i) {
+      const int q = min(tid + PA_THREADS * i, VITEMS - 1), pr = q % (KT / 2), ch = q / (KT / 2);
+      const int s0 = min(t0 + 2 * pr, stride - 1), s1 = min(t0 + 2 * pr + 1, stride - 1);
+      va[i] = *reinterpret_cast<const v4u*>(vc + ((long)kvh * stride + s0) * HD + ch * 8);
+      vb[i] = *reinterpret_cast<const v4u*>(vc + ((long)kvh * stride + s1) * HD + ch * 8);
+    }
+  };
+  auto store_tile = [&]() {
+#pragma unroll
+    for (int i = 0; i < KLD; ++i) {
+      const int q = tid + PA_THREADS * i, key = q / CPR, ch = q % CPR;
+      if (q < KITEMS) *reinterpret_cast<v4u*>(ksh + key * KP + ch * 16) = kr[i];
+    }
+#pragma unroll
+    for (int i = 0; i < VLD; ++i) {
+      const int q = tid + PA_THREADS * i, pr = q % (KT / 2), ch = q / (KT / 2);
+      if (q >= VITEMS) continue;
+#pragma unroll
+      for (int w = 0; w < 4; ++w) {
+        // elements 8 ch + 2w, 8 ch + 2w + 1 of keys 2 pr (low half) and 2 pr + 1 (high half)
+        const uint32_t a = va[i][w], b = vb[i][w];
+        *reinterpret_cast<uint32_t*>(vsh + (8 * ch + 2 * w) * VP + 4 * pr) = (a & 0xFFFFu) | (b << 16);
+        *reinterpret_cast<uint32_t*>(vsh + (8 * ch + 2 * w + 1) * VP + 4 * pr) = (a >> 16) | (b & 0xFFFF0000u);
+      }
+    }
+  };
+  load_tile(k0);  // in flight while q is prepared
+
   // ---- this lane's query row: q-norm, RoPE, hi/lo split ----
-  const int R = r0 + 16 * wave + c;
+  const int R = r0 + 16 * rg + c;
   const bool live = R < nrows;
   const int m = live ? R / grp : 0;
   const int h = kvh * grp + (live ? R % grp : 0);
@@ -143,52 +199,16 @@ pre_attn_kernel(const void* __restrict__ qin, int ldq, const float* __restrict__
   for (int d = 0; d < NDT; ++d) oacc[d] = v4f{0.0f, 0.0f, 0.0f, 0.0f};
   float mrun = -INFINITY, lrun = 0.0f;
 
-  for (int t0 = k0; t0 < kend; t0 += PA_KT) {
-    // ---- stage the tile's K (row-major) and V (transposed, key pairs); one
-    //      operand at a time, so the staging registers are those of one ----
-    {
-      v4u kr[KLD];
-#pragma unroll
-      for (int i = 0; i < KLD; ++i) {
-        const int q = min(tid + PA_THREADS * i, KITEMS - 1), key = q / CPR, ch = q % CPR;
-        const int slot = min(t0 + key, stride - 1);
-        kr[i] = *reinterpret_cast<const v4u*>(kc + ((long)kvh * stride + slot) * HD + ch * 8);
-      }
-      __syncthreads();  // every wave is done with the previous tile
-#pragma unroll
-      for (int i = 0; i < KLD; ++i) {
-        const int q = tid + PA_THREADS * i, key = q / CPR, ch = q % CPR;
-        if (q < KITEMS) *reinterpret_cast<v4u*>(ksh + key * KP + ch * 16) = kr[i];
-      }
-    }
-    {
-      v4u va[VLD], vb[VLD];
-#pragma unroll
-      for (int i = 0; i < VLD; ++i) {
-        const int q = min(tid + PA_THREADS * i, VITEMS - 1), pr = q / CPR, ch = q % CPR;
-        const int s0 = min(t0 + 2 * pr, stride - 1), s1 = min(t0 + 2 * pr + 1, stride - 1);
-        va[i] = *reinterpret_cast<const v4u*>(vc + ((long)kvh * stride + s0) * HD + ch * 8);
-        vb[i] = *reinterpret_cast<const v4u*>(vc + ((long)kvh * stride + s1) * HD + ch * 8);
-      }
-#pragma unroll
-      for (int i = 0; i < VLD; ++i) {
-        const int q = tid + PA_THREADS * i, pr = q / CPR, ch = q % CPR;
-        if (q >= VITEMS) continue;
-#pragma unroll
-        for (int w = 0; w < 4; ++w) {
-          // elements 8 ch + 2w, 8 ch + 2w + 1 of keys 2 pr (low half) and 2 pr + 1 (high half)
-          const uint32_t a = va[i][w], b = vb[i][w];
-          *reinterpret_cast<uint32_t*>(vsh + (8 * ch + 2 * w) * VP + 4 * pr) = (a & 0xFFFFu) | (b << 16);
-          *reinterpret_cast<uint32_t*>(vsh + (8 * ch + 2 * w + 1) * VP + 4 * pr) = (a >> 16) | (b & 0xFFFF0000u);
-        }
-      }
-    }
+  for (int t0 = k0; t0 < kend; t0 += KT) {
+    __syncthreads();  // every wave is done with the previous tile
+    store_tile();
     __syncthreads();
+    if (t0 + KT < kend) load_tile(t0 + KT);  // the next tile's loads run under this tile's math
 
-    // ---- scores of the tile's 32 keys for this lane's row ----
-    float sc[2][4];
+    // ---- scores of the tile's keys for this lane's row ----
+    float sc[NST][4];
 #pragma unroll
-    for (int st = 0; st < 2; ++st) {
+    for (int st = 0; st < NST; ++st) {
       v4f s = v4f{0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
       for (int j = 0; j < NCH; ++j) {
@@ -206,7 +226,7 @@ pre_attn_kernel(const void* __restrict__ qin, int ldq, const float* __restrict__
     // ---- online softmax over the tile ----
     float tmax = -INFINITY;
 #pragma unroll
-    for (int st = 0; st < 2; ++st)
+    for (int st = 0; st < NST; ++st)
 #pragma unroll
       for (int e = 0; e < 4; ++e) tmax = fmaxf(tmax, sc[st][e]);
     tmax = fmaxf(tmax, __shfl_xor(tmax, 16, 64));
@@ -215,9 +235,9 @@ pre_attn_kernel(const void* __restrict__ qin, int ldq, const float* __restrict__
     const bool any = mnew != -INFINITY;
     const float corr = any ? expf(mrun - mnew) : 1.0f;
     float psum = 0.0f;
-    v4h pb[2];
+    v4h pb[NST];
 #pragma unroll
-    for (int st = 0; st < 2; ++st)
+    for (int st = 0; st < NST; ++st)
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
         // the weights the V product uses are the fp16-rounded ones: the sum
@@ -235,12 +255,12 @@ pre_attn_kernel(const void* __restrict__ qin, int ldq, const float* __restrict__
     for (int d = 0; d < NDT; ++d)
 #pragma unroll
       for (int e = 0; e < 4; ++e) oacc[d][e] *= corr;
-    // ---- O^T += V^T P^T ----
+    // ---- O^T += V^T P^T over this wave's output dims ----
 #pragma unroll
-    for (int st = 0; st < 2; ++st)
+    for (int st = 0; st < NST; ++st)
 #pragma unroll
       for (int d = 0; d < NDT; ++d) {
-        const v4h a = *reinterpret_cast<const v4h*>(vsh + (16 * d + c) * VP + (16 * st + 4 * g) * 2);
+        const v4h a = *reinterpret_cast<const v4h*>(vsh + (16 * (dp * NDT + d) + c) * VP + (16 * st + 4 * g) * 2);
         oacc[d] = __builtin_amdgcn_mfma_f32_16x16x16f16(a, pb[st], oacc[d], 0, 0, 0);
       }
   }
@@ -248,13 +268,16 @@ pre_attn_kernel(const void* __restrict__ qin, int ldq, const float* __restrict__
   // ---- this split's partial for the row ----
   if (!live) return;
   float* o = ws + pa_ws_index(m, h, nH, ks, nsplit, HD);
-  if (g == 0) {
+  if (g == 0 && dp == 0) {
     o[0] = mrun;
     o[1] = lrun;
   }
 #pragma unroll
-  for (int d = 0; d < NDT; ++d) *reinterpret_cast<v4f*>(o + 4 + 16 * d + 4 * g) = oacc[d];
+  for (int d = 0; d < NDT; ++d) *reinterpret_cast<v4f*>(o + 4 + 16 * (dp * NDT + d) + 4 * g) = oacc[d];
 }
+
+// rows per workgroup for head dim hd (PaGeom<hd>::ROWS)
+static int pa_rows(int hd) { return hd >= 512 ? PaGeom<512>::ROWS : PaGeom<256>::ROWS; }
 
 // out[m][h hd + i] = sum_c acc_c w_c / sum_c l_c w_c over the splits that
 // hold keys of token m, w_c = exp(max_c - max); fp32 or fp16 out.
@@ -286,10 +309,10 @@ pre_attn_merge_kernel(const float* __restrict__ ws, void* __restrict__ out, int 
   }
 }
 
-// Keys per split for a launch: a multiple of PA_KT, long enough that the
+// Keys per split for a launch: a multiple of the tile, long enough that the
 // (KV head, row block, split) grid has about PA_TARGET_WGS workgroups.
-static int pa_split_len(int M, int nH, int nkv, int max_keys) {
-  const int blocks = nkv * ceil_div(M * (nH / nkv), PA_ROWS);
+static int pa_split_len(int M, int nH, int nkv, int hd, int max_keys) {
+  const int blocks = nkv * ceil_div(M * (nH / nkv), pa_rows(hd));
   const int want = max(1, ceil_div(PA_TARGET_WGS, blocks));
   return PA_KT * ceil_div(max_keys, PA_KT * want);
 }
@@ -302,7 +325,7 @@ extern "C" {
 
 size_t q4_pre_attn_workspace_bytes(int M, int nH, int nkv, int hd, int max_keys) {
   if (M <= 0 || nH <= 0 || nkv <= 0 || nH % nkv || hd <= 0 || max_keys <= 0) return 0;
-  const int ns = ceil_div(max_keys, pa_split_len(M, nH, nkv, max_keys));
+  const int ns = ceil_div(max_keys, pa_split_len(M, nH, nkv, hd, max_keys));
   return (size_t)M * nH * ns * (hd + 4) * sizeof(float);
 }
 
@@ -328,8 +351,8 @@ int q4_pre_attn(const void* q, int q_dtype, int ldq, const float* qnw, const flo
   Q4_ARG(window == 0 || max_keys >= window, "a ring layer needs max_keys >= window (%d)", window);
   const size_t need = q4_pre_attn_workspace_bytes(M, nH, nkv, hd, max_keys);
   Q4_ARG(ws_bytes >= need, "prefill attention needs a %zu-byte workspace (got %zu)", need, ws_bytes);
-  const int grp = nH / nkv, ksl = pa_split_len(M, nH, nkv, max_keys), ns = ceil_div(max_keys, ksl);
-  const dim3 grid(nkv, ceil_div(M * grp, PA_ROWS), ns);
+  const int grp = nH / nkv, ksl = pa_split_len(M, nH, nkv, hd, max_keys), ns = ceil_div(max_keys, ksl);
+  const dim3 grid(nkv, ceil_div(M * grp, pa_rows(hd)), ns);
   hipStream_t st = as_stream(stream);
   float* w = reinterpret_cast<float*>(ws);
 #define PA_LAUNCH(HD_)                                                                                            \
