@@ -24,8 +24,9 @@
 //    32-bit word) in LDS from registers. Scores S^T = K q^T: one
 //    v_mfma_f32_16x16x32_f16 pair per 16 keys x 16 rows x 32 elements; lane
 //    (c, g) gets keys 4g .. 4g+3 of row c. Masked keys (past the row's
-//    length, or in a ring slot a later token of the chunk now holds) are
-//    -inf. Online softmax per row over the tile (xor-shuffles across the 4
+//    length, or in a ring slot a later token of the chunk now holds: slot s
+//    holds position last - ((last - s) mod window) once the chunk's last
+//    position is written, vk/pre_attn.comp:40) are -inf. Online softmax per row over the tile (xor-shuffles across the 4
 //    lanes of a row), then O^T += V^T P^T with v_mfma_f32_16x16x16_f16: the
 //    B operand is exactly the score layout (P rounded to fp16), the A
 //    operand one 8-byte LDS read of the transposed V.
@@ -43,16 +44,26 @@ constexpr float PA_EPS = 1e-6f;
 
 typedef _Float16 v4h __attribute__((ext_vector_type(4)));
 
+// 8 consecutive elements at element index i (a multiple of 8) of fp32 or
+// fp16 data, as fp32, in 16-byte loads.
 template <int QT>
-__device__ inline float ld_q(const void* q, long i) {
-  if constexpr (QT == Q4_DT_F16) return h2f(reinterpret_cast<const uint16_t*>(q)[i]);
-  else return reinterpret_cast<const float*>(q)[i];
-}
-
-// Position of the key ring slot s holds once positions up to `last` are
-// written (vk/pre_attn.comp:40); for slots never written it is negative.
-__device__ inline long ring_position(int s, uint32_t last, int window) {
-  return (long)last - (long)(((long)last + window - s) % window);
+__device__ inline void ld8f(const void* q, long i, float* out) {
+  if constexpr (QT == Q4_DT_F16) {
+    const v4u u = *reinterpret_cast<const v4u*>(reinterpret_cast<const uint16_t*>(q) + i);
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      out[2 * k] = h2f((uint16_t)(u[k] & 0xFFFFu));
+      out[2 * k + 1] = h2f((uint16_t)(u[k] >> 16));
+    }
+  } else {
+    const v4f a = *reinterpret_cast<const v4f*>(reinterpret_cast<const float*>(q) + i);
+    const v4f b = *reinterpret_cast<const v4f*>(reinterpret_cast<const float*>(q) + i + 4);
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      out[k] = a[k];
+      out[4 + k] = b[k];
+    }
+  }
 }
 
 // Workspace row of (token m, head h), split ks: [max, sum, -, -, acc[HD]].
@@ -154,36 +165,45 @@ pre_attn_kernel(const void* __restrict__ qin, int ldq, const float* __restrict__
   const int T = att_len(pos, window, stride);
   v8h qh[NCH], ql[NCH];
   {
+    // the lane's 8 consecutive elements of each chunk come in 16-byte loads
     float qf[NCH][8];
     const long qb = (long)m * ldq + (long)h * HD;
     float ss = 0.0f;
 #pragma unroll
-    for (int j = 0; j < NCH; ++j)
+    for (int j = 0; j < NCH; ++j) {
+      ld8f<QT>(qin, qb + 32 * j + 8 * g, qf[j]);
 #pragma unroll
-      for (int u = 0; u < 8; ++u) {
-        qf[j][u] = ld_q<QT>(qin, qb + 32 * j + 8 * g + u);
-        ss = fmaf(qf[j][u], qf[j][u], ss);
-      }
+      for (int u = 0; u < 8; ++u) ss = fmaf(qf[j][u], qf[j][u], ss);
+    }
     ss += __shfl_xor(ss, 16, 64);
     ss += __shfl_xor(ss, 32, 64);
     const float inv = 1.0f / sqrtf(ss / (float)HD + PA_EPS);
 #pragma unroll
-    for (int j = 0; j < NCH; ++j)
+    for (int j = 0; j < NCH; ++j) {
+      float w[8];
+      ld8f<Q4_DT_F32>(qnw, 32 * j + 8 * g, w);
 #pragma unroll
-      for (int u = 0; u < 8; ++u) qf[j][u] = __fmul_rn(__fmul_rn(qf[j][u], inv), qnw[32 * j + 8 * g + u]);
+      for (int u = 0; u < 8; ++u) qf[j][u] = __fmul_rn(__fmul_rn(qf[j][u], inv), w[u]);
+    }
     const float* cs = cosM + (long)m * HD;
     const float* sn = sinM + (long)m * HD;
 #pragma unroll
-    for (int j = 0; j < NCH / 2; ++j)
+    for (int j = 0; j < NCH / 2; ++j) {
+      const int e = 32 * j + 8 * g, e2 = e + HD / 2;
+      float c1[8], s1[8], c2[8], s2[8];
+      ld8f<Q4_DT_F32>(cs, e, c1);
+      ld8f<Q4_DT_F32>(sn, e, s1);
+      ld8f<Q4_DT_F32>(cs, e2, c2);
+      ld8f<Q4_DT_F32>(sn, e2, s2);
 #pragma unroll
       for (int u = 0; u < 8; ++u) {
-        const int e = 32 * j + 8 * g + u, e2 = e + HD / 2;
         const float a = qf[j][u], b = qf[j + NCH / 2][u];
-        const float ra = __fadd_rn(__fmul_rn(a, cs[e]), __fmul_rn(-b, sn[e]));
-        const float rb = __fadd_rn(__fmul_rn(b, cs[e2]), __fmul_rn(a, sn[e2]));
+        const float ra = __fadd_rn(__fmul_rn(a, c1[u]), __fmul_rn(-b, s1[u]));
+        const float rb = __fadd_rn(__fmul_rn(b, c2[u]), __fmul_rn(a, s2[u]));
         qf[j][u] = ra;
         qf[j + NCH / 2][u] = rb;
       }
+    }
 #pragma unroll
     for (int j = 0; j < NCH; ++j)
 #pragma unroll
@@ -205,21 +225,34 @@ pre_attn_kernel(const void* __restrict__ qin, int ldq, const float* __restrict__
     __syncthreads();
     if (t0 + KT < kend) load_tile(t0 + KT);  // the next tile's loads run under this tile's math
 
-    // ---- scores of the tile's keys for this lane's row ----
+    // ---- scores of the tile's keys for this lane's row: four independent
+    //      MFMA chains (hi/lo x even/odd chunks) so consecutive MFMAs do not
+    //      wait on each other's results ----
+    // ring slots t0 + i hold position last - ((last - t0 - i) mod window):
+    // one (uniform) division per tile
+    const int rt = window > 0 ? (int)(((long)last - t0) % window) : 0;
     float sc[NST][4];
 #pragma unroll
     for (int st = 0; st < NST; ++st) {
-      v4f s = v4f{0.0f, 0.0f, 0.0f, 0.0f};
+      v4f s0 = v4f{0.0f, 0.0f, 0.0f, 0.0f}, s1 = s0, s2 = s0, s3 = s0;
 #pragma unroll
-      for (int j = 0; j < NCH; ++j) {
-        const v8h a = *reinterpret_cast<const v8h*>(ksh + (16 * st + c) * KP + (4 * j + g) * 16);
-        s = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, qh[j], s, 0, 0, 0);
-        s = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, ql[j], s, 0, 0, 0);
+      for (int j = 0; j < NCH; j += 2) {
+        const v8h a0 = *reinterpret_cast<const v8h*>(ksh + (16 * st + c) * KP + (4 * j + g) * 16);
+        const v8h a1 = *reinterpret_cast<const v8h*>(ksh + (16 * st + c) * KP + (4 * j + 4 + g) * 16);
+        s0 = __builtin_amdgcn_mfma_f32_16x16x32_f16(a0, qh[j], s0, 0, 0, 0);
+        s1 = __builtin_amdgcn_mfma_f32_16x16x32_f16(a1, qh[j + 1], s1, 0, 0, 0);
+        s2 = __builtin_amdgcn_mfma_f32_16x16x32_f16(a0, ql[j], s2, 0, 0, 0);
+        s3 = __builtin_amdgcn_mfma_f32_16x16x32_f16(a1, ql[j + 1], s3, 0, 0, 0);
       }
+      const v4f s = (s0 + s1) + (s2 + s3);
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
-        const int slot = t0 + 16 * st + 4 * g + e;
-        const bool ok = slot < kend && slot < T && (window == 0 || ring_position(slot, last, window) <= (long)pos);
+        const int i = 16 * st + 4 * g + e, slot = t0 + i;
+        bool ok = slot < kend && slot < T;
+        if (window > 0) {
+          const int r = rt - i;  // (last - slot) mod window, for i < window
+          ok = ok && (long)last - (r >= 0 ? r : r + window) <= (long)pos;
+        }
         sc[st][e] = ok ? s[e] : -INFINITY;
       }
     }
@@ -347,6 +380,9 @@ int q4_pre_attn(const void* q, int q_dtype, int ldq, const float* qnw, const flo
   Q4_ARG(window == 0 || M <= window, "a chunk of %d tokens is longer than the %d-slot ring", M, window);
   Q4_ARG(ldq >= nH * hd && ldo >= nH * hd, "row strides ldq=%d ldo=%d are shorter than nH * hd = %d", ldq, ldo,
          nH * hd);
+  Q4_ARG(ldq % 8 == 0 && ((uintptr_t)q & 15) == 0 && ((uintptr_t)qnw & 15) == 0 && ((uintptr_t)cosM & 15) == 0 &&
+             ((uintptr_t)sinM & 15) == 0,
+         "q, qnw, cosM and sinM must be 16-byte aligned and ldq a multiple of 8");
   Q4_ARG(max_keys > 0 && max_keys <= stride, "max_keys=%d must be in 1..stride=%d", max_keys, stride);
   Q4_ARG(window == 0 || max_keys >= window, "a ring layer needs max_keys >= window (%d)", window);
   const size_t need = q4_pre_attn_workspace_bytes(M, nH, nkv, hd, max_keys);
