@@ -535,12 +535,19 @@ def bench_w8a8(ops, iters: int = 50):
 
     us = timed(lambda i: ops.gemm_w8a8_packed(A, W8ps[i % 4], sa, sw, N, Y=Y))
     us_nk = timed(lambda i: ops.gemm_w8a8(A, W8s[i % 4], sa, sw, Y=Y))
+    # W4A8: the same product with B requantized to int8 on the fly from the int4 codes
+    del W8s
+    wq4 = [torch.randint(-2 ** 31, 2 ** 31 - 1, (N * K // 8,), dtype=torch.int64, device=dev,
+                         generator=gen).to(torch.int32) for _ in range(4)]
+    ratio = (torch.rand(N * K // 32, device=dev, generator=gen) * 4 + 1).to(torch.float16)
+    us_w4 = timed(lambda i: ops.gemm_w4a8(A, wq4[i % 4], ratio, sa, sw, N, Y=Y))
     # activation quantizer (bandwidth-bound: 2MK read + MK write)
     us_q = timed(lambda i: ops.quant_act_i8(X, A, sa))
     tops = 2.0 * M * N * K / (us * 1e-6) / 1e12
     return {"M": M, "N": N, "K": K, "weights": "packed (tile-32)", "us": round(us, 2), "TOPS": round(tops, 1),
             "frac_of_int8_peak": round(tops / INT8_PEAK_TOPS, 4),
             "us_row_major_weights": round(us_nk, 2),
+            "w4a8_us": round(us_w4, 2), "w4a8_TOPS": round(2.0 * M * N * K / (us_w4 * 1e-6) / 1e12, 1),
             "quant_act_us": round(us_q, 2), "quant_act_GBps": round(3 * M * K / (us_q * 1e-6) / 1e9, 1)}
 
 
