@@ -541,6 +541,9 @@ def bench_w8a8(ops, iters: int = 50):
                          generator=gen).to(torch.int32) for _ in range(4)]
     ratio = (torch.rand(N * K // 32, device=dev, generator=gen) * 4 + 1).to(torch.float16)
     us_w4 = timed(lambda i: ops.gemm_w4a8(A, wq4[i % 4], ratio, sa, sw, N, Y=Y))
+    # ... or with its int8 weights formed once (q4_w4a8_weights) and packed: the W8A8 kernel, same results
+    W8w4 = [ops.w8_pack(ops.w4a8_weights(w, ratio, N, K)) for w in wq4]
+    us_w4o = timed(lambda i: ops.gemm_w8a8_packed(A, W8w4[i % 4], sa, sw, N, Y=Y))
     # activation quantizer (bandwidth-bound: 2MK read + MK write)
     us_q = timed(lambda i: ops.quant_act_i8(X, A, sa))
     tops = 2.0 * M * N * K / (us * 1e-6) / 1e12
@@ -548,6 +551,7 @@ def bench_w8a8(ops, iters: int = 50):
             "frac_of_int8_peak": round(tops / INT8_PEAK_TOPS, 4),
             "us_row_major_weights": round(us_nk, 2),
             "w4a8_us": round(us_w4, 2), "w4a8_TOPS": round(2.0 * M * N * K / (us_w4 * 1e-6) / 1e12, 1),
+            "w4a8_int8_weights_once_us": round(us_w4o, 2),
             "quant_act_us": round(us_q, 2), "quant_act_GBps": round(3 * M * K / (us_q * 1e-6) / 1e9, 1)}
 
 

@@ -1156,6 +1156,25 @@ __global__ void __launch_bounds__(256) quant_act_kernel(const void* __restrict__
   }
 }
 
+// W4A8's int8 weights computed once: unit u (row n, block b) of the
+// panel-64 words -> W8[n][32 b .. 32 b + 31] = the bytes requant_words_i8
+// gives for that unit (the values w4_kernel forms on the fly, per M-tile).
+__global__ void __launch_bounds__(256) w4a8_weights_kernel(const uint4* __restrict__ wq,
+                                                           const uint16_t* __restrict__ ratio, int N, int K,
+                                                           int8_t* __restrict__ W8) {
+  const int nblk = K / BLK;
+  const long u = (long)blockIdx.x * 256 + threadIdx.x;  // unit index over the rows' (row, block) pairs
+  if (u >= (long)N * nblk) return;
+  const int n = (int)(u / nblk), b = (int)(u % nblk);
+  const long ix = panel_index(n, b, nblk);
+  const uint4 w = wq[ix];
+  const float r = h2f(ratio[ix]);
+  const v4u lo = requant_words_i8(w.x, w.y, r), hi = requant_words_i8(w.z, w.w, r);
+  uint4* dst = reinterpret_cast<uint4*>(W8 + (long)n * K + (long)b * BLK);
+  dst[0] = make_uint4(lo[0], lo[1], lo[2], lo[3]);
+  dst[1] = make_uint4(hi[0], hi[1], hi[2], hi[3]);
+}
+
 // ---- host-side launch policy ----------------------------------------------------
 // 256 x 256 tiles when they give >= 256 workgroups (one per CU), else
 // 128 x 256. W4A16 splits K until the grid has >= 240 workgroups, keeping
@@ -1232,6 +1251,18 @@ int q4_gemm_w8a8(const int8_t* A, const int8_t* W8, const float* sa, const void*
 size_t q4_w8_packed_bytes(int N, int K) {
   if (N <= 0 || K <= 0 || K % 32) return 0;
   return (size_t)ceil_div(N, 32) * 32 * w8p_kpad(K);
+}
+
+int q4_w4a8_weights(const uint32_t* wq, const uint16_t* ratio, int N, int K, int8_t* W8, void* stream) {
+  clear_error();
+  Q4_ARG(N > 0 && K > 0 && K % 32 == 0, "bad W4A8 weight shape N=%d K=%d (K must be a multiple of 32)", N, K);
+  Q4_ARG(wq && ratio && W8, "null pointer");
+  Q4_ARG(((uintptr_t)wq & 15) == 0 && ((uintptr_t)W8 & 15) == 0, "wq and W8 must be 16-byte aligned");
+  const long units = (long)N * (K / BLK);
+  hipLaunchKernelGGL(w4a8_weights_kernel, dim3((unsigned)ceil_div(units, 256)), dim3(256), 0, as_stream(stream),
+                     reinterpret_cast<const uint4*>(wq), ratio, N, K, W8);
+  Q4_LAUNCHED("w4a8_weights");
+  return Q4_OK;
 }
 
 int q4_w8_pack(const int8_t* W8, int N, int K, int8_t* W8p, void* stream) {

@@ -385,6 +385,16 @@ def gemm_w8a8_packed(A: torch.Tensor, W8p: torch.Tensor, sa: torch.Tensor, sw: t
     return (Y, Cm) if want_c else Y
 
 
+def w4a8_weights(wq: torch.Tensor, ratio: torch.Tensor, N: int, K: int) -> torch.Tensor:
+    """The int8 weights W4A8 forms on the fly, once: W8 [N][K] (pack with
+    :func:`w8_pack` and run :func:`gemm_w8a8_packed` for W4A8's results at
+    the W8A8 speed)."""
+    _check_int4(wq, ratio, N, K)
+    W8 = torch.empty((N, K), dtype=torch.int8, device=wq.device)
+    call("q4_w4a8_weights", _p(wq), _p(ratio), N, K, _p(W8), _stream())
+    return W8
+
+
 def gemm_w4a8(A: torch.Tensor, wq: torch.Tensor, ratio: torch.Tensor, sa: torch.Tensor, sw: torch.Tensor, N: int, *,
               want_c: bool = False, Y: torch.Tensor | None = None):
     M, K = A.shape

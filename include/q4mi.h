@@ -239,6 +239,16 @@ int q4_gemm_w4a8(const int8_t* A, const uint32_t* wq, const uint16_t* ratio,
                  const float* sa, const void* sw, int sw_dtype, uint16_t* Y,
                  int32_t* C, int M, int N, int K, void* stream);
 
+/* W4A8's int8 weights formed once instead of per M-tile: W8 [N][K] =
+ * int8(clamp(rint((q-8) * ratio[n,b]), -127, 127)), exactly the values
+ * q4_gemm_w4a8 forms on the fly (vk/coopgemm_w4a8.comp:28-34). With
+ * q4_w8_pack and q4_gemm_w8a8_packed this gives q4_gemm_w4a8's results bit
+ * for bit at the W8A8 speed, for callers that can hold the int8 weights
+ * (twice the int4 bytes; the reference's PREFILL_I8 path holds int8 weights
+ * too, src/vk_engine.py:152-157). */
+int q4_w4a8_weights(const uint32_t* wq, const uint16_t* ratio, int N, int K,
+                    int8_t* W8, void* stream);
+
 /* f32 <-> f16 staging casts around a prefill GEMM.
  * vk/cast_dn.comp:7, vk/cast_up.comp:7 (wired at src/vk_engine.py:398-400). */
 int q4_cast_f32_f16(const float* src, uint16_t* dst, size_t n, void* stream);

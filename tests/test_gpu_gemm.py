@@ -144,6 +144,30 @@ def test_w4a8_bit_exact(gpu, M, N, K):
     assert (to_np(gY).view(np.uint16) == Y.view(np.uint16)).all()
 
 
+@pytest.mark.parametrize("N,K", [(256, 64), (300, 256), (15360, 3840)])
+def test_w4a8_weights_once_then_w8a8_bit_identical(gpu, N, K):
+    """W4A8's int8 weights formed once (q4_w4a8_weights) equal the oracle's
+    requant bit for bit, and packed W8A8 on them gives q4_gemm_w4a8's Y and C
+    bit for bit."""
+    rng = np.random.default_rng(N + K + 7)
+    W = (rng.standard_normal((N, K)) * 0.08).astype(np.float32)
+    q, sc = O.quant_codes(W)
+    _, sw = O.w8_fold(q, sc)
+    ratio = O.w4a8_ratio(sc, sw)
+    wq = torch.from_numpy(O.pack_dev(q).view(np.int32)).cuda()
+    r = torch.from_numpy(O.scales_dev(ratio)).cuda()
+    W8 = gpu.w4a8_weights(wq, r, N, K)
+    assert (to_np(W8) == O.w4a8_weights(q, ratio)).all()
+    M = 128
+    X = (rng.standard_normal((M, K)) * 0.3).astype(np.float32)
+    A, sa = O.quant_act_i8(X)
+    tA, tsa = torch.from_numpy(A).cuda(), torch.from_numpy(sa).cuda()
+    sw16 = torch.from_numpy(sw.astype(np.float16)).cuda()
+    Y4, C4 = gpu.gemm_w4a8(tA, wq, r, tsa, sw16, N, want_c=True)
+    Y8, C8 = gpu.gemm_w8a8_packed(tA, gpu.w8_pack(W8), tsa, sw16, N, want_c=True)
+    assert torch.equal(C4, C8) and torch.equal(Y4, Y8)
+
+
 # ----------------------------------------------------------------- W4A16
 @pytest.mark.parametrize("M,N,K", [(64, 256, 32), (100, 320, 96), (40, 300, 224), (128, 3840, 15360),
                                    (512, 15360, 3840), (512, 3840, 15360), (1024, 8192, 256), (2048, 8192, 96)])
