@@ -313,32 +313,41 @@ pre_attn_kernel(const void* __restrict__ qin, int ldq, const float* __restrict__
 static int pa_rows(int hd) { return hd >= 512 ? PaGeom<512>::ROWS : PaGeom<256>::ROWS; }
 
 // out[m][h hd + i] = sum_c acc_c w_c / sum_c l_c w_c over the splits that
-// hold keys of token m, w_c = exp(max_c - max); fp32 or fp16 out.
+// hold keys of token m, w_c = exp(max_c - max); fp32 or fp16 out. A
+// workgroup of 256 threads merges 1024 / hd rows; each thread takes 4
+// consecutive elements of its row (16-byte loads of every split's
+// accumulator).
 template <int OT>
 __global__ void __launch_bounds__(256)
 pre_attn_merge_kernel(const float* __restrict__ ws, void* __restrict__ out, int ldo, int hd, int nH, int nsplit,
-                      int ksl, int stride, int window, const uint32_t* __restrict__ dyn) {
-  const int row = blockIdx.x, m = row / nH, h = row % nH, t = threadIdx.x;
+                      int ksl, int stride, int window, int rows, const uint32_t* __restrict__ dyn) {
+  const int tpr = hd / 4;  // threads per row
+  const int row = blockIdx.x * (256 / tpr) + threadIdx.x / tpr, i = 4 * (threadIdx.x % tpr);
+  if (row >= rows) return;
+  const int m = row / nH, h = row % nH;
   const int T = att_len(dyn[0] + (uint32_t)m, window, stride);
   const int ns = min((T + ksl - 1) / ksl, nsplit);
   const float* w = ws + (long)row * nsplit * (hd + 4);
   float mx = -INFINITY;
   for (int cc = 0; cc < ns; ++cc) mx = fmaxf(mx, w[(long)cc * (hd + 4)]);
   float L = 0.0f;
+  v4f a = v4f{0.0f, 0.0f, 0.0f, 0.0f};
   for (int cc = 0; cc < ns; ++cc) {
-    const float mc = w[(long)cc * (hd + 4)];
-    if (mc != -INFINITY) L = fmaf(w[(long)cc * (hd + 4) + 1], expf(mc - mx), L);
+    const float* wc = w + (long)cc * (hd + 4);
+    const float mc = wc[0];
+    if (mc == -INFINITY) continue;
+    const float e = expf(mc - mx);
+    L = fmaf(wc[1], e, L);
+    const v4f v = *reinterpret_cast<const v4f*>(wc + 4 + i);
+#pragma unroll
+    for (int k = 0; k < 4; ++k) a[k] = fmaf(v[k], e, a[k]);
   }
-  for (int i = t; i < hd; i += 256) {
-    float a = 0.0f;
-    for (int cc = 0; cc < ns; ++cc) {
-      const float mc = w[(long)cc * (hd + 4)];
-      if (mc != -INFINITY) a = fmaf(w[(long)cc * (hd + 4) + 4 + i], expf(mc - mx), a);
-    }
-    const float v = a / L;
-    const long oi = (long)m * ldo + (long)h * hd + i;
-    if constexpr (OT == Q4_DT_F16) reinterpret_cast<uint16_t*>(out)[oi] = f2h(v);
-    else reinterpret_cast<float*>(out)[oi] = v;
+  const long oi = (long)m * ldo + (long)h * hd + i;
+#pragma unroll
+  for (int k = 0; k < 4; ++k) {
+    const float v = a[k] / L;
+    if constexpr (OT == Q4_DT_F16) reinterpret_cast<uint16_t*>(out)[oi + k] = f2h(v);
+    else reinterpret_cast<float*>(out)[oi + k] = v;
   }
 }
 
@@ -406,12 +415,13 @@ int q4_pre_attn(const void* q, int q_dtype, int ldq, const float* qnw, const flo
   }
 #undef PA_LAUNCH
   Q4_LAUNCHED("pre_attn");
+  const int rows = M * nH, mgrid = ceil_div(rows, 256 / (hd / 4));
   if (out_dtype == Q4_DT_F16)
-    hipLaunchKernelGGL(pre_attn_merge_kernel<Q4_DT_F16>, dim3(M * nH), dim3(256), 0, st, w, out, ldo, hd, nH, ns,
-                       ksl, stride, window, dyn);
+    hipLaunchKernelGGL(pre_attn_merge_kernel<Q4_DT_F16>, dim3(mgrid), dim3(256), 0, st, w, out, ldo, hd, nH, ns, ksl,
+                       stride, window, rows, dyn);
   else
-    hipLaunchKernelGGL(pre_attn_merge_kernel<Q4_DT_F32>, dim3(M * nH), dim3(256), 0, st, w, out, ldo, hd, nH, ns,
-                       ksl, stride, window, dyn);
+    hipLaunchKernelGGL(pre_attn_merge_kernel<Q4_DT_F32>, dim3(mgrid), dim3(256), 0, st, w, out, ldo, hd, nH, ns, ksl,
+                       stride, window, rows, dyn);
   Q4_LAUNCHED("pre_attn_merge");
   return Q4_OK;
 }
