@@ -365,7 +365,8 @@ def bench_prefill(ops, reps: int = 5, p0: int = 3968):
             "weight_bytes": weight_bytes, "weight_GBps": round(weight_bytes / (ms * 1e-3) / 1e9, 1)}
 
 
-def bench_token_step(ops, steps: int, warmup: int, pos: int = 1023, fast: bool = False):
+def bench_token_step(ops, steps: int, warmup: int, pos: int = 1023, fast: bool = False,
+                     fuse_gemv: bool = True):
     """A whole decode token through the engine mirror (vk_engine.py): the
     reference's per-layer dispatch order (norm, q/k/v, prepkv, attention, o,
     normadd, norm, gate/up, gelumul, down, normadd) for 48 layers of the
@@ -376,7 +377,9 @@ def bench_token_step(ops, steps: int, warmup: int, pos: int = 1023, fast: bool =
     everywhere and one launch per reference dispatch (the reference's
     buffers); ``fast=True``: every normadd fused with the rmsnorm that
     follows it, gate/up interleaved with the gelumul in their GEMV's
-    epilogue, and fp16 GEMV inputs (the residual stream stays fp32)."""
+    epilogue, and fp16 GEMV inputs (the residual stream stays fp32); with
+    ``fuse_gemv`` too, each fused norm runs inside the q/k/v or gate/up GEMV
+    launch that reads it."""
     import importlib
 
     import numpy as np
@@ -435,7 +438,9 @@ def bench_token_step(ops, steps: int, warmup: int, pos: int = 1023, fast: bool =
     d_fin = E.normbg(B["h"], vec(H), B["normed_f"], DUH, out_dtype=xdt)
     d_lm = E.gemv_ds(qw(V, H), B["normed_f"], B["logits"], 0, x_dtype=xdt)
     B["h"].write(np.ones(H, np.float32))
-    graph = E.record_decode(layers, d_fin, d_lm, fuse=fast)
+    graph = E.record_decode(layers, d_fin, d_lm, fuse=fast, fuse_gemv=fuse_gemv)
+    # one launch per recorded descriptor, plus the split merge of every attention
+    launches = len(graph.seq) + sum(1 for op in graph.seq if getattr(op, "fn", None) in (ops.attn, ops.prepkv_attn))
     for _ in range(warmup):
         graph.launch()
     torch.cuda.synchronize()
@@ -457,11 +462,12 @@ def bench_token_step(ops, steps: int, warmup: int, pos: int = 1023, fast: bool =
     E.KEEP.clear()
     torch.cuda.empty_cache()
     return {"ms_per_token": round(ms, 4), "position": pos, "keys_attended": T,
-            "activations": ("fp32 residual stream, fp16 GEMV inputs, fused norms, gelumul in the gate/up GEMV"
+            "activations": (("fp32 residual stream, fp16 GEMV inputs, fused norms, gelumul in the gate/up GEMV"
+                             + (", norms inside the q/k/v and gate/up GEMV launches" if fuse_gemv else ""))
                             if fast else "fp32 (reference)"),
             "weight_bytes": wbytes, "kv_cache_bytes_read": kvbytes,
             "GBps": round((wbytes + kvbytes) / (ms * 1e-3) / 1e9, 1),
-            "kernels_per_token": LAYERS * (8 if fast else 12) + 2}
+            "kernels_per_token": launches}
 
 
 def counter_workload(ops):
@@ -681,7 +687,9 @@ def main():
     tok = None
     if not args.no_token:
         tok = {"reference_dispatches": bench_token_step(ops, max(20, args.steps // 4), 5),
-               "fused": bench_token_step(ops, max(20, args.steps // 4), 5, fast=True)}
+               "fused": bench_token_step(ops, max(20, args.steps // 4), 5, fast=True),
+               "fused_norm_launches": bench_token_step(ops, max(20, args.steps // 4), 5, fast=True,
+                                                       fuse_gemv=False)}
         print(f"[bench] token step {tok}", flush=True)
     single = {"c1_15360x3840_f16_scales": bench_gemv_single(ops, I, H, False),
               "c3_15360x3840_e4m3_scales": bench_gemv_single(ops, I, H, True),

@@ -41,6 +41,8 @@ SIGNATURES = {
     "q4_gemv_e4m3s": (_i, [_vp, _i, _vp, _vp, _f, _vp, _i, _i, _i, _i, _vp, _sz, _vp]),
     "q4_gemv_batch": (_i, [_vp, _i, _i, _i, _i, _i, _vp, _vp, _vp, _vp, _vp, _vp]),
     "q4_gemv_gated": (_i, [_vp, _i, _vp, _vp, _i, _f, _vp, _i, _i, _i, _i, _vp, _sz, _vp]),
+    "q4_gemv_normadd": (_i, [_vp, _vp, _vp, _vp, _f, _vp, _vp, _vp, _i, _f, _vp, _i, _i, _i, _i, _vp]),
+    "q4_gemv_batch_normadd": (_i, [_vp, _vp, _vp, _vp, _f, _vp, _i, _i, _i, _i, _vp, _vp, _vp, _vp, _vp, _vp]),
     "q4_pre_rmsnorm": (_i, [_vp, _vp, _vp, _i, _i, _i, _vp]),
     "q4_pre_normadd": (_i, [_vp, _i, _vp, _vp, _i, _i, _f, _vp]),
     "q4_pre_normadd_rmsnorm": (_i, [_vp, _i, _vp, _vp, _i, _i, _f, _vp, _vp, _i, _vp]),

@@ -31,9 +31,7 @@ constexpr int NORM_THREADS = 1024;
 constexpr int ATT_THREADS = 256;
 constexpr int ATT_CH = 64;        // keys per attention split (16 per wave)
 constexpr int ATT_MAX_HD = 512;   // head dims up to 512 (global layers)
-constexpr float NORM_EPS = 1e-6f;
 
-__device__ inline float inv_rms(float sumsq, int D) { return 1.0f / sqrtf(sumsq / (float)D + NORM_EPS); }
 
 // Sum over the workgroup, identical in every thread. red: blockDim/64 floats.
 __device__ inline float block_sum(float v, float* red) {

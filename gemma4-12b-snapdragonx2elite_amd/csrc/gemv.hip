@@ -156,6 +156,87 @@ __device__ inline int stage_words(int nb) {
   return GEMV_WAVES * nvw * 256 + (XT == Q4_DT_F16 ? GEMV_WAVES * nbw : 0);
 }
 
+// Fused input of a GEMV (the normadd and rmsnorm recorded before it,
+// vk/normadd.comp:8-12 then vk/rmsnorm.comp:8-12 on the new residual):
+//   h_out = (h + (a * inv_rms(a)) * w) * sc,   x = f16((h_out * inv_rms(h_out)) * w2)
+// over K = D elements. Every workgroup computes x itself (the GEMV's x is
+// never written to memory); workgroup 0 writes h_out, which must not alias
+// h or a (other workgroups may still be reading them).
+struct NormIn {
+  const float* a;
+  const float* w;
+  const float* h;
+  float* h_out;
+  const float* w2;
+  float sc;
+};
+constexpr int NX_PER = 4;                                    // 16-byte loads per thread per operand
+constexpr int NX_MAX_K = NX_PER * 4 * GEMV_THREADS;          // 4096 elements
+
+// Sum over the 4 waves of one 256-thread half, in a fixed order (slot: 4
+// floats of the half's own LDS).
+__device__ inline float half_sum(float v, float* slot) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
+  if ((threadIdx.x & 63) == 0) slot[(threadIdx.x >> 6) & (GEMV_WAVES - 1)] = v;
+  __syncthreads();
+  return ((slot[0] + slot[1]) + slot[2]) + slot[3];
+}
+
+// The normadd + rmsnorm of a NormIn on the operands this thread loaded
+// (elements 4 i4 .. 4 i4 + 3 for i4 = t + 256 r), the fp16 result written
+// straight into the per-wave x staging areas of gemv_rows (block j belongs
+// to wave (j mod S) / SW at local block (j / S) SW + j mod SW), then one
+// barrier. Arithmetic per element as normadd_kernel's. (Elements are
+// converted by value, __uint_as_float(v[c]): a bit cast of a vector element
+// lvalue inside an unrolled loop is compiled to element 0 every time.)
+template <int R>
+__device__ inline void nx_stage(const NormIn& nx, const v4u* na, const v4u* nh, const v4u* nw, const v4u* nw2,
+                                int nblk, int nvw, uint32_t* __restrict__ smem, float (*red)[R], bool writer) {
+  static_assert(R >= GEMV_WAVES, "reduction slots");
+  constexpr int SW = 64 / R, S = SW * GEMV_WAVES;
+  const int ht = threadIdx.x & (GEMV_THREADS - 1), D = nblk * BLK, K4 = D / 4;
+  float s = 0.0f;
+#pragma unroll
+  for (int r = 0; r < NX_PER; ++r) {
+    const bool ok = ht + GEMV_THREADS * r < K4;
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+      const float a = ok ? __uint_as_float(na[r][c]) : 0.0f;
+      s = fmaf(a, a, s);
+    }
+  }
+  const float inv = inv_rms(half_sum(s, red[0]), D);
+  float hv[NX_PER][4];
+  float s2 = 0.0f;
+#pragma unroll
+  for (int r = 0; r < NX_PER; ++r) {
+    const bool ok = ht + GEMV_THREADS * r < K4;
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+      const float a = __uint_as_float(na[r][c]), w = __uint_as_float(nw[r][c]);
+      const float v = __fmul_rn(__fadd_rn(__uint_as_float(nh[r][c]), __fmul_rn(__fmul_rn(a, inv), w)), nx.sc);
+      hv[r][c] = ok ? v : 0.0f;
+      s2 = fmaf(hv[r][c], hv[r][c], s2);
+    }
+  }
+  const float inv2 = inv_rms(half_sum(s2, red[1]), D);
+#pragma unroll
+  for (int r = 0; r < NX_PER; ++r) {
+    const int i4 = ht + GEMV_THREADS * r;
+    if (i4 < K4) {
+      uint32_t e[4];
+#pragma unroll
+      for (int c = 0; c < 4; ++c) e[c] = f2h(__fmul_rn(__fmul_rn(hv[r][c], inv2), __uint_as_float(nw2[r][c])));
+      const int j = i4 / (BLK / 4), lb = j / S * SW + j % SW;
+      uint32_t* dst = smem + ((j % S) / SW) * nvw * 256 + lb * 16 + (i4 % (BLK / 4)) * 2;
+      *reinterpret_cast<uint2*>(dst) = make_uint2(e[0] | (e[1] << 16), e[2] | (e[3] << 16));
+      if (writer) *reinterpret_cast<float4*>(nx.h_out + 4 * i4) = make_float4(hv[r][0], hv[r][1], hv[r][2], hv[r][3]);
+    }
+  }
+  __syncthreads();
+}
+
 // Rows [g*R, g*R + R) of one GEMV over the K slice s of split (the whole K
 // when split == 1). NP = row groups of the launch * R (split-K partial stride).
 //
@@ -166,12 +247,18 @@ __device__ inline int stage_words(int nb) {
 // barrier, (4) each unit is used as soon as it has landed and its registers
 // are refilled with the lane's unit U places further on, so every lane keeps
 // U units in flight until its last round.
-template <int R, int U, int XT, int ST, int YT>
+//
+// NX (fp16 x, split 1): x is not read from memory but formed from the
+// NormIn's operands, which are loaded in place of step (1) (before the
+// weights, so the same wait covers them) and turned into x in LDS after it.
+template <int R, int U, int XT, int ST, int YT, bool NX = false>
 __device__ __forceinline__ void gemv_rows(const void* __restrict__ xv, const uint4* __restrict__ wq,
                                           const void* __restrict__ scv, float outscale, void* __restrict__ yv,
                                           int N, int nblk, int g, int s, int split, long NP,
                                           float* __restrict__ part, uint32_t* __restrict__ cnt,
-                                          uint32_t* __restrict__ smem, float (*red)[R], int gated) {
+                                          uint32_t* __restrict__ smem, float (*red)[R], int gated,
+                                          NormIn nx = {}) {
+  static_assert(!NX || XT == Q4_DT_F16, "fused norm input is staged as fp16");
   constexpr bool XH = (XT == Q4_DT_F16);
   constexpr int SW = 64 / R;               // block slots per wave
   constexpr int S = SW * GEMV_WAVES;       // block slots per workgroup
@@ -195,7 +282,19 @@ __device__ __forceinline__ void gemv_rows(const void* __restrict__ xv, const uin
   const int nbw = (nb + S - 1) / S * SW;    // local blocks per wave (wave-uniform)
   const int nvw = (nbw + BPD - 1) / BPD;    // direct loads per wave
   uint32_t* xw = smem + wave * nvw * 256;
-  {
+  [[maybe_unused]] v4u na[NX ? NX_PER : 1], nh[NX ? NX_PER : 1], nw[NX ? NX_PER : 1], nw2[NX ? NX_PER : 1];
+  if constexpr (NX) {
+    // index clamped so every thread issues the same loads; elements past K are zeroed in nx_stage
+    const int ht = threadIdx.x & (GEMV_THREADS - 1), K4 = nblk * (BLK / 4);
+#pragma unroll
+    for (int v = 0; v < NX_PER; ++v) {
+      const long o = 4L * min(ht + GEMV_THREADS * v, K4 - 1);
+      na[v] = ld16(nx.a + o);
+      nh[v] = ld16(nx.h + o);
+      nw[v] = ld16(nx.w + o);
+      nw2[v] = ld16(nx.w2 + o);
+    }
+  } else {
     const uint8_t* xsrc = reinterpret_cast<const uint8_t*>(xv) + k0 * (XH ? 2 : 4);
     for (int v = 0; v < nvw; ++v) {
       const int lb = v * BPD + lane / CPB;
@@ -220,6 +319,16 @@ __device__ __forceinline__ void gemv_rows(const void* __restrict__ xv, const uin
   //     x the wave sums each of its blocks into its own LDS area. A wave's
   //     LDS operations execute in order: no barrier is needed.
   vmwait<2 * U>();
+  if constexpr (NX) {
+#pragma unroll
+    for (int v = 0; v < NX_PER; ++v) {
+      pin(na[v]);
+      pin(nh[v]);
+      pin(nw[v]);
+      pin(nw2[v]);
+    }
+    nx_stage<R>(nx, na, nh, nw, nw2, nblk, nvw, smem, red, blockIdx.x == 0 && threadIdx.x < GEMV_THREADS);
+  }
   const uint32_t* xs_h = xw;
   const float* xs_f = reinterpret_cast<const float*>(xw);
   float* xsum = reinterpret_cast<float*>(smem + GEMV_WAVES * nvw * 256) + wave * nbw;
@@ -621,37 +730,76 @@ struct GemvSegs {
   int count;
 };
 
-template <int R, int U, int XT, int ST, int YT>
-__global__ void __launch_bounds__(2 * GEMV_THREADS)
-gemv_batch_kernel(const void* __restrict__ xv, int nblk, const GemvSegs segs) {
-  extern __shared__ __attribute__((aligned(16))) uint32_t smem[];
-  __shared__ float red[2][GEMV_WAVES][R];
-  const int halves = blockDim.x / GEMV_THREADS, half = threadIdx.x / GEMV_THREADS;
-  const int g = xcd_major(blockIdx.x, gridDim.x) * halves + half;
-  // segment selection with compile-time indices only (the argument block
-  // stays in the kernarg segment; a dynamic index would copy it to scratch)
-  const uint4* wq = segs.s[0].wq;
-  const void* sc = segs.s[0].sc;
-  void* y = segs.s[0].y;
-  float os = segs.s[0].outscale;
-  int N = segs.s[0].N, g0 = 0;
+// The segment of row group g: its matrix, scales, output, scale factor,
+// rows, and its first row group g0. Compile-time indices only (the argument
+// block stays in the kernarg segment; a dynamic index would copy it to
+// scratch).
+struct SegSel {
+  const uint4* wq;
+  const void* sc;
+  void* y;
+  float os;
+  int N, g0;
+};
+__device__ inline SegSel select_seg(const GemvSegs& segs, int g) {
+  SegSel r{segs.s[0].wq, segs.s[0].sc, segs.s[0].y, segs.s[0].outscale, segs.s[0].N, 0};
 #pragma unroll
   for (int t = 1; t < Q4_GEMV_MAX_BATCH; ++t) {
-    if (t < segs.count && g >= segs.s[t - 1].g_end) {
-      wq = segs.s[t].wq;
-      sc = segs.s[t].sc;
-      y = segs.s[t].y;
-      os = segs.s[t].outscale;
-      N = segs.s[t].N;
-      g0 = segs.s[t - 1].g_end;
-    }
+    if (t < segs.count && g >= segs.s[t - 1].g_end)
+      r = SegSel{segs.s[t].wq, segs.s[t].sc, segs.s[t].y, segs.s[t].outscale, segs.s[t].N, segs.s[t - 1].g_end};
   }
-  gemv_rows<R, U, XT, ST, YT>(xv, wq, sc, os, y, N, nblk, g - g0, 0, 1, 0, nullptr, nullptr,
+  return r;
+}
+
+// Row group of this wave in a launch of 256-thread halves (halves = 1 or
+// 2 per workgroup, passed by the host: reading blockDim.x here is a vector
+// load from the dispatch's implicit arguments that the first weight loads
+// would wait behind). A wave lies in one half, so g is wave-uniform and the
+// segment selection stays in scalar registers.
+__device__ inline int wave_group(int halves) {
+  const int half = threadIdx.x / GEMV_THREADS;
+  return __builtin_amdgcn_readfirstlane(xcd_major(blockIdx.x, gridDim.x) * halves + half);
+}
+
+template <int R, int U, int XT, int ST, int YT>
+__global__ void __launch_bounds__(2 * GEMV_THREADS)
+gemv_batch_kernel(const void* __restrict__ xv, int nblk, const GemvSegs segs, int halves) {
+  extern __shared__ __attribute__((aligned(16))) uint32_t smem[];
+  __shared__ float red[2][GEMV_WAVES][R];
+  const int half = threadIdx.x / GEMV_THREADS;
+  const int g = wave_group(halves);
+  const SegSel q = select_seg(segs, g);
+  gemv_rows<R, U, XT, ST, YT>(xv, q.wq, q.sc, q.os, q.y, q.N, nblk, g - q.g0, 0, 1, 0, nullptr, nullptr,
                               smem + half * stage_words<R, XT>(nblk), red[half], 0);
 }
 
+// gemv_kernel and gemv_batch_kernel (split 1) with x formed from a NormIn
+// in every workgroup (see nx_stage).
+template <int R, int U, int ST, int YT>
+__global__ void __launch_bounds__(2 * GEMV_THREADS)
+gemv_nx_kernel(const NormIn nx, const uint4* __restrict__ wq, const void* __restrict__ scv, float outscale,
+               void* __restrict__ yv, int N, int nblk, int gated, int halves) {
+  extern __shared__ __attribute__((aligned(16))) uint32_t smem[];
+  __shared__ float red[2][GEMV_WAVES][R];
+  const int half = threadIdx.x / GEMV_THREADS;
+  const int g = wave_group(halves);
+  gemv_rows<R, U, Q4_DT_F16, ST, YT, true>(nullptr, wq, scv, outscale, yv, N, nblk, g, 0, 1, 0, nullptr, nullptr,
+                                           smem + half * stage_words<R, Q4_DT_F16>(nblk), red[half], gated, nx);
+}
+template <int R, int U, int ST, int YT>
+__global__ void __launch_bounds__(2 * GEMV_THREADS)
+gemv_batch_nx_kernel(const NormIn nx, int nblk, const GemvSegs segs, int halves) {
+  extern __shared__ __attribute__((aligned(16))) uint32_t smem[];
+  __shared__ float red[2][GEMV_WAVES][R];
+  const int half = threadIdx.x / GEMV_THREADS;
+  const int g = wave_group(halves);
+  const SegSel q = select_seg(segs, g);
+  gemv_rows<R, U, Q4_DT_F16, ST, YT, true>(nullptr, q.wq, q.sc, q.os, q.y, q.N, nblk, g - q.g0, 0, 1, 0, nullptr,
+                                           nullptr, smem + half * stage_words<R, Q4_DT_F16>(nblk), red[half], 0, nx);
+}
+
 typedef void (*gemv_fn)(const void*, const uint4*, const void*, float, void*, int, int, int, float*, uint32_t*, int);
-typedef void (*gemv_batch_fn)(const void*, int, const GemvSegs);
+typedef void (*gemv_batch_fn)(const void*, int, const GemvSegs, int);
 struct GemvFns {
   gemv_fn one;
   gemv_batch_fn many;
@@ -680,6 +828,34 @@ static GemvFns pick(int R, int U, int xt, int st, int yt) {
     case 32: return pick_u<32>(U, xt, st, yt);
     case 16: return pick_u<16>(U, xt, st, yt);
     default: return pick_u<8>(U, xt, st, yt);
+  }
+}
+
+typedef void (*gemv_nx_fn)(const NormIn, const uint4*, const void*, float, void*, int, int, int, int);
+typedef void (*gemv_batch_nx_fn)(const NormIn, int, const GemvSegs, int);
+struct GemvNxFns {
+  gemv_nx_fn one;
+  gemv_batch_nx_fn many;
+};
+template <int R, int U, int ST>
+static GemvNxFns pick_nx_y(int yt) {
+  if (yt == Q4_DT_F16) return {gemv_nx_kernel<R, U, ST, Q4_DT_F16>, gemv_batch_nx_kernel<R, U, ST, Q4_DT_F16>};
+  return {gemv_nx_kernel<R, U, ST, Q4_DT_F32>, gemv_batch_nx_kernel<R, U, ST, Q4_DT_F32>};
+}
+template <int R, int U>
+static GemvNxFns pick_nx_s(int st, int yt) {
+  return st == Q4_SCALE_E4M3 ? pick_nx_y<R, U, Q4_SCALE_E4M3>(yt) : pick_nx_y<R, U, Q4_SCALE_F16>(yt);
+}
+template <int R>
+static GemvNxFns pick_nx_u(int U, int st, int yt) {
+  return U == 4 ? pick_nx_s<R, 4>(st, yt) : pick_nx_s<R, 8>(st, yt);
+}
+static GemvNxFns pick_nx(int R, int U, int st, int yt) {
+  switch (R) {
+    case 64: return pick_nx_u<64>(U, st, yt);
+    case 32: return pick_nx_u<32>(U, st, yt);
+    case 16: return pick_nx_u<16>(U, st, yt);
+    default: return pick_nx_u<8>(U, st, yt);
   }
 }
 
@@ -861,11 +1037,33 @@ int q4_workspace_init(void* ws, size_t bytes, void* stream) {
   return Q4_OK;
 }
 
+// Checks of a NormIn over K elements: operands present and 16-byte aligned,
+// K within what one thread's loads cover, h_out apart from every operand.
+static int nx_check(const NormIn& nx, int K) {
+  Q4_ARG(nx.a && nx.w && nx.h && nx.h_out && nx.w2, "null norm operand");
+  Q4_ARG(K <= NX_MAX_K, "a GEMV with a fused norm input takes K <= %d (got %d)", NX_MAX_K, K);
+  const void* ops[5] = {nx.a, nx.w, nx.h, nx.h_out, nx.w2};
+  for (const void* p : ops) Q4_ARG(((uintptr_t)p & 15) == 0, "norm operands must be 16-byte aligned");
+  const uintptr_t o = (uintptr_t)nx.h_out, n = (uintptr_t)K * sizeof(float);
+  for (int i = 0; i < 5; ++i) {
+    if (i == 3) continue;
+    const uintptr_t p = (uintptr_t)ops[i];
+    Q4_ARG(o + n <= p || p + n <= o, "h_out must not overlap h, a, w or w2");
+  }
+  return Q4_OK;
+}
+
+// x (x_dtype) or, with nx, x formed from the NormIn (split 1).
 static int gemv_launch(const void* x, int x_dtype, const uint32_t* wq, const void* scales, int scale_fmt, float inv,
                        void* y, int y_dtype, int N, int K, int split, void* ws, size_t ws_size, void* stream,
-                       int gated) {
+                       int gated, const NormIn* nx = nullptr) {
   Q4_ARG(N > 0 && K > 0 && K % BLK == 0, "bad GEMV shape N=%d K=%d (K must be a positive multiple of 32)", N, K);
-  Q4_ARG(x && wq && scales && y, "null pointer");
+  Q4_ARG((x || nx) && wq && scales && y, "null pointer");
+  if (nx) {
+    x_dtype = Q4_DT_F16;
+    split = 1;
+    if (int e = nx_check(*nx, K)) return e;
+  }
   Q4_ARG(x_dtype == Q4_DT_F32 || x_dtype == Q4_DT_F16, "bad x dtype %d", x_dtype);
   Q4_ARG(y_dtype == Q4_DT_F32 || y_dtype == Q4_DT_F16, "bad y dtype %d", y_dtype);
   Q4_ARG(scale_fmt == Q4_SCALE_F16 || scale_fmt == Q4_SCALE_E4M3, "bad scale format %d", scale_fmt);
@@ -879,8 +1077,16 @@ static int gemv_launch(const void* x, int x_dtype, const uint32_t* wq, const voi
   uint32_t* cnt = pl.ws ? reinterpret_cast<uint32_t*>(ws) : nullptr;
   float* part = pl.ws ? reinterpret_cast<float*>(reinterpret_cast<char*>(ws) + GEMV_TICKET_BYTES) : nullptr;
   const float outscale = scale_fmt == Q4_SCALE_E4M3 ? inv * 256.0f : 1.0f;
-  gemv_fn fn = pick(pl.R, pl.U, x_dtype, scale_fmt, y_dtype).one;
   const int hv = pair_groups(groups, pl.split, pl.lds);
+  if (nx) {
+    Q4_ARG(pl.split == 1, "internal: fused-norm GEMV planned with split %d", pl.split);
+    hipLaunchKernelGGL(pick_nx(pl.R, pl.U, scale_fmt, y_dtype).one, dim3(groups / hv), dim3(GEMV_THREADS * hv),
+                       pl.lds * hv, as_stream(stream), *nx, reinterpret_cast<const uint4*>(wq), scales, outscale, y, N,
+                       K / BLK, gated, hv);
+    Q4_LAUNCHED("gemv_normadd");
+    return Q4_OK;
+  }
+  gemv_fn fn = pick(pl.R, pl.U, x_dtype, scale_fmt, y_dtype).one;
   hipLaunchKernelGGL(fn, dim3(groups / hv, pl.split), dim3(GEMV_THREADS * hv), pl.lds * hv, as_stream(stream), x,
                      reinterpret_cast<const uint4*>(wq), scales, outscale, y, N, K / BLK, pl.split, part, cnt, gated);
   Q4_LAUNCHED("gemv");
@@ -952,12 +1158,19 @@ int q4_gemv_multi(const void* x, int M, const uint32_t* wq, const void* scales, 
   return Q4_OK;
 }
 
-int q4_gemv_batch(const void* x, int x_dtype, int K, int scale_fmt, int y_dtype, int count,
-                  const uint32_t* const* wq, const void* const* scales, const float* inv, void* const* y,
-                  const int* N, void* stream) {
-  clear_error();
+}  // extern "C"
+
+// x (x_dtype) or, with nx, x formed from the NormIn.
+static int gemv_batch_launch(const void* x, int x_dtype, int K, int scale_fmt, int y_dtype, int count,
+                             const uint32_t* const* wq, const void* const* scales, const float* inv, void* const* y,
+                             const int* N, void* stream, const NormIn* nx) {
   Q4_ARG(count >= 1 && count <= Q4_GEMV_MAX_BATCH, "batch of %d GEMVs (1..%d)", count, Q4_GEMV_MAX_BATCH);
-  Q4_ARG(wq && scales && y && N && x, "null pointer");
+  Q4_ARG(wq && scales && y && N && (x || nx), "null pointer");
+  if (nx) {
+    x_dtype = Q4_DT_F16;
+    Q4_ARG(K > 0 && K % BLK == 0, "bad GEMV K=%d (a positive multiple of 32)", K);
+    if (int e = nx_check(*nx, K)) return e;
+  }
   Q4_ARG(K > 0 && K % BLK == 0 && (long)K <= (1L << 24), "bad GEMV K=%d (a positive multiple of 32)", K);
   Q4_ARG(x_dtype == Q4_DT_F32 || x_dtype == Q4_DT_F16, "bad x dtype %d", x_dtype);
   Q4_ARG(y_dtype == Q4_DT_F32 || y_dtype == Q4_DT_F16, "bad y dtype %d", y_dtype);
@@ -989,14 +1202,47 @@ int q4_gemv_batch(const void* x, int x_dtype, int K, int scale_fmt, int y_dtype,
     segs.s[i].g_end = groups;
   }
   const int U = units_in_flight(nblk, R, groups);
-  gemv_batch_fn fn = pick(R, U, x_dtype, scale_fmt, y_dtype).many;
   const size_t lds = x_stage_lds(nblk, x_dtype, R);
   const int hv = pair_groups(groups, 1, lds);
+  if (nx) {
+    hipLaunchKernelGGL(pick_nx(R, U, scale_fmt, y_dtype).many, dim3(groups / hv), dim3(GEMV_THREADS * hv), lds * hv,
+                       as_stream(stream), *nx, nblk, segs, hv);
+    Q4_LAUNCHED("gemv_batch_normadd");
+    return Q4_OK;
+  }
+  gemv_batch_fn fn = pick(R, U, x_dtype, scale_fmt, y_dtype).many;
   hipLaunchKernelGGL(fn, dim3(groups / hv), dim3(GEMV_THREADS * hv), lds * hv,
-                     as_stream(stream), x, nblk,
-                     segs);
+                     as_stream(stream), x, nblk, segs, hv);
   Q4_LAUNCHED("gemv_batch");
   return Q4_OK;
+}
+
+extern "C" {
+
+int q4_gemv_batch(const void* x, int x_dtype, int K, int scale_fmt, int y_dtype, int count,
+                  const uint32_t* const* wq, const void* const* scales, const float* inv, void* const* y,
+                  const int* N, void* stream) {
+  clear_error();
+  return gemv_batch_launch(x, x_dtype, K, scale_fmt, y_dtype, count, wq, scales, inv, y, N, stream, nullptr);
+}
+
+int q4_gemv_normadd(const float* a, const float* w, const float* h, float* h_out, float scale, const float* w2,
+                    const uint32_t* wq, const void* scales, int scale_fmt, float inv, void* y, int y_dtype, int N,
+                    int K, int gated, void* stream) {
+  clear_error();
+  Q4_ARG(!gated || (N > 0 && N % 2 == 0), "gated GEMV needs an even row count (interleaved gate/up rows), got N=%d",
+         N);
+  const NormIn nx{a, w, h, h_out, w2, scale == 0.0f ? 1.0f : scale};
+  return gemv_launch(nullptr, Q4_DT_F16, wq, scales, scale_fmt, inv, y, y_dtype, N, K, 1, nullptr, 0, stream,
+                     gated ? 1 : 0, &nx);
+}
+
+int q4_gemv_batch_normadd(const float* a, const float* w, const float* h, float* h_out, float scale, const float* w2,
+                          int K, int scale_fmt, int y_dtype, int count, const uint32_t* const* wq,
+                          const void* const* scales, const float* inv, void* const* y, const int* N, void* stream) {
+  clear_error();
+  const NormIn nx{a, w, h, h_out, w2, scale == 0.0f ? 1.0f : scale};
+  return gemv_batch_launch(nullptr, Q4_DT_F16, K, scale_fmt, y_dtype, count, wq, scales, inv, y, N, stream, &nx);
 }
 
 }  // extern "C"

@@ -224,4 +224,9 @@ __device__ __forceinline__ void static_for(F&& f) {
   }
 }
 
+// RMS norm factor 1 / sqrt(mean(x^2) + eps) from a sum of squares over D
+// elements (vk/rmsnorm.comp:8-12, vk/normadd.comp:8-12)
+constexpr float NORM_EPS = 1e-6f;
+__device__ inline float inv_rms(float sumsq, int D) { return 1.0f / sqrtf(sumsq / (float)D + NORM_EPS); }
+
 }  // namespace q4

@@ -302,6 +302,70 @@ def gemv_batch(x: torch.Tensor, mats, K: int, *, scale_fmt: int = SCALE_F16, y_d
     return ys
 
 
+GEMV_NORMADD_MAX_K = 4096
+
+
+def _norm_in(a, w, h, h_out, w2, K: int):
+    """Checks of the fused normadd + rmsnorm operands of a GEMV."""
+    for t, nm in ((a, "a"), (w, "w"), (h, "h"), (h_out, "h_out"), (w2, "w2")):
+        _f32(t, K, nm)
+    if K > GEMV_NORMADD_MAX_K:
+        raise ValueError(f"a GEMV with a fused norm input takes K <= {GEMV_NORMADD_MAX_K}, got {K}")
+    lo, hi = h_out.data_ptr(), h_out.data_ptr() + 4 * K
+    for t, nm in ((a, "a"), (w, "w"), (h, "h"), (w2, "w2")):
+        if t.data_ptr() < hi and lo < t.data_ptr() + 4 * K:
+            raise ValueError(f"h_out must not overlap {nm}")
+
+
+def gemv_normadd(a: torch.Tensor, w: torch.Tensor, h: torch.Tensor, h_out: torch.Tensor, w2: torch.Tensor,
+                 wq: torch.Tensor, scales: torch.Tensor, N: int, K: int, *, scale: float = 0.0,
+                 scale_fmt: int = SCALE_F16, inv: float = 1.0, y: torch.Tensor | None = None,
+                 y_dtype=torch.float32, gated: bool = False) -> torch.Tensor:
+    """:func:`normadd_rmsnorm` (fp16 norm output, into ``h_out`` instead of
+    ``h`` in place) and the GEMV (or, with ``gated``, :func:`gemv_gated`)
+    that reads its output, in one launch; returns ``y`` (``act`` when gated)."""
+    _norm_in(a, w, h, h_out, w2, K)
+    if gated and N % 2:
+        raise ValueError("gated GEMV needs an even row count")
+    rows = N // 2 if gated else N
+    if y is None:
+        y = torch.empty(rows, dtype=y_dtype, device=a.device)
+    _check_int4(wq, scales, N, K, 1 if scale_fmt == SCALE_E4M3 else 2)
+    _need(y, rows * y.element_size(), "y")
+    call("q4_gemv_normadd", _p(a), _p(w), _p(h), _p(h_out), C.c_float(scale), _p(w2), _p(wq), _p(scales),
+         scale_fmt, C.c_float(inv), _p(y), _dt(y), N, K, int(gated), _stream())
+    return y
+
+
+def gemv_batch_normadd(a: torch.Tensor, w: torch.Tensor, h: torch.Tensor, h_out: torch.Tensor, w2: torch.Tensor,
+                       mats, K: int, *, scale: float = 0.0, scale_fmt: int = SCALE_F16, y_dtype=torch.float32):
+    """:func:`gemv_batch` whose x is formed as in :func:`gemv_normadd`.
+    ``mats``: sequence of ``(wq, scales, N, y, inv)``; returns the outputs."""
+    _norm_in(a, w, h, h_out, w2, K)
+    n = len(mats)
+    if not 1 <= n <= GEMV_MAX_BATCH:
+        raise ValueError(f"gemv_batch_normadd takes 1..{GEMV_MAX_BATCH} matrices, got {n}")
+    ys = []
+    wqs, scs, yps = (C.c_void_p * n)(), (C.c_void_p * n)(), (C.c_void_p * n)()
+    Ns, invs = (C.c_int * n)(), (C.c_float * n)()
+    ydt = None
+    for i, (wq, sc, N, y, inv) in enumerate(mats):
+        if y is None:
+            y = torch.empty(N, dtype=y_dtype, device=a.device)
+        _check_int4(wq, sc, N, K, 1 if scale_fmt == SCALE_E4M3 else 2)
+        _need(y, N * y.element_size(), f"y of batch entry {i}")
+        if ydt is None:
+            ydt = _dt(y)
+        elif _dt(y) != ydt:
+            raise ValueError("all outputs of a GEMV batch must share one dtype")
+        wqs[i], scs[i], yps[i] = _p(wq), _p(sc), _p(y)
+        Ns[i], invs[i] = int(N), float(inv if inv is not None else 1.0)
+        ys.append(y)
+    call("q4_gemv_batch_normadd", _p(a), _p(w), _p(h), _p(h_out), C.c_float(scale), _p(w2), K, scale_fmt, ydt, n,
+         wqs, scs, invs, yps, Ns, _stream())
+    return ys
+
+
 # ------------------------------------------------------------------ GEMMs
 def gemm_w4a16(X: torch.Tensor, wq: torch.Tensor, sc16: torch.Tensor, N: int, Y: torch.Tensor | None = None,
                ws: torch.Tensor | None = None):

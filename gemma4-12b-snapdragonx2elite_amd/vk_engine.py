@@ -555,7 +555,7 @@ def record(body) -> ops.Graph:
     return g
 
 
-def record_decode(layers, d_fin: OpDesc, d_lm: GemvDesc, fuse: bool = True) -> ops.Graph:
+def record_decode(layers, d_fin: OpDesc, d_lm: GemvDesc, fuse: bool = True, fuse_gemv: bool = True) -> ops.Graph:
     """Record one decode token in the reference's dispatch order
     (src/vk_engine.py:274-287): per layer norm, q/k/v (one batched launch),
     prepkv, attention, o, normadd, norm, gate/up (one launch), gelumul,
@@ -571,7 +571,10 @@ def record_decode(layers, d_fin: OpDesc, d_lm: GemvDesc, fuse: bool = True) -> o
     a layer's last normadd and the next layer's input norm or the final
     norm) runs as one :func:`ops.normadd_rmsnorm` launch, and prepkv with
     the attention after it as :func:`ops.prepkv_attn`: three launches fewer
-    per layer, same arithmetic."""
+    per layer, same arithmetic. With ``fuse_gemv`` too, each such fused
+    norm with an fp16 output runs inside the GEMV launch that reads it
+    (q/k/v, gate/up; :func:`ops.gemv_batch_normadd`, :func:`ops.gemv_normadd`),
+    two launches fewer per layer."""
     seq = []
     for L in layers:
         seq += [L["d_in"], ("gemvs", [L["d_q"], L["d_k"]] + ([L["d_v"]] if L.get("d_v") is not None else [])),
@@ -581,14 +584,100 @@ def record_decode(layers, d_fin: OpDesc, d_lm: GemvDesc, fuse: bool = True) -> o
     seq += [d_fin, ("gemvs", [d_lm])]
     if fuse:
         seq = _fuse_norms(seq)
+        if fuse_gemv:
+            seq = _fuse_norm_gemvs(seq)
 
     def body():
         for op in seq:
             if isinstance(op, tuple) and op and op[0] == "gemvs":
                 gemv_many(op[1])
+            elif isinstance(op, tuple) and op and op[0] == "gemvs_nx":
+                a, w, h, h_out, w2, sc = op[1]
+                d0 = op[2][0].dp
+                ops.gemv_batch_normadd(a, w, h, h_out, w2, [(d.dp[1], d.dp[2], d.dp[6], d.dp[5], d.dp[4])
+                                                            for d in op[2]], d0[7], scale=sc, scale_fmt=d0[3])
             else:
                 disp(op)
-    return record(body)
+    g = record(body)
+    g.seq = seq          # the recorded descriptor sequence, for inspection
+    return g
+
+
+# GEMVs this tall keep their own norm launch: every workgroup of a fused
+# launch forms the whole x, which a grid of thousands of workgroups (lm_head)
+# would repeat thousands of times.
+_NX_MAX_ROWS = 65536
+
+
+def _copy_into(dst: torch.Tensor, src: torch.Tensor) -> None:
+    dst.copy_(src)
+
+
+def _aligned(*ts) -> bool:
+    return all(t.data_ptr() % 16 == 0 for t in ts)
+
+
+def _fuse_norm_gemvs(seq):
+    """A :func:`ops.normadd_rmsnorm` with an fp16 output and the GEMV launch
+    after it that reads that output (a ``("gemvs", descs)`` group or a gated
+    gate/up descriptor) become one launch. The norm output is read by that
+    launch only (src/vk_engine.py:231-234, 243-244: the norm buffer is
+    rewritten before its next use). The fused launch writes the new residual
+    to a second buffer (other workgroups still read the old one), so the
+    residual alternates between its buffer and a twin; later descriptors
+    that use the residual are pointed at the buffer that holds it, and a
+    copy at the end puts it back where the reference keeps it."""
+    out, cur, home = [], {}, {}
+    twin: dict = {}
+
+    def sub(t):
+        return cur.get(t.data_ptr(), t) if isinstance(t, torch.Tensor) else t
+
+    i = 0
+    while i < len(seq):
+        a = seq[i]
+        b = seq[i + 1] if i + 1 < len(seq) else None
+        fused = None
+        if isinstance(a, OpDesc) and a.fn is ops.normadd_rmsnorm:
+            x, w, h, w2, sc, y = a.args
+            D = x.numel()
+            h_in = sub(h)
+            ok = (y.dtype == torch.float16 and D <= ops.GEMV_NORMADD_MAX_K and _aligned(x, w, h, w2)
+                  and y.data_ptr() not in cur)
+            if ok and isinstance(b, tuple) and b and b[0] == "gemvs":
+                ds = b[1]
+                d0 = ds[0].dp
+                if (len(ds) <= ops.GEMV_MAX_BATCH and sum(d.dp[6] for d in ds) <= _NX_MAX_ROWS
+                        and all(d.dp[0].data_ptr() == y.data_ptr() and d.dp[0].dtype == torch.float16
+                                and d.dp[7] == D and d.dp[3] == d0[3] and d.dp[5].dtype == d0[5].dtype for d in ds)):
+                    fused = lambda h_out: ("gemvs_nx", (x, w, h_in, h_out, w2, sc), ds)  # noqa: E731
+            elif (ok and isinstance(b, OpDesc) and b.fn is ops.gemv_gated and b.args[0].data_ptr() == y.data_ptr()
+                  and b.args[4] == D and b.args[3] <= _NX_MAX_ROWS):
+                _x, wo, so, N, K = b.args
+                kw = b.kw
+                fused = lambda h_out: OpDesc(ops.gemv_normadd, (x, w, h_in, h_out, w2, wo, so, N, K),  # noqa: E731
+                                             dict(scale=sc, scale_fmt=kw["scale_fmt"], inv=kw["inv"], y=kw["act"],
+                                                  gated=True))
+            if fused is not None:
+                key = h.data_ptr()
+                home.setdefault(key, h)
+                if key not in twin:
+                    twin[key] = torch.empty_like(h)
+                    KEEP.append(twin[key])
+                h_out = twin[key] if h_in.data_ptr() == key else home[key]
+                out.append(fused(h_out))
+                cur[key] = h_out
+                if h_out.data_ptr() == key:
+                    del cur[key]
+                i += 2
+                continue
+        if isinstance(a, OpDesc):
+            a = OpDesc(a.fn, tuple(sub(t) for t in a.args), {k: sub(v) for k, v in a.kw.items()})
+        out.append(a)
+        i += 1
+    for key, t in cur.items():
+        out.append(OpDesc(_copy_into, (home[key], t), {}))
+    return out
 
 
 def _fuse_norms(seq):

@@ -165,6 +165,29 @@ int q4_gemv_batch(const void* x, int x_dtype, int K, int scale_fmt,
                   const void* const* scales, const float* inv,
                   void* const* y, const int* N, void* stream);
 
+/* The normadd and rmsnorm recorded before a decode GEMV, fused into its
+ * launch: h_out = (h + rmsnorm(a) * w) * scale (scale 0: unscaled) as
+ * q4_normadd, then x = fp16(rmsnorm(h_out) * w2) as q4_rmsnorm, and y = the
+ * GEMV of x (q4_gemv's arithmetic with fp16 x, split 1; gated as
+ * q4_gemv_gated). Replaces the d_na / d_nas normadd followed by the norm
+ * and the GEMV(s) that read it (src/vk_engine.py:242-243 -> :284,
+ * :248-249 -> the next layer's :231-234). Every workgroup forms x itself;
+ * x is never written to memory. h_out is a separate buffer (it may not
+ * overlap h, a, w or w2): callers alternate two residual buffers. a, w, h,
+ * h_out and w2 are fp32 [K], 16-byte aligned; K <= 4096. The norm sums
+ * are reduced in another order than q4_normadd_rmsnorm's, so h_out and x
+ * may differ from the two-launch sequence in the last bits. */
+int q4_gemv_normadd(const float* a, const float* w, const float* h, float* h_out, float scale,
+                    const float* w2, const uint32_t* wq, const void* scales, int scale_fmt,
+                    float inv, void* y, int y_dtype, int N, int K, int gated, void* stream);
+
+/* q4_gemv_batch with x formed as in q4_gemv_normadd (q/k/v after the
+ * previous layer's closing normadd and this layer's input norm). */
+int q4_gemv_batch_normadd(const float* a, const float* w, const float* h, float* h_out,
+                          float scale, const float* w2, int K, int scale_fmt, int y_dtype,
+                          int count, const uint32_t* const* wq, const void* const* scales,
+                          const float* inv, void* const* y, const int* N, void* stream);
+
 /* Several activation vectors through one matrix: Y[m][n] = (GEMV of x_m)
  * for m < M, x fp16 [M][K] (row-major), Y y_dtype [M][N], with the decode
  * GEMV's arithmetic (exact (q - 8) x products summed per block in fp32,

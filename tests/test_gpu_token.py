@@ -32,13 +32,16 @@ def _rope(pos, hd):
     return (np.concatenate([np.cos(ang)] * 2).astype(np.float32), np.concatenate([np.sin(ang)] * 2).astype(np.float32))
 
 
-@pytest.mark.parametrize("fuse,half,gated", [(False, False, False), (True, False, False), (True, True, False),
-                                             (True, True, True), (False, False, True)])
-def test_decode_token_through_the_engine_mirror(g4, gpu, fuse, half, gated):
+@pytest.mark.parametrize("fuse,half,gated,fg", [(False, False, False, False), (True, False, False, True),
+                                                (True, True, False, False), (True, True, False, True),
+                                                (True, True, True, False), (True, True, True, True),
+                                                (False, False, True, False)])
+def test_decode_token_through_the_engine_mirror(g4, gpu, fuse, half, gated, fg):
     """fuse: normadd + next rmsnorm as one launch; half: fp16 GEMV inputs
     (norm, gelumul and attention write fp16, the residual stream stays
     fp32): the oracle rounds the same GEMV inputs to fp16; gated: gate/up
-    interleaved with the gelumul in the GEMV epilogue."""
+    interleaved with the gelumul in the GEMV epilogue; fg: the fused norms
+    with fp16 outputs inside the GEMV launches that read them."""
     E = importlib.import_module("g4mi.vk_engine")
     xdt = torch.float16 if half else torch.float32
     rx = (lambda v: np.asarray(v).astype(np.float16).astype(np.float64)) if half else (lambda v: v)
@@ -104,7 +107,12 @@ def test_decode_token_through_the_engine_mirror(g4, gpu, fuse, half, gated):
     finw = f32(rng.random(H) + 0.5)
     d_fin = E.normbg(B["h"], wbuf(finw), B["normed_f"], DUH, out_dtype=xdt)
     d_lm = E.gemv_ds(lm[:2], B["normed_f"], B["logits"], 0, x_dtype=xdt)
-    graph = E.record_decode(layers, d_fin, d_lm, fuse=fuse)
+    graph = E.record_decode(layers, d_fin, d_lm, fuse=fuse, fuse_gemv=fg)
+    n_nx = sum(1 for op in graph.seq if (isinstance(op, tuple) and op[0] == "gemvs_nx")
+               or getattr(op, "fn", None) is gpu.gemv_normadd)
+    # per layer: the gate/up GEMV(s) and the next layer's q/k/v or (last layer) the 1024-row lm_head
+    assert n_nx == (2 * len(layers) if (fuse and half and fg) else 0)
+    print(f"token fuse={fuse} half={half} gated={gated} fg={fg}: {n_nx} fused norm GEMVs", flush=True)
 
     gv = lambda qs, x: O.gemv_ref(qs[0], qs[1], x).astype(np.float64)
     for pos in range(20):
