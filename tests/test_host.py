@@ -81,3 +81,51 @@ def test_split_matches_library(ops, g4):
         assert 1 <= s <= K // 32
         ws = ops.Workspace.bytes_for(N, K)
         assert (ws == 0) == (s == 1)
+
+
+def test_norm_gemv_fusion_alternates_the_residual(g4):
+    """The recorder's norm-into-GEMV pass on CPU tensors (no launch): each
+    fused launch reads the buffer that holds the residual and writes the
+    other one, later descriptors that use the residual follow it, an fp32
+    norm output or an lm_head-sized GEMV stays unfused, and a final copy
+    puts the residual back in its own buffer when the count is odd."""
+    import torch
+
+    E = importlib.import_module("g4mi.vk_engine")
+    ops = importlib.import_module("g4mi.ops")
+    D = 256
+    f32 = lambda: torch.zeros(D, dtype=torch.float32)  # noqa: E731
+    h, x, w, w2 = f32(), f32(), f32(), f32()
+    y16 = torch.zeros(D, dtype=torch.float16)
+    y32 = f32()
+
+    def gemv_desc(xin, N):
+        dp = (xin, None, None, ops.SCALE_F16, 1.0, torch.zeros(N), N, D, 1, None)
+        return E.GemvDesc(dp, None, N, 1, (N + 63) // 64)
+
+    na = lambda y: E.OpDesc(ops.normadd_rmsnorm, (x, w, h, w2, 0.0, y), {})  # noqa: E731
+    seq = [na(y16), ("gemvs", [gemv_desc(y16, 512), gemv_desc(y16, 256)]),
+           E.OpDesc(ops.normadd, (x, w, h, 0.5), {}),
+           na(y32), ("gemvs", [gemv_desc(y32, 512)]),
+           na(y16), ("gemvs", [gemv_desc(y16, 262144)])]
+    out = E._fuse_norm_gemvs(seq)
+    assert out[0][0] == "gemvs_nx"
+    a, ww, h_in, h_out, ww2, sc = out[0][1]
+    assert h_in.data_ptr() == h.data_ptr() and h_out.data_ptr() != h.data_ptr() and h_out.numel() == D
+    twin = h_out
+    # the unfused normadd and the fp32-output norm now act on the twin
+    assert out[1].fn is ops.normadd and out[1].args[2].data_ptr() == twin.data_ptr()
+    assert out[2].fn is ops.normadd_rmsnorm and out[2].args[2].data_ptr() == twin.data_ptr()
+    assert out[3][0] == "gemvs"
+    # lm_head-sized GEMV: its norm stays a launch of its own, on the twin
+    assert out[4].fn is ops.normadd_rmsnorm and out[4].args[2].data_ptr() == twin.data_ptr()
+    assert out[5][0] == "gemvs"
+    # one fused launch: the residual is copied back into h at the end
+    assert out[6].fn is E._copy_into and out[6].args[0].data_ptr() == h.data_ptr()
+    assert out[6].args[1].data_ptr() == twin.data_ptr() and len(out) == 7
+    # two fused launches: back in h, no copy
+    seq2 = [na(y16), ("gemvs", [gemv_desc(y16, 512)]), na(y16), ("gemvs", [gemv_desc(y16, 512)])]
+    out2 = E._fuse_norm_gemvs(seq2)
+    assert [op[0] for op in out2] == ["gemvs_nx", "gemvs_nx"]
+    assert out2[1][1][2].data_ptr() == out2[0][1][3].data_ptr()      # second reads what the first wrote
+    assert out2[1][1][3].data_ptr() == h.data_ptr()
