@@ -1053,6 +1053,19 @@ static int nx_check(const NormIn& nx, int K) {
   return Q4_OK;
 }
 
+// An output y of y_bytes of a norm-fused GEMV apart from every norm operand
+// and h_out: workgroups that finish early write y while others still read
+// a and h, and workgroup 0 writes h_out.
+static int nx_check_y(const NormIn& nx, int K, const void* y, size_t y_bytes) {
+  const void* ops[5] = {nx.a, nx.w, nx.h, nx.h_out, nx.w2};
+  const uintptr_t yo = (uintptr_t)y, n = (uintptr_t)K * sizeof(float);
+  for (const void* q : ops) {
+    const uintptr_t p = (uintptr_t)q;
+    Q4_ARG(yo + y_bytes <= p || p + n <= yo, "y must not overlap a, w, h, h_out or w2 of a fused norm input");
+  }
+  return Q4_OK;
+}
+
 // x (x_dtype) or, with nx, x formed from the NormIn (split 1).
 static int gemv_launch(const void* x, int x_dtype, const uint32_t* wq, const void* scales, int scale_fmt, float inv,
                        void* y, int y_dtype, int N, int K, int split, void* ws, size_t ws_size, void* stream,
@@ -1063,6 +1076,9 @@ static int gemv_launch(const void* x, int x_dtype, const uint32_t* wq, const voi
     x_dtype = Q4_DT_F16;
     split = 1;
     if (int e = nx_check(*nx, K)) return e;
+    Q4_ARG(N > 0 && (y_dtype == Q4_DT_F32 || y_dtype == Q4_DT_F16), "bad GEMV rows N=%d or y dtype %d", N, y_dtype);
+    const size_t rows = gated ? (size_t)N / 2 : (size_t)N;
+    if (int e = nx_check_y(*nx, K, y, rows * (y_dtype == Q4_DT_F16 ? 2 : 4))) return e;
   }
   Q4_ARG(x_dtype == Q4_DT_F32 || x_dtype == Q4_DT_F16, "bad x dtype %d", x_dtype);
   Q4_ARG(y_dtype == Q4_DT_F32 || y_dtype == Q4_DT_F16, "bad y dtype %d", y_dtype);
@@ -1187,6 +1203,11 @@ static int gemv_batch_launch(const void* x, int x_dtype, int K, int scale_fmt, i
     NP += pad_rows(N[i]);
   }
   Q4_ARG(NP <= (1L << 30), "batched GEMV too large");
+  if (nx) {
+    Q4_ARG(y_dtype == Q4_DT_F32 || y_dtype == Q4_DT_F16, "bad y dtype %d", y_dtype);
+    for (int i = 0; i < count; ++i)
+      if (int e = nx_check_y(*nx, K, y[i], (size_t)N[i] * (y_dtype == Q4_DT_F16 ? 2 : 4))) return e;
+  }
   const int R = rows_per_group((int)NP);
   GemvSegs segs;
   memset(&segs, 0, sizeof(segs));

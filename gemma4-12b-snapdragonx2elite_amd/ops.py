@@ -317,6 +317,15 @@ def _norm_in(a, w, h, h_out, w2, K: int):
             raise ValueError(f"h_out must not overlap {nm}")
 
 
+def _norm_out(y, nbytes: int, a, w, h, h_out, w2, K: int) -> None:
+    """A fused-norm GEMV's output must not overlap its norm operands or h_out:
+    early workgroups write y while later ones still read a and h."""
+    lo, hi = y.data_ptr(), y.data_ptr() + nbytes
+    for t, nm in ((a, "a"), (w, "w"), (h, "h"), (h_out, "h_out"), (w2, "w2")):
+        if t.data_ptr() < hi and lo < t.data_ptr() + 4 * K:
+            raise ValueError(f"y must not overlap {nm}")
+
+
 def gemv_normadd(a: torch.Tensor, w: torch.Tensor, h: torch.Tensor, h_out: torch.Tensor, w2: torch.Tensor,
                  wq: torch.Tensor, scales: torch.Tensor, N: int, K: int, *, scale: float = 0.0,
                  scale_fmt: int = SCALE_F16, inv: float = 1.0, y: torch.Tensor | None = None,
@@ -332,6 +341,7 @@ def gemv_normadd(a: torch.Tensor, w: torch.Tensor, h: torch.Tensor, h_out: torch
         y = torch.empty(rows, dtype=y_dtype, device=a.device)
     _check_int4(wq, scales, N, K, 1 if scale_fmt == SCALE_E4M3 else 2)
     _need(y, rows * y.element_size(), "y")
+    _norm_out(y, rows * y.element_size(), a, w, h, h_out, w2, K)
     call("q4_gemv_normadd", _p(a), _p(w), _p(h), _p(h_out), C.c_float(scale), _p(w2), _p(wq), _p(scales),
          scale_fmt, C.c_float(inv), _p(y), _dt(y), N, K, int(gated), _stream())
     return y
@@ -354,6 +364,7 @@ def gemv_batch_normadd(a: torch.Tensor, w: torch.Tensor, h: torch.Tensor, h_out:
             y = torch.empty(N, dtype=y_dtype, device=a.device)
         _check_int4(wq, sc, N, K, 1 if scale_fmt == SCALE_E4M3 else 2)
         _need(y, N * y.element_size(), f"y of batch entry {i}")
+        _norm_out(y, N * y.element_size(), a, w, h, h_out, w2, K)
         if ydt is None:
             ydt = _dt(y)
         elif _dt(y) != ydt:

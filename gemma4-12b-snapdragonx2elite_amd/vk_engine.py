@@ -190,7 +190,9 @@ def load_quant(path, device="cuda") -> dict:
             if name == "format":
                 continue
             m = json.loads(js)
-            N, K = m["N"], m["K"]
+            N, K = int(m["N"]), int(m["K"])
+            if N <= 0 or K <= 0 or K % BLK or int(m["nblk"]) != K // BLK:
+                raise ValueError(f"{path}: matrix {name!r} has a bad shape N={N} K={K} nblk={m['nblk']}")
             get = lambda k: Buf(tensor=f.get_tensor(f"{name}.{k}").to(device)) if f"{name}.{k}" in keys else None
             bw, bs16 = get("wq"), get("sc16")
             if bw is None or bs16 is None:
@@ -201,8 +203,14 @@ def load_quant(path, device="cuda") -> dict:
             bs = get("sc8") if m["e4m3"] else bs16
             if bs is None:
                 raise ValueError(f"{path}: matrix {name!r} lacks its e4m3 scales")
-            out[name] = (QW(bw, bs, int(m["split"]), int(m["nblk"]), float(m["inv"]), bs16, get("w8"), get("sw8")),
-                         (N, K))
+            if m["e4m3"] and (bs.size != se or bs.t.dtype != torch.uint8):
+                raise ValueError(f"{path}: matrix {name!r} has e4m3 scales of the wrong size for {N}x{K}")
+            w8, sw8 = get("w8"), get("sw8")
+            if (w8 is None) != (sw8 is None):
+                raise ValueError(f"{path}: matrix {name!r} has only one of its int8 weights and row scales")
+            if w8 is not None and (w8.size != int(ops.lib().q4_w8_packed_bytes(N, K)) or sw8.size != 2 * N):
+                raise ValueError(f"{path}: matrix {name!r} has int8 weights of the wrong size for {N}x{K}")
+            out[name] = (QW(bw, bs, int(m["split"]), int(m["nblk"]), float(m["inv"]), bs16, w8, sw8), (N, K))
     return out
 
 

@@ -3,6 +3,7 @@
 normadd and rmsnorm, then the fp32 GEMV of the fp16-rounded norm output)
 and against the two-launch sequence they replace (q4_normadd_rmsnorm, then
 q4_gemv / q4_gemv_batch / q4_gemv_gated)."""
+import ctypes as C
 import os
 
 import numpy as np
@@ -133,4 +134,62 @@ def test_gemv_normadd_rejects_bad_operands(gpu):
     rc = lib.q4_gemv_normadd(a.data_ptr(), w.data_ptr(), h.data_ptr(), a.data_ptr() + 16, 0.0, w2.data_ptr(),
                              wq.data_ptr(), sc.data_ptr(), 0, 1.0, h.data_ptr(), 0, N, K, 0, None)
     assert rc == _lib.Q4_ERR_ARG and b"overlap" in lib.q4_last_error()
+    # y may not overlap a norm operand or h_out (early workgroups write y while others read them)
+    h_out = torch.empty_like(h)
+    for tgt, nm in ((a, "a"), (h, "h"), (w, "w"), (w2, "w2"), (h_out, "h_out")):
+        with pytest.raises(ValueError, match=f"y must not overlap {nm}"):
+            gpu.gemv_normadd(a, w, h, h_out, w2, wq, sc, N, K, y=tgt)
+        rc = lib.q4_gemv_normadd(a.data_ptr(), w.data_ptr(), h.data_ptr(), h_out.data_ptr(), 0.0, w2.data_ptr(),
+                                 wq.data_ptr(), sc.data_ptr(), 0, 1.0, tgt.data_ptr() + 8, 0, N, K, 0, None)
+        assert rc == _lib.Q4_ERR_ARG and b"y must not overlap" in lib.q4_last_error()
+    with pytest.raises(ValueError, match="y must not overlap h"):
+        gpu.gemv_batch_normadd(a, w, h, h_out, w2, [(wq, sc, N, None, None), (wq, sc, N, h[32:], None)], K)
+    ys = (C.c_void_p * 2)(h_out.data_ptr() + 4 * K, h.data_ptr())
+    ptrs = (C.c_void_p * 2)(wq.data_ptr(), wq.data_ptr())
+    scs = (C.c_void_p * 2)(sc.data_ptr(), sc.data_ptr())
+    Ns = (C.c_int * 2)(N, N)
+    tmp = torch.empty(4 * K, dtype=torch.float32, device="cuda")
+    ys[0] = tmp.data_ptr()
+    rc = lib.q4_gemv_batch_normadd(a.data_ptr(), w.data_ptr(), h.data_ptr(), h_out.data_ptr(), 0.0, w2.data_ptr(),
+                                   K, 0, 0, 2, ptrs, scs, None, ys, Ns, None)
+    assert rc == _lib.Q4_ERR_ARG and b"y must not overlap" in lib.q4_last_error()
     torch.cuda.synchronize()
+
+
+@pytest.mark.parametrize("pair", ["0", "1"])
+@pytest.mark.parametrize("gated", [False, True])
+def test_gemv_normadd_rows64(gpu, pair, gated, monkeypatch):
+    """64 rows per workgroup: one block slot per wave in nx_stage's LDS mapping,
+    the plan the real gate/up launch (30720 x 3840, gated, paired) takes."""
+    monkeypatch.setenv("Q4MI_GEMV_PAIR", pair)
+    K, I = 3840, 15360 if gated else 2048
+    N = 2 * I if gated else 4096
+    if not gated:
+        monkeypatch.setenv("Q4MI_GEMV_ROWS", "64")
+    print(f"gemv_normadd rows64 N={N} gated={gated} pair={pair}", flush=True)
+    rng = np.random.default_rng(21 + int(gated))
+    a, h, w, w2 = _norm_inputs(rng, K)
+    ta, th, tw, tw2 = _cuda(a, h, w, w2)
+    hn, xr = _oracle_x(a, w, h, w2, 0.0)
+    h_out = torch.empty_like(th)
+    if gated:
+        qg, sg = synth_int4(rng, I, K)
+        qu, su = synth_int4(rng, I, K)
+        wg, scg = upload_int4(qg, sg)
+        wu, scu = upload_int4(qu, su)
+        wo, so = gpu.interleave_rows(wg, scg, wu, scu, I, K)
+        y = gpu.gemv_normadd(ta, tw, th, h_out, tw2, wo, so, N, K, y_dtype=torch.float16, gated=True)
+        ref = D.gelumul_ref(O.gemv_ref(qg, sg, xr), O.gemv_ref(qu, su, xr))
+        xn = gpu.normadd_rmsnorm(ta, tw, th.clone(), tw2, 0.0, y_dtype=torch.float16)
+        y2 = gpu.gemv_gated(xn, wo, so, N, K, act_dtype=torch.float16)
+    else:
+        q, s = synth_int4(rng, N, K)
+        wq, sc = upload_int4(q, s)
+        y = gpu.gemv_normadd(ta, tw, th, h_out, tw2, wq, sc, N, K, y_dtype=torch.float32)
+        ref = O.gemv_ref(q, s, xr)
+        xn = gpu.normadd_rmsnorm(ta, tw, th.clone(), tw2, 0.0, y_dtype=torch.float16)
+        y2 = gpu.gemv(xn, wq, sc, N, K, y_dtype=torch.float32)
+    yn = to_np(y).astype(np.float32)
+    assert O.normwise_rel_err(to_np(h_out), hn) <= 2e-6
+    assert O.normwise_rel_err(yn, ref) <= 1e-3
+    assert O.normwise_rel_err(yn, to_np(y2).astype(np.float32)) <= 1e-3

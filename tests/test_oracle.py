@@ -8,6 +8,8 @@ the e4m3 codec, the dependency src/vk_engine.py:136 calls), or brute force
 on tiny inputs. Each check is chosen so that a plausible slip (dropped
 term, wrong sign/index, transposed operand, wrong rounding) fails it.
 """
+from fractions import Fraction
+
 import numpy as np
 import pytest
 import torch
@@ -294,6 +296,77 @@ def test_w8_fold_uses_unrounded_scale():
     deq1 = np.float32(1.0) * sc[0, 0]
     assert W8[0, 1] == np.rint(deq1 / sw[0])
     assert O.w4a8_ratio(sc, sw).dtype == np.float16
+
+
+def _rne(x: Fraction, p: int) -> Fraction:
+    """x > 0 rounded to p significant bits, ties to even (normal range)."""
+    e = x.numerator.bit_length() - x.denominator.bit_length()
+    if Fraction(2) ** e > x:
+        e -= 1
+    ulp = Fraction(2) ** (e - p + 1)
+    m = x / ulp
+    f = m.numerator // m.denominator
+    rem = m - f
+    if rem > Fraction(1, 2) or (rem == Fraction(1, 2) and f % 2):
+        f += 1
+    return f * ulp
+
+
+def _f32(bits: int) -> np.float32:
+    return np.array([bits], np.uint32).view(np.float32)[0]
+
+
+def _f16_bits(v: Fraction) -> int:
+    return int(np.array([float(v)], np.float64).astype(np.float16).view(np.uint16)[0])
+
+
+# W4A8 ratio (benchmarks/coopgemm_w4a8.py:84): fp32 sc / fp32 s_w, rounded to
+# fp32 by the division, then to fp16. Known answers worked out with exact
+# rational arithmetic (quotient of the two fp32 values, round to 24 bits, then
+# to 11 bits); each value pair is chosen so that a plausible mistake gives a
+# different fp16 pattern.
+#   pair A (sc 0x3c82ed64 = 0.015982337, s_w 0x3b1909c5 = 0.002335177):
+#     f16(sc/s_w) = 0x46d8, swapped f16(s_w/sc) = 0x30ad,
+#     f16(f16(sc)/s_w) = 0x46d7, f16(sc/f16(s_w)) = 0x46d9
+#   pair B (sc 0x3a384351, s_w 0x3a382c4b): the fp32 quotient is exactly the
+#     fp16 midpoint 1 + 2^-11, which ties to even (0x3c00); rounding the exact
+#     quotient straight to fp16 would give 0x3c01, and f16(s_w/sc) 0x3bff.
+_RATIO_PINS = [(0x3C82ED64, 0x3B1909C5, 0x46D8, (0x30AD, 0x46D7, 0x46D9)),
+               (0x3A384351, 0x3A382C4B, 0x3C00, (0x3BFF, 0x3C01))]
+
+
+@pytest.mark.parametrize("sc_bits,sw_bits,want,wrong", _RATIO_PINS)
+def test_w4a8_ratio_known_answer(sc_bits, sw_bits, want, wrong):
+    sc, sw = _f32(sc_bits), _f32(sw_bits)
+    # the known answer from exact arithmetic: two roundings, fp32 then fp16
+    exact = Fraction(float(sc)) / Fraction(float(sw))
+    assert _f16_bits(_rne(_rne(exact, 24), 11)) == want
+    got = O.w4a8_ratio(np.array([[sc]], np.float32), np.array([sw], np.float32))
+    assert got.dtype == np.float16 and got.shape == (1, 1)
+    assert int(got.view(np.uint16)[0, 0]) == want
+    assert want not in wrong
+    # the alternatives really are the patterns quoted above
+    alts = [_f16_bits(_rne(_rne(Fraction(float(sw)) / Fraction(float(sc)), 24), 11))]
+    if len(wrong) == 3:
+        sc16 = Fraction(float(np.float16(sc)))
+        sw16 = Fraction(float(np.float16(sw)))
+        alts += [_f16_bits(_rne(_rne(sc16 / Fraction(float(sw)), 24), 11)),
+                 _f16_bits(_rne(_rne(Fraction(float(sc)) / sw16, 24), 11))]
+    else:
+        alts += [_f16_bits(_rne(exact, 11))]
+    assert tuple(alts) == wrong
+
+
+def test_w4a8_ratio_layout():
+    # row n divides by s_w[n], block b takes sc[n, b]: [N, nblk] out, no transpose
+    sc = np.array([[0.5, 1.0, 2.0], [3.0, 6.0, 12.0]], np.float32)
+    sw = np.array([0.25, 1.5], np.float32)
+    got = O.w4a8_ratio(sc, sw)
+    assert got.shape == (2, 3)
+    np.testing.assert_array_equal(got.astype(np.float32), np.array([[2, 4, 8], [2, 4, 8]], np.float32))
+    sw2 = np.array([0.25, 0.5], np.float32)
+    np.testing.assert_array_equal(O.w4a8_ratio(sc, sw2).astype(np.float32),
+                                  np.array([[2, 4, 8], [6, 12, 24]], np.float32))
 
 
 def test_w4a8_weights_known_answer():
