@@ -510,17 +510,23 @@ def counter_workload(ops):
     print(f"[bench] counter workload done: copy {src.numel() * 4} B", flush=True)
 
 
+ROTATE_BYTES = 1 << 30     # distinct weights a GEMM leg cycles through (4x the 256 MB Infinity Cache)
+
+
 def bench_w8a8(ops, iters: int = 50):
     """W8A8 at M=2048, N=15360, K=3840 on packed weights (the product path:
-    weights are packed once at load time), 4 rotating weight sets; the same
-    product on row-major [N][K] weights is reported beside it."""
+    weights are packed once at load time), 50 back-to-back launches cycling
+    through >= 1 GB of distinct weight sets (so the Infinity Cache cannot
+    serve repeats); the same product on row-major [N][K] weights, W4A8 and
+    the activation quantizer are reported beside it."""
     import torch
 
     dev = torch.device("cuda:0")
     gen = torch.Generator(device=dev).manual_seed(1)
     M, N, K = 2048, 15360, 3840
     X = torch.randn((M, K), device=dev, generator=gen).to(torch.float16)
-    W8s = [torch.randint(-127, 128, (N, K), device=dev, generator=gen, dtype=torch.int8) for _ in range(4)]
+    nw = -(-ROTATE_BYTES // (N * K))
+    W8s = [torch.randint(-127, 128, (N, K), device=dev, generator=gen, dtype=torch.int8) for _ in range(nw)]
     W8ps = [ops.w8_pack(w) for w in W8s]
     sw = (torch.rand(N, device=dev, generator=gen) * 1e-3 + 1e-4).to(torch.float32)
     A, sa = ops.quant_act_i8(X)
@@ -539,21 +545,26 @@ def bench_w8a8(ops, iters: int = 50):
         b.synchronize()
         return a.elapsed_time(b) * 1e3 / iters
 
-    us = timed(lambda i: ops.gemm_w8a8_packed(A, W8ps[i % 4], sa, sw, N, Y=Y))
-    us_nk = timed(lambda i: ops.gemm_w8a8(A, W8s[i % 4], sa, sw, Y=Y))
+    us = timed(lambda i: ops.gemm_w8a8_packed(A, W8ps[i % nw], sa, sw, N, Y=Y))
+    us_nk = timed(lambda i: ops.gemm_w8a8(A, W8s[i % nw], sa, sw, Y=Y))
     # W4A8: the same product with B requantized to int8 on the fly from the int4 codes
     del W8s
+    del W8ps
+    n4 = -(-ROTATE_BYTES // (N * K // 2))
     wq4 = [torch.randint(-2 ** 31, 2 ** 31 - 1, (N * K // 8,), dtype=torch.int64, device=dev,
-                         generator=gen).to(torch.int32) for _ in range(4)]
+                         generator=gen).to(torch.int32) for _ in range(n4)]
     ratio = (torch.rand(N * K // 32, device=dev, generator=gen) * 4 + 1).to(torch.float16)
-    us_w4 = timed(lambda i: ops.gemm_w4a8(A, wq4[i % 4], ratio, sa, sw, N, Y=Y))
+    us_w4 = timed(lambda i: ops.gemm_w4a8(A, wq4[i % n4], ratio, sa, sw, N, Y=Y))
     # ... or with its int8 weights formed once (q4_w4a8_weights) and packed: the W8A8 kernel, same results
-    W8w4 = [ops.w8_pack(ops.w4a8_weights(w, ratio, N, K)) for w in wq4]
-    us_w4o = timed(lambda i: ops.gemm_w8a8_packed(A, W8w4[i % 4], sa, sw, N, Y=Y))
+    W8w4 = [ops.w8_pack(ops.w4a8_weights(w, ratio, N, K)) for w in wq4[:nw]]
+    us_w4o = timed(lambda i: ops.gemm_w8a8_packed(A, W8w4[i % nw], sa, sw, N, Y=Y))
+    del wq4, W8w4
     # activation quantizer (bandwidth-bound: 2MK read + MK write)
     us_q = timed(lambda i: ops.quant_act_i8(X, A, sa))
     tops = 2.0 * M * N * K / (us * 1e-6) / 1e12
-    return {"M": M, "N": N, "K": K, "weights": "packed (tile-32)", "us": round(us, 2), "TOPS": round(tops, 1),
+    torch.cuda.empty_cache()
+    return {"M": M, "N": N, "K": K, "weights": "packed (tile-32)", "launches": iters,
+            "distinct_weight_sets": nw, "rotated_bytes": nw * N * K, "us": round(us, 2), "TOPS": round(tops, 1),
             "frac_of_int8_peak": round(tops / INT8_PEAK_TOPS, 4),
             "us_row_major_weights": round(us_nk, 2),
             "w4a8_us": round(us_w4, 2), "w4a8_TOPS": round(2.0 * M * N * K / (us_w4 * 1e-6) / 1e12, 1),
@@ -561,7 +572,9 @@ def bench_w8a8(ops, iters: int = 50):
             "quant_act_us": round(us_q, 2), "quant_act_GBps": round(3 * M * K / (us_q * 1e-6) / 1e9, 1)}
 
 
-def bench_w4a16(ops, iters: int = 30):
+def bench_w4a16(ops, iters: int = 50):
+    """W4A16 at the two M=512 prefill shapes, back-to-back launches cycling
+    through >= 1 GB of distinct int4 weight sets."""
     import torch
 
     dev = torch.device("cuda:0")
@@ -569,24 +582,184 @@ def bench_w4a16(ops, iters: int = 30):
     out = {}
     for M, N, K in [(512, 15360, 3840), (512, 3840, 15360)]:
         X = torch.randn((M, K), device=dev, generator=gen).to(torch.float16)
-        words = torch.randint(-2 ** 31, 2 ** 31 - 1, (N * K // 8,), dtype=torch.int64, device=dev,
-                              generator=gen).to(torch.int32)
-        sc = (torch.randn(N * K // 32, device=dev, generator=gen) * 0.02).abs().to(torch.float16)
+        per = N * K // 2 + N * K // 16
+        nw = -(-ROTATE_BYTES // per)
+        mats = [(torch.randint(-2 ** 31, 2 ** 31 - 1, (N * K // 8,), dtype=torch.int64, device=dev,
+                               generator=gen).to(torch.int32),
+                 (torch.randn(N * K // 32, device=dev, generator=gen) * 0.02).abs().to(torch.float16))
+                for _ in range(nw)]
+        need = ops.gemm_workspace_bytes(M, N, K)
+        ws = torch.empty(need, dtype=torch.uint8, device=dev) if need else None
         Y = torch.empty((M, N), dtype=torch.float16, device=dev)
         st = torch.cuda.current_stream()
-        for _ in range(3):
-            ops.gemm_w4a16(X, words, sc, N, Y=Y)
+        for i in range(5):
+            ops.gemm_w4a16(X, mats[i % nw][0], mats[i % nw][1], N, Y=Y, ws=ws)
         a = torch.cuda.Event(enable_timing=True)
         b = torch.cuda.Event(enable_timing=True)
         a.record(st)
-        for _ in range(iters):
-            ops.gemm_w4a16(X, words, sc, N, Y=Y)
+        for i in range(iters):
+            ops.gemm_w4a16(X, mats[i % nw][0], mats[i % nw][1], N, Y=Y, ws=ws)
         b.record(st)
         b.synchronize()
         us = a.elapsed_time(b) * 1e3 / iters
         tf = 2.0 * M * N * K / (us * 1e-6) / 1e12
         out[f"M{M}_N{N}_K{K}"] = {"us": round(us, 2), "TFLOPS": round(tf, 1),
-                                 "frac_of_f16_peak": round(tf / F16_PEAK_TFLOPS, 4)}
+                                 "frac_of_f16_peak": round(tf / F16_PEAK_TFLOPS, 4), "launches": iters,
+                                 "distinct_weight_sets": nw}
+        del mats
+        torch.cuda.empty_cache()
+    return out
+
+
+def _timed_graph(ops, fn, n: int, reps: int) -> float:
+    """us per call of fn(i), i < n, captured once as a graph and replayed reps times (HIP events on the graph's
+    stream)."""
+    import torch
+
+    g = ops.Graph()
+    with g.capture():
+        for i in range(n):
+            fn(i)
+    g.launch()
+    g.launch()
+    a = torch.cuda.Event(enable_timing=True)
+    b = torch.cuda.Event(enable_timing=True)
+    a.record(g.stream)
+    for _ in range(reps):
+        g.launch()
+    b.record(g.stream)
+    b.synchronize()
+    g.destroy()
+    return a.elapsed_time(b) * 1e3 / (reps * n)
+
+
+def bench_ceilings(ops):
+    """Ceilings measured on this part (the denominators worth quoting beside
+    the data-sheet peaks):
+    - stream_read: the probe streaming-read kernel at each decode GEMV's byte
+      count, as a graph of launches over distinct buffers (>= 1 GB, so every
+      launch reads from HBM) - the best time for a dependent launch that
+      reads that many bytes once; best of a sweep of grid sizes, loads in
+      flight and chunked/strided order; at the 15360x3840 size also with
+      each launch prefetching its successor's first bytes into L2;
+    - mfma: MFMA-only loops (int8 32x32x32, f16 32x32x16), one short launch
+      and 50 back-to-back launches, with the shader clock read back;
+    - hipblaslt: torch's int8 (_int_mm) and fp16 (matmul) GEMMs at the W8A8
+      and W4A16 shapes, cycling through >= 1 GB of distinct weights."""
+    import torch
+
+    dev = torch.device("cuda:0")
+    gen = torch.Generator(device=dev).manual_seed(7)
+    out = {}
+    sink = torch.empty(65536, dtype=torch.int32, device=dev)
+    sizes = {"o_3840x4096": gemv_bytes(H, QN), "qkv_8192x3840": gemv_bytes(QN + 2 * KVN, H),
+             "c1_15360x3840": gemv_bytes(I, H), "gate_up_30720x3840": gemv_bytes(2 * I, H),
+             "lm_head_262144x3840": gemv_bytes(V, H)}
+    sweep = [(w, u, c) for w in (256, 512, 1024, 2048) for u in (4, 8, 16) for c in (True, False)]
+    sr = {}
+    for name, nbytes in sizes.items():
+        nbytes = -(-nbytes // 16) * 16
+        n = max(3, ROTATE_BYTES // nbytes + 1)
+        bufs = [torch.randint(-2 ** 31, 2 ** 31 - 1, (nbytes // 4,), dtype=torch.int32, device=dev, generator=gen)
+                for _ in range(n)]
+        reps = 3 if nbytes > (256 << 20) else 5
+        res = {}
+        for w, u, c in sweep:
+            res[(w, u, c)] = _timed_graph(ops, lambda i: ops.probe_stream_read(bufs[i], w, units=u, chunked=c,
+                                                                               sink=sink), n, reps)
+        (w, u, c), us = min(res.items(), key=lambda kv: kv[1])
+        ent = {"bytes": nbytes, "us_per_launch": round(us, 3), "GBps": round(nbytes / us / 1e3, 1),
+               "frac_of_hbm_peak": round(nbytes / us / 1e3 / HBM_PEAK_GBS, 4),
+               "best": {"wgs": w, "units": u, "order": "chunked" if c else "strided"}, "distinct_buffers": n}
+        if name == "c1_15360x3840":
+            pf = {}
+            for mb in (2, 4, 8, 16):
+                t = _timed_graph(ops, lambda i: ops.probe_stream_read(
+                    bufs[i], w, units=u, chunked=c, next=bufs[(i + 1) % n], prefetch_bytes=mb << 20, sink=sink),
+                    n, reps)
+                pf[f"{mb}MB"] = {"us_per_launch": round(t, 3), "GBps": round(nbytes / t / 1e3, 1)}
+            ent["with_successor_prefetch"] = pf
+        sr[name] = ent
+        print(f"[bench] ceiling stream_read {name}: {ent}", flush=True)
+        del bufs
+        torch.cuda.empty_cache()
+    out["stream_read"] = sr
+
+    khz = ops.probe_wall_clock_khz()
+    mf = {}
+    for kind, nm, per_mfma, peak in ((0, "int8_32x32x32", 65536, INT8_PEAK_TOPS), (1, "f16_32x32x16", 32768,
+                                                                                 F16_PEAK_TFLOPS)):
+        for wgs in (256, 512):
+            iters = 2000
+            clocks = torch.zeros((wgs, 2), dtype=torch.int64, device=dev)
+            st = torch.cuda.current_stream()
+            ops_per = wgs * 4 * iters * 4 * per_mfma
+            res = {}
+            for label, launches in (("short", 1), ("sustained_50", 50)):
+                for _ in range(3):
+                    ops.probe_mfma(kind, wgs, iters, clocks, sink)
+                torch.cuda.synchronize()
+                a = torch.cuda.Event(enable_timing=True)
+                b = torch.cuda.Event(enable_timing=True)
+                a.record(st)
+                for _ in range(launches):
+                    ops.probe_mfma(kind, wgs, iters, clocks, sink)
+                b.record(st)
+                b.synchronize()
+                us = a.elapsed_time(b) * 1e3 / launches
+                c = clocks.cpu().double()
+                ghz = float((c[:, 0] / (c[:, 1] / (khz * 1e3))).median()) / 1e9
+                t = ops_per / (us * 1e-6) / 1e12
+                res[label] = {"us_per_launch": round(us, 2), "T_per_s": round(t, 1),
+                              "frac_of_peak": round(t / peak, 4), "shader_clock_GHz": round(ghz, 3),
+                              "frac_of_peak_at_measured_clock": round(t / (peak * ghz / 2.4), 4)}
+            mf[f"{nm}_{wgs // 256}wave_per_simd"] = res
+    out["mfma"] = mf
+    out["wall_clock_khz"] = khz
+    print(f"[bench] ceiling mfma {mf}", flush=True)
+
+    hb = {}
+    st = torch.cuda.current_stream()
+
+    def timed(fn, iters=50):
+        for i in range(5):
+            fn(i)
+        a = torch.cuda.Event(enable_timing=True)
+        b = torch.cuda.Event(enable_timing=True)
+        a.record(st)
+        for i in range(iters):
+            fn(i)
+        b.record(st)
+        b.synchronize()
+        return a.elapsed_time(b) * 1e3 / iters
+
+    try:
+        M, N, K = 2048, 15360, 3840
+        A8 = torch.randint(-127, 128, (M, K), dtype=torch.int8, device=dev, generator=gen)
+        nw = -(-ROTATE_BYTES // (N * K))
+        Bs = [torch.randint(-127, 128, (K, N), dtype=torch.int8, device=dev, generator=gen) for _ in range(nw)]
+        us = timed(lambda i: torch._int_mm(A8, Bs[i % nw]))
+        t = 2.0 * M * N * K / (us * 1e-6) / 1e12
+        hb["int8_M2048_N15360_K3840"] = {"us": round(us, 2), "TOPS": round(t, 1),
+                                         "frac_of_int8_peak": round(t / INT8_PEAK_TOPS, 4), "op": "torch._int_mm"}
+        del Bs
+    except Exception as e:  # noqa: BLE001 - a ceiling that cannot be measured is reported as such
+        hb["int8_M2048_N15360_K3840"] = {"error": repr(e)[:200]}
+    for M, N, K in ((512, 15360, 3840), (512, 3840, 15360), (2048, 15360, 3840)):
+        try:
+            X = torch.randn((M, K), device=dev, generator=gen).to(torch.float16)
+            nw = -(-ROTATE_BYTES // (2 * N * K))
+            Bs = [torch.randn((K, N), device=dev, generator=gen).to(torch.float16) for _ in range(nw)]
+            us = timed(lambda i: torch.matmul(X, Bs[i % nw]))
+            t = 2.0 * M * N * K / (us * 1e-6) / 1e12
+            hb[f"f16_M{M}_N{N}_K{K}"] = {"us": round(us, 2), "TFLOPS": round(t, 1),
+                                         "frac_of_f16_peak": round(t / F16_PEAK_TFLOPS, 4), "op": "torch.matmul"}
+            del Bs
+        except Exception as e:  # noqa: BLE001
+            hb[f"f16_M{M}_N{N}_K{K}"] = {"error": repr(e)[:200]}
+    torch.cuda.empty_cache()
+    out["hipblaslt"] = hb
+    print(f"[bench] ceiling hipblaslt {hb}", flush=True)
     return out
 
 
@@ -604,13 +777,37 @@ def committed_traffic(shape: str):
 
 
 # --------------------------------------------------------- CPU baseline
+def _cpu_info():
+    """Host cores the numpy legs can use: os.cpu_count(), the affinity mask and
+    the BLAS thread pool (threadpoolctl when present, else OMP_NUM_THREADS)."""
+    threads = None
+    try:
+        from threadpoolctl import threadpool_info
+
+        threads = max((p.get("num_threads") or 0) for p in threadpool_info()) or None
+    except Exception:  # noqa: BLE001 - the count is informational
+        pass
+    if threads is None:
+        threads = int(os.environ.get("OMP_NUM_THREADS", "1"))
+    return {"cpu_count": os.cpu_count(), "affinity": len(os.sched_getaffinity(0)), "blas_threads": threads}
+
+
 def cpu_baseline(budget_s: float = 15.0):
-    """The oracle's numpy GEMV (dequant + matmul, the reference's formulation)
-    over whole layers of the decode set, repeated until ~budget_s of CPU work."""
+    """The reference's numpy formulations, through the oracle, on the host cores:
+    - value: GEMV dequant + matmul (benchmarks/coopgemm_i4.py:51-52 pattern)
+      over whole decode layers of the decode-set shapes, ~half the budget;
+    - gemv_matmul_only: the same GEMVs with the fp32 dequantized weights
+      formed beforehand, only Wdq @ x timed (GB/s of the same int4 bytes);
+    - w4a16: X.f32 @ Wdq.T at M=512, N=15360, K=3840 (dequant outside and
+      inside the timed region);
+    - w8a8: M=2048, N=15360, K=3840: per-row int8 activation quant
+      (benchmarks/coopgemm_w4a8.py:87-88), the exact product as
+      A.f64 @ W8.f64.T, and the f16((C sa) sw) epilogue."""
     import numpy as np
 
     from oracle import q4_oracle as O
 
+    info = _cpu_info()
     rng = np.random.default_rng(0)
     x = {K: rng.standard_normal(K).astype(np.float16) for K in (H, QN, I)}
     layer = []
@@ -619,7 +816,7 @@ def cpu_baseline(budget_s: float = 15.0):
         s = np.abs(rng.normal(0, 0.02, (N, K // 32))).astype(np.float16).astype(np.float32)
         layer.append((N, K, q, s))
     t_total, nbytes, gemvs, layers = 0.0, 0, 0, 0
-    while t_total < budget_s and layers < 64:
+    while t_total < budget_s / 2 and layers < 64:
         for N, K, q, s in layer:
             t0 = time.perf_counter()
             O.gemv_ref(q, s, x[K]).astype(np.float16)
@@ -627,19 +824,57 @@ def cpu_baseline(budget_s: float = 15.0):
             nbytes += gemv_bytes(N, K)
             gemvs += 1
         layers += 1
-    threads = None
-    try:
-        from threadpoolctl import threadpool_info
-
-        threads = max((p.get("num_threads") or 0) for p in threadpool_info()) or None
-    except Exception:
-        pass
-    if threads is None:
-        threads = int(os.environ.get("OMP_NUM_THREADS", "1"))
-    return {"value": round(nbytes / t_total / 1e9, 3), "unit": "GB/s", "cores": threads, "kind": "port",
+    # matmul only: Wdq formed outside the timed region
+    wdq = [(N, K, O.dequant(q, s)) for N, K, q, s in layer]
+    xf = {K: v.astype(np.float32) for K, v in x.items()}
+    t_mm, b_mm, l_mm = 0.0, 0, 0
+    while t_mm < budget_s / 6 and l_mm < 64:
+        for N, K, W in wdq:
+            t0 = time.perf_counter()
+            (W @ xf[K]).astype(np.float16)
+            t_mm += time.perf_counter() - t0
+            b_mm += gemv_bytes(N, K)
+        l_mm += 1
+    del wdq
+    # W4A16 at M=512, N=15360, K=3840
+    M4, N4, K4 = 512, I, H
+    q4 = rng.integers(0, 16, (N4, K4), dtype=np.uint8)
+    s4 = np.abs(rng.normal(0, 0.02, (N4, K4 // 32))).astype(np.float16).astype(np.float32)
+    X4 = rng.standard_normal((M4, K4)).astype(np.float16)
+    t0 = time.perf_counter()
+    Wd = O.dequant(q4, s4)
+    t_dq = time.perf_counter() - t0
+    t0 = time.perf_counter()
+    (X4.astype(np.float32) @ Wd.T).astype(np.float16)
+    t_w4 = time.perf_counter() - t0
+    del Wd, q4
+    # W8A8 at M=2048, N=15360, K=3840
+    M8, N8, K8 = 2048, I, H
+    W8 = rng.integers(-127, 128, (N8, K8), dtype=np.int8)
+    sw = (rng.random(N8) * 1e-3 + 1e-4).astype(np.float32)
+    X8 = rng.standard_normal((M8, K8)).astype(np.float16)
+    t0 = time.perf_counter()
+    A, sa = O.quant_act_i8(X8)
+    t_q = time.perf_counter() - t0
+    t0 = time.perf_counter()
+    C = O.int_matmul_exact(A, W8)
+    t_c = time.perf_counter() - t0
+    t0 = time.perf_counter()
+    O.w8a8_epilogue(C, sa, sw)
+    t_e = time.perf_counter() - t0
+    del W8, C
+    f4 = 2.0 * M4 * N4 * K4
+    f8 = 2.0 * M8 * N8 * K8
+    return {"value": round(nbytes / t_total / 1e9, 3), "unit": "GB/s", "cores": info["blas_threads"], "kind": "port",
             "sample": f"{layers} decode layers ({gemvs} GEMVs, {nbytes / 1e9:.2f} GB algorithmic) of the same "
-                      f"shapes through the oracle's numpy dequant+matmul in {t_total:.1f} s; "
-                      f"os.cpu_count()={os.cpu_count()}, affinity={len(os.sched_getaffinity(0))}"}
+                      f"shapes through the oracle's numpy dequant+matmul in {t_total:.1f} s",
+            **info,
+            "gemv_matmul_only_GBps": round(b_mm / t_mm / 1e9, 3),
+            "gemv_matmul_only_sample": f"{l_mm} decode layers, fp32 Wdq formed beforehand, {t_mm:.1f} s",
+            "w4a16": {"shape": f"M{M4}_N{N4}_K{K4}", "matmul_s": round(t_w4, 3), "dequant_s": round(t_dq, 3),
+                      "TFLOPS": round(f4 / t_w4 / 1e12, 4), "TFLOPS_with_dequant": round(f4 / (t_w4 + t_dq) / 1e12, 4)},
+            "w8a8": {"shape": f"M{M8}_N{N8}_K{K8}", "quant_act_s": round(t_q, 3), "exact_matmul_f64_s": round(t_c, 3),
+                     "epilogue_s": round(t_e, 3), "TOPS": round(f8 / (t_q + t_c + t_e) / 1e12, 4)}}
 
 
 def main():
@@ -654,6 +889,11 @@ def main():
                     help="run only the decode GEMV launches (16 per layer shape, 2 lm_head) and a 512 MiB "
                          "calibration copy, for rocprofv3 --pmc passes; prints no JSON line")
     ap.add_argument("--no-token", action="store_true", help="skip the whole-token legs")
+    ap.add_argument("--no-ceilings", action="store_true", help="skip the measured-ceiling probes")
+    ap.add_argument("--ceilings-only", action="store_true",
+                    help="run only the measured-ceiling probes; prints their results, no JSON line")
+    ap.add_argument("--gemm-only", action="store_true",
+                    help="run only the W8A8 and W4A16 legs; prints their results, no JSON line")
     ap.add_argument("--prefill-only", action="store_true",
                     help="run only the prefill-chunk leg; prints its result, no JSON line")
     ap.add_argument("--token-only", action="store_true",
@@ -674,6 +914,13 @@ def main():
         return
     if args.prefill_only:
         print(f"[bench] prefill chunk {bench_prefill(ops, reps=max(1, args.steps // 40))}", flush=True)
+        return
+    if args.ceilings_only:
+        bench_ceilings(ops)
+        return
+    if args.gemm_only:
+        print(f"[bench] w8a8 {bench_w8a8(ops)}", flush=True)
+        print(f"[bench] w4a16 {bench_w4a16(ops)}", flush=True)
         return
     if args.token_only:
         for fast in (False, True):
@@ -705,6 +952,9 @@ def main():
         print(f"[bench] w8a8 {w8}", flush=True)
         w4 = bench_w4a16(ops)
         print(f"[bench] w4a16 {w4}", flush=True)
+    ceil = None
+    if not args.no_ceilings:
+        ceil = bench_ceilings(ops)
     cpu = None
     if not args.no_cpu:
         cpu = cpu_baseline(args.cpu_budget)
@@ -744,6 +994,7 @@ def main():
             "full_token_step": tok,
             "small_m_gemv": small,
             "prefill_chunk": pre,
+            "ceilings": ceil,
         },
         "roofline": {
             "bound": "hbm",

@@ -763,3 +763,32 @@ def stream_wait(stream=None, timeout_ms: int = 0, label: str = "") -> None:
     if st == _lib.Q4_ERR_TIMEOUT:
         raise RuntimeError(f"GPU fence TIMEOUT after {timeout_ms}ms at [{label}]")
     _lib.check("q4_stream_wait", st)
+
+
+# ------------------------------------------------------------------ probes
+def probe_stream_read(buf: torch.Tensor, wgs: int, *, units: int = 8, chunked: bool = True,
+                      next: torch.Tensor | None = None, prefetch_bytes: int = 0,
+                      sink: torch.Tensor | None = None) -> torch.Tensor:
+    """Streaming read of all of ``buf`` (a measurement probe; computes nothing).
+    With ``next``, each workgroup then reads its successor's first
+    ``prefetch_bytes / wgs`` bytes of ``next`` into L2. Returns the sink."""
+    if sink is None:
+        sink = torch.empty(wgs, dtype=torch.int32, device=buf.device)
+    _need(sink, 4 * wgs, "sink")
+    nb = _nbytes(next) if next is not None else 0
+    call("q4_probe_stream_read", _p(buf), _nbytes(buf) // 16 * 16, wgs, units, int(chunked),
+         _p(next) if next is not None else None, nb, prefetch_bytes if next is not None else 0, _p(sink),
+         _nbytes(sink), _stream())
+    return sink
+
+
+def probe_mfma(kind: int, wgs: int, iters: int, clocks: torch.Tensor, sink: torch.Tensor) -> None:
+    """MFMA-only loop (kind 0 int8 32x32x32, 1 f16 32x32x16); ``clocks`` int64
+    [wgs, 2] receives (shader cycles, wall-clock ticks) per workgroup."""
+    call("q4_probe_mfma", kind, wgs, iters, _p(clocks), _nbytes(clocks), _p(sink), _nbytes(sink), _stream())
+
+
+def probe_wall_clock_khz() -> int:
+    k = C.c_int()
+    call("q4_probe_wall_clock_khz", C.byref(k))
+    return k.value

@@ -385,6 +385,29 @@ int q4_pre_attn(const void* q, int q_dtype, int ldq, const float* qnw,
                 int nkv, int hd, int stride, int window, int M, int max_keys,
                 const uint32_t* dyn, void* ws, size_t ws_bytes, void* stream);
 
+/* ---- measurement probes ----------------------------------------------------
+ * Ceilings measured on the part itself; they compute nothing of the model.
+ * Streaming read of `bytes` (16-byte nontemporal loads, `units` (4/8/16) per
+ * lane in flight, `wgs` workgroups of 256 threads over contiguous chunks
+ * (chunked) or grid-strided 4 KB rows): the counterpart of the reference's
+ * streaming-read microbenchmark (benchmarks/microbench_bw.py:26-35). With
+ * next/prefetch_bytes, each workgroup then reads its successor's first
+ * prefetch_bytes/wgs bytes of `next` (laid out like buf, reads clamped to
+ * next_bytes) with L2-allocating loads. sink: one uint32 per workgroup,
+ * written only when a data hash hits a magic value. */
+int q4_probe_stream_read(const void* buf, size_t bytes, int wgs, int units, int chunked, const void* next,
+                         size_t next_bytes, size_t prefetch_bytes, uint32_t* sink, size_t sink_bytes,
+                         void* stream);
+/* `iters` rounds of four independent MFMAs per wave, wgs workgroups of four
+ * waves: kind 0 = v_mfma_i32_32x32x32_i8 (65536 int ops each), 1 =
+ * v_mfma_f32_32x32x16_f16 (32768 flops each). clocks[2b] = shader-clock
+ * cycles and clocks[2b+1] = wall-clock ticks (q4_probe_wall_clock_khz) of
+ * workgroup b's loop: the matrix-core ceiling and the clock under that load
+ * (the counterpart of vk/coopgemm_i8.comp, benchmarks/coopgemm_i8.py:85). */
+int q4_probe_mfma(int kind, int wgs, int iters, unsigned long long* clocks, size_t clocks_bytes, int* sink,
+                  size_t sink_bytes, void* stream);
+int q4_probe_wall_clock_khz(int* khz);
+
 /* ---- record-once submit --------------------------------------------------
  * The per-token command buffer recorded once and resubmitted
  * (src/vk_engine.py:254-290, forward() :312-319) becomes a hipGraph captured
