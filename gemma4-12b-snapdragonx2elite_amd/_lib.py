@@ -37,6 +37,8 @@ SIGNATURES = {
     "q4_workspace_init": (_i, [_vp, _sz, _vp]),
     "q4_gemv_auto_split": (_i, [_i, _i]),
     "q4_gemv": (_i, [_vp, _i, _vp, _vp, _i, _f, _vp, _i, _i, _i, _i, _vp, _sz, _vp]),
+    "q4_gemv_scratch_bytes": (_sz, []),
+    "q4_gemv_noalloc": (_i, [_vp, _i, _vp, _vp, _i, _f, _vp, _i, _i, _i, _i, _vp]),
     "q4_gemv_f16s": (_i, [_vp, _i, _vp, _vp, _vp, _i, _i, _i, _i, _vp, _sz, _vp]),
     "q4_gemv_e4m3s": (_i, [_vp, _i, _vp, _vp, _f, _vp, _i, _i, _i, _i, _vp, _sz, _vp]),
     "q4_gemv_batch": (_i, [_vp, _i, _i, _i, _i, _i, _vp, _vp, _vp, _vp, _vp, _vp]),

@@ -39,6 +39,8 @@
 //    the workspace is ready for the next call (and hipGraph replay).
 #include "q4mi_common.h"
 
+#include <mutex>
+
 namespace q4 {
 
 constexpr int GEMV_THREADS = 256;
@@ -1264,6 +1266,75 @@ int q4_gemv_batch_normadd(const float* a, const float* w, const float* h, float*
   clear_error();
   const NormIn nx{a, w, h, h_out, w2, scale == 0.0f ? 1.0f : scale};
   return gemv_batch_launch(nullptr, Q4_DT_F16, K, scale_fmt, y_dtype, count, wq, scales, inv, y, N, stream, &nx);
+}
+
+}  // extern "C"
+
+// ---- allocation-free split-K GEMV ------------------------------------------
+// q4_gemv_noalloc runs q4_gemv's kernels with the split-K workspace (tickets,
+// then fp32 partials) in this file-scope device array instead of a caller
+// buffer: one copy per GPU, held until the process ends. Every call on a GPU
+// shares it, so calls that overlap on one GPU (other streams, other threads)
+// race; calls issued in order on one stream do not.
+constexpr size_t GEMV_SCRATCH_BYTES = 2u << 20;
+static __device__ __align__(256) uint8_t scratch[GEMV_SCRATCH_BYTES];
+
+namespace {
+constexpr int SCRATCH_MAX_DEVICES = 64;
+std::mutex g_scratch_mu;
+void* g_scratch_ptr[SCRATCH_MAX_DEVICES];
+
+// Device address of this GPU's scratch array (the current device's), resolved
+// once per device with hipGetSymbolAddress: the host-side name of a
+// __device__ array is a stand-in, not a device address.
+int scratch_addr(void** out) {
+  int dev = 0;
+  Q4_HIP(hipGetDevice(&dev));
+  Q4_ARG(dev >= 0 && dev < SCRATCH_MAX_DEVICES, "device %d out of range for the GEMV scratch table", dev);
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (!g_scratch_ptr[dev]) {
+    void* p = nullptr;
+    Q4_HIP(hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)));
+    Q4_ARG(p != nullptr, "hipGetSymbolAddress returned no address for the GEMV scratch");
+    g_scratch_ptr[dev] = p;
+  }
+  *out = g_scratch_ptr[dev];
+  return Q4_OK;
+}
+}  // namespace
+
+__global__ void __launch_bounds__(256) zero_words_kernel(uint32_t* __restrict__ p, int n) {
+  const int i = blockIdx.x * 256 + threadIdx.x;
+  if (i < n) p[i] = 0u;
+}
+
+extern "C" {
+
+size_t q4_gemv_scratch_bytes(void) { return GEMV_SCRATCH_BYTES; }
+
+int q4_gemv_noalloc(const void* x, int x_dtype, const uint32_t* wq, const void* scales, int scale_fmt, float inv,
+                    void* y, int y_dtype, int N, int K, int split, void* stream) {
+  clear_error();
+  Q4_ARG(N > 0 && K > 0 && K % BLK == 0, "bad GEMV shape N=%d K=%d (K must be a positive multiple of 32)", N, K);
+  Q4_ARG(x_dtype == Q4_DT_F32 || x_dtype == Q4_DT_F16, "bad x dtype %d", x_dtype);
+  Q4_ARG(N <= (1 << 30) && (long)K <= (1L << 24), "GEMV too large");
+  const GemvPlan pl = plan(N, K, split, x_dtype);
+  if (pl.ws == 0)   // unsplit plan: no workspace at all
+    return gemv_launch(x, x_dtype, wq, scales, scale_fmt, inv, y, y_dtype, N, K, split, nullptr, 0, stream, 0);
+  Q4_ARG(pl.ws <= GEMV_SCRATCH_BYTES,
+         "q4_gemv_noalloc: GEMV N=%d K=%d split=%d needs %zu bytes of split-K scratch, more than its %zu", N, K,
+         pl.split, pl.ws, GEMV_SCRATCH_BYTES);
+  const int groups = pad_rows(N) / pl.R;
+  Q4_ARG(groups <= GEMV_MAX_TICKETS, "split-K GEMV supports at most %d row groups", GEMV_MAX_TICKETS);
+  void* ws = nullptr;
+  if (int e = scratch_addr(&ws)) return e;
+  // the tickets of this call's row groups start at zero (a fill kernel, not a
+  // memset node, so the call can be captured in a graph)
+  hipLaunchKernelGGL(zero_words_kernel, dim3(ceil_div(groups, 256)), dim3(256), 0, as_stream(stream),
+                     reinterpret_cast<uint32_t*>(ws), groups);
+  Q4_LAUNCHED("zero_words");
+  return gemv_launch(x, x_dtype, wq, scales, scale_fmt, inv, y, y_dtype, N, K, split, ws, GEMV_SCRATCH_BYTES, stream,
+                     0);
 }
 
 }  // extern "C"

@@ -130,6 +130,19 @@ int q4_gemv(const void* x, int x_dtype, const uint32_t* wq,
             const void* scales, int scale_fmt, float inv, void* y,
             int y_dtype, int N, int K, int split, void* ws, size_t ws_bytes,
             void* stream);
+/* q4_gemv without a workspace argument, for callers that cannot allocate
+ * (code under hipGraph capture, tight serving loops, harnesses that forbid
+ * hipMalloc). No counterpart in the reference. The split-K workspace is a
+ * file-scope device array of q4_gemv_scratch_bytes() (2 MiB) per GPU, held
+ * until the process ends; a GEMV whose split-K plan needs more is rejected
+ * (Q4_ERR_ARG). Nothing is allocated or freed. The array is shared by every
+ * call on that GPU: calls that overlap on one GPU (other streams or
+ * threads) race; calls in order on one stream do not. Its address is
+ * resolved on the first call per device (make that call outside a stream
+ * capture). Results are bit-identical to q4_gemv's. */
+size_t q4_gemv_scratch_bytes(void);
+int q4_gemv_noalloc(const void* x, int x_dtype, const uint32_t* wq, const void* scales, int scale_fmt, float inv,
+                    void* y, int y_dtype, int N, int K, int split, void* stream);
 /* fp16-scale GEMV (vk/gemv.comp). */
 int q4_gemv_f16s(const void* x, int x_dtype, const uint32_t* wq,
                  const uint16_t* sc16, void* y, int y_dtype, int N, int K,
