@@ -239,8 +239,20 @@ __device__ inline void nx_stage(const NormIn& nx, const v4u* na, const v4u* nh, 
   __syncthreads();
 }
 
-// Rows [g*R, g*R + R) of one GEMV over the K slice s of split (the whole K
-// when split == 1). NP = row groups of the launch * R (split-K partial stride).
+// Rows [lo, lo + cnt) of row group g of Gm over N rows: a balanced partition
+// (counts differ by at most one unit), in units of row pairs for a gated
+// matrix (row 2i = gate row i, 2i + 1 = up row i stay together).
+__device__ inline void group_rows(int g, int Gm, int N, int gated, int& lo, int& cnt) {
+  const int u = gated ? 2 : 1;
+  const long Nu = N / u;
+  lo = (int)((long)g * Nu / Gm) * u;
+  cnt = (int)((long)(g + 1) * Nu / Gm) * u - lo;
+}
+
+// Rows [lo, lo + cnt) (group_rows(g, Gm): cnt <= R) of one GEMV over the K
+// slice s of split (the whole K when split == 1); lane row r >= cnt
+// repeats row lo + cnt - 1 and stores nothing. The rows may span two
+// panels. NP = split-K partial stride (>= N).
 //
 // Order of work per wave: (1) direct-to-LDS loads of the wave's share of the
 // x slice (no registers), (2) the lane's first U weight units (streaming
@@ -256,7 +268,7 @@ __device__ inline void nx_stage(const NormIn& nx, const v4u* na, const v4u* nh, 
 template <int R, int U, int XT, int ST, int YT, bool NX = false>
 __device__ __forceinline__ void gemv_rows(const void* __restrict__ xv, const uint4* __restrict__ wq,
                                           const void* __restrict__ scv, float outscale, void* __restrict__ yv,
-                                          int N, int nblk, int g, int s, int split, long NP,
+                                          int N, int nblk, int g, int Gm, int s, int split, long NP,
                                           float* __restrict__ part, uint32_t* __restrict__ cnt,
                                           uint32_t* __restrict__ smem, float (*red)[R], int gated,
                                           NormIn nx = {}) {
@@ -306,8 +318,11 @@ __device__ __forceinline__ void gemv_rows(const void* __restrict__ xv, const uin
   }
 
   // (2) first U weight units and scales of the lane: blocks slot, slot + S, ...
-  const int n0 = g * R;
-  const long ubase = ((long)(n0 / PANEL) * nblk + b_lo) * PANEL + (n0 % PANEL) + r;  // unit of block j: ubase + 64 j
+  int n0, rows;
+  group_rows(g, Gm, N, gated, n0, rows);
+  const bool live = r < rows;
+  const int nl = n0 + min(r, rows - 1);
+  const long ubase = ((long)(nl / PANEL) * nblk + b_lo) * PANEL + (nl % PANEL);  // unit of block j: ubase + 64 j
   const uint8_t* wb = reinterpret_cast<const uint8_t*>(wq);
   v4u u[U];
   uint32_t sb[U];
@@ -389,15 +404,16 @@ __device__ __forceinline__ void gemv_rows(const void* __restrict__ xv, const uin
   if (wave != 0) return;
 
   const int n = n0 + r;
+  const bool own = lane < R && live;
   float v = 0.0f;
-  if (lane < R) v = (((red[0][r] + red[1][r]) + red[2][r]) + red[3][r]) * outscale;
+  if (own) v = (((red[0][r] + red[1][r]) + red[2][r]) + red[3][r]) * outscale;
   if (split == 1) {
-    store_rows<YT>(yv, n, v, N, lane < R, gated);
+    store_rows<YT>(yv, n, v, N, own, gated);
     return;
   }
 
   // ---- split-K: publish this workgroup's partial; the last one reduces ----
-  if (lane < R) part[(long)s * NP + n] = v;
+  if (own) part[(long)s * NP + n] = v;
   __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");
   uint32_t prev = 0;
   if (lane == 0) prev = __hip_atomic_fetch_add(&cnt[g], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -405,10 +421,10 @@ __device__ __forceinline__ void gemv_rows(const void* __restrict__ xv, const uin
   if (prev != (uint32_t)(split - 1)) return;
   __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
   float t = 0.0f;
-  if (lane < R)
+  if (own)
     for (int c = 0; c < split; ++c)
       t += __hip_atomic_load(part + (long)c * NP + n, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-  store_rows<YT>(yv, n, t, N, lane < R, gated);
+  store_rows<YT>(yv, n, t, N, own, gated);
   if (lane == 0) __hip_atomic_store(&cnt[g], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
@@ -429,9 +445,8 @@ gemv_kernel(const void* __restrict__ xv, const uint4* __restrict__ wq, const voi
   // split-K grids (small matrices only) keep the plain order: their row
   // groups are reduced through the workspace, not through L2 reuse
   const int g = (gridDim.y == 1 ? xcd_major(blockIdx.x, gridDim.x) : blockIdx.x) * halves + half;
-  gemv_rows<R, U, XT, ST, YT>(xv, wq, scv, outscale, yv, N, nblk, g, blockIdx.y, split,
-                              (long)gridDim.x * halves * R, part, cnt, smem + half * stage_words<R, XT>(nblk),
-                              red[half], gated);
+  gemv_rows<R, U, XT, ST, YT>(xv, wq, scv, outscale, yv, N, nblk, g, gridDim.x * halves, blockIdx.y, split, N, part,
+                              cnt, smem + half * stage_words<R, XT>(nblk), red[half], gated);
 }
 
 // Several activation vectors through one weight stream (speculative-decode
@@ -741,14 +756,15 @@ struct SegSel {
   const void* sc;
   void* y;
   float os;
-  int N, g0;
+  int N, g0, Gm;
 };
 __device__ inline SegSel select_seg(const GemvSegs& segs, int g) {
-  SegSel r{segs.s[0].wq, segs.s[0].sc, segs.s[0].y, segs.s[0].outscale, segs.s[0].N, 0};
+  SegSel r{segs.s[0].wq, segs.s[0].sc, segs.s[0].y, segs.s[0].outscale, segs.s[0].N, 0, segs.s[0].g_end};
 #pragma unroll
   for (int t = 1; t < Q4_GEMV_MAX_BATCH; ++t) {
     if (t < segs.count && g >= segs.s[t - 1].g_end)
-      r = SegSel{segs.s[t].wq, segs.s[t].sc, segs.s[t].y, segs.s[t].outscale, segs.s[t].N, segs.s[t - 1].g_end};
+      r = SegSel{segs.s[t].wq, segs.s[t].sc, segs.s[t].y, segs.s[t].outscale, segs.s[t].N, segs.s[t - 1].g_end,
+                 segs.s[t].g_end - segs.s[t - 1].g_end};
   }
   return r;
 }
@@ -771,7 +787,7 @@ gemv_batch_kernel(const void* __restrict__ xv, int nblk, const GemvSegs segs, in
   const int half = threadIdx.x / GEMV_THREADS;
   const int g = wave_group(halves);
   const SegSel q = select_seg(segs, g);
-  gemv_rows<R, U, XT, ST, YT>(xv, q.wq, q.sc, q.os, q.y, q.N, nblk, g - q.g0, 0, 1, 0, nullptr, nullptr,
+  gemv_rows<R, U, XT, ST, YT>(xv, q.wq, q.sc, q.os, q.y, q.N, nblk, g - q.g0, q.Gm, 0, 1, 0, nullptr, nullptr,
                               smem + half * stage_words<R, XT>(nblk), red[half], 0);
 }
 
@@ -785,8 +801,9 @@ gemv_nx_kernel(const NormIn nx, const uint4* __restrict__ wq, const void* __rest
   __shared__ float red[2][GEMV_WAVES][R];
   const int half = threadIdx.x / GEMV_THREADS;
   const int g = wave_group(halves);
-  gemv_rows<R, U, Q4_DT_F16, ST, YT, true>(nullptr, wq, scv, outscale, yv, N, nblk, g, 0, 1, 0, nullptr, nullptr,
-                                           smem + half * stage_words<R, Q4_DT_F16>(nblk), red[half], gated, nx);
+  gemv_rows<R, U, Q4_DT_F16, ST, YT, true>(nullptr, wq, scv, outscale, yv, N, nblk, g, gridDim.x * halves, 0, 1, 0,
+                                           nullptr, nullptr, smem + half * stage_words<R, Q4_DT_F16>(nblk), red[half],
+                                           gated, nx);
 }
 template <int R, int U, int ST, int YT>
 __global__ void __launch_bounds__(2 * GEMV_THREADS)
@@ -796,8 +813,9 @@ gemv_batch_nx_kernel(const NormIn nx, int nblk, const GemvSegs segs, int halves)
   const int half = threadIdx.x / GEMV_THREADS;
   const int g = wave_group(halves);
   const SegSel q = select_seg(segs, g);
-  gemv_rows<R, U, Q4_DT_F16, ST, YT, true>(nullptr, q.wq, q.sc, q.os, q.y, q.N, nblk, g - q.g0, 0, 1, 0, nullptr,
-                                           nullptr, smem + half * stage_words<R, Q4_DT_F16>(nblk), red[half], 0, nx);
+  gemv_rows<R, U, Q4_DT_F16, ST, YT, true>(nullptr, q.wq, q.sc, q.os, q.y, q.N, nblk, g - q.g0, q.Gm, 0, 1, 0,
+                                           nullptr, nullptr, smem + half * stage_words<R, Q4_DT_F16>(nblk), red[half],
+                                           0, nx);
 }
 
 typedef void (*gemv_fn)(const void*, const uint4*, const void*, float, void*, int, int, int, float*, uint32_t*, int);
@@ -981,10 +999,37 @@ static size_t x_stage_lds(int nb, int x_dtype, int R) {
   return GEMV_WAVES * per_wave + (x_dtype == Q4_DT_F16 ? (size_t)GEMV_WAVES * nbw * sizeof(float) : 0);
 }
 
+
 struct GemvPlan {
   int R, U, split, nb_max;
   size_t lds, ws;
 };
+
+// Balanced unsplit grids (Q4MI_GEMV_BAL=m, tuning): 256 m row groups (or
+// more, until a group fits 64 rows) spread the rows evenly over all CUs, in
+// units of `unit` rows (2: gate/up pairs); R is the smallest of 8..64 that
+// holds the largest group. Returns 0 when not selected.
+static int balance_mult() {
+  const char* e = getenv("Q4MI_GEMV_BAL");
+  const int m = e ? atoi(e) : 0;
+  return m > 0 && m <= 64 ? m : 0;
+}
+static int pow2_rows(int rows) {
+  int R = 8;
+  while (R < rows) R <<= 1;
+  return R;
+}
+static bool balanced_groups(int N, int unit, int& R, int& groups) {
+  const int m = balance_mult();
+  if (!m) return false;
+  const long Nu = N / unit;
+  long G = 256L * m;
+  while (G < Nu && unit * ceil_div(Nu, G) > 64) G += 256;
+  if (G > Nu) G = Nu;
+  groups = (int)G;
+  R = pow2_rows(unit * ceil_div(Nu, G));
+  return true;
+}
 
 static GemvPlan plan(int N, int K, int split_req, int x_dtype) {
   const int NP = pad_rows(N), nblk = K / BLK;
@@ -1087,10 +1132,17 @@ static int gemv_launch(const void* x, int x_dtype, const uint32_t* wq, const voi
   Q4_ARG(scale_fmt == Q4_SCALE_F16 || scale_fmt == Q4_SCALE_E4M3, "bad scale format %d", scale_fmt);
   Q4_ARG(((uintptr_t)wq & 15) == 0 && ((uintptr_t)x & 15) == 0, "wq and x must be 16-byte aligned");
   Q4_ARG(N <= (1 << 30) && (long)K <= (1L << 24), "GEMV too large");
-  const GemvPlan pl = plan(N, K, split, x_dtype);
+  GemvPlan pl = plan(N, K, split, x_dtype);
   Q4_ARG(pl.ws == 0 || (ws && ws_size >= pl.ws), "GEMV N=%d K=%d split=%d needs a %zu-byte workspace (got %zu)", N,
          K, pl.split, pl.ws, ws ? ws_size : (size_t)0);
-  const int groups = pad_rows(N) / pl.R;
+  // row groups: NP / R of the plan, at most one per row (pair, when gated)
+  const int unit = gated ? 2 : 1;
+  int groups = pad_rows(N) / pl.R;
+  if (groups > N / unit) groups = N / unit;
+  if (pl.split == 1 && balanced_groups(N, unit, pl.R, groups)) {
+    pl.U = units_in_flight(pl.nb_max, pl.R, groups);
+    pl.lds = x_stage_lds(pl.nb_max, x_dtype, pl.R);
+  }
   Q4_ARG(pl.ws == 0 || groups <= GEMV_MAX_TICKETS, "split-K GEMV supports at most %d row groups", GEMV_MAX_TICKETS);
   uint32_t* cnt = pl.ws ? reinterpret_cast<uint32_t*>(ws) : nullptr;
   float* part = pl.ws ? reinterpret_cast<float*>(reinterpret_cast<char*>(ws) + GEMV_TICKET_BYTES) : nullptr;
@@ -1210,13 +1262,29 @@ static int gemv_batch_launch(const void* x, int x_dtype, int K, int scale_fmt, i
     for (int i = 0; i < count; ++i)
       if (int e = nx_check_y(*nx, K, y[i], (size_t)N[i] * (y_dtype == Q4_DT_F16 ? 2 : 4))) return e;
   }
-  const int R = rows_per_group((int)NP);
+  int R = rows_per_group((int)NP);
+  // row groups per matrix: NP_i / R, or with a balanced plan 256 m groups
+  // shared out in proportion to the rows (same rows per group everywhere)
+  int gm[Q4_GEMV_MAX_BATCH];
+  int Rb = 0, Gb = 0;
+  if (balanced_groups((int)NP, 1, Rb, Gb)) {
+    R = 8;
+    for (int i = 0; i < count; ++i) {
+      gm[i] = (int)(((long)Gb * N[i] + NP / 2) / NP);
+      if (gm[i] < 1) gm[i] = 1;
+      if (gm[i] > N[i]) gm[i] = N[i];
+      while (ceil_div(N[i], gm[i]) > 64) ++gm[i];
+      R = max(R, pow2_rows(ceil_div(N[i], gm[i])));
+    }
+  } else {
+    for (int i = 0; i < count; ++i) gm[i] = min(pad_rows(N[i]) / R, N[i]);
+  }
   GemvSegs segs;
   memset(&segs, 0, sizeof(segs));
   segs.count = count;
   int groups = 0;
   for (int i = 0; i < count; ++i) {
-    groups += pad_rows(N[i]) / R;
+    groups += gm[i];
     segs.s[i].wq = reinterpret_cast<const uint4*>(wq[i]);
     segs.s[i].sc = scales[i];
     segs.s[i].y = y[i];
