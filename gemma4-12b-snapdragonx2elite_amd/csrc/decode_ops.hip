@@ -15,21 +15,21 @@
 //    kernels, so a captured graph replays every token without updates (the
 //    reference's DYN uniform buffer, src/vk_engine.py:306-310).
 //  * Attention is split along the cached keys (flash-decoding): workgroup
-//    (head, split) takes ATT_CH = 64 keys, 16 per wave, reads each key and
-//    value row with one coalesced wave access (all 16 rows of a wave in
-//    flight at once), forms its chunk's softmax numerator and maximum and
-//    the unnormalised p V; a second kernel merges the splits' (max, sum,
-//    accumulator) triples. The grid covers the cache capacity and splits
-//    past the current length exit at once, so the launch shape does not
-//    depend on the position; 64-key splits put a 1024-key window of 16
-//    heads on 256 workgroups.
+//    (head group, split) serves up to 4 query heads of one KV head over 32
+//    keys (8 per wave), with every K and V row it needs in flight from the
+//    start; a second kernel merges the splits' (max, sum, accumulator)
+//    triples. The grid covers the cache capacity and splits past the current
+//    length exit at once, so the launch shape does not depend on the
+//    position; a 1024-key window of 8 KV heads with 2 query heads each is
+//    256 workgroups.
 #include "q4mi_common.h"
 
 namespace q4 {
 
 constexpr int NORM_THREADS = 1024;
 constexpr int ATT_THREADS = 256;
-constexpr int ATT_CH = 64;        // keys per attention split (16 per wave)
+constexpr int ATT_KCH = 32;       // keys per attention split (8 per wave)
+constexpr int ATT_HPW = 4;        // query heads per attention workgroup (at most)
 constexpr int ATT_MAX_HD = 512;   // head dims up to 512 (global layers)
 
 
@@ -273,179 +273,302 @@ __device__ inline HalfVec<E> ld_halves(const uint16_t* p) {
   return r;
 }
 
-// Split blockIdx.y of head blockIdx.x: keys [ATT_CH y, ATT_CH (y+1)) of the
-// current length, hd = 64 EPL. Wave w takes keys 16 w .. 16 w + 15 of the
-// split. Scores: a key row (128 EPL bytes) is read by LPK = 8 EPL lanes, 16
-// bytes each, so one wave load covers 64 / LPK whole rows (coalesced) and
-// the wave's 16 rows are all in flight at once; each lane keeps its 8
-// elements of q in registers and the row's lanes reduce with xor-shuffles.
-// p V: lane l owns elements EPL l .. EPL l + EPL - 1, one coalesced load
-// per key, the wave's 16 keys in flight at once. Keys past the length read
-// the last live row (in bounds) with weight 0. Writes (max, sum,
-// unnormalised accumulator[hd]) to ws.
+// Decode attention, split along the keys (vk/attn.comp:18-53,
+// flash-decoding). Workgroup (g, s): head group g = hpw query heads of one
+// KV head (they share that KV head's rows, so the rows are read once for all
+// of them) and keys [ATT_KCH s, ATT_KCH (s + 1)) of the current length; wave
+// w takes 8 of those keys. Every global load of the split is issued first,
+// none of them waiting for the position: the wave's K rows (8 lanes per row,
+// lane c reading its 16-byte chunks c, c + 8, ..: a row's 8 lanes cover 128
+// contiguous bytes per load), its V rows (one coalesced row per key, lane l
+// owning elements EPL l ..; rows clamped to the cache, rows past the length
+// masked), the raw q of the group's heads, this KV head's raw k and v of
+// this token, the norm weights and the RoPE row. The vectors in use are then
+// normalised together (one reduction round), q (and k) get RoPE, the scores
+// of each head come from the same K registers (3 shuffle levels per key),
+// and per head the split's maximum m, sum l of exp(s - m) and unnormalised
+// p V go to the workspace for attn_merge_kernel. Splits past the length
+// exit at once (the grid covers the cache depth, so a captured graph replays
+// every position).
 //
-// With PREP (prepkv folded in, vk/prepkv.comp:16-30): the workgroups of the
-// split that holds this token's cache slot form the token's K (k-norm with
-// weight, RoPE) and V (v-norm) themselves, rounded to fp16 as the cache
-// holds them, and use them for that key in place of the cache row (which
-// they never read); the workgroup of the first query head of each KV head
-// writes them to the cache for the next tokens. No other workgroup touches
-// that row, so one launch replaces prepkv + this kernel.
+// With PREP (prepkv folded in, vk/prepkv.comp:16-30): the split holding this
+// token's slot forms its K (k-norm with weight, RoPE) and V (v-norm),
+// rounded to fp16 as the cache holds them, uses them for that key in place
+// of the cache row, and the first head group of each KV head writes them to
+// the cache for the next tokens; no other workgroup reads that row.
 template <int EPL, bool PREP>
-__global__ void __launch_bounds__(ATT_THREADS) attn_split_kernel(const float* __restrict__ qkv, const float* __restrict__ qnw,
-                                                                 const float* __restrict__ cs, const float* __restrict__ sn,
-                                                                 uint16_t* __restrict__ kc, uint16_t* __restrict__ vc,
-                                                                 int stride, int window, int qoff, int grp,
-                                                                 const uint32_t* __restrict__ dyn,
-                                                                 float* __restrict__ ws, const float* __restrict__ knw,
-                                                                 int koff, int voff) {
-  constexpr int HD = 64 * EPL, LPK = 8 * EPL, KPI = 64 / LPK, KPW = ATT_CH / (ATT_THREADS / 64);
-  constexpr int NI = KPW / KPI;  // score loads per wave
-  __shared__ float qv[HD], qr[HD], p[ATT_CH], red[ATT_THREADS / 64];
+__global__ void __launch_bounds__(ATT_THREADS)
+attn_split_kernel(const float* __restrict__ qkv, const float* __restrict__ qnw, const float* __restrict__ cs,
+                  const float* __restrict__ sn, uint16_t* __restrict__ kc, uint16_t* __restrict__ vc, int stride,
+                  int window, int qoff, int grp, int hpw, const uint32_t* __restrict__ dyn, float* __restrict__ part,
+                  int nsplit, const float* __restrict__ knw, int koff, int voff) {
+  constexpr int HD = 64 * EPL, KPW = ATT_KCH / (ATT_THREADS / 64);  // 8 keys per wave
+  constexpr int EPT = (HD + ATT_THREADS - 1) / ATT_THREADS;        // vector elements per thread
+  constexpr int NV = ATT_HPW + 2;                                  // q heads, k, v
+  static_assert(KPW == 8, "one K row per 8 lanes");
+  __shared__ float vec[NV][HD];                   // raw, then normalised vectors
+  __shared__ float qr[ATT_HPW][HD];               // q after RoPE
+  __shared__ float p[ATT_HPW][ATT_KCH], sml[ATT_HPW][2];
+  __shared__ float red[NV][ATT_THREADS / 64];
   __shared__ float accp[ATT_THREADS / 64][HD];
-  __shared__ float knew[PREP ? HD : 1], vnew[PREP ? HD : 1];
-  const int h = blockIdx.x, sp = blockIdx.y, t = threadIdx.x;
+  const int g = blockIdx.x, sp = blockIdx.y, t = threadIdx.x, wave = t >> 6, lane = t & 63;
+  const int gpk = grp / hpw;  // head groups per KV head
+  const int kvh = g / gpk, h0 = g * hpw;
+  const int j0 = sp * ATT_KCH;
+  const long kv0 = (long)kvh * stride * HD;
+
+  // (1) every global load of the split
+  const int kk = lane >> 3, c8 = lane & 7;  // K: key kk of the wave, chunks c8 + 8 m
+  v4u ku[EPL];
+  {
+    const int j = min(j0 + KPW * wave + kk, stride - 1);
+#pragma unroll
+    for (int m = 0; m < EPL; ++m) ku[m] = *reinterpret_cast<const v4u*>(kc + kv0 + (long)j * HD + 8 * (c8 + 8 * m));
+  }
+  HalfVec<EPL> vv[KPW];
+#pragma unroll
+  for (int k = 0; k < KPW; ++k) {
+    const int j = min(j0 + KPW * wave + k, stride - 1);
+    vv[k] = ld_halves<EPL>(vc + kv0 + (long)j * HD + EPL * lane);
+  }
+  float raw[NV][EPT], wq[EPT], wk[EPT], csv[EPT], snv[EPT];
+#pragma unroll
+  for (int e = 0; e < EPT; ++e) {
+    const int i = min(t + ATT_THREADS * e, HD - 1);
+#pragma unroll
+    for (int h = 0; h < ATT_HPW; ++h) raw[h][e] = h < hpw ? qkv[qoff + (h0 + h) * HD + i] : 0.0f;
+    raw[ATT_HPW][e] = PREP ? qkv[koff + kvh * HD + i] : 0.0f;
+    raw[ATT_HPW + 1][e] = PREP ? qkv[voff + kvh * HD + i] : 0.0f;
+    wq[e] = qnw[i];
+    wk[e] = PREP ? knw[i] : 0.0f;
+    csv[e] = cs[i];
+    snv[e] = sn[i];
+  }
   const uint32_t pos = dyn[0];
   const int T = att_len(pos, window, stride);
-  const int j0 = sp * ATT_CH;
-  if (j0 >= T) return;  // past the current length: the merge reads only the live splits
-  const int n = min(ATT_CH, T - j0);
-  const int kvh = h / grp;
-  const int wave = t >> 6, lane = t & 63;
+  if (j0 >= T) {  // past the current length: the merge reads only the live splits
+    vmwait<0>();   // (the loads above land before the wave ends)
+    return;
+  }
+  const int n = min(ATT_KCH, T - j0);
   const int slot = kv_slot(pos, window);
-  const int kslot = PREP && slot < stride && slot >= j0 && slot < j0 + n ? slot - j0 : -1;  // workgroup-uniform
+  const bool fresh_split = PREP && slot < stride && slot >= j0 && slot < j0 + n;  // workgroup-uniform
+  const int kslot = fresh_split ? slot - j0 : -1;
+  const int nvec = fresh_split ? NV : hpw;  // vectors in use: q heads h < hpw, k and v when fresh
+  auto used = [&](int v) { return v < ATT_HPW ? v < hpw : fresh_split; };
 
-  if constexpr (PREP) {
-    if (kslot >= 0) {
-      for (int i = t; i < HD; i += ATT_THREADS) qv[i] = qkv[koff + kvh * HD + i];
-      __syncthreads();
-      norm_rope_head(qv, knew, knw, cs, sn, HD, red);
-      for (int i = t; i < HD; i += ATT_THREADS) knew[i] = h2f(f2h(knew[i]));
-      for (int i = t; i < HD; i += ATT_THREADS) vnew[i] = qkv[voff + kvh * HD + i];
-      __syncthreads();
-      norm_rope_head(vnew, nullptr, nullptr, nullptr, nullptr, HD, red);
-      for (int i = t; i < HD; i += ATT_THREADS) vnew[i] = h2f(f2h(vnew[i]));
-      if (h % grp == 0) {
-        const long o = ((long)kvh * stride + slot) * HD;
-        for (int i = t; i < HD; i += ATT_THREADS) {
-          kc[o + i] = f2h(knew[i]);
-          vc[o + i] = f2h(vnew[i]);
+  // (2) norms (weights: qnw for q, knw for k, none for v), one reduction round
+#pragma unroll
+  for (int v = 0; v < NV; ++v) {
+    if (!used(v)) continue;
+    float sq = 0.0f;
+#pragma unroll
+    for (int e = 0; e < EPT; ++e)
+      if (t + ATT_THREADS * e < HD) sq = fmaf(raw[v][e], raw[v][e], sq);
+    sq = reduce64<false>(sq);
+    if (lane == 0) red[v][wave] = sq;
+  }
+  (void)nvec;
+  __syncthreads();
+#pragma unroll
+  for (int v = 0; v < NV; ++v) {
+    if (!used(v)) continue;
+    float sq = 0.0f;
+    for (int w = 0; w < ATT_THREADS / 64; ++w) sq += red[v][w];
+    const float inv = inv_rms(sq, HD);
+#pragma unroll
+    for (int e = 0; e < EPT; ++e) {
+      const int i = t + ATT_THREADS * e;
+      const float wt = v < ATT_HPW ? wq[e] : wk[e];
+      if (i < HD) vec[v][i] = v <= ATT_HPW ? __fmul_rn(__fmul_rn(raw[v][e], inv), wt) : __fmul_rn(raw[v][e], inv);
+    }
+  }
+  __syncthreads();
+  // RoPE (rotate-half) of the q heads and k
+  constexpr int HF = HD / 2;
+#pragma unroll
+  for (int v = 0; v < ATT_HPW + 1; ++v) {
+    if (!used(v)) continue;
+#pragma unroll
+    for (int e = 0; e < EPT; ++e) {
+      const int i = t + ATT_THREADS * e;
+      if (i < HD) {
+        const float r = i < HF ? -vec[v][i + HF] : vec[v][i - HF];
+        const float o = __fadd_rn(__fmul_rn(vec[v][i], csv[e]), __fmul_rn(r, snv[e]));
+        if (v < ATT_HPW) qr[v][i] = o;
+        else raw[ATT_HPW][e] = o;  // k after RoPE, kept in registers until vec is free
+      }
+    }
+  }
+  __syncthreads();
+  float* knew = vec[ATT_HPW];
+  float* vnew = vec[ATT_HPW + 1];
+  if (fresh_split) {  // this token's K and V, rounded to fp16 as the cache holds them
+#pragma unroll
+    for (int e = 0; e < EPT; ++e) {
+      const int i = t + ATT_THREADS * e;
+      if (i < HD) {
+        const uint16_t kb = f2h(raw[ATT_HPW][e]), vb = f2h(vnew[i]);
+        knew[i] = h2f(kb);
+        vnew[i] = h2f(vb);
+        if (g % gpk == 0) {
+          const long o = ((long)kvh * stride + slot) * HD;
+          kc[o + i] = kb;
+          vc[o + i] = vb;
         }
       }
-      __syncthreads();  // qv is reused for q below
     }
+    __syncthreads();
   }
 
-  // q: norm with weight, RoPE (vk/attn.comp:23-30)
-  for (int i = t; i < HD; i += ATT_THREADS) qv[i] = qkv[qoff + h * HD + i];
-  __syncthreads();
-  norm_rope_head(qv, qr, qnw, cs, sn, HD, red);
-
-  const long kv0 = (long)kvh * stride * HD;
+  // (3) scores: the 8 lanes of a key row reduce with xor-shuffles
   {
-    const int kk = lane / LPK, ch = lane % LPK;
-    float q8[8];
-#pragma unroll
-    for (int e = 0; e < 8; ++e) q8[e] = qr[8 * ch + e];
-    v4u u[NI];
-#pragma unroll
-    for (int b = 0; b < NI; ++b) {
-      const int j = min(j0 + KPW * wave + KPI * b + kk, T - 1);
-      u[b] = *reinterpret_cast<const v4u*>(kc + kv0 + (long)j * HD + 8 * ch);
-    }
-#pragma unroll
-    for (int b = 0; b < NI; ++b) {
-      const int key = KPW * wave + KPI * b + kk;
-      // this token's key (PREP): its fp16-rounded k_new in place of the cache row
-      // it replaces, in the same summation order as every other key
-      const bool fresh = PREP && key == kslot;
+    const int key = KPW * wave + kk;
+    const bool fresh = PREP && key == kslot;
+    for (int h = 0; h < hpw; ++h) {
       float d = 0.0f;
 #pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        const float k0 = fresh ? knew[8 * ch + 2 * e] : h2f((uint16_t)(u[b][e] & 0xFFFFu));
-        const float k1 = fresh ? knew[8 * ch + 2 * e + 1] : h2f((uint16_t)(u[b][e] >> 16));
-        d = fmaf(q8[2 * e], k0, d);
-        d = fmaf(q8[2 * e + 1], k1, d);
-      }
+      for (int m = 0; m < EPL; ++m) {
+        const int b = 8 * (c8 + 8 * m);
 #pragma unroll
-      for (int o = LPK / 2; o > 0; o >>= 1) d += __shfl_xor(d, o, 64);
-      if (ch == 0) p[key] = key < n ? d : -INFINITY;
+        for (int e = 0; e < 4; ++e) {
+          const float k0 = fresh ? knew[b + 2 * e] : h2f((uint16_t)(ku[m][e] & 0xFFFFu));
+          const float k1 = fresh ? knew[b + 2 * e + 1] : h2f((uint16_t)(ku[m][e] >> 16));
+          d = fmaf(qr[h][b + 2 * e], k0, d);
+          d = fmaf(qr[h][b + 2 * e + 1], k1, d);
+        }
+      }
+      d = reduce8<false>(d);
+      if (c8 == 0) p[h][key] = key < n ? d : -INFINITY;
     }
   }
   __syncthreads();
-  const float s = p[t < ATT_CH ? t : 0];
-  const float m = block_max(t < ATT_CH ? s : -INFINITY, red);
-  const float pj = (t < ATT_CH && s != -INFINITY) ? expf(s - m) : 0.0f;
-  __syncthreads();
-  if (t < ATT_CH) p[t] = pj;
-  const float l = block_sum(pj, red);  // (its barriers also publish p)
-
-  float a[EPL];
-#pragma unroll
-  for (int e = 0; e < EPL; ++e) a[e] = 0.0f;
-  {
-    HalfVec<EPL> v[KPW];
-#pragma unroll
-    for (int k = 0; k < KPW; ++k) {
-      const int j = min(j0 + KPW * wave + k, T - 1);
-      v[k] = ld_halves<EPL>(vc + kv0 + (long)j * HD + EPL * lane);
+  // (4) softmax of the split, 32 lanes per head
+  if (t < hpw * ATT_KCH) {
+    const int h = t / ATT_KCH, key = t % ATT_KCH;
+    const float sc = p[h][key];
+    static_assert(ATT_KCH == 32, "one 32-lane row pair per head");
+    const float m = reduce32<true>(sc);
+    const float pj = sc != -INFINITY ? expf(sc - m) : 0.0f;
+    const float l = reduce32<false>(pj);
+    p[h][key] = pj;
+    if (key == 0) {
+      sml[h][0] = m;
+      sml[h][1] = l;
     }
+  }
+  __syncthreads();
+  // (5) unnormalised p V per head from the same V registers; waves meet in LDS
+  for (int h = 0; h < hpw; ++h) {
+    float a[EPL];
+#pragma unroll
+    for (int e = 0; e < EPL; ++e) a[e] = 0.0f;
 #pragma unroll
     for (int k = 0; k < KPW; ++k) {
-      const float pw = p[KPW * wave + k];
+      const float pw = p[h][KPW * wave + k];
       if (PREP && KPW * wave + k == kslot) {  // this token's value row
 #pragma unroll
         for (int e = 0; e < EPL; ++e) a[e] = fmaf(pw, vnew[EPL * lane + e], a[e]);
       } else {
 #pragma unroll
-        for (int e = 0; e < EPL; ++e) a[e] = fmaf(pw, h2f(v[k].h[e]), a[e]);
+        for (int e = 0; e < EPL; ++e) a[e] = fmaf(pw, h2f(vv[k].h[e]), a[e]);
       }
     }
+#pragma unroll
+    for (int e = 0; e < EPL; ++e) accp[wave][EPL * lane + e] = a[e];
+    __syncthreads();
+    float* o = part + ((long)(h0 + h) * nsplit + sp) * (HD + 2);
+    if (t == 0) {
+      o[0] = sml[h][0];
+      o[1] = sml[h][1];
+    }
+    for (int i = t; i < HD; i += ATT_THREADS) o[2 + i] = ((accp[0][i] + accp[1][i]) + accp[2][i]) + accp[3][i];
+    __syncthreads();  // accp is rewritten by the next head
+  }
+}
+
+// Head blockIdx.x: out = sum_c acc_c e^(m_c - M) / sum_c l_c e^(m_c - M),
+// M = max_c m_c, over the live splits c. The (m, l) pairs and the first
+// batch of MB accumulator values per thread are loaded together, before the
+// position; the weights and L come from wave 0 in a fixed order. ml: 2
+// nsplit floats of dynamic shared memory. out fp32 or fp16.
+template <int YT, int EPL>
+__global__ void __launch_bounds__(ATT_THREADS) attn_merge_kernel(const float* __restrict__ part, void* __restrict__ out,
+                                                                 int nsplit, int stride, int window,
+                                                                 const uint32_t* __restrict__ dyn) {
+  constexpr int HD = 64 * EPL, EPT = (HD + ATT_THREADS - 1) / ATT_THREADS, MB = 32;
+  extern __shared__ float ml[];
+  __shared__ float sL;
+  const int h = blockIdx.x, t = threadIdx.x;
+  const float* w = part + (long)h * nsplit * (HD + 2);
+  // the first batch of accumulator values and the (m, l) of the first
+  // ATT_THREADS splits are requested before the position (which sets the
+  // live split count) arrives; indices are clamped to the workspace
+  float x[MB][EPT];
+  auto fetch = [&](int c0, int cmax) {
+#pragma unroll
+    for (int c = 0; c < MB; ++c)
+#pragma unroll
+      for (int e = 0; e < EPT; ++e)
+        x[c][e] = w[(long)min(c0 + c, cmax) * (HD + 2) + 2 + min(t + ATT_THREADS * e, HD - 1)];
+  };
+  fetch(0, nsplit - 1);
+  const int c_t = min(t, nsplit - 1);
+  const float m_t = w[(long)c_t * (HD + 2)], l_t = w[(long)c_t * (HD + 2) + 1];
+  const int T = att_len(dyn[0], window, stride);
+  const int ns = (T + ATT_KCH - 1) / ATT_KCH;
+  if (t < ns) {
+    ml[2 * t] = m_t;
+    ml[2 * t + 1] = l_t;
+  }
+  for (int c = t + ATT_THREADS; c < ns; c += ATT_THREADS) {
+    ml[2 * c] = w[(long)c * (HD + 2)];
+    ml[2 * c + 1] = w[(long)c * (HD + 2) + 1];
+  }
+  float acc[EPT];
+#pragma unroll
+  for (int e = 0; e < EPT; ++e) acc[e] = 0.0f;
+  __syncthreads();
+  if (t < 64) {
+    float M = -INFINITY;
+    for (int c = t; c < ns; c += 64) M = fmaxf(M, ml[2 * c]);
+    M = reduce64<true>(M);
+    float L = 0.0f;
+    for (int c = t; c < ns; c += 64) {
+      const float wc = expf(ml[2 * c] - M);
+      ml[2 * c] = wc;
+      L = fmaf(ml[2 * c + 1], wc, L);
+    }
+    L = reduce64<false>(L);
+    if (t == 0) sL = L;
+  }
+  __syncthreads();
+  for (int c0 = 0; c0 < ns; c0 += MB) {
+    if (c0 > 0) fetch(c0, ns - 1);
+#pragma unroll
+    for (int c = 0; c < MB; ++c)
+      if (c0 + c < ns)
+#pragma unroll
+        for (int e = 0; e < EPT; ++e) acc[e] = fmaf(x[c][e], ml[2 * (c0 + c)], acc[e]);
   }
 #pragma unroll
-  for (int e = 0; e < EPL; ++e) accp[wave][EPL * lane + e] = a[e];
-  __syncthreads();
-  float* out = ws + ((long)h * gridDim.y + sp) * (HD + 2);
-  if (t == 0) {
-    out[0] = m;
-    out[1] = l;
-  }
-  for (int i = t; i < HD; i += ATT_THREADS) out[2 + i] = ((accp[0][i] + accp[1][i]) + accp[2][i]) + accp[3][i];
-}
-
-// out[h] = sum_c acc_c w_c / sum_c l_c w_c, w_c = exp(m_c - M), over the
-// live splits (weights staged in LDS: ns floats of dynamic shared memory);
-// out fp32 or fp16
-template <int YT>
-__global__ void __launch_bounds__(ATT_THREADS) attn_merge_kernel(const float* __restrict__ ws, void* __restrict__ out,
-                                                                 int hd, int nsplit, int stride, int window,
-                                                                 const uint32_t* __restrict__ dyn) {
-  extern __shared__ float wsh[];
-  __shared__ float red[ATT_THREADS / 64];
-  const int h = blockIdx.x, t = threadIdx.x;
-  const int T = att_len(dyn[0], window, stride);
-  const int ns = (T + ATT_CH - 1) / ATT_CH;
-  const float* w = ws + (long)h * nsplit * (hd + 2);
-  float M = -INFINITY;
-  for (int c = t; c < ns; c += ATT_THREADS) M = fmaxf(M, w[(long)c * (hd + 2)]);
-  M = block_max(M, red);
-  float L = 0.0f;
-  for (int c = t; c < ns; c += ATT_THREADS) {
-    const float wc = expf(w[(long)c * (hd + 2)] - M);
-    wsh[c] = wc;
-    L = fmaf(w[(long)c * (hd + 2) + 1], wc, L);
-  }
-  L = block_sum(L, red);  // (its barriers also publish wsh)
-  for (int i = t; i < hd; i += ATT_THREADS) {
-    float a = 0.0f;
-    for (int c = 0; c < ns; ++c) a = fmaf(w[(long)c * (hd + 2) + 2 + i], wsh[c], a);
-    const float v = a / L;
-    if constexpr (YT == Q4_DT_F16) reinterpret_cast<uint16_t*>(out)[h * hd + i] = f2h(v);
-    else reinterpret_cast<float*>(out)[h * hd + i] = v;
+  for (int e = 0; e < EPT; ++e) {
+    const int i = t + ATT_THREADS * e;
+    if (i < HD) {
+      const float v = acc[e] / sL;
+      if constexpr (YT == Q4_DT_F16) reinterpret_cast<uint16_t*>(out)[h * HD + i] = f2h(v);
+      else reinterpret_cast<float*>(out)[h * HD + i] = v;
+    }
   }
 }
 
-static int attn_splits(int stride) { return ceil_div(stride, ATT_CH); }
+static int attn_splits(int stride) { return ceil_div(stride, ATT_KCH); }
+// query heads per attention workgroup: the largest of ATT_HPW, .., 2, 1 dividing grp
+static int attn_hpw(int grp) {
+  int h = ATT_HPW;
+  while (grp % h) h >>= 1;
+  return h;
+}
 
 template <bool FUSE, int YT>
 static void pre_normadd_launch(const void* x, int x_dtype, const float* w, float* h, int D, int M, float sc,
@@ -543,33 +666,39 @@ static int attn_launch(const float* qkv, const float* qnw, const float* cosb, co
   Q4_ARG(nH > 0 && nkv > 0 && grp > 0 && nH == nkv * grp, "need nH == nkv * grp (got %d, %d, %d)", nH, nkv, grp);
   Q4_ARG(hd == 64 || hd == 128 || hd == 256 || hd == 512, "head dim must be 64, 128, 256 or 512 (got %d)", hd);
   Q4_ARG(stride > 0 && window >= 0 && window <= stride && qoff >= 0 && koff >= 0 && voff >= 0, "bad sizes");
-  Q4_ARG(((uintptr_t)kc & 15) == 0, "kc must be 16-byte aligned");
+  Q4_ARG(((uintptr_t)kc & 15) == 0 && ((uintptr_t)vc & 15) == 0, "kc and vc must be 16-byte aligned");
   const size_t need = q4_attn_workspace_bytes(nH, hd, stride);
   Q4_ARG(ws_bytes >= need, "attention workspace too small: %zu < %zu bytes", ws_bytes, need);
-  const int ns = attn_splits(stride);
-  const size_t msh = (size_t)ns * sizeof(float);
+  const int ns = attn_splits(stride), hpw = attn_hpw(grp);
+  const size_t msh = (size_t)2 * ns * sizeof(float);
   Q4_ARG(msh <= 64 * 1024, "cache depth %d needs %d attention splits (more than the merge stages)", stride, ns);
   hipStream_t st = as_stream(stream);
-  float* wsf = reinterpret_cast<float*>(ws);
-  const dim3 grid(nH, ns), blk(ATT_THREADS);
-#define Q4_ATT(E, P)                                                                                            \
+  float* part = reinterpret_cast<float*>(ws);
+  const dim3 grid(nH / hpw, ns), blk(ATT_THREADS);
+  const bool prep = knw != nullptr, h16 = out_dtype == Q4_DT_F16;
+#define Q4_ATT(E, P)                                                                                               \
   hipLaunchKernelGGL((attn_split_kernel<E, P>), grid, blk, 0, st, qkv, qnw, cosb, sinb, kc, vc, stride, window, \
-                     qoff, grp, dyn, wsf, knw, koff, voff)
-  const bool prep = knw != nullptr;
+                     qoff, grp, hpw, dyn, part, ns, knw, koff, voff)
+#define Q4_MRG(E)                                                                                                  \
+  if (h16) hipLaunchKernelGGL((attn_merge_kernel<Q4_DT_F16, E>), dim3(nH), blk, msh, st, part, out, ns, stride,  \
+                              window, dyn);                                                                       \
+  else hipLaunchKernelGGL((attn_merge_kernel<Q4_DT_F32, E>), dim3(nH), blk, msh, st, part, out, ns, stride, window, \
+                          dyn)
   switch (hd) {
-    case 64: if (prep) Q4_ATT(1, true); else Q4_ATT(1, false); break;
-    case 128: if (prep) Q4_ATT(2, true); else Q4_ATT(2, false); break;
-    case 256: if (prep) Q4_ATT(4, true); else Q4_ATT(4, false); break;
-    default: if (prep) Q4_ATT(8, true); else Q4_ATT(8, false); break;
+    case 64: if (prep) { Q4_ATT(1, true); } else { Q4_ATT(1, false); } break;
+    case 128: if (prep) { Q4_ATT(2, true); } else { Q4_ATT(2, false); } break;
+    case 256: if (prep) { Q4_ATT(4, true); } else { Q4_ATT(4, false); } break;
+    default: if (prep) { Q4_ATT(8, true); } else { Q4_ATT(8, false); } break;
   }
-#undef Q4_ATT
   Q4_LAUNCHED("attn_split");
-  if (out_dtype == Q4_DT_F16)
-    hipLaunchKernelGGL(attn_merge_kernel<Q4_DT_F16>, dim3(nH), dim3(ATT_THREADS), msh, st, wsf, out, hd, ns, stride,
-                       window, dyn);
-  else
-    hipLaunchKernelGGL(attn_merge_kernel<Q4_DT_F32>, dim3(nH), dim3(ATT_THREADS), msh, st, wsf, out, hd, ns, stride,
-                       window, dyn);
+  switch (hd) {
+    case 64: Q4_MRG(1); break;
+    case 128: Q4_MRG(2); break;
+    case 256: Q4_MRG(4); break;
+    default: Q4_MRG(8); break;
+  }
+#undef Q4_MRG
+#undef Q4_ATT
   Q4_LAUNCHED("attn_merge");
   return Q4_OK;
 }

@@ -186,6 +186,45 @@ __device__ inline v4u ld16_nt(const void* p) {
   asm volatile("global_load_dwordx4 %0, %1, off nt" : "=v"(r) : "v"(p));
   return r;
 }
+// Cross-lane reductions on VALU (DPP row operations and gfx950's
+// permlane swaps) instead of LDS-routed shuffles: every lane of the group
+// ends with the same bits. Pair order (per lane): quad xor 1, quad xor 2,
+// 8-lane mirror, 16-lane mirror, then rows 0+1 / 2+3 (permlane16 swap),
+// then halves (permlane32 swap).
+template <int CTRL>
+__device__ inline float dpp_f(float v) {
+  return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, 0xF, 0xF, true));
+}
+constexpr int DPP_XOR1 = 0xB1, DPP_XOR2 = 0x4E, DPP_MIRROR8 = 0x141, DPP_MIRROR16 = 0x140;
+template <bool MAX>
+__device__ inline float red_op(float a, float b) {
+  if constexpr (MAX) return fmaxf(a, b);
+  else return a + b;
+}
+template <bool MAX>
+__device__ inline float reduce8(float v) {
+  v = red_op<MAX>(v, dpp_f<DPP_XOR1>(v));
+  v = red_op<MAX>(v, dpp_f<DPP_XOR2>(v));
+  return red_op<MAX>(v, dpp_f<DPP_MIRROR8>(v));
+}
+template <bool MAX>
+__device__ inline float reduce16(float v) {
+  v = reduce8<MAX>(v);
+  return red_op<MAX>(v, dpp_f<DPP_MIRROR16>(v));
+}
+template <bool MAX>
+__device__ inline float reduce32(float v) {
+  v = reduce16<MAX>(v);
+  const auto p = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return red_op<MAX>(__uint_as_float(p[0]), __uint_as_float(p[1]));
+}
+template <bool MAX>
+__device__ inline float reduce64(float v) {
+  v = reduce32<MAX>(v);
+  const auto p = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return red_op<MAX>(__uint_as_float(p[0]), __uint_as_float(p[1]));
+}
+
 template <int N>
 __device__ inline void vmwait() {
   static_assert(N >= 0 && N < 64, "vmcnt range");

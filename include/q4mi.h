@@ -327,10 +327,10 @@ int q4_prepkv(const float* qkv, const float* knw, const float* cosb, const float
 /* Decode attention of nH query heads (q at qoff in qkv; q-norm with qnw,
  * RoPE) over the first T = dyn[0]+1 (or min(dyn[0]+1, window)) cached keys
  * of KV head h/grp: softmax(q.k) weighted sum of V into out[nH*hd] (fp32
- * or fp16, out_dtype). Split
- * along the keys (two launches); ws: q4_attn_workspace_bytes(nH, hd, stride)
- * bytes, no initialisation needed. vk/attn.comp:18-53 (d_attn,
- * src/vk_engine.py:238-239). */
+ * or fp16, out_dtype). Split along the keys (two launches: the splits of
+ * each group of query heads sharing a KV head, then their merge); ws:
+ * q4_attn_workspace_bytes(nH, hd, stride) bytes, no initialisation needed.
+ * vk/attn.comp:18-53 (d_attn, src/vk_engine.py:238-239). */
 size_t q4_attn_workspace_bytes(int nH, int hd, int stride);
 int q4_attn(const float* qkv, const float* qnw, const float* cosb, const float* sinb,
             const uint16_t* kc, const uint16_t* vc, void* out, int out_dtype, int nH, int nkv,

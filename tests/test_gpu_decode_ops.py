@@ -142,6 +142,8 @@ def _attn_case(rng, nH, nkv, hd, stride):
     (16, 8, 256, 1024, 1024, 300),    # two splits, ragged
     (16, 8, 256, 1024, 1024, 5000),   # ring full: T = window
     (16, 2, 512, 2048, 0, 1500),      # global layer, hd 512, grp 8
+    (16, 1, 512, 4096, 0, 4095),      # one KV head for 16 query heads: four head groups, 128 splits
+    (6, 2, 128, 100, 0, 77),          # grp 3: one query head per workgroup
     (4, 4, 64, 40, 0, 39),            # tiny, last slot
 ])
 def test_attn(gpu, nH, nkv, hd, stride, window, pos):
