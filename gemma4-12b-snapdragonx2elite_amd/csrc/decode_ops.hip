@@ -35,8 +35,7 @@ constexpr int ATT_MAX_HD = 512;   // head dims up to 512 (global layers)
 
 // Sum over the workgroup, identical in every thread. red: blockDim/64 floats.
 __device__ inline float block_sum(float v, float* red) {
-#pragma unroll
-  for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
+  v = reduce64<false>(v);
   const int wave = threadIdx.x >> 6, nw = blockDim.x >> 6;
   __syncthreads();  // red may still be read by a previous call
   if ((threadIdx.x & 63) == 0) red[wave] = v;
@@ -46,8 +45,7 @@ __device__ inline float block_sum(float v, float* red) {
   return s;
 }
 __device__ inline float block_max(float v, float* red) {
-#pragma unroll
-  for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, 64));
+  v = reduce64<true>(v);
   const int wave = threadIdx.x >> 6, nw = blockDim.x >> 6;
   __syncthreads();
   if ((threadIdx.x & 63) == 0) red[wave] = v;

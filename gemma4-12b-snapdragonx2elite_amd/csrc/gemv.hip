@@ -137,7 +137,7 @@ template <int YT>
 __device__ inline void store_rows(void* __restrict__ yv, int n, float v, int N, bool live, int gated) {
   int o = n;
   if (gated) {
-    const float up = __shfl_xor(v, 1, 64);
+    const float up = dpp_f<DPP_XOR1>(v);
     if (n & 1) return;
     v = __fmul_rn(gelu_tanh(v), up);
     o = n >> 1;
@@ -178,8 +178,7 @@ constexpr int NX_MAX_K = NX_PER * 4 * GEMV_THREADS;          // 4096 elements
 // Sum over the 4 waves of one 256-thread half, in a fixed order (slot: 4
 // floats of the half's own LDS).
 __device__ inline float half_sum(float v, float* slot) {
-#pragma unroll
-  for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
+  v = reduce64<false>(v);
   if ((threadIdx.x & 63) == 0) slot[(threadIdx.x >> 6) & (GEMV_WAVES - 1)] = v;
   __syncthreads();
   return ((slot[0] + slot[1]) + slot[2]) + slot[3];
@@ -239,17 +238,25 @@ __device__ inline void nx_stage(const NormIn& nx, const v4u* na, const v4u* nh, 
   __syncthreads();
 }
 
-// Rows [lo, lo + cnt) of row group g of Gm over N rows: a balanced partition
-// (counts differ by at most one unit), in units of row pairs for a gated
-// matrix (row 2i = gate row i, 2i + 1 = up row i stay together).
-__device__ inline void group_rows(int g, int Gm, int N, int gated, int& lo, int& cnt) {
+// Rows [lo, lo + cnt) of row group g: a balanced partition of the rows into
+// groups of gq units plus one more unit for the first gr groups (gq, gr =
+// quotient and remainder of the units by the group count, from the host), a
+// unit being a row, or a row pair for a gated matrix (row 2i = gate row i,
+// 2i + 1 = up row i stay together). One 32-bit multiply: the first weight
+// addresses wait for it.
+__device__ inline void group_rows(int g, int gq, int gr, int gated, int& lo, int& cnt) {
   const int u = gated ? 2 : 1;
-  const long Nu = N / u;
-  lo = (int)((long)g * Nu / Gm) * u;
-  cnt = (int)((long)(g + 1) * Nu / Gm) * u - lo;
+  lo = (g * gq + min(g, gr)) * u;
+  cnt = (gq + (g < gr ? 1 : 0)) * u;
+}
+// (gq, gr) of Gm groups over N rows
+__host__ inline void group_split(int N, int Gm, int gated, int& gq, int& gr) {
+  const int Nu = gated ? N / 2 : N;
+  gq = Nu / Gm;
+  gr = Nu % Gm;
 }
 
-// Rows [lo, lo + cnt) (group_rows(g, Gm): cnt <= R) of one GEMV over the K
+// Rows [lo, lo + cnt) (group_rows(g, gq, gr): cnt <= R) of one GEMV over the K
 // slice s of split (the whole K when split == 1); lane row r >= cnt
 // repeats row lo + cnt - 1 and stores nothing. The rows may span two
 // panels. NP = split-K partial stride (>= N).
@@ -268,7 +275,7 @@ __device__ inline void group_rows(int g, int Gm, int N, int gated, int& lo, int&
 template <int R, int U, int XT, int ST, int YT, bool NX = false>
 __device__ __forceinline__ void gemv_rows(const void* __restrict__ xv, const uint4* __restrict__ wq,
                                           const void* __restrict__ scv, float outscale, void* __restrict__ yv,
-                                          int N, int nblk, int g, int Gm, int s, int split, long NP,
+                                          int N, int nblk, int g, int gq, int gr, int s, int split, long NP,
                                           float* __restrict__ part, uint32_t* __restrict__ cnt,
                                           uint32_t* __restrict__ smem, float (*red)[R], int gated,
                                           NormIn nx = {}) {
@@ -319,7 +326,7 @@ __device__ __forceinline__ void gemv_rows(const void* __restrict__ xv, const uin
 
   // (2) first U weight units and scales of the lane: blocks slot, slot + S, ...
   int n0, rows;
-  group_rows(g, Gm, N, gated, n0, rows);
+  group_rows(g, gq, gr, gated, n0, rows);
   const bool live = r < rows;
   const int nl = n0 + min(r, rows - 1);
   const long ubase = ((long)(nl / PANEL) * nblk + b_lo) * PANEL + (nl % PANEL);  // unit of block j: ubase + 64 j
@@ -397,8 +404,7 @@ __device__ __forceinline__ void gemv_rows(const void* __restrict__ xv, const uin
     use(j + t * S, lb + t * SW, u[t], sb[t]);
   });
   // slots of a row: lanes r, r + R, r + 2R, ... of each wave, then the 4 waves
-#pragma unroll
-  for (int off = R; off < 64; off <<= 1) acc += __shfl_xor(acc, off, 64);
+  acc = slot_sum<R>(acc);
   if (lane < R) red[wave][r] = acc;
   __syncthreads();
   if (wave != 0) return;
@@ -438,15 +444,15 @@ template <int R, int U, int XT, int ST, int YT>
 __global__ void __launch_bounds__(2 * GEMV_THREADS)
 gemv_kernel(const void* __restrict__ xv, const uint4* __restrict__ wq, const void* __restrict__ scv, float outscale,
             void* __restrict__ yv, int N, int nblk, int split, float* __restrict__ part, uint32_t* __restrict__ cnt,
-            int gated) {
+            int gated, int gq, int gr) {
   extern __shared__ __attribute__((aligned(16))) uint32_t smem[];
   __shared__ float red[2][GEMV_WAVES][R];
   const int halves = blockDim.x / GEMV_THREADS, half = threadIdx.x / GEMV_THREADS;
   // split-K grids (small matrices only) keep the plain order: their row
   // groups are reduced through the workspace, not through L2 reuse
   const int g = (gridDim.y == 1 ? xcd_major(blockIdx.x, gridDim.x) : blockIdx.x) * halves + half;
-  gemv_rows<R, U, XT, ST, YT>(xv, wq, scv, outscale, yv, N, nblk, g, gridDim.x * halves, blockIdx.y, split, N, part,
-                              cnt, smem + half * stage_words<R, XT>(nblk), red[half], gated);
+  gemv_rows<R, U, XT, ST, YT>(xv, wq, scv, outscale, yv, N, nblk, g, gq, gr, blockIdx.y, split, N, part, cnt,
+                              smem + half * stage_words<R, XT>(nblk), red[half], gated);
 }
 
 // Several activation vectors through one weight stream (speculative-decode
@@ -541,8 +547,7 @@ __device__ __forceinline__ void gemv_rows_mv(const uint16_t* __restrict__ X, int
   });
 #pragma unroll
   for (int v = 0; v < MV; ++v) {
-#pragma unroll
-    for (int off = R; off < 64; off <<= 1) acc[v] += __shfl_xor(acc[v], off, 64);
+    acc[v] = slot_sum<R>(acc[v]);
     if (lane < R) red[wave][v][r] = acc[v];
   }
   __syncthreads();
@@ -741,6 +746,7 @@ struct GemvSeg {
   float outscale;
   int N;
   int g_end;
+  int gq, gr;  // row partition of the segment's groups (group_rows)
 };
 struct GemvSegs {
   GemvSeg s[Q4_GEMV_MAX_BATCH];
@@ -756,15 +762,15 @@ struct SegSel {
   const void* sc;
   void* y;
   float os;
-  int N, g0, Gm;
+  int N, g0, gq, gr;
 };
 __device__ inline SegSel select_seg(const GemvSegs& segs, int g) {
-  SegSel r{segs.s[0].wq, segs.s[0].sc, segs.s[0].y, segs.s[0].outscale, segs.s[0].N, 0, segs.s[0].g_end};
+  SegSel r{segs.s[0].wq, segs.s[0].sc, segs.s[0].y, segs.s[0].outscale, segs.s[0].N, 0, segs.s[0].gq, segs.s[0].gr};
 #pragma unroll
   for (int t = 1; t < Q4_GEMV_MAX_BATCH; ++t) {
     if (t < segs.count && g >= segs.s[t - 1].g_end)
       r = SegSel{segs.s[t].wq, segs.s[t].sc, segs.s[t].y, segs.s[t].outscale, segs.s[t].N, segs.s[t - 1].g_end,
-                 segs.s[t].g_end - segs.s[t - 1].g_end};
+                 segs.s[t].gq, segs.s[t].gr};
   }
   return r;
 }
@@ -787,7 +793,7 @@ gemv_batch_kernel(const void* __restrict__ xv, int nblk, const GemvSegs segs, in
   const int half = threadIdx.x / GEMV_THREADS;
   const int g = wave_group(halves);
   const SegSel q = select_seg(segs, g);
-  gemv_rows<R, U, XT, ST, YT>(xv, q.wq, q.sc, q.os, q.y, q.N, nblk, g - q.g0, q.Gm, 0, 1, 0, nullptr, nullptr,
+  gemv_rows<R, U, XT, ST, YT>(xv, q.wq, q.sc, q.os, q.y, q.N, nblk, g - q.g0, q.gq, q.gr, 0, 1, 0, nullptr, nullptr,
                               smem + half * stage_words<R, XT>(nblk), red[half], 0);
 }
 
@@ -796,14 +802,14 @@ gemv_batch_kernel(const void* __restrict__ xv, int nblk, const GemvSegs segs, in
 template <int R, int U, int ST, int YT>
 __global__ void __launch_bounds__(2 * GEMV_THREADS)
 gemv_nx_kernel(const NormIn nx, const uint4* __restrict__ wq, const void* __restrict__ scv, float outscale,
-               void* __restrict__ yv, int N, int nblk, int gated, int halves) {
+               void* __restrict__ yv, int N, int nblk, int gated, int halves, int gq, int gr) {
   extern __shared__ __attribute__((aligned(16))) uint32_t smem[];
   __shared__ float red[2][GEMV_WAVES][R];
   const int half = threadIdx.x / GEMV_THREADS;
   const int g = wave_group(halves);
-  gemv_rows<R, U, Q4_DT_F16, ST, YT, true>(nullptr, wq, scv, outscale, yv, N, nblk, g, gridDim.x * halves, 0, 1, 0,
-                                           nullptr, nullptr, smem + half * stage_words<R, Q4_DT_F16>(nblk), red[half],
-                                           gated, nx);
+  gemv_rows<R, U, Q4_DT_F16, ST, YT, true>(nullptr, wq, scv, outscale, yv, N, nblk, g, gq, gr, 0, 1, 0, nullptr,
+                                           nullptr, smem + half * stage_words<R, Q4_DT_F16>(nblk), red[half], gated,
+                                           nx);
 }
 template <int R, int U, int ST, int YT>
 __global__ void __launch_bounds__(2 * GEMV_THREADS)
@@ -813,12 +819,13 @@ gemv_batch_nx_kernel(const NormIn nx, int nblk, const GemvSegs segs, int halves)
   const int half = threadIdx.x / GEMV_THREADS;
   const int g = wave_group(halves);
   const SegSel q = select_seg(segs, g);
-  gemv_rows<R, U, Q4_DT_F16, ST, YT, true>(nullptr, q.wq, q.sc, q.os, q.y, q.N, nblk, g - q.g0, q.Gm, 0, 1, 0,
+  gemv_rows<R, U, Q4_DT_F16, ST, YT, true>(nullptr, q.wq, q.sc, q.os, q.y, q.N, nblk, g - q.g0, q.gq, q.gr, 0, 1, 0,
                                            nullptr, nullptr, smem + half * stage_words<R, Q4_DT_F16>(nblk), red[half],
                                            0, nx);
 }
 
-typedef void (*gemv_fn)(const void*, const uint4*, const void*, float, void*, int, int, int, float*, uint32_t*, int);
+typedef void (*gemv_fn)(const void*, const uint4*, const void*, float, void*, int, int, int, float*, uint32_t*, int, int,
+                        int);
 typedef void (*gemv_batch_fn)(const void*, int, const GemvSegs, int);
 struct GemvFns {
   gemv_fn one;
@@ -851,7 +858,7 @@ static GemvFns pick(int R, int U, int xt, int st, int yt) {
   }
 }
 
-typedef void (*gemv_nx_fn)(const NormIn, const uint4*, const void*, float, void*, int, int, int, int);
+typedef void (*gemv_nx_fn)(const NormIn, const uint4*, const void*, float, void*, int, int, int, int, int, int);
 typedef void (*gemv_batch_nx_fn)(const NormIn, int, const GemvSegs, int);
 struct GemvNxFns {
   gemv_nx_fn one;
@@ -1148,17 +1155,20 @@ static int gemv_launch(const void* x, int x_dtype, const uint32_t* wq, const voi
   float* part = pl.ws ? reinterpret_cast<float*>(reinterpret_cast<char*>(ws) + GEMV_TICKET_BYTES) : nullptr;
   const float outscale = scale_fmt == Q4_SCALE_E4M3 ? inv * 256.0f : 1.0f;
   const int hv = pair_groups(groups, pl.split, pl.lds);
+  int gq = 0, gr = 0;
+  group_split(N, groups, gated, gq, gr);
   if (nx) {
     Q4_ARG(pl.split == 1, "internal: fused-norm GEMV planned with split %d", pl.split);
     hipLaunchKernelGGL(pick_nx(pl.R, pl.U, scale_fmt, y_dtype).one, dim3(groups / hv), dim3(GEMV_THREADS * hv),
                        pl.lds * hv, as_stream(stream), *nx, reinterpret_cast<const uint4*>(wq), scales, outscale, y, N,
-                       K / BLK, gated, hv);
+                       K / BLK, gated, hv, gq, gr);
     Q4_LAUNCHED("gemv_normadd");
     return Q4_OK;
   }
   gemv_fn fn = pick(pl.R, pl.U, x_dtype, scale_fmt, y_dtype).one;
   hipLaunchKernelGGL(fn, dim3(groups / hv, pl.split), dim3(GEMV_THREADS * hv), pl.lds * hv, as_stream(stream), x,
-                     reinterpret_cast<const uint4*>(wq), scales, outscale, y, N, K / BLK, pl.split, part, cnt, gated);
+                     reinterpret_cast<const uint4*>(wq), scales, outscale, y, N, K / BLK, pl.split, part, cnt, gated, gq,
+                     gr);
   Q4_LAUNCHED("gemv");
   return Q4_OK;
 }
@@ -1291,6 +1301,7 @@ static int gemv_batch_launch(const void* x, int x_dtype, int K, int scale_fmt, i
     segs.s[i].outscale = scale_fmt == Q4_SCALE_E4M3 ? (inv ? inv[i] : 1.0f) * 256.0f : 1.0f;
     segs.s[i].N = N[i];
     segs.s[i].g_end = groups;
+    group_split(N[i], gm[i], 0, segs.s[i].gq, segs.s[i].gr);
   }
   const int U = units_in_flight(nblk, R, groups);
   const size_t lds = x_stage_lds(nblk, x_dtype, R);

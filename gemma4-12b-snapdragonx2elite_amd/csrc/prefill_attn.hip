@@ -175,8 +175,7 @@ pre_attn_kernel(const void* __restrict__ qin, int ldq, const float* __restrict__
 #pragma unroll
       for (int u = 0; u < 8; ++u) ss = fmaf(qf[j][u], qf[j][u], ss);
     }
-    ss += __shfl_xor(ss, 16, 64);
-    ss += __shfl_xor(ss, 32, 64);
+    ss = slot_reduce<16>(ss);
     const float inv = 1.0f / sqrtf(ss / (float)HD + PA_EPS);
 #pragma unroll
     for (int j = 0; j < NCH; ++j) {
@@ -262,8 +261,7 @@ pre_attn_kernel(const void* __restrict__ qin, int ldq, const float* __restrict__
     for (int st = 0; st < NST; ++st)
 #pragma unroll
       for (int e = 0; e < 4; ++e) tmax = fmaxf(tmax, sc[st][e]);
-    tmax = fmaxf(tmax, __shfl_xor(tmax, 16, 64));
-    tmax = fmaxf(tmax, __shfl_xor(tmax, 32, 64));
+    tmax = slot_reduce<16, true>(tmax);
     const float mnew = fmaxf(mrun, tmax);
     const bool any = mnew != -INFINITY;
     const float corr = any ? expf(mrun - mnew) : 1.0f;
@@ -280,8 +278,7 @@ pre_attn_kernel(const void* __restrict__ qin, int ldq, const float* __restrict__
         psum += (float)p;
         pb[st][e] = p;
       }
-    psum += __shfl_xor(psum, 16, 64);
-    psum += __shfl_xor(psum, 32, 64);
+    psum = slot_reduce<16>(psum);
     lrun = fmaf(lrun, corr, psum);
     mrun = mnew;
 #pragma unroll

@@ -225,6 +225,28 @@ __device__ inline float reduce64(float v) {
   return red_op<MAX>(__uint_as_float(p[0]), __uint_as_float(p[1]));
 }
 
+// Sum (or max) over lanes l, l + R, l + 2R, .. (R = 8, 16, 32, 64), valid
+// in lanes l < R (with R = 16 or 32, in every lane): the xor-8, xor-16,
+// xor-32 pairings of a shuffle loop, each own + partner (so the bits equal
+// those of that loop), on VALU: DPP row rotate by 8 within 16 lanes, then
+// the permlane16 and permlane32 swaps.
+template <int R, bool MAX = false>
+__device__ inline float slot_reduce(float v) {
+  static_assert(R == 8 || R == 16 || R == 32 || R == 64, "slot width");
+  if constexpr (R <= 8) v = red_op<MAX>(v, dpp_f<0x128>(v));  // row_ror:8 = lane ^ 8 within 16
+  if constexpr (R <= 16) {
+    const auto p = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    v = red_op<MAX>(__uint_as_float(p[0]), __uint_as_float(p[1]));
+  }
+  if constexpr (R <= 32) {
+    const auto p = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    v = red_op<MAX>(__uint_as_float(p[0]), __uint_as_float(p[1]));
+  }
+  return v;
+}
+template <int R>
+__device__ inline float slot_sum(float v) { return slot_reduce<R, false>(v); }
+
 template <int N>
 __device__ inline void vmwait() {
   static_assert(N >= 0 && N < 64, "vmcnt range");

@@ -56,7 +56,7 @@ __global__ void absmax_bits_kernel(const float* __restrict__ x, long n, uint32_t
   float m = 0.0f;
   for (long i = (long)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (long)gridDim.x * blockDim.x)
     m = fmaxf(m, fabsf(x[i]));
-  for (int off = 32; off > 0; off >>= 1) m = fmaxf(m, __shfl_xor(m, off, 64));
+  m = reduce64<true>(m);
   if ((threadIdx.x & 63) == 0) atomicMax(out, __float_as_uint(m));  // m >= 0: bit order == value order
 }
 
@@ -119,7 +119,7 @@ __global__ void __launch_bounds__(256) w8_fold_kernel(const uint4* __restrict__ 
 #pragma unroll
     for (int k = 0; k < BLK; ++k) amax = fmaxf(amax, fabsf(__fmul_rn(q[k], s)));
   }
-  for (int off = 32; off > 0; off >>= 1) amax = fmaxf(amax, __shfl_xor(amax, off, 64));
+  amax = reduce64<true>(amax);
   if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = amax;
   __syncthreads();
   amax = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
