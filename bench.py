@@ -546,6 +546,8 @@ def bench_w8a8(ops, iters: int = 50):
         return a.elapsed_time(b) * 1e3 / iters
 
     us = timed(lambda i: ops.gemm_w8a8_packed(A, W8ps[i % nw], sa, sw, N, Y=Y))
+    stamped = w8a8_stamped(ops, lambda i, stp: ops.gemm_w8a8_packed(A, W8ps[i % nw], sa, sw, N, Y=Y, stamps=stp),
+                           M, N, iters)
     us_nk = timed(lambda i: ops.gemm_w8a8(A, W8s[i % nw], sa, sw, Y=Y))
     # W4A8: the same product with B requantized to int8 on the fly from the int4 codes
     del W8s
@@ -567,9 +569,43 @@ def bench_w8a8(ops, iters: int = 50):
             "distinct_weight_sets": nw, "rotated_bytes": nw * N * K, "us": round(us, 2), "TOPS": round(tops, 1),
             "frac_of_int8_peak": round(tops / INT8_PEAK_TOPS, 4),
             "us_row_major_weights": round(us_nk, 2),
+            "stamped": stamped,
             "w4a8_us": round(us_w4, 2), "w4a8_TOPS": round(2.0 * M * N * K / (us_w4 * 1e-6) / 1e12, 1),
             "w4a8_int8_weights_once_us": round(us_w4o, 2),
             "quant_act_us": round(us_q, 2), "quant_act_GBps": round(3 * M * K / (us_q * 1e-6) / 1e9, 1)}
+
+
+def w8a8_stamped(ops, run, M: int, N: int, iters: int):
+    """``iters`` back-to-back launches of the stamped W8A8 (each workgroup
+    reads the wall clock at its start, after its k-loop and at its end, and
+    counts shader cycles): the clock the chip held, how a launch's time
+    splits into k-loop and epilogue, and the gap between launches, measured
+    from inside the run."""
+    import numpy as np
+    import torch
+
+    wgs = ops.w8a8_workgroups(M, N)
+    stamps = torch.zeros((iters, wgs, 4), dtype=torch.int64, device="cuda:0")
+    for i in range(5):
+        run(i, stamps[0])
+    torch.cuda.synchronize()
+    for i in range(iters):
+        run(i, stamps[i])
+    torch.cuda.synchronize()
+    tick_us = 1e3 / ops.probe_wall_clock_khz()
+    s = stamps.cpu().numpy().astype(np.int64)
+    w0, w1, w2, cyc = s[..., 0], s[..., 1], s[..., 2], s[..., 3]
+    ghz = cyc / ((w2 - w0) * tick_us * 1e3)
+    span = (w2.max(1) - w0.min(1)) * tick_us
+    gaps = (w0.min(1)[1:] - w2.max(1)[:-1]) * tick_us
+    half = iters // 2   # the second half: the sustained state
+    return {"launches": iters, "workgroups": wgs,
+            "shader_clock_GHz_median": round(float(np.median(ghz[half:])), 3),
+            "shader_clock_GHz_first_launch": round(float(np.median(ghz[0])), 3),
+            "span_us_median": round(float(np.median(span[half:])), 2),
+            "kloop_us_median": round(float(np.median((w1 - w0)[half:]) * tick_us), 2),
+            "epilogue_us_median": round(float(np.median((w2 - w1)[half:]) * tick_us), 2),
+            "gap_between_launches_us_median": round(float(np.median(gaps[half - 1:])), 2)}
 
 
 def bench_w4a16(ops, iters: int = 50):
@@ -642,8 +678,10 @@ def bench_ceilings(ops):
       reads that many bytes once; best of a sweep of grid sizes, loads in
       flight and chunked/strided order; at the 15360x3840 size also with
       each launch prefetching its successor's first bytes into L2;
-    - mfma: MFMA-only loops (int8 32x32x32, f16 32x32x16), one short launch
-      and 50 back-to-back launches, with the shader clock read back;
+    - mfma: MFMA-only loops (int8 32x32x32, f16 32x32x16), on the same
+      operands every time and on random operands that change with every
+      MFMA, one short launch and 50 back-to-back launches, with the shader
+      clock read back;
     - hipblaslt: torch's int8 (_int_mm) and fp16 (matmul) GEMMs at the W8A8
       and W4A16 shapes, cycling through >= 1 GB of distinct weights."""
     import torch
@@ -687,6 +725,10 @@ def bench_ceilings(ops):
 
     khz = ops.probe_wall_clock_khz()
     mf = {}
+    # random operand bytes (int8 values / f16 values of either sign below 1
+    # in magnitude), a different fragment for every MFMA of a round
+    rnd = torch.randint(-2 ** 31, 2 ** 31 - 1, (16384,), dtype=torch.int32, device=dev, generator=gen)
+    rnd_f16 = rnd & (0xBBFFBBFF - 2 ** 32)
     for kind, nm, per_mfma, peak in ((0, "int8_32x32x32", 65536, INT8_PEAK_TOPS), (1, "f16_32x32x16", 32768,
                                                                                  F16_PEAK_TFLOPS)):
         for wgs in (256, 512):
@@ -695,24 +737,25 @@ def bench_ceilings(ops):
             st = torch.cuda.current_stream()
             ops_per = wgs * 4 * iters * 4 * per_mfma
             res = {}
-            for label, launches in (("short", 1), ("sustained_50", 50)):
-                for _ in range(3):
-                    ops.probe_mfma(kind, wgs, iters, clocks, sink)
-                torch.cuda.synchronize()
-                a = torch.cuda.Event(enable_timing=True)
-                b = torch.cuda.Event(enable_timing=True)
-                a.record(st)
-                for _ in range(launches):
-                    ops.probe_mfma(kind, wgs, iters, clocks, sink)
-                b.record(st)
-                b.synchronize()
-                us = a.elapsed_time(b) * 1e3 / launches
-                c = clocks.cpu().double()
-                ghz = float((c[:, 0] / (c[:, 1] / (khz * 1e3))).median()) / 1e9
-                t = ops_per / (us * 1e-6) / 1e12
-                res[label] = {"us_per_launch": round(us, 2), "T_per_s": round(t, 1),
-                              "frac_of_peak": round(t / peak, 4), "shader_clock_GHz": round(ghz, 3),
-                              "frac_of_peak_at_measured_clock": round(t / (peak * ghz / 2.4), 4)}
+            for opn, operands in (("same_operands", None), ("random_operands", rnd if kind == 0 else rnd_f16)):
+                for label, launches in (("short", 1), ("sustained_50", 50)):
+                    for _ in range(3):
+                        ops.probe_mfma(kind, wgs, iters, clocks, sink, operands)
+                    torch.cuda.synchronize()
+                    a = torch.cuda.Event(enable_timing=True)
+                    b = torch.cuda.Event(enable_timing=True)
+                    a.record(st)
+                    for _ in range(launches):
+                        ops.probe_mfma(kind, wgs, iters, clocks, sink, operands)
+                    b.record(st)
+                    b.synchronize()
+                    us = a.elapsed_time(b) * 1e3 / launches
+                    c = clocks.cpu().double()
+                    ghz = float((c[:, 0] / (c[:, 1] / (khz * 1e3))).median()) / 1e9
+                    t = ops_per / (us * 1e-6) / 1e12
+                    res[f"{opn}_{label}"] = {"us_per_launch": round(us, 2), "T_per_s": round(t, 1),
+                                             "frac_of_peak": round(t / peak, 4), "shader_clock_GHz": round(ghz, 3),
+                                             "frac_of_peak_at_measured_clock": round(t / (peak * ghz / 2.4), 4)}
             mf[f"{nm}_{wgs // 256}wave_per_simd"] = res
     out["mfma"] = mf
     out["wall_clock_khz"] = khz

@@ -65,6 +65,8 @@ SIGNATURES = {
     "q4_w8_packed_bytes": (_sz, [_i, _i]),
     "q4_w8_pack": (_i, [_vp, _i, _i, _vp, _vp]),
     "q4_gemm_w8a8_packed": (_i, [_vp, _vp, _vp, _vp, _i, _vp, _vp, _i, _i, _i, _vp]),
+    "q4_gemm_w8a8_packed_stamped": (_i, [_vp, _vp, _vp, _vp, _i, _vp, _vp, _i, _i, _i, _vp, _sz, _vp]),
+    "q4_gemm_w8a8_packed_workgroups": (_sz, [_i, _i]),
     "q4_cast_f32_f16": (_i, [_vp, _vp, _sz, _vp]),
     "q4_cast_f16_f32": (_i, [_vp, _vp, _sz, _vp]),
     "q4_rmsnorm": (_i, [_vp, _vp, _vp, _i, _i, _vp]),
@@ -77,7 +79,7 @@ SIGNATURES = {
     "q4_prepkv_attn": (_i, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _i, _i, _i, _i, _i, _i, _i, _i, _i, _i, _i, _vp,
                             _vp, _sz, _vp]),
     "q4_probe_stream_read": (_i, [_vp, _sz, _i, _i, _i, _vp, _sz, _sz, _vp, _sz, _vp]),
-    "q4_probe_mfma": (_i, [_i, _i, _i, _vp, _sz, _vp, _sz, _vp]),
+    "q4_probe_mfma": (_i, [_i, _i, _i, _vp, _sz, _vp, _sz, _vp, _sz, _vp]),
     "q4_probe_wall_clock_khz": (_i, [C.POINTER(_i)]),
     "q4_graph_begin": (_i, [_vp]),
     "q4_graph_end": (_i, [_vp, C.POINTER(_vp)]),

@@ -61,6 +61,7 @@ struct GemmArgs {
   int32_t* C;           // int32 [M][N] or NULL
   float* P;             // W4A16 split-K: fp32 partials [split][M][N]
   int M, N, K;
+  unsigned long long* stamps;  // stamped W8A8 only: 4 words per workgroup
 };
 
 // LDS byte offset of 16-byte chunk c (0..3) of staged 64-byte row r. The XOR
@@ -495,7 +496,10 @@ __global__ void __launch_bounds__(256) w8_pack_kernel(const int8_t* __restrict__
 // before the barrier of k-step kt-1. When K % 128 == 64 the packed weights
 // of the last k-step's two missing slices are zero, so the (clamped, stale)
 // activation chunks there add nothing: every k-step runs all four slices.
-template <int BM, bool TAIL>
+// STAMP: thread 0 of workgroup b writes g.stamps[4b ..] = wall clock at the
+// start, after the k-loop and at the end, and shader-clock cycles from start
+// to end (measurement only: the product path is STAMP = false).
+template <int BM, bool TAIL, bool STAMP = false>
 __global__ void __launch_bounds__(256) w8p_kernel(const GemmArgs g) {
   constexpr int S = 4, FM = BM / 32, FN = 2;
   constexpr int AST = BM * 128;        // bytes per A stage
@@ -504,6 +508,23 @@ __global__ void __launch_bounds__(256) w8p_kernel(const GemmArgs g) {
   constexpr int EPI = 4 * 64 * EST * 4;  // four waves' epilogue strips (64 rows each)
   __shared__ __attribute__((aligned(16))) uint8_t ldsA[S * AST > EPI ? S * AST : EPI];
 
+  unsigned long long sw0 = 0, sc0 = 0, sw1 = 0;
+  if constexpr (STAMP) {
+    sw0 = wall_clock64();
+    sc0 = clock64();
+  }
+  auto stamp_end = [&]() {
+    if constexpr (STAMP) {
+      const unsigned long long sw2 = wall_clock64(), sc2 = clock64();
+      if (threadIdx.x == 0) {
+        unsigned long long* o = g.stamps + 4 * (long)blockIdx.x;
+        o[0] = sw0;
+        o[1] = sw1;
+        o[2] = sw2;
+        o[3] = sc2 - sc0;
+      }
+    }
+  };
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int M = g.M, N = g.N, K = g.K;
   int tm, tn;
@@ -654,12 +675,14 @@ __global__ void __launch_bounds__(256) w8p_kernel(const GemmArgs g) {
 #pragma unroll
       for (int q = 0; q < 4; ++q) pin(rb[s][j][q]);
   __syncthreads();  // every direct load landed and every fragment read before the strips reuse LDS
+  if constexpr (STAMP) sw1 = wall_clock64();
 
   uint32_t* strip = reinterpret_cast<uint32_t*>(ldsA) + wave * (64 * EST);
   if constexpr (BM == 256) {
     // a tile wholly inside Y (N % 4 == 0 keeps the 8-byte stores aligned), Y only
     if (m0 + BM <= M && n0 + 256 <= N && !g.C && g.Y && (N & 3) == 0) {
       epilogue_w8_full(g, strip, acc, m0, n0 + 64 * wave);
+      stamp_end();
       return;
     }
   }
@@ -669,6 +692,7 @@ __global__ void __launch_bounds__(256) w8p_kernel(const GemmArgs g) {
     const v16i sub[2][FN] = {{acc[2 * c][0], acc[2 * c][1]}, {acc[2 * c + 1][0], acc[2 * c + 1][1]}};
     epilogue<0, 64, FN>(g, strip, sub, m0 + 64 * c, n0 + 64 * wave, nullptr);
   }
+  stamp_end();
 }
 
 // ---- W4A16, waves split along N -------------------------------------------------
@@ -1277,9 +1301,9 @@ int q4_w8_pack(const int8_t* W8, int N, int K, int8_t* W8p, void* stream) {
   return Q4_OK;
 }
 
-int q4_gemm_w8a8_packed(const int8_t* A, const int8_t* W8p, const float* sa, const void* sw, int sw_dtype,
-                        uint16_t* Y, int32_t* C, int M, int N, int K, void* stream) {
-  clear_error();
+static int gemm_w8a8_packed(const int8_t* A, const int8_t* W8p, const float* sa, const void* sw, int sw_dtype,
+                            uint16_t* Y, int32_t* C, int M, int N, int K, unsigned long long* stamps,
+                            size_t stamps_bytes, void* stream) {
   Q4_ARG(M > 0 && N > 0 && K > 0 && K % 64 == 0, "bad W8A8 shape M=%d N=%d K=%d (K must be a multiple of 64)", M, N,
          K);
   Q4_ARG((long)127 * 127 * K < (1L << 31), "K=%d overflows the int32 accumulator", K);
@@ -1289,18 +1313,43 @@ int q4_gemm_w8a8_packed(const int8_t* A, const int8_t* W8p, const float* sa, con
   Q4_ARG(((uintptr_t)A & 15) == 0 && ((uintptr_t)W8p & 15) == 0, "A and W8p must be 16-byte aligned");
   Q4_ARG((long)M * K < (1L << 31) && (long)q4_w8_packed_bytes(N, K) < (1L << 31),
          "packed W8A8 needs M*K and the packed weights under 2 GiB (32-bit offsets)");
-  GemmArgs g{A, W8p, nullptr, sa, sw, sw_dtype == Q4_DT_F16, Y, C, nullptr, M, N, K};
+  const int bm = pick_bm(M, N);
+  const int wgs = tiles(M, N, bm);
+  if (stamps) Q4_ARG(stamps_bytes >= (size_t)wgs * 32 && ((uintptr_t)stamps & 7) == 0,
+                     "stamps need 4 aligned 8-byte words per workgroup (%d workgroups)", wgs);
+  GemmArgs g{A, W8p, nullptr, sa, sw, sw_dtype == Q4_DT_F16, Y, C, nullptr, M, N, K, stamps};
   const bool tail = K % 128 != 0;
   const hipStream_t st = as_stream(stream);
-  if (pick_bm(M, N) == 256) {
-    if (tail) hipLaunchKernelGGL((w8p_kernel<256, true>), dim3(tiles(M, N, 256)), dim3(256), 0, st, g);
-    else hipLaunchKernelGGL((w8p_kernel<256, false>), dim3(tiles(M, N, 256)), dim3(256), 0, st, g);
+  void (*fn)(const GemmArgs);
+  if (bm == 256) {
+    fn = stamps ? (tail ? w8p_kernel<256, true, true> : w8p_kernel<256, false, true>)
+                : (tail ? w8p_kernel<256, true> : w8p_kernel<256, false>);
   } else {
-    if (tail) hipLaunchKernelGGL((w8p_kernel<128, true>), dim3(tiles(M, N, 128)), dim3(256), 0, st, g);
-    else hipLaunchKernelGGL((w8p_kernel<128, false>), dim3(tiles(M, N, 128)), dim3(256), 0, st, g);
+    fn = stamps ? (tail ? w8p_kernel<128, true, true> : w8p_kernel<128, false, true>)
+                : (tail ? w8p_kernel<128, true> : w8p_kernel<128, false>);
   }
+  hipLaunchKernelGGL(fn, dim3(wgs), dim3(256), 0, st, g);
   Q4_LAUNCHED("gemm_w8a8_packed");
   return Q4_OK;
+}
+
+int q4_gemm_w8a8_packed(const int8_t* A, const int8_t* W8p, const float* sa, const void* sw, int sw_dtype,
+                        uint16_t* Y, int32_t* C, int M, int N, int K, void* stream) {
+  clear_error();
+  return gemm_w8a8_packed(A, W8p, sa, sw, sw_dtype, Y, C, M, N, K, nullptr, 0, stream);
+}
+
+int q4_gemm_w8a8_packed_stamped(const int8_t* A, const int8_t* W8p, const float* sa, const void* sw, int sw_dtype,
+                                uint16_t* Y, int32_t* C, int M, int N, int K, unsigned long long* stamps,
+                                size_t stamps_bytes, void* stream) {
+  clear_error();
+  Q4_ARG(stamps, "null stamps");
+  return gemm_w8a8_packed(A, W8p, sa, sw, sw_dtype, Y, C, M, N, K, stamps, stamps_bytes, stream);
+}
+
+size_t q4_gemm_w8a8_packed_workgroups(int M, int N) {
+  if (M <= 0 || N <= 0) return 0;
+  return (size_t)tiles(M, N, pick_bm(M, N));
 }
 
 int q4_gemm_w4a8(const int8_t* A, const uint32_t* wq, const uint16_t* ratio, const float* sa, const void* sw,

@@ -79,9 +79,14 @@ stream_read_kernel(const uint8_t* __restrict__ buf, long n16, long per_rows, con
 
 // iters rounds of four independent MFMAs per wave; clocks[2 b] = shader
 // clock cycles, clocks[2 b + 1] = wall-clock ticks of workgroup b's wave 0.
-template <bool I8>
+// RND: every MFMA takes another of 8 A and 8 B fragments per lane, read from
+// `operands` at the start (random bytes: the operand bits toggle as real
+// data does, and the chip's clock under that load is the one a GEMM sees);
+// otherwise the same fragments every time.
+template <bool I8, bool RND>
 __global__ void __launch_bounds__(PROBE_THREADS)
-mfma_loop_kernel(int iters, unsigned long long* __restrict__ clocks, int* __restrict__ sink) {
+mfma_loop_kernel(int iters, const v4i* __restrict__ operands, unsigned long long* __restrict__ clocks,
+                 int* __restrict__ sink) {
   const int t = threadIdx.x;
   v16i_p ai[4];
   v16f_p af[4];
@@ -92,16 +97,31 @@ mfma_loop_kernel(int iters, unsigned long long* __restrict__ clocks, int* __rest
       af[j][e] = 0.0f;
     }
   }
-  const v4i a = {t, t * 3 + 1, t ^ 0x55, t + 7}, b = {t * 5, t + 11, t ^ 0x33, t * 7 + 2};
-  const v8h ah = __builtin_bit_cast(v8h, a), bh = __builtin_bit_cast(v8h, b);
+  v4i a[8], b[8];
+#pragma unroll
+  for (int k = 0; k < 8; ++k) {
+    if constexpr (RND) {
+      a[k] = operands[(2 * k) * PROBE_THREADS + t];
+      b[k] = operands[(2 * k + 1) * PROBE_THREADS + t];
+    } else {
+      a[k] = v4i{t, t * 3 + 1, t ^ 0x55, t + 7};
+      b[k] = v4i{t * 5, t + 11, t ^ 0x33, t * 7 + 2};
+    }
+  }
   __syncthreads();
   const unsigned long long c0 = clock64(), r0 = wall_clock64();
-  for (int i = 0; i < iters; ++i) {
+  for (int i = 0; i < iters; i += 8) {
+    static_for<0, 8>([&](auto uc) {
+      constexpr int u = decltype(uc)::value;
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      if constexpr (I8) ai[j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(a, b, ai[j], 0, 0, 0);
-      else af[j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(ah, bh, af[j], 0, 0, 0);
-    }
+      for (int j = 0; j < 4; ++j) {
+        const v4i& x = a[(u + j) & 7];
+        const v4i& y = b[(3 * u + j) & 7];
+        if constexpr (I8) ai[j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(x, y, ai[j], 0, 0, 0);
+        else af[j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(v8h, x), __builtin_bit_cast(v8h, y),
+                                                            af[j], 0, 0, 0);
+      }
+    });
   }
   int s = 0;
 #pragma unroll
@@ -153,15 +173,21 @@ int q4_probe_stream_read(const void* buf, size_t bytes, int wgs, int units, int 
   return Q4_OK;
 }
 
-int q4_probe_mfma(int kind, int wgs, int iters, unsigned long long* clocks, size_t clocks_bytes, int* sink,
-                  size_t sink_bytes, void* stream) {
+int q4_probe_mfma(int kind, int wgs, int iters, const void* operands, size_t operand_bytes,
+                  unsigned long long* clocks, size_t clocks_bytes, int* sink, size_t sink_bytes, void* stream) {
   clear_error();
   Q4_ARG(clocks && sink, "null pointer");
   Q4_ARG(clocks_bytes >= (size_t)wgs * 16 && sink_bytes >= (size_t)wgs * 4, "clocks need 2 and sink 1 word per workgroup");
   Q4_ARG(kind == 0 || kind == 1, "kind 0 (int8 32x32x32) or 1 (f16 32x32x16), got %d", kind);
-  Q4_ARG(wgs >= 1 && wgs <= 65536 && iters >= 1, "bad probe size wgs=%d iters=%d", wgs, iters);
-  hipLaunchKernelGGL(kind == 0 ? mfma_loop_kernel<true> : mfma_loop_kernel<false>, dim3(wgs), dim3(PROBE_THREADS), 0,
-                     as_stream(stream), iters, clocks, sink);
+  Q4_ARG(wgs >= 1 && wgs <= 65536 && iters >= 8 && iters % 8 == 0, "bad probe size wgs=%d iters=%d (a multiple of 8)",
+         wgs, iters);
+  Q4_ARG(!operands || (operand_bytes >= (size_t)16 * PROBE_THREADS * 16 && ((uintptr_t)operands & 15) == 0),
+         "operands: 64 KB, 16-byte aligned (or NULL)");
+  const v4i* ops = reinterpret_cast<const v4i*>(operands);
+  void (*fn)(int, const v4i*, unsigned long long*, int*) =
+      kind == 0 ? (ops ? mfma_loop_kernel<true, true> : mfma_loop_kernel<true, false>)
+                : (ops ? mfma_loop_kernel<false, true> : mfma_loop_kernel<false, false>);
+  hipLaunchKernelGGL(fn, dim3(wgs), dim3(PROBE_THREADS), 0, as_stream(stream), iters, ops, clocks, sink);
   Q4_LAUNCHED("mfma_loop");
   return Q4_OK;
 }

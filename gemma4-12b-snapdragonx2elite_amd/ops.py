@@ -445,8 +445,11 @@ def w8_pack(W8: torch.Tensor) -> torch.Tensor:
 
 
 def gemm_w8a8_packed(A: torch.Tensor, W8p: torch.Tensor, sa: torch.Tensor, sw: torch.Tensor, N: int, *,
-                     want_c: bool = False, Y: torch.Tensor | None = None):
-    """W8A8 on packed weights (:func:`w8_pack`); same results as :func:`gemm_w8a8`."""
+                     want_c: bool = False, Y: torch.Tensor | None = None, stamps: torch.Tensor | None = None):
+    """W8A8 on packed weights (:func:`w8_pack`); same results as :func:`gemm_w8a8`.
+    ``stamps`` (int64 [w8a8_workgroups(M, N), 4]) takes the stamped launch:
+    per workgroup the wall clock at start / after the k-loop / at the end and
+    the shader cycles from start to end."""
     M, K = A.shape
     if A.dtype != torch.int8 or W8p.dtype != torch.int8:
         raise ValueError("gemm_w8a8_packed expects int8 A [M, K] and packed int8 weights")
@@ -456,8 +459,17 @@ def gemm_w8a8_packed(A: torch.Tensor, W8p: torch.Tensor, sa: torch.Tensor, sw: t
     Y = torch.empty((M, N), dtype=torch.float16, device=A.device) if Y is None else Y
     _need(Y, M * N * 2, "Y")
     Cm = torch.empty((M, N), dtype=torch.int32, device=A.device) if want_c else None
-    call("q4_gemm_w8a8_packed", _p(A), _p(W8p), _p(sa), _p(sw), _dt(sw), _p(Y), _p(Cm), M, N, K, _stream())
+    if stamps is None:
+        call("q4_gemm_w8a8_packed", _p(A), _p(W8p), _p(sa), _p(sw), _dt(sw), _p(Y), _p(Cm), M, N, K, _stream())
+    else:
+        call("q4_gemm_w8a8_packed_stamped", _p(A), _p(W8p), _p(sa), _p(sw), _dt(sw), _p(Y), _p(Cm), M, N, K,
+             _p(stamps), _nbytes(stamps), _stream())
     return (Y, Cm) if want_c else Y
+
+
+def w8a8_workgroups(M: int, N: int) -> int:
+    """Workgroups of one :func:`gemm_w8a8_packed` launch (rows of its stamps)."""
+    return int(lib().q4_gemm_w8a8_packed_workgroups(M, N))
 
 
 def w4a8_weights(wq: torch.Tensor, ratio: torch.Tensor, N: int, K: int) -> torch.Tensor:
@@ -782,10 +794,14 @@ def probe_stream_read(buf: torch.Tensor, wgs: int, *, units: int = 8, chunked: b
     return sink
 
 
-def probe_mfma(kind: int, wgs: int, iters: int, clocks: torch.Tensor, sink: torch.Tensor) -> None:
+def probe_mfma(kind: int, wgs: int, iters: int, clocks: torch.Tensor, sink: torch.Tensor,
+               operands: torch.Tensor | None = None) -> None:
     """MFMA-only loop (kind 0 int8 32x32x32, 1 f16 32x32x16); ``clocks`` int64
-    [wgs, 2] receives (shader cycles, wall-clock ticks) per workgroup."""
-    call("q4_probe_mfma", kind, wgs, iters, _p(clocks), _nbytes(clocks), _p(sink), _nbytes(sink), _stream())
+    [wgs, 2] receives (shader cycles, wall-clock ticks) per workgroup;
+    ``operands`` (64 KB of random bytes) makes every MFMA take other operand
+    bits, None repeats the same fragments."""
+    call("q4_probe_mfma", kind, wgs, iters, _p(operands), _nbytes(operands) if operands is not None else 0,
+         _p(clocks), _nbytes(clocks), _p(sink), _nbytes(sink), _stream())
 
 
 def probe_wall_clock_khz() -> int:

@@ -268,6 +268,21 @@ int q4_gemm_w8a8_packed(const int8_t* A, const int8_t* W8p, const float* sa,
                         const void* sw, int sw_dtype, uint16_t* Y,
                         int32_t* C, int M, int N, int K, void* stream);
 
+/* q4_gemm_w8a8_packed with per-workgroup timestamps (measurement; no
+ * counterpart in the reference, which times its GEMMs only from the host,
+ * benchmarks/coopgemm_i8.py:85): stamps[4b .. 4b+3] of workgroup b = wall
+ * clock (q4_probe_wall_clock_khz ticks) at its start, after its k-loop and at
+ * its end, and shader-clock cycles from start to end, so the clock the chip
+ * ran the GEMM at and the main-loop / epilogue split are read from the run
+ * itself. stamps_bytes >= 32 * q4_gemm_w8a8_packed_workgroups(M, N).
+ * Results are those of q4_gemm_w8a8_packed. */
+int q4_gemm_w8a8_packed_stamped(const int8_t* A, const int8_t* W8p, const float* sa,
+                                const void* sw, int sw_dtype, uint16_t* Y,
+                                int32_t* C, int M, int N, int K,
+                                unsigned long long* stamps, size_t stamps_bytes,
+                                void* stream);
+size_t q4_gemm_w8a8_packed_workgroups(int M, int N);
+
 /* W4A8: as W8A8 with B = int8(clamp(rint((q-8) * ratio[n,b]), -127, 127))
  * formed on the fly from the int4 codes and the panel-64 fp16 ratio.
  * vk/coopgemm_w4a8.comp:21-50. */
@@ -411,14 +426,17 @@ int q4_pre_attn(const void* q, int q_dtype, int ldq, const float* qnw,
 int q4_probe_stream_read(const void* buf, size_t bytes, int wgs, int units, int chunked, const void* next,
                          size_t next_bytes, size_t prefetch_bytes, uint32_t* sink, size_t sink_bytes,
                          void* stream);
-/* `iters` rounds of four independent MFMAs per wave, wgs workgroups of four
- * waves: kind 0 = v_mfma_i32_32x32x32_i8 (65536 int ops each), 1 =
- * v_mfma_f32_32x32x16_f16 (32768 flops each). clocks[2b] = shader-clock
- * cycles and clocks[2b+1] = wall-clock ticks (q4_probe_wall_clock_khz) of
- * workgroup b's loop: the matrix-core ceiling and the clock under that load
- * (the counterpart of vk/coopgemm_i8.comp, benchmarks/coopgemm_i8.py:85). */
-int q4_probe_mfma(int kind, int wgs, int iters, unsigned long long* clocks, size_t clocks_bytes, int* sink,
-                  size_t sink_bytes, void* stream);
+/* `iters` (a multiple of 8) rounds of four independent MFMAs per wave, wgs
+ * workgroups of four waves: kind 0 = v_mfma_i32_32x32x32_i8 (65536 int ops
+ * each), 1 = v_mfma_f32_32x32x16_f16 (32768 flops each). operands: 64 KB of
+ * (random) bytes, 8 A and 8 B fragments per lane taken in turn, or NULL for
+ * the same fragments every time (less bit toggling, less power). clocks[2b]
+ * = shader-clock cycles and clocks[2b+1] = wall-clock ticks
+ * (q4_probe_wall_clock_khz) of workgroup b's loop: the matrix-core ceiling
+ * and the clock under that load (the counterpart of vk/coopgemm_i8.comp,
+ * benchmarks/coopgemm_i8.py:85). */
+int q4_probe_mfma(int kind, int wgs, int iters, const void* operands, size_t operand_bytes,
+                  unsigned long long* clocks, size_t clocks_bytes, int* sink, size_t sink_bytes, void* stream);
 int q4_probe_wall_clock_khz(int* khz);
 
 /* ---- record-once submit --------------------------------------------------

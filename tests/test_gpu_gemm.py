@@ -123,6 +123,29 @@ def test_w8a8_packed_config_size_rows(gpu):
     assert (to_np(gY).view(np.uint16) == Y.view(np.uint16)).all()
 
 
+@pytest.mark.parametrize("M,N,K", [(100, 320, 192), (2048, 15360, 3840)])
+def test_w8a8_packed_stamped(gpu, M, N, K):
+    """The stamped launch (per-workgroup clocks) gives the plain launch's
+    results bit for bit, on both tile heights (128 rows below 256 tiles,
+    256 at the full size), and its stamps are ordered: start <= end of the
+    k-loop <= end, cycles > 0."""
+    rng = np.random.default_rng(M + N + K)
+    A, sa, W8, sw = _w8a8_case(rng, M, N, K)
+    gA, gsa, gsw = torch.from_numpy(A).cuda(), torch.from_numpy(sa).cuda(), torch.from_numpy(sw).cuda()
+    W8p = torch.from_numpy(O.pack_w8_dev(W8)).cuda()
+    wgs = gpu.w8a8_workgroups(M, N)
+    assert wgs == (-(-M // 256) * -(-N // 256) if -(-M // 256) * -(-N // 256) >= 256 else -(-M // 128) * -(-N // 256))
+    stamps = torch.zeros((wgs, 4), dtype=torch.int64, device="cuda")
+    gY, gC = gpu.gemm_w8a8_packed(gA, W8p, gsa, gsw, N, want_c=True)
+    sY, sC = gpu.gemm_w8a8_packed(gA, W8p, gsa, gsw, N, want_c=True, stamps=stamps)
+    assert (to_np(sC) == to_np(gC)).all()
+    assert (to_np(sY).view(np.uint16) == to_np(gY).view(np.uint16)).all()
+    s = to_np(stamps)
+    assert (s[:, 0] > 0).all() and (s[:, 0] <= s[:, 1]).all() and (s[:, 1] <= s[:, 2]).all() and (s[:, 3] > 0).all()
+    with pytest.raises(RuntimeError, match="stamps"):
+        gpu.gemm_w8a8_packed(gA, W8p, gsa, gsw, N, stamps=stamps[: wgs - 1])
+
+
 # ------------------------------------------------------------------ W4A8
 @pytest.mark.parametrize("M,N,K", [(64, 256, 64), (100, 512, 3840), (33, 300, 320), (128, 15360, 3840)])
 def test_w4a8_bit_exact(gpu, M, N, K):
