@@ -21,7 +21,10 @@
 //    triples. The grid covers the cache capacity and splits past the current
 //    length exit at once, so the launch shape does not depend on the
 //    position; a 1024-key window of 8 KV heads with 2 query heads each is
-//    256 workgroups.
+//    256 workgroups. Per-head vector work (q/k norms, RoPE) runs once per
+//    wave in row layout (EPL elements per lane: 64-lane sums, the RoPE
+//    partner from lane l ^ 32), not once per key row: the kernel is bound by
+//    VALU issue and latency, not by its 8 MB of reads.
 #include "q4mi_common.h"
 
 namespace q4 {
@@ -215,6 +218,103 @@ __global__ void __launch_bounds__(ATT_THREADS) prepkv_kernel(const float* __rest
   for (int i = t; i < hd; i += ATT_THREADS) vc[o + i] = f2h(hv[i]);
 }
 
+// Row layout of one head vector of HD = 64 EPL fp32 values over a wave:
+// lane l holds elements EPL l .. EPL l + EPL - 1. The rotate-half partner
+// of element i (i +- HD / 2) is the same element slot of lane l +- 32.
+template <int EPL>
+__device__ inline void ld_row(const float* __restrict__ p, float (&v)[EPL]) {
+  const float* q = p + EPL * (threadIdx.x & 63);
+  if constexpr (EPL >= 4) {
+#pragma unroll
+    for (int c = 0; c < EPL / 4; ++c) {
+      const float4 f = *reinterpret_cast<const float4*>(q + 4 * c);
+      v[4 * c] = f.x;
+      v[4 * c + 1] = f.y;
+      v[4 * c + 2] = f.z;
+      v[4 * c + 3] = f.w;
+    }
+  } else if constexpr (EPL == 2) {
+    const float2 f = *reinterpret_cast<const float2*>(q);
+    v[0] = f.x;
+    v[1] = f.y;
+  } else {
+    v[0] = q[0];
+  }
+}
+
+// Sum of squares over the wave, the same bits in every lane: each lane's
+// elements in order, then the 64-lane pairing levels of reduce64.
+template <int EPL>
+__device__ inline float row_sumsq(const float (&v)[EPL]) {
+  float s = 0.0f;
+#pragma unroll
+  for (int e = 0; e < EPL; ++e) s = fmaf(v[e], v[e], s);
+  return reduce64<false>(s);
+}
+
+// x <- RoPE((x * inv(x)) * w) for a row-layout vector (the arithmetic of
+// norm_rope_head per element; the partner comes from lane l ^ 32).
+template <int EPL>
+__device__ inline void row_norm_rope(float (&x)[EPL], const float (&w)[EPL], const float (&cs)[EPL],
+                                     const float (&sn)[EPL]) {
+  constexpr int HD = 64 * EPL;
+  const float inv = inv_rms(row_sumsq<EPL>(x), HD);
+  const bool lo = (threadIdx.x & 63) < 32;
+#pragma unroll
+  for (int e = 0; e < EPL; ++e) {
+    const float y = __fmul_rn(__fmul_rn(x[e], inv), w[e]);
+    const auto p = __builtin_amdgcn_permlane32_swap(__float_as_uint(y), __float_as_uint(y), false, false);
+    const float pr = __uint_as_float(lo ? p[1] : p[0]);
+    x[e] = __fadd_rn(__fmul_rn(y, cs[e]), __fmul_rn(lo ? -pr : pr, sn[e]));
+  }
+}
+
+// This token's K (k-norm with weight, RoPE) and V (v-norm) of one KV head in
+// row layout, rounded to fp16 as the cache holds them. Each value is rounded
+// to fp32 before the fp16 conversion (two roundings, as the reference's
+// float16_t(v * inv)). prepkv_row_kernel and the attention with prepkv
+// folded in both use this, so their cache rows are the same bits.
+template <int EPL>
+__device__ inline void fresh_kv(float (&k)[EPL], const float (&v)[EPL], const float (&knw)[EPL],
+                                const float (&cs)[EPL], const float (&sn)[EPL], uint16_t (&kb)[EPL],
+                                uint16_t (&vb)[EPL]) {
+  constexpr int HD = 64 * EPL;
+  row_norm_rope<EPL>(k, knw, cs, sn);
+#pragma unroll
+  for (int e = 0; e < EPL; ++e) kb[e] = f2h_after_f32(k[e]);
+  const float iv = inv_rms(row_sumsq<EPL>(v), HD);
+#pragma unroll
+  for (int e = 0; e < EPL; ++e) vb[e] = f2h_after_f32(__fmul_rn(v[e], iv));
+}
+
+// prepkv for the attention's head dims (64 EPL): one wave per KV head
+// (vk/prepkv.comp:16-30).
+template <int EPL>
+__global__ void __launch_bounds__(64) prepkv_row_kernel(const float* __restrict__ qkv, const float* __restrict__ knw,
+                                                        const float* __restrict__ cs, const float* __restrict__ sn,
+                                                        uint16_t* __restrict__ kc, uint16_t* __restrict__ vc,
+                                                        int koff, int voff, int stride, int window,
+                                                        const uint32_t* __restrict__ dyn) {
+  constexpr int HD = 64 * EPL;
+  const int kvh = blockIdx.x, lane = threadIdx.x;
+  const int slot = kv_slot(dyn[0], window);
+  if (slot >= stride) return;
+  float k[EPL], v[EPL], w[EPL], c[EPL], sv[EPL];
+  ld_row<EPL>(qkv + koff + kvh * HD, k);
+  ld_row<EPL>(qkv + voff + kvh * HD, v);
+  ld_row<EPL>(knw, w);
+  ld_row<EPL>(cs, c);
+  ld_row<EPL>(sn, sv);
+  uint16_t kb[EPL], vb[EPL];
+  fresh_kv<EPL>(k, v, w, c, sv, kb, vb);
+  const long o = ((long)kvh * stride + slot) * HD;
+#pragma unroll
+  for (int e = 0; e < EPL; ++e) {
+    kc[o + EPL * lane + e] = kb[e];
+    vc[o + EPL * lane + e] = vb[e];
+  }
+}
+
 // Prefill: K and V of KV head blockIdx.x of token blockIdx.y (position
 // dyn[0] + token) into the token's slot, with the token's cos/sin row
 // (vk/pre_prepkv.comp:18-32). k, v: [M][ld] rows of fp32 or fp16 (the
@@ -275,53 +375,57 @@ __device__ inline HalfVec<E> ld_halves(const uint16_t* p) {
 // flash-decoding). Workgroup (g, s): head group g = hpw query heads of one
 // KV head (they share that KV head's rows, so the rows are read once for all
 // of them) and keys [ATT_KCH s, ATT_KCH (s + 1)) of the current length; wave
-// w takes 8 of those keys. Every global load of the split is issued first,
-// none of them waiting for the position: the wave's K rows (8 lanes per row,
-// lane c reading its 16-byte chunks c, c + 8, ..: a row's 8 lanes cover 128
-// contiguous bytes per load), its V rows (one coalesced row per key, lane l
-// owning elements EPL l ..; rows clamped to the cache, rows past the length
-// masked), the raw q of the group's heads, this KV head's raw k and v of
-// this token, the norm weights and the RoPE row. The vectors in use are then
-// normalised together (one reduction round), q (and k) get RoPE, the scores
-// of each head come from the same K registers (3 shuffle levels per key),
-// and per head the split's maximum m, sum l of exp(s - m) and unnormalised
-// p V go to the workspace for attn_merge_kernel. Splits past the length
-// exit at once (the grid covers the cache depth, so a captured graph replays
-// every position).
+// w takes 8 of those keys. Every global load is issued first, none of them
+// waiting for the position: the wave's K rows (8 lanes per row, lane c8
+// reading 16-byte chunks c8, c8 + 8, ..: 128 contiguous bytes per row and
+// load), its V rows (one coalesced row per key, lane l owning elements
+// EPL l ..; rows clamped to the cache, rows past the length masked), and in
+// row layout (EPL elements per lane) the raw q of the group's heads, the
+// q-norm weight and the RoPE row (and this token's raw k, v and k-norm
+// weight). Each wave normalises and rotates the q heads in row layout (a
+// 64-lane sum, the RoPE partner from lane l ^ 32) and hands them to its K
+// layout through its own LDS area (no barrier); the score of each head
+// comes from the same K registers (8-lane sums). Two barriers: after the
+// scores (every wave takes the split's softmax per head from LDS: m, l, and
+// the p of its own keys by lane broadcast) and after the waves' p V
+// partials. Per head the split's maximum m, sum l of exp(s - m) and
+// unnormalised p V go to the workspace for attn_merge_kernel. Splits past
+// the length exit at once (the grid covers the cache depth, so a captured
+// graph replays every position).
 //
 // With PREP (prepkv folded in, vk/prepkv.comp:16-30): the split holding this
-// token's slot forms its K (k-norm with weight, RoPE) and V (v-norm),
-// rounded to fp16 as the cache holds them, uses them for that key in place
-// of the cache row, and the first head group of each KV head writes them to
-// the cache for the next tokens; no other workgroup reads that row.
+// token's slot forms its K and V with fresh_kv (the same bits as
+// prepkv_row_kernel), uses them for that key in place of the cache row, and
+// the first head group of each KV head writes them to the cache for the
+// next tokens; no other workgroup reads that row.
 template <int EPL, bool PREP>
 __global__ void __launch_bounds__(ATT_THREADS)
 attn_split_kernel(const float* __restrict__ qkv, const float* __restrict__ qnw, const float* __restrict__ cs,
                   const float* __restrict__ sn, uint16_t* __restrict__ kc, uint16_t* __restrict__ vc, int stride,
                   int window, int qoff, int grp, int hpw, const uint32_t* __restrict__ dyn, float* __restrict__ part,
                   int nsplit, const float* __restrict__ knw, int koff, int voff) {
-  constexpr int HD = 64 * EPL, KPW = ATT_KCH / (ATT_THREADS / 64);  // 8 keys per wave
-  constexpr int EPT = (HD + ATT_THREADS - 1) / ATT_THREADS;        // vector elements per thread
-  constexpr int NV = ATT_HPW + 2;                                  // q heads, k, v
+  constexpr int HD = 64 * EPL, NW = ATT_THREADS / 64, KPW = ATT_KCH / NW;  // 8 keys per wave
+  constexpr int NR = PREP ? ATT_HPW + 1 : ATT_HPW;  // row-layout vectors handed to the K layout: q heads (, k)
   static_assert(KPW == 8, "one K row per 8 lanes");
-  __shared__ float vec[NV][HD];                   // raw, then normalised vectors
-  __shared__ float qr[ATT_HPW][HD];               // q after RoPE
-  __shared__ float p[ATT_HPW][ATT_KCH], sml[ATT_HPW][2];
-  __shared__ float red[NV][ATT_THREADS / 64];
-  __shared__ float accp[ATT_THREADS / 64][HD];
-  const int g = blockIdx.x, sp = blockIdx.y, t = threadIdx.x, wave = t >> 6, lane = t & 63;
+  __shared__ __attribute__((aligned(16))) float rows[NW][NR][HD];
+  __shared__ float ps[ATT_HPW][ATT_KCH];
+  __shared__ float accp[NW][ATT_HPW][HD];
+  const int g = blockIdx.x, sp = blockIdx.y, t = threadIdx.x, lane = t & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(t >> 6);
   const int gpk = grp / hpw;  // head groups per KV head
   const int kvh = g / gpk, h0 = g * hpw;
   const int j0 = sp * ATT_KCH;
   const long kv0 = (long)kvh * stride * HD;
+  const int kk = lane >> 3, c8 = lane & 7;
+  const int key = KPW * wave + kk;  // this lane's K row within the split
 
   // (1) every global load of the split
-  const int kk = lane >> 3, c8 = lane & 7;  // K: key kk of the wave, chunks c8 + 8 m
   v4u ku[EPL];
   {
-    const int j = min(j0 + KPW * wave + kk, stride - 1);
+    const int j = min(j0 + key, stride - 1);
 #pragma unroll
-    for (int m = 0; m < EPL; ++m) ku[m] = *reinterpret_cast<const v4u*>(kc + kv0 + (long)j * HD + 8 * (c8 + 8 * m));
+    for (int m = 0; m < EPL; ++m)
+      ku[m] = *reinterpret_cast<const v4u*>(kc + kv0 + (long)j * HD + 8 * (c8 + 8 * m));
   }
   HalfVec<EPL> vv[KPW];
 #pragma unroll
@@ -329,18 +433,17 @@ attn_split_kernel(const float* __restrict__ qkv, const float* __restrict__ qnw, 
     const int j = min(j0 + KPW * wave + k, stride - 1);
     vv[k] = ld_halves<EPL>(vc + kv0 + (long)j * HD + EPL * lane);
   }
-  float raw[NV][EPT], wq[EPT], wk[EPT], csv[EPT], snv[EPT];
+  float q[ATT_HPW][EPL], wq[EPL], cr[EPL], sr[EPL], kr[EPL], vr[EPL], wk[EPL];
 #pragma unroll
-  for (int e = 0; e < EPT; ++e) {
-    const int i = min(t + ATT_THREADS * e, HD - 1);
-#pragma unroll
-    for (int h = 0; h < ATT_HPW; ++h) raw[h][e] = h < hpw ? qkv[qoff + (h0 + h) * HD + i] : 0.0f;
-    raw[ATT_HPW][e] = PREP ? qkv[koff + kvh * HD + i] : 0.0f;
-    raw[ATT_HPW + 1][e] = PREP ? qkv[voff + kvh * HD + i] : 0.0f;
-    wq[e] = qnw[i];
-    wk[e] = PREP ? knw[i] : 0.0f;
-    csv[e] = cs[i];
-    snv[e] = sn[i];
+  for (int h = 0; h < ATT_HPW; ++h)
+    if (h < hpw) ld_row<EPL>(qkv + qoff + (h0 + h) * HD, q[h]);
+  ld_row<EPL>(qnw, wq);
+  ld_row<EPL>(cs, cr);
+  ld_row<EPL>(sn, sr);
+  if constexpr (PREP) {
+    ld_row<EPL>(qkv + koff + kvh * HD, kr);
+    ld_row<EPL>(qkv + voff + kvh * HD, vr);
+    ld_row<EPL>(knw, wk);
   }
   const uint32_t pos = dyn[0];
   const int T = att_len(pos, window, stride);
@@ -352,136 +455,129 @@ attn_split_kernel(const float* __restrict__ qkv, const float* __restrict__ qnw, 
   const int slot = kv_slot(pos, window);
   const bool fresh_split = PREP && slot < stride && slot >= j0 && slot < j0 + n;  // workgroup-uniform
   const int kslot = fresh_split ? slot - j0 : -1;
-  const int nvec = fresh_split ? NV : hpw;  // vectors in use: q heads h < hpw, k and v when fresh
-  auto used = [&](int v) { return v < ATT_HPW ? v < hpw : fresh_split; };
 
-  // (2) norms (weights: qnw for q, knw for k, none for v), one reduction round
+  // (2) q heads in row layout -> this wave's LDS rows; with the fresh slot
+  //     in this split, this token's K and V (K also through the LDS rows)
+  float(*rw)[HD] = rows[wave];
 #pragma unroll
-  for (int v = 0; v < NV; ++v) {
-    if (!used(v)) continue;
-    float sq = 0.0f;
+  for (int h = 0; h < ATT_HPW; ++h) {
+    if (h >= hpw) break;
+    row_norm_rope<EPL>(q[h], wq, cr, sr);
 #pragma unroll
-    for (int e = 0; e < EPT; ++e)
-      if (t + ATT_THREADS * e < HD) sq = fmaf(raw[v][e], raw[v][e], sq);
-    sq = reduce64<false>(sq);
-    if (lane == 0) red[v][wave] = sq;
+    for (int e = 0; e < EPL; ++e) rw[h][EPL * lane + e] = q[h][e];
   }
-  (void)nvec;
-  __syncthreads();
+  float vnew[EPL];
+  if constexpr (PREP) {
+    if (fresh_split) {
+      uint16_t kb[EPL], vb[EPL];
+      fresh_kv<EPL>(kr, vr, wk, cr, sr, kb, vb);
 #pragma unroll
-  for (int v = 0; v < NV; ++v) {
-    if (!used(v)) continue;
-    float sq = 0.0f;
-    for (int w = 0; w < ATT_THREADS / 64; ++w) sq += red[v][w];
-    const float inv = inv_rms(sq, HD);
-#pragma unroll
-    for (int e = 0; e < EPT; ++e) {
-      const int i = t + ATT_THREADS * e;
-      const float wt = v < ATT_HPW ? wq[e] : wk[e];
-      if (i < HD) vec[v][i] = v <= ATT_HPW ? __fmul_rn(__fmul_rn(raw[v][e], inv), wt) : __fmul_rn(raw[v][e], inv);
-    }
-  }
-  __syncthreads();
-  // RoPE (rotate-half) of the q heads and k
-  constexpr int HF = HD / 2;
-#pragma unroll
-  for (int v = 0; v < ATT_HPW + 1; ++v) {
-    if (!used(v)) continue;
-#pragma unroll
-    for (int e = 0; e < EPT; ++e) {
-      const int i = t + ATT_THREADS * e;
-      if (i < HD) {
-        const float r = i < HF ? -vec[v][i + HF] : vec[v][i - HF];
-        const float o = __fadd_rn(__fmul_rn(vec[v][i], csv[e]), __fmul_rn(r, snv[e]));
-        if (v < ATT_HPW) qr[v][i] = o;
-        else raw[ATT_HPW][e] = o;  // k after RoPE, kept in registers until vec is free
+      for (int e = 0; e < EPL; ++e) {
+        rw[ATT_HPW][EPL * lane + e] = h2f(kb[e]);
+        vnew[e] = h2f(vb[e]);
       }
-    }
-  }
-  __syncthreads();
-  float* knew = vec[ATT_HPW];
-  float* vnew = vec[ATT_HPW + 1];
-  if (fresh_split) {  // this token's K and V, rounded to fp16 as the cache holds them
+      if (g % gpk == 0 && wave == 0) {
+        const long o = ((long)kvh * stride + slot) * HD;
 #pragma unroll
-    for (int e = 0; e < EPT; ++e) {
-      const int i = t + ATT_THREADS * e;
-      if (i < HD) {
-        const uint16_t kb = f2h(raw[ATT_HPW][e]), vb = f2h(vnew[i]);
-        knew[i] = h2f(kb);
-        vnew[i] = h2f(vb);
-        if (g % gpk == 0) {
-          const long o = ((long)kvh * stride + slot) * HD;
-          kc[o + i] = kb;
-          vc[o + i] = vb;
+        for (int e = 0; e < EPL; ++e) {
+          kc[o + EPL * lane + e] = kb[e];
+          vc[o + EPL * lane + e] = vb[e];
         }
       }
     }
-    __syncthreads();
   }
+  // (the wave reads back what it wrote: its LDS operations run in order)
+  __builtin_amdgcn_wave_barrier();
 
-  // (3) scores: the 8 lanes of a key row reduce with xor-shuffles
-  {
-    const int key = KPW * wave + kk;
-    const bool fresh = PREP && key == kslot;
-    for (int h = 0; h < hpw; ++h) {
-      float d = 0.0f;
+  // (3) scores: this lane's K row (or this token's K) against each q head in
+  //     K layout, 8-lane sums
+  const bool fresh = PREP && key == kslot;
+  float kf[EPL][8];
 #pragma unroll
-      for (int m = 0; m < EPL; ++m) {
-        const int b = 8 * (c8 + 8 * m);
+  for (int m = 0; m < EPL; ++m)
 #pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          const float k0 = fresh ? knew[b + 2 * e] : h2f((uint16_t)(ku[m][e] & 0xFFFFu));
-          const float k1 = fresh ? knew[b + 2 * e + 1] : h2f((uint16_t)(ku[m][e] >> 16));
-          d = fmaf(qr[h][b + 2 * e], k0, d);
-          d = fmaf(qr[h][b + 2 * e + 1], k1, d);
-        }
-      }
-      d = reduce8<false>(d);
-      if (c8 == 0) p[h][key] = key < n ? d : -INFINITY;
+    for (int e = 0; e < 4; ++e) {
+      kf[m][2 * e] = h2f((uint16_t)(ku[m][e] & 0xFFFFu));
+      kf[m][2 * e + 1] = h2f((uint16_t)(ku[m][e] >> 16));
     }
+  if (fresh) {
+#pragma unroll
+    for (int m = 0; m < EPL; ++m)
+#pragma unroll
+      for (int e = 0; e < 8; ++e) kf[m][e] = rw[ATT_HPW][8 * (c8 + 8 * m) + e];
+  }
+#pragma unroll
+  for (int h = 0; h < ATT_HPW; ++h) {
+    if (h >= hpw) break;
+    float d = 0.0f;
+#pragma unroll
+    for (int m = 0; m < EPL; ++m) {
+      const float4 a = *reinterpret_cast<const float4*>(&rw[h][8 * (c8 + 8 * m)]);
+      const float4 b = *reinterpret_cast<const float4*>(&rw[h][8 * (c8 + 8 * m) + 4]);
+      const float qv[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
+#pragma unroll
+      for (int e = 0; e < 8; ++e) d = fmaf(qv[e], kf[m][e], d);
+    }
+    d = reduce8<false>(d);
+    if (c8 == 0) ps[h][key] = key < n ? d : -INFINITY;
   }
   __syncthreads();
-  // (4) softmax of the split, 32 lanes per head
-  if (t < hpw * ATT_KCH) {
-    const int h = t / ATT_KCH, key = t % ATT_KCH;
-    const float sc = p[h][key];
-    static_assert(ATT_KCH == 32, "one 32-lane row pair per head");
+
+  // (4) softmax of the split, two heads per wave pass (lanes 0-31, 32-63),
+  //     in every wave: m and l, and the p of this wave's keys by broadcast
+  float pw[ATT_HPW][KPW], mh[ATT_HPW], lh[ATT_HPW];
+#pragma unroll
+  for (int hb = 0; hb < ATT_HPW; hb += 2) {
+    if (hb >= hpw) break;
+    const int h = hb + (lane >> 5);
+    const float sc = h < hpw ? ps[h][lane & 31] : -INFINITY;
     const float m = reduce32<true>(sc);
     const float pj = sc != -INFINITY ? expf(sc - m) : 0.0f;
     const float l = reduce32<false>(pj);
-    p[h][key] = pj;
-    if (key == 0) {
-      sml[h][0] = m;
-      sml[h][1] = l;
+#pragma unroll
+    for (int u = 0; u < 2; ++u) {
+#pragma unroll
+      for (int k = 0; k < KPW; ++k)
+        pw[hb + u][k] = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(pj), 32 * u + KPW * wave + k));
+      mh[hb + u] = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(m), 32 * u));
+      lh[hb + u] = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(l), 32 * u));
     }
   }
-  __syncthreads();
-  // (5) unnormalised p V per head from the same V registers; waves meet in LDS
-  for (int h = 0; h < hpw; ++h) {
+
+  // (5) unnormalised p V of every head from the same V registers; the waves
+  //     meet in LDS
+  float vf[KPW][EPL];
+#pragma unroll
+  for (int k = 0; k < KPW; ++k)
+#pragma unroll
+    for (int e = 0; e < EPL; ++e) vf[k][e] = (PREP && KPW * wave + k == kslot) ? vnew[e] : h2f(vv[k].h[e]);
+#pragma unroll
+  for (int h = 0; h < ATT_HPW; ++h) {
+    if (h >= hpw) break;
     float a[EPL];
 #pragma unroll
     for (int e = 0; e < EPL; ++e) a[e] = 0.0f;
 #pragma unroll
-    for (int k = 0; k < KPW; ++k) {
-      const float pw = p[h][KPW * wave + k];
-      if (PREP && KPW * wave + k == kslot) {  // this token's value row
+    for (int k = 0; k < KPW; ++k)
 #pragma unroll
-        for (int e = 0; e < EPL; ++e) a[e] = fmaf(pw, vnew[EPL * lane + e], a[e]);
-      } else {
+      for (int e = 0; e < EPL; ++e) a[e] = fmaf(pw[h][k], vf[k][e], a[e]);
 #pragma unroll
-        for (int e = 0; e < EPL; ++e) a[e] = fmaf(pw, h2f(vv[k].h[e]), a[e]);
-      }
-    }
-#pragma unroll
-    for (int e = 0; e < EPL; ++e) accp[wave][EPL * lane + e] = a[e];
-    __syncthreads();
+    for (int e = 0; e < EPL; ++e) accp[wave][h][EPL * lane + e] = a[e];
+  }
+  __syncthreads();
+  for (int i = t; i < hpw * HD; i += ATT_THREADS) {
+    const int h = i / HD, c = i % HD;
     float* o = part + ((long)(h0 + h) * nsplit + sp) * (HD + 2);
-    if (t == 0) {
-      o[0] = sml[h][0];
-      o[1] = sml[h][1];
+    o[2 + c] = ((accp[0][h][c] + accp[1][h][c]) + accp[2][h][c]) + accp[3][h][c];
+  }
+  if (t == 0) {
+#pragma unroll
+    for (int h = 0; h < ATT_HPW; ++h) {
+      if (h >= hpw) break;
+      float* o = part + ((long)(h0 + h) * nsplit + sp) * (HD + 2);
+      o[0] = mh[h];
+      o[1] = lh[h];
     }
-    for (int i = t; i < HD; i += ATT_THREADS) o[2 + i] = ((accp[0][i] + accp[1][i]) + accp[2][i]) + accp[3][i];
-    __syncthreads();  // accp is rewritten by the next head
   }
 }
 
@@ -644,8 +740,25 @@ int q4_prepkv(const float* qkv, const float* knw, const float* cosb, const float
   Q4_ARG(nkv > 0 && stride > 0 && window >= 0 && koff >= 0 && voff >= 0, "bad sizes");
   Q4_ARG(hd > 0 && hd % 2 == 0 && hd <= ATT_MAX_HD, "head dim must be even and <= %d (got %d)", ATT_MAX_HD, hd);
   Q4_ARG(window <= stride, "window %d exceeds the cache depth %d", window, stride);
-  hipLaunchKernelGGL(prepkv_kernel, dim3(nkv), dim3(ATT_THREADS), 0, as_stream(stream), qkv, knw, cosb, sinb, kc, vc,
-                     hd, koff, keqv ? koff : voff, stride, window, dyn);
+  Q4_ARG(((uintptr_t)qkv & 15) == 0 && ((uintptr_t)knw & 15) == 0 && ((uintptr_t)cosb & 15) == 0 &&
+             ((uintptr_t)sinb & 15) == 0 && koff % 4 == 0 && voff % 4 == 0,
+         "qkv, knw, cos and sin must be 16-byte aligned and the k/v offsets multiples of 4 elements");
+  const hipStream_t st = as_stream(stream);
+  const int vo = keqv ? koff : voff;
+  // head dims the attention takes: the attention's own layouts and sums, so
+  // these rows equal those of q4_prepkv_attn bit for bit
+  switch (hd) {
+    case 64: hipLaunchKernelGGL(prepkv_row_kernel<1>, dim3(nkv), dim3(64), 0, st, qkv, knw, cosb, sinb, kc, vc, koff,
+                                vo, stride, window, dyn); break;
+    case 128: hipLaunchKernelGGL(prepkv_row_kernel<2>, dim3(nkv), dim3(64), 0, st, qkv, knw, cosb, sinb, kc, vc, koff,
+                                 vo, stride, window, dyn); break;
+    case 256: hipLaunchKernelGGL(prepkv_row_kernel<4>, dim3(nkv), dim3(64), 0, st, qkv, knw, cosb, sinb, kc, vc, koff,
+                                 vo, stride, window, dyn); break;
+    case 512: hipLaunchKernelGGL(prepkv_row_kernel<8>, dim3(nkv), dim3(64), 0, st, qkv, knw, cosb, sinb, kc, vc, koff,
+                                 vo, stride, window, dyn); break;
+    default: hipLaunchKernelGGL(prepkv_kernel, dim3(nkv), dim3(ATT_THREADS), 0, st, qkv, knw, cosb, sinb, kc, vc, hd,
+                                koff, vo, stride, window, dyn); break;
+  }
   Q4_LAUNCHED("prepkv");
   return Q4_OK;
 }
@@ -665,6 +778,10 @@ static int attn_launch(const float* qkv, const float* qnw, const float* cosb, co
   Q4_ARG(hd == 64 || hd == 128 || hd == 256 || hd == 512, "head dim must be 64, 128, 256 or 512 (got %d)", hd);
   Q4_ARG(stride > 0 && window >= 0 && window <= stride && qoff >= 0 && koff >= 0 && voff >= 0, "bad sizes");
   Q4_ARG(((uintptr_t)kc & 15) == 0 && ((uintptr_t)vc & 15) == 0, "kc and vc must be 16-byte aligned");
+  Q4_ARG(((uintptr_t)qkv & 15) == 0 && ((uintptr_t)qnw & 15) == 0 && ((uintptr_t)cosb & 15) == 0 &&
+             ((uintptr_t)sinb & 15) == 0 && ((uintptr_t)knw & 15) == 0 && qoff % 4 == 0 && koff % 4 == 0 &&
+             voff % 4 == 0,
+         "qkv, qnw, cos, sin and knw must be 16-byte aligned and the q/k/v offsets multiples of 4 elements");
   const size_t need = q4_attn_workspace_bytes(nH, hd, stride);
   Q4_ARG(ws_bytes >= need, "attention workspace too small: %zu < %zu bytes", ws_bytes, need);
   const int ns = attn_splits(stride), hpw = attn_hpw(grp);
