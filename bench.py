@@ -709,6 +709,22 @@ def bench_ceilings(ops):
         ent = {"bytes": nbytes, "us_per_launch": round(us, 3), "GBps": round(nbytes / us / 1e3, 1),
                "frac_of_hbm_peak": round(nbytes / us / 1e3 / HBM_PEAK_GBS, 4),
                "best": {"wgs": w, "units": u, "order": "chunked" if c else "strided"}, "distinct_buffers": n}
+        # the same read with a 2-byte companion load per 16-byte unit (the
+        # GEMV's fp16 block scales: 1/8 more bytes, twice the loads), best of
+        # the chunked grids
+        if name != "lm_head_262144x3840":
+            comps = [torch.randint(-2 ** 31, 2 ** 31 - 1, (nbytes // 32,), dtype=torch.int32, device=dev,
+                                   generator=gen) for _ in range(n)]
+            rc = {}
+            for w2 in (256, 512, 1024, 2048):
+                for u2 in (4, 8):
+                    rc[(w2, u2)] = _timed_graph(ops, lambda i: ops.probe_stream_read(
+                        bufs[i], w2, units=u2, chunked=True, comp=comps[i], sink=sink), n, reps)
+            (w2, u2), us2 = min(rc.items(), key=lambda kv: kv[1])
+            ent["with_scale_companion_loads"] = {"us_per_launch": round(us2, 3),
+                                                 "bytes_incl_companion": nbytes + nbytes // 8,
+                                                 "best": {"wgs": w2, "units": u2}}
+            del comps
         if name == "c1_15360x3840":
             pf = {}
             for mb in (2, 4, 8, 16):

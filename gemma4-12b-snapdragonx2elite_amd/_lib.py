@@ -78,7 +78,7 @@ SIGNATURES = {
     "q4_attn": (_i, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _i, _i, _i, _i, _i, _i, _i, _i, _vp, _vp, _sz, _vp]),
     "q4_prepkv_attn": (_i, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _i, _i, _i, _i, _i, _i, _i, _i, _i, _i, _i, _vp,
                             _vp, _sz, _vp]),
-    "q4_probe_stream_read": (_i, [_vp, _sz, _i, _i, _i, _vp, _sz, _sz, _vp, _sz, _vp]),
+    "q4_probe_stream_read": (_i, [_vp, _sz, _i, _i, _i, _vp, _sz, _sz, _vp, _sz, _vp, _sz, _vp]),
     "q4_probe_mfma": (_i, [_i, _i, _i, _vp, _sz, _vp, _sz, _vp, _sz, _vp]),
     "q4_probe_wall_clock_khz": (_i, [C.POINTER(_i)]),
     "q4_graph_begin": (_i, [_vp]),

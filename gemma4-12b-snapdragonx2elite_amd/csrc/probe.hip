@@ -9,7 +9,8 @@
 //    counterpart of the reference's streaming-read microbenchmark
 //    (benchmarks/microbench_bw.py:26-35). Optionally each workgroup, after
 //    its own share, reads the first bytes that the same workgroup of the
-//    next launch will read (a cross-launch prefetch into its XCD's L2).
+//    next launch will read (a cross-launch prefetch into its XCD's L2), or
+//    every unit load takes a 2-byte companion load (the GEMV's scales).
 //  * mfma_loop_kernel: back-to-back independent int8 (32x32x32) or f16
 //    (32x32x16) MFMAs on registers, with the shader clock (s_memtime)
 //    and the constant wall clock (s_memrealtime) read at both ends of the
@@ -30,12 +31,16 @@ constexpr uint32_t PROBE_MAGIC = 0x9E3779B9u;   // a store only if the data hash
 // (CHUNK) or every G-th 4 KB row of the buffer (grid-strided); lane t reads
 // unit t of each 256-unit row. U loads per lane stay in flight: unit i's
 // registers are refilled with unit i + U right after use. Indices past the
-// buffer are clamped (re-read, not counted).
-template <int U, bool CHUNK>
+// buffer are clamped (re-read, not counted). SC: every unit load has a
+// 2-byte companion load at unit index * 2 of `comp` (n16 * 2 bytes), the
+// access pattern of the GEMV's block scales (1/8 of the bytes, one load per
+// unit), so the pair of probes prices the scale loads.
+template <int U, bool CHUNK, bool SC>
 __global__ void __launch_bounds__(PROBE_THREADS)
 stream_read_kernel(const uint8_t* __restrict__ buf, long n16, long per_rows, const uint8_t* __restrict__ next,
-                   long next_n16, long pf_rows, uint32_t* __restrict__ sink) {
+                   long next_n16, long pf_rows, const uint8_t* __restrict__ comp, uint32_t* __restrict__ sink) {
   __shared__ __attribute__((aligned(16))) uint32_t pf_lds[PROBE_THREADS * 4];
+  constexpr int LPU = SC ? 2 : 1;  // loads per unit
   const int t = threadIdx.x;
   const long G = gridDim.x, w = blockIdx.x;
   auto unit = [&](long i) -> long {   // unit of row i of this workgroup
@@ -45,26 +50,43 @@ stream_read_kernel(const uint8_t* __restrict__ buf, long n16, long per_rows, con
   const long last = n16 - 1;
   uint32_t acc = 0;
   v4u r[U];
+  uint32_t c[U];
+  // the companion load writes its ring slot in place (an in-out operand): an
+  // output-only asm result may be copied by the register allocator while the
+  // load is still in flight, and the landing load then overwrites a register
+  // that holds something else by then
+  auto issue = [&](int k, long j) {
+    const long u = min(unit(j < per_rows ? j : per_rows - 1), last);
+    r[k] = ld16_nt(buf + u * 16);
+    if constexpr (SC) asm volatile("global_load_ushort %0, %1, off" : "+v"(c[k]) : "v"(comp + u * 2));
+  };
+  // a companion value is consumed by an ordered (volatile) instruction right
+  // after its wait, so it is dead before the same slot's next load: the
+  // compiler cannot sink its use below that load and keep two copies
+  auto take = [&](int k) {
+    pin(r[k]);
+    uint32_t v = (r[k][0] + r[k][1]) ^ (r[k][2] + r[k][3]);
+    if constexpr (SC) asm volatile("v_xor_b32 %0, %0, %1" : "+v"(v) : "v"(c[k]));
+    return v;
+  };
 #pragma unroll
-  for (int k = 0; k < U; ++k) r[k] = ld16_nt(buf + min(unit(k < per_rows ? k : per_rows - 1), last) * 16);
+  for (int k = 0; k < U; ++k) issue(k, k);
   const long rounds = (per_rows + U - 1) / U;
   long i = 0;
   for (long rd = 1; rd < rounds; ++rd) {
     static_for<0, U>([&](auto kc) {
       constexpr int k = decltype(kc)::value;
-      vmwait<U - 1>();
-      pin(r[k]);
-      acc ^= (r[k][0] + r[k][1]) ^ (r[k][2] + r[k][3]);
-      const long j = i + k + U;
-      r[k] = ld16_nt(buf + min(unit(j < per_rows ? j : per_rows - 1), last) * 16);
+      vmwait<LPU * (U - 1)>();
+      acc ^= take(k);
+      issue(k, i + k + U);
     });
     i += U;
   }
   static_for<0, U>([&](auto kc) {
     constexpr int k = decltype(kc)::value;
-    vmwait<U - 1 - k>();
-    pin(r[k]);
-    if (i + k < per_rows) acc ^= (r[k][0] + r[k][1]) ^ (r[k][2] + r[k][3]);
+    vmwait<LPU * (U - 1 - k)>();
+    const uint32_t v = take(k);
+    if (i + k < per_rows) acc ^= v;
   });
   // the first rows this workgroup's successor (same index, next launch,
   // same XCD) reads, with ordinary (L2-allocating) direct-to-LDS loads: no
@@ -135,10 +157,10 @@ mfma_loop_kernel(int iters, const v4i* __restrict__ operands, unsigned long long
   if (s == (int)PROBE_MAGIC) sink[blockIdx.x] = s;
 }
 
-typedef void (*stream_fn)(const uint8_t*, long, long, const uint8_t*, long, long, uint32_t*);
-template <bool C>
+typedef void (*stream_fn)(const uint8_t*, long, long, const uint8_t*, long, long, const uint8_t*, uint32_t*);
+template <bool C, bool SC>
 static stream_fn pick_stream_c(int U) {
-  return U == 4 ? stream_read_kernel<4, C> : U == 8 ? stream_read_kernel<8, C> : stream_read_kernel<16, C>;
+  return U == 4 ? stream_read_kernel<4, C, SC> : U == 8 ? stream_read_kernel<8, C, SC> : stream_read_kernel<16, C, SC>;
 }
 
 }  // namespace q4
@@ -148,7 +170,8 @@ using namespace q4;
 extern "C" {
 
 int q4_probe_stream_read(const void* buf, size_t bytes, int wgs, int units, int chunked, const void* next,
-                         size_t next_bytes, size_t prefetch_bytes, uint32_t* sink, size_t sink_bytes, void* stream) {
+                         size_t next_bytes, size_t prefetch_bytes, const void* comp, size_t comp_bytes,
+                         uint32_t* sink, size_t sink_bytes, void* stream) {
   clear_error();
   Q4_ARG(buf && sink, "null pointer");
   Q4_ARG(bytes >= 16 && bytes % 16 == 0 && ((uintptr_t)buf & 15) == 0, "buffer must be 16-byte aligned and sized");
@@ -166,9 +189,16 @@ int q4_probe_stream_read(const void* buf, size_t bytes, int wgs, int units, int 
     if (pf_rows > per_rows) pf_rows = per_rows;
     next_n16 = (long)(next_bytes / 16);
   }
-  hipLaunchKernelGGL(chunked ? pick_stream_c<true>(units) : pick_stream_c<false>(units), dim3(wgs),
-                     dim3(PROBE_THREADS), 0, as_stream(stream), reinterpret_cast<const uint8_t*>(buf), n16, per_rows,
-                     reinterpret_cast<const uint8_t*>(pf_rows ? next : buf), next_n16, pf_rows, sink);
+  if (comp) {
+    Q4_ARG(comp_bytes >= (size_t)n16 * 2 && ((uintptr_t)comp & 1) == 0, "companion buffer needs bytes / 8 (%ld)",
+           n16 * 2);
+    Q4_ARG(pf_rows == 0, "companion loads and successor prefetch are separate probes");
+  }
+  const stream_fn fn = comp ? (chunked ? pick_stream_c<true, true>(units) : pick_stream_c<false, true>(units))
+                            : (chunked ? pick_stream_c<true, false>(units) : pick_stream_c<false, false>(units));
+  hipLaunchKernelGGL(fn, dim3(wgs), dim3(PROBE_THREADS), 0, as_stream(stream), reinterpret_cast<const uint8_t*>(buf),
+                     n16, per_rows, reinterpret_cast<const uint8_t*>(pf_rows ? next : buf), next_n16, pf_rows,
+                     reinterpret_cast<const uint8_t*>(comp), sink);
   Q4_LAUNCHED("stream_read");
   return Q4_OK;
 }

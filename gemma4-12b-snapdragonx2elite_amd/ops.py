@@ -780,16 +780,19 @@ def stream_wait(stream=None, timeout_ms: int = 0, label: str = "") -> None:
 # ------------------------------------------------------------------ probes
 def probe_stream_read(buf: torch.Tensor, wgs: int, *, units: int = 8, chunked: bool = True,
                       next: torch.Tensor | None = None, prefetch_bytes: int = 0,
-                      sink: torch.Tensor | None = None) -> torch.Tensor:
+                      comp: torch.Tensor | None = None, sink: torch.Tensor | None = None) -> torch.Tensor:
     """Streaming read of all of ``buf`` (a measurement probe; computes nothing).
     With ``next``, each workgroup then reads its successor's first
-    ``prefetch_bytes / wgs`` bytes of ``next`` into L2. Returns the sink."""
+    ``prefetch_bytes / wgs`` bytes of ``next`` into L2; with ``comp`` (>= 1/8
+    of ``buf``), every 16-byte load has a 2-byte companion load (the GEMV's
+    scale pattern). Returns the sink."""
     if sink is None:
         sink = torch.empty(wgs, dtype=torch.int32, device=buf.device)
     _need(sink, 4 * wgs, "sink")
     nb = _nbytes(next) if next is not None else 0
     call("q4_probe_stream_read", _p(buf), _nbytes(buf) // 16 * 16, wgs, units, int(chunked),
-         _p(next) if next is not None else None, nb, prefetch_bytes if next is not None else 0, _p(sink),
+         _p(next) if next is not None else None, nb, prefetch_bytes if next is not None else 0,
+         _p(comp) if comp is not None else None, _nbytes(comp) if comp is not None else 0, _p(sink),
          _nbytes(sink), _stream())
     return sink
 

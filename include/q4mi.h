@@ -421,11 +421,13 @@ int q4_pre_attn(const void* q, int q_dtype, int ldq, const float* qnw,
  * streaming-read microbenchmark (benchmarks/microbench_bw.py:26-35). With
  * next/prefetch_bytes, each workgroup then reads its successor's first
  * prefetch_bytes/wgs bytes of `next` (laid out like buf, reads clamped to
- * next_bytes) with L2-allocating loads. sink: one uint32 per workgroup,
- * written only when a data hash hits a magic value. */
+ * next_bytes) with L2-allocating loads. With comp (>= bytes / 8), every
+ * 16-byte load has a 2-byte companion load from comp at the unit's index
+ * (the access pattern of the GEMV's fp16 block scales). sink: one uint32
+ * per workgroup, written only when a data hash hits a magic value. */
 int q4_probe_stream_read(const void* buf, size_t bytes, int wgs, int units, int chunked, const void* next,
-                         size_t next_bytes, size_t prefetch_bytes, uint32_t* sink, size_t sink_bytes,
-                         void* stream);
+                         size_t next_bytes, size_t prefetch_bytes, const void* comp, size_t comp_bytes,
+                         uint32_t* sink, size_t sink_bytes, void* stream);
 /* `iters` (a multiple of 8) rounds of four independent MFMAs per wave, wgs
  * workgroups of four waves: kind 0 = v_mfma_i32_32x32x32_i8 (65536 int ops
  * each), 1 = v_mfma_f32_32x32x16_f16 (32768 flops each). operands: 64 KB of
