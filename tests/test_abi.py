@@ -170,3 +170,47 @@ def test_prepkv_attn_argument_errors_without_gpu(g4):
     assert st == g4._lib.Q4_ERR_ARG and "null" in _err(g4)
     st = lib.q4_prepkv_attn(*[fake] * 8, 0, 16, 8, 96, 64, 0, 0, 4096, 6144, 0, 2, fake, fake, 1 << 20, null)
     assert st == g4._lib.Q4_ERR_ARG and "64, 128, 256 or 512" in _err(g4)
+
+
+def test_probe_and_stamped_gemm_argument_errors_without_gpu(g4):
+    """Entry points added for measurement reject bad arguments before any
+    device work: the streaming-read probe (units, companion size), the MFMA
+    probe (round count, operand buffer), the stamped W8A8 (stamp buffer)."""
+    lib = g4._lib.lib()
+    p, null = C.c_void_p(1 << 20), C.c_void_p(0)
+    st = lib.q4_probe_stream_read(p, 1 << 20, 64, 3, 1, null, 0, 0, null, 0, p, 4096, null)
+    assert st == g4._lib.Q4_ERR_ARG and "units" in _err(g4)
+    st = lib.q4_probe_stream_read(p, 1 << 20, 64, 4, 1, null, 0, 0, p, (1 << 17) - 2, p, 4096, null)
+    assert st == g4._lib.Q4_ERR_ARG and "companion" in _err(g4)
+    st = lib.q4_probe_stream_read(p, 1 << 20, 64, 4, 1, p, 1 << 20, 1 << 20, p, 1 << 17, p, 4096, null)
+    assert st == g4._lib.Q4_ERR_ARG and "separate probes" in _err(g4)
+    st = lib.q4_probe_mfma(0, 4, 12, null, 0, p, 64, p, 16, null)
+    assert st == g4._lib.Q4_ERR_ARG and "multiple of 8" in _err(g4)
+    st = lib.q4_probe_mfma(0, 4, 16, p, 1024, p, 64, p, 16, null)
+    assert st == g4._lib.Q4_ERR_ARG and "operands" in _err(g4)
+    st = lib.q4_probe_mfma(2, 4, 16, null, 0, p, 64, p, 16, null)
+    assert st == g4._lib.Q4_ERR_ARG and "kind" in _err(g4)
+    # stamped W8A8: 480 workgroups at M=2048, N=15360 (256-row tiles); one stamp row short
+    assert lib.q4_gemm_w8a8_packed_workgroups(2048, 15360) == 480
+    assert lib.q4_gemm_w8a8_packed_workgroups(128, 512) == 2       # 128-row tiles below 256 workgroups
+    assert lib.q4_gemm_w8a8_packed_workgroups(0, 512) == 0
+    st = lib.q4_gemm_w8a8_packed_stamped(p, p, p, p, 0, p, null, 2048, 15360, 3840, p, 480 * 32 - 8, null)
+    assert st == g4._lib.Q4_ERR_ARG and "stamps" in _err(g4)
+    st = lib.q4_gemm_w8a8_packed_stamped(p, p, p, p, 0, p, null, 2048, 15360, 3840, null, 0, null)
+    assert st == g4._lib.Q4_ERR_ARG and "stamps" in _err(g4)
+
+
+def test_attention_alignment_errors_without_gpu(g4):
+    """The decode attention and prepkv read q, k, v, the norm weights and the
+    RoPE row in 16-byte pieces: misaligned buffers or offsets are refused."""
+    lib = g4._lib.lib()
+    a, m, null = C.c_void_p(1 << 20), C.c_void_p((1 << 20) + 4), C.c_void_p(0)
+    ws = lib.q4_attn_workspace_bytes(16, 256, 1024)
+    st = lib.q4_attn(m, a, a, a, a, a, a, 0, 16, 8, 256, 1024, 1024, 0, 2, a, a, ws, null)
+    assert st == g4._lib.Q4_ERR_ARG and "16-byte aligned" in _err(g4)
+    st = lib.q4_attn(a, a, a, a, a, a, a, 0, 16, 8, 256, 1024, 1024, 2, 2, a, a, ws, null)
+    assert st == g4._lib.Q4_ERR_ARG and "offsets" in _err(g4)
+    st = lib.q4_prepkv_attn(a, m, a, a, a, a, a, a, 0, 16, 8, 256, 1024, 1024, 0, 4096, 6144, 0, 2, a, a, ws, null)
+    assert st == g4._lib.Q4_ERR_ARG and "16-byte aligned" in _err(g4)
+    st = lib.q4_prepkv(a, a, a, m, a, a, 8, 256, 4096, 6144, 0, 1024, 1024, a, null)
+    assert st == g4._lib.Q4_ERR_ARG and "16-byte aligned" in _err(g4)
