@@ -334,7 +334,8 @@ int q4_gelumul(const float* gate, const float* up, void* out, int out_dtype, int
 /* This token's K (k-norm with weight knw, RoPE with cosb/sinb) and V
  * (v-norm; read at koff when keqv) of every KV head into cache slot
  * dyn[0] % window (window > 0) or dyn[0]; nothing is written when the slot
- * is past stride. vk/prepkv.comp:16-30 (d_prep, src/vk_engine.py:236-237). */
+ * is past stride. qkv, knw, cosb and sinb 16-byte aligned, koff and voff
+ * multiples of 4. vk/prepkv.comp:16-30 (d_prep, src/vk_engine.py:236-237). */
 int q4_prepkv(const float* qkv, const float* knw, const float* cosb, const float* sinb,
               uint16_t* kc, uint16_t* vc, int nkv, int hd, int koff, int voff, int keqv,
               int stride, int window, const uint32_t* dyn, void* stream);
@@ -345,6 +346,8 @@ int q4_prepkv(const float* qkv, const float* knw, const float* cosb, const float
  * or fp16, out_dtype). Split along the keys (two launches: the splits of
  * each group of query heads sharing a KV head, then their merge); ws:
  * q4_attn_workspace_bytes(nH, hd, stride) bytes, no initialisation needed.
+ * hd 64, 128, 256 or 512; qkv, qnw, cosb, sinb (and knw), kc and vc 16-byte
+ * aligned, qoff (koff, voff) multiples of 4.
  * vk/attn.comp:18-53 (d_attn, src/vk_engine.py:238-239). */
 size_t q4_attn_workspace_bytes(int nH, int hd, int stride);
 int q4_attn(const float* qkv, const float* qnw, const float* cosb, const float* sinb,
