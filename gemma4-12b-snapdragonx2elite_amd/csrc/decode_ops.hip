@@ -581,79 +581,56 @@ attn_split_kernel(const float* __restrict__ qkv, const float* __restrict__ qnw, 
   }
 }
 
-// Head blockIdx.x: out = sum_c acc_c e^(m_c - M) / sum_c l_c e^(m_c - M),
-// M = max_c m_c, over the live splits c. The (m, l) pairs and the first
-// batch of MB accumulator values per thread are loaded together, before the
-// position; the weights and L come from wave 0 in a fixed order. ml: 2
-// nsplit floats of dynamic shared memory. out fp32 or fp16.
+// Head blockIdx.x, dims 64 blockIdx.y .. + 63, one wave (lane = dim):
+// out = sum_c acc_c e^(m_c - M) / sum_c l_c e^(m_c - M), M = max_c m_c,
+// over the live splits c. No barrier: the wave loads its dims of the first
+// MB splits and the (m, l) of splits lane, lane + 64, .. before the position
+// (which sets the live split count) arrives, takes M and L with cross-lane
+// reductions (lane c holds split c, c + 64, ..), passes the weights through
+// its own LDS and sums the splits in order. Per head and dim the arithmetic
+// and its order are the same whichever wave does it. ml: nsplit floats of
+// dynamic shared memory. out fp32 or fp16.
 template <int YT, int EPL>
-__global__ void __launch_bounds__(ATT_THREADS) attn_merge_kernel(const float* __restrict__ part, void* __restrict__ out,
-                                                                 int nsplit, int stride, int window,
-                                                                 const uint32_t* __restrict__ dyn) {
-  constexpr int HD = 64 * EPL, EPT = (HD + ATT_THREADS - 1) / ATT_THREADS, MB = 32;
+__global__ void __launch_bounds__(64) attn_merge_kernel(const float* __restrict__ part, void* __restrict__ out,
+                                                        int nsplit, int stride, int window,
+                                                        const uint32_t* __restrict__ dyn) {
+  constexpr int HD = 64 * EPL, MB = 32;
   extern __shared__ float ml[];
-  __shared__ float sL;
-  const int h = blockIdx.x, t = threadIdx.x;
+  const int h = blockIdx.x, t = threadIdx.x, d = blockIdx.y * 64 + t;
   const float* w = part + (long)h * nsplit * (HD + 2);
-  // the first batch of accumulator values and the (m, l) of the first
-  // ATT_THREADS splits are requested before the position (which sets the
-  // live split count) arrives; indices are clamped to the workspace
-  float x[MB][EPT];
+  // indices clamped to the workspace until the live split count is known
+  float x[MB];
   auto fetch = [&](int c0, int cmax) {
 #pragma unroll
-    for (int c = 0; c < MB; ++c)
-#pragma unroll
-      for (int e = 0; e < EPT; ++e)
-        x[c][e] = w[(long)min(c0 + c, cmax) * (HD + 2) + 2 + min(t + ATT_THREADS * e, HD - 1)];
+    for (int c = 0; c < MB; ++c) x[c] = w[(long)min(c0 + c, cmax) * (HD + 2) + 2 + d];
   };
   fetch(0, nsplit - 1);
   const int c_t = min(t, nsplit - 1);
   const float m_t = w[(long)c_t * (HD + 2)], l_t = w[(long)c_t * (HD + 2) + 1];
   const int T = att_len(dyn[0], window, stride);
   const int ns = (T + ATT_KCH - 1) / ATT_KCH;
-  if (t < ns) {
-    ml[2 * t] = m_t;
-    ml[2 * t + 1] = l_t;
+  float M = t < ns ? m_t : -INFINITY;
+  for (int c = t + 64; c < ns; c += 64) M = fmaxf(M, w[(long)c * (HD + 2)]);
+  M = reduce64<true>(M);
+  float L = 0.0f;
+  for (int c = t; c < ns; c += 64) {
+    const float mc = c == t ? m_t : w[(long)c * (HD + 2)];
+    const float lc = c == t ? l_t : w[(long)c * (HD + 2) + 1];
+    const float wc = expf(mc - M);
+    ml[c] = wc;
+    L = fmaf(lc, wc, L);
   }
-  for (int c = t + ATT_THREADS; c < ns; c += ATT_THREADS) {
-    ml[2 * c] = w[(long)c * (HD + 2)];
-    ml[2 * c + 1] = w[(long)c * (HD + 2) + 1];
-  }
-  float acc[EPT];
-#pragma unroll
-  for (int e = 0; e < EPT; ++e) acc[e] = 0.0f;
-  __syncthreads();
-  if (t < 64) {
-    float M = -INFINITY;
-    for (int c = t; c < ns; c += 64) M = fmaxf(M, ml[2 * c]);
-    M = reduce64<true>(M);
-    float L = 0.0f;
-    for (int c = t; c < ns; c += 64) {
-      const float wc = expf(ml[2 * c] - M);
-      ml[2 * c] = wc;
-      L = fmaf(ml[2 * c + 1], wc, L);
-    }
-    L = reduce64<false>(L);
-    if (t == 0) sL = L;
-  }
-  __syncthreads();
+  L = reduce64<false>(L);
+  float acc = 0.0f;
   for (int c0 = 0; c0 < ns; c0 += MB) {
     if (c0 > 0) fetch(c0, ns - 1);
 #pragma unroll
     for (int c = 0; c < MB; ++c)
-      if (c0 + c < ns)
-#pragma unroll
-        for (int e = 0; e < EPT; ++e) acc[e] = fmaf(x[c][e], ml[2 * (c0 + c)], acc[e]);
+      if (c0 + c < ns) acc = fmaf(x[c], ml[c0 + c], acc);
   }
-#pragma unroll
-  for (int e = 0; e < EPT; ++e) {
-    const int i = t + ATT_THREADS * e;
-    if (i < HD) {
-      const float v = acc[e] / sL;
-      if constexpr (YT == Q4_DT_F16) reinterpret_cast<uint16_t*>(out)[h * HD + i] = f2h(v);
-      else reinterpret_cast<float*>(out)[h * HD + i] = v;
-    }
-  }
+  const float v = acc / L;
+  if constexpr (YT == Q4_DT_F16) reinterpret_cast<uint16_t*>(out)[h * HD + d] = f2h(v);
+  else reinterpret_cast<float*>(out)[h * HD + d] = v;
 }
 
 static int attn_splits(int stride) { return ceil_div(stride, ATT_KCH); }
@@ -785,7 +762,7 @@ static int attn_launch(const float* qkv, const float* qnw, const float* cosb, co
   const size_t need = q4_attn_workspace_bytes(nH, hd, stride);
   Q4_ARG(ws_bytes >= need, "attention workspace too small: %zu < %zu bytes", ws_bytes, need);
   const int ns = attn_splits(stride), hpw = attn_hpw(grp);
-  const size_t msh = (size_t)2 * ns * sizeof(float);
+  const size_t msh = (size_t)ns * sizeof(float);
   Q4_ARG(msh <= 64 * 1024, "cache depth %d needs %d attention splits (more than the merge stages)", stride, ns);
   hipStream_t st = as_stream(stream);
   float* part = reinterpret_cast<float*>(ws);
@@ -794,11 +771,11 @@ static int attn_launch(const float* qkv, const float* qnw, const float* cosb, co
 #define Q4_ATT(E, P)                                                                                               \
   hipLaunchKernelGGL((attn_split_kernel<E, P>), grid, blk, 0, st, qkv, qnw, cosb, sinb, kc, vc, stride, window, \
                      qoff, grp, hpw, dyn, part, ns, knw, koff, voff)
-#define Q4_MRG(E)                                                                                                  \
-  if (h16) hipLaunchKernelGGL((attn_merge_kernel<Q4_DT_F16, E>), dim3(nH), blk, msh, st, part, out, ns, stride,  \
-                              window, dyn);                                                                       \
-  else hipLaunchKernelGGL((attn_merge_kernel<Q4_DT_F32, E>), dim3(nH), blk, msh, st, part, out, ns, stride, window, \
-                          dyn)
+#define Q4_MRG(E)                                                                                                \
+  if (h16) hipLaunchKernelGGL((attn_merge_kernel<Q4_DT_F16, E>), dim3(nH, E), dim3(64), msh, st, part, out, ns, \
+                              stride, window, dyn);                                                             \
+  else hipLaunchKernelGGL((attn_merge_kernel<Q4_DT_F32, E>), dim3(nH, E), dim3(64), msh, st, part, out, ns,     \
+                          stride, window, dyn)
   switch (hd) {
     case 64: if (prep) { Q4_ATT(1, true); } else { Q4_ATT(1, false); } break;
     case 128: if (prep) { Q4_ATT(2, true); } else { Q4_ATT(2, false); } break;
