@@ -325,19 +325,52 @@ pre_attn_merge_kernel(const float* __restrict__ ws, void* __restrict__ out, int 
   const int T = att_len(dyn[0] + (uint32_t)m, window, stride);
   const int ns = min((T + ksl - 1) / ksl, nsplit);
   const float* w = ws + (long)row * nsplit * (hd + 4);
-  float mx = -INFINITY;
-  for (int cc = 0; cc < ns; ++cc) mx = fmaxf(mx, w[(long)cc * (hd + 4)]);
-  float L = 0.0f;
+  // each batch of PM_CB splits is loaded with all of its loads in flight
+  // (one round trip per batch, not one per split); the arithmetic and its
+  // order are those of a split-by-split walk
+  constexpr int PM_CB = 8;
+  float mx = -INFINITY, L = 0.0f;
   v4f a = v4f{0.0f, 0.0f, 0.0f, 0.0f};
-  for (int cc = 0; cc < ns; ++cc) {
-    const float* wc = w + (long)cc * (hd + 4);
-    const float mc = wc[0];
-    if (mc == -INFINITY) continue;
-    const float e = expf(mc - mx);
-    L = fmaf(wc[1], e, L);
-    const v4f v = *reinterpret_cast<const v4f*>(wc + 4 + i);
+  float mv[PM_CB], lv[PM_CB];
+  v4f vv[PM_CB];
+  auto fetch = [&](int c0, bool all) {
 #pragma unroll
-    for (int k = 0; k < 4; ++k) a[k] = fmaf(v[k], e, a[k]);
+    for (int j = 0; j < PM_CB; ++j) {
+      const float* wc = w + (long)min(c0 + j, ns - 1) * (hd + 4);
+      mv[j] = wc[0];
+      if (all) {
+        lv[j] = wc[1];
+        vv[j] = *reinterpret_cast<const v4f*>(wc + 4 + i);
+      }
+    }
+  };
+  auto accumulate = [&](int c0) {
+#pragma unroll
+    for (int j = 0; j < PM_CB; ++j) {
+      if (c0 + j >= ns || mv[j] == -INFINITY) continue;
+      const float e = expf(mv[j] - mx);
+      L = fmaf(lv[j], e, L);
+#pragma unroll
+      for (int k = 0; k < 4; ++k) a[k] = fmaf(vv[j][k], e, a[k]);
+    }
+  };
+  if (ns <= PM_CB) {  // every split in one batch (the chunk layouts: 4 or 8 splits)
+    fetch(0, true);
+#pragma unroll
+    for (int j = 0; j < PM_CB; ++j)
+      if (j < ns) mx = fmaxf(mx, mv[j]);
+    accumulate(0);
+  } else {
+    for (int c0 = 0; c0 < ns; c0 += PM_CB) {
+      fetch(c0, false);
+#pragma unroll
+      for (int j = 0; j < PM_CB; ++j)
+        if (c0 + j < ns) mx = fmaxf(mx, mv[j]);
+    }
+    for (int c0 = 0; c0 < ns; c0 += PM_CB) {
+      fetch(c0, true);
+      accumulate(c0);
+    }
   }
   const long oi = (long)m * ldo + (long)h * hd + i;
 #pragma unroll
