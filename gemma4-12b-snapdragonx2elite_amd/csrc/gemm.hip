@@ -95,6 +95,25 @@ __device__ inline v4u dequant_word_f16(uint32_t w, v2h sv) {
   return v4u{pk_h2(p0), pk_h2(p1), pk_h2(p2), pk_h2(p3)};
 }
 
+// Pair P (codes e = 2P, 2P + 1 in k order) of dequant_word_f16, in three VALU
+// operations: high nibbles use 0x5400 | 16q = 64 + q (ulp 1/16), so both
+// halves become q - 8 with one exact add before the RNE multiply by s. mlo =
+// 0x64006400 and mhi = 0x54005400 come in VGPRs: v_and_or_b32 takes no
+// literal constants, and the masks go to SGPRs.
+template <int P>
+__device__ inline uint32_t dequant_pair_f16(uint32_t w, v2h sv, uint32_t mlo, uint32_t mhi) {
+  const uint32_t x = P >= 2 ? w >> 8 : w;
+  v2h p;
+  if constexpr (P & 1) {
+    const v2h off = {(_Float16)-72.0f, (_Float16)-72.0f};
+    p = __builtin_bit_cast(v2h, (x & 0x00F000F0u) | mhi) + off;
+  } else {
+    const v2h off = {(_Float16)-1032.0f, (_Float16)-1032.0f};
+    p = __builtin_bit_cast(v2h, (x & 0x000F000Fu) | mlo) + off;
+  }
+  return pk_h2(p * sv);
+}
+
 // Two device words (16 codes, k order) -> 16 int8 values
 // clamp(rint((q - 8) * r), -127, 127) in k order (vk/coopgemm_w4a8.comp:28-34).
 __device__ inline v4u requant_words_i8(uint32_t wa, uint32_t wb, float r) {
@@ -713,16 +732,30 @@ __global__ void __launch_bounds__(256) w8p_kernel(const GemmArgs g) {
 // count leaves a last k-step with one block: the other block's scales read
 // as zero, and its (clamped, stale) A chunks add nothing. With split > 1,
 // blockIdx.y selects a contiguous range of k-steps and fp32 partials go to P.
-template <int BM, bool TAIL>
-__global__ void __launch_bounds__(256) w4p_kernel(const GemmArgs g, int split) {
+// KG = 2 runs two groups of 4 waves (512 threads, two waves per SIMD, each
+// with its own A ring) over the two halves of the workgroup's k-steps: one
+// wave per SIMD is bound by its own instruction issue (dequant, A reads,
+// addresses between the MFMAs), and a second wave issues while the first
+// one's MFMAs run. Both groups run the same number of k-steps (barriers stay
+// paired); the second group's surplus step, for an odd count, reads zero
+// scales. Group 1 then hands its accumulators to group 0 through LDS, and
+// group 0 adds them (acc0 + acc1) and runs the epilogue.
+template <int BM, bool TAIL, int KG = 1>
+__global__ void __launch_bounds__(256 * KG) w4p_kernel(const GemmArgs g, int split) {
   constexpr int S = 4, FM = BM / 32, FN = 2;
   constexpr int AST = BM * 128;      // bytes per A stage
   constexpr int NA = BM / 32;        // A direct loads per wave per k-step
   constexpr int NB = FN * 2 * 2;     // B loads per lane per k-step: n-tile x block x (half-unit, scale)
   constexpr int EPI = 4 * 64 * EST * 4;
-  __shared__ __attribute__((aligned(16))) uint8_t ldsA[S * AST > EPI ? S * AST : EPI];
+  constexpr int RING = KG * S * AST;
+  constexpr int XCH = KG > 1 ? 4 * FM * FN * 16 * 64 * 4 : 0;  // group 1's accumulators
+  constexpr int LDSB = RING > EPI ? (RING > XCH ? RING : XCH) : (EPI > XCH ? EPI : XCH);
+  static_assert(KG == 1 || (KG == 2 && BM == 128), "two k-groups at 128-row tiles");
+  __shared__ __attribute__((aligned(16))) uint8_t ldsA[LDSB];
 
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  // grp through readfirstlane: wave-uniform, so the group's k range stays in SGPRs
+  const int tid = threadIdx.x, lane = tid & 63, wave = (tid >> 6) & 3,
+            grp = KG > 1 ? __builtin_amdgcn_readfirstlane(tid >> 8) : 0;
   const int M = g.M, N = g.N, K = g.K;
   int tm, tn;
   tile_of(blockIdx.x, gridDim.x, (M + BM - 1) / BM, tm, tn);
@@ -730,8 +763,13 @@ __global__ void __launch_bounds__(256) w4p_kernel(const GemmArgs g, int split) {
   const int nblk = K / BLK;
   const int nk_all = (nblk + 1) / 2;
   const int kz = blockIdx.y;
-  const int k_lo = (int)((long)kz * nk_all / split), nk = (int)((long)(kz + 1) * nk_all / split) - k_lo;
+  const int k_wg = (int)((long)kz * nk_all / split), nk_wg = (int)((long)(kz + 1) * nk_all / split) - k_wg;
+  // this group's k-steps: [k_lo, k_lo + nk); both groups run nit steps (the
+  // entry point gives KG = 2 workgroups at least 2 k-steps, so nk >= 1)
+  const int nit = KG > 1 ? (nk_wg + 1) / 2 : nk_wg;
+  const int k_lo = k_wg + grp * nit, nk = grp ? nk_wg - nit : nit;
   const int h = lane >> 5;
+  uint8_t* const ring = ldsA + grp * (S * AST);
 
   // A: as w8p_kernel, rows of 2K bytes (32-bit offsets: the entry point checks 2MK < 2^31)
   int chunk[2];
@@ -752,6 +790,8 @@ __global__ void __launch_bounds__(256) w4p_kernel(const GemmArgs g, int split) {
   const uint8_t* Ab = reinterpret_cast<const uint8_t*>(g.A);
   const uint8_t* Bb = reinterpret_cast<const uint8_t*>(g.B);
   const uint8_t* Sb = reinterpret_cast<const uint8_t*>(g.bsc);
+  uint32_t mlo = 0x64006400u, mhi = 0x54005400u;  // dequant_pair_f16's VGPR operands
+  asm volatile("" : "+v"(mlo), "+v"(mhi));
 
   v2u ru[3][FN][2];        // [set][n-tile][block] half-units
   uint32_t rs[3][FN][2];   // [set][n-tile][block] scale bits
@@ -767,7 +807,7 @@ __global__ void __launch_bounds__(256) w4p_kernel(const GemmArgs g, int split) {
       else rs[setl][j][bb] = ld2_so(Sb + (long)blk * PANEL * 2, ubase[j] * 2);
     } else if constexpr (o < NB + NA) {
       constexpr int i = o - NB;
-      uint8_t* st = ldsA + (kst & 3) * AST + (wave * NA + i) * 1024;
+      uint8_t* st = ring + (kst & 3) * AST + (wave * NA + i) * 1024;
       if constexpr (TAIL) {  // chunks past the row's end (a one-block last k-step) clamped inside the row
         const int c = chunk[(wave * NA + i) & 1];
         const int lim = 2 * K - 16 - k_lo * 128;  // last 16-byte chunk of the row, relative to k_lo
@@ -789,7 +829,7 @@ __global__ void __launch_bounds__(256) w4p_kernel(const GemmArgs g, int split) {
   auto rdA = [&](int st, int i, int q) {
     const int r = 32 * i + frow;
     const int c = 4 * (q >> 1) + 2 * h + (q & 1);
-    return *reinterpret_cast<const v4i*>(ldsA + st * AST + r * 128 + ((c ^ w8p_swz(r)) << 4));
+    return *reinterpret_cast<const v4i*>(ring + st * AST + r * 128 + ((c ^ w8p_swz(r)) << 4));
   };
   v4i fa[2][FM];
 
@@ -814,20 +854,22 @@ __global__ void __launch_bounds__(256) w4p_kernel(const GemmArgs g, int split) {
 #pragma unroll
   for (int i = 0; i < FM; ++i) fa[0][i] = rdA(0, i, 0);
 
-  // B fragment of n-tile j for k-slice q = 2bb + s of the k-step whose
-  // half-units sit in register set SET; zero scale for the absent second
-  // block of an odd block count
-  auto bfrag = [&](auto setc, int j, int q, bool half) {
-    constexpr int set = decltype(setc)::value;
+  // Word P of the B fragment of n-tile j for k-slice q = 2bb + s of the
+  // k-step whose half-units sit in register set SET; zero scale for the
+  // absent second block of an odd block count (half) and for both blocks of
+  // a surplus step (dead)
+  auto bpair = [&](auto setc, int j, int q, bool half, bool dead, auto pc) -> int {
+    constexpr int set = decltype(setc)::value, P = decltype(pc)::value;
     const int bb = q >> 1;
-    const uint16_t sbits = (bb == 1 && half) ? (uint16_t)0 : (uint16_t)rs[set][j][bb];
+    const uint16_t sbits = ((bb == 1 && half) || dead) ? (uint16_t)0 : (uint16_t)rs[set][j][bb];
     const _Float16 sc = __builtin_bit_cast(_Float16, sbits);
     const v2h sv = {sc, sc};
-    return __builtin_bit_cast(v4i, dequant_word_f16((q & 1) ? ru[set][j][bb].y : ru[set][j][bb].x, sv));
+    return (int)dequant_pair_f16<P>((q & 1) ? ru[set][j][bb].y : ru[set][j][bb].x, sv, mlo, mhi);
   };
   v4i fb[2][FN];  // [slice parity][n-tile]: slice q's fragments, built during slice q - 1
 #pragma unroll
-  for (int j = 0; j < FN; ++j) fb[0][j] = bfrag(I0{}, j, 0, 2 * k_lo + 1 >= nblk);
+  for (int j = 0; j < FN; ++j)
+    static_for<0, 4>([&](auto pc) { fb[0][j][decltype(pc)::value] = bpair(I0{}, j, 0, 2 * k_lo + 1 >= nblk, false, pc); });
 
   static_assert(NB == 8 && NB + NA <= 16 && FM % 4 == 0, "one VMEM operation per group");
   int kt = 0;
@@ -836,6 +878,7 @@ __global__ void __launch_bounds__(256) w4p_kernel(const GemmArgs g, int split) {
     const int st = kt & 3, stn = (kt + 1) & 3;
     const int kl = min(kt + 2, nk - 1);
     const bool half = 2 * (k_lo + kt) + 1 >= nblk, half_n = 2 * (k_lo + kt + 1) + 1 >= nblk;
+    const bool dead = KG > 1 && kt >= nk, dead_n = KG > 1 && kt + 1 >= nk;
     static_for<0, 4>([&](auto qc) {
       constexpr int q = decltype(qc)::value, cb = q & 1, nbuf = cb ^ 1;
       if constexpr (q == 2) {
@@ -854,10 +897,12 @@ __global__ void __launch_bounds__(256) w4p_kernel(const GemmArgs g, int split) {
         constexpr int i0 = g * (FM / 4);
 #pragma unroll
         for (int ii = i0; ii < i0 + FM / 4; ++ii) fa[nbuf][ii] = q < 3 ? rdA(st, ii, q + 1) : rdA(stn, ii, 0);
-        // the next slice's B fragment of n-tile g, while this slice's MFMAs run
-        if constexpr (g < FN) {
-          if constexpr (q < 3) fb[nbuf][g] = bfrag(setc, g, q + 1, half);
-          else fb[nbuf][g] = bfrag(setnc, g, 0, half_n);
+        // word g of the next slice's B fragments, while this slice's MFMAs
+        // run: the dequant spreads evenly over the slice's MFMAs
+#pragma unroll
+        for (int j = 0; j < FN; ++j) {
+          if constexpr (q < 3) fb[nbuf][j][g] = bpair(setc, j, q + 1, half, dead, gc);
+          else fb[nbuf][j][g] = bpair(setnc, j, 0, half_n, dead_n, gc);
         }
 #pragma unroll
         for (int ii = i0; ii < i0 + FM / 4; ++ii)
@@ -865,26 +910,18 @@ __global__ void __launch_bounds__(256) w4p_kernel(const GemmArgs g, int split) {
           for (int j = 0; j < FN; ++j)
             acc[ii][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(v8h, fa[cb][ii]),
                                                                 __builtin_bit_cast(v8h, fb[cb][j]), acc[ii][j], 0, 0, 0);
-        if constexpr (g < FN) {
-          __builtin_amdgcn_sched_group_barrier(0x100, FM / 4, 0);
+        __builtin_amdgcn_sched_group_barrier(0x100, FM / 4, 0);
 #pragma unroll
-          for (int r = 0; r < FM / 4 * FN; ++r) {
-            __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-            __builtin_amdgcn_sched_group_barrier(0x002, 6, 0);
-          }
-        } else {
-#pragma unroll
-          for (int r = 0; r < FM / 4; ++r) {
-            __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
-            __builtin_amdgcn_sched_group_barrier(0x008, FN, 0);
-          }
+        for (int r = 0; r < FM / 4 * FN; ++r) {
+          __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+          __builtin_amdgcn_sched_group_barrier(0x002, 16 / FM, 0);
         }
         vmem_op(std::integral_constant<int, 4 * q + g>{}, setlc, kl, kt + 2);
         __builtin_amdgcn_sched_barrier(0);
       });
     });
   };
-  for (; kt + 2 < nk; kt += 3) {
+  for (; kt + 2 < nit; kt += 3) {
     kstep(I0{}, I1{}, I2{});
     ++kt;
     kstep(I1{}, I2{}, I0{});
@@ -892,10 +929,10 @@ __global__ void __launch_bounds__(256) w4p_kernel(const GemmArgs g, int split) {
     kstep(I2{}, I0{}, I1{});
     kt -= 2;
   }
-  if (kt < nk) {
+  if (kt < nit) {
     kstep(I0{}, I1{}, I2{});
     ++kt;
-    if (kt < nk) kstep(I1{}, I2{}, I0{});
+    if (kt < nit) kstep(I1{}, I2{}, I0{});
   }
   vmwait<0>();
 #pragma unroll
@@ -908,6 +945,38 @@ __global__ void __launch_bounds__(256) w4p_kernel(const GemmArgs g, int split) {
         pin(rs[s3][j][bb]);
       }
   __syncthreads();  // every direct load landed and every fragment read before the strips reuse LDS
+
+  if constexpr (KG > 1) {
+    // group 1's accumulators to group 0: tile (i, j) of wave w, 16-byte piece
+    // c, lane l at float ((((w * FM + i) * FN + j) * 4 + c) * 64 + l) * 4
+    float* xch = reinterpret_cast<float*>(ldsA);
+    if (grp) {
+#pragma unroll
+      for (int i = 0; i < FM; ++i)
+#pragma unroll
+        for (int j = 0; j < FN; ++j)
+#pragma unroll
+          for (int c = 0; c < 4; ++c) {
+            const v4f t = {acc[i][j][4 * c], acc[i][j][4 * c + 1], acc[i][j][4 * c + 2], acc[i][j][4 * c + 3]};
+            *reinterpret_cast<v4f*>(xch + ((((wave * FM + i) * FN + j) * 4 + c) * 64 + lane) * 4) = t;
+          }
+    }
+    __syncthreads();
+    if (!grp) {
+#pragma unroll
+      for (int i = 0; i < FM; ++i)
+#pragma unroll
+        for (int j = 0; j < FN; ++j)
+#pragma unroll
+          for (int c = 0; c < 4; ++c) {
+            const v4f t = *reinterpret_cast<const v4f*>(xch + ((((wave * FM + i) * FN + j) * 4 + c) * 64 + lane) * 4);
+#pragma unroll
+            for (int e = 0; e < 4; ++e) acc[i][j][4 * c + e] += t[e];
+          }
+    }
+    __syncthreads();  // the exchange is read before the strips reuse LDS
+    if (grp) return;
+  }
 
   uint32_t* strip = reinterpret_cast<uint32_t*>(ldsA) + wave * (64 * EST);
 #pragma unroll
@@ -1221,11 +1290,26 @@ static int w4a16_split(int M, int N, int K) {
   return s;
 }
 
-template <int BM>
+// k-groups per W4A16 workgroup: two at 128-row tiles when every split has
+// at least 32 k-steps. Measured at M = 512: 62 against 65 us (N 15360, K
+// 3840) and 69 against 73 us (N 3840, K 15360); at 15 k-steps per group the
+// two are even, and below that the hand-over and the shorter loops lose.
+static int w4a16_kgroups(int M, int N, int K, int split) {
+  if (pick_bm(M, N) != 128) return 1;
+  const int nk = (K / 32 + 1) / 2;
+  int kg = nk / split >= 32 ? 2 : 1;
+  if (const char* e = getenv("Q4MI_W4A16_KG")) {  // tuning sweeps and tests: force one or two groups
+    const int v = atoi(e);
+    if (v == 1 || (v == 2 && nk / split >= 2)) kg = v;
+  }
+  return kg;
+}
+
+template <int BM, int KG = 1>
 static void launch_w4p(const GemmArgs& g, int split, hipStream_t st) {
   const dim3 grid(tiles(g.M, g.N, BM), split);
-  if (g.K % 64) hipLaunchKernelGGL((w4p_kernel<BM, true>), grid, dim3(256), 0, st, g, split);
-  else hipLaunchKernelGGL((w4p_kernel<BM, false>), grid, dim3(256), 0, st, g, split);
+  if (g.K % 64) hipLaunchKernelGGL((w4p_kernel<BM, true, KG>), grid, dim3(256 * KG), 0, st, g, split);
+  else hipLaunchKernelGGL((w4p_kernel<BM, false, KG>), grid, dim3(256 * KG), 0, st, g, split);
 }
 
 template <int OP, int BM>
@@ -1393,6 +1477,8 @@ int q4_gemm_w4a16_ws(const uint16_t* X, const uint32_t* wq, const uint16_t* sc16
          "W4A16 needs X and the int4 weights under 2 GiB (32-bit offsets)");
   if (pick_bm(M, N) == 256)
     launch_w4p<256>(g, split, as_stream(stream));
+  else if (w4a16_kgroups(M, N, K, split) == 2)
+    launch_w4p<128, 2>(g, split, as_stream(stream));
   else
     launch_w4p<128>(g, split, as_stream(stream));
   Q4_LAUNCHED("gemm_w4a16");

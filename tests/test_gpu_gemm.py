@@ -205,6 +205,27 @@ def test_w4a16(gpu, M, N, K):
     assert O.cosine(Yh, ref) > 0.99999
 
 
+@pytest.mark.parametrize("M,N,K", [(128, 3840, 15360), (512, 3840, 1920), (100, 320, 96), (256, 1024, 224)])
+def test_w4a16_two_kgroups_match_one(gpu, M, N, K, monkeypatch):
+    """128-row tiles can run two groups of 4 waves over the two halves of
+    each workgroup's k-steps (forced here with Q4MI_W4A16_KG=2) and add group
+    1's sums into group 0's. Against the one-group kernel (Q4MI_W4A16_KG=1)
+    only the fp32 summation order differs. The shapes cover an odd k-step count per workgroup (group 1's
+    surplus step reads zero scales), a one-block last k-step, and split-K."""
+    rng = np.random.default_rng(M + N + K)
+    q, s = synth_int4(rng, N, K)
+    X = torch.from_numpy(rng.standard_normal((M, K)).astype(np.float16)).cuda()
+    wq, sc = upload_int4(q, s)
+    monkeypatch.setenv("Q4MI_W4A16_KG", "2")
+    Y2 = to_np(gpu.gemm_w4a16(X, wq, sc, N)).astype(np.float64)
+    monkeypatch.setenv("Q4MI_W4A16_KG", "1")
+    Y1 = to_np(gpu.gemm_w4a16(X, wq, sc, N)).astype(np.float64)
+    assert np.isfinite(Y2).all()
+    assert np.abs(Y2 - Y1).max() <= np.abs(Y1).max() * 2.0 ** -9
+    ref = O.gemm_w4a16_ref(to_np(X), q, s)
+    assert O.normwise_rel_err(Y2.astype(np.float32), ref) <= 1e-3
+
+
 def test_w4a16_matches_f16_rounded_weights(gpu):
     """The kernel's dequant is f16((q-8)*s) per weight: against that exact
     product (computed in float64) the only remaining error is fp32
