@@ -145,6 +145,7 @@ def _attn_case(rng, nH, nkv, hd, stride):
     (16, 1, 512, 4096, 0, 4095),      # one KV head for 16 query heads: four head groups, 128 splits
     (6, 2, 128, 100, 0, 77),          # grp 3: one query head per workgroup
     (4, 4, 64, 40, 0, 39),            # tiny, last slot
+    (4, 2, 64, 9000, 0, 8999),        # 282 live splits: the merging workgroup takes the weights 256 at a time
 ])
 def test_attn(gpu, nH, nkv, hd, stride, window, pos):
     rng = np.random.default_rng(nH * hd + pos)
