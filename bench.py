@@ -263,12 +263,13 @@ def bench_small_m(ops, reps: int = 6):
     return out
 
 
-def bench_prefill(ops, reps: int = 5, p0: int = 3968):
+def bench_prefill(ops, reps: int = 5, p0: int = 3968, gated: bool = True):
     """One 128-token prefill chunk through the 48-layer stack with the
     batched-prefill layer graph (vk_engine.record_prefill: per layer
     pre_norm, q/k/v W4A16 GEMMs, pre_prepkv, pre_attn, o GEMM, pre_na +
     pre_norm, gate/up GEMMs, gelumul, down GEMM, pre_na), fp16 buffers
-    between producers and GEMMs, fused norms. Layers: 40 sliding (16 query
+    between producers and GEMMs, fused norms; with ``gated``, gate/up and the
+    gelumul run as one gated W4A16 GEMM over interleaved gate/up rows. Layers: 40 sliding (16 query
     and 8 KV heads of 256, 1024-slot ring) and 8 global (16 query heads and
     one k == v head of 512, every sixth layer), H 3840, I 15360; the chunk
     is the last of a 4096-token prompt (p0 = 3968: sliding layers attend
@@ -336,6 +337,7 @@ def bench_prefill(ops, reps: int = 5, p0: int = 3968):
             p_pfn=E.pre_norm_ds(Xp, nb["pfw"], Np, DUH, out_dtype=h16),
             p_g=E.gemm_ds(g, Np, Gp, **gk), p_u=E.gemm_ds(u, Np, Upp, **gk),
             p_gm=E.pre_gelumul_ds(Gp, Upp, ACp, DUIp, in_dtype=h16, out_dtype=h16),
+            p_gu=E.pre_gate_up_ds(g, u, Np, ACp) if gated else None,
             p_d=E.gemm_ds(d, ACp, Tp, **gk),
             p_nas=E.pre_na_ds(Tp, nb["ofw"], Xp, nas, x_dtype=h16)))
     graph = E.record_prefill(layers, fuse=True)
@@ -997,6 +999,8 @@ def main():
         return
     if args.prefill_only:
         print(f"[bench] prefill chunk {bench_prefill(ops, reps=max(1, args.steps // 40))}", flush=True)
+        print(f"[bench] prefill chunk, separate gate/up GEMMs and gelumul "
+              f"{bench_prefill(ops, reps=max(1, args.steps // 40), gated=False)}", flush=True)
         return
     if args.ceilings_only:
         bench_ceilings(ops)
@@ -1028,6 +1032,7 @@ def main():
     small = bench_small_m(ops)
     print(f"[bench] small-M gemv {small}", flush=True)
     pre = bench_prefill(ops)
+    pre["separate_gate_up_ms_per_chunk"] = bench_prefill(ops, gated=False)["ms_per_chunk"]
     print(f"[bench] prefill chunk {pre}", flush=True)
     w8 = w4 = None
     if not args.no_gemm:

@@ -982,7 +982,7 @@ __global__ void __launch_bounds__(256 * KG) w4p_kernel(const GemmArgs g, int spl
 #pragma unroll
   for (int c = 0; c < FM / 2; ++c) {
     const v16f sub[2][FN] = {{acc[2 * c][0], acc[2 * c][1]}, {acc[2 * c + 1][0], acc[2 * c + 1][1]}};
-    if (split > 1)
+    if (g.P)  // split-K partials (also at split 1 for the gated entry point)
       epilogue<2, 64, FN>(g, strip, sub, m0 + 64 * c, n0 + 64 * wave, g.P + (long)kz * M * N);
     else
       epilogue<1, 64, FN>(g, strip, sub, m0 + 64 * c, n0 + 64 * wave, nullptr);
@@ -1202,6 +1202,39 @@ __global__ void __launch_bounds__(256) splitk_reduce_kernel(const float* __restr
       float t = P[e];
       for (int s = 1; s < split; ++s) t += P[(long)s * n + e];
       Y[e] = f2h(t);
+    }
+  }
+}
+
+// Gate/up rows interleaved (row 2i gate i, 2i + 1 up i): Y[o] = f16(gelu(g)
+// u) with g = f16(sum over splits of P[s][2o]), u = f16(... P[s][2o + 1]),
+// split order: the separate gate and up GEMMs' fp16 outputs through
+// gelumul_kernel (vk/gelumul.comp:7-8), bit for bit at the same split. An
+// output row m holds P columns m N .. + N, so output o reads partial 2o. 4
+// outputs per thread.
+__global__ void __launch_bounds__(256) splitk_reduce_gated_kernel(const float* __restrict__ P,
+                                                                  uint16_t* __restrict__ Y, long n, int split) {
+  const long o = ((long)blockIdx.x * 256 + threadIdx.x) * 4;
+  if (o >= n) return;
+  const long np = 2 * n;  // partials per split
+  auto act = [](float g, float u) {
+    return f2h(__fmul_rn(gelu_tanh(h2f(f2h(g))), h2f(f2h(u))));
+  };
+  if (o + 3 < n) {
+    v4f a = *reinterpret_cast<const v4f*>(P + 2 * o), b = *reinterpret_cast<const v4f*>(P + 2 * o + 4);
+    for (int s = 1; s < split; ++s) {
+      a += *reinterpret_cast<const v4f*>(P + (long)s * np + 2 * o);
+      b += *reinterpret_cast<const v4f*>(P + (long)s * np + 2 * o + 4);
+    }
+    *reinterpret_cast<ushort4*>(Y + o) = make_ushort4(act(a.x, a.y), act(a.z, a.w), act(b.x, b.y), act(b.z, b.w));
+  } else {
+    for (long e = o; e < n; ++e) {
+      float gs = P[2 * e], us = P[2 * e + 1];
+      for (int s = 1; s < split; ++s) {
+        gs += P[(long)s * np + 2 * e];
+        us += P[(long)s * np + 2 * e + 1];
+      }
+      Y[e] = act(gs, us);
     }
   }
 }
@@ -1488,6 +1521,40 @@ int q4_gemm_w4a16_ws(const uint16_t* X, const uint32_t* wq, const uint16_t* sc16
                        split);
     Q4_LAUNCHED("gemm_w4a16 split-K reduce");
   }
+  return Q4_OK;
+}
+
+size_t q4_gemm_w4a16_gated_workspace_bytes(int M, int N, int K) {
+  if (M <= 0 || N <= 0 || N % 2 || K <= 0 || K % 32) return 0;
+  return (size_t)w4a16_split(M, N, K) * M * N * sizeof(float);
+}
+
+int q4_gemm_w4a16_gated(const uint16_t* X, const uint32_t* wq, const uint16_t* sc16, uint16_t* Y, int M, int N,
+                        int K, void* ws, size_t ws_bytes, void* stream) {
+  clear_error();
+  Q4_ARG(M > 0 && N > 0 && N % 2 == 0 && K > 0 && K % 32 == 0,
+         "bad gated W4A16 shape M=%d N=%d K=%d (N even: interleaved gate/up rows; K a multiple of 32)", M, N, K);
+  Q4_ARG(X && wq && sc16 && Y && ws, "null pointer");
+  Q4_ARG(((uintptr_t)X & 15) == 0 && ((uintptr_t)wq & 15) == 0 && ((uintptr_t)ws & 15) == 0,
+         "X, wq and the workspace must be 16-byte aligned");
+  const int split = w4a16_split(M, N, K);
+  Q4_ARG(ws_bytes >= (size_t)split * M * N * sizeof(float), "gated W4A16 workspace too small: %zu < %zu bytes",
+         ws_bytes, (size_t)split * M * N * sizeof(float));
+  Q4_ARG(2L * M * K < (1L << 31) && (long)pad_rows(N) * (K / BLK) * 16 < (1L << 31),
+         "W4A16 needs X and the int4 weights under 2 GiB (32-bit offsets)");
+  // fp32 partials at every split (the reduce applies the gelumul)
+  GemmArgs g{X, wq, sc16, nullptr, nullptr, 0, Y, nullptr, reinterpret_cast<float*>(ws), M, N, K};
+  if (pick_bm(M, N) == 256)
+    launch_w4p<256>(g, split, as_stream(stream));
+  else if (w4a16_kgroups(M, N, K, split) == 2)
+    launch_w4p<128, 2>(g, split, as_stream(stream));
+  else
+    launch_w4p<128>(g, split, as_stream(stream));
+  Q4_LAUNCHED("gemm_w4a16_gated");
+  const long n = (long)M * (N / 2);
+  hipLaunchKernelGGL(splitk_reduce_gated_kernel, dim3(ceil_div(n, 1024)), dim3(256), 0, as_stream(stream), g.P, Y, n,
+                     split);
+  Q4_LAUNCHED("gemm_w4a16_gated reduce");
   return Q4_OK;
 }
 

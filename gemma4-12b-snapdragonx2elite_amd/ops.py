@@ -404,6 +404,37 @@ def gemm_w4a16(X: torch.Tensor, wq: torch.Tensor, sc16: torch.Tensor, N: int, Y:
     return Y
 
 
+def gemm_w4a16_gated(X: torch.Tensor, wq: torch.Tensor, sc16: torch.Tensor, N: int, Y: torch.Tensor | None = None,
+                     ws: torch.Tensor | None = None):
+    """Y f16 [M, N/2] = gelu_tanh(G) * U of the W4A16 product over an
+    interleaved gate/up matrix of N rows (:func:`interleave_rows`), G and U
+    rounded to fp16 first (the reference's p_g, p_u then p_gm). ``ws``: at
+    least ``gemm_gated_workspace_bytes(M, N, K)`` bytes (allocated here when
+    omitted; capture code must pass its own)."""
+    if X.dtype != torch.float16 or X.dim() != 2:
+        raise ValueError("X must be a 2-D float16 tensor")
+    if N % 2:
+        raise ValueError("gated W4A16 needs an even row count (interleaved gate/up rows)")
+    M, K = X.shape
+    _check_int4(wq, sc16, N, K)
+    Y = torch.empty((M, N // 2), dtype=torch.float16, device=X.device) if Y is None else Y
+    _need(Y, M * (N // 2) * 2, "Y")
+    need = gemm_gated_workspace_bytes(M, N, K)
+    if ws is None:
+        if _CAPTURING[0]:
+            raise RuntimeError("a gated W4A16 GEMM inside a graph capture needs a workspace allocated before the "
+                               "capture (pass ws=...)")
+        ws = torch.empty(need, dtype=torch.uint8, device=X.device)
+    _need(ws, need, "gated W4A16 workspace")
+    call("q4_gemm_w4a16_gated", _p(X), _p(wq), _p(sc16), _p(Y), M, N, K, _p(ws), _nbytes(ws), _stream())
+    return Y
+
+
+def gemm_gated_workspace_bytes(M: int, N: int, K: int) -> int:
+    """Workspace bytes of :func:`gemm_w4a16_gated` (fp32 partials, at least one split)."""
+    return int(lib().q4_gemm_w4a16_gated_workspace_bytes(M, N, K))
+
+
 def gemm_workspace_bytes(M: int, N: int, K: int) -> int:
     """Workspace bytes of a W4A16 GEMM (0 when it runs without splitting K)."""
     return int(lib().q4_gemm_workspace_bytes(_lib.OP_W4A16, M, N, K))

@@ -476,6 +476,25 @@ def pre_gelumul_ds(gate: Buf, up: Buf, out: Buf, du, in_dtype=torch.float32, out
     return OpDesc(ops.pre_gelumul, (gate.view(in_dtype, n), up.view(in_dtype, n), out.view(out_dtype, n)), {})
 
 
+def pre_gate_up_ds(qg, qu, inbuf: Buf, actbuf: Buf) -> OpDesc | None:
+    """The prefill gate and up GEMMs and the gelumul after them (p_g, p_u,
+    p_gm: src/vk_engine.py:381-382, 421-422) as one gated W4A16 product
+    (:func:`ops.gemm_w4a16_gated`) over the two matrices interleaved row by
+    row (a copy made once): ``actbuf`` gets the fp16 activations the
+    separate route's gelumul writes, from fp16 normed rows in ``inbuf``.
+    Returns None when the two cannot share one matrix (different shapes) or
+    on the W8A8 route; then record the separate descriptors."""
+    (bwg, _bsg, _sg, _nb, _ig, bs16g, _a, _b), (N, K) = qg
+    (bwu, _bsu, _su, _nb2, _iu, bs16u, _c, _d), (N2, K2) = qu
+    if (N, K) != (N2, K2) or PREFILL_I8 or bs16g is None or bs16u is None:
+        return None
+    wo, so = ops.interleave_rows(bwg.t, bs16g.t, bwu.t, bs16u.t, N, K)
+    ws = torch.empty(ops.gemm_gated_workspace_bytes(MC, 2 * N, K), dtype=torch.uint8, device=wo.device)
+    KEEP.extend([wo, so, ws])
+    return OpDesc(ops.gemm_w4a16_gated, (inbuf.view(torch.float16, MC * K).view(MC, K), wo, so, 2 * N),
+                  dict(Y=actbuf.view(torch.float16, MC * N).view(MC, N), ws=ws))
+
+
 def pre_prepkv_ds(kbuf: Buf, vbuf: Buf, knw: Buf, cosM: Buf, sinM: Buf, kc: Buf, vc: Buf, Pp, dyn: Buf,
                   kv_dtype=torch.float32) -> OpDesc:
     """The chunk's K/V into the caches (p_prep, :372-374); ``Pp`` = (nkv, hd,
@@ -513,7 +532,9 @@ def record_prefill(layers, fuse: bool = True) -> ops.Graph:
     p_in, the q/k/v GEMMs, p_prep, p_attn, the o GEMM, p_na, p_pfn, the
     gate/up GEMMs, p_gm, the down GEMM, p_nas. ``layers`` holds the
     reference's per-layer keys (``p_in`` ... ``p_nas``; ``p_v`` may be None;
-    GEMM entries are :func:`gemm_ds` tuples). The reference submits one
+    GEMM entries are :func:`gemm_ds` tuples); a layer with a ``p_gu``
+    descriptor (:func:`pre_gate_up_ds`) runs it in place of ``p_g``, ``p_u``
+    and ``p_gm``. The reference submits one
     command buffer per layer; one graph holds them all here (the chunk's
     buffers persist between layers either way). With ``fuse``, each
     pre_na and the pre_norm of the same rows after it run as one launch."""
@@ -521,8 +542,9 @@ def record_prefill(layers, fuse: bool = True) -> ops.Graph:
     for L in layers:
         seq += [L["p_in"], ("gmm", L["p_q"]), ("gmm", L["p_k"])] + \
                ([("gmm", L["p_v"])] if L.get("p_v") is not None else []) + \
-               [L["p_prep"], L["p_attn"], ("gmm", L["p_o"]), L["p_na"], L["p_pfn"], ("gmm", L["p_g"]),
-                ("gmm", L["p_u"]), L["p_gm"], ("gmm", L["p_d"]), L["p_nas"]]
+               [L["p_prep"], L["p_attn"], ("gmm", L["p_o"]), L["p_na"], L["p_pfn"]] + \
+               ([L["p_gu"]] if L.get("p_gu") is not None else [("gmm", L["p_g"]), ("gmm", L["p_u"]), L["p_gm"]]) + \
+               [("gmm", L["p_d"]), L["p_nas"]]
     if fuse:
         seq = _fuse_pre_norms(seq)
 

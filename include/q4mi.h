@@ -239,6 +239,18 @@ size_t q4_gemm_workspace_bytes(int op, int M, int N, int K);
 int q4_gemm_w4a16_ws(const uint16_t* X, const uint32_t* wq,
                      const uint16_t* sc16, uint16_t* Y, int M, int N, int K,
                      void* ws, size_t ws_bytes, void* stream);
+/* The prefill gate and up GEMMs and the gelumul after them (p_g, p_u and
+ * p_gm: src/vk_engine.py:381-382, 421-422; vk/gelumul.comp:7-8) as one
+ * W4A16 product over an interleaved gate/up matrix (q4_interleave_rows; N
+ * = 2 I rows): Y f16 [M][N/2], Y[m][i] = f16(gelu_tanh(g) * u) with g and u
+ * the fp16-rounded products of rows 2i and 2i + 1, as the reference's fp16
+ * GEMM outputs reach its gelumul. fp32 partials go to ws
+ * (q4_gemm_w4a16_gated_workspace_bytes, required, 16-byte aligned) and
+ * the split-K reduce applies the gelumul. */
+size_t q4_gemm_w4a16_gated_workspace_bytes(int M, int N, int K);
+int q4_gemm_w4a16_gated(const uint16_t* X, const uint32_t* wq, const uint16_t* sc16,
+                        uint16_t* Y, int M, int N, int K, void* ws, size_t ws_bytes,
+                        void* stream);
 
 /* Per-row int8 activation quantizer: sa[m] = max(absmax/127, 1e-12),
  * A = clamp(rint(x / sa), -127, 127) (IEEE fp32 divide).

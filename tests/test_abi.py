@@ -214,3 +214,23 @@ def test_attention_alignment_errors_without_gpu(g4):
     assert st == g4._lib.Q4_ERR_ARG and "16-byte aligned" in _err(g4)
     st = lib.q4_prepkv(a, a, a, m, a, a, 8, 256, 4096, 6144, 0, 1024, 1024, a, null)
     assert st == g4._lib.Q4_ERR_ARG and "16-byte aligned" in _err(g4)
+
+
+def test_gated_w4a16_argument_errors_without_gpu(g4):
+    """The gated W4A16 GEMM (interleaved gate/up rows) takes an even row
+    count, a workspace of at least one split of fp32 partials, and 16-byte
+    aligned operands; every refusal comes before a launch."""
+    lib = g4._lib.lib()
+    a, m, null = C.c_void_p(1 << 20), C.c_void_p((1 << 20) + 8), C.c_void_p(0)
+    need = lib.q4_gemm_w4a16_gated_workspace_bytes(128, 30720, 3840)
+    assert need == 2 * 128 * 30720 * 4   # split 2 at the prefill chunk's gate/up
+    assert lib.q4_gemm_w4a16_gated_workspace_bytes(128, 30721, 3840) == 0
+    assert lib.q4_gemm_w4a16_gated_workspace_bytes(2048, 1024, 256) == 2048 * 1024 * 4  # split 1: still partials
+    st = lib.q4_gemm_w4a16_gated(a, a, a, a, 128, 30721, 3840, a, need, null)
+    assert st == g4._lib.Q4_ERR_ARG and "N even" in _err(g4)
+    st = lib.q4_gemm_w4a16_gated(a, a, a, a, 128, 30720, 3840, null, need, null)
+    assert st == g4._lib.Q4_ERR_ARG and "null" in _err(g4)
+    st = lib.q4_gemm_w4a16_gated(a, a, a, a, 128, 30720, 3840, a, need - 4, null)
+    assert st == g4._lib.Q4_ERR_ARG and "workspace too small" in _err(g4)
+    st = lib.q4_gemm_w4a16_gated(m, a, a, a, 128, 30720, 3840, a, need, null)
+    assert st == g4._lib.Q4_ERR_ARG and "16-byte aligned" in _err(g4)

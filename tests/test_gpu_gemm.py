@@ -9,6 +9,7 @@ import numpy as np
 import pytest
 import torch
 
+from oracle import decode_ops_oracle as D
 from oracle import q4_oracle as O
 from tests.helpers import synth_int4, to_np, upload_int4
 
@@ -224,6 +225,46 @@ def test_w4a16_two_kgroups_match_one(gpu, M, N, K, monkeypatch):
     assert np.abs(Y2 - Y1).max() <= np.abs(Y1).max() * 2.0 ** -9
     ref = O.gemm_w4a16_ref(to_np(X), q, s)
     assert O.normwise_rel_err(Y2.astype(np.float32), ref) <= 1e-3
+
+
+@pytest.mark.parametrize("M,I,K,dev_interleave", [(128, 15360, 3840, True), (128, 512, 256, True),
+                                                  (100, 330, 96, False), (37, 7, 224, False),
+                                                  (512, 1024, 1920, True)])
+def test_w4a16_gated_equals_separate_gemms_and_gelumul(gpu, M, I, K, dev_interleave, monkeypatch):
+    """The gated W4A16 GEMM over interleaved gate/up rows gives the separate
+    route's activations bit for bit (gate GEMM, up GEMM, each rounded to
+    fp16, then gelumul) when both split K the same way (Q4MI_W4A16_SPLIT),
+    and matches the oracle: gelu_tanh(f16(X Wg^T)) * f16(X Wu^T), rounded to
+    fp16, within an fp16 step of the largest output. Shapes: the prefill
+    chunk's gate/up (I 15360), a one-block last k-step (K % 64 = 32), an
+    output count that is no multiple of 4 (the reduce's scalar tail; rows
+    interleaved on the host, as q4_interleave_rows takes multiples of 32),
+    and two k-groups at M = 512."""
+    rng = np.random.default_rng(M + I + K)
+    qg, sg = synth_int4(rng, I, K)
+    qu, su = synth_int4(rng, I, K)
+    X = torch.from_numpy(rng.standard_normal((M, K)).astype(np.float16)).cuda()
+    wg, scg = upload_int4(qg, sg)
+    wu, scu = upload_int4(qu, su)
+    if dev_interleave:
+        wi, si = gpu.interleave_rows(wg, scg, wu, scu, I, K)
+    else:
+        qi, s_i = np.empty((2 * I, K), qg.dtype), np.empty((2 * I, K // 32), sg.dtype)
+        qi[0::2], qi[1::2], s_i[0::2], s_i[1::2] = qg, qu, sg, su
+        wi, si = upload_int4(qi, s_i)
+    split = max(1, gpu.gemm_workspace_bytes(M, 2 * I, K) // (M * 2 * I * 4))
+    monkeypatch.setenv("Q4MI_W4A16_SPLIT", str(split))
+    A = to_np(gpu.gemm_w4a16_gated(X, wi, si, 2 * I))
+    G = gpu.gemm_w4a16(X, wg, scg, I)
+    U = gpu.gemm_w4a16(X, wu, scu, I)
+    sep = to_np(gpu.pre_gelumul(G.reshape(-1), U.reshape(-1), torch.empty(M * I, dtype=torch.float16,
+                                                                            device="cuda"))).reshape(M, I)
+    assert np.array_equal(A.view(np.uint16), sep.view(np.uint16))
+    Xn = to_np(X)
+    g16 = O.gemm_w4a16_ref(Xn, qg, sg).astype(np.float16).astype(np.float64)
+    u16 = O.gemm_w4a16_ref(Xn, qu, su).astype(np.float16).astype(np.float64)
+    act = D.gelumul_ref(g16, u16)
+    assert np.abs(A.astype(np.float64) - act).max() <= np.abs(act).max() * 2.0 ** -9
 
 
 def test_w4a16_matches_f16_rounded_weights(gpu):

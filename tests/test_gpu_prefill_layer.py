@@ -47,11 +47,12 @@ def _f16(a):
     return np.asarray(a, np.float64).astype(np.float16).astype(np.float64)
 
 
-@pytest.mark.parametrize("fast", [False, True])
-def test_prefill_chunks_through_the_engine_mirror(g4, gpu, fast):
+@pytest.mark.parametrize("fast,gated", [(False, False), (True, False), (True, True)])
+def test_prefill_chunks_through_the_engine_mirror(g4, gpu, fast, gated):
     """fast: fp16 buffers between producers and GEMMs (no cast launches) and
     each pre_na fused with the pre_norm after it; otherwise the reference's
-    fp32 buffers, casts and separate launches."""
+    fp32 buffers, casts and separate launches. gated: gate/up and the
+    gelumul as one gated W4A16 GEMM over interleaved rows (p_gu)."""
     E = importlib.import_module("g4mi.vk_engine")
     MC = E.MC
     rng = np.random.default_rng(0)
@@ -109,6 +110,7 @@ def test_prefill_chunks_through_the_engine_mirror(g4, gpu, fast):
                  p_pfn=E.pre_norm_ds(Xp, nb["pfw"], Np, DUH, out_dtype=h16),
                  p_g=E.gemm_ds(gp[:2], Np, Gp, **gk), p_u=E.gemm_ds(up[:2], Np, Upp, **gk),
                  p_gm=E.pre_gelumul_ds(Gp, Upp, ACp, DUIp, in_dtype=h16, out_dtype=h16),
+                 p_gu=E.pre_gate_up_ds(gp[:2], up[:2], Np, ACp) if gated else None,
                  p_d=E.gemm_ds(dp[:2], ACp, Tp, **gk),
                  p_nas=E.pre_na_ds(Tp, nb["ofw"], Xp, nas, x_dtype=h16))
         layers.append((L, kc, vc))
