@@ -263,13 +263,14 @@ def bench_small_m(ops, reps: int = 6):
     return out
 
 
-def bench_prefill(ops, reps: int = 5, p0: int = 3968, gated: bool = True):
+def bench_prefill(ops, reps: int = 5, p0: int = 3968, stacked: bool = True):
     """One 128-token prefill chunk through the 48-layer stack with the
     batched-prefill layer graph (vk_engine.record_prefill: per layer
     pre_norm, q/k/v W4A16 GEMMs, pre_prepkv, pre_attn, o GEMM, pre_na +
     pre_norm, gate/up GEMMs, gelumul, down GEMM, pre_na), fp16 buffers
-    between producers and GEMMs, fused norms; with ``gated``, gate/up and the
-    gelumul run as one gated W4A16 GEMM over interleaved gate/up rows. Layers: 40 sliding (16 query
+    between producers and GEMMs, fused norms; with ``stacked``, q/k/v run as
+    one GEMM over their stacked rows and gate/up and the gelumul as one gated
+    W4A16 GEMM over interleaved gate/up rows. Layers: 40 sliding (16 query
     and 8 KV heads of 256, 1024-slot ring) and 8 global (16 query heads and
     one k == v head of 512, every sixth layer), H 3840, I 15360; the chunk
     is the last of a 4096-token prompt (p0 = 3968: sliding layers attend
@@ -303,6 +304,7 @@ def bench_prefill(ops, reps: int = 5, p0: int = 3968, gated: bool = True):
     Qp, Ap = E.Buf(MC * NHq * 512 * 4), E.Buf(MC * NHq * 512 * 4)
     Kp, Vp = E.Buf(MC * 8 * 256 * 4), E.Buf(MC * 8 * 256 * 4)
     Gp, Upp, ACp = E.Buf(MC * I * 4), E.Buf(MC * I * 4), E.Buf(MC * I * 4)
+    QKVp = E.Buf(MC * (NHq * 512 + 512) * 2)   # the stacked q/k/v GEMM's fp16 rows
     cosM = {hd: fbuf(MC * hd) for hd in (256, 512)}
     sinM = {hd: fbuf(MC * hd) for hd in (256, 512)}
     DYNP = E.buf_u32([p0, MC, 0, 0])
@@ -323,21 +325,27 @@ def bench_prefill(ops, reps: int = 5, p0: int = 3968, gated: bool = True):
         nb = {kk: fbuf(n, 0.1) for kk, n in dict(qnw=hd, knw=hd, inw=H, paw=H, pfw=H, ofw=H).items()}
         Pp = [nkv, hd, nk, 0, stride, window, 0, 0]
         Aa = [NHq, nq, hd, stride, window, NHq // nkv, 0, 0]
+        # stacked q/k/v: one GEMM, q, k (and v) at column offsets of one row
+        ldc = nq + (nk if glob else 2 * nk)
+        qsrc, ksrc, vsrc = (QKVp, QKVp, QKVp) if stacked else (Qp, Kp, Kp if glob else Vp)
+        kv_at = dict(ld=ldc, koff=nq, voff=nq if glob else nq + nk) if stacked else {}
+        q_at = dict(ldq=ldc) if stacked else {}
         nas = E.buf_u32([H, int(np.array([0.5], np.float32).view(np.uint32)[0]), 0, 0])
         layers.append(dict(
             p_in=E.pre_norm_ds(Xp, nb["inw"], Np, DUH, out_dtype=h16),
             p_q=E.gemm_ds(q, Np, Qp, **gk), p_k=E.gemm_ds(k, Np, Kp, **gk),
             p_v=None if glob else E.gemm_ds(v, Np, Vp, **gk),
-            p_prep=E.pre_prepkv_ds(Kp, Kp if glob else Vp, nb["knw"], cosM[hd], sinM[hd], kc, vc, Pp, DYNP,
-                                   kv_dtype=h16),
-            p_attn=E.pre_attn_ds(Qp, nb["qnw"], cosM[hd], sinM[hd], kc, vc, Ap, Aa, DYNP, nkv,
-                                 max_keys=prompt if glob else window, q_dtype=h16, out_dtype=h16),
+            p_qkv=E.gemm_cat_ds([q, k] + ([] if glob else [v]), Np, QKVp, **gk) if stacked else None,
+            p_prep=E.pre_prepkv_ds(ksrc, vsrc, nb["knw"], cosM[hd], sinM[hd], kc, vc, Pp, DYNP, kv_dtype=h16,
+                                   **kv_at),
+            p_attn=E.pre_attn_ds(qsrc, nb["qnw"], cosM[hd], sinM[hd], kc, vc, Ap, Aa, DYNP, nkv,
+                                 max_keys=prompt if glob else window, q_dtype=h16, out_dtype=h16, **q_at),
             p_o=E.gemm_ds(o, Ap, Tp, **gk),
             p_na=E.pre_na_ds(Tp, nb["paw"], Xp, DUH, x_dtype=h16),
             p_pfn=E.pre_norm_ds(Xp, nb["pfw"], Np, DUH, out_dtype=h16),
             p_g=E.gemm_ds(g, Np, Gp, **gk), p_u=E.gemm_ds(u, Np, Upp, **gk),
             p_gm=E.pre_gelumul_ds(Gp, Upp, ACp, DUIp, in_dtype=h16, out_dtype=h16),
-            p_gu=E.pre_gate_up_ds(g, u, Np, ACp) if gated else None,
+            p_gu=E.pre_gate_up_ds(g, u, Np, ACp) if stacked else None,
             p_d=E.gemm_ds(d, ACp, Tp, **gk),
             p_nas=E.pre_na_ds(Tp, nb["ofw"], Xp, nas, x_dtype=h16)))
     graph = E.record_prefill(layers, fuse=True)
@@ -999,8 +1007,8 @@ def main():
         return
     if args.prefill_only:
         print(f"[bench] prefill chunk {bench_prefill(ops, reps=max(1, args.steps // 40))}", flush=True)
-        print(f"[bench] prefill chunk, separate gate/up GEMMs and gelumul "
-              f"{bench_prefill(ops, reps=max(1, args.steps // 40), gated=False)}", flush=True)
+        print(f"[bench] prefill chunk, separate q/k/v and gate/up GEMMs and gelumul "
+              f"{bench_prefill(ops, reps=max(1, args.steps // 40), stacked=False)}", flush=True)
         return
     if args.ceilings_only:
         bench_ceilings(ops)
@@ -1032,7 +1040,7 @@ def main():
     small = bench_small_m(ops)
     print(f"[bench] small-M gemv {small}", flush=True)
     pre = bench_prefill(ops)
-    pre["separate_gate_up_ms_per_chunk"] = bench_prefill(ops, gated=False)["ms_per_chunk"]
+    pre["separate_qkv_gate_up_ms_per_chunk"] = bench_prefill(ops, stacked=False)["ms_per_chunk"]
     print(f"[bench] prefill chunk {pre}", flush=True)
     w8 = w4 = None
     if not args.no_gemm:

@@ -716,6 +716,15 @@ def _rows(t, M: int, D: int, what: str, dtypes=(torch.float32,)):
     _need(t, M * D * t.element_size(), what)
 
 
+def _rows_ld(t, M: int, ld: int, width: int, what: str, dtypes=(torch.float32,)):
+    """M rows of ``width`` elements ``ld`` apart (the last row needs only its width)."""
+    if t.dtype not in dtypes:
+        raise ValueError(f"{what} must be {' or '.join(str(d) for d in dtypes)}")
+    if ld < width:
+        raise ValueError(f"{what}: row stride {ld} is shorter than the row width {width}")
+    _need(t, ((M - 1) * ld + width) * t.element_size(), what)
+
+
 def pre_rmsnorm(x, w, y=None, *, M: int, D: int, y_dtype=torch.float32):
     """rmsnorm of each of the M rows of x [M][D] (fp32)."""
     _rows(x, M, D, "x")
@@ -762,8 +771,8 @@ def pre_prepkv(k, v, knw, cosM, sinM, kc, vc, *, M: int, ld: int, nkv: int, hd: 
     v = k if v is None else v
     if v.dtype != k.dtype:
         raise ValueError("k and v must share a dtype")
-    _rows(k, M, ld, "k", (torch.float32, torch.float16))
-    _rows(v, M, ld, "v", (torch.float32, torch.float16))
+    _rows_ld(k, M, ld, nkv * hd, "k", (torch.float32, torch.float16))
+    _rows_ld(v, M, ld, nkv * hd, "v", (torch.float32, torch.float16))
     _f32(knw, hd, "knw")
     _f32(cosM, M * hd, "cosM")
     _f32(sinM, M * hd, "sinM")
@@ -783,7 +792,7 @@ def pre_attn(q, qnw, cosM, sinM, kc, vc, out=None, *, M: int, ldq: int, nH: int,
              out_dtype=torch.float32) -> torch.Tensor:
     """Causal attention of the chunk's M tokens over the cache (after the
     chunk's K/V were written); q [M][ldq] fp32 or fp16; out [M][nH * hd]."""
-    _rows(q, M, ldq, "q", (torch.float32, torch.float16))
+    _rows_ld(q, M, ldq, nH * hd, "q", (torch.float32, torch.float16))
     _f32(qnw, hd, "qnw")
     _f32(cosM, M * hd, "cosM")
     _f32(sinM, M * hd, "sinM")

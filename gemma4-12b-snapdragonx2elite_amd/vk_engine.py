@@ -476,6 +476,34 @@ def pre_gelumul_ds(gate: Buf, up: Buf, out: Buf, du, in_dtype=torch.float32, out
     return OpDesc(ops.pre_gelumul, (gate.view(in_dtype, n), up.view(in_dtype, n), out.view(out_dtype, n)), {})
 
 
+def gemm_cat_ds(qws, inbuf: Buf, outbuf: Buf, **kw):
+    """The prefill GEMMs of several matrices that read the same rows (the
+    q, k and v projections, p_q/p_k/p_v: src/vk_engine.py:370-371, 414-415)
+    as one GEMM over their rows stacked (a copy made once): ``outbuf`` gets
+    rows of sum(N) elements, matrix i's outputs at column offset sum(N[:i]).
+    Each N must be a multiple of 64 (whole weight panels). ``kw`` as
+    :func:`gemm_ds`; returns its tuple (for :func:`gmm`)."""
+    Ns = [N for _, (N, _K) in qws]
+    K = qws[0][1][1]
+    if any(N % 64 for N in Ns) or any(k != K for _, (_n, k) in qws):
+        raise ValueError("stacked GEMMs need a common K and N multiples of 64")
+    parts = [q for q, _ in qws]
+
+    def cat(field):
+        vals = [getattr(q, field) for q in parts]
+        if any(v is None for v in vals):
+            return None
+        t = torch.cat([v.t.reshape(-1) for v in vals])
+        KEEP.append(t)
+        return Buf(tensor=t)
+    bw, bs16 = cat("bw"), cat("bs16")
+    bs = cat("bs") if len({q.bs.t.dtype for q in parts}) == 1 else None
+    w8, sw8 = cat("w8"), cat("sw8")
+    q0 = parts[0]
+    qw = QW(bw, bs if bs is not None else bs16, q0.split, q0.nblk, q0.inv, bs16, w8, sw8)
+    return gemm_ds((qw, (sum(Ns), K)), inbuf, outbuf, **kw)
+
+
 def pre_gate_up_ds(qg, qu, inbuf: Buf, actbuf: Buf) -> OpDesc | None:
     """The prefill gate and up GEMMs and the gelumul after them (p_g, p_u,
     p_gm: src/vk_engine.py:381-382, 421-422) as one gated W4A16 product
@@ -496,32 +524,39 @@ def pre_gate_up_ds(qg, qu, inbuf: Buf, actbuf: Buf) -> OpDesc | None:
 
 
 def pre_prepkv_ds(kbuf: Buf, vbuf: Buf, knw: Buf, cosM: Buf, sinM: Buf, kc: Buf, vc: Buf, Pp, dyn: Buf,
-                  kv_dtype=torch.float32) -> OpDesc:
+                  kv_dtype=torch.float32, ld: int | None = None, koff: int = 0, voff: int = 0) -> OpDesc:
     """The chunk's K/V into the caches (p_prep, :372-374); ``Pp`` = (nkv, hd,
     nk, 0, stride, window, 0, 0), ``vbuf`` the K buffer for k == v layers,
-    ``dyn`` = (p0, MC, 0, 0)."""
+    ``dyn`` = (p0, MC, 0, 0). ``ld``, ``koff``, ``voff`` (elements): rows of
+    K and V inside a wider buffer (the q/k/v GEMM's output, :func:`gemm_cat_ds`)."""
     nkv, hd, nk, _z, stride, window = (int(v) for v in np.asarray(Pp, np.uint32)[:6])
-    kw = dict(M=MC, ld=nk, nkv=nkv, hd=hd, stride=stride, window=window, dyn=dyn.view(torch.int32, 4))
-    return OpDesc(ops.pre_prepkv, (kbuf.view(kv_dtype, MC * nk), vbuf.view(kv_dtype, MC * nk), _f32v(knw, hd),
-                                   _f32v(cosM, MC * hd), _f32v(sinM, MC * hd), kc.view(torch.float16),
-                                   vc.view(torch.float16)), kw)
+    ld = ld or nk
+    esz = torch.empty((), dtype=kv_dtype).element_size()
+    n = (MC - 1) * ld + nk
+    kw = dict(M=MC, ld=ld, nkv=nkv, hd=hd, stride=stride, window=window, dyn=dyn.view(torch.int32, 4))
+    return OpDesc(ops.pre_prepkv, (kbuf.view(kv_dtype, n, koff * esz), vbuf.view(kv_dtype, n, voff * esz),
+                                   _f32v(knw, hd), _f32v(cosM, MC * hd), _f32v(sinM, MC * hd),
+                                   kc.view(torch.float16), vc.view(torch.float16)), kw)
 
 
 def pre_attn_ds(qbuf: Buf, qnw: Buf, cosM: Buf, sinM: Buf, kc: Buf, vc: Buf, out: Buf, Aa, dyn: Buf, nkv: int,
-                max_keys: int | None = None, q_dtype=torch.float32, out_dtype=torch.float32) -> OpDesc:
+                max_keys: int | None = None, q_dtype=torch.float32, out_dtype=torch.float32,
+                ldq: int | None = None) -> OpDesc:
     """Causal attention of the chunk (p_attn, :375-377); ``Aa`` = (nH, nq, hd,
     stride, window, grp, 0, 0). ``max_keys`` bounds the keys a token will
     see (default: the ring for sliding layers, the cache for global ones);
-    the split-key scratch is allocated here, before any recording."""
+    the split-key scratch is allocated here, before any recording. ``ldq``:
+    the q rows' stride inside a wider buffer (:func:`gemm_cat_ds`)."""
     nH, nq, hd, stride, window, grp = (int(v) for v in np.asarray(Aa, np.uint32)[:6])
     if nH // grp != nkv:
         raise ValueError(f"grp={grp} does not match nH={nH} / nkv={nkv}")
     mk = max_keys or (window if window > 0 else stride)
     ws = ops.pre_attn_workspace(MC, nH, nkv, hd, mk, qbuf.t.device)
     KEEP.append(ws)
-    kw = dict(M=MC, ldq=nq, nH=nH, nkv=nkv, hd=hd, stride=stride, window=window, max_keys=mk,
+    ldq = ldq or nq
+    kw = dict(M=MC, ldq=ldq, nH=nH, nkv=nkv, hd=hd, stride=stride, window=window, max_keys=mk,
               dyn=dyn.view(torch.int32, 4), ws=ws)
-    return OpDesc(ops.pre_attn, (qbuf.view(q_dtype, MC * nq), _f32v(qnw, hd), _f32v(cosM, MC * hd),
+    return OpDesc(ops.pre_attn, (qbuf.view(q_dtype, (MC - 1) * ldq + nq), _f32v(qnw, hd), _f32v(cosM, MC * hd),
                                  _f32v(sinM, MC * hd), kc.view(torch.float16), vc.view(torch.float16),
                                  out.view(out_dtype, MC * nH * hd)), kw)
 
@@ -534,17 +569,21 @@ def record_prefill(layers, fuse: bool = True) -> ops.Graph:
     reference's per-layer keys (``p_in`` ... ``p_nas``; ``p_v`` may be None;
     GEMM entries are :func:`gemm_ds` tuples); a layer with a ``p_gu``
     descriptor (:func:`pre_gate_up_ds`) runs it in place of ``p_g``, ``p_u``
-    and ``p_gm``. The reference submits one
+    and ``p_gm``, and one with ``p_qkv`` (:func:`gemm_cat_ds`) in place of
+    the q/k/v GEMMs. The reference submits one
     command buffer per layer; one graph holds them all here (the chunk's
     buffers persist between layers either way). With ``fuse``, each
     pre_na and the pre_norm of the same rows after it run as one launch."""
     seq = []
     for L in layers:
-        seq += [L["p_in"], ("gmm", L["p_q"]), ("gmm", L["p_k"])] + \
-               ([("gmm", L["p_v"])] if L.get("p_v") is not None else []) + \
-               [L["p_prep"], L["p_attn"], ("gmm", L["p_o"]), L["p_na"], L["p_pfn"]] + \
-               ([L["p_gu"]] if L.get("p_gu") is not None else [("gmm", L["p_g"]), ("gmm", L["p_u"]), L["p_gm"]]) + \
-               [("gmm", L["p_d"]), L["p_nas"]]
+        if L.get("p_qkv") is not None:
+            seq += [L["p_in"], ("gmm", L["p_qkv"])]
+        else:
+            seq += [L["p_in"], ("gmm", L["p_q"]), ("gmm", L["p_k"])] + \
+                   ([("gmm", L["p_v"])] if L.get("p_v") is not None else [])
+        seq += [L["p_prep"], L["p_attn"], ("gmm", L["p_o"]), L["p_na"], L["p_pfn"]] + \
+            ([L["p_gu"]] if L.get("p_gu") is not None else [("gmm", L["p_g"]), ("gmm", L["p_u"]), L["p_gm"]]) + \
+            [("gmm", L["p_d"]), L["p_nas"]]
     if fuse:
         seq = _fuse_pre_norms(seq)
 

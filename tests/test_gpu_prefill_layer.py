@@ -47,12 +47,14 @@ def _f16(a):
     return np.asarray(a, np.float64).astype(np.float16).astype(np.float64)
 
 
-@pytest.mark.parametrize("fast,gated", [(False, False), (True, False), (True, True)])
-def test_prefill_chunks_through_the_engine_mirror(g4, gpu, fast, gated):
+@pytest.mark.parametrize("fast,stacked", [(False, False), (True, False), (True, True)])
+def test_prefill_chunks_through_the_engine_mirror(g4, gpu, fast, stacked):
     """fast: fp16 buffers between producers and GEMMs (no cast launches) and
     each pre_na fused with the pre_norm after it; otherwise the reference's
-    fp32 buffers, casts and separate launches. gated: gate/up and the
-    gelumul as one gated W4A16 GEMM over interleaved rows (p_gu)."""
+    fp32 buffers, casts and separate launches. stacked: q/k/v as one GEMM
+    over their stacked rows (p_qkv; prepkv and attention read q, k, v at
+    column offsets of its rows) and gate/up with the gelumul as one gated
+    W4A16 GEMM over interleaved rows (p_gu)."""
     E = importlib.import_module("g4mi.vk_engine")
     MC = E.MC
     rng = np.random.default_rng(0)
@@ -76,6 +78,7 @@ def test_prefill_chunks_through_the_engine_mirror(g4, gpu, fast, gated):
     Xp, Np, Tp = fb(MC * H), fb(MC * H), fb(MC * H)
     Qp, Ap, Kp, Vp = fb(MC * maxq), fb(MC * maxq), fb(MC * maxk), fb(MC * maxk)
     Gp, Upp, ACp = fb(MC * I), fb(MC * I), fb(MC * I)
+    QKVp = fb(MC * (maxq + 2 * maxk))
     cosM = {hd: fb(MC * hd) for hd in (64, 128)}
     sinM = {hd: fb(MC * hd) for hd in (64, 128)}
     DYNP = E.buf_u32([0, MC, 0, 0])
@@ -98,19 +101,27 @@ def test_prefill_chunks_through_the_engine_mirror(g4, gpu, fast, gated):
         vsrc = Kp if keqv else Vp
         Pp = [nkv, hd, nk, 0, cfg["stride"], cfg["window"], 0, 0]
         Aa = [NH, nq, hd, cfg["stride"], cfg["window"], NH // nkv, 0, 0]
+        ldc = nq + (nk if keqv else 2 * nk)
+        qsrc, ksrc = (QKVp, QKVp) if stacked else (Qp, Kp)
+        vsrc = QKVp if stacked else vsrc
+        kv_at = dict(ld=ldc, koff=nq, voff=nq if keqv else nq + nk) if stacked else {}
+        q_at = dict(ldq=ldc) if stacked else {}
         nas = E.buf_u32([H, int(np.array([cfg["scl"]], np.float32).view(np.uint32)[0]), 0, 0])
         L = dict(p_in=E.pre_norm_ds(Xp, nb["inw"], Np, DUH, out_dtype=h16),
                  p_q=E.gemm_ds(qp[:2], Np, Qp, **gk), p_k=E.gemm_ds(kp[:2], Np, Kp, **gk),
                  p_v=None if keqv else E.gemm_ds(vp[:2], Np, Vp, **gk),
-                 p_prep=E.pre_prepkv_ds(Kp, vsrc, nb["knw"], cosM[hd], sinM[hd], kc, vc, Pp, DYNP, kv_dtype=h16),
-                 p_attn=E.pre_attn_ds(Qp, nb["qnw"], cosM[hd], sinM[hd], kc, vc, Ap, Aa, DYNP, nkv, q_dtype=h16,
-                                      out_dtype=h16),
+                 p_qkv=E.gemm_cat_ds([qp[:2], kp[:2]] + ([] if keqv else [vp[:2]]), Np, QKVp, **gk)
+                 if stacked else None,
+                 p_prep=E.pre_prepkv_ds(ksrc, vsrc, nb["knw"], cosM[hd], sinM[hd], kc, vc, Pp, DYNP, kv_dtype=h16,
+                                        **kv_at),
+                 p_attn=E.pre_attn_ds(qsrc, nb["qnw"], cosM[hd], sinM[hd], kc, vc, Ap, Aa, DYNP, nkv, q_dtype=h16,
+                                      out_dtype=h16, **q_at),
                  p_o=E.gemm_ds(op[:2], Ap, Tp, **gk),
                  p_na=E.pre_na_ds(Tp, nb["paw"], Xp, DUH, x_dtype=h16),
                  p_pfn=E.pre_norm_ds(Xp, nb["pfw"], Np, DUH, out_dtype=h16),
                  p_g=E.gemm_ds(gp[:2], Np, Gp, **gk), p_u=E.gemm_ds(up[:2], Np, Upp, **gk),
                  p_gm=E.pre_gelumul_ds(Gp, Upp, ACp, DUIp, in_dtype=h16, out_dtype=h16),
-                 p_gu=E.pre_gate_up_ds(gp[:2], up[:2], Np, ACp) if gated else None,
+                 p_gu=E.pre_gate_up_ds(gp[:2], up[:2], Np, ACp) if stacked else None,
                  p_d=E.gemm_ds(dp[:2], ACp, Tp, **gk),
                  p_nas=E.pre_na_ds(Tp, nb["ofw"], Xp, nas, x_dtype=h16))
         layers.append((L, kc, vc))
