@@ -263,14 +263,15 @@ def bench_small_m(ops, reps: int = 6):
     return out
 
 
-def bench_prefill(ops, reps: int = 5, p0: int = 3968, stacked: bool = True):
+def bench_prefill(ops, reps: int = 5, p0: int = 3968, stacked: bool = True, gemm_norms: bool = True):
     """One 128-token prefill chunk through the 48-layer stack with the
     batched-prefill layer graph (vk_engine.record_prefill: per layer
     pre_norm, q/k/v W4A16 GEMMs, pre_prepkv, pre_attn, o GEMM, pre_na +
     pre_norm, gate/up GEMMs, gelumul, down GEMM, pre_na), fp16 buffers
     between producers and GEMMs, fused norms; with ``stacked``, q/k/v run as
-    one GEMM over their stacked rows and gate/up and the gelumul as one gated
-    W4A16 GEMM over interleaved gate/up rows. Layers: 40 sliding (16 query
+    one GEMM over their stacked rows, gate/up and the gelumul as one gated
+    W4A16 GEMM over interleaved gate/up rows, and the o and down GEMMs hand
+    their split-K partials straight to the normadd after them. Layers: 40 sliding (16 query
     and 8 KV heads of 256, 1024-slot ring) and 8 global (16 query heads and
     one k == v head of 512, every sixth layer), H 3840, I 15360; the chunk
     is the last of a 4096-token prompt (p0 = 3968: sliding layers attend
@@ -348,7 +349,7 @@ def bench_prefill(ops, reps: int = 5, p0: int = 3968, stacked: bool = True):
             p_gu=E.pre_gate_up_ds(g, u, Np, ACp) if stacked else None,
             p_d=E.gemm_ds(d, ACp, Tp, **gk),
             p_nas=E.pre_na_ds(Tp, nb["ofw"], Xp, nas, x_dtype=h16)))
-    graph = E.record_prefill(layers, fuse=True)
+    graph = E.record_prefill(layers, fuse=True, gemm_norms=stacked and gemm_norms)
     att = E.record(lambda: [E.disp(L["p_attn"]) for L in layers])
 
     def timed(gr, n):
@@ -1007,6 +1008,8 @@ def main():
         return
     if args.prefill_only:
         print(f"[bench] prefill chunk {bench_prefill(ops, reps=max(1, args.steps // 40))}", flush=True)
+        print(f"[bench] prefill chunk, o/down GEMMs with their own split-K reduce "
+              f"{bench_prefill(ops, reps=max(1, args.steps // 40), gemm_norms=False)}", flush=True)
         print(f"[bench] prefill chunk, separate q/k/v and gate/up GEMMs and gelumul "
               f"{bench_prefill(ops, reps=max(1, args.steps // 40), stacked=False)}", flush=True)
         return

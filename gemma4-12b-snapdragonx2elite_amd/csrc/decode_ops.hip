@@ -106,15 +106,29 @@ __global__ void __launch_bounds__(NORM_THREADS) rmsnorm_kernel(const float* __re
 // or the final norm :250), in the same workgroup: h never leaves registers.
 // Row blockIdx.x of [rows][D] x, h and y; x fp32 or fp16 (a prefill GEMM's
 // output, whose fp32 value the reference's up-cast gives exactly).
+// XT_SPLITK: x is a W4A16 GEMM's fp32 split-K partials [split][rows][D]
+// (stride ps between splits); the value is that GEMM's fp16 output, f16 of
+// the sum in split order (its split-K reduce), taken without the round trip
+// through memory.
+constexpr int XT_SPLITK = 2;
 template <int XT>
-__device__ inline float ld_act(const void* x, long i) {
-  if constexpr (XT == Q4_DT_F16) return h2f(reinterpret_cast<const uint16_t*>(x)[i]);
-  else return reinterpret_cast<const float*>(x)[i];
+__device__ inline float ld_act(const void* x, long i, int split = 1, long ps = 0) {
+  if constexpr (XT == Q4_DT_F16) {
+    return h2f(reinterpret_cast<const uint16_t*>(x)[i]);
+  } else if constexpr (XT == XT_SPLITK) {
+    const float* p = reinterpret_cast<const float*>(x) + i;
+    float v = p[0];
+    for (int s = 1; s < split; ++s) v += p[(long)s * ps];
+    return h2f(f2h(v));
+  } else {
+    return reinterpret_cast<const float*>(x)[i];
+  }
 }
 template <bool FUSE, int YT, int XT = Q4_DT_F32>
 __global__ void __launch_bounds__(NORM_THREADS) normadd_kernel(const void* __restrict__ xin, const float* __restrict__ w,
                                                                float* __restrict__ h, int D, float sc,
-                                                               const float* __restrict__ w2, void* __restrict__ y) {
+                                                               const float* __restrict__ w2, void* __restrict__ y,
+                                                               int split = 1, long ps = 0) {
   __shared__ float red[NORM_THREADS / 64];
   const int t = threadIdx.x;
   const void* x = reinterpret_cast<const char*>(xin) + (long)blockIdx.x * D * (XT == Q4_DT_F16 ? 2 : 4);
@@ -124,16 +138,41 @@ __global__ void __launch_bounds__(NORM_THREADS) normadd_kernel(const void* __res
 #pragma unroll
   for (int r = 0; r < NORM_PER; ++r) {
     const int i = t + NORM_THREADS * r;
-    xv[r] = i < D ? ld_act<XT>(x, i) : 0.0f;
+    if constexpr (XT == XT_SPLITK) xv[r] = i < D ? reinterpret_cast<const float*>(x)[i] : 0.0f;
+    else xv[r] = i < D ? ld_act<XT>(x, i) : 0.0f;
     wv[r] = i < D ? w[i] : 0.0f;
     hv[r] = i < D ? h[i] : 0.0f;
     if constexpr (FUSE) w2v[r] = i < D ? w2[i] : 0.0f;
+  }
+  if constexpr (XT == XT_SPLITK) {
+    // the other splits, SB at a time with all their loads in flight, added in split order
+    constexpr int SB = 8;
+    const float* p = reinterpret_cast<const float*>(x);
+    for (int s0 = 1; s0 < split; s0 += SB) {
+      float tv[SB][NORM_PER];
+#pragma unroll
+      for (int u = 0; u < SB; ++u)
+#pragma unroll
+        for (int r = 0; r < NORM_PER; ++r) {
+          const int i = t + NORM_THREADS * r;
+          tv[u][r] = p[(long)min(s0 + u, split - 1) * ps + min(i, D - 1)];  // (clamped; unused past the ends)
+        }
+#pragma unroll
+      for (int u = 0; u < SB; ++u)
+        if (s0 + u < split) {
+#pragma unroll
+          for (int r = 0; r < NORM_PER; ++r)
+            if (t + NORM_THREADS * r < D) xv[r] += tv[u][r];
+        }
+    }
+#pragma unroll
+    for (int r = 0; r < NORM_PER; ++r) xv[r] = h2f(f2h(xv[r]));
   }
   float s = 0.0f;
 #pragma unroll
   for (int r = 0; r < NORM_PER; ++r) s = fmaf(xv[r], xv[r], s);
   for (int i = t + NORM_THREADS * NORM_PER; i < D; i += NORM_THREADS) {
-    const float v = ld_act<XT>(x, i);
+    const float v = ld_act<XT>(x, i, split, ps);
     s = fmaf(v, v, s);
   }
   const float inv = inv_rms(block_sum(s, red), D);
@@ -146,7 +185,7 @@ __global__ void __launch_bounds__(NORM_THREADS) normadd_kernel(const void* __res
     s2 = fmaf(hv[r], hv[r], s2);  // padding elements are 0
   }
   for (int i = t + NORM_THREADS * NORM_PER; i < D; i += NORM_THREADS) {
-    const float v = __fmul_rn(__fadd_rn(h[i], __fmul_rn(__fmul_rn(ld_act<XT>(x, i), inv), w[i])), sc);
+    const float v = __fmul_rn(__fadd_rn(h[i], __fmul_rn(__fmul_rn(ld_act<XT>(x, i, split, ps), inv), w[i])), sc);
     h[i] = v;
     s2 = fmaf(v, v, s2);
   }
@@ -853,6 +892,34 @@ int q4_pre_normadd_rmsnorm(const void* x, int x_dtype, const float* w, float* h,
   else
     pre_normadd_launch<true, Q4_DT_F32>(x, x_dtype, w, h, D, M, sc, w2, y, as_stream(stream));
   Q4_LAUNCHED("pre_normadd_rmsnorm");
+  return Q4_OK;
+}
+
+size_t q4_gemm_w4a16_normadd_workspace_bytes(int M, int N, int K) { return w4a16_partials_bytes(M, N, K); }
+
+int q4_gemm_w4a16_normadd(const uint16_t* X, const uint32_t* wq, const uint16_t* sc16, int M, int N, int K,
+                          const float* w, float* h, float scale, const float* w2, void* y, int y_dtype, void* ws,
+                          size_t ws_bytes, void* stream) {
+  clear_error();
+  Q4_ARG(w && h, "null pointer");
+  Q4_ARG((w2 == nullptr) == (y == nullptr), "w2 and y come together (the rmsnorm after the normadd)");
+  Q4_ARG(!y || y_dtype == Q4_DT_F32 || y_dtype == Q4_DT_F16, "bad y_dtype");
+  int split = 0;
+  if (int st = w4a16_partials(X, wq, sc16, M, N, K, ws, ws_bytes, as_stream(stream), &split)) return st;
+  const float sc = scale == 0.0f ? 1.0f : scale;
+  const float* P = reinterpret_cast<const float*>(ws);
+  const long ps = (long)M * N;
+  hipStream_t st = as_stream(stream);
+  if (!y)
+    hipLaunchKernelGGL((normadd_kernel<false, Q4_DT_F32, XT_SPLITK>), dim3(M), dim3(NORM_THREADS), 0, st, P, w, h, N,
+                       sc, nullptr, nullptr, split, ps);
+  else if (y_dtype == Q4_DT_F16)
+    hipLaunchKernelGGL((normadd_kernel<true, Q4_DT_F16, XT_SPLITK>), dim3(M), dim3(NORM_THREADS), 0, st, P, w, h, N,
+                       sc, w2, y, split, ps);
+  else
+    hipLaunchKernelGGL((normadd_kernel<true, Q4_DT_F32, XT_SPLITK>), dim3(M), dim3(NORM_THREADS), 0, st, P, w, h, N,
+                       sc, w2, y, split, ps);
+  Q4_LAUNCHED("gemm_w4a16_normadd normadd");
   return Q4_OK;
 }
 

@@ -1350,6 +1350,35 @@ static void launch_w4(const GemmArgs& g, int split, hipStream_t st) {
   hipLaunchKernelGGL((w4_kernel<OP, BM>), dim3(tiles(g.M, g.N, BM), split), dim3(256), 0, st, g, split);
 }
 
+size_t w4a16_partials_bytes(int M, int N, int K) {
+  if (M <= 0 || N <= 0 || K <= 0 || K % 32) return 0;
+  return (size_t)w4a16_split(M, N, K) * M * N * sizeof(float);
+}
+
+int w4a16_partials(const uint16_t* X, const uint32_t* wq, const uint16_t* sc16, int M, int N, int K, void* ws,
+                   size_t ws_bytes, hipStream_t st, int* split_out) {
+  Q4_ARG(M > 0 && N > 0 && K > 0 && K % 32 == 0, "bad W4A16 shape M=%d N=%d K=%d (K must be a multiple of 32)", M,
+         N, K);
+  Q4_ARG(X && wq && sc16 && ws, "null pointer");
+  Q4_ARG(((uintptr_t)X & 15) == 0 && ((uintptr_t)wq & 15) == 0 && ((uintptr_t)ws & 15) == 0,
+         "X, wq and the workspace must be 16-byte aligned");
+  const int split = w4a16_split(M, N, K);
+  Q4_ARG(ws_bytes >= w4a16_partials_bytes(M, N, K), "W4A16 partials workspace too small: %zu < %zu bytes", ws_bytes,
+         w4a16_partials_bytes(M, N, K));
+  Q4_ARG(2L * M * K < (1L << 31) && (long)pad_rows(N) * (K / BLK) * 16 < (1L << 31),
+         "W4A16 needs X and the int4 weights under 2 GiB (32-bit offsets)");
+  GemmArgs g{X, wq, sc16, nullptr, nullptr, 0, nullptr, nullptr, reinterpret_cast<float*>(ws), M, N, K};
+  if (pick_bm(M, N) == 256)
+    launch_w4p<256>(g, split, st);
+  else if (w4a16_kgroups(M, N, K, split) == 2)
+    launch_w4p<128, 2>(g, split, st);
+  else
+    launch_w4p<128>(g, split, st);
+  Q4_LAUNCHED("gemm_w4a16 (partials)");
+  *split_out = split;
+  return Q4_OK;
+}
+
 }  // namespace q4
 
 using namespace q4;
@@ -1525,8 +1554,8 @@ int q4_gemm_w4a16_ws(const uint16_t* X, const uint32_t* wq, const uint16_t* sc16
 }
 
 size_t q4_gemm_w4a16_gated_workspace_bytes(int M, int N, int K) {
-  if (M <= 0 || N <= 0 || N % 2 || K <= 0 || K % 32) return 0;
-  return (size_t)w4a16_split(M, N, K) * M * N * sizeof(float);
+  if (N % 2) return 0;
+  return w4a16_partials_bytes(M, N, K);
 }
 
 int q4_gemm_w4a16_gated(const uint16_t* X, const uint32_t* wq, const uint16_t* sc16, uint16_t* Y, int M, int N,
@@ -1534,26 +1563,12 @@ int q4_gemm_w4a16_gated(const uint16_t* X, const uint32_t* wq, const uint16_t* s
   clear_error();
   Q4_ARG(M > 0 && N > 0 && N % 2 == 0 && K > 0 && K % 32 == 0,
          "bad gated W4A16 shape M=%d N=%d K=%d (N even: interleaved gate/up rows; K a multiple of 32)", M, N, K);
-  Q4_ARG(X && wq && sc16 && Y && ws, "null pointer");
-  Q4_ARG(((uintptr_t)X & 15) == 0 && ((uintptr_t)wq & 15) == 0 && ((uintptr_t)ws & 15) == 0,
-         "X, wq and the workspace must be 16-byte aligned");
-  const int split = w4a16_split(M, N, K);
-  Q4_ARG(ws_bytes >= (size_t)split * M * N * sizeof(float), "gated W4A16 workspace too small: %zu < %zu bytes",
-         ws_bytes, (size_t)split * M * N * sizeof(float));
-  Q4_ARG(2L * M * K < (1L << 31) && (long)pad_rows(N) * (K / BLK) * 16 < (1L << 31),
-         "W4A16 needs X and the int4 weights under 2 GiB (32-bit offsets)");
-  // fp32 partials at every split (the reduce applies the gelumul)
-  GemmArgs g{X, wq, sc16, nullptr, nullptr, 0, Y, nullptr, reinterpret_cast<float*>(ws), M, N, K};
-  if (pick_bm(M, N) == 256)
-    launch_w4p<256>(g, split, as_stream(stream));
-  else if (w4a16_kgroups(M, N, K, split) == 2)
-    launch_w4p<128, 2>(g, split, as_stream(stream));
-  else
-    launch_w4p<128>(g, split, as_stream(stream));
-  Q4_LAUNCHED("gemm_w4a16_gated");
+  Q4_ARG(Y, "null pointer");
+  int split = 0;
+  if (int st = w4a16_partials(X, wq, sc16, M, N, K, ws, ws_bytes, as_stream(stream), &split)) return st;
   const long n = (long)M * (N / 2);
-  hipLaunchKernelGGL(splitk_reduce_gated_kernel, dim3(ceil_div(n, 1024)), dim3(256), 0, as_stream(stream), g.P, Y, n,
-                     split);
+  hipLaunchKernelGGL(splitk_reduce_gated_kernel, dim3(ceil_div(n, 1024)), dim3(256), 0, as_stream(stream),
+                     reinterpret_cast<const float*>(ws), Y, n, split);
   Q4_LAUNCHED("gemm_w4a16_gated reduce");
   return Q4_OK;
 }

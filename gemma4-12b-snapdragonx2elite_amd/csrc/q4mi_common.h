@@ -290,4 +290,12 @@ __device__ __forceinline__ void static_for(F&& f) {
 constexpr float NORM_EPS = 1e-6f;
 __device__ inline float inv_rms(float sumsq, int D) { return 1.0f / sqrtf(sumsq / (float)D + NORM_EPS); }
 
+// W4A16 GEMM into fp32 split-K partials [split][M][N] at every split
+// (split 1 included) for a caller that reduces them itself (gemm.hip):
+// w4a16_partials_bytes is the workspace it needs, *split_out the split it
+// used; returns Q4_OK or an error (set).
+size_t w4a16_partials_bytes(int M, int N, int K);
+int w4a16_partials(const uint16_t* X, const uint32_t* wq, const uint16_t* sc16, int M, int N, int K, void* ws,
+                   size_t ws_bytes, hipStream_t st, int* split_out);
+
 }  // namespace q4

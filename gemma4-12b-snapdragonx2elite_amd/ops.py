@@ -752,6 +752,43 @@ def pre_normadd(x, w, h, *, M: int, D: int, scale: float = 0.0, w2=None, y=None,
     return y
 
 
+def gemm_w4a16_normadd(X: torch.Tensor, wq: torch.Tensor, sc16: torch.Tensor, N: int, w, h, *, scale: float = 0.0,
+                       w2=None, y=None, y_dtype=torch.float32, ws: torch.Tensor | None = None):
+    """The W4A16 GEMM ``X @ W^T`` (N outputs per row, rounded to fp16 as
+    :func:`gemm_w4a16` rounds them) straight into :func:`pre_normadd` on h
+    [M][N] (and, with ``w2``, the rmsnorm of the new h into y), without the
+    GEMM's output in memory. ``ws``: at least
+    ``gemm_normadd_workspace_bytes(M, N, K)`` bytes."""
+    if X.dtype != torch.float16 or X.dim() != 2:
+        raise ValueError("X must be a 2-D float16 tensor")
+    M, K = X.shape
+    _check_int4(wq, sc16, N, K)
+    _f32(w, N, "w")
+    _rows(h, M, N, "h")
+    need = gemm_normadd_workspace_bytes(M, N, K)
+    if ws is None:
+        if _CAPTURING[0]:
+            raise RuntimeError("a GEMM + normadd inside a graph capture needs a workspace allocated before the "
+                               "capture (pass ws=...)")
+        ws = torch.empty(need, dtype=torch.uint8, device=X.device)
+    _need(ws, need, "GEMM + normadd workspace")
+    if w2 is None:
+        call("q4_gemm_w4a16_normadd", _p(X), _p(wq), _p(sc16), M, N, K, _p(w), _p(h), C.c_float(scale),
+             C.c_void_p(0), C.c_void_p(0), 0, _p(ws), _nbytes(ws), _stream())
+        return h
+    _f32(w2, N, "w2")
+    y = torch.empty(M, N, dtype=y_dtype, device=X.device) if y is None else y
+    _rows(y, M, N, "y", (torch.float32, torch.float16))
+    call("q4_gemm_w4a16_normadd", _p(X), _p(wq), _p(sc16), M, N, K, _p(w), _p(h), C.c_float(scale), _p(w2), _p(y),
+         _dt(y), _p(ws), _nbytes(ws), _stream())
+    return y
+
+
+def gemm_normadd_workspace_bytes(M: int, N: int, K: int) -> int:
+    """Workspace bytes of :func:`gemm_w4a16_normadd` (fp32 partials, at least one split)."""
+    return int(lib().q4_gemm_w4a16_normadd_workspace_bytes(M, N, K))
+
+
 def pre_gelumul(gate, up, out=None, out_dtype=torch.float32):
     """out = gelu_tanh(gate) * up elementwise (gate/up fp32 or fp16, same dtype)."""
     n = gate.numel()

@@ -561,7 +561,7 @@ def pre_attn_ds(qbuf: Buf, qnw: Buf, cosM: Buf, sinM: Buf, kc: Buf, vc: Buf, out
                                  out.view(out_dtype, MC * nH * hd)), kw)
 
 
-def record_prefill(layers, fuse: bool = True) -> ops.Graph:
+def record_prefill(layers, fuse: bool = True, gemm_norms: bool = False) -> ops.Graph:
     """Record the prefill of one ``MC``-token chunk through ``layers`` in the
     reference's order (rec_layer, src/vk_engine.py:410-424): per layer
     p_in, the q/k/v GEMMs, p_prep, p_attn, the o GEMM, p_na, p_pfn, the
@@ -570,7 +570,9 @@ def record_prefill(layers, fuse: bool = True) -> ops.Graph:
     GEMM entries are :func:`gemm_ds` tuples); a layer with a ``p_gu``
     descriptor (:func:`pre_gate_up_ds`) runs it in place of ``p_g``, ``p_u``
     and ``p_gm``, and one with ``p_qkv`` (:func:`gemm_cat_ds`) in place of
-    the q/k/v GEMMs. The reference submits one
+    the q/k/v GEMMs. With ``gemm_norms``, a GEMM whose fp16 output only
+    feeds the pre_na after it (the o and down projections) runs with that
+    normadd as :func:`ops.gemm_w4a16_normadd`. The reference submits one
     command buffer per layer; one graph holds them all here (the chunk's
     buffers persist between layers either way). With ``fuse``, each
     pre_na and the pre_norm of the same rows after it run as one launch."""
@@ -586,6 +588,8 @@ def record_prefill(layers, fuse: bool = True) -> ops.Graph:
             [("gmm", L["p_d"]), L["p_nas"]]
     if fuse:
         seq = _fuse_pre_norms(seq)
+    if gemm_norms:
+        seq = _fuse_gemm_normadd(seq)
 
     def body():
         for op in seq:
@@ -594,6 +598,34 @@ def record_prefill(layers, fuse: bool = True) -> ops.Graph:
             else:
                 disp(op)
     return record(body)
+
+
+def _fuse_gemm_normadd(seq):
+    """A W4A16 prefill GEMM with fp16 input and output followed by a pre_na
+    (or pre_na + pre_norm) that reads its output: one GEMM into split-K
+    partials and one normadd launch that sums them (:func:`ops.gemm_w4a16_normadd`)."""
+    out, i = [], 0
+    while i < len(seq):
+        a = seq[i]
+        b = seq[i + 1] if i + 1 < len(seq) else None
+        gem = a[1][1] if isinstance(a, tuple) and a and a[0] == "gmm" else None
+        if (gem is not None and gem[0] == "w4a16" and a[1][0] is None and a[1][2] is None and
+                isinstance(b, OpDesc) and b.fn is ops.pre_normadd and b.args[0].dtype == torch.float16 and
+                b.args[0].data_ptr() == gem[5].data_ptr() and b.kw["D"] == gem[4]):
+            _k, x16, wq, sc16, N, _y16, _ws = gem
+            M, K = x16.shape
+            need = ops.gemm_normadd_workspace_bytes(M, N, K)
+            ws = _stage("W4nws", need).view(torch.uint8, need)
+            _x, w, h = b.args
+            kw = dict(scale=b.kw.get("scale", 0.0), ws=ws)
+            if b.kw.get("w2") is not None:
+                kw.update(w2=b.kw["w2"], y=b.kw["y"])
+            out.append(OpDesc(ops.gemm_w4a16_normadd, (x16, wq, sc16, N, w, h.view(M, N)), kw))
+            i += 2
+        else:
+            out.append(a)
+            i += 1
+    return out
 
 
 def _fuse_pre_norms(seq):

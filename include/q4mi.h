@@ -248,6 +248,19 @@ int q4_gemm_w4a16_ws(const uint16_t* X, const uint32_t* wq,
  * (q4_gemm_w4a16_gated_workspace_bytes, required, 16-byte aligned) and
  * the split-K reduce applies the gelumul. */
 size_t q4_gemm_w4a16_gated_workspace_bytes(int M, int N, int K);
+/* A prefill GEMM whose output goes straight into the residual normadd (and
+ * the rmsnorm after it): the o projection with p_na (+ p_pfn) and the down
+ * projection with p_nas (+ the next layer's p_in), src/vk_engine.py:418-420,
+ * 423-424 and :413. W4A16 into fp32 partials in ws
+ * (q4_gemm_w4a16_normadd_workspace_bytes, required, 16-byte aligned), then
+ * one launch per row: x = f16 of the partials' sum in split order (the
+ * GEMM's fp16 output, as q4_gemm_w4a16_ws rounds it), h = (h + rmsnorm(x)
+ * w) * scale (scale 0 = 1) as q4_pre_normadd, and with w2 and y the
+ * rmsnorm of the new h into y (y_dtype) as q4_pre_normadd_rmsnorm. D = N. */
+size_t q4_gemm_w4a16_normadd_workspace_bytes(int M, int N, int K);
+int q4_gemm_w4a16_normadd(const uint16_t* X, const uint32_t* wq, const uint16_t* sc16, int M,
+                          int N, int K, const float* w, float* h, float scale, const float* w2,
+                          void* y, int y_dtype, void* ws, size_t ws_bytes, void* stream);
 int q4_gemm_w4a16_gated(const uint16_t* X, const uint32_t* wq, const uint16_t* sc16,
                         uint16_t* Y, int M, int N, int K, void* ws, size_t ws_bytes,
                         void* stream);

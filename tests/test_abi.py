@@ -234,3 +234,19 @@ def test_gated_w4a16_argument_errors_without_gpu(g4):
     assert st == g4._lib.Q4_ERR_ARG and "workspace too small" in _err(g4)
     st = lib.q4_gemm_w4a16_gated(m, a, a, a, 128, 30720, 3840, a, need, null)
     assert st == g4._lib.Q4_ERR_ARG and "16-byte aligned" in _err(g4)
+
+
+def test_gemm_normadd_argument_errors_without_gpu(g4):
+    """The GEMM + normadd entry point: w2 and y come together, a workspace of
+    fp32 partials is required, and the W4A16 checks apply."""
+    lib = g4._lib.lib()
+    a, null = C.c_void_p(1 << 20), C.c_void_p(0)
+    need = lib.q4_gemm_w4a16_normadd_workspace_bytes(128, 3840, 15360)
+    assert need == 16 * 128 * 3840 * 4   # the down projection at M = 128 splits K 16 ways
+    assert lib.q4_gemm_w4a16_normadd_workspace_bytes(128, 3840, 100) == 0
+    st = lib.q4_gemm_w4a16_normadd(a, a, a, 128, 3840, 15360, a, a, C.c_float(0.5), a, null, 1, a, need, null)
+    assert st == g4._lib.Q4_ERR_ARG and "come together" in _err(g4)
+    st = lib.q4_gemm_w4a16_normadd(a, a, a, 128, 3840, 15360, a, a, C.c_float(0.5), null, null, 1, a, need - 4, null)
+    assert st == g4._lib.Q4_ERR_ARG and "workspace too small" in _err(g4)
+    st = lib.q4_gemm_w4a16_normadd(a, a, a, 128, 3840, 15360, null, a, C.c_float(0.5), null, null, 1, a, need, null)
+    assert st == g4._lib.Q4_ERR_ARG and "null" in _err(g4)

@@ -267,6 +267,34 @@ def test_w4a16_gated_equals_separate_gemms_and_gelumul(gpu, M, I, K, dev_interle
     assert np.abs(A.astype(np.float64) - act).max() <= np.abs(act).max() * 2.0 ** -9
 
 
+@pytest.mark.parametrize("M,N,K,fuse_norm", [(128, 3840, 4096, True), (128, 3840, 15360, True),
+                                              (100, 320, 96, False), (37, 256, 224, True), (512, 1024, 1920, True)])
+def test_w4a16_normadd_equals_gemm_then_normadd(gpu, M, N, K, fuse_norm):
+    """The GEMM handing its split-K partials to the normadd (and the rmsnorm
+    after it) gives h and y bit for bit as q4_gemm_w4a16_ws (fp16 output)
+    followed by q4_pre_normadd(_rmsnorm): the normadd sums the partials in
+    split order and rounds to fp16 as the reduce does. Shapes: the prefill
+    o (K 4096) and down (K 15360) projections, a one-block last k-step, a
+    row count that is no multiple of the tile, two k-groups at M = 512."""
+    rng = np.random.default_rng(M + N + K)
+    q, s = synth_int4(rng, N, K)
+    wq, sc = upload_int4(q, s)
+    X = torch.from_numpy(rng.standard_normal((M, K)).astype(np.float16)).cuda()
+    w = torch.from_numpy((rng.random(N) + 0.5).astype(np.float32)).cuda()
+    w2 = torch.from_numpy((rng.random(N) + 0.5).astype(np.float32)).cuda()
+    h0 = torch.from_numpy(rng.standard_normal((M, N)).astype(np.float32)).cuda()
+    h1, h2 = h0.clone(), h0.clone()
+    Y = gpu.gemm_w4a16(X, wq, sc, N)
+    if fuse_norm:
+        y1 = gpu.pre_normadd(Y, w, h1, M=M, D=N, scale=0.5, w2=w2, y_dtype=torch.float16)
+        y2 = gpu.gemm_w4a16_normadd(X, wq, sc, N, w, h2, scale=0.5, w2=w2, y_dtype=torch.float16)
+        assert torch.equal(y1, y2)
+    else:
+        gpu.pre_normadd(Y, w, h1, M=M, D=N, scale=0.5)
+        gpu.gemm_w4a16_normadd(X, wq, sc, N, w, h2, scale=0.5)
+    assert torch.equal(h1, h2)
+
+
 def test_w4a16_matches_f16_rounded_weights(gpu):
     """The kernel's dequant is f16((q-8)*s) per weight: against that exact
     product (computed in float64) the only remaining error is fp32

@@ -53,8 +53,9 @@ def test_prefill_chunks_through_the_engine_mirror(g4, gpu, fast, stacked):
     each pre_na fused with the pre_norm after it; otherwise the reference's
     fp32 buffers, casts and separate launches. stacked: q/k/v as one GEMM
     over their stacked rows (p_qkv; prepkv and attention read q, k, v at
-    column offsets of its rows) and gate/up with the gelumul as one gated
-    W4A16 GEMM over interleaved rows (p_gu)."""
+    column offsets of its rows), gate/up with the gelumul as one gated
+    W4A16 GEMM over interleaved rows (p_gu), and the o and down GEMMs' split-K
+    partials summed inside the normadd after them (gemm_norms)."""
     E = importlib.import_module("g4mi.vk_engine")
     MC = E.MC
     rng = np.random.default_rng(0)
@@ -128,7 +129,7 @@ def test_prefill_chunks_through_the_engine_mirror(g4, gpu, fast, stacked):
         ref_layers.append(dict(cfg, nq=nq, nk=nk, q=qp[2], k=kp[2], v=None if keqv else vp[2], o=op[2], g=gp[2],
                                u=up[2], d=dp[2], kc=np.zeros(nkv * cfg["stride"] * hd, np.float16),
                                vc=np.zeros(nkv * cfg["stride"] * hd, np.float16), **norms))
-    graph = E.record_prefill([L for L, _, _ in layers], fuse=fast)
+    graph = E.record_prefill([L for L, _, _ in layers], fuse=fast, gemm_norms=stacked)
 
     gemm = lambda x, wd16: _f16(_f16(x) @ wd16.T)
     for chunk in range(CHUNKS):
