@@ -35,7 +35,10 @@ HIPCC_FLAGS = [
 
 # per-source extra flags: the small-M GEMV's MFMA results are read by VALU
 # at once; in VGPRs (not AGPRs) that saves one v_accvgpr_read per value
-FILE_FLAGS = {"gemv.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"]}
+FILE_FLAGS = {"gemv.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"],
+              # the online softmax rescales the attention accumulators every key tile: in AGPRs each
+              # rescale moved them out and back (~20% of the loop's instructions)
+              "prefill_attn.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"]}
 
 
 def _hipcc() -> str:
