@@ -270,8 +270,9 @@ def bench_prefill(ops, reps: int = 5, p0: int = 3968, stacked: bool = True, gemm
     pre_norm, gate/up GEMMs, gelumul, down GEMM, pre_na), fp16 buffers
     between producers and GEMMs, fused norms; with ``stacked``, q/k/v run as
     one GEMM over their stacked rows, gate/up and the gelumul as one gated
-    W4A16 GEMM over interleaved gate/up rows, and the o and down GEMMs hand
-    their split-K partials straight to the normadd after them. Layers: 40 sliding (16 query
+    W4A16 GEMM over interleaved gate/up rows, and the GEMMs hand their
+    split-K partials straight to the op after them (o and down: the normadd;
+    q/k/v: the q store and prepkv). Layers: 40 sliding (16 query
     and 8 KV heads of 256, 1024-slot ring) and 8 global (16 query heads and
     one k == v head of 512, every sixth layer), H 3840, I 15360; the chunk
     is the last of a 4096-token prompt (p0 = 3968: sliding layers attend
@@ -1008,7 +1009,7 @@ def main():
         return
     if args.prefill_only:
         print(f"[bench] prefill chunk {bench_prefill(ops, reps=max(1, args.steps // 40))}", flush=True)
-        print(f"[bench] prefill chunk, o/down GEMMs with their own split-K reduce "
+        print(f"[bench] prefill chunk, GEMMs with their own split-K reduce (no normadd/prepkv fusion) "
               f"{bench_prefill(ops, reps=max(1, args.steps // 40), gemm_norms=False)}", flush=True)
         print(f"[bench] prefill chunk, separate q/k/v and gate/up GEMMs and gelumul "
               f"{bench_prefill(ops, reps=max(1, args.steps // 40), stacked=False)}", flush=True)

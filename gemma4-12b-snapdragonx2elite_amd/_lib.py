@@ -61,6 +61,8 @@ SIGNATURES = {
     "q4_gemm_w4a16_gated_workspace_bytes": (_sz, [_i, _i, _i]),
     "q4_gemm_w4a16_gated": (_i, [_vp, _vp, _vp, _vp, _i, _i, _i, _vp, _sz, _vp]),
     "q4_gemm_w4a16_normadd_workspace_bytes": (_sz, [_i, _i, _i]),
+    "q4_gemm_w4a16_qkv_prepkv": (_i, [_vp, _vp, _vp, _i, _i, _i, _vp, _i, _i, _vp, _vp, _vp, _vp, _vp, _i, _i, _i,
+                                      _i, _i, _vp, _vp, _sz, _vp]),
     "q4_gemm_w4a16_normadd": (_i, [_vp, _vp, _vp, _i, _i, _i, _vp, _vp, _f, _vp, _vp, _i, _vp, _sz, _vp]),
     "q4_quant_act_i8": (_i, [_vp, _i, _vp, _vp, _i, _i, _vp]),
     "q4_gemm_w8a8": (_i, [_vp, _vp, _vp, _vp, _i, _vp, _vp, _i, _i, _i, _vp]),

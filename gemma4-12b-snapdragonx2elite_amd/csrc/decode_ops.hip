@@ -386,6 +386,68 @@ __global__ void __launch_bounds__(ATT_THREADS) pre_prepkv_kernel(const void* __r
   for (int i = t; i < hd; i += ATT_THREADS) vc[o + i] = f2h(hv[i]);
 }
 
+// The stacked q/k/v GEMM's split-K reduce and the prepkv after it in one
+// launch, from fp32 partials P [split][M][N] (N = nq + nk (+ nk), row m of
+// split s at s ps + m N): blocks x < QB sum 1024 q columns of token
+// blockIdx.y in split order and store them as fp16 (the GEMM's output) at
+// q + m ldq; block QB + h takes KV head h: its k and v columns, summed and
+// rounded the same way, then pre_prepkv_kernel's arithmetic into the
+// caches. The split sums run SB splits at a time with every load in flight.
+constexpr int QKV_QCOLS = 4 * ATT_THREADS;
+template <int SB = 8>
+__device__ inline float split_sum_f16(const float* p, int split, long ps) {
+  float v = p[0];
+  for (int s0 = 1; s0 < split; s0 += SB) {
+    float t[SB];
+#pragma unroll
+    for (int u = 0; u < SB; ++u) t[u] = p[(long)min(s0 + u, split - 1) * ps];
+#pragma unroll
+    for (int u = 0; u < SB; ++u)
+      if (s0 + u < split) v += t[u];
+  }
+  return h2f(f2h(v));
+}
+__global__ void __launch_bounds__(ATT_THREADS) pre_qkv_prepkv_kernel(
+    const float* __restrict__ P, int split, long ps, int N, int nq, int kvoff, int voff, uint16_t* __restrict__ q,
+    int ldq, const float* __restrict__ knw, const float* __restrict__ cosM, const float* __restrict__ sinM,
+    uint16_t* __restrict__ kc, uint16_t* __restrict__ vc, int hd, int stride, int window, int M,
+    const uint32_t* __restrict__ dyn) {
+  __shared__ float hv[ATT_MAX_HD], ro[ATT_MAX_HD], red[ATT_THREADS / 64];
+  const int QB = (nq + QKV_QCOLS - 1) / QKV_QCOLS;
+  const int m = blockIdx.y, t = threadIdx.x;
+  const float* row = P + (long)m * N;
+  if ((int)blockIdx.x < QB) {
+    const int c = blockIdx.x * QKV_QCOLS + 4 * t;
+    if (c >= nq) return;
+    v4f a = *reinterpret_cast<const v4f*>(row + c);
+    constexpr int SB = 8;
+    for (int s0 = 1; s0 < split; s0 += SB) {
+      v4f tv[SB];
+#pragma unroll
+      for (int u = 0; u < SB; ++u) tv[u] = *reinterpret_cast<const v4f*>(row + (long)min(s0 + u, split - 1) * ps + c);
+#pragma unroll
+      for (int u = 0; u < SB; ++u)
+        if (s0 + u < split) a += tv[u];
+    }
+    *reinterpret_cast<ushort4*>(q + (long)m * ldq + c) = make_ushort4(f2h(a.x), f2h(a.y), f2h(a.z), f2h(a.w));
+    return;
+  }
+  const int kvh = blockIdx.x - QB;
+  if (window > 0 && m + window < M) return;  // a later token of the chunk takes this slot
+  const uint32_t pos = dyn[0] + (uint32_t)m;
+  const int slot = kv_slot(pos, window);
+  if (slot >= stride) return;  // position past a global layer's cache: nothing to write
+  const long o = ((long)kvh * stride + slot) * hd;
+  for (int i = t; i < hd; i += ATT_THREADS) hv[i] = split_sum_f16(row + kvoff + kvh * hd + i, split, ps);
+  __syncthreads();
+  norm_rope_head(hv, ro, knw, cosM + (long)m * hd, sinM + (long)m * hd, hd, red);
+  for (int i = t; i < hd; i += ATT_THREADS) kc[o + i] = f2h(ro[i]);
+  for (int i = t; i < hd; i += ATT_THREADS) hv[i] = split_sum_f16(row + voff + kvh * hd + i, split, ps);
+  __syncthreads();
+  norm_rope_head(hv, ro, nullptr, nullptr, nullptr, hd, red);
+  for (int i = t; i < hd; i += ATT_THREADS) vc[o + i] = f2h(hv[i]);
+}
+
 
 // Loads of E halves (E = 1, 2, 4, 8) as one 2/4/8/16-byte access.
 template <int E>
@@ -896,6 +958,30 @@ int q4_pre_normadd_rmsnorm(const void* x, int x_dtype, const float* w, float* h,
 }
 
 size_t q4_gemm_w4a16_normadd_workspace_bytes(int M, int N, int K) { return w4a16_partials_bytes(M, N, K); }
+
+int q4_gemm_w4a16_qkv_prepkv(const uint16_t* X, const uint32_t* wq, const uint16_t* sc16, int M, int N, int K,
+                             uint16_t* q, int ldq, int nq, const float* knw, const float* cosM, const float* sinM,
+                             uint16_t* kc, uint16_t* vc, int nkv, int hd, int keqv, int stride, int window,
+                             const uint32_t* dyn, void* ws, size_t ws_bytes, void* stream) {
+  clear_error();
+  Q4_ARG(q && knw && cosM && sinM && kc && vc && dyn, "null pointer");
+  Q4_ARG(nq > 0 && nq % 4 == 0 && nkv > 0 && hd > 0 && hd % 2 == 0 && hd <= ATT_MAX_HD,
+         "bad q/k/v sizes nq=%d nkv=%d hd=%d (nq a multiple of 4, hd even and <= %d)", nq, nkv, hd, ATT_MAX_HD);
+  Q4_ARG(N == nq + nkv * hd * (keqv ? 1 : 2), "N=%d is not nq + nk%s = %d", N, keqv ? "" : " + nk",
+         nq + nkv * hd * (keqv ? 1 : 2));
+  Q4_ARG(ldq >= nq && ldq % 4 == 0 && ((uintptr_t)q & 7) == 0, "q rows: ldq=%d must be >= nq and a multiple of 4, "
+         "q 8-byte aligned", ldq);
+  Q4_ARG(stride > 0 && window >= 0 && window <= stride, "bad cache sizes stride=%d window=%d", stride, window);
+  int split = 0;
+  if (int st = w4a16_partials(X, wq, sc16, M, N, K, ws, ws_bytes, as_stream(stream), &split)) return st;
+  const int qb = (nq + QKV_QCOLS - 1) / QKV_QCOLS;
+  const int nk = nkv * hd;
+  hipLaunchKernelGGL(pre_qkv_prepkv_kernel, dim3(qb + nkv, M), dim3(ATT_THREADS), 0, as_stream(stream),
+                     reinterpret_cast<const float*>(ws), split, (long)M * N, N, nq, nq, keqv ? nq : nq + nk, q, ldq,
+                     knw, cosM, sinM, kc, vc, hd, stride, window, M, dyn);
+  Q4_LAUNCHED("gemm_w4a16_qkv_prepkv reduce + prepkv");
+  return Q4_OK;
+}
 
 int q4_gemm_w4a16_normadd(const uint16_t* X, const uint32_t* wq, const uint16_t* sc16, int M, int N, int K,
                           const float* w, float* h, float scale, const float* w2, void* y, int y_dtype, void* ws,

@@ -784,6 +784,37 @@ def gemm_w4a16_normadd(X: torch.Tensor, wq: torch.Tensor, sc16: torch.Tensor, N:
     return y
 
 
+def gemm_w4a16_qkv_prepkv(X: torch.Tensor, wq: torch.Tensor, sc16: torch.Tensor, N: int, q, knw, cosM, sinM, kc, vc,
+                          *, nq: int, ldq: int, nkv: int, hd: int, keqv: bool, stride: int, window: int,
+                          dyn: torch.Tensor, ws: torch.Tensor | None = None):
+    """The stacked q/k/v W4A16 GEMM (rows q, k (, v); N = nq + nk (+ nk))
+    with its q columns written as fp16 to ``q`` [M][ldq] and its k/v columns
+    going straight through :func:`pre_prepkv`'s arithmetic into the caches
+    (the k/v outputs are not stored). ``ws``: at least
+    ``gemm_normadd_workspace_bytes(M, N, K)`` bytes."""
+    if X.dtype != torch.float16 or X.dim() != 2:
+        raise ValueError("X must be a 2-D float16 tensor")
+    M, K = X.shape
+    if N != nq + nkv * hd * (1 if keqv else 2):
+        raise ValueError(f"N={N} is not nq + nk{'' if keqv else ' + nk'}")
+    _check_int4(wq, sc16, N, K)
+    _rows_ld(q, M, ldq, nq, "q", (torch.float16,))
+    _f32(knw, hd, "knw")
+    _f32(cosM, M * hd, "cosM")
+    _f32(sinM, M * hd, "sinM")
+    _kv_checks(kc, vc, nkv, stride, hd, dyn)
+    need = gemm_normadd_workspace_bytes(M, N, K)
+    if ws is None:
+        if _CAPTURING[0]:
+            raise RuntimeError("a q/k/v GEMM + prepkv inside a graph capture needs a workspace allocated before the "
+                               "capture (pass ws=...)")
+        ws = torch.empty(need, dtype=torch.uint8, device=X.device)
+    _need(ws, need, "q/k/v GEMM + prepkv workspace")
+    call("q4_gemm_w4a16_qkv_prepkv", _p(X), _p(wq), _p(sc16), M, N, K, _p(q), ldq, nq, _p(knw), _p(cosM), _p(sinM),
+         _p(kc), _p(vc), nkv, hd, int(bool(keqv)), stride, window, _p(dyn), _p(ws), _nbytes(ws), _stream())
+    return q
+
+
 def gemm_normadd_workspace_bytes(M: int, N: int, K: int) -> int:
     """Workspace bytes of :func:`gemm_w4a16_normadd` (fp32 partials, at least one split)."""
     return int(lib().q4_gemm_w4a16_normadd_workspace_bytes(M, N, K))

@@ -572,7 +572,9 @@ def record_prefill(layers, fuse: bool = True, gemm_norms: bool = False) -> ops.G
     and ``p_gm``, and one with ``p_qkv`` (:func:`gemm_cat_ds`) in place of
     the q/k/v GEMMs. With ``gemm_norms``, a GEMM whose fp16 output only
     feeds the pre_na after it (the o and down projections) runs with that
-    normadd as :func:`ops.gemm_w4a16_normadd`. The reference submits one
+    normadd as :func:`ops.gemm_w4a16_normadd`, and the stacked q/k/v GEMM
+    with the pre_prepkv after it as :func:`ops.gemm_w4a16_qkv_prepkv`. The
+    reference submits one
     command buffer per layer; one graph holds them all here (the chunk's
     buffers persist between layers either way). With ``fuse``, each
     pre_na and the pre_norm of the same rows after it run as one launch."""
@@ -589,7 +591,7 @@ def record_prefill(layers, fuse: bool = True, gemm_norms: bool = False) -> ops.G
     if fuse:
         seq = _fuse_pre_norms(seq)
     if gemm_norms:
-        seq = _fuse_gemm_normadd(seq)
+        seq = _fuse_gemm_prepkv(_fuse_gemm_normadd(seq))
 
     def body():
         for op in seq:
@@ -625,6 +627,39 @@ def _fuse_gemm_normadd(seq):
         else:
             out.append(a)
             i += 1
+    return out
+
+
+def _fuse_gemm_prepkv(seq):
+    """The stacked q/k/v GEMM (fp16 in and out) followed by the pre_prepkv
+    that reads its k/v columns: one GEMM into split-K partials and one
+    launch that stores the q columns and writes the caches
+    (:func:`ops.gemm_w4a16_qkv_prepkv`)."""
+    out, i = [], 0
+    while i < len(seq):
+        a = seq[i]
+        b = seq[i + 1] if i + 1 < len(seq) else None
+        gem = a[1][1] if isinstance(a, tuple) and a and a[0] == "gmm" else None
+        if (gem is not None and gem[0] == "w4a16" and a[1][0] is None and a[1][2] is None and
+                isinstance(b, OpDesc) and b.fn is ops.pre_prepkv and b.args[0].dtype == torch.float16 and
+                b.kw["ld"] == gem[4]):
+            _k, x16, wq, sc16, N, y16, _ws = gem
+            k, v = b.args[0], b.args[1]
+            koff = (k.data_ptr() - y16.data_ptr()) // 2
+            voff = (v.data_ptr() - y16.data_ptr()) // 2
+            nk = b.kw["nkv"] * b.kw["hd"]
+            keqv = voff == koff
+            if koff > 0 and N == koff + nk * (1 if keqv else 2) and (keqv or voff == koff + nk):
+                M, K = x16.shape
+                need = ops.gemm_normadd_workspace_bytes(M, N, K)
+                ws = _stage("W4nws", need).view(torch.uint8, need)
+                kw = {kk: b.kw[kk] for kk in ("nkv", "hd", "stride", "window", "dyn")}
+                out.append(OpDesc(ops.gemm_w4a16_qkv_prepkv, (x16, wq, sc16, N, y16.view(-1)) + tuple(b.args[2:]),
+                                  dict(kw, nq=koff, ldq=N, keqv=keqv, ws=ws)))
+                i += 2
+                continue
+        out.append(a)
+        i += 1
     return out
 
 

@@ -258,6 +258,19 @@ size_t q4_gemm_w4a16_gated_workspace_bytes(int M, int N, int K);
  * w) * scale (scale 0 = 1) as q4_pre_normadd, and with w2 and y the
  * rmsnorm of the new h into y (y_dtype) as q4_pre_normadd_rmsnorm. D = N. */
 size_t q4_gemm_w4a16_normadd_workspace_bytes(int M, int N, int K);
+/* The stacked q/k/v prefill GEMM (p_q, p_k, p_v over rows stacked q, k, v;
+ * k == v layers stack q, k) and the prepkv after it (p_prep:
+ * src/vk_engine.py:370-374, 414-416): W4A16 into fp32 partials in ws
+ * (q4_gemm_w4a16_normadd_workspace_bytes(M, N, K), required), then one
+ * launch that writes the q columns as fp16 (the GEMM's output, summed in
+ * split order) to q [M][ldq] and, per (KV head, token), the k and v columns
+ * rounded the same way through q4_pre_prepkv's arithmetic into kc and vc
+ * (the k and v outputs themselves are not stored). N = nq + nk (+ nk). */
+int q4_gemm_w4a16_qkv_prepkv(const uint16_t* X, const uint32_t* wq, const uint16_t* sc16, int M,
+                             int N, int K, uint16_t* q, int ldq, int nq, const float* knw,
+                             const float* cosM, const float* sinM, uint16_t* kc, uint16_t* vc,
+                             int nkv, int hd, int keqv, int stride, int window,
+                             const uint32_t* dyn, void* ws, size_t ws_bytes, void* stream);
 int q4_gemm_w4a16_normadd(const uint16_t* X, const uint32_t* wq, const uint16_t* sc16, int M,
                           int N, int K, const float* w, float* h, float scale, const float* w2,
                           void* y, int y_dtype, void* ws, size_t ws_bytes, void* stream);

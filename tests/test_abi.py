@@ -250,3 +250,24 @@ def test_gemm_normadd_argument_errors_without_gpu(g4):
     assert st == g4._lib.Q4_ERR_ARG and "workspace too small" in _err(g4)
     st = lib.q4_gemm_w4a16_normadd(a, a, a, 128, 3840, 15360, null, a, C.c_float(0.5), null, null, 1, a, need, null)
     assert st == g4._lib.Q4_ERR_ARG and "null" in _err(g4)
+
+
+def test_qkv_prepkv_argument_errors_without_gpu(g4):
+    """The stacked q/k/v GEMM + prepkv: N must be nq + nk (+ nk), the q rows
+    wide and aligned enough, the workspace large enough; refusals come before
+    any launch."""
+    lib = g4._lib.lib()
+    a, m, null = C.c_void_p(1 << 20), C.c_void_p((1 << 20) + 2), C.c_void_p(0)
+    need = lib.q4_gemm_w4a16_normadd_workspace_bytes(128, 8192, 3840)
+    args = lambda N=8192, q=a, ldq=8192, keqv=0, ws_bytes=need: (a, a, a, 128, N, 3840, q, ldq, 4096, a, a, a, a, a,
+                                                                 8, 256, keqv, 1024, 1024, a, a, ws_bytes, null)
+    st = lib.q4_gemm_w4a16_qkv_prepkv(*args(N=8190))
+    assert st == g4._lib.Q4_ERR_ARG and "nq + nk" in _err(g4)
+    st = lib.q4_gemm_w4a16_qkv_prepkv(*args(keqv=1))   # k == v: N would be 4096 + 2048
+    assert st == g4._lib.Q4_ERR_ARG and "nq + nk" in _err(g4)
+    st = lib.q4_gemm_w4a16_qkv_prepkv(*args(ldq=4094))
+    assert st == g4._lib.Q4_ERR_ARG and "ldq" in _err(g4)
+    st = lib.q4_gemm_w4a16_qkv_prepkv(*args(q=m))
+    assert st == g4._lib.Q4_ERR_ARG and "aligned" in _err(g4)
+    st = lib.q4_gemm_w4a16_qkv_prepkv(*args(ws_bytes=need - 4))
+    assert st == g4._lib.Q4_ERR_ARG and "workspace too small" in _err(g4)

@@ -295,6 +295,40 @@ def test_w4a16_normadd_equals_gemm_then_normadd(gpu, M, N, K, fuse_norm):
     assert torch.equal(h1, h2)
 
 
+@pytest.mark.parametrize("M,nH,nkv,hd,keqv,window,stride,p0", [
+    (128, 16, 8, 256, False, 1024, 1024, 3968),   # a sliding layer of the prefill chunk
+    (128, 16, 1, 512, True, 0, 4096, 3968),       # a global layer (k == v)
+    (37, 4, 2, 64, False, 16, 16, 5),             # ragged M; the chunk wraps the 16-slot ring
+    (64, 4, 2, 128, True, 0, 80, 40),             # global, positions past the cache depth write nothing
+])
+def test_w4a16_qkv_prepkv_equals_gemm_then_prepkv(gpu, M, nH, nkv, hd, keqv, window, stride, p0):
+    """The stacked q/k/v GEMM with its reduce and the prepkv in one launch
+    gives the q rows and both caches bit for bit as q4_gemm_w4a16_ws (fp16
+    output) followed by q4_pre_prepkv on its k/v columns."""
+    rng = np.random.default_rng(M + nH + hd + p0)
+    nq, nk = nH * hd, nkv * hd
+    N, K = nq + nk * (1 if keqv else 2), 512
+    q, s = synth_int4(rng, N, K)
+    wq, sc = upload_int4(q, s)
+    X = torch.from_numpy(rng.standard_normal((M, K)).astype(np.float16)).cuda()
+    knw = torch.from_numpy((rng.random(hd) + 0.5).astype(np.float32)).cuda()
+    cosM = torch.from_numpy((rng.random(M * hd) - 0.5).astype(np.float32)).cuda()
+    sinM = torch.from_numpy((rng.random(M * hd) - 0.5).astype(np.float32)).cuda()
+    dyn = torch.tensor([p0, M, 0, 0], dtype=torch.int32, device="cuda")
+    kc0 = torch.from_numpy(rng.standard_normal(nkv * stride * hd).astype(np.float16)).cuda()
+    vc0 = torch.from_numpy(rng.standard_normal(nkv * stride * hd).astype(np.float16)).cuda()
+    kc1, vc1, kc2, vc2 = kc0.clone(), vc0.clone(), kc0.clone(), vc0.clone()
+    Y = gpu.gemm_w4a16(X, wq, sc, N)
+    Yf = Y.reshape(-1)
+    gpu.pre_prepkv(Yf[nq:], Yf[nq if keqv else nq + nk:], knw, cosM, sinM, kc1, vc1, M=M, ld=N, nkv=nkv, hd=hd,
+                   stride=stride, window=window, dyn=dyn)
+    Q = torch.zeros(M, N, dtype=torch.float16, device="cuda")
+    gpu.gemm_w4a16_qkv_prepkv(X, wq, sc, N, Q, knw, cosM, sinM, kc2, vc2, nq=nq, ldq=N, nkv=nkv, hd=hd, keqv=keqv,
+                              stride=stride, window=window, dyn=dyn)
+    assert torch.equal(Q[:, :nq], Y[:, :nq])
+    assert torch.equal(kc1, kc2) and torch.equal(vc1, vc2)
+
+
 def test_w4a16_matches_f16_rounded_weights(gpu):
     """The kernel's dequant is f16((q-8)*s) per weight: against that exact
     product (computed in float64) the only remaining error is fp32
