@@ -54,8 +54,9 @@ def test_prefill_chunks_through_the_engine_mirror(g4, gpu, fast, stacked):
     fp32 buffers, casts and separate launches. stacked: q/k/v as one GEMM
     over their stacked rows (p_qkv; prepkv and attention read q, k, v at
     column offsets of its rows), gate/up with the gelumul as one gated
-    W4A16 GEMM over interleaved rows (p_gu), and the o and down GEMMs' split-K
-    partials summed inside the normadd after them (gemm_norms)."""
+    W4A16 GEMM over interleaved rows (p_gu), the o and down GEMMs' split-K
+    partials summed inside the normadd after them, and the q/k/v GEMM's inside
+    the q store + prepkv after it (gemm_norms)."""
     E = importlib.import_module("g4mi.vk_engine")
     MC = E.MC
     rng = np.random.default_rng(0)
