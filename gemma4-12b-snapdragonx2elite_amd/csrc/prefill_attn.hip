@@ -266,7 +266,10 @@ pre_attn_kernel(const void* __restrict__ qin, int ldq, const float* __restrict__
     tmax = slot_reduce<16, true>(tmax);
     const float mnew = fmaxf(mrun, tmax);
     const bool any = mnew != -INFINITY;
-    const float corr = any ? expf(mrun - mnew) : 1.0f;
+    // v_exp_f32-based exponentials (relative error ~1e-6): the weights are
+    // rounded to fp16 (2^-11) before use, and the reference's GLSL exp()
+    // is itself approximate; 8 fewer VALU operations per score
+    const float corr = any ? __expf(mrun - mnew) : 1.0f;
     float psum = 0.0f;
     v4h pb[NST];
 #pragma unroll
@@ -276,7 +279,7 @@ pre_attn_kernel(const void* __restrict__ qin, int ldq, const float* __restrict__
         // the weights the V product uses are the fp16-rounded ones: the sum
         // is taken over the same values, so the output stays a weighted mean
         // of V rows (the row maximum's weight, 1, is exact)
-        const _Float16 p = (_Float16)(any ? expf(sc[st][e] - mnew) : 0.0f);
+        const _Float16 p = (_Float16)(any ? __expf(sc[st][e] - mnew) : 0.0f);
         psum += (float)p;
         pb[st][e] = p;
       }
