@@ -738,7 +738,9 @@ __global__ void __launch_bounds__(256) w8p_kernel(const GemmArgs g) {
 // addresses between the MFMAs), and a second wave issues while the first
 // one's MFMAs run. Both groups run the same number of k-steps (barriers stay
 // paired); the second group's surplus step, for an odd count, reads zero
-// scales. Group 1 then hands its accumulators to group 0 through LDS, and
+// scales (its A chunks, those of the group's last k-step again, add nothing
+// unless they hold Inf or NaN, as with the absent block of an odd block
+// count). Group 1 then hands its accumulators to group 0 through LDS, and
 // group 0 adds them (acc0 + acc1) and runs the epilogue.
 template <int BM, bool TAIL, int KG = 1>
 __global__ void __launch_bounds__(256 * KG) w4p_kernel(const GemmArgs g, int split) {

@@ -645,7 +645,8 @@ def _fuse_gemm_prepkv(seq):
                 b.kw["ld"] == gem[4]):
             _k, x16, wq, sc16, N, y16, _ws = gem
             k, v = b.args[0], b.args[1]
-            koff = (k.data_ptr() - y16.data_ptr()) // 2
+            same = all(t.untyped_storage().data_ptr() == y16.untyped_storage().data_ptr() for t in (k, v))
+            koff = (k.data_ptr() - y16.data_ptr()) // 2 if same else -1
             voff = (v.data_ptr() - y16.data_ptr()) // 2
             nk = b.kw["nkv"] * b.kw["hd"]
             keqv = voff == koff
