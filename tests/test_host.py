@@ -129,3 +129,58 @@ def test_norm_gemv_fusion_alternates_the_residual(g4):
     assert [op[0] for op in out2] == ["gemvs_nx", "gemvs_nx"]
     assert out2[1][1][2].data_ptr() == out2[0][1][3].data_ptr()      # second reads what the first wrote
     assert out2[1][1][3].data_ptr() == h.data_ptr()
+
+
+def test_prefill_gemm_fusions_pair_gemms_with_their_consumers(g4, monkeypatch):
+    """The prefill recorder's GEMM passes on CPU tensors (no launch): a W4A16
+    GEMM with fp16 in and out followed by the pre_na(+norm) that reads its
+    output becomes one gemm_w4a16_normadd; the stacked q/k/v GEMM followed by
+    the pre_prepkv that reads its k/v columns becomes one
+    gemm_w4a16_qkv_prepkv (q stored at the GEMM's own output with ldq = N);
+    a consumer of some other buffer, or a GEMM with a cast, stays as it is."""
+    import torch
+
+    E = importlib.import_module("g4mi.vk_engine")
+    ops = importlib.import_module("g4mi.ops")
+    monkeypatch.setattr(E, "_stage", lambda name, nbytes: E.Buf(tensor=torch.empty(nbytes, dtype=torch.uint8)))
+    MC, K = E.MC, 256
+    x16 = torch.zeros(MC, K, dtype=torch.float16)
+    f32 = lambda n: torch.zeros(n, dtype=torch.float32)  # noqa: E731
+
+    def gmm(N, y16, cin=None):
+        return ("gmm", (cin, ("w4a16", x16, torch.zeros(N * K // 8, dtype=torch.int32),
+                              torch.zeros(N * K // 32, dtype=torch.float16), N, y16.view(MC, N), None), None, N, K))
+
+    # o projection + pre_na + pre_norm (already merged by _fuse_pre_norms)
+    N = 512
+    T = torch.zeros(MC * N, dtype=torch.float16)
+    h, w, w2, y = f32(MC * N), f32(N), f32(N), torch.zeros(MC * N, dtype=torch.float16)
+    na = E.OpDesc(ops.pre_normadd, (T, w, h), dict(M=MC, D=N, scale=0.5, w2=w2, y=y))
+    out = E._fuse_gemm_normadd([gmm(N, T), na])
+    assert len(out) == 1 and out[0].fn is ops.gemm_w4a16_normadd
+    assert out[0].args[3] == N and out[0].args[5].data_ptr() == h.data_ptr()
+    assert out[0].kw["scale"] == 0.5 and out[0].kw["y"] is y and out[0].kw["w2"] is w2
+    other = torch.zeros(MC * N, dtype=torch.float16)
+    na_other = E.OpDesc(ops.pre_normadd, (other, w, h), dict(M=MC, D=N, scale=0.5))
+    assert [type(o) for o in E._fuse_gemm_normadd([gmm(N, T), na_other])] == [tuple, E.OpDesc]
+    assert len(E._fuse_gemm_normadd([gmm(N, T, cin=("cast_dn", None, None)), na])) == 2
+
+    # stacked q/k/v + pre_prepkv, with and without k == v
+    nkv, hd, nq = 2, 64, 256
+    dyn = torch.zeros(4, dtype=torch.int32)
+    tabs = (f32(hd), f32(MC * hd), f32(MC * hd), torch.zeros(8, dtype=torch.float16), torch.zeros(8, dtype=torch.float16))
+    for keqv in (False, True):
+        nk = nkv * hd
+        N = nq + nk * (1 if keqv else 2)
+        QKV = torch.zeros(MC * N, dtype=torch.float16)
+        kv = QKV[nq:], QKV[nq if keqv else nq + nk:]
+        prep = E.OpDesc(ops.pre_prepkv, kv + tabs, dict(M=MC, ld=N, nkv=nkv, hd=hd, stride=64, window=32, dyn=dyn))
+        out = E._fuse_gemm_prepkv([gmm(N, QKV), prep])
+        assert len(out) == 1 and out[0].fn is ops.gemm_w4a16_qkv_prepkv
+        assert out[0].kw["nq"] == nq and out[0].kw["ldq"] == N and out[0].kw["keqv"] is keqv
+        assert out[0].args[4].data_ptr() == QKV.data_ptr() and out[0].kw["window"] == 32
+        # k/v rows of another buffer: no fusion
+        Kp = torch.zeros(MC * N, dtype=torch.float16)
+        prep2 = E.OpDesc(ops.pre_prepkv, (Kp[nq:], Kp[nq:]) + tabs,
+                         dict(M=MC, ld=N, nkv=nkv, hd=hd, stride=64, window=32, dyn=dyn))
+        assert len(E._fuse_gemm_prepkv([gmm(N, QKV), prep2])) == 2
