@@ -969,6 +969,7 @@ int q4_gemm_w4a16_qkv_prepkv(const uint16_t* X, const uint32_t* wq, const uint16
          "bad q/k/v sizes nq=%d nkv=%d hd=%d (nq a multiple of 4, hd even and <= %d)", nq, nkv, hd, ATT_MAX_HD);
   Q4_ARG(N == nq + nkv * hd * (keqv ? 1 : 2), "N=%d is not nq + nk%s = %d", N, keqv ? "" : " + nk",
          nq + nkv * hd * (keqv ? 1 : 2));
+  Q4_ARG(N % 4 == 0, "N=%d must be a multiple of 4 (16-byte partial rows)", N);
   Q4_ARG(ldq >= nq && ldq % 4 == 0 && ((uintptr_t)q & 7) == 0, "q rows: ldq=%d must be >= nq and a multiple of 4, "
          "q 8-byte aligned", ldq);
   Q4_ARG(stride > 0 && window >= 0 && window <= stride, "bad cache sizes stride=%d window=%d", stride, window);

@@ -1195,12 +1195,12 @@ __global__ void __launch_bounds__(256) splitk_reduce_kernel(const float* __restr
                                                             long n, int split) {
   const long i = ((long)blockIdx.x * 256 + threadIdx.x) * 4;
   if (i >= n) return;
-  if (i + 3 < n) {
+  if (i + 3 < n && (n & 3) == 0) {  // 16-byte loads need 16-byte split strides
     v4f t = *reinterpret_cast<const v4f*>(P + i);
     for (int s = 1; s < split; ++s) t += *reinterpret_cast<const v4f*>(P + (long)s * n + i);
     *reinterpret_cast<ushort4*>(Y + i) = make_ushort4(f2h(t.x), f2h(t.y), f2h(t.z), f2h(t.w));
   } else {
-    for (long e = i; e < n; ++e) {
+    for (long e = i; e < min(i + 4, n); ++e) {
       float t = P[e];
       for (int s = 1; s < split; ++s) t += P[(long)s * n + e];
       Y[e] = f2h(t);
@@ -1222,7 +1222,7 @@ __global__ void __launch_bounds__(256) splitk_reduce_gated_kernel(const float* _
   auto act = [](float g, float u) {
     return f2h(__fmul_rn(gelu_tanh(h2f(f2h(g))), h2f(f2h(u))));
   };
-  if (o + 3 < n) {
+  if (o + 3 < n && (np & 3) == 0) {  // 16-byte loads need 16-byte split strides
     v4f a = *reinterpret_cast<const v4f*>(P + 2 * o), b = *reinterpret_cast<const v4f*>(P + 2 * o + 4);
     for (int s = 1; s < split; ++s) {
       a += *reinterpret_cast<const v4f*>(P + (long)s * np + 2 * o);
@@ -1230,7 +1230,7 @@ __global__ void __launch_bounds__(256) splitk_reduce_gated_kernel(const float* _
     }
     *reinterpret_cast<ushort4*>(Y + o) = make_ushort4(act(a.x, a.y), act(a.z, a.w), act(b.x, b.y), act(b.z, b.w));
   } else {
-    for (long e = o; e < n; ++e) {
+    for (long e = o; e < min(o + 4, n); ++e) {
       float gs = P[2 * e], us = P[2 * e + 1];
       for (int s = 1; s < split; ++s) {
         gs += P[(long)s * np + 2 * e];
@@ -1534,6 +1534,7 @@ int q4_gemm_w4a16_ws(const uint16_t* X, const uint32_t* wq, const uint16_t* sc16
          K);
   Q4_ARG(X && wq && sc16 && Y, "null pointer");
   Q4_ARG(((uintptr_t)X & 15) == 0 && ((uintptr_t)wq & 15) == 0, "X and wq must be 16-byte aligned");
+  Q4_ARG(((uintptr_t)Y & 7) == 0, "Y must be 8-byte aligned");
   Q4_ARG(!ws || ((uintptr_t)ws & 15) == 0, "workspace must be 16-byte aligned");
   int split = w4a16_split(M, N, K);
   if (split > 1 && (!ws || ws_bytes < (size_t)split * M * N * sizeof(float))) split = 1;  // no room: one pass
@@ -1568,6 +1569,7 @@ int q4_gemm_w4a16_gated(const uint16_t* X, const uint32_t* wq, const uint16_t* s
   Q4_ARG(M > 0 && N > 0 && N % 2 == 0 && K > 0 && K % 32 == 0,
          "bad gated W4A16 shape M=%d N=%d K=%d (N even: interleaved gate/up rows; K a multiple of 32)", M, N, K);
   Q4_ARG(Y, "null pointer");
+  Q4_ARG(((uintptr_t)Y & 7) == 0, "Y must be 8-byte aligned");
   int split = 0;
   if (int st = w4a16_partials(X, wq, sc16, M, N, K, ws, ws_bytes, as_stream(stream), &split)) return st;
   const long n = (long)M * (N / 2);

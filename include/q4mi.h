@@ -223,7 +223,8 @@ int q4_gemv_multi(const void* x, int M, const uint32_t* wq,
                   int y_dtype, int N, int K, int exact, void* stream);
 
 /* ---- prefill GEMMs -------------------------------------------------------
- * W4A16: Y f16 [M][N] = X f16 [M][K] @ f16((q-8)*s)^T, fp32 accumulate.
+ * W4A16: Y f16 [M][N] = X f16 [M][K] @ f16((q-8)*s)^T, fp32 accumulate; X
+ * and wq 16-byte aligned, Y 8-byte aligned.
  * Replaces coopgemm_i4h.comp (vk/coopgemm_i4h.comp:13-35) as wired by
  * gemm_ds()/gmm() (src/vk_engine.py:351-365, 391-400). */
 int q4_gemm_w4a16(const uint16_t* X, const uint32_t* wq, const uint16_t* sc16,

@@ -192,7 +192,8 @@ def test_w4a8_weights_once_then_w8a8_bit_identical(gpu, N, K):
 
 # ----------------------------------------------------------------- W4A16
 @pytest.mark.parametrize("M,N,K", [(64, 256, 32), (100, 320, 96), (40, 300, 224), (128, 3840, 15360),
-                                   (512, 15360, 3840), (512, 3840, 15360), (1024, 8192, 256), (2048, 8192, 96)])
+                                   (512, 15360, 3840), (512, 3840, 15360), (1024, 8192, 256), (2048, 8192, 96),
+                                   (37, 70, 15360)])   # split K with M N not a multiple of 4: scalar reduce
 def test_w4a16(gpu, M, N, K):
     rng = np.random.default_rng(M + 2 * N + K)
     q, s = synth_int4(rng, N, K)
@@ -229,7 +230,7 @@ def test_w4a16_two_kgroups_match_one(gpu, M, N, K, monkeypatch):
 
 @pytest.mark.parametrize("M,I,K,dev_interleave", [(128, 15360, 3840, True), (128, 512, 256, True),
                                                   (100, 330, 96, False), (37, 7, 224, False),
-                                                  (512, 1024, 1920, True)])
+                                                  (512, 1024, 1920, True), (37, 35, 15360, False)])
 def test_w4a16_gated_equals_separate_gemms_and_gelumul(gpu, M, I, K, dev_interleave, monkeypatch):
     """The gated W4A16 GEMM over interleaved gate/up rows gives the separate
     route's activations bit for bit (gate GEMM, up GEMM, each rounded to
