@@ -207,7 +207,8 @@ def bench_gemv_single(ops, N: int, K: int, e4m3: bool, reps: int = 10):
 def bench_small_m(ops, reps: int = 6):
     """Small-M GEMV (speculative-decode verification: M tokens against one
     matrix) on the decode shapes, each path timed as a graph of launches over
-    distinct weights (>= 1.5 GB): the MFMA path, the bit-exact VALU path, the
+    distinct weights (>= 1.5 GB): the MFMA path (K split where planned, and
+    unsplit beside it), the bit-exact VALU path, the
     W4A16 prefill GEMM at the same M, and M single-vector GEMVs. GB/s counts
     the weight and scale bytes once per launch (what one GEMV reads)."""
     import torch
@@ -248,13 +249,19 @@ def bench_small_m(ops, reps: int = 6):
         for M in (4, 8, 16):
             X = torch.randn((M, K), device=dev, generator=gen).to(torch.float16)
             Y = torch.empty((M, N), dtype=torch.float16, device=dev)
-            t_mm = timed(lambda i: ops.gemv_multi(X, mats[i][0], mats[i][1], N, K, y=Y), n)
+            mws = ops.gemv_multi_workspace_bytes(M, N, K)
+            mws = torch.empty(mws, dtype=torch.uint8, device=dev) if mws else None
+            t_mm = timed(lambda i: ops.gemv_multi(X, mats[i][0], mats[i][1], N, K, y=Y, ws=mws), n)
+            t_mm1 = timed(lambda i: ops.gemv_multi(X, mats[i][0], mats[i][1], N, K, y=Y, ksplit=False), n) \
+                if mws is not None else t_mm
             t_ex = timed(lambda i: ops.gemv_multi(X, mats[i][0], mats[i][1], N, K, y=Y, exact=True), n)
             need = ops.gemm_workspace_bytes(M, N, K)
             ws = torch.empty(need, dtype=torch.uint8, device=dev) if need else None
             t_w4 = timed(lambda i: ops.gemm_w4a16(X, mats[i][0], mats[i][1], N, Y=Y, ws=ws), n)
             out[f"{name}_{N}x{K}_M{M}"] = {
                 "mfma_us": round(t_mm, 2), "mfma_GBps": round(per / t_mm / 1e3, 1),
+                "mfma_k_split": ops.gemv_multi_workspace_bytes(M, N, K) // (4 * M * N),
+                "mfma_unsplit_us": round(t_mm1, 2),
                 "exact_us": round(t_ex, 2), "w4a16_gemm_us": round(t_w4, 2),
                 "m_single_gemvs_us": round(M * t1, 2), "speedup_vs_w4a16": round(t_w4 / t_mm, 2),
                 "speedup_vs_m_gemvs": round(M * t1 / t_mm, 2)}
@@ -991,6 +998,8 @@ def main():
                     help="run only the W8A8 and W4A16 legs; prints their results, no JSON line")
     ap.add_argument("--prefill-only", action="store_true",
                     help="run only the prefill-chunk leg; prints its result, no JSON line")
+    ap.add_argument("--small-m-only", action="store_true",
+                    help="run only the small-M GEMV leg; prints its result, no JSON line")
     ap.add_argument("--token-only", action="store_true",
                     help="run only the whole-token legs (reference dispatches, then fused) for --steps replays; "
                          "prints their results, no JSON line")
@@ -1016,6 +1025,9 @@ def main():
         return
     if args.ceilings_only:
         bench_ceilings(ops)
+        return
+    if args.small_m_only:
+        print(f"[bench] small-M gemv {bench_small_m(ops)}", flush=True)
         return
     if args.gemm_only:
         print(f"[bench] w8a8 {bench_w8a8(ops)}", flush=True)

@@ -54,6 +54,8 @@ SIGNATURES = {
     "q4_pre_attn": (_i, [_vp, _i, _i, _vp, _vp, _vp, _vp, _vp, _vp, _i, _i, _i, _i, _i, _i, _i, _i, _i, _vp, _vp,
                          _sz, _vp]),
     "q4_gemv_multi": (_i, [_vp, _i, _vp, _vp, _i, _f, _vp, _i, _i, _i, _i, _vp]),
+    "q4_gemv_multi_workspace_bytes": (_sz, [_i, _i, _i]),
+    "q4_gemv_multi_ws": (_i, [_vp, _i, _vp, _vp, _i, _f, _vp, _i, _i, _i, _vp, _sz, _vp]),
     "q4_interleave_rows": (_i, [_vp, _vp, _vp, _vp, _i, _i, _i, _vp, _vp, _vp]),
     "q4_gemm_w4a16": (_i, [_vp, _vp, _vp, _vp, _i, _i, _i, _vp]),
     "q4_gemm_workspace_bytes": (_sz, [_i, _i, _i, _i]),

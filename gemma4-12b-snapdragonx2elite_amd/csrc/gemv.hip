@@ -633,7 +633,7 @@ __device__ inline uint32_t mm_scale(const uint8_t* sbase, uint32_t voff) {
 template <int T, int U, int ST, int YT>
 __global__ void __launch_bounds__(GEMV_THREADS)
 gemv_mm_kernel(const uint16_t* __restrict__ X, int M, const uint8_t* __restrict__ wq, const void* __restrict__ scv,
-               float outscale, void* __restrict__ Y, int N, int nblk) {
+               float outscale, void* __restrict__ Y, int N, int nblk, int kspan, float* __restrict__ part) {
   constexpr int BPS = 4 / T;                      // blocks per step
   constexpr int L = BPS + 1 + 4;                  // loads per step: x slices, the unit, 4 scales
   constexpr int SB = ST == Q4_SCALE_F16 ? 2 : 1;  // scale bytes
@@ -643,15 +643,17 @@ gemv_mm_kernel(const uint16_t* __restrict__ X, int M, const uint8_t* __restrict_
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // uniform: block indices and bases live in SGPRs
   const int c = lane & 15, g = lane >> 4;
   const int n0 = xcd_major(blockIdx.x, gridDim.x) * 16 * T;
+  // K split ky (blockIdx.y) owns blocks [kb0, kb0 + nb); the host leaves no split empty
+  const int ky = blockIdx.y, kb0 = ky * kspan, nb = min(kspan, nblk - kb0);
   // unit index of (row n0 + r, block b) = pu + r + 64 b (the 16T rows lie in one panel)
   const long pu = (long)(n0 / PANEL) * nblk * PANEL + (n0 % PANEL);
-  const uint8_t* xbase = reinterpret_cast<const uint8_t*>(X);
-  const uint8_t* wbase = wq + pu * 16;
-  const uint8_t* sbase = reinterpret_cast<const uint8_t*>(scv) + pu * SB;
+  const uint8_t* xbase = reinterpret_cast<const uint8_t*>(X) + (long)kb0 * (BLK * 2);
+  const uint8_t* wbase = wq + pu * 16 + (long)kb0 * (PANEL * 16);
+  const uint8_t* sbase = reinterpret_cast<const uint8_t*>(scv) + (pu + (long)kb0 * PANEL) * SB;
   const uint32_t xo = (uint32_t)min(c, M - 1) * (uint32_t)(nblk * BLK * 2) + g * 16;
   const int lrow = 16 * (g % T) + c, lblk = g / T;  // the unit lane (c, g) loads: row, block within the step
   const uint32_t so = c * SB;
-  const int nsteps = (nblk + BPS - 1) / BPS;
+  const int nsteps = (nb + BPS - 1) / BPS;
   const int rounds = ((nsteps + GEMV_WAVES - 1) / GEMV_WAVES + U - 1) / U;
   v4u xr[U][BPS], wr[U];
   uint32_t sr[U][4];
@@ -659,12 +661,12 @@ gemv_mm_kernel(const uint16_t* __restrict__ X, int M, const uint8_t* __restrict_
     const int b0 = (wave + GEMV_WAVES * s) * BPS;  // first block of the step
     static_for<0, BPS>([&](auto ic) {
       constexpr int i = decltype(ic)::value;
-      xr[u][i] = ld16_so(xbase + (long)min(b0 + i, nblk - 1) * (BLK * 2), xo);
+      xr[u][i] = ld16_so(xbase + (long)min(b0 + i, nb - 1) * (BLK * 2), xo);
     });
-    wr[u] = ld16_so(wbase, (uint32_t)(lrow * 16) + ((uint32_t)min(b0 + lblk, nblk - 1) << 10));
+    wr[u] = ld16_so(wbase, (uint32_t)(lrow * 16) + ((uint32_t)min(b0 + lblk, nb - 1) << 10));
     static_for<0, 4>([&](auto jc) {
       constexpr int j = decltype(jc)::value;
-      sr[u][j] = mm_scale<ST, 16 * (j % T) * SB>(sbase + (long)min(b0 + j / T, nblk - 1) * (PANEL * SB), so);
+      sr[u][j] = mm_scale<ST, 16 * (j % T) * SB>(sbase + (long)min(b0 + j / T, nb - 1) * (PANEL * SB), so);
     });
   };
   v4f acc[T];
@@ -672,18 +674,18 @@ gemv_mm_kernel(const uint16_t* __restrict__ X, int M, const uint8_t* __restrict_
   for (int t = 0; t < T; ++t) acc[t] = v4f{0.0f, 0.0f, 0.0f, 0.0f};
   auto use = [&](int u, int s) {
     const int b0 = (wave + GEMV_WAVES * s) * BPS;
-    if (b0 < nblk) {
+    if (b0 < nb) {
       const v4u w = transpose_rows(wr[u]);
       v4f d[4];
       static_for<0, 4>([&](auto jc) {
         constexpr int j = decltype(jc)::value;
-        if (j / T == 0 || b0 + j / T < nblk)
+        if (j / T == 0 || b0 + j / T < nb)
           d[j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(v8h, xr[u][j / T]), codes_to_h8(w[j]),
                                                         v4f{0.0f, 0.0f, 0.0f, 0.0f}, 0, 0, 0);
       });
       static_for<0, 4>([&](auto jc) {
         constexpr int j = decltype(jc)::value;
-        if (j / T == 0 || b0 + j / T < nblk) {
+        if (j / T == 0 || b0 + j / T < nb) {
           const float sc = scale_value<ST>(sr[u][j]);
 #pragma unroll
           for (int r = 0; r < 4; ++r) acc[j % T][r] = fmaf(sc, d[j][r], acc[j % T][r]);
@@ -728,11 +730,42 @@ gemv_mm_kernel(const uint16_t* __restrict__ X, int M, const uint8_t* __restrict_
     for (int r = 0; r < 4; ++r) {
       const int m = 4 * g + r;
       if (m < M && n < N) {
+        if (part) {  // split K: this split's fp32 sums, scaled after the split-order sum
+          part[((long)ky * M + m) * N + n] = y[r];
+          continue;
+        }
         const float v = y[r] * outscale;
         if constexpr (YT == Q4_DT_F16) reinterpret_cast<uint16_t*>(Y)[(long)m * N + n] = f2h(v);
         else reinterpret_cast<float*>(Y)[(long)m * N + n] = v;
       }
     }
+  }
+}
+
+// Y[e] = (P[0][e] + P[1][e] + ... + P[split-1][e]) * outscale over the
+// split partials P[split][mn] (mn = M * N, rows of Y contiguous), summed in
+// split order. VEC: four outputs per thread (mn % 4 == 0, Y aligned to four
+// outputs; the partials always are, at 16-byte split strides).
+template <int YT, bool VEC>
+__global__ void __launch_bounds__(256)
+gemv_mm_reduce_kernel(const float* __restrict__ P, void* __restrict__ Y, long mn, int split, float outscale) {
+  const long e = ((long)blockIdx.x * 256 + threadIdx.x) * (VEC ? 4 : 1);
+  if (e >= mn) return;
+  if constexpr (VEC) {
+    v4f t = *reinterpret_cast<const v4f*>(P + e);
+    for (int s = 1; s < split; ++s) t += *reinterpret_cast<const v4f*>(P + (long)s * mn + e);
+    t *= outscale;
+    if constexpr (YT == Q4_DT_F16)
+      *reinterpret_cast<ushort4*>(reinterpret_cast<uint16_t*>(Y) + e) =
+          make_ushort4(f2h(t[0]), f2h(t[1]), f2h(t[2]), f2h(t[3]));
+    else
+      *reinterpret_cast<v4f*>(reinterpret_cast<float*>(Y) + e) = t;
+  } else {
+    float t = P[e];
+    for (int s = 1; s < split; ++s) t += P[(long)s * mn + e];
+    t *= outscale;
+    if constexpr (YT == Q4_DT_F16) reinterpret_cast<uint16_t*>(Y)[e] = f2h(t);
+    else reinterpret_cast<float*>(Y)[e] = t;
   }
 }
 
@@ -911,7 +944,7 @@ static gemv_multi_fn pick_mv(int R, int U, int mv, int st, int yt) {
   }
 }
 
-typedef void (*gemv_mm_fn)(const uint16_t*, int, const uint8_t*, const void*, float, void*, int, int);
+typedef void (*gemv_mm_fn)(const uint16_t*, int, const uint8_t*, const void*, float, void*, int, int, int, float*);
 template <int T, int U>
 static gemv_mm_fn pick_mm_sy(int st, int yt) {
   if (st == Q4_SCALE_E4M3)
@@ -941,6 +974,22 @@ static int mm_tiles(int NP) {
     if (v == 1 || v == 2 || v == 4) T = v;
   }
   return T;
+}
+// K splits for the small-M GEMV at T = 4 tiles: 1 where NP / 64 row groups
+// already give GEMV_MIN_WGS workgroups, else enough splits to reach it, each
+// split at least GEMV_MM_MIN_SPLIT_BLOCKS blocks (8 steps per wave).
+// Q4MI_GEMV_MM_SPLIT (1..64) overrides the plan for tuning sweeps.
+constexpr int GEMV_MM_MIN_SPLIT_BLOCKS = 32;
+static int mm_split(int NP, int nblk) {
+  const int groups = NP / 64;
+  int s = groups >= GEMV_MIN_WGS ? 1 : (GEMV_MIN_WGS + groups - 1) / groups;
+  s = std::min(s, std::max(1, nblk / GEMV_MM_MIN_SPLIT_BLOCKS));
+  if (const char* e = getenv("Q4MI_GEMV_MM_SPLIT")) {
+    const int v = atoi(e);
+    if (v >= 1 && v <= 64) s = v;
+  }
+  const int span = (nblk + s - 1) / s;
+  return (nblk + span - 1) / span;  // no empty split
 }
 static bool mm_deep() {
   const char* e = getenv("Q4MI_GEMV_MM_DEEP");
@@ -1196,9 +1245,41 @@ int q4_gemv_e4m3s(const void* x, int x_dtype, const uint32_t* wq, const uint8_t*
   return q4_gemv(x, x_dtype, wq, sc8, Q4_SCALE_E4M3, inv, y, y_dtype, N, K, split, ws, ws_size, stream);
 }
 
-int q4_gemv_multi(const void* x, int M, const uint32_t* wq, const void* scales, int scale_fmt, float inv, void* y,
-                  int y_dtype, int N, int K, int exact, void* stream) {
-  clear_error();
+// The MFMA small-M GEMV: unsplit (ws == nullptr) as one launch of T tiles,
+// else T = 4 and `split` K ranges into fp32 partials in ws, then the
+// split-order reduce.
+static int gemv_mm_launch(const void* x, int M, const uint32_t* wq, const void* scales, int scale_fmt,
+                          float outscale, void* y, int y_dtype, int N, int nblk, int split, float* ws,
+                          hipStream_t st) {
+  const int NP = pad_rows(N);
+  if (split <= 1) {
+    const int T = mm_tiles(NP);
+    hipLaunchKernelGGL(pick_mm(T, mm_deep(), scale_fmt, y_dtype), dim3(NP / (16 * T)), dim3(GEMV_THREADS), 0, st,
+                       reinterpret_cast<const uint16_t*>(x), M, reinterpret_cast<const uint8_t*>(wq), scales,
+                       outscale, y, N, nblk, nblk, nullptr);
+    Q4_LAUNCHED("gemv_mm");
+    return Q4_OK;
+  }
+  const int span = (nblk + split - 1) / split;
+  hipLaunchKernelGGL(pick_mm(4, mm_deep(), scale_fmt, y_dtype), dim3(NP / 64, split), dim3(GEMV_THREADS), 0, st,
+                     reinterpret_cast<const uint16_t*>(x), M, reinterpret_cast<const uint8_t*>(wq), scales, outscale,
+                     y, N, nblk, span, ws);
+  Q4_LAUNCHED("gemv_mm split");
+  const long mn = (long)M * N;
+  const size_t ysz = y_dtype == Q4_DT_F16 ? 2 : 4;
+  const bool vec = mn % 4 == 0 && (uintptr_t)y % (4 * ysz) == 0;
+  const long per = vec ? 4 : 1;
+  const dim3 grid((unsigned)((mn + 256 * per - 1) / (256 * per)));
+  typedef void (*reduce_fn)(const float*, void*, long, int, float);
+  reduce_fn fn = y_dtype == Q4_DT_F16 ? (vec ? gemv_mm_reduce_kernel<Q4_DT_F16, true> : gemv_mm_reduce_kernel<Q4_DT_F16, false>)
+                                      : (vec ? gemv_mm_reduce_kernel<Q4_DT_F32, true> : gemv_mm_reduce_kernel<Q4_DT_F32, false>);
+  hipLaunchKernelGGL(fn, grid, dim3(256), 0, st, ws, y, mn, split, outscale);
+  Q4_LAUNCHED("gemv_mm reduce");
+  return Q4_OK;
+}
+
+static int gemv_multi_check(const void* x, int M, const uint32_t* wq, const void* scales, int scale_fmt, void* y,
+                            int y_dtype, int N, int K) {
   Q4_ARG(M >= 1 && M <= Q4_GEMV_MAX_VECTORS, "multi-vector GEMV takes 1..%d vectors (got M=%d)", Q4_GEMV_MAX_VECTORS,
          M);
   Q4_ARG(N > 0 && K > 0 && K % BLK == 0, "bad GEMV shape N=%d K=%d (K must be a positive multiple of 32)", N, K);
@@ -1207,16 +1288,38 @@ int q4_gemv_multi(const void* x, int M, const uint32_t* wq, const void* scales, 
   Q4_ARG(scale_fmt == Q4_SCALE_F16 || scale_fmt == Q4_SCALE_E4M3, "bad scale format %d", scale_fmt);
   Q4_ARG(((uintptr_t)wq & 15) == 0 && ((uintptr_t)x & 15) == 0, "wq and x must be 16-byte aligned");
   Q4_ARG(N <= (1 << 30) && (long)K <= (1L << 24), "GEMV too large");
+  return Q4_OK;
+}
+
+size_t q4_gemv_multi_workspace_bytes(int M, int N, int K) {
+  if (M < 1 || M > Q4_GEMV_MAX_VECTORS || N <= 0 || K <= 0 || K % BLK || N > (1 << 30) || (long)K > (1L << 24))
+    return 0;
+  const int split = mm_split(pad_rows(N), K / BLK);
+  return split > 1 ? (size_t)split * M * N * sizeof(float) : 0;
+}
+
+int q4_gemv_multi_ws(const void* x, int M, const uint32_t* wq, const void* scales, int scale_fmt, float inv, void* y,
+                     int y_dtype, int N, int K, void* ws, size_t ws_size, void* stream) {
+  clear_error();
+  if (const int rc = gemv_multi_check(x, M, wq, scales, scale_fmt, y, y_dtype, N, K)) return rc;
+  Q4_ARG(((uintptr_t)ws & 15) == 0, "workspace must be 16-byte aligned");
+  const int nblk = K / BLK;
+  const float outscale = scale_fmt == Q4_SCALE_E4M3 ? inv * 256.0f : 1.0f;
+  const size_t need = q4_gemv_multi_workspace_bytes(M, N, K);
+  const bool split = need && ws && ws_size >= need;
+  return gemv_mm_launch(x, M, wq, scales, scale_fmt, outscale, y, y_dtype, N, nblk,
+                        split ? mm_split(pad_rows(N), nblk) : 1, split ? reinterpret_cast<float*>(ws) : nullptr,
+                        as_stream(stream));
+}
+
+int q4_gemv_multi(const void* x, int M, const uint32_t* wq, const void* scales, int scale_fmt, float inv, void* y,
+                  int y_dtype, int N, int K, int exact, void* stream) {
+  clear_error();
+  if (const int rc = gemv_multi_check(x, M, wq, scales, scale_fmt, y, y_dtype, N, K)) return rc;
   const int NP = pad_rows(N), nblk = K / BLK;
   const float outscale = scale_fmt == Q4_SCALE_E4M3 ? inv * 256.0f : 1.0f;
-  if (!exact) {
-    const int T = mm_tiles(NP);
-    hipLaunchKernelGGL(pick_mm(T, mm_deep(), scale_fmt, y_dtype), dim3(NP / (16 * T)), dim3(GEMV_THREADS), 0,
-                       as_stream(stream), reinterpret_cast<const uint16_t*>(x), M,
-                       reinterpret_cast<const uint8_t*>(wq), scales, outscale, y, N, nblk);
-    Q4_LAUNCHED("gemv_mm");
-    return Q4_OK;
-  }
+  if (!exact)
+    return gemv_mm_launch(x, M, wq, scales, scale_fmt, outscale, y, y_dtype, N, nblk, 1, nullptr, as_stream(stream));
   const int R = rows_per_group(NP), groups = NP / R;
   const int U = units_in_flight(nblk, R, groups);
   const size_t ysz = y_dtype == Q4_DT_F16 ? 2 : 4;

@@ -206,14 +206,24 @@ def gemv(x: torch.Tensor, wq: torch.Tensor, scales: torch.Tensor, N: int, K: int
 GEMV_MAX_VECTORS = 16
 
 
+def gemv_multi_workspace_bytes(M: int, N: int, K: int) -> int:
+    """Bytes of the K-split workspace of the MFMA small-M GEMV (0: unsplit)."""
+    return int(lib().q4_gemv_multi_workspace_bytes(M, N, K))
+
+
 def gemv_multi(x: torch.Tensor, wq: torch.Tensor, scales: torch.Tensor, N: int, K: int, *,
                scale_fmt: int = SCALE_F16, inv: float = 1.0, y: torch.Tensor | None = None,
-               y_dtype=None, exact: bool = False) -> torch.Tensor:
+               y_dtype=None, exact: bool = False, ws: torch.Tensor | None = None,
+               ksplit: bool = True) -> torch.Tensor:
     """Y[m] = GEMV of x[m] for the M fp16 rows of ``x`` [M][K] (M <= 16),
     reading the weights once. ``exact``: every row bit-identical to
     :func:`gemv` of that row when :func:`gemv` runs unsplit (VALU path, one
-    weight stream per 2-8 vectors); otherwise one MFMA launch for all rows,
-    equal to :func:`gemv` to fp32 rounding. Returns Y [M][N]."""
+    weight stream per 2-8 vectors); otherwise the MFMA path, equal to
+    :func:`gemv` to fp32 rounding: one launch, or for matrices of fewer than
+    15360 rows a K-split launch into fp32 partials plus their reduce — pass
+    ``ws`` (at least :func:`gemv_multi_workspace_bytes` bytes) or one is
+    allocated here; capture code must pass its own. ``ksplit=False`` runs
+    the MFMA path unsplit whatever the shape. Returns Y [M][N]."""
     if x.dtype != torch.float16:
         raise ValueError("multi-vector GEMV takes fp16 activations")
     if x.dim() != 2 or x.shape[1] != K or not x.is_contiguous():
@@ -226,8 +236,22 @@ def gemv_multi(x: torch.Tensor, wq: torch.Tensor, scales: torch.Tensor, N: int, 
     elif y.dim() != 2 or tuple(y.shape) != (M, N) or not y.is_contiguous():
         raise ValueError(f"y must be a contiguous [{M}][{N}] tensor")
     _check_int4(wq, scales, N, K, 1 if scale_fmt == SCALE_E4M3 else 2)
-    call("q4_gemv_multi", _p(x), M, _p(wq), _p(scales), scale_fmt, C.c_float(inv), _p(y), _dt(y), N, K,
-         int(bool(exact)), _stream())
+    if exact:
+        call("q4_gemv_multi", _p(x), M, _p(wq), _p(scales), scale_fmt, C.c_float(inv), _p(y), _dt(y), N, K, 1,
+             _stream())
+        return y
+    need = gemv_multi_workspace_bytes(M, N, K) if ksplit else 0
+    if not ksplit:
+        ws = None
+    if need and ws is None:
+        if _CAPTURING[0]:
+            raise RuntimeError("a K-split small-M GEMV inside a graph capture needs a workspace allocated before "
+                               "the capture (pass ws=...)")
+        ws = torch.empty(need, dtype=torch.uint8, device=x.device)
+    if ws is not None:
+        _need(ws, need, "small-M GEMV split-K workspace")
+    call("q4_gemv_multi_ws", _p(x), M, _p(wq), _p(scales), scale_fmt, C.c_float(inv), _p(y), _dt(y), N, K,
+         _p(ws), _nbytes(ws) if ws is not None else 0, _stream())
     return y
 
 

@@ -221,6 +221,21 @@ int q4_gemv_batch_normadd(const float* a, const float* w, const float* h, float*
 int q4_gemv_multi(const void* x, int M, const uint32_t* wq,
                   const void* scales, int scale_fmt, float inv, void* y,
                   int y_dtype, int N, int K, int exact, void* stream);
+/* The MFMA path (exact = 0) with a caller-owned workspace for matrices
+ * with fewer than 15360 rows (tall-K shapes such as the down projection):
+ * K is split across workgroups so each reads 64 rows' x slices once for
+ * four 16-row tiles, fp32 partials [split][M][N] go to ws (16-byte
+ * aligned) and a second kernel sums them in split order, times the scale
+ * factor. Rows agree with q4_gemv to fp32 rounding, as the unsplit path's
+ * do. ws may be NULL or smaller than q4_gemv_multi_workspace_bytes(M, N,
+ * K) (0 where no split is planned): the call then runs unsplit, exactly
+ * like q4_gemv_multi(..., exact = 0, ...). Same row as q4_gemv_multi:
+ * JOURNEY.md:666. */
+size_t q4_gemv_multi_workspace_bytes(int M, int N, int K);
+int q4_gemv_multi_ws(const void* x, int M, const uint32_t* wq,
+                     const void* scales, int scale_fmt, float inv, void* y,
+                     int y_dtype, int N, int K, void* ws, size_t ws_size,
+                     void* stream);
 
 /* ---- prefill GEMMs -------------------------------------------------------
  * W4A16: Y f16 [M][N] = X f16 [M][K] @ f16((q-8)*s)^T, fp32 accumulate; X

@@ -84,6 +84,17 @@ def test_argument_errors_without_gpu(g4):
     assert st == g4._lib.Q4_ERR_ARG and "LDS" in _err(g4)
     st = lib.q4_gemv_multi(p, 2, null, p, 0, C.c_float(1.0), p, 1, 256, 256, 0, null)
     assert st == g4._lib.Q4_ERR_ARG and "null" in _err(g4)
+    # its K-split variant: the same checks, a misaligned workspace, and the plan's workspace size
+    for M in (0, 17):
+        st = lib.q4_gemv_multi_ws(p, M, p, p, 0, C.c_float(1.0), p, 1, 256, 256, p, 1 << 20, null)
+        assert st == g4._lib.Q4_ERR_ARG and f"M={M}" in _err(g4)
+    st = lib.q4_gemv_multi_ws(p, 2, p, p, 0, C.c_float(1.0), p, 1, 3840, 15360, C.c_void_p((1 << 20) + 8), 1 << 24,
+                              null)
+    assert st == g4._lib.Q4_ERR_ARG and "16-byte" in _err(g4)
+    # 3840 rows: 60 groups of 64 rows, split 4 (240 workgroups); 15360 rows fill the grid unsplit
+    assert lib.q4_gemv_multi_workspace_bytes(16, 3840, 15360) == 4 * 16 * 3840 * 4
+    assert lib.q4_gemv_multi_workspace_bytes(16, 15360, 3840) == 0
+    assert lib.q4_gemv_multi_workspace_bytes(17, 3840, 15360) == 0
 
 
 def test_prefill_op_argument_errors_without_gpu(g4):

@@ -159,3 +159,51 @@ def test_gemv_multi_mfma_zero_and_extreme_codes(gpu):
         else:
             for m in range(M):
                 assert O.normwise_rel_err(to_np(Y[m]), ref[m]) <= TOL[torch.float32], (code, m)
+
+
+@pytest.mark.parametrize("split", ["1", "2", "3", "5", "8"])
+def test_gemv_multi_ksplit_variants(gpu, split, monkeypatch):
+    """K split across workgroups (T = 4 tiles, fp32 partials, split-order
+    reduce) at forced split counts, with block counts that leave the last
+    split shorter (203 blocks) and M * N not a multiple of 4 (the reduce's
+    one-output-per-thread path), fp16 and fp32 y, against the oracle and
+    against the unsplit launch."""
+    monkeypatch.setenv("Q4MI_GEMV_MM_SPLIT", split)
+    for N, nblk, M in [(3840, 203, 16), (1001, 96, 3), (4096, 120, 5)]:
+        K = 32 * nblk
+        rng = np.random.default_rng(N + nblk + int(split))
+        q, s = synth_int4(rng, N, K)
+        X = _x(rng, M, K)
+        wq, sc = upload_int4(q, s)
+        Xd = torch.from_numpy(X).cuda()
+        ref = O.gemm_w4a16_ref(X, q, s)
+        need = gpu.gemv_multi_workspace_bytes(M, N, K)
+        assert need == (int(split) * M * N * 4 if split != "1" else 0)
+        for ydt in (torch.float16, torch.float32):
+            Y = gpu.gemv_multi(Xd, wq, sc, N, K, y_dtype=ydt)
+            monkeypatch.setenv("Q4MI_GEMV_MM_SPLIT", "1")
+            Y1 = gpu.gemv_multi(Xd, wq, sc, N, K, y_dtype=ydt)
+            monkeypatch.setenv("Q4MI_GEMV_MM_SPLIT", split)
+            Yh = to_np(Y).astype(np.float32)
+            for m in range(M):
+                assert O.normwise_rel_err(Yh[m], ref[m]) <= TOL[ydt], (N, nblk, m, ydt)
+                if ydt == torch.float32:
+                    assert O.normwise_rel_err(Yh[m], to_np(Y1[m])) <= TOL[ydt], (N, nblk, m)
+
+
+def test_gemv_multi_ksplit_down_shape_reuses_workspace(gpu):
+    """The down shape (3840 x 15360) at M = 16 and then M = 4 through one
+    workspace sized for M = 16: the second call's partials are all written
+    by the second call (the reduce reads only [split][4][N])."""
+    N, K = 3840, 15360
+    rng = np.random.default_rng(77)
+    q, s = synth_int4(rng, N, K)
+    wq, sc = upload_int4(q, s)
+    ws = torch.empty(gpu.gemv_multi_workspace_bytes(16, N, K), dtype=torch.uint8, device="cuda")
+    assert ws.numel() > 0
+    for M in (16, 4):
+        X = _x(rng, M, K)
+        Y = gpu.gemv_multi(torch.from_numpy(X).cuda(), wq, sc, N, K, y_dtype=torch.float32, ws=ws)
+        ref = O.gemm_w4a16_ref(X, q, s)
+        for m in range(M):
+            assert O.normwise_rel_err(to_np(Y[m]), ref[m]) <= TOL[torch.float32], (M, m)
