@@ -220,7 +220,8 @@ def gemv_multi(x: torch.Tensor, wq: torch.Tensor, scales: torch.Tensor, N: int, 
     :func:`gemv` of that row when :func:`gemv` runs unsplit (VALU path, one
     weight stream per 2-8 vectors); otherwise the MFMA path, equal to
     :func:`gemv` to fp32 rounding: one launch, or for matrices of fewer than
-    15360 rows a K-split launch into fp32 partials plus their reduce — pass
+    15360 rows and K >= 2048 a K-split launch into fp32 partials plus their
+    reduce — pass
     ``ws`` (at least :func:`gemv_multi_workspace_bytes` bytes) or one is
     allocated here; capture code must pass its own. ``ksplit=False`` runs
     the MFMA path unsplit whatever the shape. Returns Y [M][N]."""

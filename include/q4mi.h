@@ -222,10 +222,12 @@ int q4_gemv_multi(const void* x, int M, const uint32_t* wq,
                   const void* scales, int scale_fmt, float inv, void* y,
                   int y_dtype, int N, int K, int exact, void* stream);
 /* The MFMA path (exact = 0) with a caller-owned workspace for matrices
- * with fewer than 15360 rows (tall-K shapes such as the down projection):
- * K is split across workgroups so each reads 64 rows' x slices once for
- * four 16-row tiles, fp32 partials [split][M][N] go to ws (16-byte
- * aligned) and a second kernel sums them in split order, times the scale
+ * with fewer than 15360 rows and K >= 2048 (tall-K shapes such as the down
+ * projection): K is split across workgroups into ceil(240 / (rows / 64))
+ * ranges (fewer where a range would hold under 32 blocks), so each
+ * workgroup reads 64 rows' x slices once for four 16-row tiles; fp32
+ * partials [split][M][N] go to ws (16-byte aligned) and a second kernel
+ * sums them in split order, times the scale
  * factor. Rows agree with q4_gemv to fp32 rounding, as the unsplit path's
  * do. ws may be NULL or smaller than q4_gemv_multi_workspace_bytes(M, N,
  * K) (0 where no split is planned): the call then runs unsplit, exactly
