@@ -1271,8 +1271,9 @@ static int gemv_mm_launch(const void* x, int M, const uint32_t* wq, const void* 
   const long per = vec ? 4 : 1;
   const dim3 grid((unsigned)((mn + 256 * per - 1) / (256 * per)));
   typedef void (*reduce_fn)(const float*, void*, long, int, float);
-  reduce_fn fn = y_dtype == Q4_DT_F16 ? (vec ? gemv_mm_reduce_kernel<Q4_DT_F16, true> : gemv_mm_reduce_kernel<Q4_DT_F16, false>)
-                                      : (vec ? gemv_mm_reduce_kernel<Q4_DT_F32, true> : gemv_mm_reduce_kernel<Q4_DT_F32, false>);
+  const reduce_fn f16v[2] = {gemv_mm_reduce_kernel<Q4_DT_F16, false>, gemv_mm_reduce_kernel<Q4_DT_F16, true>};
+  const reduce_fn f32v[2] = {gemv_mm_reduce_kernel<Q4_DT_F32, false>, gemv_mm_reduce_kernel<Q4_DT_F32, true>};
+  const reduce_fn fn = y_dtype == Q4_DT_F16 ? f16v[vec] : f32v[vec];
   hipLaunchKernelGGL(fn, grid, dim3(256), 0, st, ws, y, mn, split, outscale);
   Q4_LAUNCHED("gemv_mm reduce");
   return Q4_OK;
