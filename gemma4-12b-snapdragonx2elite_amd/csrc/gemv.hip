@@ -1034,14 +1034,19 @@ static int units_in_flight(int nb, int R, long wgs) {
 }
 
 // Row groups per workgroup: 2 (a 512-thread workgroup, see gemv_kernel) for
-// unsplit grids of an even number of groups that still give one workgroup
-// per CU after pairing (>= 2 GEMV_MIN_WGS groups) and whose two staging
-// areas fit 64 KB of LDS, else 1. Q4MI_GEMV_PAIR=0
-// forces 1, =1 pairs every unsplit even grid (tests and tuning sweeps).
-static int pair_groups(int groups, int split, size_t lds) {
+// the batched launch without a fused norm (`paired`) when its grid is
+// unsplit, has an even number of groups that still give one workgroup per
+// CU after pairing (>= 2 GEMV_MIN_WGS groups) and its two staging areas fit
+// 64 KB of LDS; else 1. Measured on MI355X in the graph of a decode token:
+// pairing the q/k/v batch saves 0.14 us per launch (5.80 -> 5.66 us), while
+// the single and fused-norm launches run faster unpaired between their
+// neighbours (the 48-layer GEMV set 1.611 -> 1.595 ms, the fused token
+// 2.362 -> 2.293 ms). Q4MI_GEMV_PAIR=0 forces 1, =1 pairs every unsplit
+// even grid (tests and tuning sweeps).
+static int pair_groups(int groups, int split, size_t lds, bool paired) {
   const bool can = split == 1 && groups % 2 == 0 && 2 * lds <= 64 * 1024;
   if (const char* e = getenv("Q4MI_GEMV_PAIR")) return atoi(e) != 0 && can ? 2 : 1;
-  return can && groups >= 2 * GEMV_MIN_WGS ? 2 : 1;
+  return paired && can && groups >= 2 * GEMV_MIN_WGS ? 2 : 1;
 }
 
 // LDS bytes of x per block, and of the staging area for nb blocks and R
@@ -1203,7 +1208,7 @@ static int gemv_launch(const void* x, int x_dtype, const uint32_t* wq, const voi
   uint32_t* cnt = pl.ws ? reinterpret_cast<uint32_t*>(ws) : nullptr;
   float* part = pl.ws ? reinterpret_cast<float*>(reinterpret_cast<char*>(ws) + GEMV_TICKET_BYTES) : nullptr;
   const float outscale = scale_fmt == Q4_SCALE_E4M3 ? inv * 256.0f : 1.0f;
-  const int hv = pair_groups(groups, pl.split, pl.lds);
+  const int hv = pair_groups(groups, pl.split, pl.lds, false);
   int gq = 0, gr = 0;
   group_split(N, groups, gated, gq, gr);
   if (nx) {
@@ -1409,7 +1414,7 @@ static int gemv_batch_launch(const void* x, int x_dtype, int K, int scale_fmt, i
   }
   const int U = units_in_flight(nblk, R, groups);
   const size_t lds = x_stage_lds(nblk, x_dtype, R);
-  const int hv = pair_groups(groups, 1, lds);
+  const int hv = pair_groups(groups, 1, lds, nx == nullptr);
   if (nx) {
     hipLaunchKernelGGL(pick_nx(R, U, scale_fmt, y_dtype).many, dim3(groups / hv), dim3(GEMV_THREADS * hv), lds * hv,
                        as_stream(stream), *nx, nblk, segs, hv);
