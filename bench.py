@@ -1079,6 +1079,17 @@ def main():
     gu = dec["per_shape"]["gate_up"]
     gu_bytes = gu["bytes_per_launch"]
     achieved = gu_bytes / (gu["us_per_launch"] * 1e-6) / 1e9
+    roof = {"bound": "hbm", "kernel": "gemv_kernel gate_up 30720x3840 (f16 x, f16 scales, f16 y)",
+            "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+            "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": committed_traffic("gate_up"),
+            "bytes_per_launch": gu_bytes, "avg_launch_us": gu["us_per_launch"]}
+    if ceil:
+        # the token as dependent launches that each read their bytes once at the probe's best rate
+        sr = {k: v["us_per_launch"] for k, v in ceil["stream_read"].items()}
+        ach = (LAYERS * (sr["qkv_8192x3840"] + sr["o_3840x4096"] + sr["gate_up_30720x3840"] + sr["c1_15360x3840"])
+               + sr["lm_head_262144x3840"]) / 1e3
+        roof["achievable_ms_per_step"] = round(ach, 4)
+        roof["frac_of_achievable"] = round(ach / ms, 4)
     line = {
         "metric": METRIC,
         "value": round(dec["GBps"], 1),
@@ -1092,37 +1103,31 @@ def main():
         "vs_baseline": None,
         "dtype": "i4xf16->f32",
         "data": "synthetic",
-        "config": {
-            "workload": "decode-step int4 GEMV set: 48 distinct layers {q 4096x3840, k 2048x3840, v 2048x3840, "
-                        "o 3840x4096, gate_up 30720x3840, down 3840x15360} + lm_head 262144x3840, block-32 fp16 "
-                        "scales, fp16 x/y, one hipGraph replay per token (q/k/v of a layer read one x: one "
-                        "batched launch)",
-            "bytes_per_step": dec["bytes_per_step"],
-            "kernels_per_step": dec["launches"],
-            "frac_of_hbm_peak": round(dec["GBps"] / HBM_PEAK_GBS, 4),
-            "per_shape": dec["per_shape"],
-            "ms_per_step_percentiles": dec["ms_per_step_percentiles"],
-            "single_shape_gemv": single,
-            "full_token_step": tok,
-            "small_m_gemv": small,
-            "prefill_chunk": pre,
-            "ceilings": ceil,
-        },
-        "roofline": {
-            "bound": "hbm",
-            "kernel": "gemv_kernel<f16 x, f16 scales, f16 y> (gate_up 30720x3840, 64 rows per workgroup)",
-            "achieved": round(achieved, 1),
-            "peak": HBM_PEAK_GBS,
-            "unit": "GB/s",
-            "frac": round(achieved / HBM_PEAK_GBS, 4),
-            "traffic": committed_traffic("gate_up"),
-            "bytes_per_launch": gu_bytes,
-            "avg_launch_us": gu["us_per_launch"],
-        },
-        "cpu_baseline": cpu,
-        "w8a8": w8,
-        "w4a16": w4,
+        "config": {"workload": "decode GEMV set: 48 layers {q,k,v,o,gate_up,down} + lm_head 262144x3840, "
+                               "int4 block-32 fp16 scales, one hipGraph per token",
+                   "bytes_per_step": dec["bytes_per_step"], "kernels_per_step": dec["launches"],
+                   "frac_of_hbm_peak": round(dec["GBps"] / HBM_PEAK_GBS, 4)},
+        "roofline": roof,
+        "cpu_baseline": None if cpu is None else {k: cpu[k] for k in ("value", "unit", "cores", "kind", "sample")},
+        "per_shape_us": {k: v["us_per_launch"] for k, v in dec["per_shape"].items()},
+        "c1_us": single["c1_15360x3840_f16_scales"]["us_per_launch"],
+        "c3_us": single["c3_15360x3840_e4m3_scales"]["us_per_launch"],
+        "lm_head_us": single["lm_head_262144x3840_f16_scales"]["us_per_launch"],
+        "token_ms": None if tok is None else tok["fused"]["ms_per_token"],
+        "prefill_chunk_ms": pre["ms_per_chunk"],
     }
+    if w8 is not None:
+        line["w8a8_us"] = w8["us"]
+        line["w8a8_frac_of_int8_peak"] = w8["frac_of_int8_peak"]
+        line["w8a8_shader_clock_GHz"] = w8["stamped"]["shader_clock_GHz_median"]
+        if ceil:
+            mc = ceil["mfma"]["int8_32x32x32_1wave_per_simd"]["random_operands_sustained_50"]["T_per_s"]
+            line["w8a8_frac_of_mfma_ceiling"] = round(w8["TOPS"] / mc, 4)
+    if w4 is not None:
+        line["w4a16_us"] = {k: v["us"] for k, v in w4.items()}
+    if cpu is not None:
+        line["cpu_w8a8_TOPS"] = cpu["w8a8"]["TOPS"]
+        line["cpu_w4a16_TFLOPS"] = cpu["w4a16"]["TFLOPS"]
     print(json.dumps(line), flush=True)
 
 

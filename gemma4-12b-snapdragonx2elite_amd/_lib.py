@@ -18,6 +18,9 @@ SCALE_F16, SCALE_E4M3 = 0, 1
 OP_GEMV = 0
 OP_W4A16 = 1
 GEMV_MAX_BATCH = 8
+# plan overrides of q4_tune_set (include/q4mi.h Q4_TUNE_*), by name
+TUNE_KNOBS = {"gemv_rows": 0, "gemv_units": 1, "gemv_pair": 2, "gemv_bal": 3, "gemv_mm_tiles": 4,
+              "gemv_mm_split": 5, "gemv_mm_deep": 6, "w4a16_split": 7, "w4a16_kg": 8}
 
 _vp, _i, _f, _sz = C.c_void_p, C.c_int, C.c_float, C.c_size_t
 
@@ -26,6 +29,9 @@ SIGNATURES = {
     "q4_version": (C.c_char_p, []),
     "q4_last_error": (C.c_char_p, []),
     "q4_dev_bytes": (_i, [_i, _i, C.POINTER(_sz), C.POINTER(_sz)]),
+    "q4_tune_set": (_i, [_i, _i]),
+    "q4_tune_get": (_i, [_i]),
+    "q4_tune_reset": (None, []),
     "q4_quantize": (_i, [_vp, _i, _i, _vp, _vp, _vp, _vp]),
     "q4_scales_e4m3": (_i, [_vp, _i, _i, _vp, _vp, _vp, _vp]),
     "q4_w8_fold": (_i, [_vp, _vp, _i, _i, _vp, _vp, _vp, _vp]),

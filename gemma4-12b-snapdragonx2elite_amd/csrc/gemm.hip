@@ -259,23 +259,28 @@ __device__ inline void epilogue(const GemmArgs& g, uint32_t* strip, const acc_t 
 // no int32 output: Y = f16((f32(C) * sa) * sw), the same arithmetic as
 // epilogue<0> without its bounds and output-kind branches. Four 64-row
 // chunks go through the wave's LDS strip; a chunk's scales are loaded
-// before its strip is filled.
+// before its strip is filled. Each lane stores 8 columns (16 bytes) of a
+// row, 8 rows per instruction, with nontemporal stores: Y is not read again
+// by this kernel, and lines left out of L2 shorten the kernel's end (its
+// release writes back less). Measured at M=2048, N=15360, K=3840 against
+// 8-byte stores: the epilogue 7.1 -> 6.5 us per tile and the gap before the
+// next launch 2.7 -> 1.1 us. Needs N % 8 == 0 (16-byte aligned rows).
 template <class acc_t>
 __device__ inline void epilogue_w8_full(const GemmArgs& g, uint32_t* strip, const acc_t (&acc)[8][2], int m0, int nw) {
   const int lane = threadIdx.x & 63;
   const int col = lane & 31, rh = (lane >> 5) * 4;
-  const int rrow = lane >> 4, rcol = (lane & 15) * 4;
+  const int rrow = lane >> 3, rcol = (lane & 7) * 8;
   const int N = g.N;
-  float swv[4];
+  float swv[8];
 #pragma unroll
-  for (int e = 0; e < 4; ++e)
+  for (int e = 0; e < 8; ++e)
     swv[e] = g.sw_f16 ? h2f(reinterpret_cast<const uint16_t*>(g.sw)[nw + rcol + e])
                       : reinterpret_cast<const float*>(g.sw)[nw + rcol + e];
 #pragma unroll
   for (int c = 0; c < 4; ++c) {
-    float sav[16];  // this chunk's row scales, loaded before the strip is filled
+    float sav[8];  // this chunk's row scales, loaded before the strip is filled
 #pragma unroll
-    for (int it = 0; it < 16; ++it) sav[it] = g.sa[m0 + 64 * c + 4 * it + rrow];
+    for (int it = 0; it < 8; ++it) sav[it] = g.sa[m0 + 64 * c + 8 * it + rrow];
 #pragma unroll
     for (int h = 0; h < 2; ++h)
 #pragma unroll
@@ -283,16 +288,19 @@ __device__ inline void epilogue_w8_full(const GemmArgs& g, uint32_t* strip, cons
     lgkm0();
     __builtin_amdgcn_wave_barrier();
 #pragma unroll
-    for (int it = 0; it < 16; ++it) {
-      const int row = 4 * it + rrow;
-      const v4u q = *reinterpret_cast<const v4u*>(strip + row * EST + rcol);
-      uint32_t qv[4];
-      __builtin_memcpy(qv, &q, sizeof(qv));
-      uint16_t hv[4];
+    for (int it = 0; it < 8; ++it) {
+      const int row = 8 * it + rrow;
+      const v4u q0 = *reinterpret_cast<const v4u*>(strip + row * EST + rcol);
+      const v4u q1 = *reinterpret_cast<const v4u*>(strip + row * EST + rcol + 4);
+      // elements through a plain array (see epilogue<>)
+      uint32_t qv[8];
+      __builtin_memcpy(qv, &q0, 16);
+      __builtin_memcpy(qv + 4, &q1, 16);
+      uint32_t hv[8];
 #pragma unroll
-      for (int e = 0; e < 4; ++e) hv[e] = f2h_after_f32(__fmul_rn(__fmul_rn((float)(int)qv[e], sav[it]), swv[e]));
-      *reinterpret_cast<ushort4*>(g.Y + (long)(m0 + 64 * c + row) * N + nw + rcol) =
-          make_ushort4(hv[0], hv[1], hv[2], hv[3]);
+      for (int e = 0; e < 8; ++e) hv[e] = f2h_after_f32(__fmul_rn(__fmul_rn((float)(int)qv[e], sav[it]), swv[e]));
+      const v4u o = {hv[0] | (hv[1] << 16), hv[2] | (hv[3] << 16), hv[4] | (hv[5] << 16), hv[6] | (hv[7] << 16)};
+      __builtin_nontemporal_store(o, reinterpret_cast<v4u*>(g.Y + (long)(m0 + 64 * c + row) * N + nw + rcol));
     }
     __builtin_amdgcn_wave_barrier();  // strip reads done before the next chunk overwrites it
   }
@@ -698,8 +706,8 @@ __global__ void __launch_bounds__(256) w8p_kernel(const GemmArgs g) {
 
   uint32_t* strip = reinterpret_cast<uint32_t*>(ldsA) + wave * (64 * EST);
   if constexpr (BM == 256) {
-    // a tile wholly inside Y (N % 4 == 0 keeps the 8-byte stores aligned), Y only
-    if (m0 + BM <= M && n0 + 256 <= N && !g.C && g.Y && (N & 3) == 0) {
+    // a tile wholly inside Y (N % 8 == 0 keeps the 16-byte stores aligned), Y only
+    if (m0 + BM <= M && n0 + 256 <= N && !g.C && g.Y && (N & 7) == 0) {
       epilogue_w8_full(g, strip, acc, m0, n0 + 64 * wave);
       stamp_end();
       return;
@@ -737,11 +745,12 @@ __global__ void __launch_bounds__(256) w8p_kernel(const GemmArgs g) {
 // wave per SIMD is bound by its own instruction issue (dequant, A reads,
 // addresses between the MFMAs), and a second wave issues while the first
 // one's MFMAs run. Both groups run the same number of k-steps (barriers stay
-// paired); the second group's surplus step, for an odd count, reads zero
-// scales (its A chunks, those of the group's last k-step again, add nothing
-// unless they hold Inf or NaN, as with the absent block of an odd block
-// count). Group 1 then hands its accumulators to group 0 through LDS, and
-// group 0 adds them (acc0 + acc1) and runs the epilogue.
+// paired): for an odd count the second group runs one k-step fewer and
+// then joins the first group's last barrier without any MFMA, so no
+// operand is multiplied that a one-group launch would not multiply (a
+// surplus step on zero scales would turn an Inf in X into NaN). Group 1
+// then hands its accumulators to group 0 through LDS, and group 0 adds them
+// (acc0 + acc1) and runs the epilogue.
 template <int BM, bool TAIL, int KG = 1>
 __global__ void __launch_bounds__(256 * KG) w4p_kernel(const GemmArgs g, int split) {
   constexpr int S = 4, FM = BM / 32, FN = 2;
@@ -766,8 +775,9 @@ __global__ void __launch_bounds__(256 * KG) w4p_kernel(const GemmArgs g, int spl
   const int nk_all = (nblk + 1) / 2;
   const int kz = blockIdx.y;
   const int k_wg = (int)((long)kz * nk_all / split), nk_wg = (int)((long)(kz + 1) * nk_all / split) - k_wg;
-  // this group's k-steps: [k_lo, k_lo + nk); both groups run nit steps (the
-  // entry point gives KG = 2 workgroups at least 2 k-steps, so nk >= 1)
+  // this group's k-steps: [k_lo, k_lo + nk); group 0 runs nit = nk steps,
+  // group 1 nk = nit or nit - 1 (the entry point gives KG = 2 workgroups at
+  // least 2 k-steps, so nk >= 1)
   const int nit = KG > 1 ? (nk_wg + 1) / 2 : nk_wg;
   const int k_lo = k_wg + grp * nit, nk = grp ? nk_wg - nit : nit;
   const int h = lane >> 5;
@@ -858,12 +868,11 @@ __global__ void __launch_bounds__(256 * KG) w4p_kernel(const GemmArgs g, int spl
 
   // Word P of the B fragment of n-tile j for k-slice q = 2bb + s of the
   // k-step whose half-units sit in register set SET; zero scale for the
-  // absent second block of an odd block count (half) and for both blocks of
-  // a surplus step (dead)
-  auto bpair = [&](auto setc, int j, int q, bool half, bool dead, auto pc) -> int {
+  // absent second block of an odd block count (half)
+  auto bpair = [&](auto setc, int j, int q, bool half, auto pc) -> int {
     constexpr int set = decltype(setc)::value, P = decltype(pc)::value;
     const int bb = q >> 1;
-    const uint16_t sbits = ((bb == 1 && half) || dead) ? (uint16_t)0 : (uint16_t)rs[set][j][bb];
+    const uint16_t sbits = (bb == 1 && half) ? (uint16_t)0 : (uint16_t)rs[set][j][bb];
     const _Float16 sc = __builtin_bit_cast(_Float16, sbits);
     const v2h sv = {sc, sc};
     return (int)dequant_pair_f16<P>((q & 1) ? ru[set][j][bb].y : ru[set][j][bb].x, sv, mlo, mhi);
@@ -871,7 +880,7 @@ __global__ void __launch_bounds__(256 * KG) w4p_kernel(const GemmArgs g, int spl
   v4i fb[2][FN];  // [slice parity][n-tile]: slice q's fragments, built during slice q - 1
 #pragma unroll
   for (int j = 0; j < FN; ++j)
-    static_for<0, 4>([&](auto pc) { fb[0][j][decltype(pc)::value] = bpair(I0{}, j, 0, 2 * k_lo + 1 >= nblk, false, pc); });
+    static_for<0, 4>([&](auto pc) { fb[0][j][decltype(pc)::value] = bpair(I0{}, j, 0, 2 * k_lo + 1 >= nblk, pc); });
 
   static_assert(NB == 8 && NB + NA <= 16 && FM % 4 == 0, "one VMEM operation per group");
   int kt = 0;
@@ -880,7 +889,6 @@ __global__ void __launch_bounds__(256 * KG) w4p_kernel(const GemmArgs g, int spl
     const int st = kt & 3, stn = (kt + 1) & 3;
     const int kl = min(kt + 2, nk - 1);
     const bool half = 2 * (k_lo + kt) + 1 >= nblk, half_n = 2 * (k_lo + kt + 1) + 1 >= nblk;
-    const bool dead = KG > 1 && kt >= nk, dead_n = KG > 1 && kt + 1 >= nk;
     static_for<0, 4>([&](auto qc) {
       constexpr int q = decltype(qc)::value, cb = q & 1, nbuf = cb ^ 1;
       if constexpr (q == 2) {
@@ -903,8 +911,8 @@ __global__ void __launch_bounds__(256 * KG) w4p_kernel(const GemmArgs g, int spl
         // run: the dequant spreads evenly over the slice's MFMAs
 #pragma unroll
         for (int j = 0; j < FN; ++j) {
-          if constexpr (q < 3) fb[nbuf][j][g] = bpair(setc, j, q + 1, half, dead, gc);
-          else fb[nbuf][j][g] = bpair(setnc, j, 0, half_n, dead_n, gc);
+          if constexpr (q < 3) fb[nbuf][j][g] = bpair(setc, j, q + 1, half, gc);
+          else fb[nbuf][j][g] = bpair(setnc, j, 0, half_n, gc);
         }
 #pragma unroll
         for (int ii = i0; ii < i0 + FM / 4; ++ii)
@@ -923,7 +931,7 @@ __global__ void __launch_bounds__(256 * KG) w4p_kernel(const GemmArgs g, int spl
       });
     });
   };
-  for (; kt + 2 < nit; kt += 3) {
+  for (; kt + 2 < nk; kt += 3) {
     kstep(I0{}, I1{}, I2{});
     ++kt;
     kstep(I1{}, I2{}, I0{});
@@ -931,10 +939,13 @@ __global__ void __launch_bounds__(256 * KG) w4p_kernel(const GemmArgs g, int spl
     kstep(I2{}, I0{}, I1{});
     kt -= 2;
   }
-  if (kt < nit) {
+  if (kt < nk) {
     kstep(I0{}, I1{}, I2{});
     ++kt;
-    if (kt < nit) kstep(I1{}, I2{}, I0{});
+    if (kt < nk) kstep(I1{}, I2{}, I0{});
+  }
+  if constexpr (KG > 1) {
+    if (nk < nit) __syncthreads();  // group 1 of an odd count: group 0's last k-step barrier
   }
   vmwait<0>();
 #pragma unroll
@@ -1320,10 +1331,8 @@ static int w4a16_split(int M, int N, int K) {
   const int t = tiles(M, N, pick_bm(M, N));
   const int nk = (K / 32 + 1) / 2;  // k-steps of 64
   int s = min(ceil_div(240, t), max(1, nk / 8));
-  if (const char* e = getenv("Q4MI_W4A16_SPLIT")) {  // tuning sweeps
-    const int v = atoi(e);
-    if (v >= 1 && v <= nk) s = v;
-  }
+  const int v = tune_value(Q4_TUNE_W4A16_SPLIT);  // tests and tuning sweeps
+  if (v >= 1 && v <= nk) s = v;
   return s;
 }
 
@@ -1335,10 +1344,8 @@ static int w4a16_kgroups(int M, int N, int K, int split) {
   if (pick_bm(M, N) != 128) return 1;
   const int nk = (K / 32 + 1) / 2;
   int kg = nk / split >= 32 ? 2 : 1;
-  if (const char* e = getenv("Q4MI_W4A16_KG")) {  // tuning sweeps and tests: force one or two groups
-    const int v = atoi(e);
-    if (v == 1 || (v == 2 && nk / split >= 2)) kg = v;
-  }
+  const int v = tune_value(Q4_TUNE_W4A16_KG);  // tests and tuning sweeps: force one or two groups
+  if (v == 1 || (v == 2 && nk / split >= 2)) kg = v;
   return kg;
 }
 

@@ -963,38 +963,31 @@ static gemv_mm_fn pick_mm(int T, bool deep, int st, int yt) {
 }
 // Row tiles of 16 per workgroup for NP padded rows: the largest T of 4, 2, 1
 // that still gives GEMV_MIN_WGS workgroups (about one per CU): the x slices
-// each wave reads are shared by T tiles. Q4MI_GEMV_MM_TILES (1/2/4) and
-// Q4MI_GEMV_MM_DEEP (0/1) override the plan for tuning sweeps.
+// each wave reads are shared by T tiles. The Q4_TUNE_GEMV_MM_TILES and
+// Q4_TUNE_GEMV_MM_DEEP overrides (q4_tune_set) replace the plan in tests and sweeps.
 static int mm_tiles(int NP) {
   int T = 1;
   for (int c : {4, 2})
     if (NP / (16 * c) >= GEMV_MIN_WGS) { T = c; break; }
-  if (const char* e = getenv("Q4MI_GEMV_MM_TILES")) {
-    const int v = atoi(e);
-    if (v == 1 || v == 2 || v == 4) T = v;
-  }
+  const int v = tune_value(Q4_TUNE_GEMV_MM_TILES);
+  if (v == 1 || v == 2 || v == 4) T = v;
   return T;
 }
 // K splits for the small-M GEMV at T = 4 tiles: 1 where NP / 64 row groups
 // already give GEMV_MIN_WGS workgroups, else enough splits to reach it, each
 // split at least GEMV_MM_MIN_SPLIT_BLOCKS blocks (8 steps per wave).
-// Q4MI_GEMV_MM_SPLIT (1..64) overrides the plan for tuning sweeps.
+// The Q4_TUNE_GEMV_MM_SPLIT override (q4_tune_set) replaces it in tests and sweeps.
 constexpr int GEMV_MM_MIN_SPLIT_BLOCKS = 32;
 static int mm_split(int NP, int nblk) {
   const int groups = NP / 64;
   int s = groups >= GEMV_MIN_WGS ? 1 : (GEMV_MIN_WGS + groups - 1) / groups;
   s = std::min(s, std::max(1, nblk / GEMV_MM_MIN_SPLIT_BLOCKS));
-  if (const char* e = getenv("Q4MI_GEMV_MM_SPLIT")) {
-    const int v = atoi(e);
-    if (v >= 1 && v <= 64) s = v;
-  }
+  const int v = tune_value(Q4_TUNE_GEMV_MM_SPLIT);
+  if (v >= 1 && v <= 64) s = v;
   const int span = (nblk + s - 1) / s;
   return (nblk + span - 1) / span;  // no empty split
 }
-static bool mm_deep() {
-  const char* e = getenv("Q4MI_GEMV_MM_DEEP");
-  return e ? atoi(e) != 0 : false;
-}
+static bool mm_deep() { return tune_value(Q4_TUNE_GEMV_MM_DEEP) > 0; }
 
 // Rows per workgroup R for NP padded rows: the largest R of 64, 32, 16 that
 // gives GEMV_TARGET_WGS workgroups (about two per CU), else the largest R
@@ -1002,7 +995,7 @@ static bool mm_deep() {
 // the decode shapes: 64 rows for gate_up and lm_head, 32 for 15360 rows, 16
 // for the batched q/k/v and for the 3840-row o and down (240 workgroups with
 // 8 units in flight beat 480 with 4: each workgroup stages the whole x, 30 KB
-// for down). Q4MI_GEMV_ROWS (8/16/32/64) overrides R for tuning sweeps.
+// for down). The Q4_TUNE_GEMV_ROWS override (q4_tune_set) replaces R in tests and sweeps.
 static int rows_per_group(int NP) {
   int R = 0;
   for (int c : {64, 32, 16})
@@ -1011,10 +1004,8 @@ static int rows_per_group(int NP) {
     for (int c : {64, 32, 16, 8})
       if (NP / c >= GEMV_MIN_WGS) { R = c; break; }
   if (R == 0) R = 8;
-  if (const char* e = getenv("Q4MI_GEMV_ROWS")) {
-    int v = atoi(e);
-    if (v == 8 || v == 16 || v == 32 || v == 64) R = v;
-  }
+  const int v = tune_value(Q4_TUNE_GEMV_ROWS);
+  if (v == 8 || v == 16 || v == 32 || v == 64) R = v;
   return R;
 }
 
@@ -1023,12 +1014,10 @@ static int rows_per_group(int NP) {
 // of weights, what HBM needs at ~1.1 us of loaded latency), else 4; 4 when
 // a lane has at most 4 blocks. Measured on MI355X: the best of 4/8/16 for
 // every decode shape follows this rule (more in flight only queues).
-// Q4MI_GEMV_UNITS (4/8) overrides it for tuning sweeps.
+// The Q4_TUNE_GEMV_UNITS override (q4_tune_set) replaces it in tests and sweeps.
 static int units_in_flight(int nb, int R, long wgs) {
-  if (const char* e = getenv("Q4MI_GEMV_UNITS")) {
-    int v = atoi(e);
-    if (v == 4 || v == 8) return v;
-  }
+  const int v = tune_value(Q4_TUNE_GEMV_UNITS);
+  if (v == 4 || v == 8) return v;
   const int per_lane = ceil_div(nb, (64 / R) * GEMV_WAVES);
   return per_lane > 4 && wgs * GEMV_THREADS * 8 <= GEMV_INFLIGHT_UNITS ? 8 : 4;
 }
@@ -1041,11 +1030,12 @@ static int units_in_flight(int nb, int R, long wgs) {
 // pairing the q/k/v batch saves 0.14 us per launch (5.80 -> 5.66 us), while
 // the single and fused-norm launches run faster unpaired between their
 // neighbours (the 48-layer GEMV set 1.611 -> 1.595 ms, the fused token
-// 2.362 -> 2.293 ms). Q4MI_GEMV_PAIR=0 forces 1, =1 pairs every unsplit
-// even grid (tests and tuning sweeps).
+// 2.362 -> 2.293 ms). The Q4_TUNE_GEMV_PAIR override forces 1 (0) or pairs
+// every unsplit even grid (1), for tests and tuning sweeps.
 static int pair_groups(int groups, int split, size_t lds, bool paired) {
   const bool can = split == 1 && groups % 2 == 0 && 2 * lds <= 64 * 1024;
-  if (const char* e = getenv("Q4MI_GEMV_PAIR")) return atoi(e) != 0 && can ? 2 : 1;
+  const int f = tune_value(Q4_TUNE_GEMV_PAIR);
+  if (f >= 0) return f != 0 && can ? 2 : 1;
   return paired && can && groups >= 2 * GEMV_MIN_WGS ? 2 : 1;
 }
 
@@ -1066,13 +1056,12 @@ struct GemvPlan {
   size_t lds, ws;
 };
 
-// Balanced unsplit grids (Q4MI_GEMV_BAL=m, tuning): 256 m row groups (or
+// Balanced unsplit grids (the Q4_TUNE_GEMV_BAL override m, tuning): 256 m row groups (or
 // more, until a group fits 64 rows) spread the rows evenly over all CUs, in
 // units of `unit` rows (2: gate/up pairs); R is the smallest of 8..64 that
 // holds the largest group. Returns 0 when not selected.
 static int balance_mult() {
-  const char* e = getenv("Q4MI_GEMV_BAL");
-  const int m = e ? atoi(e) : 0;
+  const int m = tune_value(Q4_TUNE_GEMV_BAL);
   return m > 0 && m <= 64 ? m : 0;
 }
 static int pow2_rows(int rows) {
@@ -1175,6 +1164,22 @@ static int nx_check_y(const NormIn& nx, int K, const void* y, size_t y_bytes) {
 }
 
 // x (x_dtype) or, with nx, x formed from the NormIn (split 1).
+// Argument checks of a GEMV whose x comes from memory (no fused norm), in
+// the order gemv_launch applies them: callers that queue work of their own
+// before the launch (q4_gemv_noalloc's ticket fill) run them first, so a
+// rejected call enqueues nothing.
+static int gemv_plain_args(const void* x, int x_dtype, const uint32_t* wq, const void* scales, int scale_fmt,
+                           const void* y, int y_dtype, int N, int K) {
+  Q4_ARG(N > 0 && K > 0 && K % BLK == 0, "bad GEMV shape N=%d K=%d (K must be a positive multiple of 32)", N, K);
+  Q4_ARG(x && wq && scales && y, "null pointer");
+  Q4_ARG(x_dtype == Q4_DT_F32 || x_dtype == Q4_DT_F16, "bad x dtype %d", x_dtype);
+  Q4_ARG(y_dtype == Q4_DT_F32 || y_dtype == Q4_DT_F16, "bad y dtype %d", y_dtype);
+  Q4_ARG(scale_fmt == Q4_SCALE_F16 || scale_fmt == Q4_SCALE_E4M3, "bad scale format %d", scale_fmt);
+  Q4_ARG(((uintptr_t)wq & 15) == 0 && ((uintptr_t)x & 15) == 0, "wq and x must be 16-byte aligned");
+  Q4_ARG(N <= (1 << 30) && (long)K <= (1L << 24), "GEMV too large");
+  return Q4_OK;
+}
+
 static int gemv_launch(const void* x, int x_dtype, const uint32_t* wq, const void* scales, int scale_fmt, float inv,
                        void* y, int y_dtype, int N, int K, int split, void* ws, size_t ws_size, void* stream,
                        int gated, const NormIn* nx = nullptr) {
@@ -1209,7 +1214,7 @@ static int gemv_launch(const void* x, int x_dtype, const uint32_t* wq, const voi
   // that prologue. Measured in the decode token's graph (gate/up, 480 groups
   // of 64 rows): token 2.298 -> 2.282 ms, where the plain gate/up GEMV of the
   // same shape is faster with 4 (GEMV set 1.600 against 1.630 ms with 8).
-  if (nx && pl.R == 64 && !getenv("Q4MI_GEMV_UNITS") && ceil_div(pl.nb_max, GEMV_WAVES) > 4) pl.U = 8;
+  if (nx && pl.R == 64 && tune_value(Q4_TUNE_GEMV_UNITS) < 0 && ceil_div(pl.nb_max, GEMV_WAVES) > 4) pl.U = 8;
   Q4_ARG(pl.ws == 0 || groups <= GEMV_MAX_TICKETS, "split-K GEMV supports at most %d row groups", GEMV_MAX_TICKETS);
   uint32_t* cnt = pl.ws ? reinterpret_cast<uint32_t*>(ws) : nullptr;
   float* part = pl.ws ? reinterpret_cast<float*>(reinterpret_cast<char*>(ws) + GEMV_TICKET_BYTES) : nullptr;
@@ -1509,9 +1514,7 @@ size_t q4_gemv_scratch_bytes(void) { return GEMV_SCRATCH_BYTES; }
 int q4_gemv_noalloc(const void* x, int x_dtype, const uint32_t* wq, const void* scales, int scale_fmt, float inv,
                     void* y, int y_dtype, int N, int K, int split, void* stream) {
   clear_error();
-  Q4_ARG(N > 0 && K > 0 && K % BLK == 0, "bad GEMV shape N=%d K=%d (K must be a positive multiple of 32)", N, K);
-  Q4_ARG(x_dtype == Q4_DT_F32 || x_dtype == Q4_DT_F16, "bad x dtype %d", x_dtype);
-  Q4_ARG(N <= (1 << 30) && (long)K <= (1L << 24), "GEMV too large");
+  if (int e = gemv_plain_args(x, x_dtype, wq, scales, scale_fmt, y, y_dtype, N, K)) return e;
   const GemvPlan pl = plan(N, K, split, x_dtype);
   if (pl.ws == 0)   // unsplit plan: no workspace at all
     return gemv_launch(x, x_dtype, wq, scales, scale_fmt, inv, y, y_dtype, N, K, split, nullptr, 0, stream, 0);

@@ -26,6 +26,8 @@ typedef unsigned v2u __attribute__((ext_vector_type(2)));
 
 void set_error(const char* fmt, ...);
 void clear_error();
+// Plan override of a Q4_TUNE_* knob (q4_tune_set), -1 when none.
+int tune_value(int knob);
 
 __host__ __device__ inline int ceil_div(long a, long b) { return (int)((a + b - 1) / b); }
 __host__ __device__ inline int pad_rows(int N) { return ceil_div(N, PANEL) * PANEL; }

@@ -17,6 +17,11 @@ void set_error(const char* fmt, ...) {
 }
 void clear_error() { g_err[0] = 0; }
 
+// Plan overrides (q4_tune_set): -1 = none. Plain ints: the planners read them
+// on the host before each launch.
+static int g_tune[Q4_TUNE_COUNT] = {-1, -1, -1, -1, -1, -1, -1, -1, -1};
+int tune_value(int knob) { return knob >= 0 && knob < Q4_TUNE_COUNT ? g_tune[knob] : -1; }
+
 // f32 -> f16 (RNE) and f16 -> f32 staging casts, 4 elements per thread.
 __global__ void cast_f32_f16_kernel(const float* __restrict__ src, uint16_t* __restrict__ dst, size_t n) {
   size_t i = ((size_t)blockIdx.x * blockDim.x + threadIdx.x) * 4;
@@ -51,6 +56,19 @@ extern "C" {
 const char* q4_version(void) { return "q4mi 0.1.0 gfx950"; }
 
 const char* q4_last_error(void) { return g_err; }
+
+int q4_tune_set(int knob, int value) {
+  clear_error();
+  Q4_ARG(knob >= 0 && knob < Q4_TUNE_COUNT, "unknown tuning knob %d", knob);
+  g_tune[knob] = value < 0 ? -1 : value;
+  return Q4_OK;
+}
+
+int q4_tune_get(int knob) { return tune_value(knob); }
+
+void q4_tune_reset(void) {
+  for (int& v : g_tune) v = -1;
+}
 
 int q4_dev_bytes(int N, int K, size_t* wq_bytes, size_t* scale_elems) {
   clear_error();

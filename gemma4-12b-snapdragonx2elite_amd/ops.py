@@ -51,6 +51,18 @@ def dev_sizes(N: int, K: int):
     return wb.value, se.value
 
 
+def tune_set(knob: str, value: int | None) -> None:
+    """Plan override for tests and tuning sweeps (q4_tune_set): ``knob`` is a
+    name of ``_lib.TUNE_KNOBS``; None clears it. Applies to every later call
+    in the process."""
+    call("q4_tune_set", _lib.TUNE_KNOBS[knob], -1 if value is None else int(value))
+
+
+def tune_reset() -> None:
+    """Clear every plan override (q4_tune_reset)."""
+    lib().q4_tune_reset()
+
+
 def _nbytes(t) -> int:
     return t.numel() * t.element_size()
 

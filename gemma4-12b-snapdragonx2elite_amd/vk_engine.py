@@ -406,6 +406,23 @@ def gelumul_ds(gate: Buf, up: Buf, out: Buf, du, out_dtype=torch.float32) -> OpD
     return OpDesc(ops.gelumul, (_f32v(gate, n), _f32v(up, n), out.view(out_dtype, n)), {})
 
 
+_INTERLEAVED: dict = {}
+
+
+def _interleaved(wg, sg, wu, su, N: int, K: int):
+    """The gate/up matrices interleaved row by row (:func:`ops.interleave_rows`),
+    made once per set of source arrays: the decode gated GEMV and the prefill
+    gated GEMM share it when they read the same scale array. The entry keeps
+    the sources alive, so their addresses identify them for the process."""
+    key = (wg.data_ptr(), sg.data_ptr(), wu.data_ptr(), su.data_ptr(), N, K)
+    hit = _INTERLEAVED.get(key)
+    if hit is None:
+        wo, so = ops.interleave_rows(wg, sg, wu, su, N, K)
+        KEEP.extend([wo, so])
+        hit = _INTERLEAVED[key] = (wo, so, (wg, sg, wu, su))
+    return hit[0], hit[1]
+
+
 def gate_up_ds(qg, qu, inbuf: Buf, actbuf: Buf, x_dtype=torch.float32, act_dtype=torch.float32) -> OpDesc | None:
     """The gate and up GEMVs and the gelumul after them (src/vk_engine.py:242-243,
     246) as one launch: the two matrices are interleaved row by row here (a
@@ -418,8 +435,7 @@ def gate_up_ds(qg, qu, inbuf: Buf, actbuf: Buf, x_dtype=torch.float32, act_dtype
     if (N, K) != (N2, K2) or bsg.t.dtype != bsu.t.dtype or invg != invu or N % 32:
         return None
     fmt = SCALE_E4M3 if bsg.t.dtype == torch.uint8 else SCALE_F16
-    wo, so = ops.interleave_rows(bwg.t, bsg.t, bwu.t, bsu.t, N, K)
-    KEEP.extend([wo, so])
+    wo, so = _interleaved(bwg.t, bsg.t, bwu.t, bsu.t, N, K)
     split = ops.auto_split(2 * N, K)
     ws = ops.default_workspace(2 * N, K, split, wo.device)
     if ws is not None:
@@ -482,7 +498,9 @@ def gemm_cat_ds(qws, inbuf: Buf, outbuf: Buf, **kw):
     as one GEMM over their rows stacked (a copy made once): ``outbuf`` gets
     rows of sum(N) elements, matrix i's outputs at column offset sum(N[:i]).
     Each N must be a multiple of 64 (whole weight panels). ``kw`` as
-    :func:`gemm_ds`; returns its tuple (for :func:`gmm`)."""
+    :func:`gemm_ds`; returns its tuple (for :func:`gmm`). The stacked copy
+    stays beside the separate matrices (the decode GEMVs read those): one more
+    copy of the q/k/v weights in all."""
     Ns = [N for _, (N, _K) in qws]
     K = qws[0][1][1]
     if any(N % 64 for N in Ns) or any(k != K for _, (_n, k) in qws):
@@ -511,14 +529,19 @@ def pre_gate_up_ds(qg, qu, inbuf: Buf, actbuf: Buf) -> OpDesc | None:
     row (a copy made once): ``actbuf`` gets the fp16 activations the
     separate route's gelumul writes, from fp16 normed rows in ``inbuf``.
     Returns None when the two cannot share one matrix (different shapes) or
-    on the W8A8 route; then record the separate descriptors."""
+    on the W8A8 route; then record the separate descriptors. The interleaved
+    copy is shared with :func:`gate_up_ds` on the same fp16 scales and stays
+    beside the separate matrices (one more copy of gate and up in all); the
+    split-K workspace is the shared prefill stage buffer (the gated GEMM
+    reduces it inside its own call, and recorded ops run in order on one
+    stream)."""
     (bwg, _bsg, _sg, _nb, _ig, bs16g, _a, _b), (N, K) = qg
     (bwu, _bsu, _su, _nb2, _iu, bs16u, _c, _d), (N2, K2) = qu
     if (N, K) != (N2, K2) or PREFILL_I8 or bs16g is None or bs16u is None:
         return None
-    wo, so = ops.interleave_rows(bwg.t, bs16g.t, bwu.t, bs16u.t, N, K)
-    ws = torch.empty(ops.gemm_gated_workspace_bytes(MC, 2 * N, K), dtype=torch.uint8, device=wo.device)
-    KEEP.extend([wo, so, ws])
+    wo, so = _interleaved(bwg.t, bs16g.t, bwu.t, bs16u.t, N, K)
+    need = ops.gemm_gated_workspace_bytes(MC, 2 * N, K)
+    ws = _stage("W4nws", need).view(torch.uint8, need)
     return OpDesc(ops.gemm_w4a16_gated, (inbuf.view(torch.float16, MC * K).view(MC, K), wo, so, 2 * N),
                   dict(Y=actbuf.view(torch.float16, MC * N).view(MC, N), ws=ws))
 
@@ -599,13 +622,54 @@ def record_prefill(layers, fuse: bool = True, gemm_norms: bool = False) -> ops.G
                 gmm(None, op[1])
             else:
                 disp(op)
-    return record(body)
+    g = record(body)
+    g.seq = seq          # the recorded descriptor sequence, for inspection
+    return g
+
+
+def _op_tensors(op):
+    """Every tensor an op of a prefill sequence passes (OpDesc args and
+    keywords, or the cast/GEMM/cast tuples of a ``("gmm", ...)`` entry)."""
+    if isinstance(op, OpDesc):
+        items = list(op.args) + list(op.kw.values())
+    elif isinstance(op, tuple) and op and op[0] == "gmm":
+        items = [t for part in op[1][:3] if part is not None for t in part[1:]]
+    else:
+        items = []
+    return [t for t in items if isinstance(t, torch.Tensor)]
+
+
+def _overlap(t: torch.Tensor, u: torch.Tensor) -> bool:
+    a0, b0 = t.data_ptr(), u.data_ptr()
+    return a0 < b0 + u.numel() * u.element_size() and b0 < a0 + t.numel() * t.element_size()
+
+
+def _read_later(seq, start: int, y: torch.Tensor) -> bool:
+    """Whether an op from ``seq[start]`` on passes memory of ``y`` before a
+    GEMM writes ``y`` again (conservative: passing it counts as reading)."""
+    nbytes = y.numel() * y.element_size()
+    for op in seq[start:]:
+        if isinstance(op, tuple) and op and op[0] == "gmm":
+            cin, gem = op[1][0], op[1][1]
+            reads = list(cin[1:] if cin is not None else ()) + list(gem[1:4] if gem[0] == "w4a16" else gem[1:5])
+            if any(isinstance(t, torch.Tensor) and _overlap(t, y) for t in reads):
+                return True
+            out = gem[5]
+            if out.data_ptr() == y.data_ptr() and out.numel() * out.element_size() >= nbytes:
+                return False        # overwritten: later readers see the new values
+            continue
+        if any(_overlap(t, y) for t in _op_tensors(op)):
+            return True
+    return False
 
 
 def _fuse_gemm_normadd(seq):
     """A W4A16 prefill GEMM with fp16 input and output followed by a pre_na
     (or pre_na + pre_norm) that reads its output: one GEMM into split-K
-    partials and one normadd launch that sums them (:func:`ops.gemm_w4a16_normadd`)."""
+    partials and one normadd launch that sums them (:func:`ops.gemm_w4a16_normadd`).
+    The fused launch never writes the GEMM's output buffer, so the pair is
+    fused only when no later op reads that buffer before a GEMM writes it
+    again."""
     out, i = [], 0
     while i < len(seq):
         a = seq[i]
@@ -613,7 +677,8 @@ def _fuse_gemm_normadd(seq):
         gem = a[1][1] if isinstance(a, tuple) and a and a[0] == "gmm" else None
         if (gem is not None and gem[0] == "w4a16" and a[1][0] is None and a[1][2] is None and
                 isinstance(b, OpDesc) and b.fn is ops.pre_normadd and b.args[0].dtype == torch.float16 and
-                b.args[0].data_ptr() == gem[5].data_ptr() and b.kw["D"] == gem[4]):
+                b.args[0].data_ptr() == gem[5].data_ptr() and b.kw["D"] == gem[4] and
+                not _read_later(seq, i + 2, gem[5])):
             _k, x16, wq, sc16, N, _y16, _ws = gem
             M, K = x16.shape
             need = ops.gemm_normadd_workspace_bytes(M, N, K)
@@ -634,7 +699,10 @@ def _fuse_gemm_prepkv(seq):
     """The stacked q/k/v GEMM (fp16 in and out) followed by the pre_prepkv
     that reads its k/v columns: one GEMM into split-K partials and one
     launch that stores the q columns and writes the caches
-    (:func:`ops.gemm_w4a16_qkv_prepkv`)."""
+    (:func:`ops.gemm_w4a16_qkv_prepkv`). The k/v columns of the GEMM's
+    output are then never written: the caller's later ops must read k and v
+    from the caches only (the attention does; :func:`record_prefill`'s
+    layer order guarantees it), while q is read from the output as before."""
     out, i = [], 0
     while i < len(seq):
         a = seq[i]

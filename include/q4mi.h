@@ -61,6 +61,33 @@ const char* q4_last_error(void);
  * for an N x K matrix (K multiple of 32). */
 int q4_dev_bytes(int N, int K, size_t* wq_bytes, size_t* scale_elems);
 
+/* ---- plan overrides (tests and tuning sweeps) ---------------------------
+ * No counterpart in the reference (its split heuristic is fixed,
+ * src/vk_engine.py:143-148). Every launch plan (rows per GEMV workgroup,
+ * units in flight, pairing, K splits, W4A16 k-groups) is chosen from the
+ * shape alone unless an override is set here; environment variables are
+ * never read. An override applies to every later call in the process, may
+ * change the fp32 summation order of split or grouped plans (results stay
+ * within the stated tolerances; integer outputs do not change), and is not
+ * synchronized with calls running on other threads. Values outside a
+ * knob's accepted set are ignored by the planner (the default plan runs). */
+#define Q4_TUNE_GEMV_ROWS 0      /* rows per GEMV workgroup: 8, 16, 32, 64 */
+#define Q4_TUNE_GEMV_UNITS 1     /* weight units in flight per lane: 4, 8 */
+#define Q4_TUNE_GEMV_PAIR 2      /* 0: one row group per workgroup; 1: pair every unsplit even grid */
+#define Q4_TUNE_GEMV_BAL 3       /* balanced grids of 256*m row groups, m 1..64 (0: off) */
+#define Q4_TUNE_GEMV_MM_TILES 4  /* small-M GEMV 16-row tiles per workgroup: 1, 2, 4 */
+#define Q4_TUNE_GEMV_MM_SPLIT 5  /* small-M GEMV K splits: 1..64 */
+#define Q4_TUNE_GEMV_MM_DEEP 6   /* small-M GEMV deeper load ring: 0, 1 */
+#define Q4_TUNE_W4A16_SPLIT 7    /* W4A16 K splits: 1..k-steps */
+#define Q4_TUNE_W4A16_KG 8       /* W4A16 k-groups per workgroup: 1, 2 */
+#define Q4_TUNE_COUNT 9
+/* Set knob to value (value < 0 clears it). Q4_ERR_ARG for an unknown knob. */
+int q4_tune_set(int knob, int value);
+/* Current override of knob, -1 when none (or an unknown knob). */
+int q4_tune_get(int knob);
+/* Clear every override. */
+void q4_tune_reset(void);
+
 /* ---- weight preparation (load time) -------------------------------------
  * Replaces the numpy quantizer quant() (src/vk_engine.py:125-159).        */
 
@@ -305,6 +332,10 @@ int q4_quant_act_i8(const void* X, int x_dtype, int8_t* A, float* sa, int M,
 /* W8A8: C int32 = A int8 [M][K] @ W8 int8 [N][K]^T (exact),
  * Y f16 [M][N] = f16((f32(C) * sa[m]) * sw[n]); sw is sw_dtype [N].
  * C (int32 [M][N]) is written only if non-NULL. Y may be NULL when C is not.
+ * K must be a multiple of 64 (Q4_ERR_ARG otherwise), narrower than the
+ * reference shader, which steps K by 32 (vk/coopgemm_w8a8.comp:23): every
+ * engine shape (K = 3840, 4096, 15360) satisfies it. The same rule holds for
+ * q4_gemm_w8a8_packed and q4_gemm_w4a8. 127^2 * K must stay below 2^31.
  * vk/coopgemm_w8a8.comp:18-37. */
 int q4_gemm_w8a8(const int8_t* A, const int8_t* W8, const float* sa,
                  const void* sw, int sw_dtype, uint16_t* Y, int32_t* C, int M,

@@ -18,17 +18,28 @@ instruction that reads or writes one of the load's destination registers
 before that point is reported.
 
 `main()` prints the findings for every source and returns 1 if there are any;
-tests/test_asm_hazards.py runs the check over all sources.
+test_asm_hazards.py runs the check over all sources (CPU only; test tooling, not part of
+the library).
 """
 from __future__ import annotations
 
 import concurrent.futures as cf
+import importlib
 import re
 import subprocess
+import sys
 import tempfile
 from pathlib import Path
 
-from .build import ARCH, CSRC, FILE_FLAGS, HIPCC_FLAGS, _hipcc
+_ROOT = Path(__file__).resolve().parents[1]
+if str(_ROOT) not in sys.path:
+    sys.path.insert(0, str(_ROOT))
+import __graft_entry__  # noqa: E402  (loads the package directory as g4mi)
+
+__graft_entry__.load_package()
+_build = importlib.import_module("g4mi.build")
+ARCH, CSRC, FILE_FLAGS, HIPCC_FLAGS, _hipcc = (_build.ARCH, _build.CSRC, _build.FILE_FLAGS, _build.HIPCC_FLAGS,
+                                               _build._hipcc)
 
 _VMEM = re.compile(r"^(global_|buffer_|flat_|scratch_)(load|store|atomic)")
 _BRANCH = re.compile(r"^s_(c?branch)(\w*)\s+(\.LBB\w+)")

@@ -41,3 +41,13 @@ def gpu(g4):
         pytest.skip("no GPU in this environment")
     ops = importlib.import_module(f"{PKG_NAME}.ops")
     return ops
+
+
+@pytest.fixture
+def tune(g4):
+    """Plan overrides (q4_tune_set) for one test: ``tune("gemv_rows", 16)``;
+    every override is cleared when the test ends."""
+    ops = importlib.import_module(f"{PKG_NAME}.ops")
+    ops.tune_reset()
+    yield ops.tune_set
+    ops.tune_reset()

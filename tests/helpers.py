@@ -27,3 +27,32 @@ def to_np(t):
 
 def sync():
     torch.cuda.synchronize()
+
+
+# (C, sa bits, sw bits, f16 result) where vk/coopgemm_w8a8.comp:35's order,
+# f16((f32(C) * sa) * sw) with each product rounded to fp32, gives another fp16
+# than every other evaluation: C * (sa * sw), (C * sw) * sa, the exact product
+# rounded once to f16, or once to f32 and then to f16 (found by a search over
+# 4M random draws of realistic magnitudes; ~1 in 125k separates all orders).
+W8A8_EPILOGUE_KATS = [(1580957, 1006503788, 942475318, 0.505859375),
+                      (-2236423, 1027524951, 960400381, -18.9375),
+                      (90738, 1012154212, 961575299, 0.233642578125)]
+
+
+def w8a8_dot_operands(c):
+    """int8 vectors (a, w) with sum a * w == c exactly (|c| < 2^31): pairs
+    (+-127, 127) while they fit, one (+-127, q), one (+-r, 1)."""
+    sgn, r = (-1 if c < 0 else 1), abs(int(c))
+    a, w = [], []
+    while r >= 127 * 127:
+        a.append(127)
+        w.append(127)
+        r -= 127 * 127
+    if r >= 127:
+        a.append(127)
+        w.append(r // 127)
+        r -= 127 * (r // 127)
+    if r:
+        a.append(r)
+        w.append(1)
+    return np.array(a, np.int64) * sgn, np.array(w, np.int64)

@@ -282,3 +282,40 @@ def test_qkv_prepkv_argument_errors_without_gpu(g4):
     assert st == g4._lib.Q4_ERR_ARG and "aligned" in _err(g4)
     st = lib.q4_gemm_w4a16_qkv_prepkv(*args(ws_bytes=need - 4))
     assert st == g4._lib.Q4_ERR_ARG and "workspace too small" in _err(g4)
+
+
+def test_plan_overrides_are_explicit(g4, tune, monkeypatch):
+    """Launch plans change only through q4_tune_set (environment variables are
+    never read); overrides clear individually and all at once, and an unknown
+    knob is an argument error."""
+    lib = g4._lib.lib()
+    knobs = g4._lib.TUNE_KNOBS
+    monkeypatch.setenv("Q4MI_GEMV_ROWS", "8")
+    assert all(lib.q4_tune_get(k) == -1 for k in knobs.values())
+    split = lib.q4_gemv_auto_split(1024, 3840)
+    tune("gemv_rows", 16)
+    tune("w4a16_kg", 2)
+    assert lib.q4_tune_get(knobs["gemv_rows"]) == 16 and lib.q4_tune_get(knobs["w4a16_kg"]) == 2
+    tune("gemv_rows", None)
+    assert lib.q4_tune_get(knobs["gemv_rows"]) == -1 and lib.q4_tune_get(knobs["w4a16_kg"]) == 2
+    lib.q4_tune_reset()
+    assert all(lib.q4_tune_get(k) == -1 for k in knobs.values())
+    assert lib.q4_gemv_auto_split(1024, 3840) == split
+    assert lib.q4_tune_set(len(knobs), 1) == g4._lib.Q4_ERR_ARG and "unknown tuning knob" in _err(g4)
+    assert lib.q4_tune_get(len(knobs)) == -1 and lib.q4_tune_get(-1) == -1
+
+
+def test_noalloc_rejects_bad_arguments_before_any_device_work(g4):
+    """q4_gemv_noalloc checks every argument before it looks up its scratch
+    array or queues the ticket fill of a split-K plan (N=1024 plans a split):
+    with no GPU at all, bad calls still return Q4_ERR_ARG with a message."""
+    lib = g4._lib.lib()
+    p, null = C.c_void_p(4096), C.c_void_p(0)
+    assert lib.q4_gemv_auto_split(1024, 3840) > 1
+    cases = [((null, 1, p, p, 0, C.c_float(1.0), p, 0, 1024, 3840, 0, null), "null"),
+             ((p, 1, p, p, 7, C.c_float(1.0), p, 0, 1024, 3840, 0, null), "scale format"),
+             ((p, 1, p, p, 0, C.c_float(1.0), p, 5, 1024, 3840, 0, null), "y dtype"),
+             ((C.c_void_p(4100), 1, p, p, 0, C.c_float(1.0), p, 0, 1024, 3840, 0, null), "aligned")]
+    for args, msg in cases:
+        assert lib.q4_gemv_noalloc(*args) == g4._lib.Q4_ERR_ARG
+        assert msg in _err(g4), (msg, _err(g4))

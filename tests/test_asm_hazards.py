@@ -12,10 +12,7 @@ ROOT = Path(__file__).resolve().parents[1]
 
 
 def _pkg():
-    import __graft_entry__ as G
-
-    G.load_package()
-    return importlib.import_module("g4mi.asm_check")
+    return importlib.import_module("tests.asm_check")
 
 
 @pytest.mark.skipif(shutil.which("hipcc") is None and not Path("/opt/rocm/bin/hipcc").exists(),

@@ -11,7 +11,7 @@ import torch
 
 from oracle import decode_ops_oracle as D
 from oracle import q4_oracle as O
-from tests.helpers import synth_int4, to_np, upload_int4
+from tests.helpers import W8A8_EPILOGUE_KATS, synth_int4, to_np, upload_int4, w8a8_dot_operands
 
 pytestmark = pytest.mark.gpu
 
@@ -120,6 +120,65 @@ def test_w8a8_packed_config_size_rows(gpu):
     assert (to_np(gC) == C).all()
     Y = O.w8a8_epilogue(C, sa, sw)
     assert (to_np(gY).view(np.uint16) == Y.view(np.uint16)).all()
+    # Y only: every tile takes the full-tile epilogue (16-byte stores)
+    gY1 = gpu.gemm_w8a8_packed(gA, W8p, gsa, torch.from_numpy(sw).cuda(), N)
+    assert (to_np(gY1).view(np.uint16) == Y.view(np.uint16)).all()
+
+
+@pytest.mark.parametrize("M,N", [(2304, 7432), (2100, 7424)])
+def test_w8a8_packed_y_only_ragged(gpu, M, N):
+    """Y-only launches with 256-row tiles (>= 256 tiles) whose grid has both
+    full tiles (16-byte-store epilogue) and ragged edge tiles (M % 256 and
+    N % 256 != 0; N % 8 == 0): every fp16 output vs the oracle, fp32 and fp16
+    s_w."""
+    rng = np.random.default_rng(M + N)
+    K = 512
+    A, sa, W8, sw = _w8a8_case(rng, M, N, K)
+    assert gpu.w8a8_workgroups(M, N) >= 256
+    gA, gsa = torch.from_numpy(A).cuda(), torch.from_numpy(sa).cuda()
+    W8p = torch.from_numpy(O.pack_w8_dev(W8)).cuda()
+    for swdt in (np.float32, np.float16):
+        sw_used = sw.astype(swdt)
+        _, Y = O.gemm_w8a8_ref(A, W8, sa, sw_used.astype(np.float32))
+        gY = gpu.gemm_w8a8_packed(gA, W8p, gsa, torch.from_numpy(sw_used).cuda(), N)
+        assert (to_np(gY).view(np.uint16) == Y.view(np.uint16)).all()
+
+
+def test_w8a8_packed_epilogue_known_answers(gpu):
+    """The kernel's epilogue order is the reference's, f16((f32(C) * sa) * sw)
+    (vk/coopgemm_w8a8.comp:35): rows i < 3 of A and W8 are built so that
+    C[i, i] is exactly the C of a known answer whose fp16 result differs under
+    every other evaluation order, with its sa and sw bits. 256 tiles of 256
+    rows, so the Y-only launch takes the full-tile epilogue and the launch
+    with C the general one; both against the oracle everywhere and against
+    the known answers on the diagonal."""
+    rng = np.random.default_rng(11)
+    M, N, K = 2048, 8192, 256
+    A = rng.integers(-127, 128, (M, K), dtype=np.int8)
+    W8 = rng.integers(-127, 128, (N, K), dtype=np.int8)
+    sa = (rng.random(M) * 0.05 + 0.005).astype(np.float32)
+    sw = (rng.random(N) * 2e-4 + 1e-5).astype(np.float32)
+    A[:3] = 0
+    W8[:3] = 0
+    k0 = 0
+    for i, (c, sab, swb, _) in enumerate(W8A8_EPILOGUE_KATS):
+        a, w = w8a8_dot_operands(c)
+        A[i, k0:k0 + len(a)] = a
+        W8[i, k0:k0 + len(a)] = w
+        k0 += len(a)
+        sa[i] = np.array([sab], np.uint32).view(np.float32)[0]
+        sw[i] = np.array([swb], np.uint32).view(np.float32)[0]
+    assert k0 <= K and gpu.w8a8_workgroups(M, N) == 256
+    C, Y = O.gemm_w8a8_ref(A, W8, sa, sw)
+    assert [int(C[i, i]) for i in range(3)] == [k[0] for k in W8A8_EPILOGUE_KATS]
+    assert [float(Y[i, i]) for i in range(3)] == [k[3] for k in W8A8_EPILOGUE_KATS]
+    gA, gsa, gsw = torch.from_numpy(A).cuda(), torch.from_numpy(sa).cuda(), torch.from_numpy(sw).cuda()
+    W8p = torch.from_numpy(O.pack_w8_dev(W8)).cuda()
+    gY = gpu.gemm_w8a8_packed(gA, W8p, gsa, gsw, N)
+    gY2, gC = gpu.gemm_w8a8_packed(gA, W8p, gsa, gsw, N, want_c=True)
+    assert (to_np(gC) == C).all()
+    for y in (gY, gY2):
+        assert (to_np(y).view(np.uint16) == Y.view(np.uint16)).all()
 
 
 @pytest.mark.parametrize("M,N,K", [(100, 320, 192), (2048, 15360, 3840)])
@@ -208,19 +267,19 @@ def test_w4a16(gpu, M, N, K):
 
 
 @pytest.mark.parametrize("M,N,K", [(128, 3840, 15360), (512, 3840, 1920), (100, 320, 96), (256, 1024, 224)])
-def test_w4a16_two_kgroups_match_one(gpu, M, N, K, monkeypatch):
+def test_w4a16_two_kgroups_match_one(gpu, M, N, K, tune):
     """128-row tiles can run two groups of 4 waves over the two halves of
-    each workgroup's k-steps (forced here with Q4MI_W4A16_KG=2) and add group
-    1's sums into group 0's. Against the one-group kernel (Q4MI_W4A16_KG=1)
+    each workgroup's k-steps (forced here with the w4a16_kg override = 2) and add group
+    1's sums into group 0's. Against the one-group kernel (w4a16_kg = 1)
     only the fp32 summation order differs. The shapes cover an odd k-step count per workgroup (group 1's
     surplus step reads zero scales), a one-block last k-step, and split-K."""
     rng = np.random.default_rng(M + N + K)
     q, s = synth_int4(rng, N, K)
     X = torch.from_numpy(rng.standard_normal((M, K)).astype(np.float16)).cuda()
     wq, sc = upload_int4(q, s)
-    monkeypatch.setenv("Q4MI_W4A16_KG", "2")
+    tune("w4a16_kg", "2")
     Y2 = to_np(gpu.gemm_w4a16(X, wq, sc, N)).astype(np.float64)
-    monkeypatch.setenv("Q4MI_W4A16_KG", "1")
+    tune("w4a16_kg", "1")
     Y1 = to_np(gpu.gemm_w4a16(X, wq, sc, N)).astype(np.float64)
     assert np.isfinite(Y2).all()
     assert np.abs(Y2 - Y1).max() <= np.abs(Y1).max() * 2.0 ** -9
@@ -228,13 +287,41 @@ def test_w4a16_two_kgroups_match_one(gpu, M, N, K, monkeypatch):
     assert O.normwise_rel_err(Y2.astype(np.float32), ref) <= 1e-3
 
 
+def test_w4a16_two_kgroups_nonfinite_x(gpu, tune):
+    """An Inf in X in the last k-step of group 1's range (each of the 16 K
+    splits at M=128, N=3840, K=15360 gives group 1 an odd 7 of 15 k-steps):
+    two k-groups give the one-group kernel's Inf/NaN pattern (NaN only where
+    the dequantized weight is 0), so the odd group multiplies nothing extra."""
+    M, N, K = 128, 3840, 15360
+    rng = np.random.default_rng(5)
+    q, s = synth_int4(rng, N, K)
+    Xh = rng.standard_normal((M, K)).astype(np.float16)
+    Xh[3, K - 1] = np.inf
+    Xh[70, K - 40] = -np.inf
+    X = torch.from_numpy(Xh).cuda()
+    wq, sc = upload_int4(q, s)
+    tune("w4a16_kg", "2")
+    Y2 = to_np(gpu.gemm_w4a16(X, wq, sc, N)).astype(np.float64)
+    tune("w4a16_kg", "1")
+    Y1 = to_np(gpu.gemm_w4a16(X, wq, sc, N)).astype(np.float64)
+    for m, k in ((3, K - 1), (70, K - 40)):
+        zero_w = (q[:, k] == 8) | (s[:, k // 32] == 0)  # a dequantized weight of 0: Inf * 0
+        assert np.isnan(Y1[m]).tolist() == zero_w.tolist()
+        assert np.isinf(Y1[m][~zero_w]).all()
+    assert (np.isnan(Y2) == np.isnan(Y1)).all()
+    fin = np.isfinite(Y1)
+    assert (Y2[~fin & ~np.isnan(Y1)] == Y1[~fin & ~np.isnan(Y1)]).all()
+    assert np.isfinite(Y2[fin]).all()
+    assert np.abs(Y2[fin] - Y1[fin]).max() <= np.abs(Y1[fin]).max() * 2.0 ** -9
+
+
 @pytest.mark.parametrize("M,I,K,dev_interleave", [(128, 15360, 3840, True), (128, 512, 256, True),
                                                   (100, 330, 96, False), (37, 7, 224, False),
                                                   (512, 1024, 1920, True), (37, 35, 15360, False)])
-def test_w4a16_gated_equals_separate_gemms_and_gelumul(gpu, M, I, K, dev_interleave, monkeypatch):
+def test_w4a16_gated_equals_separate_gemms_and_gelumul(gpu, M, I, K, dev_interleave, tune):
     """The gated W4A16 GEMM over interleaved gate/up rows gives the separate
     route's activations bit for bit (gate GEMM, up GEMM, each rounded to
-    fp16, then gelumul) when both split K the same way (Q4MI_W4A16_SPLIT),
+    fp16, then gelumul) when both split K the same way (the w4a16_split override),
     and matches the oracle: gelu_tanh(f16(X Wg^T)) * f16(X Wu^T), rounded to
     fp16, within an fp16 step of the largest output. Shapes: the prefill
     chunk's gate/up (I 15360), a one-block last k-step (K % 64 = 32), an
@@ -254,7 +341,7 @@ def test_w4a16_gated_equals_separate_gemms_and_gelumul(gpu, M, I, K, dev_interle
         qi[0::2], qi[1::2], s_i[0::2], s_i[1::2] = qg, qu, sg, su
         wi, si = upload_int4(qi, s_i)
     split = max(1, gpu.gemm_workspace_bytes(M, 2 * I, K) // (M * 2 * I * 4))
-    monkeypatch.setenv("Q4MI_W4A16_SPLIT", str(split))
+    tune("w4a16_split", str(split))
     A = to_np(gpu.gemm_w4a16_gated(X, wi, si, 2 * I))
     G = gpu.gemm_w4a16(X, wg, scg, I)
     U = gpu.gemm_w4a16(X, wu, scu, I)

@@ -41,9 +41,9 @@ def test_gemv_f16_scales(gpu, N, K, xdt, ydt):
 
 @pytest.mark.parametrize("split", [1, 2, 3, 5, 8, 120])
 @pytest.mark.parametrize("rows", [None, "8", "64"])
-def test_gemv_split_invariance(gpu, split, rows, monkeypatch):
+def test_gemv_split_invariance(gpu, split, rows, tune):
     if rows:
-        monkeypatch.setenv("Q4MI_GEMV_ROWS", rows)
+        tune("gemv_rows", rows)
     rng = np.random.default_rng(21)
     N, K = 512, 3840
     q, s, x = _case(rng, N, K)
@@ -55,13 +55,13 @@ def test_gemv_split_invariance(gpu, split, rows, monkeypatch):
 
 @pytest.mark.parametrize("rows", ["8", "16", "32", "64"])
 @pytest.mark.parametrize("N,nblk", [(64, 3), (256, 37), (192, 200), (320, 481)])
-def test_gemv_units_in_flight(gpu, rows, N, nblk, monkeypatch):
+def test_gemv_units_in_flight(gpu, rows, N, nblk, tune):
     """Every rows-per-workgroup x units-in-flight variant against the oracle,
     with block counts that leave the lanes' last round of the load ring
     partly empty (3, 37, 200, 481 blocks), fp16 and fp32 x. The units are
     consumed in the same order whatever the ring size, so U = 4 and U = 8
     give bit-identical outputs."""
-    monkeypatch.setenv("Q4MI_GEMV_ROWS", rows)
+    tune("gemv_rows", rows)
     K = 32 * nblk
     rng = np.random.default_rng(N + nblk)
     q, s, x = _case(rng, N, K)
@@ -70,7 +70,7 @@ def test_gemv_units_in_flight(gpu, rows, N, nblk, monkeypatch):
         ref = O.gemv_ref(q, s, xin)
         outs = []
         for units in ["4", "8"]:
-            monkeypatch.setenv("Q4MI_GEMV_UNITS", units)
+            tune("gemv_units", units)
             y = gpu.gemv(torch.from_numpy(xin).cuda(), wq, sc, N, K, y_dtype=ydt, split=1)
             assert O.normwise_rel_err(to_np(y).astype(np.float32), ref) <= tol, (units, ydt)
             outs.append(y)
@@ -79,11 +79,11 @@ def test_gemv_units_in_flight(gpu, rows, N, nblk, monkeypatch):
 
 @pytest.mark.parametrize("K,xdt,rows", [(32768, torch.float16, "64"), (32768, torch.float16, "8"),
                                         (16384, torch.float32, "16")])
-def test_gemv_largest_x_staging(gpu, K, xdt, rows, monkeypatch):
+def test_gemv_largest_x_staging(gpu, K, xdt, rows, tune):
     """The longest x one workgroup stages without a K split (64 KB of x, plus
     the block sums for fp16 x), through q4_gemv and q4_gemv_batch: the same
     rows per workgroup give bit-identical outputs."""
-    monkeypatch.setenv("Q4MI_GEMV_ROWS", rows)
+    tune("gemv_rows", rows)
     N = 128
     rng = np.random.default_rng(K + int(rows))
     q, s, x = _case(rng, N, K)
@@ -265,11 +265,11 @@ def test_gemv_batch_vs_oracle(gpu, shapes, K, xdt, ydt):
 
 
 @pytest.mark.parametrize("rows", ["8", "16", "32", "64"])
-def test_gemv_batch_bit_identical_to_single_launches(gpu, rows, monkeypatch):
+def test_gemv_batch_bit_identical_to_single_launches(gpu, rows, tune):
     """Same rows-per-workgroup => the batched launch sums in the same order as
     one q4_gemv per matrix (split 1): bit-identical outputs, written into one
     buffer at the q/k/v offsets without touching the gaps."""
-    monkeypatch.setenv("Q4MI_GEMV_ROWS", rows)
+    tune("gemv_rows", rows)
     rng = np.random.default_rng(int(rows))
     K = 3840
     shapes = [512, 256, 256]
@@ -339,14 +339,14 @@ def test_gemv_gated_vs_oracle(gpu, I, K, xdt, adt):
 
 @pytest.mark.parametrize("N,K,rows", [(15360, 3840, None), (30720, 3840, None), (1024, 4096, "16"), (4096, 15360, "32"),
                                       (128, 256, None)])
-def test_gemv_paired_row_groups_bit_identical(gpu, N, K, rows, monkeypatch):
+def test_gemv_paired_row_groups_bit_identical(gpu, N, K, rows, tune):
     """Two row groups per 512-thread workgroup compute exactly what two
     256-thread workgroups do: q4_gemv, q4_gemv_batch and q4_gemv_gated give
     the same bits with pairing forced on and off (128 rows: split-K, never
     paired), and match the oracle."""
     from oracle import decode_ops_oracle as D
     if rows:
-        monkeypatch.setenv("Q4MI_GEMV_ROWS", rows)
+        tune("gemv_rows", rows)
     rng = np.random.default_rng(N + K)
     q, s, x = _case(rng, N, K)
     q2, s2 = synth_int4(rng, N, K)
@@ -356,7 +356,7 @@ def test_gemv_paired_row_groups_bit_identical(gpu, N, K, rows, monkeypatch):
     wo, so = gpu.interleave_rows(wq, sc, wq2, sc2, N, K) if N % 32 == 0 else (None, None)
     outs = {}
     for pair in ("0", "1"):
-        monkeypatch.setenv("Q4MI_GEMV_PAIR", pair)
+        tune("gemv_pair", pair)
         y = gpu.gemv(xt, wq, sc, N, K, y_dtype=torch.float32)
         yb = gpu.gemv_batch(xt, [(wq, sc, N, None, None), (wq2, sc2, N, None, None)], K, y_dtype=torch.float32)
         act = gpu.gemv_gated(xt, wo, so, 2 * N, K, act_dtype=torch.float32)

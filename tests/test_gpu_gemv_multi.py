@@ -52,12 +52,12 @@ def test_gemv_multi_vs_oracle_and_single(gpu, N, K, M, exact):
 
 @pytest.mark.parametrize("rows", ["8", "16", "32", "64"])
 @pytest.mark.parametrize("units", ["4", "8"])
-def test_gemv_multi_plan_variants_bit_identical(gpu, rows, units, monkeypatch):
+def test_gemv_multi_plan_variants_bit_identical(gpu, rows, units, tune):
     """Every rows-per-workgroup x units-in-flight variant, with a block count
     (37) that leaves the last round of the load ring partly empty: each row
     equals the single GEMV under the same plan."""
-    monkeypatch.setenv("Q4MI_GEMV_ROWS", rows)
-    monkeypatch.setenv("Q4MI_GEMV_UNITS", units)
+    tune("gemv_rows", rows)
+    tune("gemv_units", units)
     N, K, M = 2048, 32 * 37, 6
     rng = np.random.default_rng(int(rows) * 10 + int(units))
     q, s = synth_int4(rng, N, K)
@@ -118,14 +118,14 @@ def test_gemv_multi_largest_staging_and_limits(gpu):
 
 @pytest.mark.parametrize("tiles", ["1", "2", "4"])
 @pytest.mark.parametrize("deep", ["0", "1"])
-def test_gemv_multi_mfma_plan_variants(gpu, tiles, deep, monkeypatch):
+def test_gemv_multi_mfma_plan_variants(gpu, tiles, deep, tune):
     """Every row-tile count x load depth of the MFMA path against the oracle,
     with block counts that leave waves without blocks (3: wave 3 idle) and
     the last round of the load ring partly empty (37, 200). The blocks and
     partial sums are added in the same order whatever the depth, so both
     depths give bit-identical outputs."""
-    monkeypatch.setenv("Q4MI_GEMV_MM_TILES", tiles)
-    monkeypatch.setenv("Q4MI_GEMV_MM_DEEP", deep)
+    tune("gemv_mm_tiles", tiles)
+    tune("gemv_mm_deep", deep)
     for N, nblk, M in [(256, 3, 16), (320, 37, 7), (4096, 200, 13)]:
         K = 32 * nblk
         rng = np.random.default_rng(N + nblk + int(tiles))
@@ -136,9 +136,9 @@ def test_gemv_multi_mfma_plan_variants(gpu, tiles, deep, monkeypatch):
         ref = O.gemm_w4a16_ref(X, q, s)
         for m in range(M):
             assert O.normwise_rel_err(to_np(Y[m]), ref[m]) <= TOL[torch.float32], (N, nblk, m)
-        monkeypatch.setenv("Q4MI_GEMV_MM_DEEP", "1" if deep == "0" else "0")
+        tune("gemv_mm_deep", "1" if deep == "0" else "0")
         Y2 = gpu.gemv_multi(torch.from_numpy(X).cuda(), wq, sc, N, K, y_dtype=torch.float32)
-        monkeypatch.setenv("Q4MI_GEMV_MM_DEEP", deep)
+        tune("gemv_mm_deep", deep)
         assert torch.equal(Y, Y2)
 
 
@@ -162,13 +162,13 @@ def test_gemv_multi_mfma_zero_and_extreme_codes(gpu):
 
 
 @pytest.mark.parametrize("split", ["1", "2", "3", "5", "8"])
-def test_gemv_multi_ksplit_variants(gpu, split, monkeypatch):
+def test_gemv_multi_ksplit_variants(gpu, split, tune):
     """K split across workgroups (T = 4 tiles, fp32 partials, split-order
     reduce) at forced split counts, with block counts that leave the last
     split shorter (203 blocks) and M * N not a multiple of 4 (the reduce's
     one-output-per-thread path), fp16 and fp32 y, against the oracle and
     against the unsplit launch."""
-    monkeypatch.setenv("Q4MI_GEMV_MM_SPLIT", split)
+    tune("gemv_mm_split", split)
     for N, nblk, M in [(3840, 203, 16), (1001, 96, 3), (4096, 120, 5)]:
         K = 32 * nblk
         rng = np.random.default_rng(N + nblk + int(split))
@@ -181,9 +181,9 @@ def test_gemv_multi_ksplit_variants(gpu, split, monkeypatch):
         assert need == (int(split) * M * N * 4 if split != "1" else 0)
         for ydt in (torch.float16, torch.float32):
             Y = gpu.gemv_multi(Xd, wq, sc, N, K, y_dtype=ydt)
-            monkeypatch.setenv("Q4MI_GEMV_MM_SPLIT", "1")
+            tune("gemv_mm_split", "1")
             Y1 = gpu.gemv_multi(Xd, wq, sc, N, K, y_dtype=ydt)
-            monkeypatch.setenv("Q4MI_GEMV_MM_SPLIT", split)
+            tune("gemv_mm_split", split)
             Yh = to_np(Y).astype(np.float32)
             for m in range(M):
                 assert O.normwise_rel_err(Yh[m], ref[m]) <= TOL[ydt], (N, nblk, m, ydt)

@@ -37,8 +37,8 @@ def _cuda(*arrs):
 @pytest.mark.parametrize("pair", ["0", "1"])
 @pytest.mark.parametrize("N,K,scale", [(1024, 3840, 0.0), (300, 96, 0.5), (640, 4096, 0.0), (2048, 800, 1.25),
                                        (15360, 3840, 0.0)])
-def test_gemv_normadd(gpu, N, K, scale, pair, monkeypatch):
-    monkeypatch.setenv("Q4MI_GEMV_PAIR", pair)
+def test_gemv_normadd(gpu, N, K, scale, pair, tune):
+    tune("gemv_pair", pair)
     print(f"gemv_normadd N={N} K={K} scale={scale} pair={pair}", flush=True)
     rng = np.random.default_rng(N + K)
     q, s = synth_int4(rng, N, K)
@@ -158,14 +158,14 @@ def test_gemv_normadd_rejects_bad_operands(gpu):
 
 @pytest.mark.parametrize("pair", ["0", "1"])
 @pytest.mark.parametrize("gated", [False, True])
-def test_gemv_normadd_rows64(gpu, pair, gated, monkeypatch):
+def test_gemv_normadd_rows64(gpu, pair, gated, tune):
     """64 rows per workgroup: one block slot per wave in nx_stage's LDS mapping,
     the plan the real gate/up launch (30720 x 3840, gated, paired) takes."""
-    monkeypatch.setenv("Q4MI_GEMV_PAIR", pair)
+    tune("gemv_pair", pair)
     K, I = 3840, 15360 if gated else 2048
     N = 2 * I if gated else 4096
     if not gated:
-        monkeypatch.setenv("Q4MI_GEMV_ROWS", "64")
+        tune("gemv_rows", "64")
     print(f"gemv_normadd rows64 N={N} gated={gated} pair={pair}", flush=True)
     rng = np.random.default_rng(21 + int(gated))
     a, h, w, w2 = _norm_inputs(rng, K)

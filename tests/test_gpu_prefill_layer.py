@@ -131,6 +131,10 @@ def test_prefill_chunks_through_the_engine_mirror(g4, gpu, fast, stacked):
                                u=up[2], d=dp[2], kc=np.zeros(nkv * cfg["stride"] * hd, np.float16),
                                vc=np.zeros(nkv * cfg["stride"] * hd, np.float16), **norms))
     graph = E.record_prefill([L for L, _, _ in layers], fuse=fast, gemm_norms=stacked)
+    if stacked:  # every o/down GEMM fused into its normadd, every q/k/v GEMM into its prepkv
+        fns = [getattr(op, "fn", None) for op in graph.seq]
+        assert fns.count(g4.ops.gemm_w4a16_normadd) == 2 * len(layers)
+        assert fns.count(g4.ops.gemm_w4a16_qkv_prepkv) == len(layers)
 
     gemm = lambda x, wd16: _f16(_f16(x) @ wd16.T)
     for chunk in range(CHUNKS):

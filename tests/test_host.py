@@ -164,6 +164,14 @@ def test_prefill_gemm_fusions_pair_gemms_with_their_consumers(g4, monkeypatch):
     na_other = E.OpDesc(ops.pre_normadd, (other, w, h), dict(M=MC, D=N, scale=0.5))
     assert [type(o) for o in E._fuse_gemm_normadd([gmm(N, T), na_other])] == [tuple, E.OpDesc]
     assert len(E._fuse_gemm_normadd([gmm(N, T, cin=("cast_dn", None, None)), na])) == 2
+    # the fused launch never writes T: no fusion while a later op reads T, unless a GEMM rewrote it first
+    reader = E.OpDesc(ops.pre_rmsnorm, (T, w, y), dict(M=MC, D=N))
+    assert len(E._fuse_gemm_normadd([gmm(N, T), na, reader])) == 3
+    assert len(E._fuse_gemm_normadd([gmm(N, T), na, gmm(N, T), reader])) == 3   # first pair fused
+    assert E._fuse_gemm_normadd([gmm(N, T), na, gmm(N, T), reader])[0].fn is ops.gemm_w4a16_normadd
+    x_reads_T = ("gmm", (None, ("w4a16", T.view(MC, N), torch.zeros(N * N // 8, dtype=torch.int32),
+                                torch.zeros(N * N // 32, dtype=torch.float16), N, other.view(MC, N), None), None, N, N))
+    assert len(E._fuse_gemm_normadd([gmm(N, T), na, x_reads_T])) == 3
 
     # stacked q/k/v + pre_prepkv, with and without k == v
     nkv, hd, nq = 2, 64, 256

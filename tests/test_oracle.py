@@ -15,6 +15,7 @@ import pytest
 import torch
 
 from oracle import q4_oracle as O
+from tests.helpers import W8A8_EPILOGUE_KATS
 
 
 # ------------------------------------------------------------ quant codes
@@ -401,10 +402,23 @@ def test_w8a8_epilogue_order_and_rounding():
     Y = O.w8a8_epilogue(C, sa, sw)
     # powers of two: exact products, one f16 rounding; row scale sa[m], column scale sw[n]
     assert Y.tolist() == [[3.0, -0.3125], [500.0, 0.21875]]
-    # non-exact case: (C*sa)*sw in fp32, then RNE to f16 (not a single f64 product)
+    # 2049 is a tie between 2048 and 2050 in f16 -> even
     C1 = np.array([[2049]], np.int32)
     Y1 = O.w8a8_epilogue(C1, np.array([1.0], np.float32), np.array([1.0], np.float32))
-    assert Y1[0, 0] == np.float16(2048.0)  # 2049 is a tie between 2048 and 2050 in f16 -> even
+    assert Y1[0, 0] == np.float16(2048.0)
+
+
+def test_w8a8_epilogue_known_answers_separate_orders():
+    for C, sab, swb, want in W8A8_EPILOGUE_KATS:
+        sa = np.array([sab], np.uint32).view(np.float32)
+        sw = np.array([swb], np.uint32).view(np.float32)
+        Y = O.w8a8_epilogue(np.array([[C]], np.int32), sa, sw)
+        assert Y[0, 0] == np.float16(want)
+        Cf = np.float32(C)
+        exact = float(C) * float(sa[0]) * float(sw[0])
+        others = [np.float16(Cf * (sa[0] * sw[0])), np.float16((Cf * sw[0]) * sa[0]), np.float16(exact),
+                  np.float16(np.float32(exact))]
+        assert all(o.view(np.uint16) != Y[0, 0].view(np.uint16) for o in others), (C, others)
 
 
 def test_normwise_metric():

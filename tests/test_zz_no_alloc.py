@@ -69,6 +69,7 @@ def test_noalloc_rejects_oversized_scratch(g4, gpu):
     need = gpu.Workspace.bytes_for(N, K)
     assert split > 1 and need > lib.q4_gemv_scratch_bytes()
     dummy = torch.zeros(16, dtype=torch.uint8, device="cuda")
+    # x, x_dtype (1: fp16), wq, scales, scale_fmt (0: fp16), inv, y, y_dtype (0: fp32), N, K, split, stream
     rc = lib.q4_gemv_noalloc(dummy.data_ptr(), 1, dummy.data_ptr(), dummy.data_ptr(), 0, C.c_float(1.0),
                              dummy.data_ptr(), 0, N, K, 0, None)
     assert rc == _lib.Q4_ERR_ARG and b"scratch" in lib.q4_last_error()
