@@ -385,7 +385,7 @@ def bench_prefill(ops, reps: int = 5, p0: int = 3968, stacked: bool = True, gemm
 
 
 def bench_token_step(ops, steps: int, warmup: int, pos: int = 1023, fast: bool = False,
-                     fuse_gemv: bool = True):
+                     fuse_gemv: bool = True, host_loop: bool = False):
     """A whole decode token through the engine mirror (vk_engine.py): the
     reference's per-layer dispatch order (norm, q/k/v, prepkv, attention, o,
     normadd, norm, gate/up, gelumul, down, normadd) for 48 layers of the
@@ -398,7 +398,13 @@ def bench_token_step(ops, steps: int, warmup: int, pos: int = 1023, fast: bool =
     follows it, gate/up interleaved with the gelumul in their GEMV's
     epilogue, and fp16 GEMV inputs (the residual stream stays fp32); with
     ``fuse_gemv`` too, each fused norm runs inside the q/k/v or gate/up GEMV
-    launch that reads it."""
+    launch that reads it. With ``host_loop``, the graph starts with the
+    token-inputs launch (embedding row from a device table of all 262144
+    tokens, position, RoPE rows from a table) and each token is one
+    ``vk_engine.forward`` call at the next position: pinned-memory write of
+    (tid, pos), graph launch, bounded wait, timed on the host clock
+    (``ms_per_token``) beside the back-to-back replays of the same graph
+    (``graph_replay_ms_per_token``)."""
     import importlib
 
     import numpy as np
@@ -457,9 +463,29 @@ def bench_token_step(ops, steps: int, warmup: int, pos: int = 1023, fast: bool =
     d_fin = E.normbg(B["h"], vec(H), B["normed_f"], DUH, out_dtype=xdt)
     d_lm = E.gemv_ds(qw(V, H), B["normed_f"], B["logits"], 0, x_dtype=xdt)
     B["h"].write(np.ones(H, np.float32))
-    graph = E.record_decode(layers, d_fin, d_lm, fuse=fast, fuse_gemv=fuse_gemv)
+    d_tok = step = None
+    max_pos = pos + 2 * (warmup + steps) + 2
+    if host_loop:
+        emb = E.Buf(tensor=torch.randn(V * H, device=dev, generator=gen) * 0.05)
+        ctab, stab = vec(max_pos * hd, -0.5), vec(max_pos * hd, -0.5)
+        step = torch.zeros(2, dtype=torch.int32, pin_memory=True)
+        d_tok = E.token_inputs_ds(step, emb, B["h"], DYN, [(ctab, stab, hd, cosb, sinb)], vocab=V, H=H,
+                                  max_pos=max_pos)
+    graph = E.record_decode(layers, d_fin, d_lm, fuse=fast, fuse_gemv=fuse_gemv, d_tok=d_tok)
     # one launch per recorded descriptor, plus the split merge of every attention
     launches = len(graph.seq) + sum(1 for op in graph.seq if getattr(op, "fn", None) in (ops.attn, ops.prepkv_attn))
+    host = None
+    if host_loop:
+        tids = torch.randint(0, V, (warmup + steps,), generator=torch.Generator().manual_seed(5)).tolist()
+        p = pos
+        for i in range(warmup):
+            E.forward(graph, step, tids[i], p, vocab=V, max_pos=max_pos, timeout_ms=20000)
+            p += 1
+        t0 = time.perf_counter()
+        for i in range(steps):
+            E.forward(graph, step, tids[warmup + i], p, vocab=V, max_pos=max_pos, timeout_ms=20000)
+            p += 1
+        host = (time.perf_counter() - t0) * 1e3 / steps
     for _ in range(warmup):
         graph.launch()
     torch.cuda.synchronize()
@@ -480,13 +506,18 @@ def bench_token_step(ops, steps: int, warmup: int, pos: int = 1023, fast: bool =
     del layers, B
     E.KEEP.clear()
     torch.cuda.empty_cache()
-    return {"ms_per_token": round(ms, 4), "position": pos, "keys_attended": T,
+    out = {"ms_per_token": round(host if host_loop else ms, 4), "position": pos, "keys_attended": T,
             "activations": (("fp32 residual stream, fp16 GEMV inputs, fused norms, gelumul in the gate/up GEMV"
                              + (", norms inside the q/k/v and gate/up GEMV launches" if fuse_gemv else ""))
                             if fast else "fp32 (reference)"),
             "weight_bytes": wbytes, "kv_cache_bytes_read": kvbytes,
             "GBps": round((wbytes + kvbytes) / (ms * 1e-3) / 1e9, 1),
             "kernels_per_token": launches}
+    if host_loop:
+        out.update(timing="vk_engine.forward per token on the host clock (pinned (tid, pos) write, graph launch, "
+                          "bounded wait), positions advancing from " + str(pos),
+                   graph_replay_ms_per_token=round(ms, 4))
+    return out
 
 
 def counter_workload(ops):
@@ -1035,7 +1066,8 @@ def main():
         return
     if args.token_only:
         for fast in (False, True):
-            print(f"[bench] token step {bench_token_step(ops, args.steps, args.warmup, fast=fast)}", flush=True)
+            print(f"[bench] token step {bench_token_step(ops, args.steps, args.warmup, fast=fast, host_loop=fast)}",
+                  flush=True)
         return
     print(f"[bench] decode graph: {LAYERS} layers + lm_head, {args.steps} steps after {args.warmup} warmup",
           flush=True)
@@ -1045,7 +1077,7 @@ def main():
     tok = None
     if not args.no_token:
         tok = {"reference_dispatches": bench_token_step(ops, max(20, args.steps // 4), 5),
-               "fused": bench_token_step(ops, max(20, args.steps // 4), 5, fast=True),
+               "fused": bench_token_step(ops, max(20, args.steps // 4), 5, fast=True, host_loop=True),
                "fused_norm_launches": bench_token_step(ops, max(20, args.steps // 4), 5, fast=True,
                                                        fuse_gemv=False)}
         print(f"[bench] token step {tok}", flush=True)
@@ -1114,6 +1146,7 @@ def main():
         "c3_us": single["c3_15360x3840_e4m3_scales"]["us_per_launch"],
         "lm_head_us": single["lm_head_262144x3840_f16_scales"]["us_per_launch"],
         "token_ms": None if tok is None else tok["fused"]["ms_per_token"],
+        "token_graph_ms": None if tok is None else tok["fused"]["graph_replay_ms_per_token"],
         "prefill_chunk_ms": pre["ms_per_chunk"],
     }
     if w8 is not None:

@@ -90,6 +90,7 @@ SIGNATURES = {
     "q4_prepkv": (_i, [_vp, _vp, _vp, _vp, _vp, _vp, _i, _i, _i, _i, _i, _i, _i, _vp, _vp]),
     "q4_attn_workspace_bytes": (_sz, [_i, _i, _i]),
     "q4_attn": (_i, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _i, _i, _i, _i, _i, _i, _i, _i, _vp, _vp, _sz, _vp]),
+    "q4_token_inputs": (_i, [_vp, _vp, _i, _i, _vp, _vp, _i, _vp, _vp, _vp, _i, _vp, _vp, _vp]),
     "q4_prepkv_attn": (_i, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _i, _i, _i, _i, _i, _i, _i, _i, _i, _i, _i, _vp,
                             _vp, _sz, _vp]),
     "q4_probe_stream_read": (_i, [_vp, _sz, _i, _i, _i, _vp, _sz, _sz, _vp, _sz, _vp, _sz, _vp]),

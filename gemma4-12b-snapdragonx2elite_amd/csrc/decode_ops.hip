@@ -751,6 +751,60 @@ static void pre_normadd_launch(const void* x, int x_dtype, const float* w, float
     hipLaunchKernelGGL((normadd_kernel<FUSE, YT, Q4_DT_F32>), dim3(M), dim3(NORM_THREADS), 0, st, x, w, h, D, sc, w2, y);
 }
 
+// ---- per-token inputs at the head of a decode graph ------------------------
+// The host writes of the reference's forward() (src/vk_engine.py:312-314:
+// the embedding row into h, DYN = (pos, pos + 1), each layer type's RoPE
+// cos/sin rows) done on the device from (tid, pos) in step[0..1], so a token
+// is one graph launch: workgroup 0 gathers the embedding row and writes DYN,
+// workgroup 1 + t gathers the rows of RoPE table t. step is read with
+// system-scope loads (it may be pinned host memory the host rewrites before
+// each launch). Out-of-range values are clamped (the host checks them
+// before writing; nothing here reads outside the tables).
+struct TokTabs {
+  const float* cos_tab[Q4_TOKEN_MAX_TABLES];
+  const float* sin_tab[Q4_TOKEN_MAX_TABLES];
+  float* cos_out[Q4_TOKEN_MAX_TABLES];
+  float* sin_out[Q4_TOKEN_MAX_TABLES];
+  int hd[Q4_TOKEN_MAX_TABLES];
+  int count;
+};
+
+__global__ void __launch_bounds__(256) token_inputs_kernel(const int32_t* __restrict__ step,
+                                                           const float* __restrict__ emb, int vocab, int H,
+                                                           float* __restrict__ h, uint32_t* __restrict__ dyn,
+                                                           int max_pos, const TokTabs tabs) {
+  const int tid_raw = __hip_atomic_load(step, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+  const int pos_raw = __hip_atomic_load(step + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+  const int tok = min(max(tid_raw, 0), vocab - 1), pos = min(max(pos_raw, 0), max_pos - 1);
+  const int t = threadIdx.x;
+  if (blockIdx.x == 0) {
+    const float* src = emb + (long)tok * H;
+    if ((H & 3) == 0) {
+      for (int i = t; i < H / 4; i += 256)
+        reinterpret_cast<float4*>(h)[i] = reinterpret_cast<const float4*>(src)[i];
+    } else {
+      for (int i = t; i < H; i += 256) h[i] = src[i];
+    }
+    if (t == 0) {
+      dyn[0] = (uint32_t)pos;
+      dyn[1] = (uint32_t)pos + 1u;
+    }
+    return;
+  }
+  // compile-time table index (the argument block stays in kernarg memory)
+#pragma unroll
+  for (int k = 0; k < Q4_TOKEN_MAX_TABLES; ++k) {
+    if (k == (int)blockIdx.x - 1 && k < tabs.count) {
+      const int hd = tabs.hd[k];
+      const long o = (long)pos * hd;
+      for (int i = t; i < hd; i += 256) {
+        tabs.cos_out[k][i] = tabs.cos_tab[k][o + i];
+        tabs.sin_out[k][i] = tabs.sin_tab[k][o + i];
+      }
+    }
+  }
+}
+
 }  // namespace q4
 
 using namespace q4;
@@ -1046,6 +1100,33 @@ int q4_pre_prepkv(const void* k, const void* v, int kv_dtype, int ld, const floa
     hipLaunchKernelGGL(pre_prepkv_kernel<Q4_DT_F32>, dim3(nkv, M), dim3(ATT_THREADS), 0, as_stream(stream), k, v, ld,
                        knw, cosM, sinM, kc, vc, hd, stride, window, M, dyn);
   Q4_LAUNCHED("pre_prepkv");
+  return Q4_OK;
+}
+
+
+int q4_token_inputs(const int32_t* step, const float* emb, int vocab, int H, float* h, uint32_t* dyn, int ntab,
+                    const float* const* cos_tab, const float* const* sin_tab, const int* hd, int max_pos,
+                    float* const* cos_out, float* const* sin_out, void* stream) {
+  clear_error();
+  Q4_ARG(step && emb && h && dyn, "null pointer");
+  Q4_ARG(vocab > 0 && H > 0 && max_pos > 0, "bad sizes vocab=%d H=%d max_pos=%d", vocab, H, max_pos);
+  Q4_ARG(ntab >= 0 && ntab <= Q4_TOKEN_MAX_TABLES, "at most %d RoPE tables (got %d)", Q4_TOKEN_MAX_TABLES, ntab);
+  Q4_ARG((H & 3) != 0 || (((uintptr_t)emb | (uintptr_t)h) & 15) == 0, "emb and h must be 16-byte aligned");
+  TokTabs tabs{};
+  tabs.count = ntab;
+  for (int k = 0; k < ntab; ++k) {
+    Q4_ARG(cos_tab && sin_tab && hd && cos_out && sin_out, "null table arrays");
+    Q4_ARG(cos_tab[k] && sin_tab[k] && cos_out[k] && sin_out[k], "null pointer in RoPE table %d", k);
+    Q4_ARG(hd[k] > 0, "bad head dim %d of RoPE table %d", hd[k], k);
+    tabs.cos_tab[k] = cos_tab[k];
+    tabs.sin_tab[k] = sin_tab[k];
+    tabs.cos_out[k] = cos_out[k];
+    tabs.sin_out[k] = sin_out[k];
+    tabs.hd[k] = hd[k];
+  }
+  hipLaunchKernelGGL(token_inputs_kernel, dim3(1 + ntab), dim3(256), 0, as_stream(stream), step, emb, vocab, H, h, dyn,
+                     max_pos, tabs);
+  Q4_LAUNCHED("token_inputs");
   return Q4_OK;
 }
 

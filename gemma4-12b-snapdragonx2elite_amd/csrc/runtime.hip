@@ -159,7 +159,9 @@ int q4_stream_wait(void* stream, int timeout_ms) {
       set_error("stream wait timed out after %d ms", timeout_ms);
       return Q4_ERR_TIMEOUT;
     }
-    std::this_thread::sleep_for(std::chrono::microseconds(50));
+    // yield rather than sleep: a sleep rounds up to the kernel's timer slack
+    // (~50 us), which a decode token (a few ms) would pay on every wait
+    std::this_thread::yield();
   }
 }
 

@@ -913,6 +913,48 @@ def pre_attn(q, qnw, cosM, sinM, kc, vc, out=None, *, M: int, ldq: int, nH: int,
     return out
 
 
+TOKEN_MAX_TABLES = 4
+
+
+def token_inputs(step: torch.Tensor, emb: torch.Tensor, h: torch.Tensor, dyn: torch.Tensor, tables=(), *,
+                 vocab: int, H: int, max_pos: int, stream=None) -> None:
+    """The per-token inputs of a decode graph from (tid, pos) = ``step[0:2]``
+    (int32; pinned host memory rewritten by the host before each launch, or
+    device memory), read when the launch runs (q4_token_inputs): ``h`` =
+    the fp32 embedding row ``emb[tid]`` (``emb`` [vocab, H]), ``dyn[0:2]`` =
+    (pos, pos + 1), and for each ``(cos_tab, sin_tab, hd, cos_out, sin_out)``
+    of ``tables`` the fp32 rows ``cos_tab[pos]``, ``sin_tab[pos]`` (tables
+    [max_pos, hd]) into the outputs."""
+    if step.dtype != torch.int32 or step.numel() < 2:
+        raise ValueError("step must hold two int32 values (tid, pos)")
+    if not (step.is_cuda or step.is_pinned()) or not step.is_contiguous():
+        raise ValueError("step must be contiguous device memory or pinned host memory")
+    if emb.dtype != torch.float32 or h.dtype != torch.float32:
+        raise ValueError("emb and h are fp32")
+    _need(emb, vocab * H * 4, "emb")
+    _need(h, H * 4, "h")
+    _need(dyn, 8, "dyn")
+    n = len(tables)
+    if n > TOKEN_MAX_TABLES:
+        raise ValueError(f"at most {TOKEN_MAX_TABLES} RoPE tables")
+    ptrs = {k: (C.c_void_p * max(1, n))() for k in ("ct", "st", "co", "so")}
+    hds = (C.c_int * max(1, n))()
+    for i, (ct, st, hd, co, so) in enumerate(tables):
+        for t in (ct, st, co, so):
+            if t.dtype != torch.float32:
+                raise ValueError("RoPE tables and rows are fp32")
+        _need(ct, max_pos * hd * 4, "cos table")
+        _need(st, max_pos * hd * 4, "sin table")
+        _need(co, hd * 4, "cos row")
+        _need(so, hd * 4, "sin row")
+        ptrs["ct"][i], ptrs["st"][i] = _p(ct).value, _p(st).value
+        ptrs["co"][i], ptrs["so"][i] = _p(co).value, _p(so).value
+        hds[i] = int(hd)
+    vp = lambda a: C.cast(a, C.c_void_p)  # noqa: E731
+    call("q4_token_inputs", C.c_void_p(step.data_ptr()), _p(emb), vocab, H, _p(h), _p(dyn), n, vp(ptrs["ct"]),
+         vp(ptrs["st"]), vp(hds), max_pos, vp(ptrs["co"]), vp(ptrs["so"]), _stream(stream))
+
+
 def stream_wait(stream=None, timeout_ms: int = 0, label: str = "") -> None:
     """Bounded wait; raises RuntimeError('GPU fence TIMEOUT after <ms>ms at [label]') on expiry,
     the message the reference's fence wait raises (src/vk_engine.py:299-302)."""

@@ -42,6 +42,7 @@ decode scales, ``PREFILL_I8=1`` the W8A8 prefill GEMM,
 from __future__ import annotations
 
 import os
+import weakref
 from typing import NamedTuple
 
 import numpy as np
@@ -412,15 +413,20 @@ _INTERLEAVED: dict = {}
 def _interleaved(wg, sg, wu, su, N: int, K: int):
     """The gate/up matrices interleaved row by row (:func:`ops.interleave_rows`),
     made once per set of source arrays: the decode gated GEMV and the prefill
-    gated GEMM share it when they read the same scale array. The entry keeps
-    the sources alive, so their addresses identify them for the process."""
+    gated GEMM share it when they read the same scale array. KEEP owns the
+    copy; the cache holds weak references only, and an entry counts only
+    while its sources and its copy are all alive (so a reused address never
+    returns a stale copy, and clearing KEEP frees the copies)."""
     key = (wg.data_ptr(), sg.data_ptr(), wu.data_ptr(), su.data_ptr(), N, K)
     hit = _INTERLEAVED.get(key)
-    if hit is None:
-        wo, so = ops.interleave_rows(wg, sg, wu, su, N, K)
-        KEEP.extend([wo, so])
-        hit = _INTERLEAVED[key] = (wo, so, (wg, sg, wu, su))
-    return hit[0], hit[1]
+    if hit is not None:
+        refs = [r() for r in hit]
+        if all(t is not None for t in refs) and all(a is b for a, b in zip(refs[2:], (wg, sg, wu, su))):
+            return refs[0], refs[1]
+    wo, so = ops.interleave_rows(wg, sg, wu, su, N, K)
+    KEEP.extend([wo, so])
+    _INTERLEAVED[key] = tuple(weakref.ref(t) for t in (wo, so, wg, sg, wu, su))
+    return wo, so
 
 
 def gate_up_ds(qg, qu, inbuf: Buf, actbuf: Buf, x_dtype=torch.float32, act_dtype=torch.float32) -> OpDesc | None:
@@ -760,7 +766,37 @@ def record(body) -> ops.Graph:
     return g
 
 
-def record_decode(layers, d_fin: OpDesc, d_lm: GemvDesc, fuse: bool = True, fuse_gemv: bool = True) -> ops.Graph:
+def token_inputs_ds(step: torch.Tensor, emb: Buf, h: Buf, dyn: Buf, tables=(), *, vocab: int, H: int,
+                    max_pos: int) -> OpDesc:
+    """The host writes of the reference's forward() (src/vk_engine.py:312-314:
+    ``B["h"].write(EMB[tid])``, the DYN position words, ``set_rope(pos)``) as
+    the first launch of a decode graph (:func:`ops.token_inputs`): ``step``
+    is a pinned int32 host tensor of (tid, pos) that :func:`forward` fills
+    before each launch; ``emb`` holds the pre-scaled fp32 embedding rows
+    [vocab, H] in device memory; ``tables`` = ``[(cos_tab, sin_tab, hd,
+    cosb, sinb)]``, per layer type, fp32 RoPE rows [max_pos, hd] (Buf) and
+    the row buffers the layers read."""
+    tabs = [(_f32v(ct, max_pos * hd), _f32v(st, max_pos * hd), hd, _f32v(co, hd), _f32v(so, hd))
+            for ct, st, hd, co, so in tables]
+    return OpDesc(ops.token_inputs, (step, _f32v(emb, vocab * H), _f32v(h, H), dyn.view(torch.int32, 4), tabs),
+                  dict(vocab=vocab, H=H, max_pos=max_pos))
+
+
+def forward(g: ops.Graph, step: torch.Tensor, tid: int, pos: int, *, vocab: int, max_pos: int, label: str = "",
+            timeout_ms: int | None = None) -> None:
+    """One decode token (src/vk_engine.py:312-319) through a graph recorded
+    with a :func:`token_inputs_ds` head: (tid, pos) into the pinned step
+    buffer (no device synchronization), one graph launch, one bounded wait.
+    The logits are in the graph's lm_head output buffer afterwards."""
+    if not (0 <= tid < vocab and 0 <= pos < max_pos):
+        raise ValueError(f"token {tid} or position {pos} out of range (vocab {vocab}, max_pos {max_pos})")
+    step[0] = tid
+    step[1] = pos
+    submit(g, label or f"decode pos={pos}", timeout_ms)
+
+
+def record_decode(layers, d_fin: OpDesc, d_lm: GemvDesc, fuse: bool = True, fuse_gemv: bool = True,
+                  d_tok: OpDesc | None = None) -> ops.Graph:
     """Record one decode token in the reference's dispatch order
     (src/vk_engine.py:274-287): per layer norm, q/k/v (one batched launch),
     prepkv, attention, o, normadd, norm, gate/up (one launch), gelumul,
@@ -779,8 +815,10 @@ def record_decode(layers, d_fin: OpDesc, d_lm: GemvDesc, fuse: bool = True, fuse
     per layer, same arithmetic. With ``fuse_gemv`` too, each such fused
     norm with an fp16 output runs inside the GEMV launch that reads it
     (q/k/v, gate/up; :func:`ops.gemv_batch_normadd`, :func:`ops.gemv_normadd`),
-    two launches fewer per layer."""
-    seq = []
+    two launches fewer per layer. ``d_tok`` (:func:`token_inputs_ds`), when
+    given, is the graph's first launch: the token's embedding row, position
+    and RoPE rows come from the step buffer that :func:`forward` writes."""
+    seq = [d_tok] if d_tok is not None else []
     for L in layers:
         seq += [L["d_in"], ("gemvs", [L["d_q"], L["d_k"]] + ([L["d_v"]] if L.get("d_v") is not None else [])),
                 L["d_prep"], L["d_attn"], ("gemvs", [L["d_o"]]), L["d_na"], L["d_pfn"],

@@ -442,6 +442,21 @@ int q4_attn(const float* qkv, const float* qnw, const float* cosb, const float* 
             int hd, int stride, int window, int qoff, int grp, const uint32_t* dyn, void* ws,
             size_t ws_bytes, void* stream);
 
+/* Per-token inputs at the head of a recorded decode graph, from (tid, pos) =
+ * step[0..1] read on the device when the graph runs (step: pinned host memory
+ * the host rewrites before each launch, read with system-scope loads, or
+ * device memory): h[0..H) = emb[tid*H ..] (the pre-scaled fp32 embedding
+ * rows [vocab][H]), dyn[0] = pos, dyn[1] = pos + 1, and for each of ntab
+ * RoPE tables cos_out[t][0..hd[t]) = cos_tab[t][pos*hd[t] ..] (rows
+ * [max_pos][hd[t]]), sin likewise. Replaces the host writes of the
+ * reference's forward() (src/vk_engine.py:312-314: EMB row, DYN, set_rope),
+ * so a token is one graph launch and one bounded wait. Values out of range
+ * are clamped on the device (callers check tid < vocab, pos < max_pos). */
+#define Q4_TOKEN_MAX_TABLES 4
+int q4_token_inputs(const int32_t* step, const float* emb, int vocab, int H, float* h, uint32_t* dyn, int ntab,
+                    const float* const* cos_tab, const float* const* sin_tab, const int* hd, int max_pos,
+                    float* const* cos_out, float* const* sin_out, void* stream);
+
 /* q4_prepkv and q4_attn of one layer as one pass (two launches instead of
  * three): the workgroups of the key split that holds this token's slot form
  * its K (k-norm with knw, RoPE) and V (v-norm; read at koff when keqv),

@@ -18,6 +18,7 @@ import torch
 
 from oracle import decode_ops_oracle as D
 from oracle import q4_oracle as O
+from tests.helpers import to_np
 
 pytestmark = pytest.mark.gpu
 
@@ -45,6 +46,49 @@ def test_decode_token_through_the_engine_mirror(g4, gpu, fuse, half, gated, fg):
     _token_steps(gpu, fuse, half, gated, fg)
 
 
+@pytest.mark.parametrize("fuse,half,gated,fg", [(True, True, True, True), (False, False, False, False)])
+def test_decode_token_forward_with_device_inputs(g4, gpu, fuse, half, gated, fg):
+    """forward(): the token id and position go into a pinned step buffer and
+    the graph's first launch gathers the embedding row, the DYN words and
+    both layer types' RoPE rows on the device (src/vk_engine.py:312-314 done
+    in the graph): one launch and one bounded wait per token, same oracle
+    tolerance over 20 tokens of random ids."""
+    _token_steps(gpu, fuse, half, gated, fg, device_inputs=True)
+
+
+def test_token_inputs_gather_and_clamp(g4, gpu):
+    """q4_token_inputs alone, step in pinned host memory and in device memory:
+    h, DYN and every table's cos/sin rows are the selected rows bit for bit,
+    the host's later rewrite of the pinned step is what the next launch
+    reads, and out-of-range values written past forward()'s check are
+    clamped to the last row / position 0 (nothing is read outside the
+    tables)."""
+    rng = np.random.default_rng(3)
+    vocab, Hh, max_pos = 300, 260, 50
+    emb = torch.from_numpy(rng.standard_normal((vocab, Hh)).astype(np.float32)).cuda()
+    tabs = []
+    for hd in (64, 128):
+        ct = torch.from_numpy(rng.standard_normal((max_pos, hd)).astype(np.float32)).cuda()
+        st = torch.from_numpy(rng.standard_normal((max_pos, hd)).astype(np.float32)).cuda()
+        tabs.append((ct, st, hd, torch.empty(hd, device="cuda"), torch.empty(hd, device="cuda")))
+    h = torch.empty(Hh, device="cuda")
+    dyn = torch.zeros(4, dtype=torch.int32, device="cuda")
+    for pinned in (True, False):
+        step = torch.zeros(2, dtype=torch.int32, pin_memory=True) if pinned else torch.zeros(2, dtype=torch.int32,
+                                                                                              device="cuda")
+        for tid, pos, want_t, want_p in [(7, 3, 7, 3), (299, 49, 299, 49), (0, 0, 0, 0), (305, -3, 299, 0)]:
+            if pinned:
+                step[0], step[1] = tid, pos
+            else:
+                step.copy_(torch.tensor([tid, pos], dtype=torch.int32))
+            gpu.token_inputs(step, emb, h, dyn, tabs, vocab=vocab, H=Hh, max_pos=max_pos)
+            torch.cuda.synchronize()
+            assert (to_np(h) == to_np(emb[want_t])).all()
+            assert to_np(dyn)[:2].tolist() == [want_p, want_p + 1]
+            for ct, st, hd, co, so in tabs:
+                assert (to_np(co) == to_np(ct[want_p])).all() and (to_np(so) == to_np(st[want_p])).all()
+
+
 @pytest.mark.parametrize("gated", [False, True])
 def test_decode_token_lm_head_keeps_its_norm_launch(g4, gpu, gated, monkeypatch):
     """The real model's case: lm_head is too tall for a norm-fused launch,
@@ -57,7 +101,7 @@ def test_decode_token_lm_head_keeps_its_norm_launch(g4, gpu, gated, monkeypatch)
     _token_steps(gpu, True, True, gated, True, V=2048, lm_fused=False)
 
 
-def _token_steps(gpu, fuse, half, gated, fg, V=V, lm_fused=True):
+def _token_steps(gpu, fuse, half, gated, fg, V=V, lm_fused=True, device_inputs=False):
     E = importlib.import_module("g4mi.vk_engine")
     xdt = torch.float16 if half else torch.float32
     rx = (lambda v: np.asarray(v).astype(np.float16).astype(np.float64)) if half else (lambda v: v)
@@ -123,7 +167,15 @@ def _token_steps(gpu, fuse, half, gated, fg, V=V, lm_fused=True):
     finw = f32(rng.random(H) + 0.5)
     d_fin = E.normbg(B["h"], wbuf(finw), B["normed_f"], DUH, out_dtype=xdt)
     d_lm = E.gemv_ds(lm[:2], B["normed_f"], B["logits"], 0, x_dtype=xdt)
-    graph = E.record_decode(layers, d_fin, d_lm, fuse=fuse, fuse_gemv=fg)
+    d_tok = step = EMB = None
+    VOC, MAXP = 512, 64
+    if device_inputs:  # embedding rows and RoPE tables on the device, (tid, pos) in pinned host memory
+        EMB = f32(rng.standard_normal((VOC, H)))
+        step = torch.zeros(2, dtype=torch.int32, pin_memory=True)
+        rope = {hd: [wbuf(np.stack([_rope(p, hd)[i] for p in range(MAXP)])) for i in (0, 1)] for hd in (64, 128)}
+        d_tok = E.token_inputs_ds(step, wbuf(EMB), B["h"], DYN, [(rope[hd][0], rope[hd][1], hd, cosb[hd], sinb[hd])
+                                                                 for hd in (64, 128)], vocab=VOC, H=H, max_pos=MAXP)
+    graph = E.record_decode(layers, d_fin, d_lm, fuse=fuse, fuse_gemv=fg, d_tok=d_tok)
     n_nx = sum(1 for op in graph.seq if (isinstance(op, tuple) and op[0] == "gemvs_nx")
                or getattr(op, "fn", None) is gpu.gemv_normadd)
     # per layer: the gate/up GEMV(s) and the next layer's q/k/v or (last layer) the 1024-row lm_head
@@ -134,14 +186,19 @@ def _token_steps(gpu, fuse, half, gated, fg, V=V, lm_fused=True):
 
     gv = lambda qs, x: O.gemv_ref(qs[0], qs[1], x).astype(np.float64)
     for pos in range(20):
-        emb = f32(rng.standard_normal(H))
-        B["h"].write(emb)
-        DYN.write(np.array([pos, pos + 1, 0, 0], np.uint32))
         tabs = {hd: _rope(pos, hd) for hd in (64, 128)}
-        for hd, (c, s) in tabs.items():
-            cosb[hd].write(c)
-            sinb[hd].write(s)
-        E.submit(graph, label=f"decode pos={pos}", timeout_ms=20000)
+        if device_inputs:
+            tid = int(rng.integers(0, VOC))
+            emb = EMB[tid]
+            E.forward(graph, step, tid, pos, vocab=VOC, max_pos=MAXP, timeout_ms=20000)
+        else:
+            emb = f32(rng.standard_normal(H))
+            B["h"].write(emb)
+            DYN.write(np.array([pos, pos + 1, 0, 0], np.uint32))
+            for hd, (c, s) in tabs.items():
+                cosb[hd].write(c)
+                sinb[hd].write(s)
+            E.submit(graph, label=f"decode pos={pos}", timeout_ms=20000)
         logits = np.frombuffer(B["logits"].read(V * 4), np.float32)
 
         h = emb.astype(np.float64)

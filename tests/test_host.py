@@ -192,3 +192,16 @@ def test_prefill_gemm_fusions_pair_gemms_with_their_consumers(g4, monkeypatch):
         prep2 = E.OpDesc(ops.pre_prepkv, (Kp[nq:], Kp[nq:]) + tabs,
                          dict(M=MC, ld=N, nkv=nkv, hd=hd, stride=64, window=32, dyn=dyn))
         assert len(E._fuse_gemm_prepkv([gmm(N, QKV), prep2])) == 2
+
+
+def test_forward_checks_token_and_position_before_any_launch(g4):
+    """forward() refuses a token id or position outside the tables it was
+    recorded with before touching the step buffer or the GPU."""
+    import torch
+
+    E = importlib.import_module("g4mi.vk_engine")
+    step = torch.zeros(2, dtype=torch.int32)
+    for tid, pos in [(10, 0), (-1, 0), (0, 10), (0, -1)]:
+        with pytest.raises(ValueError, match="out of range"):
+            E.forward(None, step, tid, pos, vocab=10, max_pos=10)
+    assert step.tolist() == [0, 0]
