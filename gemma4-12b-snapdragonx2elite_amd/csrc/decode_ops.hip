@@ -472,6 +472,14 @@ __device__ inline HalfVec<E> ld_halves(const uint16_t* p) {
   return r;
 }
 
+// The token position dyn[0] as a vector load, made uniform afterwards: it
+// then lands in order with the kernel's other vector loads. As a scalar
+// load it shares lgkmcnt with the kernel-argument loads issued after it,
+// and their wait would put its round trip before every later load.
+__device__ inline uint32_t load_pos(const uint32_t* dyn) {
+  return __builtin_amdgcn_readfirstlane(__hip_atomic_load(dyn, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT));
+}
+
 // Decode attention, split along the keys (vk/attn.comp:18-53,
 // flash-decoding). Workgroup (g, s): head group g = hpw query heads of one
 // KV head (they share that KV head's rows, so the rows are read once for all
@@ -520,7 +528,26 @@ attn_split_kernel(const float* __restrict__ qkv, const float* __restrict__ qnw, 
   const int kk = lane >> 3, c8 = lane & 7;
   const int key = KPW * wave + kk;  // this lane's K row within the split
 
-  // (1) every global load of the split
+  // (1) every global load of the split, in the order their data is used:
+  //     the position, the row-layout vectors of step (2), then the K and V
+  //     rows, so that step (2) runs while the cache rows are still in
+  //     flight. A split past the current length runs through with every key
+  //     masked (n <= 0) instead of leaving early: a branch on the position
+  //     here lets the compiler sink the vector loads below it, behind the
+  //     position's round trip.
+  const uint32_t pos = load_pos(dyn);
+  float q[ATT_HPW][EPL], wq[EPL], cr[EPL], sr[EPL], kr[EPL], vr[EPL], wk[EPL];
+#pragma unroll
+  for (int h = 0; h < ATT_HPW; ++h)
+    if (h < hpw) ld_row<EPL>(qkv + qoff + (h0 + h) * HD, q[h]);
+  ld_row<EPL>(qnw, wq);
+  ld_row<EPL>(cs, cr);
+  ld_row<EPL>(sn, sr);
+  if constexpr (PREP) {
+    ld_row<EPL>(qkv + koff + kvh * HD, kr);
+    ld_row<EPL>(qkv + voff + kvh * HD, vr);
+    ld_row<EPL>(knw, wk);
+  }
   v4u ku[EPL];
   {
     const int j = min(j0 + key, stride - 1);
@@ -534,25 +561,8 @@ attn_split_kernel(const float* __restrict__ qkv, const float* __restrict__ qnw, 
     const int j = min(j0 + KPW * wave + k, stride - 1);
     vv[k] = ld_halves<EPL>(vc + kv0 + (long)j * HD + EPL * lane);
   }
-  float q[ATT_HPW][EPL], wq[EPL], cr[EPL], sr[EPL], kr[EPL], vr[EPL], wk[EPL];
-#pragma unroll
-  for (int h = 0; h < ATT_HPW; ++h)
-    if (h < hpw) ld_row<EPL>(qkv + qoff + (h0 + h) * HD, q[h]);
-  ld_row<EPL>(qnw, wq);
-  ld_row<EPL>(cs, cr);
-  ld_row<EPL>(sn, sr);
-  if constexpr (PREP) {
-    ld_row<EPL>(qkv + koff + kvh * HD, kr);
-    ld_row<EPL>(qkv + voff + kvh * HD, vr);
-    ld_row<EPL>(knw, wk);
-  }
-  const uint32_t pos = dyn[0];
   const int T = att_len(pos, window, stride);
-  if (j0 >= T) {  // past the current length: the merge reads only the live splits
-    vmwait<0>();   // (the loads above land before the wave ends)
-    return;
-  }
-  const int n = min(ATT_KCH, T - j0);
+  const int n = min(ATT_KCH, T - j0);  // <= 0 past the current length: the merge reads only the live splits
   const int slot = kv_slot(pos, window);
   const bool fresh_split = PREP && slot < stride && slot >= j0 && slot < j0 + n;  // workgroup-uniform
   const int kslot = fresh_split ? slot - j0 : -1;
@@ -646,12 +656,16 @@ attn_split_kernel(const float* __restrict__ qkv, const float* __restrict__ qnw, 
   }
 
   // (5) unnormalised p V of every head from the same V registers; the waves
-  //     meet in LDS
+  //     meet in LDS. Rows past the length are taken as zero (their p is
+  //     zero, and a never-written cache row may hold a NaN).
   float vf[KPW][EPL];
 #pragma unroll
   for (int k = 0; k < KPW; ++k)
 #pragma unroll
-    for (int e = 0; e < EPL; ++e) vf[k][e] = (PREP && KPW * wave + k == kslot) ? vnew[e] : h2f(vv[k].h[e]);
+    for (int e = 0; e < EPL; ++e)
+      vf[k][e] = KPW * wave + k >= n                    ? 0.0f
+                 : (PREP && KPW * wave + k == kslot) ? vnew[e]
+                                                     : h2f(vv[k].h[e]);
 #pragma unroll
   for (int h = 0; h < ATT_HPW; ++h) {
     if (h >= hpw) break;
@@ -708,7 +722,7 @@ __global__ void __launch_bounds__(64) attn_merge_kernel(const float* __restrict_
   fetch(0, nsplit - 1);
   const int c_t = min(t, nsplit - 1);
   const float m_t = w[(long)c_t * (HD + 2)], l_t = w[(long)c_t * (HD + 2) + 1];
-  const int T = att_len(dyn[0], window, stride);
+  const int T = att_len(load_pos(dyn), window, stride);
   const int ns = (T + ATT_KCH - 1) / ATT_KCH;
   float M = t < ns ? m_t : -INFINITY;
   for (int c = t + 64; c < ns; c += 64) M = fmaxf(M, w[(long)c * (HD + 2)]);

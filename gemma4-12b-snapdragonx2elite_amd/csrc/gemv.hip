@@ -1009,6 +1009,21 @@ static int rows_per_group(int NP) {
   return R;
 }
 
+// Rows per workgroup of a fused-norm launch: every workgroup forms the whole
+// x from the normadd operands (16 bytes per element, 61 KB at K = 3840, read
+// from L2), so the launch takes the fewest workgroups that still give about
+// one per CU: the largest R with NP / R >= GEMV_MIN_WGS. Measured in the
+// decode token's graph (the q/k/v batch, 8192 rows: 256 groups of 32 rows
+// instead of 512 of 16): token 2.253 -> 2.216 ms; gate/up (30720 rows)
+// keeps 64 either way. The Q4_TUNE_GEMV_ROWS override replaces R here too.
+static int rows_per_group_nx(int NP) {
+  const int v = tune_value(Q4_TUNE_GEMV_ROWS);
+  if (v == 8 || v == 16 || v == 32 || v == 64) return v;
+  for (int c : {64, 32, 16})
+    if (NP / c >= GEMV_MIN_WGS) return c;
+  return 8;
+}
+
 // Units in flight per lane for a grid of wgs workgroups with nb blocks each:
 // 8 while the whole grid keeps at most GEMV_INFLIGHT_UNITS in flight (8 MB
 // of weights, what HBM needs at ~1.1 us of loaded latency), else 4; 4 when
@@ -1199,6 +1214,11 @@ static int gemv_launch(const void* x, int x_dtype, const uint32_t* wq, const voi
   Q4_ARG(((uintptr_t)wq & 15) == 0 && ((uintptr_t)x & 15) == 0, "wq and x must be 16-byte aligned");
   Q4_ARG(N <= (1 << 30) && (long)K <= (1L << 24), "GEMV too large");
   GemvPlan pl = plan(N, K, split, x_dtype);
+  if (nx && pl.split == 1) {
+    pl.R = rows_per_group_nx(pad_rows(N));
+    pl.U = units_in_flight(pl.nb_max, pl.R, pad_rows(N) / pl.R);
+    pl.lds = x_stage_lds(pl.nb_max, x_dtype, pl.R);
+  }
   Q4_ARG(pl.ws == 0 || (ws && ws_size >= pl.ws), "GEMV N=%d K=%d split=%d needs a %zu-byte workspace (got %zu)", N,
          K, pl.split, pl.ws, ws ? ws_size : (size_t)0);
   // row groups: NP / R of the plan, at most one per row (pair, when gated)
@@ -1392,7 +1412,7 @@ static int gemv_batch_launch(const void* x, int x_dtype, int K, int scale_fmt, i
     for (int i = 0; i < count; ++i)
       if (int e = nx_check_y(*nx, K, y[i], (size_t)N[i] * (y_dtype == Q4_DT_F16 ? 2 : 4))) return e;
   }
-  int R = rows_per_group((int)NP);
+  int R = nx ? rows_per_group_nx((int)NP) : rows_per_group((int)NP);
   // row groups per matrix: NP_i / R, or with a balanced plan 256 m groups
   // shared out in proportion to the rows (same rows per group everywhere)
   int gm[Q4_GEMV_MAX_BATCH];
