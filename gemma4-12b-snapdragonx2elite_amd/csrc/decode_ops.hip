@@ -31,7 +31,7 @@ namespace q4 {
 
 constexpr int NORM_THREADS = 1024;
 constexpr int ATT_THREADS = 256;
-constexpr int ATT_KCH = 32;       // keys per attention split (8 per wave)
+constexpr int ATT_KPW = 8;        // keys per wave of an attention split (one K row per 8 lanes)
 constexpr int ATT_HPW = 4;        // query heads per attention workgroup (at most)
 constexpr int ATT_MAX_HD = 512;   // head dims up to 512 (global layers)
 
@@ -483,8 +483,8 @@ __device__ inline uint32_t load_pos(const uint32_t* dyn) {
 // Decode attention, split along the keys (vk/attn.comp:18-53,
 // flash-decoding). Workgroup (g, s): head group g = hpw query heads of one
 // KV head (they share that KV head's rows, so the rows are read once for all
-// of them) and keys [ATT_KCH s, ATT_KCH (s + 1)) of the current length; wave
-// w takes 8 of those keys. Every global load is issued first, none of them
+// of them) and keys [KCH s, KCH (s + 1)) of the current length, KCH = 8 NW
+// for NW waves; wave w takes 8 of those keys. Every global load is issued first, none of them
 // waiting for the position: the wave's K rows (8 lanes per row, lane c8
 // reading 16-byte chunks c8, c8 + 8, ..: 128 contiguous bytes per row and
 // load), its V rows (one coalesced row per key, lane l owning elements
@@ -507,23 +507,24 @@ __device__ inline uint32_t load_pos(const uint32_t* dyn) {
 // prepkv_row_kernel), uses them for that key in place of the cache row, and
 // the first head group of each KV head writes them to the cache for the
 // next tokens; no other workgroup reads that row.
-template <int EPL, bool PREP>
-__global__ void __launch_bounds__(ATT_THREADS)
+template <int EPL, bool PREP, int NW>
+__global__ void __launch_bounds__(64 * NW)
 attn_split_kernel(const float* __restrict__ qkv, const float* __restrict__ qnw, const float* __restrict__ cs,
                   const float* __restrict__ sn, uint16_t* __restrict__ kc, uint16_t* __restrict__ vc, int stride,
                   int window, int qoff, int grp, int hpw, const uint32_t* __restrict__ dyn, float* __restrict__ part,
                   int nsplit, const float* __restrict__ knw, int koff, int voff) {
-  constexpr int HD = 64 * EPL, NW = ATT_THREADS / 64, KPW = ATT_KCH / NW;  // 8 keys per wave
+  constexpr int HD = 64 * EPL, KPW = ATT_KPW, KCH = KPW * NW, NT = 64 * NW;  // keys per split, threads
+  constexpr int KPL = KCH / 32;  // keys per lane in the softmax (32 lanes per head)
   constexpr int NR = PREP ? ATT_HPW + 1 : ATT_HPW;  // row-layout vectors handed to the K layout: q heads (, k)
-  static_assert(KPW == 8, "one K row per 8 lanes");
+  static_assert(KCH % 32 == 0, "whole softmax lanes");
   __shared__ __attribute__((aligned(16))) float rows[NW][NR][HD];
-  __shared__ float ps[ATT_HPW][ATT_KCH];
+  __shared__ float ps[ATT_HPW][KCH];
   __shared__ float accp[NW][ATT_HPW][HD];
   const int g = blockIdx.x, sp = blockIdx.y, t = threadIdx.x, lane = t & 63;
   const int wave = __builtin_amdgcn_readfirstlane(t >> 6);
   const int gpk = grp / hpw;  // head groups per KV head
   const int kvh = g / gpk, h0 = g * hpw;
-  const int j0 = sp * ATT_KCH;
+  const int j0 = sp * KCH;
   const long kv0 = (long)kvh * stride * HD;
   const int kk = lane >> 3, c8 = lane & 7;
   const int key = KPW * wave + kk;  // this lane's K row within the split
@@ -562,7 +563,7 @@ attn_split_kernel(const float* __restrict__ qkv, const float* __restrict__ qnw, 
     vv[k] = ld_halves<EPL>(vc + kv0 + (long)j * HD + EPL * lane);
   }
   const int T = att_len(pos, window, stride);
-  const int n = min(ATT_KCH, T - j0);  // <= 0 past the current length: the merge reads only the live splits
+  const int n = min(KCH, T - j0);  // <= 0 past the current length: the merge reads only the live splits
   const int slot = kv_slot(pos, window);
   const bool fresh_split = PREP && slot < stride && slot >= j0 && slot < j0 + n;  // workgroup-uniform
   const int kslot = fresh_split ? slot - j0 : -1;
@@ -635,21 +636,40 @@ attn_split_kernel(const float* __restrict__ qkv, const float* __restrict__ qnw, 
   __syncthreads();
 
   // (4) softmax of the split, two heads per wave pass (lanes 0-31, 32-63),
-  //     in every wave: m and l, and the p of this wave's keys by broadcast
+  //     in every wave: m and l, and the p of this wave's keys by broadcast.
+  //     Lane l of a half holds keys l, l + 32, ..; this wave's keys
+  //     KPW wave .. + KPW - 1 are all element (KPW wave) / 32 of lanes
+  //     (KPW wave) % 32 ...
   float pw[ATT_HPW][KPW], mh[ATT_HPW], lh[ATT_HPW];
+  const int we = (KPW * wave) / 32, wl = (KPW * wave) % 32;  // wave-uniform
 #pragma unroll
   for (int hb = 0; hb < ATT_HPW; hb += 2) {
     if (hb >= hpw) break;
     const int h = hb + (lane >> 5);
-    const float sc = h < hpw ? ps[h][lane & 31] : -INFINITY;
-    const float m = reduce32<true>(sc);
-    const float pj = sc != -INFINITY ? expf(sc - m) : 0.0f;
-    const float l = reduce32<false>(pj);
+    float sc[KPL];
+    float mx = -INFINITY;
+#pragma unroll
+    for (int i = 0; i < KPL; ++i) {
+      sc[i] = h < hpw ? ps[h][32 * i + (lane & 31)] : -INFINITY;
+      mx = fmaxf(mx, sc[i]);
+    }
+    const float m = reduce32<true>(mx);
+    float pj[KPL], ls = 0.0f;
+#pragma unroll
+    for (int i = 0; i < KPL; ++i) {
+      pj[i] = sc[i] != -INFINITY ? expf(sc[i] - m) : 0.0f;
+      ls += pj[i];
+    }
+    const float l = reduce32<false>(ls);
+    float pm = pj[0];  // element we of this lane (a wave-uniform choice)
+#pragma unroll
+    for (int i = 1; i < KPL; ++i)
+      if (we == i) pm = pj[i];
 #pragma unroll
     for (int u = 0; u < 2; ++u) {
 #pragma unroll
       for (int k = 0; k < KPW; ++k)
-        pw[hb + u][k] = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(pj), 32 * u + KPW * wave + k));
+        pw[hb + u][k] = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(pm), 32 * u + wl + k));
       mh[hb + u] = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(m), 32 * u));
       lh[hb + u] = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(l), 32 * u));
     }
@@ -680,10 +700,13 @@ attn_split_kernel(const float* __restrict__ qkv, const float* __restrict__ qnw, 
     for (int e = 0; e < EPL; ++e) accp[wave][h][EPL * lane + e] = a[e];
   }
   __syncthreads();
-  for (int i = t; i < hpw * HD; i += ATT_THREADS) {
+  for (int i = t; i < hpw * HD; i += NT) {
     const int h = i / HD, c = i % HD;
     float* o = part + ((long)(h0 + h) * nsplit + sp) * (HD + 2);
-    o[2 + c] = ((accp[0][h][c] + accp[1][h][c]) + accp[2][h][c]) + accp[3][h][c];
+    float v = accp[0][h][c];
+#pragma unroll
+    for (int w = 1; w < NW; ++w) v += accp[w][h][c];  // waves in order
+    o[2 + c] = v;
   }
   if (t == 0) {
 #pragma unroll
@@ -705,11 +728,11 @@ attn_split_kernel(const float* __restrict__ qkv, const float* __restrict__ qnw, 
 // its own LDS and sums the splits in order. Per head and dim the arithmetic
 // and its order are the same whichever wave does it. ml: nsplit floats of
 // dynamic shared memory. out fp32 or fp16.
-template <int YT, int EPL>
+template <int YT, int EPL, int MB>
 __global__ void __launch_bounds__(64) attn_merge_kernel(const float* __restrict__ part, void* __restrict__ out,
-                                                        int nsplit, int stride, int window,
+                                                        int nsplit, int kch, int stride, int window,
                                                         const uint32_t* __restrict__ dyn) {
-  constexpr int HD = 64 * EPL, MB = 32;
+  constexpr int HD = 64 * EPL;
   extern __shared__ float ml[];
   const int h = blockIdx.x, t = threadIdx.x, d = blockIdx.y * 64 + t;
   const float* w = part + (long)h * nsplit * (HD + 2);
@@ -723,7 +746,7 @@ __global__ void __launch_bounds__(64) attn_merge_kernel(const float* __restrict_
   const int c_t = min(t, nsplit - 1);
   const float m_t = w[(long)c_t * (HD + 2)], l_t = w[(long)c_t * (HD + 2) + 1];
   const int T = att_len(load_pos(dyn), window, stride);
-  const int ns = (T + ATT_KCH - 1) / ATT_KCH;
+  const int ns = (T + kch - 1) / kch;
   float M = t < ns ? m_t : -INFINITY;
   for (int c = t + 64; c < ns; c += 64) M = fmaxf(M, w[(long)c * (HD + 2)]);
   M = reduce64<true>(M);
@@ -748,7 +771,14 @@ __global__ void __launch_bounds__(64) attn_merge_kernel(const float* __restrict_
   else reinterpret_cast<float*>(out)[h * HD + d] = v;
 }
 
-static int attn_splits(int stride) { return ceil_div(stride, ATT_KCH); }
+// Waves per attention split workgroup (8 keys each): 8 (64-key splits, 512
+// threads) up to hd 256, 4 (32 keys) at hd 512, whose per-wave LDS rows are
+// twice as long. Measured in the decode token's graph (hd 256, 1024 keys, 8
+// KV heads of 2 query heads): 64-key splits 2.190 ms per token, 32-key 2.208
+// ms, 128-key (16 waves, 64 workgroups) 2.316 ms.
+static int attn_waves(int hd) { return hd <= 256 ? 8 : 4; }
+static int attn_kch(int hd) { return ATT_KPW * attn_waves(hd); }
+static int attn_splits(int stride, int hd) { return ceil_div(stride, attn_kch(hd)); }
 // query heads per attention workgroup: the largest of ATT_HPW, .., 2, 1 dividing grp
 static int attn_hpw(int grp) {
   int h = ATT_HPW;
@@ -911,7 +941,7 @@ int q4_prepkv(const float* qkv, const float* knw, const float* cosb, const float
 
 size_t q4_attn_workspace_bytes(int nH, int hd, int stride) {
   if (nH <= 0 || hd <= 0 || stride <= 0) return 0;
-  return (size_t)nH * attn_splits(stride) * (hd + 2) * sizeof(float);
+  return (size_t)nH * attn_splits(stride, hd) * (hd + 2) * sizeof(float);
 }
 
 static int attn_launch(const float* qkv, const float* qnw, const float* cosb, const float* sinb, uint16_t* kc,
@@ -930,26 +960,31 @@ static int attn_launch(const float* qkv, const float* qnw, const float* cosb, co
          "qkv, qnw, cos, sin and knw must be 16-byte aligned and the q/k/v offsets multiples of 4 elements");
   const size_t need = q4_attn_workspace_bytes(nH, hd, stride);
   Q4_ARG(ws_bytes >= need, "attention workspace too small: %zu < %zu bytes", ws_bytes, need);
-  const int ns = attn_splits(stride), hpw = attn_hpw(grp);
+  const int ns = attn_splits(stride, hd), hpw = attn_hpw(grp), kch = attn_kch(hd);
   const size_t msh = (size_t)ns * sizeof(float);
   Q4_ARG(msh <= 64 * 1024, "cache depth %d needs %d attention splits (more than the merge stages)", stride, ns);
   hipStream_t st = as_stream(stream);
   float* part = reinterpret_cast<float*>(ws);
-  const dim3 grid(nH / hpw, ns), blk(ATT_THREADS);
+  const dim3 grid(nH / hpw, ns), blk(64 * attn_waves(hd));
   const bool prep = knw != nullptr, h16 = out_dtype == Q4_DT_F16;
-#define Q4_ATT(E, P)                                                                                               \
-  hipLaunchKernelGGL((attn_split_kernel<E, P>), grid, blk, 0, st, qkv, qnw, cosb, sinb, kc, vc, stride, window, \
+#define Q4_ATT(E, P, W)                                                                                               \
+  hipLaunchKernelGGL((attn_split_kernel<E, P, W>), grid, blk, 0, st, qkv, qnw, cosb, sinb, kc, vc, stride, window, \
                      qoff, grp, hpw, dyn, part, ns, knw, koff, voff)
-#define Q4_MRG(E)                                                                                                \
-  if (h16) hipLaunchKernelGGL((attn_merge_kernel<Q4_DT_F16, E>), dim3(nH, E), dim3(64), msh, st, part, out, ns, \
-                              stride, window, dyn);                                                             \
-  else hipLaunchKernelGGL((attn_merge_kernel<Q4_DT_F32, E>), dim3(nH, E), dim3(64), msh, st, part, out, ns,     \
-                          stride, window, dyn)
+  // the merge fetches its splits MB at a time: the smallest of 8, 16, 32 that covers them all, or 32
+#define Q4_MRG2(E, MB)                                                                                               \
+  if (h16) hipLaunchKernelGGL((attn_merge_kernel<Q4_DT_F16, E, MB>), dim3(nH, E), dim3(64), msh, st, part, out, ns, \
+                              kch, stride, window, dyn);                                                            \
+  else hipLaunchKernelGGL((attn_merge_kernel<Q4_DT_F32, E, MB>), dim3(nH, E), dim3(64), msh, st, part, out, ns,     \
+                          kch, stride, window, dyn)
+#define Q4_MRG(E)                  \
+  if (ns <= 8) { Q4_MRG2(E, 8); }  \
+  else if (ns <= 16) { Q4_MRG2(E, 16); } \
+  else { Q4_MRG2(E, 32); }
   switch (hd) {
-    case 64: if (prep) { Q4_ATT(1, true); } else { Q4_ATT(1, false); } break;
-    case 128: if (prep) { Q4_ATT(2, true); } else { Q4_ATT(2, false); } break;
-    case 256: if (prep) { Q4_ATT(4, true); } else { Q4_ATT(4, false); } break;
-    default: if (prep) { Q4_ATT(8, true); } else { Q4_ATT(8, false); } break;
+    case 64: if (prep) { Q4_ATT(1, true, 8); } else { Q4_ATT(1, false, 8); } break;
+    case 128: if (prep) { Q4_ATT(2, true, 8); } else { Q4_ATT(2, false, 8); } break;
+    case 256: if (prep) { Q4_ATT(4, true, 8); } else { Q4_ATT(4, false, 8); } break;
+    default: if (prep) { Q4_ATT(8, true, 4); } else { Q4_ATT(8, false, 4); } break;
   }
   Q4_LAUNCHED("attn_split");
   switch (hd) {
@@ -958,6 +993,7 @@ static int attn_launch(const float* qkv, const float* qnw, const float* cosb, co
     case 256: Q4_MRG(4); break;
     default: Q4_MRG(8); break;
   }
+#undef Q4_MRG2
 #undef Q4_MRG
 #undef Q4_ATT
   Q4_LAUNCHED("attn_merge");

@@ -150,8 +150,8 @@ def test_decode_op_argument_errors_without_gpu(g4):
     fake = C.c_void_p(256)  # never dereferenced: every call below fails its checks before any launch
     null = C.c_void_p(0)
     # per head and 32-key split: (max, sum, accumulator[hd])
-    assert lib.q4_attn_workspace_bytes(16, 256, 8192) == 16 * 256 * 258 * 4
-    assert lib.q4_attn_workspace_bytes(16, 512, 1000) == 16 * 32 * 514 * 4
+    assert lib.q4_attn_workspace_bytes(16, 256, 8192) == 16 * 128 * 258 * 4   # 64-key splits up to hd 256
+    assert lib.q4_attn_workspace_bytes(16, 512, 1000) == 16 * 32 * 514 * 4    # 32-key splits at hd 512
     assert lib.q4_attn_workspace_bytes(0, 256, 8) == 0
     st = lib.q4_attn(*[fake] * 7, 0, 16, 8, 100, 64, 0, 0, 2, fake, fake, 1 << 20, null)
     assert st == g4._lib.Q4_ERR_ARG and "64, 128, 256 or 512" in _err(g4)
