@@ -6,7 +6,8 @@
 // which runs one workgroup per (head, token) and walks the keys one scalar
 // dot product at a time; here the query rows of a KV head are tiled onto
 // MFMAs:
-//  * A workgroup (4 waves) owns 64 query rows of one KV head (row = token *
+//  * A workgroup (4 waves; 8 at hd 512, two per row group splitting the head
+//    dims, see PaGeom) owns 64 query rows of one KV head (row = token *
 //    grp + query head within the group, so the rows share their K and V)
 //    and one split of the cache slots (a multiple of 32 keys, long enough
 //    that the grid has about 256 workgroups: 128 keys for a 1024-slot ring
@@ -72,37 +73,48 @@ __device__ inline long pa_ws_index(int m, int h, int nH, int ks, int nsplit, int
 }
 
 // Tile geometry per head dim: KT keys per LDS tile and DS waves per row
-// group (each wave of a group computes the group's scores and accumulates
-// 1/DS of the output dims). hd 512 takes 16-key tiles so q (hi + lo), the
-// output accumulators (AGPRs) and the next tile's prefetch registers fit
-// without spills; one wave per row group: with two, both waves of a group
-// computed the same scores (137 -> 102 us for 128 tokens x 16 heads over
-// 4096 keys, MQA).
+// group, 4 row groups of 16 rows per workgroup. With DS = 2 (hd 512) the two
+// waves of a row group split the head dims: each holds q (hi + lo) for half
+// of them, computes the partial scores over that half, and the pair adds
+// the two halves through LDS (half 0 + half 1, the same bits in both
+// waves); each then accumulates its half of the output dims. So q, the
+// accumulators and the prefetch registers of a wave fit two waves per SIMD
+// without spills, and no score is computed twice (a pair that computed the
+// full scores in both waves took 137 us against 102 us for one wave per
+// row group, 128 tokens x 16 heads over 4096 keys, MQA). Measured in the
+// prefill chunk (the 8 global layers, kernel-only): 85.6 us with one wave
+// per row group, 77.8 us with the split pair; 32-key tiles with the pair
+// spill registers (87.6 us). Without the next tile's loads (timing only) the
+// pair takes 67 us: the rest is issue and the three barriers per tile.
 template <int HD>
 struct PaGeom {
   static constexpr int KT = HD >= 512 ? 16 : 32;
-  static constexpr int DS = 1;
-  static constexpr int ROWS = 16 * PA_WAVES / DS;  // query rows per workgroup
+  static constexpr int DS = HD >= 512 ? 2 : 1;
+  static constexpr int WAVES = PA_WAVES * DS;
+  static constexpr int THREADS = 64 * WAVES;
+  static constexpr int ROWS = 16 * PA_WAVES;  // query rows per workgroup
 };
 
 template <int HD, int QT>
-__global__ void __launch_bounds__(PA_THREADS)
+__global__ void __launch_bounds__(PaGeom<HD>::THREADS)
 pre_attn_kernel(const void* __restrict__ qin, int ldq, const float* __restrict__ qnw, const float* __restrict__ cosM,
                 const float* __restrict__ sinM, const uint16_t* __restrict__ kc, const uint16_t* __restrict__ vc,
                 int stride, int window, int grp, int nH, int M, const uint32_t* __restrict__ dyn,
                 float* __restrict__ ws, int nsplit, int ksl) {
-  constexpr int KT = PaGeom<HD>::KT, DS = PaGeom<HD>::DS, ROWS = PaGeom<HD>::ROWS;
+  constexpr int KT = PaGeom<HD>::KT, DS = PaGeom<HD>::DS, ROWS = PaGeom<HD>::ROWS, NT = PaGeom<HD>::THREADS;
   constexpr int NST = KT / 16;        // 16-key subtiles per tile
-  constexpr int NCH = HD / 32;        // 32-element chunks (QK k-steps)
+  constexpr int NCH = HD / 32;        // 32-element chunks
+  constexpr int NQC = NCH / DS;       // chunks of this wave's QK (its part of the head dims)
   constexpr int NDT = HD / 16 / DS;   // 16-element output tiles of this wave
   constexpr int CPR = HD / 8;         // 16-byte chunks per K/V row
   constexpr int KP = HD * 2 + 16;     // K tile row pitch (bytes)
   constexpr int VP = KT * 2 + 8;      // V^T tile row pitch (bytes)
   constexpr int KITEMS = KT * CPR, VITEMS = (KT / 2) * CPR;  // 16-byte K chunks, V key-pair chunks per tile
-  constexpr int KLD = (KITEMS + PA_THREADS - 1) / PA_THREADS, VLD = (VITEMS + PA_THREADS - 1) / PA_THREADS;
-  static_assert(NCH % 2 == 0, "head dim");
+  constexpr int KLD = (KITEMS + NT - 1) / NT, VLD = (VITEMS + NT - 1) / NT;
+  static_assert(NQC % 2 == 0, "head dim");
   __shared__ __attribute__((aligned(16))) uint8_t ksh[KT * KP];
   __shared__ __attribute__((aligned(16))) uint8_t vsh[HD * VP];
+  __shared__ v4f xs[DS > 1 ? PaGeom<HD>::WAVES : 1][NST][64];  // partial scores of each wave (DS > 1)
 
   const int kvh = blockIdx.x, ks = blockIdx.z;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, c = lane & 15, g = lane >> 4;
@@ -125,13 +137,13 @@ pre_attn_kernel(const void* __restrict__ qin, int ldq, const float* __restrict__
   auto load_tile = [&](int t0) {
 #pragma unroll
     for (int i = 0; i < KLD; ++i) {
-      const int q = min(tid + PA_THREADS * i, KITEMS - 1), key = q / CPR, ch = q % CPR;
+      const int q = min(tid + NT * i, KITEMS - 1), key = q / CPR, ch = q % CPR;
       const int slot = min(t0 + key, stride - 1);
       kr[i] = *reinterpret_cast<const v4u*>(kc + ((long)kvh * stride + slot) * HD + ch * 8);
     }
 #pragma unroll
     for (int i = 0; i < VLD; ++i) {
-      const int q = min(tid + PA_THREADS * i, VITEMS - 1), pr = q % (KT / 2), ch = q / (KT / 2);
+      const int q = min(tid + NT * i, VITEMS - 1), pr = q % (KT / 2), ch = q / (KT / 2);
       const int s0 = min(t0 + 2 * pr, stride - 1), s1 = min(t0 + 2 * pr + 1, stride - 1);
       va[i] = *reinterpret_cast<const v4u*>(vc + ((long)kvh * stride + s0) * HD + ch * 8);
       vb[i] = *reinterpret_cast<const v4u*>(vc + ((long)kvh * stride + s1) * HD + ch * 8);
@@ -140,12 +152,12 @@ pre_attn_kernel(const void* __restrict__ qin, int ldq, const float* __restrict__
   auto store_tile = [&]() {
 #pragma unroll
     for (int i = 0; i < KLD; ++i) {
-      const int q = tid + PA_THREADS * i, key = q / CPR, ch = q % CPR;
+      const int q = tid + NT * i, key = q / CPR, ch = q % CPR;
       if (q < KITEMS) *reinterpret_cast<v4u*>(ksh + key * KP + ch * 16) = kr[i];
     }
 #pragma unroll
     for (int i = 0; i < VLD; ++i) {
-      const int q = tid + PA_THREADS * i, pr = q % (KT / 2), ch = q / (KT / 2);
+      const int q = tid + NT * i, pr = q % (KT / 2), ch = q / (KT / 2);
       if (q >= VITEMS) continue;
 #pragma unroll
       for (int w = 0; w < 4; ++w) {
@@ -165,7 +177,7 @@ pre_attn_kernel(const void* __restrict__ qin, int ldq, const float* __restrict__
   const int h = kvh * grp + (live ? R % grp : 0);
   const uint32_t pos = p0 + (uint32_t)m;
   const int T = att_len(pos, window, stride);
-  v8h qh[NCH], ql[NCH];
+  v8h qh[NQC], ql[NQC];  // chunks dp NQC .. of the row
   {
     // the lane's 8 consecutive elements of each chunk come in 16-byte loads
     float qf[NCH][8];
@@ -205,14 +217,20 @@ pre_attn_kernel(const void* __restrict__ qin, int ldq, const float* __restrict__
         qf[j + NCH / 2][u] = rb;
       }
     }
+    // this wave's part of the head dims (a wave-uniform branch keeps the
+    // register indices static)
+    auto split = [&](int j0) {
 #pragma unroll
-    for (int j = 0; j < NCH; ++j)
+      for (int j = 0; j < NQC; ++j)
 #pragma unroll
-      for (int u = 0; u < 8; ++u) {
-        const _Float16 hi = (_Float16)qf[j][u];
-        qh[j][u] = hi;
-        ql[j][u] = (_Float16)(qf[j][u] - (float)hi);
-      }
+        for (int u = 0; u < 8; ++u) {
+          const _Float16 hi = (_Float16)qf[j0 + j][u];
+          qh[j][u] = hi;
+          ql[j][u] = (_Float16)(qf[j0 + j][u] - (float)hi);
+        }
+    };
+    if (DS == 1 || dp == 0) split(0);
+    else split(NQC);
   }
 
   v4f oacc[NDT];
@@ -233,19 +251,32 @@ pre_attn_kernel(const void* __restrict__ qin, int ldq, const float* __restrict__
     // one (uniform) division per tile
     const int rt = window > 0 ? (int)(((long)last - t0) % window) : 0;
     float sc[NST][4];
+    v4f sp[NST];
 #pragma unroll
     for (int st = 0; st < NST; ++st) {
       v4f s0 = v4f{0.0f, 0.0f, 0.0f, 0.0f}, s1 = s0, s2 = s0, s3 = s0;
+      const uint8_t* kr0 = ksh + (16 * st + c) * KP + (4 * dp * NQC + g) * 16;
 #pragma unroll
-      for (int j = 0; j < NCH; j += 2) {
-        const v8h a0 = *reinterpret_cast<const v8h*>(ksh + (16 * st + c) * KP + (4 * j + g) * 16);
-        const v8h a1 = *reinterpret_cast<const v8h*>(ksh + (16 * st + c) * KP + (4 * j + 4 + g) * 16);
+      for (int j = 0; j < NQC; j += 2) {
+        const v8h a0 = *reinterpret_cast<const v8h*>(kr0 + 4 * j * 16);
+        const v8h a1 = *reinterpret_cast<const v8h*>(kr0 + (4 * j + 4) * 16);
         s0 = __builtin_amdgcn_mfma_f32_16x16x32_f16(a0, qh[j], s0, 0, 0, 0);
         s1 = __builtin_amdgcn_mfma_f32_16x16x32_f16(a1, qh[j + 1], s1, 0, 0, 0);
         s2 = __builtin_amdgcn_mfma_f32_16x16x32_f16(a0, ql[j], s2, 0, 0, 0);
         s3 = __builtin_amdgcn_mfma_f32_16x16x32_f16(a1, ql[j + 1], s3, 0, 0, 0);
       }
-      const v4f s = (s0 + s1) + (s2 + s3);
+      sp[st] = (s0 + s1) + (s2 + s3);
+    }
+    if constexpr (DS > 1) {  // the pair's partial scores: half 0 + half 1, in both waves
+#pragma unroll
+      for (int st = 0; st < NST; ++st) xs[wave][st][lane] = sp[st];
+      __syncthreads();
+#pragma unroll
+      for (int st = 0; st < NST; ++st) sp[st] = xs[rg * DS][st][lane] + xs[rg * DS + 1][st][lane];
+    }
+#pragma unroll
+    for (int st = 0; st < NST; ++st) {
+      const v4f s = sp[st];
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
         const int i = 16 * st + 4 * g + e, slot = t0 + i;
@@ -435,13 +466,13 @@ int q4_pre_attn(const void* q, int q_dtype, int ldq, const float* qnw, const flo
   const dim3 grid(nkv, ceil_div(M * grp, pa_rows(hd)), ns);
   hipStream_t st = as_stream(stream);
   float* w = reinterpret_cast<float*>(ws);
-#define PA_LAUNCH(HD_)                                                                                            \
-  if (q_dtype == Q4_DT_F16)                                                                                       \
-    hipLaunchKernelGGL((pre_attn_kernel<HD_, Q4_DT_F16>), grid, dim3(PA_THREADS), 0, st, q, ldq, qnw, cosM, sinM, \
-                       kc, vc, stride, window, grp, nH, M, dyn, w, ns, ksl);                                          \
-  else                                                                                                            \
-    hipLaunchKernelGGL((pre_attn_kernel<HD_, Q4_DT_F32>), grid, dim3(PA_THREADS), 0, st, q, ldq, qnw, cosM, sinM, \
-                       kc, vc, stride, window, grp, nH, M, dyn, w, ns, ksl);
+#define PA_LAUNCH(HD_)                                                                                           \
+  if (q_dtype == Q4_DT_F16)                                                                                      \
+    hipLaunchKernelGGL((pre_attn_kernel<HD_, Q4_DT_F16>), grid, dim3(PaGeom<HD_>::THREADS), 0, st, q, ldq, qnw,  \
+                       cosM, sinM, kc, vc, stride, window, grp, nH, M, dyn, w, ns, ksl);                             \
+  else                                                                                                           \
+    hipLaunchKernelGGL((pre_attn_kernel<HD_, Q4_DT_F32>), grid, dim3(PaGeom<HD_>::THREADS), 0, st, q, ldq, qnw,  \
+                       cosM, sinM, kc, vc, stride, window, grp, nH, M, dyn, w, ns, ksl);
   switch (hd) {
     case 64: PA_LAUNCH(64) break;
     case 128: PA_LAUNCH(128) break;
