@@ -394,7 +394,7 @@ def bench_prefill(ops, reps: int = 5, p0: int = 3968, stacked: bool = True, gemm
 
 
 def bench_token_step(ops, steps: int, warmup: int, pos: int = 1023, fast: bool = False,
-                     fuse_gemv: bool = True, host_loop: bool = False):
+                     fuse_gemv: bool = True, host_loop: bool = False, profile: bool = False):
     """A whole decode token through the engine mirror (vk_engine.py): the
     reference's per-layer dispatch order (norm, q/k/v, prepkv, attention, o,
     normadd, norm, gate/up, gelumul, down, normadd) for 48 layers of the
@@ -413,7 +413,10 @@ def bench_token_step(ops, steps: int, warmup: int, pos: int = 1023, fast: bool =
     ``vk_engine.forward`` call at the next position: pinned-memory write of
     (tid, pos), graph launch, bounded wait, timed on the host clock
     (``ms_per_token``) beside the back-to-back replays of the same graph
-    (``graph_replay_ms_per_token``)."""
+    (``graph_replay_ms_per_token``). With ``profile``, the graph carries a
+    GPU timestamp after every launch (the engine's PROFILE=1 mode) and the
+    result adds ``profile_us``: GPU time per token by op label, each op with
+    one stamp launch's gap."""
     import importlib
 
     import numpy as np
@@ -480,7 +483,7 @@ def bench_token_step(ops, steps: int, warmup: int, pos: int = 1023, fast: bool =
         step = torch.zeros(2, dtype=torch.int32, pin_memory=True)
         d_tok = E.token_inputs_ds(step, emb, B["h"], DYN, [(ctab, stab, hd, cosb, sinb)], vocab=V, H=H,
                                   max_pos=max_pos)
-    graph = E.record_decode(layers, d_fin, d_lm, fuse=fast, fuse_gemv=fuse_gemv, d_tok=d_tok)
+    graph = E.record_decode(layers, d_fin, d_lm, fuse=fast, fuse_gemv=fuse_gemv, d_tok=d_tok, profile=profile)
     # one launch per recorded descriptor, plus the split merge of every attention
     launches = len(graph.seq) + sum(1 for op in graph.seq if getattr(op, "fn", None) in (ops.attn, ops.prepkv_attn))
     host = None
@@ -498,6 +501,11 @@ def bench_token_step(ops, steps: int, warmup: int, pos: int = 1023, fast: bool =
     for _ in range(warmup):
         graph.launch()
     torch.cuda.synchronize()
+    prof = None
+    if profile:  # one wait per token, so every token's stamps are read
+        for _ in range(steps):
+            E.submit(graph, timeout_ms=20000)
+        prof = {k: round(v, 2) for k, v in E.profile_report(graph).items()}
     a = torch.cuda.Event(enable_timing=True)
     b = torch.cuda.Event(enable_timing=True)
     a.record(graph.stream)
@@ -526,6 +534,8 @@ def bench_token_step(ops, steps: int, warmup: int, pos: int = 1023, fast: bool =
         out.update(timing="vk_engine.forward per token on the host clock (pinned (tid, pos) write, graph launch, "
                           "bounded wait), positions advancing from " + str(pos),
                    graph_replay_ms_per_token=round(ms, 4))
+    if prof is not None:
+        out["profile_us"] = prof
     return out
 
 
@@ -1040,6 +1050,8 @@ def main():
                     help="run only the prefill-chunk leg; prints its result, no JSON line")
     ap.add_argument("--small-m-only", action="store_true",
                     help="run only the small-M GEMV leg; prints its result, no JSON line")
+    ap.add_argument("--token-profile", action="store_true",
+                    help="only the fused decode token with a GPU timestamp after every launch: time per op label")
     ap.add_argument("--token-only", action="store_true",
                     help="run only the whole-token legs (reference dispatches, then fused) for --steps replays; "
                          "prints their results, no JSON line")
@@ -1077,6 +1089,10 @@ def main():
         for fast in (False, True):
             print(f"[bench] token step {bench_token_step(ops, args.steps, args.warmup, fast=fast, host_loop=fast)}",
                   flush=True)
+        return
+    if args.token_profile:
+        t = bench_token_step(ops, args.steps, args.warmup, fast=True, profile=True)
+        print(f"[bench] token profile (us per token, in-graph stamps) {t['profile_us']}", flush=True)
         return
     print(f"[bench] decode graph: {LAYERS} layers + lm_head, {args.steps} steps after {args.warmup} warmup",
           flush=True)

@@ -101,6 +101,10 @@ SIGNATURES = {
     "q4_graph_launch": (_i, [_vp, _vp]),
     "q4_graph_destroy": (_i, [_vp]),
     "q4_stream_wait": (_i, [_vp, _i]),
+    "q4_timestamps_create": (_i, [_i, _vp]),
+    "q4_timestamp_record": (_i, [_vp, _i, _vp]),
+    "q4_timestamps_read": (_i, [_vp, _vp]),
+    "q4_timestamps_destroy": (_i, [_vp]),
 }
 
 

@@ -133,6 +133,83 @@ int q4_graph_launch(void* graph_exec, void* stream) {
   return Q4_OK;
 }
 
+// GPU timestamps: slot i of a device array takes the constant-rate wall
+// clock (s_memrealtime) when a one-wave stamp launch runs. Stream-ordered
+// like any launch, so inside a stream capture it is a node of the graph and
+// every replay stamps again. The host reads the array back after the wait.
+struct Timestamps {
+  int n;
+  unsigned long long* dev;
+  double khz;
+};
+
+}  // extern "C"
+
+namespace q4 {
+__global__ void __launch_bounds__(64) stamp_kernel(unsigned long long* __restrict__ t, int i) {
+  if (threadIdx.x == 0) t[i] = wall_clock64();
+}
+}  // namespace q4
+
+extern "C" {
+
+int q4_timestamps_create(int n, void** ts) {
+  clear_error();
+  Q4_ARG(n >= 2 && n <= (1 << 16) && ts, "timestamps: 2..65536 slots and an output pointer");
+  int dev = 0, khz = 0;
+  Q4_HIP(hipGetDevice(&dev));
+  Q4_HIP(hipDeviceGetAttribute(&khz, hipDeviceAttributeWallClockRate, dev));
+  Q4_ARG(khz > 0, "no wall clock rate");
+  unsigned long long* d = nullptr;
+  Q4_HIP(hipMalloc(&d, (size_t)n * sizeof(unsigned long long)));
+  hipError_t e = hipMemset(d, 0, (size_t)n * sizeof(unsigned long long));
+  if (e != hipSuccess) {
+    (void)hipFree(d);
+    set_error("hipMemset failed: %s", hipGetErrorString(e));
+    return Q4_ERR_HIP;
+  }
+  *ts = new Timestamps{n, d, (double)khz};
+  return Q4_OK;
+}
+
+int q4_timestamp_record(void* ts, int i, void* stream) {
+  clear_error();
+  Timestamps* t = reinterpret_cast<Timestamps*>(ts);
+  Q4_ARG(t && i >= 0 && i < t->n, "timestamp index %d out of range", i);
+  hipLaunchKernelGGL(stamp_kernel, dim3(1), dim3(64), 0, as_stream(stream), t->dev, i);
+  Q4_LAUNCHED("stamp");
+  return Q4_OK;
+}
+
+int q4_timestamps_read(void* ts, double* ms) {
+  clear_error();
+  Timestamps* t = reinterpret_cast<Timestamps*>(ts);
+  Q4_ARG(t && ms, "null pointer");
+  unsigned long long* h = new unsigned long long[t->n];
+  const hipError_t e = hipMemcpy(h, t->dev, (size_t)t->n * sizeof(unsigned long long), hipMemcpyDeviceToHost);
+  if (e == hipSuccess)
+    for (int i = 0; i < t->n; ++i) ms[i] = (double)(long long)(h[i] - h[0]) / t->khz;
+  delete[] h;
+  if (e != hipSuccess) {
+    set_error("hipMemcpy failed: %s", hipGetErrorString(e));
+    return Q4_ERR_HIP;
+  }
+  return Q4_OK;
+}
+
+int q4_timestamps_destroy(void* ts) {
+  clear_error();
+  Timestamps* t = reinterpret_cast<Timestamps*>(ts);
+  if (!t) return Q4_OK;
+  const hipError_t e = hipFree(t->dev);
+  delete t;
+  if (e != hipSuccess) {
+    set_error("hipFree failed: %s", hipGetErrorString(e));
+    return Q4_ERR_HIP;
+  }
+  return Q4_OK;
+}
+
 int q4_graph_destroy(void* graph_exec) {
   clear_error();
   if (!graph_exec) return Q4_OK;

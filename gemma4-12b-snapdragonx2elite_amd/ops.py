@@ -955,6 +955,31 @@ def token_inputs(step: torch.Tensor, emb: torch.Tensor, h: torch.Tensor, dyn: to
          vp(ptrs["st"]), vp(hds), max_pos, vp(ptrs["co"]), vp(ptrs["so"]), _stream(stream))
 
 
+class Timestamps:
+    """``n`` GPU timestamps (q4_timestamps_*): ``record(i)`` enqueues a stamp
+    on the current stream, inside a graph capture too (then every replay
+    stamps again); ``read_ms()`` (after the work is done) gives the
+    milliseconds from stamp 0 to each stamp."""
+
+    def __init__(self, n: int):
+        h = C.c_void_p()
+        call("q4_timestamps_create", int(n), C.byref(h))
+        self.h, self.n = h, int(n)
+
+    def record(self, i: int, stream=None) -> None:
+        call("q4_timestamp_record", self.h, int(i), _stream(stream))
+
+    def read_ms(self) -> list:
+        ms = (C.c_double * self.n)()
+        call("q4_timestamps_read", self.h, ms)
+        return list(ms)
+
+    def destroy(self) -> None:
+        if self.h:
+            call("q4_timestamps_destroy", self.h)
+            self.h = None
+
+
 def stream_wait(stream=None, timeout_ms: int = 0, label: str = "") -> None:
     """Bounded wait; raises RuntimeError('GPU fence TIMEOUT after <ms>ms at [label]') on expiry,
     the message the reference's fence wait raises (src/vk_engine.py:299-302)."""

@@ -37,7 +37,9 @@ fence wait :293-302    :func:`submit` / :func:`wait` raise
 
 Flags are read at import like the reference: ``GEMV_FP8=1`` selects e4m3
 decode scales, ``PREFILL_I8=1`` the W8A8 prefill GEMM,
-``GEMMA4_FENCE_TIMEOUT_MS`` the wait bound.
+``GEMMA4_FENCE_TIMEOUT_MS`` the wait bound, ``PROFILE=1`` / ``PREPROF=1`` a
+GPU timestamp after every op of the decode / prefill graph, summed per op
+label at every submit (:func:`profile_report`, :func:`print_profile`).
 """
 from __future__ import annotations
 
@@ -53,6 +55,8 @@ from ._lib import SCALE_E4M3, SCALE_F16
 
 FP8 = os.environ.get("GEMV_FP8") == "1"
 PREFILL_I8 = os.environ.get("PREFILL_I8") == "1"
+PROFILE = os.environ.get("PROFILE") == "1"   # per-op GPU timestamps in the decode graph (src/vk_engine.py:37)
+PREPROF = os.environ.get("PREPROF") == "1"   # ... and in the prefill graph (:38)
 BLK = 32
 MC = 128                    # prefill chunk (rows per prefill GEMM), src/vk_engine.py:339
 _FENCE_MS = int(os.environ.get("GEMMA4_FENCE_TIMEOUT_MS", "0"))
@@ -590,7 +594,7 @@ def pre_attn_ds(qbuf: Buf, qnw: Buf, cosM: Buf, sinM: Buf, kc: Buf, vc: Buf, out
                                  out.view(out_dtype, MC * nH * hd)), kw)
 
 
-def record_prefill(layers, fuse: bool = True, gemm_norms: bool = False) -> ops.Graph:
+def record_prefill(layers, fuse: bool = True, gemm_norms: bool = False, profile: bool | None = None) -> ops.Graph:
     """Record the prefill of one ``MC``-token chunk through ``layers`` in the
     reference's order (rec_layer, src/vk_engine.py:410-424): per layer
     p_in, the q/k/v GEMMs, p_prep, p_attn, the o GEMM, p_na, p_pfn, the
@@ -606,7 +610,9 @@ def record_prefill(layers, fuse: bool = True, gemm_norms: bool = False) -> ops.G
     reference submits one
     command buffer per layer; one graph holds them all here (the chunk's
     buffers persist between layers either way). With ``fuse``, each
-    pre_na and the pre_norm of the same rows after it run as one launch."""
+    pre_na and the pre_norm of the same rows after it run as one launch.
+    With ``profile`` (default: ``PREPROF=1``) a GPU timestamp follows every
+    launch (src/vk_engine.py:491-504; see :func:`record_decode`)."""
     seq = []
     for L in layers:
         if L.get("p_qkv") is not None:
@@ -622,13 +628,13 @@ def record_prefill(layers, fuse: bool = True, gemm_norms: bool = False) -> ops.G
     if gemm_norms:
         seq = _fuse_gemm_prepkv(_fuse_gemm_normadd(seq))
 
-    def body():
-        for op in seq:
-            if isinstance(op, tuple) and op and op[0] == "gmm":
-                gmm(None, op[1])
-            else:
-                disp(op)
-    g = record(body)
+    def run(op):
+        if isinstance(op, tuple) and op and op[0] == "gmm":
+            gmm(None, op[1])
+        else:
+            disp(op)
+
+    g = _record_seq(seq, run, PREPROF if profile is None else profile)
     g.seq = seq          # the recorded descriptor sequence, for inspection
     return g
 
@@ -766,6 +772,72 @@ def record(body) -> ops.Graph:
     return g
 
 
+def op_label(op) -> str:
+    """Profile label of a recorded descriptor: the op's name, or a GEMV's
+    (stacked) rows x K."""
+    if isinstance(op, tuple) and op and op[0] in ("gemvs", "gemvs_nx"):
+        ds = op[1] if op[0] == "gemvs" else op[2]
+        return ("gemv+norm " if op[0] == "gemvs_nx" else "gemv ") + f"{sum(d.N for d in ds)}x{ds[0].dp[7]}"
+    if isinstance(op, tuple) and op and op[0] == "gmm":
+        return "gemm"
+    fn = getattr(op, "fn", None)
+    if fn is ops.gemv_normadd:
+        return f"gemv+norm {op.args[7]}x{op.args[8]}"
+    return getattr(fn, "__name__", "op").lstrip("_")
+
+
+def _record_seq(seq, run, profile: bool) -> ops.Graph:
+    """Record ``run(op)`` for every op of ``seq``. With ``profile``, a GPU
+    timestamp before the first op and after each one (the reference's
+    ts(label) after each dispatch, src/vk_engine.py:263-265). Each stamp is
+    a small launch of its own, so an op's time includes one launch gap."""
+    if not profile:
+        return record(lambda: [run(op) for op in seq])
+    ts = ops.Timestamps(len(seq) + 1)
+
+    def body():
+        ts.record(0)
+        for i, op in enumerate(seq):
+            run(op)
+            ts.record(i + 1)
+    g = record(body)
+    g.ts, g.labels, g.prof, g.prof_runs = ts, [op_label(op) for op in seq], {}, 0
+    return g
+
+
+def read_profile(g: ops.Graph) -> None:
+    """After a submit of a profiled graph: add each op's time (us) to its
+    label's total (src/vk_engine.py:321-327)."""
+    ts = getattr(g, "ts", None)
+    if ts is None:
+        return
+    ms = ts.read_ms()
+    for i, lab in enumerate(g.labels):
+        g.prof[lab] = g.prof.get(lab, 0.0) + 1e3 * (ms[i + 1] - ms[i])
+    g.prof_runs += 1
+
+
+def profile_report(g: ops.Graph) -> dict:
+    """Per-label GPU time per submit (us), largest first, and their TOTAL
+    (src/vk_engine.py:329-335)."""
+    n = max(1, getattr(g, "prof_runs", 0))
+    rep = {k: v / n for k, v in sorted(getattr(g, "prof", {}).items(), key=lambda kv: -kv[1])}
+    rep["TOTAL"] = sum(rep.values())
+    return rep
+
+
+def print_profile(g: ops.Graph, what: str = "token") -> None:
+    """The reference's profile printout (src/vk_engine.py:329-335)."""
+    if not getattr(g, "prof_runs", 0):
+        return
+    rep = profile_report(g)
+    tot = rep.pop("TOTAL")
+    print(f"\n=== GPU profile (per {what}, avg of {g.prof_runs}) ===", flush=True)
+    for k, us in rep.items():
+        print(f"  {k:24} {us:9.1f} us  {100 * us / tot:5.1f}%", flush=True)
+    print(f"  {'TOTAL':24} {tot:9.1f} us", flush=True)
+
+
 def token_inputs_ds(step: torch.Tensor, emb: Buf, h: Buf, dyn: Buf, tables=(), *, vocab: int, H: int,
                     max_pos: int) -> OpDesc:
     """The host writes of the reference's forward() (src/vk_engine.py:312-314:
@@ -796,7 +868,7 @@ def forward(g: ops.Graph, step: torch.Tensor, tid: int, pos: int, *, vocab: int,
 
 
 def record_decode(layers, d_fin: OpDesc, d_lm: GemvDesc, fuse: bool = True, fuse_gemv: bool = True,
-                  d_tok: OpDesc | None = None) -> ops.Graph:
+                  d_tok: OpDesc | None = None, profile: bool | None = None) -> ops.Graph:
     """Record one decode token in the reference's dispatch order
     (src/vk_engine.py:274-287): per layer norm, q/k/v (one batched launch),
     prepkv, attention, o, normadd, norm, gate/up (one launch), gelumul,
@@ -817,7 +889,10 @@ def record_decode(layers, d_fin: OpDesc, d_lm: GemvDesc, fuse: bool = True, fuse
     (q/k/v, gate/up; :func:`ops.gemv_batch_normadd`, :func:`ops.gemv_normadd`),
     two launches fewer per layer. ``d_tok`` (:func:`token_inputs_ds`), when
     given, is the graph's first launch: the token's embedding row, position
-    and RoPE rows come from the step buffer that :func:`forward` writes."""
+    and RoPE rows come from the step buffer that :func:`forward` writes.
+    With ``profile`` (default: ``PROFILE=1``) a GPU timestamp follows every
+    launch; :func:`submit` then adds each op's time to its label
+    (:func:`profile_report`, :func:`print_profile`)."""
     seq = [d_tok] if d_tok is not None else []
     for L in layers:
         seq += [L["d_in"], ("gemvs", [L["d_q"], L["d_k"]] + ([L["d_v"]] if L.get("d_v") is not None else [])),
@@ -830,18 +905,18 @@ def record_decode(layers, d_fin: OpDesc, d_lm: GemvDesc, fuse: bool = True, fuse
         if fuse_gemv:
             seq = _fuse_norm_gemvs(seq)
 
-    def body():
-        for op in seq:
-            if isinstance(op, tuple) and op and op[0] == "gemvs":
-                gemv_many(op[1])
-            elif isinstance(op, tuple) and op and op[0] == "gemvs_nx":
-                a, w, h, h_out, w2, sc = op[1]
-                d0 = op[2][0].dp
-                ops.gemv_batch_normadd(a, w, h, h_out, w2, [(d.dp[1], d.dp[2], d.dp[6], d.dp[5], d.dp[4])
-                                                            for d in op[2]], d0[7], scale=sc, scale_fmt=d0[3])
-            else:
-                disp(op)
-    g = record(body)
+    def run(op):
+        if isinstance(op, tuple) and op and op[0] == "gemvs":
+            gemv_many(op[1])
+        elif isinstance(op, tuple) and op and op[0] == "gemvs_nx":
+            a, w, h, h_out, w2, sc = op[1]
+            d0 = op[2][0].dp
+            ops.gemv_batch_normadd(a, w, h, h_out, w2, [(d.dp[1], d.dp[2], d.dp[6], d.dp[5], d.dp[4])
+                                                        for d in op[2]], d0[7], scale=sc, scale_fmt=d0[3])
+        else:
+            disp(op)
+
+    g = _record_seq(seq, run, PROFILE if profile is None else profile)
     g.seq = seq          # the recorded descriptor sequence, for inspection
     return g
 
@@ -960,6 +1035,8 @@ def wait(stream=None, label: str = "", timeout_ms: int | None = None) -> None:
 
 
 def submit(g: ops.Graph, label: str = "", timeout_ms: int | None = None) -> None:
-    """Replay a recorded graph and wait for it (src/vk_engine.py:312-319)."""
+    """Replay a recorded graph and wait for it (src/vk_engine.py:312-319);
+    a profiled graph's op times are added to its labels (:func:`read_profile`)."""
     g.launch()
     wait(g.stream, label, timeout_ms)
+    read_profile(g)

@@ -559,6 +559,21 @@ int q4_graph_destroy(void* graph_exec);
  * GEMMA4_FENCE_TIMEOUT_MS (src/vk_engine.py:293-302). */
 int q4_stream_wait(void* stream, int timeout_ms);
 
+/* GPU timestamps for a per-op profile of a recorded graph (PROFILE=1 /
+ * PREPROF=1: vkCmdWriteTimestamp after each op into a query pool, read back
+ * after the fence, src/vk_engine.py:37-46,263-265,321-335,491-504). n >= 2
+ * slots of device memory (allocated here, freed by q4_timestamps_destroy).
+ * q4_timestamp_record enqueues a one-wave launch that writes the constant-
+ * rate wall clock into slot i when it runs, stream-ordered after the work
+ * before it (inside a q4_graph_begin/end capture it becomes a node of the
+ * graph and stamps again at every replay; each stamp adds one small
+ * dependent launch). q4_timestamps_read, after the stream's work is done,
+ * gives ms[i] = milliseconds from slot 0 to slot i (ms: n doubles). */
+int q4_timestamps_create(int n, void** ts);
+int q4_timestamp_record(void* ts, int i, void* stream);
+int q4_timestamps_read(void* ts, double* ms);
+int q4_timestamps_destroy(void* ts);
+
 #ifdef __cplusplus
 }
 #endif

@@ -101,7 +101,21 @@ def test_decode_token_lm_head_keeps_its_norm_launch(g4, gpu, gated, monkeypatch)
     _token_steps(gpu, True, True, gated, True, V=2048, lm_fused=False)
 
 
-def _token_steps(gpu, fuse, half, gated, fg, V=V, lm_fused=True, device_inputs=False):
+def test_decode_token_profile(g4, gpu):
+    """PROFILE=1's counterpart (src/vk_engine.py:37-46,263-265,321-335): a
+    GPU timestamp after every op of the recorded token; every submit adds
+    each op's time to its label. The oracle bar holds with the timestamps in
+    the graph, and the report covers every op of the token once per submit."""
+    E = importlib.import_module("g4mi.vk_engine")
+    rep, seq, runs = _token_steps(gpu, True, True, True, True, profile=True)
+    assert runs == 20
+    labels = set(rep) - {"TOTAL"}
+    assert labels == {E.op_label(op) for op in seq}
+    assert "prepkv_attn" in labels and any(k.startswith("gemv+norm ") for k in labels)
+    assert all(v > 0 for v in rep.values()) and abs(rep["TOTAL"] - sum(rep[k] for k in labels)) < 1e-6 * rep["TOTAL"]
+
+
+def _token_steps(gpu, fuse, half, gated, fg, V=V, lm_fused=True, device_inputs=False, profile=False):
     E = importlib.import_module("g4mi.vk_engine")
     xdt = torch.float16 if half else torch.float32
     rx = (lambda v: np.asarray(v).astype(np.float16).astype(np.float64)) if half else (lambda v: v)
@@ -175,7 +189,7 @@ def _token_steps(gpu, fuse, half, gated, fg, V=V, lm_fused=True, device_inputs=F
         rope = {hd: [wbuf(np.stack([_rope(p, hd)[i] for p in range(MAXP)])) for i in (0, 1)] for hd in (64, 128)}
         d_tok = E.token_inputs_ds(step, wbuf(EMB), B["h"], DYN, [(rope[hd][0], rope[hd][1], hd, cosb[hd], sinb[hd])
                                                                  for hd in (64, 128)], vocab=VOC, H=H, max_pos=MAXP)
-    graph = E.record_decode(layers, d_fin, d_lm, fuse=fuse, fuse_gemv=fg, d_tok=d_tok)
+    graph = E.record_decode(layers, d_fin, d_lm, fuse=fuse, fuse_gemv=fg, d_tok=d_tok, profile=profile)
     n_nx = sum(1 for op in graph.seq if (isinstance(op, tuple) and op[0] == "gemvs_nx")
                or getattr(op, "fn", None) is gpu.gemv_normadd)
     # per layer: the gate/up GEMV(s) and the next layer's q/k/v or (last layer) the 1024-row lm_head
@@ -221,4 +235,6 @@ def _token_steps(gpu, fuse, half, gated, fg, V=V, lm_fused=True, device_inputs=F
         if not lm_fused:
             hdev = np.frombuffer(B["h"].read(H * 4), np.float32)
             assert O.normwise_rel_err(hdev, h) <= 1e-3, pos
+    out = (E.profile_report(graph), graph.seq, graph.prof_runs) if profile else None
     graph.destroy()
+    return out
