@@ -394,7 +394,7 @@ def bench_prefill(ops, reps: int = 5, p0: int = 3968, stacked: bool = True, gemm
 
 
 def bench_token_step(ops, steps: int, warmup: int, pos: int = 1023, fast: bool = False,
-                     fuse_gemv: bool = True, host_loop: bool = False, profile: bool = False):
+                     fuse_gemv: bool = True, host_loop: bool = False, profile: bool = False, e4m3: bool = False):
     """A whole decode token through the engine mirror (vk_engine.py): the
     reference's per-layer dispatch order (norm, q/k/v, prepkv, attention, o,
     normadd, norm, gate/up, gelumul, down, normadd) for 48 layers of the
@@ -416,7 +416,9 @@ def bench_token_step(ops, steps: int, warmup: int, pos: int = 1023, fast: bool =
     (``graph_replay_ms_per_token``). With ``profile``, the graph carries a
     GPU timestamp after every launch (the engine's PROFILE=1 mode) and the
     result adds ``profile_us``: GPU time per token by op label, each op with
-    one stamp launch's gap."""
+    one stamp launch's gap. ``e4m3``: every matrix with e4m3 block scales
+    (the engine's GEMV_FP8=1 decode, one scale byte per block; values
+    2^-2 .. 2^2, timing does not depend on them)."""
     import importlib
 
     import numpy as np
@@ -433,7 +435,9 @@ def bench_token_step(ops, steps: int, warmup: int, pos: int = 1023, fast: bool =
                               generator=gen).to(torch.int32)
         sc = (torch.randn(N * K // 32, device=dev, generator=gen) * 0.02).abs().to(torch.float16)
         b = E.Buf(tensor=sc)
-        return E.QW(E.Buf(tensor=words), b, ops.auto_split(N, K), K // 32, 1.0, b, None, None), (N, K)
+        bs = E.Buf(tensor=torch.randint(0x28, 0x48, (N * K // 32,), dtype=torch.int32, device=dev,
+                                        generator=gen).to(torch.uint8)) if e4m3 else b
+        return E.QW(E.Buf(tensor=words), bs, ops.auto_split(N, K), K // 32, 1.0, b, None, None), (N, K)
 
     def vec(n, lo=0.5):
         return E.Buf(tensor=(torch.rand(n, device=dev, generator=gen) + lo).to(torch.float32))
@@ -516,8 +520,9 @@ def bench_token_step(ops, steps: int, warmup: int, pos: int = 1023, fast: bool =
     ms = a.elapsed_time(b) / steps
     T = min(pos + 1, win)
     xb = 0 if fast else 1  # fp32 x: 2K more bytes than the fp16 count
-    wbytes = LAYERS * sum(gemv_bytes(N, K) + 2 * K * xb for N, K in
-                          [(nq, H), (nk, H), (nk, H), (H, nq), (I, H), (I, H), (H, I)]) + gemv_bytes(V, H) + 2 * H * xb
+    sb = 1 if e4m3 else 2
+    wbytes = LAYERS * sum(gemv_bytes(N, K, sb) + 2 * K * xb for N, K in
+                          [(nq, H), (nk, H), (nk, H), (H, nq), (I, H), (I, H), (H, I)]) + gemv_bytes(V, H, sb) + 2 * H * xb
     kvbytes = LAYERS * 2 * nkv * T * hd * 2
     graph.destroy()
     del layers, B
@@ -1107,7 +1112,9 @@ def main():
         tok = {"reference_dispatches": bench_token_step(ops, max(20, args.steps // 4), 5),
                "fused": bench_token_step(ops, max(20, args.steps // 4), 5, fast=True, host_loop=True),
                "fused_norm_launches": bench_token_step(ops, max(20, args.steps // 4), 5, fast=True,
-                                                       fuse_gemv=False)}
+                                                       fuse_gemv=False),
+               "fused_e4m3_scales": bench_token_step(ops, max(20, args.steps // 4), 5, fast=True, host_loop=True,
+                                                     e4m3=True)}
         print(f"[bench] token step {tok}", flush=True)
     single = {"c1_15360x3840_f16_scales": bench_gemv_single(ops, I, H, False),
               "c3_15360x3840_e4m3_scales": bench_gemv_single(ops, I, H, True),
@@ -1176,6 +1183,7 @@ def main():
         "lm_head_us": single["lm_head_262144x3840_f16_scales"]["us_per_launch"],
         "token_ms": None if tok is None else tok["fused"]["ms_per_token"],
         "token_graph_ms": None if tok is None else tok["fused"]["graph_replay_ms_per_token"],
+        "token_e4m3_ms": None if tok is None else tok["fused_e4m3_scales"]["ms_per_token"],
         "prefill_chunk_ms": pre["ms_per_chunk"],
     }
     if w8 is not None:
