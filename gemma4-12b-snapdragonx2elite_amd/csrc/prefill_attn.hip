@@ -6,15 +6,17 @@
 // which runs one workgroup per (head, token) and walks the keys one scalar
 // dot product at a time; here the query rows of a KV head are tiled onto
 // MFMAs:
-//  * A workgroup (4 waves; 8 at hd 512, two per row group splitting the head
-//    dims, see PaGeom) owns 64 query rows of one KV head (row = token *
-//    grp + query head within the group, so the rows share their K and V)
-//    and one split of the cache slots (a multiple of 32 keys, long enough
-//    that the grid has about 256 workgroups: 128 keys for a 1024-slot ring
-//    of 8 KV heads, 512 for 4096 keys of one KV head); the grid covers the
-//    keys the caller bounds and splits past a workgroup's last token exit
-//    at once, so the launch shape does not depend on p0 (graph replay).
-//  * q prologue, in registers: lane (c, g) of wave w holds row 16w + c,
+//  * A workgroup owns 64 query rows of one KV head (row = token * grp +
+//    query head within the group, so the rows share their K and V), in 4
+//    row groups of 16, and one split of the cache slots (a multiple of 32
+//    keys, long enough that the grid has about 256 workgroups: 128 keys for
+//    a 1024-slot ring of 8 KV heads, 512 for 4096 keys of one KV head); the
+//    grid covers the keys the caller bounds and splits past a workgroup's
+//    last token exit at once, so the launch shape does not depend on p0
+//    (graph replay). Head dims up to 256 take one wave per row group
+//    (pre_attn_kernel); head dim 512 takes two, each holding half of the
+//    head dims (pre_attn512_kernel).
+//  * q prologue, in registers: lane (c, g) of a row group holds row c,
 //    elements 32j + 8g .. 32j + 8g + 7 of every 32-element chunk j; the
 //    RoPE partner of element e (e +- hd/2) is in the same lane, and the
 //    row's sum of squares needs two xor-shuffles. q is split into fp16
@@ -22,23 +24,26 @@
 //    rounding with fp16 MFMAs (two per k-step; k is fp16 in the cache).
 //  * Per 32-key tile the workgroup stages K row-major ([key][hd], rows
 //    padded by 16 bytes) and V transposed ([hd][key], pairs of keys per
-//    32-bit word) in LDS from registers. Scores S^T = K q^T: one
-//    v_mfma_f32_16x16x32_f16 pair per 16 keys x 16 rows x 32 elements; lane
-//    (c, g) gets keys 4g .. 4g+3 of row c. Masked keys (past the row's
-//    length, or in a ring slot a later token of the chunk now holds: slot s
-//    holds position last - ((last - s) mod window) once the chunk's last
-//    position is written, vk/pre_attn.comp:40) are -inf. Online softmax per row over the tile (xor-shuffles across the 4
-//    lanes of a row), then O^T += V^T P^T with v_mfma_f32_16x16x16_f16: the
-//    B operand is exactly the score layout (P rounded to fp16), the A
-//    operand one 8-byte LDS read of the transposed V.
+//    32-bit word) in LDS. Scores S^T = K q^T: one v_mfma_f32_16x16x32_f16
+//    pair per 16 keys x 16 rows x 32 elements; lane (c, g) gets keys
+//    4g .. 4g+3 of row c in each 16-key subtile. Masked keys (past the
+//    row's length, or in a ring slot a later token of the chunk now holds:
+//    slot s holds position last - ((last - s) mod window) once the chunk's
+//    last position is written, vk/pre_attn.comp:40) are -inf. Online
+//    softmax per row over the tile (xor-shuffles across the 4 lanes of a
+//    row), then O^T += V^T P^T with one v_mfma_f32_16x16x32_f16 per 16
+//    output dims: the B operand is the score layout of both subtiles (P
+//    rounded to fp16), the A operand 16 bytes of the transposed V, whose
+//    rows keep their keys in that order (pv_slot).
 //  * Each workgroup writes its rows' (max, sum, unnormalised accumulator)
 //    for its split; q4_pre_attn's second kernel merges the splits.
 #include "q4mi_common.h"
 
 namespace q4 {
 
-constexpr int PA_WAVES = 4;
+constexpr int PA_WAVES = 4;             // row groups of 16 rows per workgroup
 constexpr int PA_THREADS = 64 * PA_WAVES;
+constexpr int PA_ROWS = 16 * PA_WAVES;  // query rows per workgroup
 constexpr int PA_KT = 32;               // keys per LDS tile
 constexpr int PA_TARGET_WGS = 256;      // workgroups the split length aims for (one per CU)
 constexpr float PA_EPS = 1e-6f;
@@ -72,56 +77,176 @@ __device__ inline long pa_ws_index(int m, int h, int nH, int ks, int nsplit, int
   return (((long)m * nH + h) * nsplit + ks) * (hd + 4);
 }
 
-// Tile geometry per head dim: KT keys per LDS tile and DS waves per row
-// group, 4 row groups of 16 rows per workgroup. With DS = 2 (hd 512) the two
-// waves of a row group split the head dims: each holds q (hi + lo) for half
-// of them, computes the partial scores over that half, and the pair adds
-// the two halves through LDS (half 0 + half 1, the same bits in both
-// waves); each then accumulates its half of the output dims. So q, the
-// accumulators and the prefetch registers of a wave fit two waves per SIMD
-// without spills, and no score is computed twice (a pair that computed the
-// full scores in both waves took 137 us against 102 us for one wave per
-// row group, 128 tokens x 16 heads over 4096 keys, MQA). Measured in the
-// prefill chunk (the 8 global layers, kernel-only): 85.6 us with one wave
-// per row group, 77.8 us with the split pair; 32-key tiles with the pair
-// spill registers (87.6 us). Without the next tile's loads (timing only) the
-// pair takes 67 us: the rest is issue and the three barriers per tile.
-template <int HD>
-struct PaGeom {
-  static constexpr int KT = HD >= 512 ? 16 : 32;
-  static constexpr int DS = HD >= 512 ? 2 : 1;
-  static constexpr int WAVES = PA_WAVES * DS;
-  static constexpr int THREADS = 64 * WAVES;
-  static constexpr int ROWS = 16 * PA_WAVES;  // query rows per workgroup
-};
+// Position of key k of a 32-key tile in its V^T row: k = 16 st + 4 g + e
+// sits at 8 g + 4 st + e, so lane (c, g)'s weights of both 16-key subtiles
+// are the 8 consecutive k of one 16x16x32 MFMA.
+__device__ inline int pv_slot(int k) { return 8 * ((k & 15) >> 2) + 4 * (k >> 4) + (k & 3); }
 
+// Lane (c, g)'s part of its query row (q element offset qb; cs, sn: the
+// row's cos and sin): elements 32 j + 8 g .. + 7 of every chunk j after the
+// rms norm with qnw and RoPE, in fp32.
 template <int HD, int QT>
-__global__ void __launch_bounds__(PaGeom<HD>::THREADS)
+__device__ __forceinline__ void pa_q_row(const void* __restrict__ qin, long qb, const float* __restrict__ qnw,
+                                         const float* __restrict__ cs, const float* __restrict__ sn, int g,
+                                         float (&qf)[HD / 32][8]) {
+  constexpr int NCH = HD / 32;
+  float ss = 0.0f;
+#pragma unroll
+  for (int j = 0; j < NCH; ++j) {
+    ld8f<QT>(qin, qb + 32 * j + 8 * g, qf[j]);
+#pragma unroll
+    for (int u = 0; u < 8; ++u) ss = fmaf(qf[j][u], qf[j][u], ss);
+  }
+  ss = slot_reduce<16>(ss);
+  const float inv = 1.0f / sqrtf(ss / (float)HD + PA_EPS);
+#pragma unroll
+  for (int j = 0; j < NCH; ++j) {
+    float w[8];
+    ld8f<Q4_DT_F32>(qnw, 32 * j + 8 * g, w);
+#pragma unroll
+    for (int u = 0; u < 8; ++u) qf[j][u] = __fmul_rn(__fmul_rn(qf[j][u], inv), w[u]);
+  }
+#pragma unroll
+  for (int j = 0; j < NCH / 2; ++j) {
+    const int e = 32 * j + 8 * g, e2 = e + HD / 2;
+    float c1[8], s1[8], c2[8], s2[8];
+    ld8f<Q4_DT_F32>(cs, e, c1);
+    ld8f<Q4_DT_F32>(sn, e, s1);
+    ld8f<Q4_DT_F32>(cs, e2, c2);
+    ld8f<Q4_DT_F32>(sn, e2, s2);
+#pragma unroll
+    for (int u = 0; u < 8; ++u) {
+      const float a = qf[j][u], b = qf[j + NCH / 2][u];
+      const float ra = __fadd_rn(__fmul_rn(a, c1[u]), __fmul_rn(-b, s1[u]));
+      const float rb = __fadd_rn(__fmul_rn(b, c2[u]), __fmul_rn(a, s2[u]));
+      qf[j][u] = ra;
+      qf[j + NCH / 2][u] = rb;
+    }
+  }
+}
+
+// fp16 hi + lo parts of chunks j0 .. j0 + N - 1 of a lane's row.
+template <int N, int NCH>
+__device__ __forceinline__ void pa_q_split(const float (&qf)[NCH][8], int j0, v8h* qh, v8h* ql) {
+#pragma unroll
+  for (int j = 0; j < N; ++j)
+#pragma unroll
+    for (int u = 0; u < 8; ++u) {
+      const _Float16 hi = (_Float16)qf[j0 + j][u];
+      qh[j][u] = hi;
+      ql[j][u] = (_Float16)(qf[j0 + j][u] - (float)hi);
+    }
+}
+
+// The keys of slots t0 .. t0 + 31 for row (T: its length, pos: its
+// position): -inf where masked (past the split's end kend, past the row's
+// length, or a ring slot a later token holds; rt = (last - t0) mod window).
+__device__ __forceinline__ void pa_mask(const v4f* sp, float (*sc)[4], int t0, int g, int kend, int T, int window,
+                                        int rt, uint32_t last, uint32_t pos) {
+#pragma unroll
+  for (int st = 0; st < 2; ++st) {
+    const v4f s = sp[st];
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const int i = 16 * st + 4 * g + e, slot = t0 + i;
+      bool ok = slot < kend && slot < T;
+      if (window > 0) {
+        const int r = rt - i;  // (last - slot) mod window, for i < window
+        ok = ok && (long)last - (r >= 0 ? r : r + window) <= (long)pos;
+      }
+      sc[st][e] = ok ? s[e] : -INFINITY;
+    }
+  }
+}
+
+// Keys below the returned slot are live for every row of a workgroup
+// (rows r0 ..): without a ring a row's keys are the slots below its length,
+// and the workgroup's first token has the shortest; with a ring, none is
+// taken as known.
+__device__ inline int pa_full_keys(int k0, int kend, int r0, int grp, uint32_t p0, int window, int stride) {
+  return window > 0 ? k0 : min(kend, att_len(p0 + (uint32_t)(r0 / grp), window, stride));
+}
+
+// Online softmax of a lane's 8 masked scores of the tile (row maximum and
+// sum across the row's 4 lanes) and the rescale of its accumulators: P in
+// fp16 for the V product, the running (mrun, lrun) updated.
+template <int NDT>
+__device__ __forceinline__ v8h pa_softmax(const float (*sc)[4], float& mrun, float& lrun, v4f* oacc) {
+  float tmax = -INFINITY;
+#pragma unroll
+  for (int st = 0; st < 2; ++st)
+#pragma unroll
+    for (int e = 0; e < 4; ++e) tmax = fmaxf(tmax, sc[st][e]);
+  tmax = slot_reduce<16, true>(tmax);
+  const float mnew = fmaxf(mrun, tmax);
+  const bool any = mnew != -INFINITY;
+  // v_exp_f32-based exponentials (relative error ~1e-6): the weights are
+  // rounded to fp16 (2^-11) before use, and the reference's GLSL exp() is
+  // itself approximate; 8 fewer VALU operations per score
+  const float corr = any ? __expf(mrun - mnew) : 1.0f;
+  float psum = 0.0f;
+  v8h pb;
+#pragma unroll
+  for (int st = 0; st < 2; ++st)
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      // the weights the V product uses are the fp16-rounded ones: the sum
+      // is taken over the same values, so the output stays a weighted mean
+      // of V rows (the row maximum's weight, 1, is exact)
+      const _Float16 p = (_Float16)(any ? __expf(sc[st][e] - mnew) : 0.0f);
+      psum += (float)p;
+      pb[4 * st + e] = p;
+    }
+  psum = slot_reduce<16>(psum);
+  lrun = fmaf(lrun, corr, psum);
+  mrun = mnew;
+#pragma unroll
+  for (int d = 0; d < NDT; ++d)
+#pragma unroll
+    for (int e = 0; e < 4; ++e) oacc[d][e] *= corr;
+  return pb;
+}
+
+// The 8 key-pair words of one 16-byte V chunk pair into the V^T tile:
+// elements 8 ch + 2w, 8 ch + 2w + 1 of keys 2 pr (low half) and 2 pr + 1
+// (high half), at the pair's pv_slot position of each row.
+template <int VP>
+__device__ __forceinline__ void pa_store_vpair(uint8_t* vsh, v4u a, v4u b, int ch, int pr) {
+  const int wo = 2 * pv_slot(2 * pr);
+#pragma unroll
+  for (int w = 0; w < 4; ++w) {
+    // (a & 0xFFFF) | (b << 16) and (a >> 16) | (b & 0xFFFF0000), one byte permute each
+    *reinterpret_cast<uint32_t*>(vsh + (8 * ch + 2 * w) * VP + wo) = __builtin_amdgcn_perm(b[w], a[w], 0x05040100u);
+    *reinterpret_cast<uint32_t*>(vsh + (8 * ch + 2 * w + 1) * VP + wo) = __builtin_amdgcn_perm(b[w], a[w], 0x07060302u);
+  }
+}
+
+// Head dims 64 .. 256: one wave per row group (4 waves), K and V of the next
+// tile loaded into registers one tile ahead and stored to LDS after the
+// tile's first barrier.
+template <int HD, int QT>
+__global__ void __launch_bounds__(PA_THREADS)
 pre_attn_kernel(const void* __restrict__ qin, int ldq, const float* __restrict__ qnw, const float* __restrict__ cosM,
                 const float* __restrict__ sinM, const uint16_t* __restrict__ kc, const uint16_t* __restrict__ vc,
                 int stride, int window, int grp, int nH, int M, const uint32_t* __restrict__ dyn,
                 float* __restrict__ ws, int nsplit, int ksl) {
-  constexpr int KT = PaGeom<HD>::KT, DS = PaGeom<HD>::DS, ROWS = PaGeom<HD>::ROWS, NT = PaGeom<HD>::THREADS;
-  constexpr int NST = KT / 16;        // 16-key subtiles per tile
+  constexpr int KT = PA_KT, NT = PA_THREADS;
   constexpr int NCH = HD / 32;        // 32-element chunks
-  constexpr int NQC = NCH / DS;       // chunks of this wave's QK (its part of the head dims)
-  constexpr int NDT = HD / 16 / DS;   // 16-element output tiles of this wave
+  constexpr int NDT = HD / 16;        // 16-element output tiles
   constexpr int CPR = HD / 8;         // 16-byte chunks per K/V row
   constexpr int KP = HD * 2 + 16;     // K tile row pitch (bytes)
   constexpr int VP = KT * 2 + 8;      // V^T tile row pitch (bytes)
   constexpr int KITEMS = KT * CPR, VITEMS = (KT / 2) * CPR;  // 16-byte K chunks, V key-pair chunks per tile
   constexpr int KLD = (KITEMS + NT - 1) / NT, VLD = (VITEMS + NT - 1) / NT;
-  static_assert(NQC % 2 == 0, "head dim");
+  static_assert(HD <= 256 && NCH % 2 == 0, "head dim");
   __shared__ __attribute__((aligned(16))) uint8_t ksh[KT * KP];
   __shared__ __attribute__((aligned(16))) uint8_t vsh[HD * VP];
-  __shared__ v4f xs[DS > 1 ? PaGeom<HD>::WAVES : 1][NST][64];  // partial scores of each wave (DS > 1)
 
   const int kvh = blockIdx.x, ks = blockIdx.z;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, c = lane & 15, g = lane >> 4;
-  const int rg = wave / DS, dp = wave % DS;  // row group, output part
   const uint32_t p0 = dyn[0];
-  const int nrows = M * grp, r0 = blockIdx.y * ROWS;
-  const int mlast = (min(r0 + ROWS, nrows) - 1) / grp;
+  const int nrows = M * grp, r0 = blockIdx.y * PA_ROWS;
+  const int mlast = (min(r0 + PA_ROWS, nrows) - 1) / grp;
   const int Tlast = att_len(p0 + (uint32_t)mlast, window, stride);
   const int k0 = ks * ksl;
   if (k0 >= Tlast) return;  // no row of this workgroup has keys in this split (uniform)
@@ -157,86 +282,31 @@ pre_attn_kernel(const void* __restrict__ qin, int ldq, const float* __restrict__
     }
 #pragma unroll
     for (int i = 0; i < VLD; ++i) {
-      const int q = tid + NT * i, pr = q % (KT / 2), ch = q / (KT / 2);
-      if (q >= VITEMS) continue;
-#pragma unroll
-      for (int w = 0; w < 4; ++w) {
-        // elements 8 ch + 2w, 8 ch + 2w + 1 of keys 2 pr (low half) and 2 pr + 1 (high half)
-        const uint32_t a = va[i][w], b = vb[i][w];
-        *reinterpret_cast<uint32_t*>(vsh + (8 * ch + 2 * w) * VP + 4 * pr) = (a & 0xFFFFu) | (b << 16);
-        *reinterpret_cast<uint32_t*>(vsh + (8 * ch + 2 * w + 1) * VP + 4 * pr) = (a >> 16) | (b & 0xFFFF0000u);
-      }
+      const int q = tid + NT * i;
+      if (q < VITEMS) pa_store_vpair<VP>(vsh, va[i], vb[i], q / (KT / 2), q % (KT / 2));
     }
   };
   load_tile(k0);  // in flight while q is prepared
 
   // ---- this lane's query row: q-norm, RoPE, hi/lo split ----
-  const int R = r0 + 16 * rg + c;
+  const int R = r0 + 16 * wave + c;
   const bool live = R < nrows;
   const int m = live ? R / grp : 0;
   const int h = kvh * grp + (live ? R % grp : 0);
   const uint32_t pos = p0 + (uint32_t)m;
   const int T = att_len(pos, window, stride);
-  v8h qh[NQC], ql[NQC];  // chunks dp NQC .. of the row
+  v8h qh[NCH], ql[NCH];
   {
-    // the lane's 8 consecutive elements of each chunk come in 16-byte loads
     float qf[NCH][8];
-    const long qb = (long)m * ldq + (long)h * HD;
-    float ss = 0.0f;
-#pragma unroll
-    for (int j = 0; j < NCH; ++j) {
-      ld8f<QT>(qin, qb + 32 * j + 8 * g, qf[j]);
-#pragma unroll
-      for (int u = 0; u < 8; ++u) ss = fmaf(qf[j][u], qf[j][u], ss);
-    }
-    ss = slot_reduce<16>(ss);
-    const float inv = 1.0f / sqrtf(ss / (float)HD + PA_EPS);
-#pragma unroll
-    for (int j = 0; j < NCH; ++j) {
-      float w[8];
-      ld8f<Q4_DT_F32>(qnw, 32 * j + 8 * g, w);
-#pragma unroll
-      for (int u = 0; u < 8; ++u) qf[j][u] = __fmul_rn(__fmul_rn(qf[j][u], inv), w[u]);
-    }
-    const float* cs = cosM + (long)m * HD;
-    const float* sn = sinM + (long)m * HD;
-#pragma unroll
-    for (int j = 0; j < NCH / 2; ++j) {
-      const int e = 32 * j + 8 * g, e2 = e + HD / 2;
-      float c1[8], s1[8], c2[8], s2[8];
-      ld8f<Q4_DT_F32>(cs, e, c1);
-      ld8f<Q4_DT_F32>(sn, e, s1);
-      ld8f<Q4_DT_F32>(cs, e2, c2);
-      ld8f<Q4_DT_F32>(sn, e2, s2);
-#pragma unroll
-      for (int u = 0; u < 8; ++u) {
-        const float a = qf[j][u], b = qf[j + NCH / 2][u];
-        const float ra = __fadd_rn(__fmul_rn(a, c1[u]), __fmul_rn(-b, s1[u]));
-        const float rb = __fadd_rn(__fmul_rn(b, c2[u]), __fmul_rn(a, s2[u]));
-        qf[j][u] = ra;
-        qf[j + NCH / 2][u] = rb;
-      }
-    }
-    // this wave's part of the head dims (a wave-uniform branch keeps the
-    // register indices static)
-    auto split = [&](int j0) {
-#pragma unroll
-      for (int j = 0; j < NQC; ++j)
-#pragma unroll
-        for (int u = 0; u < 8; ++u) {
-          const _Float16 hi = (_Float16)qf[j0 + j][u];
-          qh[j][u] = hi;
-          ql[j][u] = (_Float16)(qf[j0 + j][u] - (float)hi);
-        }
-    };
-    if (DS == 1 || dp == 0) split(0);
-    else split(NQC);
+    pa_q_row<HD, QT>(qin, (long)m * ldq + (long)h * HD, qnw, cosM + (long)m * HD, sinM + (long)m * HD, g, qf);
+    pa_q_split<NCH>(qf, 0, qh, ql);
   }
 
   v4f oacc[NDT];
 #pragma unroll
   for (int d = 0; d < NDT; ++d) oacc[d] = v4f{0.0f, 0.0f, 0.0f, 0.0f};
   float mrun = -INFINITY, lrun = 0.0f;
+  const int kfull = pa_full_keys(k0, kend, r0, grp, p0, window, stride);
 
   for (int t0 = k0; t0 < kend; t0 += KT) {
     __syncthreads();  // every wave is done with the previous tile
@@ -250,12 +320,202 @@ pre_attn_kernel(const void* __restrict__ qin, int ldq, const float* __restrict__
     // ring slots t0 + i hold position last - ((last - t0 - i) mod window):
     // one (uniform) division per tile
     const int rt = window > 0 ? (int)(((long)last - t0) % window) : 0;
-    float sc[NST][4];
-    v4f sp[NST];
+    v4f sp[2];
 #pragma unroll
-    for (int st = 0; st < NST; ++st) {
+    for (int st = 0; st < 2; ++st) {
       v4f s0 = v4f{0.0f, 0.0f, 0.0f, 0.0f}, s1 = s0, s2 = s0, s3 = s0;
-      const uint8_t* kr0 = ksh + (16 * st + c) * KP + (4 * dp * NQC + g) * 16;
+      const uint8_t* kr0 = ksh + (16 * st + c) * KP + g * 16;
+#pragma unroll
+      for (int j = 0; j < NCH; j += 2) {
+        const v8h a0 = *reinterpret_cast<const v8h*>(kr0 + 4 * j * 16);
+        const v8h a1 = *reinterpret_cast<const v8h*>(kr0 + (4 * j + 4) * 16);
+        s0 = __builtin_amdgcn_mfma_f32_16x16x32_f16(a0, qh[j], s0, 0, 0, 0);
+        s1 = __builtin_amdgcn_mfma_f32_16x16x32_f16(a1, qh[j + 1], s1, 0, 0, 0);
+        s2 = __builtin_amdgcn_mfma_f32_16x16x32_f16(a0, ql[j], s2, 0, 0, 0);
+        s3 = __builtin_amdgcn_mfma_f32_16x16x32_f16(a1, ql[j + 1], s3, 0, 0, 0);
+      }
+      sp[st] = (s0 + s1) + (s2 + s3);
+    }
+    float sc[2][4];
+    if (t0 + KT <= kfull) {  // every key of the tile is live for every row of the workgroup (uniform)
+#pragma unroll
+      for (int st = 0; st < 2; ++st)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) sc[st][e] = sp[st][e];
+    } else {
+      pa_mask(sp, sc, t0, g, kend, T, window, rt, last, pos);
+    }
+    const v8h pb = pa_softmax<NDT>(sc, mrun, lrun, oacc);
+    // ---- O^T += V^T P^T, both subtiles in one K = 32 MFMA per output tile ----
+#pragma unroll
+    for (int d = 0; d < NDT; ++d) {
+      const uint8_t* va8 = vsh + (16 * d + c) * VP + 16 * g;
+      const v4h lo = *reinterpret_cast<const v4h*>(va8), hi = *reinterpret_cast<const v4h*>(va8 + 8);
+      const v8h a8 = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+      oacc[d] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a8, pb, oacc[d], 0, 0, 0);
+    }
+  }
+
+  // ---- this split's partial for the row ----
+  if (!live) return;
+  float* o = ws + pa_ws_index(m, h, nH, ks, nsplit, HD);
+  if (g == 0) {
+    o[0] = mrun;
+    o[1] = lrun;
+  }
+#pragma unroll
+  for (int d = 0; d < NDT; ++d) *reinterpret_cast<v4f*>(o + 4 + 16 * d + 4 * g) = oacc[d];
+}
+
+// Head dim 512 (Gemma's global layers: one KV head shared by all 16 query
+// heads): two waves per row group, each holding q (hi + lo) for half of the
+// head dims. Each computes the partial scores over its half and the pair adds
+// the two halves through LDS (half 0 + half 1, the same bits in both
+// waves); each then accumulates its half of the output dims. So q, the
+// accumulators and the loads in flight fit two waves per SIMD (8 waves, 512
+// threads) without spills, and no score is computed twice (a pair that
+// computed the full scores in both waves took 137 us against 102 us for
+// one wave per row group, 128 tokens x 16 heads over 4096 keys). Per 32-key
+// tile:
+//  * K rows go from global memory straight into LDS (a 1 KB direct load
+//    per key row, no registers), into one of two buffers: tile i + 1's rows
+//    are loaded after tile i's score exchange and land while tile i's
+//    softmax and V product run. V rows come through registers, loaded one
+//    tile ahead right after the V^T store.
+//  * Two barriers: (A) every wave's K rows and V registers of the tile have
+//    landed and every wave is done with the previous tile; (B) the pair's
+//    partial scores are exchanged (this also publishes the V^T tile).
+//  * Row addresses advance by one tile away from the end of the cache, and
+//    tiles whose keys are live for every row of the workgroup skip the mask.
+// Measured on the workload above (kernel-only, same box): 77 us with one
+// 16-key tile per three barriers and registers staging K; 68.5 us with
+// 32-key tiles, K direct loads and the K = 32 V product; 63.7 us with the
+// row address and mask changes; 58.5 us with the K rows loaded after the
+// exchange instead of with the V rows (the tile's loads all at once held
+// the score MFMAs back: 1.6k of ~7k cycles per tile). Not kept: the q
+// prologue (~10 us of the span) done once per row by a separate launch
+// (25 us for that launch), or reading qnw, cos and sin from LDS (67 us:
+// one more barrier, spills); the V rows loaded after the exchange too
+// (67 us: they no longer land before the next tile's store).
+constexpr int PA512_THREADS = 512;
+template <int QT>
+__global__ void __launch_bounds__(PA512_THREADS)
+pre_attn512_kernel(const void* __restrict__ qin, int ldq, const float* __restrict__ qnw,
+                   const float* __restrict__ cosM, const float* __restrict__ sinM, const uint16_t* __restrict__ kc,
+                   const uint16_t* __restrict__ vc, int stride, int window, int grp, int nH, int M,
+                   const uint32_t* __restrict__ dyn, float* __restrict__ ws, int nsplit, int ksl) {
+  constexpr int HD = 512, KT = PA_KT, DS = 2, WAVES = 8, NT = PA512_THREADS;
+  constexpr int NCH = HD / 32;        // 32-element chunks
+  constexpr int NQC = NCH / DS;       // chunks of this wave's QK
+  constexpr int NDT = HD / 16 / DS;   // 16-element output tiles of this wave
+  constexpr int CPR = HD / 8;         // 16-byte chunks per V row
+  constexpr int KP = HD * 2 + 16;     // K tile row pitch (bytes)
+  constexpr int VP = KT * 2 + 8;      // V^T tile row pitch (bytes)
+  constexpr int VITEMS = (KT / 2) * CPR, VLD = VITEMS / NT;  // V key-pair chunks per tile, per thread
+  constexpr int KPW = KT / WAVES;     // K rows each wave loads per tile
+  static_assert(VITEMS % NT == 0 && KT % WAVES == 0 && NQC % 2 == 0, "tile shape");
+  __shared__ __attribute__((aligned(16))) uint8_t ksh[2][KT * KP];
+  __shared__ __attribute__((aligned(16))) uint8_t vsh[HD * VP];
+  __shared__ v4f xs[WAVES][2][64];  // each wave's partial scores of the tile
+
+  const int kvh = blockIdx.x, ks = blockIdx.z;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, c = lane & 15, g = lane >> 4;
+  const int rg = wave / DS, dp = wave % DS;  // row group, half of the head dims
+  const uint32_t p0 = dyn[0];
+  const int nrows = M * grp, r0 = blockIdx.y * PA_ROWS;
+  const int mlast = (min(r0 + PA_ROWS, nrows) - 1) / grp;
+  const int Tlast = att_len(p0 + (uint32_t)mlast, window, stride);
+  const int k0 = ks * ksl;
+  if (k0 >= Tlast) return;  // uniform
+  const int kend = min(k0 + ksl, Tlast);
+  const uint32_t last = p0 + (uint32_t)M - 1;
+
+  // K rows of tile t0 -> ksh[b] (wave w loads rows w KPW .. + KPW - 1) and
+  // the V rows of its key pairs -> registers. Away from the end of the cache
+  // the addresses advance by one tile of rows (kp, vp: at the next tile to
+  // load); a tile that reaches past row stride - 1 clamps every row to it.
+  const uint16_t* kp = kc + ((long)kvh * stride + k0 + KPW * wave) * HD + lane * 8;
+  const uint16_t* vp[VLD];
+#pragma unroll
+  for (int i = 0; i < VLD; ++i) {
+    const int q = tid + NT * i, pr = q % (KT / 2), ch = q / (KT / 2);
+    vp[i] = vc + ((long)kvh * stride + k0 + 2 * pr) * HD + ch * 8;
+  }
+  v4u va[VLD], vb[VLD];
+  auto load_v = [&](int t0) {
+    if (t0 + KT <= stride) {
+#pragma unroll
+      for (int i = 0; i < VLD; ++i) {
+        va[i] = *reinterpret_cast<const v4u*>(vp[i]);
+        vb[i] = *reinterpret_cast<const v4u*>(vp[i] + HD);
+      }
+    } else {
+#pragma unroll
+      for (int i = 0; i < VLD; ++i) {
+        const int q = tid + NT * i, pr = q % (KT / 2), ch = q / (KT / 2);
+        const int s0 = min(t0 + 2 * pr, stride - 1), s1 = min(t0 + 2 * pr + 1, stride - 1);
+        va[i] = *reinterpret_cast<const v4u*>(vc + ((long)kvh * stride + s0) * HD + ch * 8);
+        vb[i] = *reinterpret_cast<const v4u*>(vc + ((long)kvh * stride + s1) * HD + ch * 8);
+      }
+    }
+#pragma unroll
+    for (int i = 0; i < VLD; ++i) vp[i] += KT * HD;
+  };
+  auto load_k = [&](int t0, int b) {
+    if (t0 + KT <= stride) {
+#pragma unroll
+      for (int i = 0; i < KPW; ++i) dma16(kp + i * HD, ksh[b] + (KPW * wave + i) * KP);
+    } else {
+#pragma unroll
+      for (int i = 0; i < KPW; ++i) {
+        const int key = KPW * wave + i, slot = min(t0 + key, stride - 1);
+        dma16(kc + ((long)kvh * stride + slot) * HD + lane * 8, ksh[b] + key * KP);
+      }
+    }
+    kp += KT * HD;
+  };
+  load_v(k0);
+  load_k(k0, 0);
+
+  // ---- this lane's query row: q-norm, RoPE, the hi/lo split of the wave's half ----
+  const int R = r0 + 16 * rg + c;
+  const bool live = R < nrows;
+  const int m = live ? R / grp : 0;
+  const int h = kvh * grp + (live ? R % grp : 0);
+  const uint32_t pos = p0 + (uint32_t)m;
+  const int T = att_len(pos, window, stride);
+  v8h qh[NQC], ql[NQC];
+  {
+    float qf[NCH][8];
+    pa_q_row<HD, QT>(qin, (long)m * ldq + (long)h * HD, qnw, cosM + (long)m * HD, sinM + (long)m * HD, g, qf);
+    // a wave-uniform branch keeps the register indices static
+    if (dp == 0) pa_q_split<NQC>(qf, 0, qh, ql);
+    else pa_q_split<NQC>(qf, NQC, qh, ql);
+  }
+
+  v4f oacc[NDT];
+#pragma unroll
+  for (int d = 0; d < NDT; ++d) oacc[d] = v4f{0.0f, 0.0f, 0.0f, 0.0f};
+  float mrun = -INFINITY, lrun = 0.0f;
+  const int kfull = pa_full_keys(k0, kend, r0, grp, p0, window, stride);
+
+  int b = 0;
+  for (int t0 = k0; t0 < kend; t0 += KT, b ^= 1) {
+    vmwait<0>();      // this wave's K rows (direct loads) and V registers of the tile
+    __syncthreads();  // (A)
+#pragma unroll
+    for (int i = 0; i < VLD; ++i) {
+      const int q = tid + NT * i;
+      pa_store_vpair<VP>(vsh, va[i], vb[i], q / (KT / 2), q % (KT / 2));
+    }
+    const bool more = t0 + KT < kend;
+    if (more) load_v(t0 + KT);  // the next tile's V rows run under this tile's math
+    const int rt = window > 0 ? (int)(((long)last - t0) % window) : 0;
+    v4f sp[2];
+#pragma unroll
+    for (int st = 0; st < 2; ++st) {
+      v4f s0 = v4f{0.0f, 0.0f, 0.0f, 0.0f}, s1 = s0, s2 = s0, s3 = s0;
+      const uint8_t* kr0 = ksh[b] + (16 * st + c) * KP + (4 * dp * NQC + g) * 16;
 #pragma unroll
       for (int j = 0; j < NQC; j += 2) {
         const v8h a0 = *reinterpret_cast<const v8h*>(kr0 + 4 * j * 16);
@@ -267,71 +527,32 @@ pre_attn_kernel(const void* __restrict__ qin, int ldq, const float* __restrict__
       }
       sp[st] = (s0 + s1) + (s2 + s3);
     }
-    if constexpr (DS > 1) {  // the pair's partial scores: half 0 + half 1, in both waves
 #pragma unroll
-      for (int st = 0; st < NST; ++st) xs[wave][st][lane] = sp[st];
-      __syncthreads();
+    for (int st = 0; st < 2; ++st) xs[wave][st][lane] = sp[st];
+    __syncthreads();  // (B)
+    // the next tile's K rows, into the buffer tile t0 - KT used (free since (A))
+    if (more) load_k(t0 + KT, b ^ 1);
 #pragma unroll
-      for (int st = 0; st < NST; ++st) sp[st] = xs[rg * DS][st][lane] + xs[rg * DS + 1][st][lane];
+    for (int st = 0; st < 2; ++st) sp[st] = xs[rg * DS][st][lane] + xs[rg * DS + 1][st][lane];
+    float sc[2][4];
+    if (t0 + KT <= kfull) {  // uniform
+#pragma unroll
+      for (int st = 0; st < 2; ++st)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) sc[st][e] = sp[st][e];
+    } else {
+      pa_mask(sp, sc, t0, g, kend, T, window, rt, last, pos);
     }
+    const v8h pb = pa_softmax<NDT>(sc, mrun, lrun, oacc);
 #pragma unroll
-    for (int st = 0; st < NST; ++st) {
-      const v4f s = sp[st];
-#pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        const int i = 16 * st + 4 * g + e, slot = t0 + i;
-        bool ok = slot < kend && slot < T;
-        if (window > 0) {
-          const int r = rt - i;  // (last - slot) mod window, for i < window
-          ok = ok && (long)last - (r >= 0 ? r : r + window) <= (long)pos;
-        }
-        sc[st][e] = ok ? s[e] : -INFINITY;
-      }
+    for (int d = 0; d < NDT; ++d) {
+      const uint8_t* va8 = vsh + (16 * (dp * NDT + d) + c) * VP + 16 * g;
+      const v4h lo = *reinterpret_cast<const v4h*>(va8), hi = *reinterpret_cast<const v4h*>(va8 + 8);
+      const v8h a8 = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+      oacc[d] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a8, pb, oacc[d], 0, 0, 0);
     }
-    // ---- online softmax over the tile ----
-    float tmax = -INFINITY;
-#pragma unroll
-    for (int st = 0; st < NST; ++st)
-#pragma unroll
-      for (int e = 0; e < 4; ++e) tmax = fmaxf(tmax, sc[st][e]);
-    tmax = slot_reduce<16, true>(tmax);
-    const float mnew = fmaxf(mrun, tmax);
-    const bool any = mnew != -INFINITY;
-    // v_exp_f32-based exponentials (relative error ~1e-6): the weights are
-    // rounded to fp16 (2^-11) before use, and the reference's GLSL exp()
-    // is itself approximate; 8 fewer VALU operations per score
-    const float corr = any ? __expf(mrun - mnew) : 1.0f;
-    float psum = 0.0f;
-    v4h pb[NST];
-#pragma unroll
-    for (int st = 0; st < NST; ++st)
-#pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        // the weights the V product uses are the fp16-rounded ones: the sum
-        // is taken over the same values, so the output stays a weighted mean
-        // of V rows (the row maximum's weight, 1, is exact)
-        const _Float16 p = (_Float16)(any ? __expf(sc[st][e] - mnew) : 0.0f);
-        psum += (float)p;
-        pb[st][e] = p;
-      }
-    psum = slot_reduce<16>(psum);
-    lrun = fmaf(lrun, corr, psum);
-    mrun = mnew;
-#pragma unroll
-    for (int d = 0; d < NDT; ++d)
-#pragma unroll
-      for (int e = 0; e < 4; ++e) oacc[d][e] *= corr;
-    // ---- O^T += V^T P^T over this wave's output dims ----
-#pragma unroll
-    for (int st = 0; st < NST; ++st)
-#pragma unroll
-      for (int d = 0; d < NDT; ++d) {
-        const v4h a = *reinterpret_cast<const v4h*>(vsh + (16 * (dp * NDT + d) + c) * VP + (16 * st + 4 * g) * 2);
-        oacc[d] = __builtin_amdgcn_mfma_f32_16x16x16f16(a, pb[st], oacc[d], 0, 0, 0);
-      }
   }
 
-  // ---- this split's partial for the row ----
   if (!live) return;
   float* o = ws + pa_ws_index(m, h, nH, ks, nsplit, HD);
   if (g == 0 && dp == 0) {
@@ -341,9 +562,6 @@ pre_attn_kernel(const void* __restrict__ qin, int ldq, const float* __restrict__
 #pragma unroll
   for (int d = 0; d < NDT; ++d) *reinterpret_cast<v4f*>(o + 4 + 16 * (dp * NDT + d) + 4 * g) = oacc[d];
 }
-
-// rows per workgroup for head dim hd (PaGeom<hd>::ROWS)
-static int pa_rows(int hd) { return hd >= 512 ? PaGeom<512>::ROWS : PaGeom<256>::ROWS; }
 
 // out[m][h hd + i] = sum_c acc_c w_c / sum_c l_c w_c over the splits that
 // hold keys of token m, w_c = exp(max_c - max); fp32 or fp16 out. A
@@ -419,8 +637,8 @@ pre_attn_merge_kernel(const float* __restrict__ ws, void* __restrict__ out, int 
 
 // Keys per split for a launch: a multiple of the tile, long enough that the
 // (KV head, row block, split) grid has about PA_TARGET_WGS workgroups.
-static int pa_split_len(int M, int nH, int nkv, int hd, int max_keys) {
-  const int blocks = nkv * ceil_div(M * (nH / nkv), pa_rows(hd));
+static int pa_split_len(int M, int nH, int nkv, int max_keys) {
+  const int blocks = nkv * ceil_div(M * (nH / nkv), PA_ROWS);
   const int want = max(1, ceil_div(PA_TARGET_WGS, blocks));
   return PA_KT * ceil_div(max_keys, PA_KT * want);
 }
@@ -433,7 +651,7 @@ extern "C" {
 
 size_t q4_pre_attn_workspace_bytes(int M, int nH, int nkv, int hd, int max_keys) {
   if (M <= 0 || nH <= 0 || nkv <= 0 || nH % nkv || hd <= 0 || max_keys <= 0) return 0;
-  const int ns = ceil_div(max_keys, pa_split_len(M, nH, nkv, hd, max_keys));
+  const int ns = ceil_div(max_keys, pa_split_len(M, nH, nkv, max_keys));
   return (size_t)M * nH * ns * (hd + 4) * sizeof(float);
 }
 
@@ -462,22 +680,22 @@ int q4_pre_attn(const void* q, int q_dtype, int ldq, const float* qnw, const flo
   Q4_ARG(window == 0 || max_keys >= window, "a ring layer needs max_keys >= window (%d)", window);
   const size_t need = q4_pre_attn_workspace_bytes(M, nH, nkv, hd, max_keys);
   Q4_ARG(ws_bytes >= need, "prefill attention needs a %zu-byte workspace (got %zu)", need, ws_bytes);
-  const int grp = nH / nkv, ksl = pa_split_len(M, nH, nkv, hd, max_keys), ns = ceil_div(max_keys, ksl);
-  const dim3 grid(nkv, ceil_div(M * grp, pa_rows(hd)), ns);
+  const int grp = nH / nkv, ksl = pa_split_len(M, nH, nkv, max_keys), ns = ceil_div(max_keys, ksl);
+  const dim3 grid(nkv, ceil_div(M * grp, PA_ROWS), ns);
   hipStream_t st = as_stream(stream);
   float* w = reinterpret_cast<float*>(ws);
-#define PA_LAUNCH(HD_)                                                                                           \
-  if (q_dtype == Q4_DT_F16)                                                                                      \
-    hipLaunchKernelGGL((pre_attn_kernel<HD_, Q4_DT_F16>), grid, dim3(PaGeom<HD_>::THREADS), 0, st, q, ldq, qnw,  \
-                       cosM, sinM, kc, vc, stride, window, grp, nH, M, dyn, w, ns, ksl);                             \
-  else                                                                                                           \
-    hipLaunchKernelGGL((pre_attn_kernel<HD_, Q4_DT_F32>), grid, dim3(PaGeom<HD_>::THREADS), 0, st, q, ldq, qnw,  \
-                       cosM, sinM, kc, vc, stride, window, grp, nH, M, dyn, w, ns, ksl);
+#define PA_LAUNCH(K16, K32, NTH)                                                                           \
+  if (q_dtype == Q4_DT_F16)                                                                                \
+    hipLaunchKernelGGL(K16, grid, dim3(NTH), 0, st, q, ldq, qnw, cosM, sinM, kc, vc, stride, window, grp, nH, M, \
+                       dyn, w, ns, ksl);                                                                       \
+  else                                                                                                     \
+    hipLaunchKernelGGL(K32, grid, dim3(NTH), 0, st, q, ldq, qnw, cosM, sinM, kc, vc, stride, window, grp, nH, M, \
+                       dyn, w, ns, ksl);
   switch (hd) {
-    case 64: PA_LAUNCH(64) break;
-    case 128: PA_LAUNCH(128) break;
-    case 256: PA_LAUNCH(256) break;
-    default: PA_LAUNCH(512) break;
+    case 64: PA_LAUNCH((pre_attn_kernel<64, Q4_DT_F16>), (pre_attn_kernel<64, Q4_DT_F32>), PA_THREADS) break;
+    case 128: PA_LAUNCH((pre_attn_kernel<128, Q4_DT_F16>), (pre_attn_kernel<128, Q4_DT_F32>), PA_THREADS) break;
+    case 256: PA_LAUNCH((pre_attn_kernel<256, Q4_DT_F16>), (pre_attn_kernel<256, Q4_DT_F32>), PA_THREADS) break;
+    default: PA_LAUNCH(pre_attn512_kernel<Q4_DT_F16>, pre_attn512_kernel<Q4_DT_F32>, PA512_THREADS) break;
   }
 #undef PA_LAUNCH
   Q4_LAUNCHED("pre_attn");
