@@ -157,6 +157,8 @@ def _attn_case(rng, *, M, nH, nkv, hd, stride, window, p0, qdt, peaky=False):
     (512, 16, 2, 2048, 0, 32, 600, 640, torch.float32, torch.float32, False),        # global layer, grp 8
     (512, 16, 1, 4096, 0, 128, 3968, 4096, torch.float16, torch.float16, False),     # last chunk of 4096, MQA
     (512, 4, 1, 300, 256, 40, 500, 256, torch.float16, torch.float32, True),         # hd 512 ring, ragged tiles
+    (512, 2, 2, 100, 0, 3, 90, 100, torch.float32, torch.float32, False),           # grp 1; last tile past the cache
+    (512, 8, 1, 77, 64, 5, 200, 77, torch.float16, torch.float16, True),            # ring of 64 in a 77-slot cache
     (128, 4, 2, 96, 64, 40, 130, 64, torch.float16, torch.float32, True),            # unscaled large scores
     (64, 6, 3, 300, 0, 21, 257, 300, torch.float32, torch.float32, False),           # ragged rows and splits
 ])
