@@ -638,7 +638,7 @@ def bench_w8a8(ops, iters: int = 50):
         return ops.gemm_w8a8_packed(A, W8p, sa, sw32, N, Y=Y, stamps=stp)
 
     us = timed(packed)
-    stamped = w8a8_stamped(ops, packed, M, N, iters)
+    stamped = w8a8_stamped(ops, packed, M, N, K, iters)
     us_nk = timed(lambda i: ops.gemm_w8a8(A, folded[i % nw][2], sa, folded[i % nw][1], Y=Y))
     del folded
     torch.cuda.empty_cache()
@@ -673,7 +673,7 @@ def bench_w8a8(ops, iters: int = 50):
             "quant_act_us": round(us_q, 2), "quant_act_GBps": round(3 * M * K / (us_q * 1e-6) / 1e9, 1)}
 
 
-def w8a8_stamped(ops, run, M: int, N: int, iters: int):
+def w8a8_stamped(ops, run, M: int, N: int, K: int, iters: int):
     """``iters`` back-to-back launches of the stamped W8A8 (each workgroup
     reads the wall clock at its start, after its k-loop and at its end, and
     counts shader cycles): the clock the chip held, how a launch's time
@@ -682,7 +682,7 @@ def w8a8_stamped(ops, run, M: int, N: int, iters: int):
     import numpy as np
     import torch
 
-    wgs = ops.w8a8_workgroups(M, N)
+    wgs = ops.w8a8_workgroups(M, N, K)
     stamps = torch.zeros((iters, wgs, 4), dtype=torch.int64, device="cuda:0")
     for i in range(5):
         run(i, stamps[0])

@@ -20,7 +20,7 @@ OP_W4A16 = 1
 GEMV_MAX_BATCH = 8
 # plan overrides of q4_tune_set (include/q4mi.h Q4_TUNE_*), by name
 TUNE_KNOBS = {"gemv_rows": 0, "gemv_units": 1, "gemv_pair": 2, "gemv_bal": 3, "gemv_mm_tiles": 4,
-              "gemv_mm_split": 5, "gemv_mm_deep": 6, "w4a16_split": 7, "w4a16_kg": 8}
+              "gemv_mm_split": 5, "gemv_mm_deep": 6, "w4a16_split": 7, "w4a16_kg": 8, "w8a8_tiles": 9}
 
 _vp, _i, _f, _sz = C.c_void_p, C.c_int, C.c_float, C.c_size_t
 
@@ -80,7 +80,7 @@ SIGNATURES = {
     "q4_w8_pack": (_i, [_vp, _i, _i, _vp, _vp]),
     "q4_gemm_w8a8_packed": (_i, [_vp, _vp, _vp, _vp, _i, _vp, _vp, _i, _i, _i, _vp]),
     "q4_gemm_w8a8_packed_stamped": (_i, [_vp, _vp, _vp, _vp, _i, _vp, _vp, _i, _i, _i, _vp, _sz, _vp]),
-    "q4_gemm_w8a8_packed_workgroups": (_sz, [_i, _i]),
+    "q4_gemm_w8a8_packed_workgroups": (_sz, [_i, _i, _i]),
     "q4_cast_f32_f16": (_i, [_vp, _vp, _sz, _vp]),
     "q4_cast_f16_f32": (_i, [_vp, _vp, _sz, _vp]),
     "q4_rmsnorm": (_i, [_vp, _vp, _vp, _i, _i, _vp]),

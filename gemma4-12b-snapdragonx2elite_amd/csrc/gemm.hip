@@ -36,6 +36,11 @@
 // Each wait also pins the registers it covers (an empty asm that reads and
 // writes them), so no use of a loaded value can be scheduled above its wait.
 //
+// Packed W8A8 on large grids (w8q_kernel) is persistent instead: one
+// workgroup per CU walks its share of 128 x 320 tiles through one load
+// pipeline and stages each tile's fp16 Y in LDS, stored behind the next
+// tile's MFMAs.
+//
 // Workgroups are remapped so each XCD (8 per MI355X, own L2) works on a
 // contiguous 1/8 of the tile grid ordered by weight panel. W4A16 splits K
 // across workgroups when the tile grid alone cannot fill the 256 CUs
@@ -720,6 +725,356 @@ __global__ void __launch_bounds__(256) w8p_kernel(const GemmArgs g) {
     epilogue<0, 64, FN>(g, strip, sub, m0 + 64 * c, n0 + 64 * wave, nullptr);
   }
   stamp_end();
+}
+
+// ---- W8A8 on packed weights, persistent 128 x 320 tiles --------------------------
+// One workgroup per CU runs a list of 128 x 320 output tiles through one
+// continuous load pipeline: at M = 2048, N = 15360 that is 768 tiles, three
+// per CU, so no CU idles in a last partial round (the 256 x 256 grid has 480
+// tiles: a second round on 224 CUs). Wave w owns columns 80 w .. 80 w + 79 of
+// a tile and all 128 rows: 8 x 5 tiles of v_mfma_i32_16x16x64_i8 with the
+// weights as the first operand, so a lane's 4 accumulators are 4
+// consecutive columns of one output row (D row = weight row n, D column =
+// activation row m). Per 128-byte k-step a wave reads 16 KB of A from LDS
+// and 10 KB of B from L2 for 80 MFMAs.
+//  * A: 3-stage LDS ring of direct loads, 128-byte rows with the 16-byte
+//    chunks at wq_swz_i positions.
+//  * B: from the tile-32 packing, lane l takes the 16 bytes of row l % 16 of
+//    its 16-column group and k-bytes 16 (l / 16) .. of the 64-byte slice
+//    (the same k-bytes as its A fragment, so the dot products pair the same
+//    k), two k-steps ahead in a 3-set register ring.
+//  * Per k-step: slice 0 (40 MFMAs, one A fragment read and one load per 5)
+//    issues 7 of the 14 loads of k-step + 2; vmcnt(7) then leaves only those
+//    in flight, so A and B of k-step + 1 have landed, and one barrier
+//    publishes A; slice 1 issues the other 7.
+//  * Epilogue: at the end of a tile each lane forms Y = f16((f32(C) sa) sw)
+//    (the reference's order, vk/coopgemm_w8a8.comp:35) from its accumulators
+//    and writes it to an 82 KB LDS stage of the tile; the next tile's first
+//    20 k-steps drain the stage to Y, one 16-byte nontemporal store per
+//    thread per k-step, behind the MFMAs. Only the last tile's stores are
+//    exposed. The tile's 128 row scales and 320 column scales arrive by
+//    direct loads at its first k-step (4 KB block, double-buffered by tile
+//    parity). With C the int32 accumulators are stored directly.
+// Measured at M = 2048, N = 15360, K = 3840 against w8p_kernel on the same
+// boxes: 2-3% faster. The exposed epilogue falls from ~8 to ~4 us and every
+// CU works to the end, but a 16x16x64 int8 MFMA issues every ~20.6 cycles in
+// this loop (a copy without loads or LDS reads), against 34 for a 32x32x32
+// with twice the products, and the layout needs 16-column groups.
+// Needs M % 128 == 0, N % 320 == 0, K % 64 == 0 with ceil(K / 128) % 3 == 0
+// (a last k-step of two slices clamps its A chunks inside the row; its
+// weights are zero padding), Y, and 16-byte aligned Y, sa and sw.
+constexpr int WQ_BM = 128, WQ_BN = 320;
+#define Q4_INLINE __attribute__((always_inline))
+constexpr int WQ_YP = 656;  // staged Y row pitch in bytes: 640 + 16, so 16 rows of one 8-byte column hit distinct banks
+
+// Position XOR of the 16-byte chunks of staged A row r: wq_swz_i((r >> 1) & 7),
+// bits 1 and 2 of (r >> 1) & 7 swapped. A 16x16x64 fragment read serves
+// lanes l and l + 32 together (rows r .. r + 7 at chunks c and c + 2, c % 4
+// == 0); these positions put those 16 reads, and those of chunks c + 1 and
+// c + 3, in 16 distinct 16-byte bank groups (measured: 10x fewer bank
+// conflicts than w8p_swz, whose positions repeat for rows r and r ^ 2).
+__device__ inline int wq_swz_i(int i) { return (i & 1) | ((i & 2) << 1) | ((i & 4) >> 1); }
+template <bool TAIL, bool STAMP = false>
+__global__ void __launch_bounds__(256) w8q_kernel(const GemmArgs g) {
+  constexpr int S = 3, FR = WQ_BM / 16, FG = 5, NA = WQ_BM / 32, NB = 2 * FG;
+  constexpr int AST = WQ_BM * 128;       // bytes per A stage
+  constexpr int YCH = WQ_BN / 8;         // 16-byte Y chunks per tile row
+  constexpr int DR = WQ_BM * YCH / 256;  // Y chunks per thread per tile
+  static_assert(NB + NA == 14 && WQ_BM * YCH % 256 == 0, "7 loads per slice, whole drain rounds");
+  __shared__ __attribute__((aligned(16))) uint8_t ldsA[S * AST];
+  __shared__ __attribute__((aligned(16))) uint8_t ys[WQ_BM * WQ_YP];
+  __shared__ __attribute__((aligned(16))) uint8_t scl[2][4096];
+
+  unsigned long long sw0 = 0, sc0 = 0, sw1 = 0;
+  if constexpr (STAMP) {
+    sw0 = wall_clock64();
+    sc0 = clock64();
+  }
+  const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int M = g.M, N = g.N, K = g.K;
+  const int ntm = M / WQ_BM, T = ntm * (N / WQ_BN);
+  const int G = gridDim.x, w = blockIdx.x;
+  // This workgroup's tiles first, first + tstride, ..: with both counts
+  // multiples of 8, XCD x (workgroups w % 8 == x) takes the contiguous
+  // eighth x of the tile order (M fastest), so the 32 tiles an XCD runs
+  // together share weight panels and activation rows in its L2.
+  int first, tstride, count;
+  if (T % 8 == 0 && G % 8 == 0) {
+    const int per = T / 8, gx = G / 8, i = w / 8;
+    first = (w % 8) * per + i;
+    tstride = gx;
+    count = i < per ? (per - i + gx - 1) / gx : 0;
+  } else {
+    first = w;
+    tstride = G;
+    count = w < T ? (T - w + G - 1) / G : 0;
+  }
+  const int ks = w8p_kpad(K) / 32, nk = ks / 4;
+  const int total = count * nk;  // the host launches at most T workgroups: count >= 1
+  auto tile_mn = [&](int j, int& m0, int& n0) Q4_INLINE {
+    const int v = first + j * tstride;
+    m0 = (v % ntm) * WQ_BM;
+    n0 = (v / ntm) * WQ_BN;
+  };
+
+  // per-lane offsets, the same for every tile
+  // A: wave instruction i stages tile row r = (wave NA + i) 8 + lane / 8, the
+  // 16-byte chunk that belongs at LDS position lane % 8 (chunk = position ^
+  // wq_swz_i((r >> 1) & 7), and (r >> 1) & 7 = ((wave NA + i) & 1) 4 + lane / 16)
+  auto a_chunk = [&](int i) Q4_INLINE { return ((lane & 7) ^ wq_swz_i((((wave * NA + i) & 1) << 2) | (lane >> 4))) << 4; };
+  uint32_t aoff[NA];
+#pragma unroll
+  for (int i = 0; i < NA; ++i) aoff[i] = (uint32_t)(((wave * NA + i) * 8 + (lane >> 3)) * K + a_chunk(i));
+  uint32_t boff[FG];  // B: 16-column group cg of the wave, lane's 16 bytes in k-slice 2 s2 + lane / 32
+#pragma unroll
+  for (int cg = 0; cg < FG; ++cg) {
+    const int nb = 80 * wave + 16 * cg;
+    boff[cg] = (uint32_t)((nb >> 5) * ks * 1024 + (lane >> 5) * 1024 +
+                          ((nb & 31) + (lane & 15) + 32 * ((lane >> 4) & 1)) * 16);
+  }
+  const uint8_t* Ab = reinterpret_cast<const uint8_t*>(g.A);
+  const uint8_t* Bb = reinterpret_cast<const uint8_t*>(g.B);
+
+  // load cursor: tile lj, k-step lk; past the last k-step it stays there
+  // (the pipeline's two extra k-steps reload it, unused)
+  int lj = 0, lk = 0, lm0, ln0;
+  tile_mn(0, lm0, ln0);
+  auto advance = [&]() Q4_INLINE {
+    if (lk + 1 < nk) {
+      ++lk;
+    } else if (lj + 1 < count) {
+      ++lj;
+      lk = 0;
+      tile_mn(lj, lm0, ln0);
+    }
+  };
+
+  v4i bw[3][FG][2];
+  // VMEM operation o (0 .. 13) of the cursor's k-step: o < NB loads B
+  // fragment (slice o / FG, group o % FG) into register set SETL; the next NA
+  // are the direct loads of its A rows into stage SETL.
+  auto vmem_op = [&](auto oc, auto setlc) Q4_INLINE {
+    constexpr int o = decltype(oc)::value, setl = decltype(setlc)::value;
+    if constexpr (o < NB) {
+      constexpr int s2 = o / FG, cg = o % FG;
+      const uint8_t* base = Bb + ((long)(ln0 >> 5) * ks + lk * 4 + 2 * s2) * 1024;
+      bw[setl][cg][s2] = __builtin_bit_cast(v4i, ld16_so(base, boff[cg]));
+    } else {
+      constexpr int i = o - NB;
+      uint8_t* st = ldsA + setl * AST + (wave * NA + i) * 1024;
+      const uint8_t* base = Ab + (long)lm0 * K;
+      if constexpr (TAIL) {  // chunks past K clamped inside the row (their weights are zero)
+        const int c = a_chunk(i);
+        dma16_so(base, aoff[i] - c + min(lk * 128 + c, K - 16), st);
+      } else {
+        dma16_so(base + lk * 128, aoff[i], st);
+      }
+    }
+  };
+
+  // the scale block of tile j (4 KB): wave 0 puts sa[m0 .. m0 + 127] at
+  // byte 0 (lanes 32-63 reload it into bytes 512-1023, unused), waves 1-2
+  // put sw[n0 .. n0 + 319] (fp32 or fp16) at byte 1024 (lanes past its end
+  // reload its last 16 bytes); wave 3 loads nothing
+  auto scale_dma = [&](int j) Q4_INLINE {
+    int m0, n0;
+    tile_mn(j, m0, n0);
+    int l = lane;
+    asm volatile("" : "+v"(l));  // offsets formed here, not kept live (spilled) across the k-loop
+    if (wave == 0) {
+      dma16_so(g.sa + m0, (uint32_t)((l & 31) * 16), scl[j & 1]);
+    } else if (wave < 3) {
+      const int esz = g.sw_f16 ? 2 : 4;
+      const uint32_t o = (uint32_t)min((wave - 1) * 1024 + l * 16, WQ_BN * esz - 16);
+      dma16_so(reinterpret_cast<const uint8_t*>(g.sw) + (long)n0 * esz, o, scl[j & 1] + wave * 1024);
+    }
+  };
+
+  v4i acc[FR][FG];  // set by the first k-step of each tile (C = 0)
+
+  const int frow = lane & 15, fq = lane >> 4;
+  // A fragment of row block rb, 64-byte slice s2 from stage st: row
+  // 16 rb + lane % 16, chunk 4 s2 + lane / 16 at its wq_swz_i position
+  auto rdA = [&](int st, int rb, int s2) Q4_INLINE {
+    const int r = 16 * rb + frow;
+    return *reinterpret_cast<const v4i*>(ldsA + st * AST + r * 128 + (((4 * s2 + fq) ^ wq_swz_i((r >> 1) & 7)) << 4));
+  };
+  v4i fa[2][FR];
+
+  using I0 = std::integral_constant<int, 0>;
+  using I1 = std::integral_constant<int, 1>;
+  using I2 = std::integral_constant<int, 2>;
+  auto load_kstep = [&](auto setc) Q4_INLINE {
+    static_for<NB, NB + NA>([&](auto oc) { vmem_op(oc, setc); });
+    static_for<0, NB>([&](auto oc) { vmem_op(oc, setc); });
+    advance();
+  };
+  load_kstep(I0{});
+  load_kstep(I1{});
+  vmwait<NA + NB>();
+#pragma unroll
+  for (int cg = 0; cg < FG; ++cg) {
+    pin(bw[0][cg][0]);
+    pin(bw[0][cg][1]);
+  }
+  __syncthreads();
+#pragma unroll
+  for (int rb = 0; rb < FR; ++rb) fa[0][rb] = rdA(0, rb, 0);
+
+  // Y drain: chunk tid + 256 d of the staged tile (m0, n0)
+  auto drain = [&](int m0, int n0, int d) Q4_INLINE {
+    int t = tid;
+    asm volatile("" : "+v"(t));  // the address math stays here, not hoisted out of the loop into spills
+    const int c = t + 256 * d, row = c / YCH, cc = c - row * YCH;
+    const v4u v = *reinterpret_cast<const v4u*>(ys + row * WQ_YP + 16 * cc);
+    __builtin_nontemporal_store(v, reinterpret_cast<v4u*>(g.Y + (long)(m0 + row) * N + n0 + 8 * cc));
+  };
+  // tile j's accumulators -> staged Y (and C)
+  auto convert = [&](int j, int m0, int n0) Q4_INLINE {
+    const float* sab = reinterpret_cast<const float*>(scl[j & 1]);
+    const uint8_t* swb = scl[j & 1] + 1024;
+    float swv[FG][4];
+    if (g.sw_f16) {
+#pragma unroll
+      for (int cg = 0; cg < FG; ++cg) {
+        const v2u h = *reinterpret_cast<const v2u*>(swb + 2 * (80 * wave + 16 * cg + 4 * fq));
+        swv[cg][0] = h2f((uint16_t)(h[0] & 0xFFFFu));
+        swv[cg][1] = h2f((uint16_t)(h[0] >> 16));
+        swv[cg][2] = h2f((uint16_t)(h[1] & 0xFFFFu));
+        swv[cg][3] = h2f((uint16_t)(h[1] >> 16));
+      }
+    } else {
+#pragma unroll
+      for (int cg = 0; cg < FG; ++cg) {
+        const float4 f = *reinterpret_cast<const float4*>(swb + 4 * (80 * wave + 16 * cg + 4 * fq));
+        swv[cg][0] = f.x;
+        swv[cg][1] = f.y;
+        swv[cg][2] = f.z;
+        swv[cg][3] = f.w;
+      }
+    }
+    if (g.C) {
+#pragma unroll
+      for (int rb = 0; rb < FR; ++rb)
+#pragma unroll
+        for (int cg = 0; cg < FG; ++cg)
+          *reinterpret_cast<v4i*>(g.C + (long)(m0 + 16 * rb + frow) * N + n0 + 80 * wave + 16 * cg + 4 * fq) =
+              acc[rb][cg];
+    }
+#pragma unroll
+    for (int rb = 0; rb < FR; ++rb) {
+      const int ml = 16 * rb + frow;
+      const float sav = sab[ml];
+#pragma unroll
+      for (int cg = 0; cg < FG; ++cg) {
+        const int nl = 80 * wave + 16 * cg + 4 * fq;
+        int c[4];
+        __builtin_memcpy(c, &acc[rb][cg], 16);
+        uint32_t hv[4];
+#pragma unroll
+        for (int r = 0; r < 4; ++r) hv[r] = f2h_after_f32(__fmul_rn(__fmul_rn((float)c[r], sav), swv[cg][r]));
+        *reinterpret_cast<v2u*>(ys + ml * WQ_YP + 2 * nl) = v2u{hv[0] | (hv[1] << 16), hv[2] | (hv[3] << 16)};
+      }
+    }
+  };
+
+  int kt = 0, pm0 = 0, pn0 = 0;
+  // One k-step of register set / stage SET (= k-step % 3; nk % 3 == 0, so
+  // the rotation is the same in every tile). j: this tile; (pm0, pn0): the
+  // previous tile, whose staged Y this tile's first DR k-steps drain.
+  // FIRST: the tile's k-step 0, whose MFMAs start from C = 0 (no separate
+  // zeroing, so the finished tile's accumulators and the new ones can share
+  // registers) and which fetches the tile's scale block.
+  auto kstep = [&](auto setc, auto firstc, int j) Q4_INLINE {
+    constexpr int set = decltype(setc)::value, setn = (set + 1) % 3, setl = (set + 2) % 3;
+    constexpr bool FIRST = decltype(firstc)::value;
+    using IL = std::integral_constant<int, setl>;
+    if constexpr (FIRST) scale_dma(j);  // lands with this k-step's A
+    static_for<0, FR>([&](auto rc) {
+      constexpr int rb = decltype(rc)::value;
+      fa[1][rb] = rdA(set, rb, 1);
+#pragma unroll
+      for (int cg = 0; cg < FG; ++cg)
+        acc[rb][cg] = __builtin_amdgcn_mfma_i32_16x16x64_i8(bw[set][cg][0], fa[0][rb], FIRST ? v4i{} : acc[rb][cg],
+                                                            0, 0, 0);
+      __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+      __builtin_amdgcn_sched_group_barrier(0x008, FG, 0);
+      if constexpr (rb < 7) vmem_op(std::integral_constant<int, rb>{}, IL{});
+      __builtin_amdgcn_sched_barrier(0);
+    });
+    vmwait<7>();  // only slice 0's loads of k-step + 2 in flight: k-step + 1 landed in this wave
+#pragma unroll
+    for (int cg = 0; cg < FG; ++cg) {
+      pin(bw[setn][cg][0]);
+      pin(bw[setn][cg][1]);
+    }
+    __syncthreads();  // ... and in every wave
+    static_for<0, FR>([&](auto rc) {
+      constexpr int rb = decltype(rc)::value;
+      fa[0][rb] = rdA(setn, rb, 0);
+#pragma unroll
+      for (int cg = 0; cg < FG; ++cg)
+        acc[rb][cg] = __builtin_amdgcn_mfma_i32_16x16x64_i8(bw[set][cg][1], fa[1][rb], acc[rb][cg], 0, 0, 0);
+      __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+      __builtin_amdgcn_sched_group_barrier(0x008, FG, 0);
+      if constexpr (rb < 7) vmem_op(std::integral_constant<int, 7 + rb>{}, IL{});
+      __builtin_amdgcn_sched_barrier(0);
+    });
+    advance();
+    if (j > 0 && kt < DR) drain(pm0, pn0, kt);
+    ++kt;
+  };
+  using F1 = std::true_type;
+  using F0 = std::false_type;
+  for (int j = 0; j < count; ++j) {
+    kt = 0;
+    kstep(I0{}, F1{}, j);
+    kstep(I1{}, F0{}, j);
+    kstep(I2{}, F0{}, j);
+    while (kt < nk) {
+      kstep(I0{}, F0{}, j);
+      kstep(I1{}, F0{}, j);
+      kstep(I2{}, F0{}, j);
+    }
+    int cm0, cn0;
+    tile_mn(j, cm0, cn0);
+    const bool last = j + 1 == count;
+    if (last) {
+      vmwait<0>();  // the unused reloads, before their registers are reused
+#pragma unroll
+      for (int s = 0; s < 3; ++s)
+#pragma unroll
+        for (int cg = 0; cg < FG; ++cg) {
+          pin(bw[s][cg][0]);
+          pin(bw[s][cg][1]);
+        }
+      if constexpr (STAMP) sw1 = wall_clock64();
+    }
+    if (j > 0 && nk <= DR) {
+      // a short tile: the rest of the previous tile's stage, then a barrier
+      // before the stage is overwritten
+      for (int d = nk; d < DR; ++d) drain(pm0, pn0, d);
+      __syncthreads();
+    }
+    convert(j, cm0, cn0);
+    if (last) {
+      __syncthreads();
+#pragma unroll 4
+      for (int d = 0; d < DR; ++d) drain(cm0, cn0, d);
+    }
+    pm0 = cm0;
+    pn0 = cn0;
+  }
+  if constexpr (STAMP) {
+    const unsigned long long sw2 = wall_clock64(), sc2 = clock64();
+    if (threadIdx.x == 0) {
+      unsigned long long* o = g.stamps + 4 * (long)blockIdx.x;
+      o[0] = sw0;
+      o[1] = sw1;
+      o[2] = sw2;
+      o[3] = sc2 - sc0;
+    }
+  }
 }
 
 // ---- W4A16, waves split along N -------------------------------------------------
@@ -1458,6 +1813,19 @@ int q4_w8_pack(const int8_t* W8, int N, int K, int8_t* W8p, void* stream) {
   return Q4_OK;
 }
 
+// Persistent 128 x 320 tiles (w8q_kernel) when the shape tiles exactly and
+// gives at least two tiles per CU, with k-steps (K / 128, rounded up) a
+// multiple of 3: 0 when the 256-row kernel runs, else the
+// grid (at most one workgroup per CU). Plan override Q4_TUNE_W8A8_TILES.
+// The caller also needs Y and 16-byte aligned Y, sa and sw.
+static int w8q_grid(int M, int N, int K) {
+  if (M % WQ_BM || N % WQ_BN || K <= 0 || K % 64 || (w8p_kpad(K) / 128) % 3) return 0;
+  const int t = (M / WQ_BM) * (N / WQ_BN);
+  const int v = tune_value(Q4_TUNE_W8A8_TILES);
+  if (v == 0 || (v != 1 && t < 512)) return 0;
+  return min(t, 256);
+}
+
 static int gemm_w8a8_packed(const int8_t* A, const int8_t* W8p, const float* sa, const void* sw, int sw_dtype,
                             uint16_t* Y, int32_t* C, int M, int N, int K, unsigned long long* stamps,
                             size_t stamps_bytes, void* stream) {
@@ -1471,14 +1839,19 @@ static int gemm_w8a8_packed(const int8_t* A, const int8_t* W8p, const float* sa,
   Q4_ARG((long)M * K < (1L << 31) && (long)q4_w8_packed_bytes(N, K) < (1L << 31),
          "packed W8A8 needs M*K and the packed weights under 2 GiB (32-bit offsets)");
   const int bm = pick_bm(M, N);
-  const int wgs = tiles(M, N, bm);
+  const bool aligned16 = Y && (((uintptr_t)Y | (uintptr_t)sa | (uintptr_t)sw) & 15) == 0;
+  const int wq = aligned16 ? w8q_grid(M, N, K) : 0;
+  const int wgs = wq ? wq : tiles(M, N, bm);
   if (stamps) Q4_ARG(stamps_bytes >= (size_t)wgs * 32 && ((uintptr_t)stamps & 7) == 0,
                      "stamps need 4 aligned 8-byte words per workgroup (%d workgroups)", wgs);
   GemmArgs g{A, W8p, nullptr, sa, sw, sw_dtype == Q4_DT_F16, Y, C, nullptr, M, N, K, stamps};
   const bool tail = K % 128 != 0;
   const hipStream_t st = as_stream(stream);
   void (*fn)(const GemmArgs);
-  if (bm == 256) {
+  if (wq) {
+    fn = stamps ? (tail ? w8q_kernel<true, true> : w8q_kernel<false, true>)
+                : (tail ? w8q_kernel<true> : w8q_kernel<false>);
+  } else if (bm == 256) {
     fn = stamps ? (tail ? w8p_kernel<256, true, true> : w8p_kernel<256, false, true>)
                 : (tail ? w8p_kernel<256, true> : w8p_kernel<256, false>);
   } else {
@@ -1504,9 +1877,10 @@ int q4_gemm_w8a8_packed_stamped(const int8_t* A, const int8_t* W8p, const float*
   return gemm_w8a8_packed(A, W8p, sa, sw, sw_dtype, Y, C, M, N, K, stamps, stamps_bytes, stream);
 }
 
-size_t q4_gemm_w8a8_packed_workgroups(int M, int N) {
+size_t q4_gemm_w8a8_packed_workgroups(int M, int N, int K) {
   if (M <= 0 || N <= 0) return 0;
-  return (size_t)tiles(M, N, pick_bm(M, N));
+  const int wq = w8q_grid(M, N, K);
+  return (size_t)(wq ? wq : tiles(M, N, pick_bm(M, N)));
 }
 
 int q4_gemm_w4a8(const int8_t* A, const uint32_t* wq, const uint16_t* ratio, const float* sa, const void* sw,

@@ -19,7 +19,7 @@ void clear_error() { g_err[0] = 0; }
 
 // Plan overrides (q4_tune_set): -1 = none. Plain ints: the planners read them
 // on the host before each launch.
-static int g_tune[Q4_TUNE_COUNT] = {-1, -1, -1, -1, -1, -1, -1, -1, -1};
+static int g_tune[Q4_TUNE_COUNT] = {-1, -1, -1, -1, -1, -1, -1, -1, -1, -1};
 int tune_value(int knob) { return knob >= 0 && knob < Q4_TUNE_COUNT ? g_tune[knob] : -1; }
 
 // f32 -> f16 (RNE) and f16 -> f32 staging casts, 4 elements per thread.

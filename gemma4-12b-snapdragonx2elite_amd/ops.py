@@ -515,7 +515,7 @@ def w8_pack(W8: torch.Tensor) -> torch.Tensor:
 def gemm_w8a8_packed(A: torch.Tensor, W8p: torch.Tensor, sa: torch.Tensor, sw: torch.Tensor, N: int, *,
                      want_c: bool = False, Y: torch.Tensor | None = None, stamps: torch.Tensor | None = None):
     """W8A8 on packed weights (:func:`w8_pack`); same results as :func:`gemm_w8a8`.
-    ``stamps`` (int64 [w8a8_workgroups(M, N), 4]) takes the stamped launch:
+    ``stamps`` (int64 [w8a8_workgroups(M, N, K), 4]) takes the stamped launch:
     per workgroup the wall clock at start / after the k-loop / at the end and
     the shader cycles from start to end."""
     M, K = A.shape
@@ -535,9 +535,9 @@ def gemm_w8a8_packed(A: torch.Tensor, W8p: torch.Tensor, sa: torch.Tensor, sw: t
     return (Y, Cm) if want_c else Y
 
 
-def w8a8_workgroups(M: int, N: int) -> int:
+def w8a8_workgroups(M: int, N: int, K: int) -> int:
     """Workgroups of one :func:`gemm_w8a8_packed` launch (rows of its stamps)."""
-    return int(lib().q4_gemm_w8a8_packed_workgroups(M, N))
+    return int(lib().q4_gemm_w8a8_packed_workgroups(M, N, K))
 
 
 def w4a8_weights(wq: torch.Tensor, ratio: torch.Tensor, N: int, K: int) -> torch.Tensor:

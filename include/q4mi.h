@@ -80,7 +80,8 @@ int q4_dev_bytes(int N, int K, size_t* wq_bytes, size_t* scale_elems);
 #define Q4_TUNE_GEMV_MM_DEEP 6   /* small-M GEMV deeper load ring: 0, 1 */
 #define Q4_TUNE_W4A16_SPLIT 7    /* W4A16 K splits: 1..k-steps */
 #define Q4_TUNE_W4A16_KG 8       /* W4A16 k-groups per workgroup: 1, 2 */
-#define Q4_TUNE_COUNT 9
+#define Q4_TUNE_W8A8_TILES 9     /* packed W8A8: 0: 256-row tiles; 1: persistent 128x320 tiles wherever they apply */
+#define Q4_TUNE_COUNT 10
 /* Set knob to value (value < 0 clears it). Q4_ERR_ARG for an unknown knob. */
 int q4_tune_set(int knob, int value);
 /* Current override of knob, -1 when none (or an unknown knob). */
@@ -361,14 +362,21 @@ int q4_gemm_w8a8_packed(const int8_t* A, const int8_t* W8p, const float* sa,
  * clock (q4_probe_wall_clock_khz ticks) at its start, after its k-loop and at
  * its end, and shader-clock cycles from start to end, so the clock the chip
  * ran the GEMM at and the main-loop / epilogue split are read from the run
- * itself. stamps_bytes >= 32 * q4_gemm_w8a8_packed_workgroups(M, N).
+ * itself (for the persistent plan, "after its k-loop" is after its last
+ * tile's k-loop). stamps_bytes >= 32 * q4_gemm_w8a8_packed_workgroups(M, N, K).
  * Results are those of q4_gemm_w8a8_packed. */
 int q4_gemm_w8a8_packed_stamped(const int8_t* A, const int8_t* W8p, const float* sa,
                                 const void* sw, int sw_dtype, uint16_t* Y,
                                 int32_t* C, int M, int N, int K,
                                 unsigned long long* stamps, size_t stamps_bytes,
                                 void* stream);
-size_t q4_gemm_w8a8_packed_workgroups(int M, int N);
+/* Workgroups of a q4_gemm_w8a8_packed launch that passes Y, with Y, sa and
+ * sw 16-byte aligned: at most 256 (one per CU) when M % 128 == 0,
+ * N % 320 == 0, the 128-byte k-steps (K / 128, rounded up) are a multiple
+ * of 3 and there are at least 512 tiles of 128 x 320 (each workgroup then
+ * runs its share of those tiles), else one per 256 x 256 (or 128 x 256)
+ * tile. */
+size_t q4_gemm_w8a8_packed_workgroups(int M, int N, int K);
 
 /* W4A8: as W8A8 with B = int8(clamp(rint((q-8) * ratio[n,b]), -127, 127))
  * formed on the fly from the int4 codes and the panel-64 fp16 ratio.

@@ -201,11 +201,15 @@ def test_probe_and_stamped_gemm_argument_errors_without_gpu(g4):
     assert st == g4._lib.Q4_ERR_ARG and "operands" in _err(g4)
     st = lib.q4_probe_mfma(2, 4, 16, null, 0, p, 64, p, 16, null)
     assert st == g4._lib.Q4_ERR_ARG and "kind" in _err(g4)
-    # stamped W8A8: 480 workgroups at M=2048, N=15360 (256-row tiles); one stamp row short
-    assert lib.q4_gemm_w8a8_packed_workgroups(2048, 15360) == 480
-    assert lib.q4_gemm_w8a8_packed_workgroups(128, 512) == 2       # 128-row tiles below 256 workgroups
-    assert lib.q4_gemm_w8a8_packed_workgroups(0, 512) == 0
-    st = lib.q4_gemm_w8a8_packed_stamped(p, p, p, p, 0, p, null, 2048, 15360, 3840, p, 480 * 32 - 8, null)
+    # stamped W8A8: 256 persistent workgroups at M=2048, N=15360, K=3840 (768 tiles of
+    # 128 x 320); 480 with 256-row tiles when the k-steps are not a multiple of 3; one stamp row short
+    assert lib.q4_gemm_w8a8_packed_workgroups(2048, 15360, 3840) == 256
+    assert lib.q4_gemm_w8a8_packed_workgroups(2048, 15360, 4096) == 480
+    assert lib.q4_gemm_w8a8_packed_workgroups(2048, 15360, 320) == 256   # 3 k-steps, the last of two slices
+    assert lib.q4_gemm_w8a8_packed_workgroups(1024, 15360, 3840) == 480  # 384 tiles of 128 x 320: too few
+    assert lib.q4_gemm_w8a8_packed_workgroups(128, 512, 3840) == 2       # 128-row tiles below 256 workgroups
+    assert lib.q4_gemm_w8a8_packed_workgroups(0, 512, 64) == 0
+    st = lib.q4_gemm_w8a8_packed_stamped(p, p, p, p, 0, p, null, 2048, 15360, 3840, p, 256 * 32 - 8, null)
     assert st == g4._lib.Q4_ERR_ARG and "stamps" in _err(g4)
     st = lib.q4_gemm_w8a8_packed_stamped(p, p, p, p, 0, p, null, 2048, 15360, 3840, null, 0, null)
     assert st == g4._lib.Q4_ERR_ARG and "stamps" in _err(g4)

@@ -125,6 +125,40 @@ def test_w8a8_packed_config_size_rows(gpu):
     assert (to_np(gY1).view(np.uint16) == Y.view(np.uint16)).all()
 
 
+@pytest.mark.parametrize("M,N,K,wgs", [
+    (128, 320, 384, 1),         # one tile, three k-steps
+    (512, 1280, 320, 16),       # K % 128 == 64: the last k-step of each tile has two slices
+    (2048, 5760, 384, 256),     # 288 tiles in XCD eighths: 1 or 2 per workgroup, tiles shorter than their drain
+    (1664, 13120, 384, 256),    # 533 tiles (not a multiple of 8): 2 or 3 per workgroup
+    (1920, 12800, 2688, 256),   # 600 tiles, 2 or 3 per workgroup, 21 k-steps (drain ends a k-step early)
+])
+def test_w8a8_persistent_tiles_bit_exact(gpu, tune, M, N, K, wgs):
+    """The persistent 128 x 320-tile kernel (forced through the plan override
+    where the default plan keeps 256-row tiles): every int32 of C and every
+    fp16 of Y vs the oracle, fp32 and fp16 s_w, and Y bit-identical to the
+    256-row kernel's."""
+    rng = np.random.default_rng(M + N + K)
+    A, sa, W8, sw = _w8a8_case(rng, M, N, K)
+    gA, gsa = torch.from_numpy(A).cuda(), torch.from_numpy(sa).cuda()
+    W8p = torch.from_numpy(O.pack_w8_dev(W8)).cuda()
+    C = O.int_matmul_exact(A, W8)
+    for swdt in (np.float32, np.float16):
+        sw_used = sw.astype(swdt)
+        Y = O.w8a8_epilogue(C, sa, sw_used.astype(np.float32))
+        gsw = torch.from_numpy(sw_used).cuda()
+        tune("w8a8_tiles", 1)
+        assert gpu.w8a8_workgroups(M, N, K) == wgs
+        gY, gC = gpu.gemm_w8a8_packed(gA, W8p, gsa, gsw, N, want_c=True)
+        assert (to_np(gC) == C).all()
+        assert (to_np(gY).view(np.uint16) == Y.view(np.uint16)).all()
+        gY1 = gpu.gemm_w8a8_packed(gA, W8p, gsa, gsw, N)
+        assert (to_np(gY1).view(np.uint16) == Y.view(np.uint16)).all()
+        tune("w8a8_tiles", 0)
+        assert gpu.w8a8_workgroups(M, N, K) != wgs
+        gY0 = gpu.gemm_w8a8_packed(gA, W8p, gsa, gsw, N)
+        assert (to_np(gY0).view(np.uint16) == to_np(gY1).view(np.uint16)).all()
+
+
 @pytest.mark.parametrize("M,N", [(2304, 7432), (2100, 7424)])
 def test_w8a8_packed_y_only_ragged(gpu, M, N):
     """Y-only launches with 256-row tiles (>= 256 tiles) whose grid has both
@@ -134,7 +168,7 @@ def test_w8a8_packed_y_only_ragged(gpu, M, N):
     rng = np.random.default_rng(M + N)
     K = 512
     A, sa, W8, sw = _w8a8_case(rng, M, N, K)
-    assert gpu.w8a8_workgroups(M, N) >= 256
+    assert gpu.w8a8_workgroups(M, N, K) >= 256
     gA, gsa = torch.from_numpy(A).cuda(), torch.from_numpy(sa).cuda()
     W8p = torch.from_numpy(O.pack_w8_dev(W8)).cuda()
     for swdt in (np.float32, np.float16):
@@ -144,16 +178,17 @@ def test_w8a8_packed_y_only_ragged(gpu, M, N):
         assert (to_np(gY).view(np.uint16) == Y.view(np.uint16)).all()
 
 
-def test_w8a8_packed_epilogue_known_answers(gpu):
+@pytest.mark.parametrize("M,N,K,wgs", [(2048, 8192, 256, 256), (2048, 10240, 384, 256)])
+def test_w8a8_packed_epilogue_known_answers(gpu, M, N, K, wgs):
     """The kernel's epilogue order is the reference's, f16((f32(C) * sa) * sw)
     (vk/coopgemm_w8a8.comp:35): rows i < 3 of A and W8 are built so that
     C[i, i] is exactly the C of a known answer whose fp16 result differs under
-    every other evaluation order, with its sa and sw bits. 256 tiles of 256
-    rows, so the Y-only launch takes the full-tile epilogue and the launch
-    with C the general one; both against the oracle everywhere and against
+    every other evaluation order, with its sa and sw bits. N = 8192: 256 tiles
+    of 256 rows, so the Y-only launch takes the full-tile epilogue and the
+    launch with C the general one; N = 10240: 512 persistent tiles of
+    128 x 320 (two per workgroup). Against the oracle everywhere and against
     the known answers on the diagonal."""
     rng = np.random.default_rng(11)
-    M, N, K = 2048, 8192, 256
     A = rng.integers(-127, 128, (M, K), dtype=np.int8)
     W8 = rng.integers(-127, 128, (N, K), dtype=np.int8)
     sa = (rng.random(M) * 0.05 + 0.005).astype(np.float32)
@@ -168,7 +203,7 @@ def test_w8a8_packed_epilogue_known_answers(gpu):
         k0 += len(a)
         sa[i] = np.array([sab], np.uint32).view(np.float32)[0]
         sw[i] = np.array([swb], np.uint32).view(np.float32)[0]
-    assert k0 <= K and gpu.w8a8_workgroups(M, N) == 256
+    assert k0 <= K and gpu.w8a8_workgroups(M, N, K) == wgs
     C, Y = O.gemm_w8a8_ref(A, W8, sa, sw)
     assert [int(C[i, i]) for i in range(3)] == [k[0] for k in W8A8_EPILOGUE_KATS]
     assert [float(Y[i, i]) for i in range(3)] == [k[3] for k in W8A8_EPILOGUE_KATS]
@@ -184,15 +219,15 @@ def test_w8a8_packed_epilogue_known_answers(gpu):
 @pytest.mark.parametrize("M,N,K", [(100, 320, 192), (2048, 15360, 3840)])
 def test_w8a8_packed_stamped(gpu, M, N, K):
     """The stamped launch (per-workgroup clocks) gives the plain launch's
-    results bit for bit, on both tile heights (128 rows below 256 tiles,
-    256 at the full size), and its stamps are ordered: start <= end of the
-    k-loop <= end, cycles > 0."""
+    results bit for bit, with 128-row tiles below 256 tiles and with the
+    persistent 128 x 320 tiles at the full size, and its stamps are ordered:
+    start <= end of the (last) k-loop <= end, cycles > 0."""
     rng = np.random.default_rng(M + N + K)
     A, sa, W8, sw = _w8a8_case(rng, M, N, K)
     gA, gsa, gsw = torch.from_numpy(A).cuda(), torch.from_numpy(sa).cuda(), torch.from_numpy(sw).cuda()
     W8p = torch.from_numpy(O.pack_w8_dev(W8)).cuda()
-    wgs = gpu.w8a8_workgroups(M, N)
-    assert wgs == (-(-M // 256) * -(-N // 256) if -(-M // 256) * -(-N // 256) >= 256 else -(-M // 128) * -(-N // 256))
+    wgs = gpu.w8a8_workgroups(M, N, K)
+    assert wgs == (256 if (M, N, K) == (2048, 15360, 3840) else -(-M // 128) * -(-N // 256))
     stamps = torch.zeros((wgs, 4), dtype=torch.int64, device="cuda")
     gY, gC = gpu.gemm_w8a8_packed(gA, W8p, gsa, gsw, N, want_c=True)
     sY, sC = gpu.gemm_w8a8_packed(gA, W8p, gsa, gsw, N, want_c=True, stamps=stamps)
