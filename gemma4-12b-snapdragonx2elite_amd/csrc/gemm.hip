@@ -796,8 +796,13 @@ __global__ void __launch_bounds__(256) w8q_kernel(const GemmArgs g) {
   const int G = gridDim.x, w = blockIdx.x;
   // This workgroup's tiles first, first + tstride, ..: with both counts
   // multiples of 8, XCD x (workgroups w % 8 == x) takes the contiguous
-  // eighth x of the tile order (M fastest), so the 32 tiles an XCD runs
-  // together share weight panels and activation rows in its L2.
+  // eighth x of the tile order, so the 32 tiles an XCD runs together share
+  // weight panels and activation rows in its L2. The order runs M fastest
+  // within groups of 4 n-tiles, 4 n-tiles fastest within 8 m-tiles, so 32
+  // consecutive tiles are 8 m-tiles x 4 n-tiles: 3.9 MB of A and 4.9 MB of
+  // weights per XCD round at N = 15360, K = 3840, against 7.9 + 2.5 MB for
+  // 16 x 2 (measured: 1.5% faster, 7% fewer k-loop cycles). Shapes without
+  // whole groups take M fastest.
   int first, tstride, count;
   if (T % 8 == 0 && G % 8 == 0) {
     const int per = T / 8, gx = G / 8, i = w / 8;
@@ -811,10 +816,17 @@ __global__ void __launch_bounds__(256) w8q_kernel(const GemmArgs g) {
   }
   const int ks = w8p_kpad(K) / 32, nk = ks / 4;
   const int total = count * nk;  // the host launches at most T workgroups: count >= 1
+  const bool grp = ntm % 8 == 0 && (N / WQ_BN) % 4 == 0;
   auto tile_mn = [&](int j, int& m0, int& n0) Q4_INLINE {
     const int v = first + j * tstride;
-    m0 = (v % ntm) * WQ_BM;
-    n0 = (v / ntm) * WQ_BN;
+    if (grp) {
+      const int g = v / (4 * ntm), r = v - g * 4 * ntm;
+      m0 = (8 * (r >> 5) + ((r & 31) >> 2)) * WQ_BM;
+      n0 = (4 * g + (r & 3)) * WQ_BN;
+    } else {
+      m0 = (v % ntm) * WQ_BM;
+      n0 = (v / ntm) * WQ_BN;
+    }
   };
 
   // per-lane offsets, the same for every tile

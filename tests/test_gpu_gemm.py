@@ -131,6 +131,7 @@ def test_w8a8_packed_config_size_rows(gpu):
     (2048, 5760, 384, 256),     # 288 tiles in XCD eighths: 1 or 2 per workgroup, tiles shorter than their drain
     (1664, 13120, 384, 256),    # 533 tiles (not a multiple of 8): 2 or 3 per workgroup
     (1920, 12800, 2688, 256),   # 600 tiles, 2 or 3 per workgroup, 21 k-steps (drain ends a k-step early)
+    (1024, 12800, 384, 256),    # 320 tiles in groups of 8 m-tiles x 4 n-tiles, 1 or 2 per workgroup
 ])
 def test_w8a8_persistent_tiles_bit_exact(gpu, tune, M, N, K, wgs):
     """The persistent 128 x 320-tile kernel (forced through the plan override
