@@ -1825,16 +1825,20 @@ int q4_w8_pack(const int8_t* W8, int N, int K, int8_t* W8p, void* stream) {
   return Q4_OK;
 }
 
-// Persistent 128 x 320 tiles (w8q_kernel) when the shape tiles exactly and
-// gives at least two tiles per CU, with k-steps (K / 128, rounded up) a
-// multiple of 3: 0 when the 256-row kernel runs, else the
-// grid (at most one workgroup per CU). Plan override Q4_TUNE_W8A8_TILES.
+// Persistent 128 x 320 tiles (w8q_kernel) when the shape tiles exactly into
+// more tiles than there are CUs, with k-steps (K / 128, rounded up) a
+// multiple of 3: 0 when the 256-row kernel runs, else the grid (at most one
+// workgroup per CU). Measured against the 256-row kernel (K = 3840, HIP
+// events, rotating weights): 384 tiles 66.5 against 74.9 us, 512 tiles 71.3
+// against 99.9, 768 tiles 109.9 against 112.8, 1536 tiles 201.1 against
+// 220.7; with 192 tiles (2048 x 3840 x 15360) 118.5 against 113.2, so fewer
+// tiles than CUs keep the 256-row kernel. Plan override Q4_TUNE_W8A8_TILES.
 // The caller also needs Y and 16-byte aligned Y, sa and sw.
 static int w8q_grid(int M, int N, int K) {
   if (M % WQ_BM || N % WQ_BN || K <= 0 || K % 64 || (w8p_kpad(K) / 128) % 3) return 0;
   const int t = (M / WQ_BM) * (N / WQ_BN);
   const int v = tune_value(Q4_TUNE_W8A8_TILES);
-  if (v == 0 || (v != 1 && t < 512)) return 0;
+  if (v == 0 || (v != 1 && t <= 256)) return 0;
   return min(t, 256);
 }
 

@@ -373,7 +373,7 @@ int q4_gemm_w8a8_packed_stamped(const int8_t* A, const int8_t* W8p, const float*
 /* Workgroups of a q4_gemm_w8a8_packed launch that passes Y, with Y, sa and
  * sw 16-byte aligned: at most 256 (one per CU) when M % 128 == 0,
  * N % 320 == 0, the 128-byte k-steps (K / 128, rounded up) are a multiple
- * of 3 and there are at least 512 tiles of 128 x 320 (each workgroup then
+ * of 3 and there are more than 256 tiles of 128 x 320 (each workgroup then
  * runs its share of those tiles), else one per 256 x 256 (or 128 x 256)
  * tile. */
 size_t q4_gemm_w8a8_packed_workgroups(int M, int N, int K);

@@ -206,7 +206,8 @@ def test_probe_and_stamped_gemm_argument_errors_without_gpu(g4):
     assert lib.q4_gemm_w8a8_packed_workgroups(2048, 15360, 3840) == 256
     assert lib.q4_gemm_w8a8_packed_workgroups(2048, 15360, 4096) == 480
     assert lib.q4_gemm_w8a8_packed_workgroups(2048, 15360, 320) == 256   # 3 k-steps, the last of two slices
-    assert lib.q4_gemm_w8a8_packed_workgroups(1024, 15360, 3840) == 480  # 384 tiles of 128 x 320: too few
+    assert lib.q4_gemm_w8a8_packed_workgroups(1024, 15360, 3840) == 256  # 384 tiles of 128 x 320
+    assert lib.q4_gemm_w8a8_packed_workgroups(2048, 3840, 15360) == 240  # 192 tiles: fewer than the CUs
     assert lib.q4_gemm_w8a8_packed_workgroups(128, 512, 3840) == 2       # 128-row tiles below 256 workgroups
     assert lib.q4_gemm_w8a8_packed_workgroups(0, 512, 64) == 0
     st = lib.q4_gemm_w8a8_packed_stamped(p, p, p, p, 0, p, null, 2048, 15360, 3840, p, 256 * 32 - 8, null)

@@ -134,10 +134,10 @@ def test_w8a8_packed_config_size_rows(gpu):
     (1024, 12800, 384, 256),    # 320 tiles in groups of 8 m-tiles x 4 n-tiles, 1 or 2 per workgroup
 ])
 def test_w8a8_persistent_tiles_bit_exact(gpu, tune, M, N, K, wgs):
-    """The persistent 128 x 320-tile kernel (forced through the plan override
-    where the default plan keeps 256-row tiles): every int32 of C and every
-    fp16 of Y vs the oracle, fp32 and fp16 s_w, and Y bit-identical to the
-    256-row kernel's."""
+    """The persistent 128 x 320-tile kernel (forced through the plan override,
+    also where the default plan keeps 256-row tiles): every int32 of C and
+    every fp16 of Y vs the oracle, fp32 and fp16 s_w, and Y bit-identical to
+    the 256-row kernel's (forced the same way)."""
     rng = np.random.default_rng(M + N + K)
     A, sa, W8, sw = _w8a8_case(rng, M, N, K)
     gA, gsa = torch.from_numpy(A).cuda(), torch.from_numpy(sa).cuda()
