@@ -160,6 +160,28 @@ def test_w8a8_persistent_tiles_bit_exact(gpu, tune, M, N, K, wgs):
         assert (to_np(gY0).view(np.uint16) == to_np(gY1).view(np.uint16)).all()
 
 
+def test_w8a8_packed_unaligned_scales_fall_back(gpu):
+    """A shape the persistent plan takes by default, called with sa and sw
+    offset from 16-byte alignment (4-byte aligned views one element into
+    larger buffers): the entry point runs the per-tile plan instead, with the
+    same bits."""
+    rng = np.random.default_rng(31)
+    M, N, K = 1024, 12800, 384
+    A, sa, W8, sw = _w8a8_case(rng, M, N, K)
+    C, Y = O.gemm_w8a8_ref(A, W8, sa, sw)
+    gA, W8p = torch.from_numpy(A).cuda(), torch.from_numpy(O.pack_w8_dev(W8)).cuda()
+    sa_b = torch.zeros(M + 1, dtype=torch.float32, device="cuda")
+    sw_b = torch.zeros(N + 1, dtype=torch.float32, device="cuda")
+    sa_b[1:] = torch.from_numpy(sa).cuda()
+    sw_b[1:] = torch.from_numpy(sw).cuda()
+    gY = gpu.gemm_w8a8_packed(gA, W8p, sa_b[1:], sw_b[1:], N)
+    assert (to_np(gY).view(np.uint16) == Y.view(np.uint16)).all()
+    gY2, gC = gpu.gemm_w8a8_packed(gA, W8p, torch.from_numpy(sa).cuda(), torch.from_numpy(sw).cuda(), N,
+                                   want_c=True)
+    assert gpu.w8a8_workgroups(M, N, K) == 256 and (to_np(gC) == C).all()
+    assert (to_np(gY2).view(np.uint16) == Y.view(np.uint16)).all()
+
+
 @pytest.mark.parametrize("M,N", [(2304, 7432), (2100, 7424)])
 def test_w8a8_packed_y_only_ragged(gpu, M, N):
     """Y-only launches with 256-row tiles (>= 256 tiles) whose grid has both
