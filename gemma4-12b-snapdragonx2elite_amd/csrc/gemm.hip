@@ -1787,6 +1787,7 @@ int q4_gemm_w8a8(const int8_t* A, const int8_t* W8, const float* sa, const void*
   Q4_ARG(!Y || (sa && sw), "Y needs sa and sw");
   Q4_ARG(sw_dtype == Q4_DT_F32 || sw_dtype == Q4_DT_F16, "bad sw dtype %d", sw_dtype);
   Q4_ARG(((uintptr_t)A & 15) == 0 && ((uintptr_t)W8 & 15) == 0, "A and W8 must be 16-byte aligned");
+  Q4_ARG((((uintptr_t)Y | (uintptr_t)C) & 15) == 0, "Y and C must be 16-byte aligned (vector stores)");
   GemmArgs g{A, W8, nullptr, sa, sw, sw_dtype == Q4_DT_F16, Y, C, nullptr, M, N, K};
   if (pick_bm(M, N) == 256)
     hipLaunchKernelGGL(w8a8_kernel<256>, dim3(tiles(M, N, 256)), dim3(256), 0, as_stream(stream), g);
@@ -1852,6 +1853,7 @@ static int gemm_w8a8_packed(const int8_t* A, const int8_t* W8p, const float* sa,
   Q4_ARG(!Y || (sa && sw), "Y needs sa and sw");
   Q4_ARG(sw_dtype == Q4_DT_F32 || sw_dtype == Q4_DT_F16, "bad sw dtype %d", sw_dtype);
   Q4_ARG(((uintptr_t)A & 15) == 0 && ((uintptr_t)W8p & 15) == 0, "A and W8p must be 16-byte aligned");
+  Q4_ARG((((uintptr_t)Y | (uintptr_t)C) & 15) == 0, "Y and C must be 16-byte aligned (vector stores)");
   Q4_ARG((long)M * K < (1L << 31) && (long)q4_w8_packed_bytes(N, K) < (1L << 31),
          "packed W8A8 needs M*K and the packed weights under 2 GiB (32-bit offsets)");
   const int bm = pick_bm(M, N);
@@ -1909,6 +1911,7 @@ int q4_gemm_w4a8(const int8_t* A, const uint32_t* wq, const uint16_t* ratio, con
   Q4_ARG(!Y || (sa && sw), "Y needs sa and sw");
   Q4_ARG(sw_dtype == Q4_DT_F32 || sw_dtype == Q4_DT_F16, "bad sw dtype %d", sw_dtype);
   Q4_ARG(((uintptr_t)A & 15) == 0 && ((uintptr_t)wq & 15) == 0, "A and wq must be 16-byte aligned");
+  Q4_ARG((((uintptr_t)Y | (uintptr_t)C) & 15) == 0, "Y and C must be 16-byte aligned (vector stores)");
   GemmArgs g{A, wq, ratio, sa, sw, sw_dtype == Q4_DT_F16, Y, C, nullptr, M, N, K};
   // 128-row tiles only: with 256 rows the requant register ring does not fit
   // without spills, and a spill of a register whose load is still in flight

@@ -333,6 +333,7 @@ int q4_quant_act_i8(const void* X, int x_dtype, int8_t* A, float* sa, int M,
 /* W8A8: C int32 = A int8 [M][K] @ W8 int8 [N][K]^T (exact),
  * Y f16 [M][N] = f16((f32(C) * sa[m]) * sw[n]); sw is sw_dtype [N].
  * C (int32 [M][N]) is written only if non-NULL. Y may be NULL when C is not.
+ * A, the weights, Y and C must be 16-byte aligned (Q4_ERR_ARG otherwise).
  * K must be a multiple of 64 (Q4_ERR_ARG otherwise), narrower than the
  * reference shader, which steps K by 32 (vk/coopgemm_w8a8.comp:23): every
  * engine shape (K = 3840, 4096, 15360) satisfies it. The same rule holds for

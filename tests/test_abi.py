@@ -212,6 +212,8 @@ def test_probe_and_stamped_gemm_argument_errors_without_gpu(g4):
     assert lib.q4_gemm_w8a8_packed_workgroups(0, 512, 64) == 0
     st = lib.q4_gemm_w8a8_packed_stamped(p, p, p, p, 0, p, null, 2048, 15360, 3840, p, 256 * 32 - 8, null)
     assert st == g4._lib.Q4_ERR_ARG and "stamps" in _err(g4)
+    st = lib.q4_gemm_w8a8_packed(p, p, p, p, 0, C.c_void_p((1 << 20) + 8), null, 2048, 15360, 3840, null)
+    assert st == g4._lib.Q4_ERR_ARG and "16-byte aligned" in _err(g4)
     st = lib.q4_gemm_w8a8_packed_stamped(p, p, p, p, 0, p, null, 2048, 15360, 3840, null, 0, null)
     assert st == g4._lib.Q4_ERR_ARG and "stamps" in _err(g4)
 
