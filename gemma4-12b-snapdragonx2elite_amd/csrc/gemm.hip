@@ -756,10 +756,11 @@ __global__ void __launch_bounds__(256) w8p_kernel(const GemmArgs g) {
 //    direct loads at its first k-step (4 KB block, double-buffered by tile
 //    parity). With C the int32 accumulators are stored directly.
 // Measured at M = 2048, N = 15360, K = 3840 against w8p_kernel on the same
-// boxes: 2-3% faster. The exposed epilogue falls from ~8 to ~4 us and every
-// CU works to the end, but a 16x16x64 int8 MFMA issues every ~20.6 cycles in
-// this loop (a copy without loads or LDS reads), against 34 for a 32x32x32
-// with twice the products, and the layout needs 16-column groups.
+// boxes: 2-3% faster. Every CU works to the end and the exposed epilogues
+// fall from two of ~8 us to one of ~4.5 us (the Y stores issued during the
+// k-loops cost ~8 us there), but a 16x16x64 int8 MFMA issues every ~20.6
+// cycles in this loop (a copy without loads or LDS reads), against 34 for a
+// 32x32x32 with twice the products, and the layout needs 16-column groups.
 // Needs M % 128 == 0, N % 320 == 0, K % 64 == 0 with ceil(K / 128) % 3 == 0
 // (a last k-step of two slices clamps its A chunks inside the row; its
 // weights are zero padding), Y, and 16-byte aligned Y, sa and sw.
@@ -820,9 +821,9 @@ __global__ void __launch_bounds__(256) w8q_kernel(const GemmArgs g) {
   auto tile_mn = [&](int j, int& m0, int& n0) Q4_INLINE {
     const int v = first + j * tstride;
     if (grp) {
-      const int g = v / (4 * ntm), r = v - g * 4 * ntm;
+      const int grp4 = v / (4 * ntm), r = v - grp4 * 4 * ntm;  // group of 4 n-tiles, tile within it
       m0 = (8 * (r >> 5) + ((r & 31) >> 2)) * WQ_BM;
-      n0 = (4 * g + (r & 3)) * WQ_BN;
+      n0 = (4 * grp4 + (r & 3)) * WQ_BN;
     } else {
       m0 = (v % ntm) * WQ_BM;
       n0 = (v / ntm) * WQ_BN;
