@@ -815,8 +815,10 @@ __global__ void __launch_bounds__(256) w8q_kernel(const GemmArgs g) {
     tstride = G;
     count = w < T ? (T - w + G - 1) / G : 0;
   }
+  // The host launches at most T workgroups, so count >= 1; a workgroup
+  // without tiles would leave before issuing any load.
+  if (count == 0) return;
   const int ks = w8p_kpad(K) / 32, nk = ks / 4;
-  const int total = count * nk;  // the host launches at most T workgroups: count >= 1
   const bool grp = ntm % 8 == 0 && (N / WQ_BN) % 4 == 0;
   auto tile_mn = [&](int j, int& m0, int& n0) Q4_INLINE {
     const int v = first + j * tstride;
